@@ -1,0 +1,267 @@
+"""Pins the CPU oracle beyond the smoke-test fixtures.
+
+Each check is chosen so a plausible restatement mistake (dropped term, wrong
+sign, transposed operand, wrong GQA map, off-by-one causal bound) fails it:
+exhaustive/IEEE comparisons for fp16 conversion, closed forms, invariants, and
+brute force against independent numpy formulations written differently from
+the oracle's loops (matrix forms, complex rotation, explicit softmax).
+"""
+import numpy as np
+import pytest
+
+import oracle
+
+
+# ------------------------------------------------------------------ f16 ----
+
+def test_f16_to_f32_exhaustive_against_numpy():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.f16_bits_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_rne_against_numpy():
+    rng = np.random.default_rng(0)
+    raw = rng.integers(0, 2**32, size=400_000, dtype=np.uint64).astype(np.uint32)
+    x = raw.view(np.float32)
+    # Edge values: ties to even, subnormal boundary, overflow boundary, signed zero.
+    edges = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, -65520.0, 1e-8, 2**-24,
+                      2**-25, 3 * 2**-26, 2**-14, 2**-14 - 2**-25, 1 + 2**-11, 1 + 3 * 2**-11,
+                      np.inf, -np.inf], np.float32)
+    x = np.concatenate([x, edges, rng.standard_normal(100_000).astype(np.float32)])
+    got = oracle.f32_to_f16_bits(x)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(got[~nan], ref[~nan])
+    assert np.all((got[nan] & 0x7C00) == 0x7C00) and np.all((got[nan] & 0x3FF) != 0)
+
+
+# ------------------------------------------------------------ attention ----
+
+def numpy_attention(q, kc, vc, start, tokens, cap, heads, kv_heads, d, layer=0):
+    """Explicit softmax attention, written from the math (not the oracle's loops)."""
+    q = q.reshape(tokens, heads, d).astype(np.float64)
+    k = kc.reshape(-1, cap, kv_heads, d)[layer].astype(np.float64)
+    v = vc.reshape(-1, cap, kv_heads, d)[layer].astype(np.float64)
+    group = heads // kv_heads
+    out = np.zeros((tokens, heads, d))
+    for t in range(tokens):
+        n = start + t + 1
+        for h in range(heads):
+            g = h // group
+            s = k[:n, g, :] @ q[t, h] / np.sqrt(np.float32(d))
+            p = np.exp(s - s.max())
+            out[t, h] = (p / p.sum()) @ v[:n, g, :]
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+@pytest.mark.parametrize("shape", [(3, 5, 12, 4, 2, 16), (0, 7, 7, 2, 1, 8), (9, 1, 10, 8, 2, 32)])
+def test_attention_brute_force(kv_f16, shape):
+    start, tokens, cap, heads, kv_heads, d = shape
+    rng = np.random.default_rng(1)
+    layers = 2
+    q = rng.standard_normal(tokens * heads * d).astype(np.float32)
+    kc = rng.standard_normal(layers * cap * kv_heads * d).astype(np.float32)
+    vc = rng.standard_normal(layers * cap * kv_heads * d).astype(np.float32)
+    if kv_f16:
+        kb, vb = oracle.f32_to_f16_bits(kc), oracle.f32_to_f16_bits(vc)
+        kref, vref = oracle.f16_bits_to_f32(kb), oracle.f16_bits_to_f32(vb)
+    else:
+        kb, vb, kref, vref = kc, vc, kc, vc
+    got = oracle.attention_batched(q, kb, vb, 1, start, tokens, cap, heads, kv_heads, d)
+    ref = numpy_attention(q, kref, vref, start, tokens, cap, heads, kv_heads, d, layer=1)
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+
+
+def test_attention_round_query_matches_prerounded_query():
+    rng = np.random.default_rng(2)
+    heads, kv_heads, d, tokens, cap = 4, 2, 16, 3, 3
+    q = rng.standard_normal(tokens * heads * d).astype(np.float32)
+    kc = oracle.f32_to_f16_bits(rng.standard_normal(cap * kv_heads * d))
+    vc = oracle.f32_to_f16_bits(rng.standard_normal(cap * kv_heads * d))
+    a = oracle.attention_batched(q, kc, vc, 0, 0, tokens, cap, heads, kv_heads, d,
+                                 round_query_f16=True)
+    b = oracle.attention_batched(q.astype(np.float16).astype(np.float32), kc, vc, 0, 0, tokens,
+                                 cap, heads, kv_heads, d)
+    np.testing.assert_array_equal(a, b)
+    c = oracle.attention_batched(q, kc, vc, 0, 0, tokens, cap, heads, kv_heads, d)
+    assert not np.array_equal(a, c)
+
+
+def test_attention_gqa_heads_with_equal_query_agree_and_groups_differ():
+    rng = np.random.default_rng(3)
+    heads, kv_heads, d, cap = 8, 2, 32, 6
+    qh = rng.standard_normal(d).astype(np.float32)
+    q = np.tile(qh, heads)
+    kc = rng.standard_normal(cap * kv_heads * d).astype(np.float32)
+    vc = rng.standard_normal(cap * kv_heads * d).astype(np.float32)
+    out = oracle.attention_batched(q, kc, vc, 0, cap - 1, 1, cap, heads, kv_heads, d)
+    out = out.reshape(heads, d)
+    for h in range(heads):
+        np.testing.assert_array_equal(out[h], out[(h // 4) * 4])
+    assert not np.allclose(out[0], out[4])
+
+
+def test_attention_key_permutation_invariance_for_last_query():
+    rng = np.random.default_rng(4)
+    d, cap = 16, 9
+    q = rng.standard_normal(d).astype(np.float32)
+    kc = rng.standard_normal((cap, d)).astype(np.float32)
+    vc = rng.standard_normal((cap, d)).astype(np.float32)
+    perm = rng.permutation(cap)
+    a = oracle.attention_batched(q, kc, vc, 0, cap - 1, 1, cap, 1, 1, d)
+    b = oracle.attention_batched(q, kc[perm], vc[perm], 0, cap - 1, 1, cap, 1, 1, d)
+    np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-7)
+
+
+# ------------------------------------------------------------------ GDN ----
+
+def numpy_gdn_matrix_form(q, k, v, g, b, s0, tokens, hk, hv, d):
+    """S_t = e^g S (I - b k k^T) + b v k^T ; y = S_t q / sqrt(d), in matrix form."""
+    q = q.reshape(tokens, hk, d).astype(np.float64)
+    k = k.reshape(tokens, hk, d).astype(np.float64)
+    v = v.reshape(tokens, hv, d).astype(np.float64)
+    g = g.reshape(tokens, hv).astype(np.float64)
+    b = b.reshape(tokens, hv).astype(np.float64)
+    s = s0.reshape(hv, d, d).astype(np.float64).copy()
+    y = np.zeros((tokens, hv, d))
+    eye = np.eye(d)
+    for t in range(tokens):
+        for h in range(hv):
+            kk = k[t, h % hk]
+            s[h] = np.exp(g[t, h]) * s[h] @ (eye - b[t, h] * np.outer(kk, kk)) + \
+                b[t, h] * np.outer(v[t, h], kk)
+            y[t, h] = s[h] @ q[t, h % hk] / np.sqrt(d)
+    return y.reshape(-1), s.reshape(-1)
+
+
+def test_gdn_matches_matrix_form_with_gqa_repeat():
+    rng = np.random.default_rng(5)
+    tokens, hk, hv, d = 6, 2, 4, 8
+    q = rng.standard_normal(tokens * hk * d).astype(np.float32)
+    k = rng.standard_normal(tokens * hk * d).astype(np.float32) * 0.3
+    v = rng.standard_normal(tokens * hv * d).astype(np.float32)
+    g = -np.abs(rng.standard_normal(tokens * hv)).astype(np.float32)
+    b = (1 / (1 + np.exp(-rng.standard_normal(tokens * hv)))).astype(np.float32)
+    s0 = rng.standard_normal(hv * d * d).astype(np.float32)
+    y, s = oracle.gated_delta_net(q, k, v, g, b, s0, tokens, hk, hv, d)
+    y_ref, s_ref = numpy_gdn_matrix_form(q, k, v, g, b, s0, tokens, hk, hv, d)
+    np.testing.assert_allclose(y, y_ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(s, s_ref, rtol=1e-5, atol=1e-5)
+
+
+def test_gdn_beta_zero_is_pure_decay():
+    rng = np.random.default_rng(6)
+    tokens, d = 4, 8
+    q = rng.standard_normal(tokens * d).astype(np.float32)
+    k = rng.standard_normal(tokens * d).astype(np.float32)
+    v = rng.standard_normal(tokens * d).astype(np.float32)
+    g = np.array([-0.1, -0.2, -0.3, -0.4], np.float32)
+    s0 = rng.standard_normal(d * d).astype(np.float32)
+    y, s = oracle.gated_delta_net(q, k, v, g, np.zeros(tokens, np.float32), s0, tokens, 1, 1, d)
+    np.testing.assert_allclose(s, s0 * np.exp(g.astype(np.float64).sum()), rtol=1e-5)
+    last = s0.reshape(d, d).astype(np.float64) * np.exp(g.astype(np.float64).sum())
+    np.testing.assert_allclose(y[-d:], last @ q[-d:] / np.sqrt(d), rtol=1e-5, atol=1e-6)
+
+
+def test_gdn_unit_key_from_zero_state():
+    d, i = 8, 3
+    q = np.arange(1, d + 1, dtype=np.float32)
+    k = np.zeros(d, np.float32)
+    k[i] = 1.0
+    v = np.linspace(-1, 1, d).astype(np.float32)
+    y, s = oracle.gated_delta_net(q, k, v, [0.0], [1.0], np.zeros(d * d, np.float32), 1, 1, 1, d)
+    np.testing.assert_allclose(y, v * q[i] / np.sqrt(d), rtol=1e-6)
+    expect = np.zeros((d, d))
+    expect[:, i] = v
+    np.testing.assert_allclose(s.reshape(d, d), expect, atol=0)
+
+
+# ------------------------------------------------------------ conv/rope ----
+
+def test_conv_chunked_equals_whole_sequence():
+    rng = np.random.default_rng(7)
+    kk, c, t = 4, 5, 9
+    x = rng.standard_normal(t * c).astype(np.float32)
+    w = rng.standard_normal(c * kk).astype(np.float32)
+    state = np.zeros(c * (kk - 1), np.float32)
+    ci, _ = oracle.build_ssm_conv_state(state, x, kk, c, t)
+    whole = oracle.ssm_conv(ci, w, kk, c, t, 1)
+    # numpy: causal depthwise conv, y[t,c] = sum_j w[c,j] x[t-(K-1)+j, c]
+    xp = np.concatenate([np.zeros((kk - 1, c)), x.reshape(t, c)])
+    ref = np.stack([(xp[tt:tt + kk] * w.reshape(c, kk).T).sum(0) for tt in range(t)])
+    np.testing.assert_allclose(whole.reshape(t, c), ref, rtol=1e-5, atol=1e-6)
+    # Same sequence fed as chunks 4 + 5 through the carried state; and token by token.
+    st = np.zeros_like(state)
+    parts = []
+    for lo, hi in ((0, 4), (4, 9)):
+        ci, st = oracle.build_ssm_conv_state(st, x[lo * c:hi * c], kk, c, hi - lo)
+        parts.append(oracle.ssm_conv(ci, w, kk, c, hi - lo, 1))
+    np.testing.assert_allclose(np.concatenate(parts), whole, rtol=1e-6, atol=1e-7)
+    st = np.zeros_like(state)
+    steps = []
+    for tt in range(t):
+        out, st = oracle.ssm_conv1_stateful(st, x[tt * c:(tt + 1) * c], w, kk, c)
+        steps.append(out)
+    np.testing.assert_allclose(np.concatenate(steps), whole, rtol=1e-6, atol=1e-7)
+
+
+def test_mrope_matches_complex_rotation_and_leaves_tail():
+    rng = np.random.default_rng(8)
+    tokens, heads, d, n_dims, sections, theta = 3, 2, 32, 16, (3, 3, 2, 0), 1e7
+    x = rng.standard_normal(tokens * heads * d).astype(np.float32)
+    pos = rng.integers(0, 5000, size=4 * tokens).astype(np.int32)
+    got = oracle.mrope(x, pos, tokens, heads, d, n_dims, sections, theta).reshape(tokens, heads, d)
+    xr = x.reshape(tokens, heads, d).astype(np.float64)
+    half = n_dims // 2
+    bounds = np.cumsum(sections)
+    for t in range(tokens):
+        for i in range(half):
+            row = int(np.searchsorted(bounds, i % sum(sections), side="right"))
+            ang = pos[t + tokens * row] * theta ** (-2 * i / n_dims)
+            z = (xr[t, :, i] + 1j * xr[t, :, half + i]) * np.exp(1j * ang)
+            np.testing.assert_allclose(got[t, :, i], z.real, rtol=1e-5, atol=1e-5)
+            np.testing.assert_allclose(got[t, :, half + i], z.imag, rtol=1e-5, atol=1e-5)
+    np.testing.assert_array_equal(got[:, :, n_dims:], x.reshape(tokens, heads, d)[:, :, n_dims:])
+
+
+def test_mrope_positions_rows_are_token_index():
+    pos = oracle.make_mrope_positions(7, 3).reshape(4, 3)
+    assert (pos == np.array([7, 8, 9])).all()
+
+
+# ------------------------------------------------------------- norms -------
+
+def test_qk_norm_unit_rms_and_l2_unit_norm():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal(3 * 4 * 16).astype(np.float32) * 5
+    y = oracle.qk_norm_f32_batched(x, np.ones(16), 3, 4, 16, 0.0).reshape(-1, 16)
+    np.testing.assert_allclose(np.sqrt((y.astype(np.float64) ** 2).mean(1)), 1.0, rtol=1e-6)
+    z = oracle.l2_norm(x, 12, 16, 1e-6).reshape(-1, 16)
+    np.testing.assert_allclose(np.linalg.norm(z.astype(np.float64), axis=1), 1.0, rtol=1e-6)
+    tiny = oracle.l2_norm(np.full(4, 1e-9, np.float32), 1, 4, 1e-6)
+    np.testing.assert_allclose(tiny, 1e-9 / 1e-6, rtol=1e-6)
+
+
+# ------------------------------------------------------- legacy Qwen3 ------
+
+def test_legacy_qwen3_attention_agrees_with_generic_attention():
+    rng = np.random.default_rng(10)
+    heads, kv_heads, d, positions = 4, 2, 16, 7
+    q = rng.standard_normal(positions * heads * d).astype(np.float32)
+    k = rng.standard_normal(positions * kv_heads * d).astype(np.float32)
+    v = rng.standard_normal(positions * kv_heads * d).astype(np.float32)
+    ones = np.ones(d, np.float32)
+    kc, vc, qo, out = oracle.qwen3_attention_sequence(q, k, v, positions, heads, kv_heads, d,
+                                                      ones, ones, 1e-6, 1e6)
+    ref = oracle.attention_batched(qo, kc, vc, 0, 0, positions, positions, heads, kv_heads, d)
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5)
+    # Position 0 rope is the identity; qk_norm with unit weights gives unit RMS.
+    q0 = oracle.qwen3_qk_norm(q[:heads * d], heads, d, ones, 1e-6)
+    np.testing.assert_array_equal(oracle.qwen3_rope(q0, heads, d, 0, 1e6), q0)
+    np.testing.assert_allclose(qo[:heads * d], q0, rtol=0, atol=0)
