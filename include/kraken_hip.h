@@ -1,0 +1,317 @@
+/*
+ * kraken_hip.h -- C ABI of the MI355X (gfx950) backend for the Qwen3.5
+ * attention hot path of kraken-infer.
+ *
+ * This is the thin C layer under the backend interface.  Each entry point
+ * replaces one operation of toyllm::mps::MpsContext
+ * (reference: include/toyllm/backends/mps/mps_backend.hpp:76-428); the comment
+ * on each declaration cites the method it replaces and its Metal
+ * implementation.  Semantics carried over from the reference:
+ *
+ *  - Status codes keep the order of toyllm::StatusCode
+ *    (include/toyllm/core/status.hpp:8-13).  Every call returns one; a non-OK
+ *    call leaves a message readable with kraken_hip_last_error() on the calling
+ *    thread (the C counterpart of Status::message()).  Nothing throws across
+ *    this boundary.
+ *  - Argument checks run in the reference's order (mps_backend.mm:10625-10713):
+ *    context valid -> dimensions positive / divisible / bounded -> capacity ->
+ *    size_t overflow -> each buffer initialized and large enough -> every
+ *    parameter fits uint32.  A failed check returns KRAKEN_INVALID_ARGUMENT.
+ *  - Buffers are caller-owned device allocations described by a non-owning
+ *    {data, byte_size} view (the reference's MpsBuffer, mps_backend.hpp:26-47).
+ *    data == NULL means "not initialized".  Ops never allocate caller-visible
+ *    memory; "_at" variants take element offsets into caller buffers.
+ *  - Synchronisation (mps_backend.mm:4416-4467): outside begin_graph/commit_graph
+ *    every op is enqueued on the context's stream and waited for; inside, ops are
+ *    only enqueued and commit_graph waits once.  Host copies wait for pending work.
+ *  - A context is used by one thread at a time; contexts are independent.
+ *
+ * Everything here is plain C: pointers, sizes, floats.  No torch or HIP types
+ * cross the boundary (streams travel as void*).
+ */
+#ifndef KRAKEN_HIP_H
+#define KRAKEN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define KRAKEN_API __attribute__((visibility("default")))
+#else
+#define KRAKEN_API
+#endif
+
+/* toyllm::StatusCode, include/toyllm/core/status.hpp:8-13 (same order). */
+typedef enum kraken_status {
+  KRAKEN_OK = 0,
+  KRAKEN_INVALID_ARGUMENT = 1,
+  KRAKEN_UNAVAILABLE = 2,
+  KRAKEN_INTERNAL_ERROR = 3
+} kraken_status;
+
+/* Non-owning view of device memory; stands in for toyllm::mps::MpsBuffer
+ * (mps_backend.hpp:26-47): valid() == (data != NULL), byte_size() == byte_size. */
+typedef struct kraken_buffer {
+  void* data;
+  size_t byte_size;
+} kraken_buffer;
+
+typedef struct kraken_hip_context kraken_hip_context;
+
+/* ------------------------------------------------------------ context ---- */
+
+/* MpsContext::create (mps_backend.hpp:87; mps_backend.mm:5043-5085).  Binds the
+ * current HIP device and creates the context's stream.  KRAKEN_UNAVAILABLE when no
+ * HIP device is present (the stub backend's answer, mps_backend_stub.cpp:52-54). */
+KRAKEN_API int kraken_hip_context_create(kraken_hip_context** out_context);
+
+/* A context with no device, for host-side tests of argument checking: every op runs
+ * its full validation and, when the arguments are accepted, returns
+ * KRAKEN_UNAVAILABLE with the message "validation-only context: arguments accepted"
+ * instead of launching.  It never computes anything.  No reference counterpart
+ * (the reference checks arguments only on a live Metal device). */
+KRAKEN_API int kraken_hip_context_create_validation_only(kraken_hip_context** out_context);
+
+/* ~MpsContext (mps_backend.mm:4461-4467).  Aborts an open graph. */
+KRAKEN_API void kraken_hip_context_destroy(kraken_hip_context* context);
+
+/* Enqueue on a caller-owned hipStream_t (passed as void*) instead of the
+ * context's own stream; NULL restores the context's stream.  No reference
+ * counterpart (Metal owns its command queue, mps_backend.mm:4330-4332). */
+KRAKEN_API int kraken_hip_context_set_stream(kraken_hip_context* context, void* hip_stream);
+KRAKEN_API void* kraken_hip_context_stream(const kraken_hip_context* context);
+
+/* Status::message() of the last non-OK call on this thread ("" if none). */
+KRAKEN_API const char* kraken_hip_last_error(void);
+
+/* MpsContext::begin_graph / commit_graph / abort_graph (mps_backend.hpp:90-94;
+ * mps_backend.mm:4430-4459).  begin while active -> KRAKEN_INVALID_ARGUMENT;
+ * commit without begin -> KRAKEN_OK. */
+KRAKEN_API int kraken_hip_begin_graph(kraken_hip_context* context);
+KRAKEN_API int kraken_hip_commit_graph(kraken_hip_context* context);
+KRAKEN_API void kraken_hip_abort_graph(kraken_hip_context* context);
+
+/* MpsContext::make_buffer (mps_backend.hpp:96): device allocation owned by the caller
+ * until kraken_hip_free_buffer. */
+KRAKEN_API int kraken_hip_make_buffer(kraken_hip_context* context, size_t byte_size,
+                                      kraken_buffer* out_buffer);
+KRAKEN_API int kraken_hip_free_buffer(kraken_hip_context* context, kraken_buffer* buffer);
+
+/* MpsContext::copy_to_buffer[_at] / copy_from_buffer[_at] / copy_buffer_region /
+ * zero_buffer (mps_backend.hpp:97-114; mps_backend.mm:5763-5874).  Host copies
+ * first finish pending work, as the reference commits the open graph. */
+KRAKEN_API int kraken_hip_copy_to_buffer(kraken_hip_context* context, kraken_buffer buffer,
+                                         const void* data, size_t byte_size);
+KRAKEN_API int kraken_hip_copy_to_buffer_at(kraken_hip_context* context, kraken_buffer buffer,
+                                            size_t destination_offset, const void* data,
+                                            size_t byte_size);
+KRAKEN_API int kraken_hip_copy_from_buffer(kraken_hip_context* context, kraken_buffer buffer,
+                                           void* data, size_t byte_size);
+KRAKEN_API int kraken_hip_copy_from_buffer_at(kraken_hip_context* context,
+                                              kraken_buffer buffer, size_t source_offset,
+                                              void* data, size_t byte_size);
+KRAKEN_API int kraken_hip_copy_buffer_region(kraken_hip_context* context, kraken_buffer source,
+                                             kraken_buffer destination, size_t source_offset,
+                                             size_t destination_offset, size_t byte_size);
+KRAKEN_API int kraken_hip_zero_buffer(kraken_hip_context* context, kraken_buffer buffer,
+                                      size_t byte_size);
+
+/* ------------------------------------------------------- attention ------ */
+
+/* MpsContext::attention_f32_batched_f16_kv (mps_backend.hpp:415-420;
+ * mps_backend.mm:10619-10869).  query f32 [tokens][heads][head_dim]; key/value cache
+ * f16 [layers][capacity_tokens][kv_heads][head_dim]; output f32 like query.  Query
+ * token t sits at position start_position + t and attends cache keys 0..position of
+ * `layer` (causal; the chunk's own K/V must already be in the cache).
+ * Dispatch: head_dim 256 with tokens >= 64 runs the flash256 MFMA prefill kernel
+ * (Q rounded to f16, as mps_backend.mm:3458-3461); otherwise the split-K decode
+ * kernel (f32 Q, mps_backend.mm:2943-3008).  KRAKEN_QWEN35_FLASH_ATTENTION=0/1
+ * forces the choice like mps_backend.mm:3716-3733. */
+KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key_cache,
+  kraken_buffer value_cache, size_t layer, size_t start_position, size_t tokens,
+  size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+  kraken_buffer output);
+
+/* MpsContext::attention_f32_batched (mps_backend.hpp:404-414; F32 KV twin,
+ * mps_backend.mm:2879-2941): same contract with an f32 cache. */
+KRAKEN_API int kraken_hip_attention_f32_batched(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key_cache,
+  kraken_buffer value_cache, size_t layer, size_t start_position, size_t tokens,
+  size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+  kraken_buffer output);
+
+/* attention_f32_batched_f16_kv followed by the full-attention output gate
+ * out *= sigmoid(gate) (qwen35_runtime.cpp:3333-3355: the attention call, then
+ * sigmoid_f32_in_place and mul_f32_in_place), fused into the attention epilogue.
+ * gate f32 [tokens][heads][head_dim]. */
+KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv_gated(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key_cache,
+  kraken_buffer value_cache, kraken_buffer gate, size_t layer, size_t start_position,
+  size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+  kraken_buffer output);
+
+/* ------------------------------------------------------ gated delta net -- */
+
+/* MpsContext::gated_delta_net_f32_batched_in_place_at (mps_backend.hpp:296-300;
+ * mps_backend.mm:8517-8701, kernels :2225-2374).  q,k f32 [tokens][key_heads][D],
+ * v f32 [tokens][value_heads][D], gate/beta f32 [tokens][value_heads], state f32
+ * [value_heads][D][D] at element offset state_offset, output [tokens][value_heads][D].
+ * key_head = head % key_heads; scale 1/sqrt(D).  The state is updated in place. */
+KRAKEN_API int kraken_hip_gated_delta_net_f32_batched_in_place_at(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key, kraken_buffer value,
+  kraken_buffer gate, kraken_buffer beta, kraken_buffer state, size_t state_offset,
+  size_t tokens, size_t key_heads, size_t value_heads, size_t head_dim, kraken_buffer output);
+
+/* MpsContext::gated_delta_net_f32_batched_in_place (mps_backend.hpp:291-295):
+ * state_offset 0. */
+KRAKEN_API int kraken_hip_gated_delta_net_f32_batched_in_place(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key, kraken_buffer value,
+  kraken_buffer gate, kraken_buffer beta, kraken_buffer state, size_t tokens,
+  size_t key_heads, size_t value_heads, size_t head_dim, kraken_buffer output);
+
+/* MpsContext::gated_delta_net_f32_in_place[_at] (mps_backend.hpp:270-289; one
+ * token, mps_backend.mm:2155-2223). */
+KRAKEN_API int kraken_hip_gated_delta_net_f32_in_place_at(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key, kraken_buffer value,
+  kraken_buffer gate, kraken_buffer beta, kraken_buffer state, size_t state_offset,
+  size_t key_heads, size_t value_heads, size_t head_dim, kraken_buffer output);
+
+/* MpsContext::ssm_conv_f32 (mps_backend.hpp:301-307; mps_backend.mm:2376-2400,
+ * 8703-8796).  input [sequences][channels][K-1+tokens], kernel [channels][K],
+ * output [sequences][tokens][channels]. */
+KRAKEN_API int kraken_hip_ssm_conv_f32(kraken_hip_context* context, kraken_buffer input,
+                                       kraken_buffer kernel, size_t conv_kernel,
+                                       size_t channels, size_t tokens, size_t sequences,
+                                       kraken_buffer output);
+
+/* MpsContext::build_ssm_conv_state_f32 (mps_backend.hpp:308-314;
+ * mps_backend.mm:2428-2457, 8801-8912).  state [channels][K-1] at element offset
+ * state_offset, input [tokens][channels], conv_input [channels][K-1+tokens]. */
+KRAKEN_API int kraken_hip_build_ssm_conv_state_f32(kraken_hip_context* context,
+                                                   kraken_buffer state, size_t state_offset,
+                                                   kraken_buffer input, size_t conv_kernel,
+                                                   size_t channels, size_t tokens,
+                                                   kraken_buffer conv_input);
+
+/* MpsContext::ssm_conv1_f32_stateful_at (mps_backend.hpp:315-327;
+ * mps_backend.mm:2402-2426). */
+KRAKEN_API int kraken_hip_ssm_conv1_f32_stateful_at(kraken_hip_context* context,
+                                                    kraken_buffer state, size_t state_offset,
+                                                    kraken_buffer input, kraken_buffer kernel,
+                                                    size_t conv_kernel, size_t channels,
+                                                    kraken_buffer output);
+
+/* The linear-attention prologue of run_qwen35_linear_layer_chunk
+ * (qwen35_runtime.cpp:2746-2796): build_ssm_conv_state_f32 + ssm_conv_f32 +
+ * silu_f32_in_place + split_qkv_l2_norm_f32_qwen35 fused in one kernel.  qkv
+ * [tokens][2*key_heads*D + value_heads*D] (the conv input projection), conv_state
+ * [channels][K-1] at state_offset (updated), conv_kernel_weights [channels][K];
+ * writes q,k (L2-normalised) [tokens][key_heads][D] and v [tokens][value_heads][D]. */
+KRAKEN_API int kraken_hip_qwen35_conv_split_l2_f32(
+  kraken_hip_context* context, kraken_buffer qkv, kraken_buffer conv_state,
+  size_t state_offset, kraken_buffer conv_kernel_weights, size_t conv_kernel, size_t tokens,
+  size_t key_heads, size_t value_heads, size_t head_dim, float eps, kraken_buffer query,
+  kraken_buffer key, kraken_buffer value);
+
+/* The recurrent core of run_qwen35_linear_layer_chunk (qwen35_runtime.cpp:2913-3008):
+ * prepare_qwen35_gdn_gate_beta_f32 + gated_delta_net_f32_batched_in_place_at +
+ * qwen35_norm_gated_f32_in_place fused.  alpha/beta_raw [tokens][value_heads] are the
+ * raw projections (not modified), dt_bias/ssm_a [value_heads], z [tokens][value_heads][D]
+ * the output gate, norm_weight [D]; output receives RMSNorm(y)*w*silu(z). */
+KRAKEN_API int kraken_hip_qwen35_gdn_gated_f32(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key, kraken_buffer value,
+  kraken_buffer alpha, kraken_buffer beta_raw, kraken_buffer dt_bias, kraken_buffer ssm_a,
+  kraken_buffer z, kraken_buffer norm_weight, kraken_buffer state, size_t state_offset,
+  size_t tokens, size_t key_heads, size_t value_heads, size_t head_dim, float eps,
+  kraken_buffer output);
+
+/* ---------------------------------------------- prologue / epilogue ops -- */
+
+/* MpsContext::split_qkv_l2_norm_f32_qwen35 (mps_backend.hpp:266-269;
+ * mps_backend.mm:2097-2153). */
+KRAKEN_API int kraken_hip_split_qkv_l2_norm_f32_qwen35(
+  kraken_hip_context* context, kraken_buffer source, kraken_buffer query, kraken_buffer key,
+  kraken_buffer value, size_t tokens, size_t key_heads, size_t value_heads, size_t head_dim,
+  float eps);
+
+/* MpsContext::l2_norm_f32_in_place (mps_backend.hpp:262-265; mps_backend.mm:2065-2095). */
+KRAKEN_API int kraken_hip_l2_norm_f32_in_place(kraken_hip_context* context,
+                                               kraken_buffer values, size_t rows,
+                                               size_t row_size, float eps);
+
+/* MpsContext::qk_norm_f32_f32_batched (mps_backend.hpp:252-257;
+ * mps_backend.mm:1991-2024). */
+KRAKEN_API int kraken_hip_qk_norm_f32_f32_batched(kraken_hip_context* context,
+                                                  kraken_buffer values, kraken_buffer weight,
+                                                  size_t tokens, size_t heads,
+                                                  size_t head_dim, float eps);
+
+/* MpsContext::qwen35_norm_gated_f32_in_place (mps_backend.hpp:258-261;
+ * mps_backend.mm:2026-2063). */
+KRAKEN_API int kraken_hip_qwen35_norm_gated_f32_in_place(
+  kraken_hip_context* context, kraken_buffer values, kraken_buffer weight, kraken_buffer gate,
+  size_t tokens, size_t heads, size_t head_dim, float eps);
+
+/* MpsContext::prepare_qwen35_gdn_gate_beta_f32 (mps_backend.hpp:356-358;
+ * mps_backend.mm:2588-2605). */
+KRAKEN_API int kraken_hip_prepare_qwen35_gdn_gate_beta_f32(
+  kraken_hip_context* context, kraken_buffer gate, kraken_buffer beta,
+  kraken_buffer gate_bias, kraken_buffer gate_scale, size_t rows, size_t row_size);
+
+/* MpsContext::mrope_f32_in_place (mps_backend.hpp:331-341; mps_backend.mm:2482-2527).
+ * positions int32 [4][tokens]. */
+KRAKEN_API int kraken_hip_mrope_f32_in_place(kraken_hip_context* context,
+                                             kraken_buffer values, kraken_buffer positions,
+                                             size_t tokens, size_t heads, size_t head_dim,
+                                             size_t n_dims, size_t section_0,
+                                             size_t section_1, size_t section_2,
+                                             size_t section_3, float theta);
+
+/* MpsContext::copy_f32_rows_to_f16 / copy_f32_rows / copy_f16_rows
+ * (mps_backend.hpp:366-383; mps_backend.mm:2627-2679): strided row copies in
+ * element units; the f16 variant rounds to nearest even. */
+KRAKEN_API int kraken_hip_copy_f32_rows_to_f16(kraken_hip_context* context,
+                                               kraken_buffer source, kraken_buffer destination,
+                                               size_t rows, size_t row_size,
+                                               size_t source_stride, size_t source_offset,
+                                               size_t destination_stride,
+                                               size_t destination_offset);
+KRAKEN_API int kraken_hip_copy_f32_rows(kraken_hip_context* context, kraken_buffer source,
+                                        kraken_buffer destination, size_t rows,
+                                        size_t row_size, size_t source_stride,
+                                        size_t source_offset, size_t destination_stride,
+                                        size_t destination_offset);
+KRAKEN_API int kraken_hip_copy_f16_rows(kraken_hip_context* context, kraken_buffer source,
+                                        kraken_buffer destination, size_t rows,
+                                        size_t row_size, size_t source_stride,
+                                        size_t source_offset, size_t destination_stride,
+                                        size_t destination_offset);
+
+/* Elementwise ops: MpsContext::sigmoid_f32_in_place / softplus_f32_in_place /
+ * silu_f32_in_place / mul_f32_in_place / add_f32_row_in_place / mul_f32_row_in_place
+ * (mps_backend.hpp:344-359; mps_backend.mm:2539-2618). */
+KRAKEN_API int kraken_hip_sigmoid_f32_in_place(kraken_hip_context* context,
+                                               kraken_buffer values, size_t size);
+KRAKEN_API int kraken_hip_softplus_f32_in_place(kraken_hip_context* context,
+                                                kraken_buffer values, size_t size);
+KRAKEN_API int kraken_hip_silu_f32_in_place(kraken_hip_context* context,
+                                            kraken_buffer values, size_t size);
+KRAKEN_API int kraken_hip_mul_f32_in_place(kraken_hip_context* context, kraken_buffer target,
+                                           kraken_buffer rhs, size_t size);
+KRAKEN_API int kraken_hip_add_f32_row_in_place(kraken_hip_context* context,
+                                               kraken_buffer target, kraken_buffer row,
+                                               size_t rows, size_t row_size);
+KRAKEN_API int kraken_hip_mul_f32_row_in_place(kraken_hip_context* context,
+                                               kraken_buffer target, kraken_buffer row,
+                                               size_t rows, size_t row_size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KRAKEN_HIP_H */

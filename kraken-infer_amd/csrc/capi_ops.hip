@@ -1,0 +1,794 @@
+// C-ABI operator entry points: argument validation in the reference's order,
+// then dispatch to the kernel launchers.  Messages follow the reference's
+// wording with the "HIP" prefix in place of "MPS" (mps_backend.mm host
+// dispatchers cited per function).
+#include <hip/hip_runtime.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "context_internal.hpp"
+
+using namespace kraken;
+
+#define KRAKEN_TRY(expr)            \
+  do {                              \
+    const int kraken_s_ = (expr);   \
+    if (kraken_s_ != KRAKEN_OK) {   \
+      return kraken_s_;             \
+    }                               \
+  } while (0)
+
+namespace {
+
+enum class FlashChoice { automatic, force_on, force_off };
+
+// flash_attention_env_flag (mps_backend.mm:3716-3733): KRAKEN_QWEN35_FLASH_ATTENTION
+// "1"/"true"/"on" forces flash, "0"/"false"/"off" disables it.
+FlashChoice flash_env() {
+  const char* v = std::getenv("KRAKEN_QWEN35_FLASH_ATTENTION");
+  if (v == nullptr) {
+    return FlashChoice::automatic;
+  }
+  if (!std::strcmp(v, "1") || !std::strcmp(v, "true") || !std::strcmp(v, "on")) {
+    return FlashChoice::force_on;
+  }
+  if (!std::strcmp(v, "0") || !std::strcmp(v, "false") || !std::strcmp(v, "off")) {
+    return FlashChoice::force_off;
+  }
+  return FlashChoice::automatic;
+}
+
+// attention_f32_batched[_f16_kv] host side (mps_backend.mm:10360-10617, 10619-10869).
+int attention_entry(kraken_hip_context* ctx, const char* what, bool kv_f16,
+                    const kraken_buffer& query, const kraken_buffer& key_cache,
+                    const kraken_buffer& value_cache, const kraken_buffer* gate, size_t layer,
+                    size_t start_position, size_t tokens, size_t capacity_tokens, size_t heads,
+                    size_t kv_heads, size_t head_dim, const kraken_buffer& output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string w = std::string("HIP ") + what;
+  if (tokens == 0 || heads == 0 || kv_heads == 0 || head_dim == 0 || capacity_tokens == 0) {
+    return invalid(w + " dimensions must be positive");
+  }
+  if (heads % kv_heads != 0) {
+    return invalid(w + " heads must be divisible by kv_heads");
+  }
+  if (head_dim > 256u) {
+    return invalid(w + " head_dim exceeds 256");
+  }
+  size_t key_count = 0;
+  if (!checked_add(start_position, tokens, key_count) || key_count > capacity_tokens) {
+    return invalid(w + " chunk exceeds KV cache capacity");
+  }
+  size_t attn_dim = 0, kv_dim = 0, query_values = 0, cache_layers = 0, cache_values = 0;
+  if (!checked_mul(heads, head_dim, attn_dim) || !checked_mul(kv_heads, head_dim, kv_dim) ||
+      !checked_mul(tokens, attn_dim, query_values) || layer == SIZE_MAX ||
+      !checked_mul(layer + 1u, capacity_tokens, cache_layers) ||
+      !checked_mul(cache_layers, kv_dim, cache_values)) {
+    return invalid(w + " value count overflow");
+  }
+  const std::string nq = std::string(what) + " query";
+  const std::string nk = std::string(what) + " key cache";
+  const std::string nv = std::string(what) + " value cache";
+  const std::string ng = std::string(what) + " gate";
+  const std::string no = std::string(what) + " output";
+  KRAKEN_TRY(validate_f32(query, query_values, nq.c_str()));
+  const size_t elem = kv_f16 ? sizeof(uint16_t) : sizeof(float);
+  KRAKEN_TRY(validate_buffer(key_cache, cache_values, elem, nk.c_str()));
+  KRAKEN_TRY(validate_buffer(value_cache, cache_values, elem, nv.c_str()));
+  if (gate != nullptr) {
+    KRAKEN_TRY(validate_f32(*gate, query_values, ng.c_str()));
+  }
+  KRAKEN_TRY(validate_f32(output, query_values, no.c_str()));
+  const std::string nl = std::string(what) + " layer";
+  const std::string ns = std::string(what) + " start position";
+  const std::string nt = std::string(what) + " tokens";
+  const std::string nc = std::string(what) + " capacity";
+  const std::string nh = std::string(what) + " heads";
+  const std::string nkv = std::string(what) + " kv_heads";
+  const std::string nd = std::string(what) + " head_dim";
+  const std::string ngr = std::string(what) + " group";
+  KRAKEN_TRY(check_u32(layer, nl.c_str()));
+  KRAKEN_TRY(check_u32(start_position, ns.c_str()));
+  KRAKEN_TRY(check_u32(tokens, nt.c_str()));
+  KRAKEN_TRY(check_u32(capacity_tokens, nc.c_str()));
+  KRAKEN_TRY(check_u32(heads, nh.c_str()));
+  KRAKEN_TRY(check_u32(kv_heads, nkv.c_str()));
+  KRAKEN_TRY(check_u32(head_dim, nd.c_str()));
+  KRAKEN_TRY(check_u32(heads / kv_heads, ngr.c_str()));
+
+  AttentionArgs a{};
+  a.query = static_cast<const float*>(query.data);
+  a.key_cache = key_cache.data;
+  a.value_cache = value_cache.data;
+  a.gate = gate != nullptr ? static_cast<const float*>(gate->data) : nullptr;
+  a.output = static_cast<float*>(output.data);
+  a.layer = (uint32_t)layer;
+  a.start_position = (uint32_t)start_position;
+  a.tokens = (uint32_t)tokens;
+  a.capacity_tokens = (uint32_t)capacity_tokens;
+  a.heads = (uint32_t)heads;
+  a.kv_heads = (uint32_t)kv_heads;
+  a.head_dim = (uint32_t)head_dim;
+  a.kv_f16 = kv_f16;
+
+  // Dispatch rule of the reference: flash for head_dim 256 and tokens >= 64,
+  // overridable through the environment (mps_backend.mm:10715-10722).
+  const FlashChoice choice = flash_env();
+  const bool flash_ok = flash_prefill_supported(a);
+  const bool use_flash = flash_ok && choice != FlashChoice::force_off &&
+                         (choice == FlashChoice::force_on || tokens >= 64u);
+
+  KRAKEN_TRY(begin_launch(ctx));
+  const size_t need = use_flash ? attention_flash_workspace_bytes(a, ctx->cu_count)
+                                : attention_decode_workspace_bytes(a, ctx->cu_count);
+  KRAKEN_TRY(ensure_workspace(ctx, need));
+  const hipError_t e =
+    use_flash ? launch_attention_flash(a, ctx->cu_count, ctx->workspace, ctx->workspace_bytes,
+                                       ctx->stream)
+              : launch_attention_decode(a, ctx->cu_count, ctx->workspace, ctx->workspace_bytes,
+                                        ctx->stream);
+  if (e != hipSuccess) {
+    return internal(w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (w + " command failed: ").c_str());
+}
+
+// gated_delta_net_f32_batched_in_place_at host side (mps_backend.mm:8517-8600).
+int gdn_entry(kraken_hip_context* ctx, const char* what, const kraken_buffer& query,
+              const kraken_buffer& key, const kraken_buffer& value, const kraken_buffer& gate,
+              const kraken_buffer& beta, const kraken_buffer& state, size_t state_offset,
+              size_t tokens, size_t key_heads, size_t value_heads, size_t head_dim,
+              const kraken_buffer& output, const kraken_buffer* dt_bias,
+              const kraken_buffer* ssm_a, const kraken_buffer* z, const kraken_buffer* norm_w,
+              float eps) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string w = std::string("HIP ") + what;
+  if (tokens == 0 || key_heads == 0 || value_heads == 0 || head_dim == 0) {
+    return invalid(w + " dimensions must be positive");
+  }
+  if (value_heads % key_heads != 0) {
+    return invalid(w + " value heads must repeat key heads");
+  }
+  if (head_dim > 256u) {
+    return invalid(w + " head_dim exceeds 256");
+  }
+  size_t kvpt = 0, vvpt = 0, key_values = 0, value_values = 0, gate_values = 0, state_values = 0;
+  if (!checked_mul(key_heads, head_dim, kvpt) || !checked_mul(value_heads, head_dim, vvpt) ||
+      !checked_mul(tokens, kvpt, key_values) || !checked_mul(tokens, vvpt, value_values) ||
+      !checked_mul(tokens, value_heads, gate_values) ||
+      !checked_mul(vvpt, head_dim, state_values)) {
+    return invalid(w + " value count overflow");
+  }
+  const std::string base(what);
+  KRAKEN_TRY(validate_f32(query, key_values, (base + " query").c_str()));
+  KRAKEN_TRY(validate_f32(key, key_values, (base + " key").c_str()));
+  KRAKEN_TRY(validate_f32(value, value_values, (base + " value").c_str()));
+  KRAKEN_TRY(validate_f32(gate, gate_values, (base + " gate").c_str()));
+  KRAKEN_TRY(validate_f32(beta, gate_values, (base + " beta").c_str()));
+  if (dt_bias != nullptr) {
+    KRAKEN_TRY(validate_f32(*dt_bias, value_heads, (base + " dt bias").c_str()));
+    KRAKEN_TRY(validate_f32(*ssm_a, value_heads, (base + " ssm a").c_str()));
+    KRAKEN_TRY(validate_f32(*z, value_values, (base + " z").c_str()));
+    KRAKEN_TRY(validate_f32(*norm_w, head_dim, (base + " norm weight").c_str()));
+  }
+  KRAKEN_TRY(validate_f32_region(state, state_offset, state_values, (base + " state").c_str()));
+  KRAKEN_TRY(validate_f32(output, value_values, (base + " output").c_str()));
+  KRAKEN_TRY(check_u32(tokens, (base + " tokens").c_str()));
+  KRAKEN_TRY(check_u32(key_heads, (base + " key_heads").c_str()));
+  KRAKEN_TRY(check_u32(value_heads, (base + " value_heads").c_str()));
+  KRAKEN_TRY(check_u32(head_dim, (base + " head_dim").c_str()));
+  KRAKEN_TRY(begin_launch(ctx));
+  GdnArgs a{};
+  a.query = static_cast<const float*>(query.data);
+  a.key = static_cast<const float*>(key.data);
+  a.value = static_cast<const float*>(value.data);
+  a.gate = static_cast<const float*>(gate.data);
+  a.beta = static_cast<const float*>(beta.data);
+  a.state = static_cast<float*>(state.data) + state_offset;
+  a.output = static_cast<float*>(output.data);
+  a.tokens = (uint32_t)tokens;
+  a.key_heads = (uint32_t)key_heads;
+  a.value_heads = (uint32_t)value_heads;
+  a.head_dim = (uint32_t)head_dim;
+  if (dt_bias != nullptr) {
+    a.dt_bias = static_cast<const float*>(dt_bias->data);
+    a.ssm_a = static_cast<const float*>(ssm_a->data);
+    a.z = static_cast<const float*>(z->data);
+    a.norm_weight = static_cast<const float*>(norm_w->data);
+    a.eps = eps;
+  }
+  const hipError_t e = launch_gated_delta_net(a, ctx->cu_count, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (w + " command failed: ").c_str());
+}
+
+// qk_norm_f32_f32_batched / qwen35_norm_gated_f32_in_place host side
+// (mps_backend.mm:8050-8210).
+int rms_heads_entry(kraken_hip_context* ctx, const char* what, const kraken_buffer& values,
+                    const kraken_buffer& weight, const kraken_buffer* gate, size_t tokens,
+                    size_t heads, size_t head_dim, float eps) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string w = std::string("HIP ") + what;
+  if (tokens == 0 || heads == 0 || head_dim == 0) {
+    return invalid(w + " dimensions must be positive");
+  }
+  const std::string base(what);
+  KRAKEN_TRY(check_u32(tokens, (base + " tokens").c_str()));
+  KRAKEN_TRY(check_u32(heads, (base + " heads").c_str()));
+  KRAKEN_TRY(check_u32(head_dim, (base + " head_dim").c_str()));
+  if (head_dim > 256u) {
+    // One wave holds a whole head row (4 values per lane); the Metal kernel's
+    // 256-thread groups have the same bound (mps_backend.mm:8090-8093).
+    return invalid(w + " head_dim exceeds 256");
+  }
+  size_t head_values = 0, values_count = 0;
+  if (!checked_mul(heads, head_dim, head_values) ||
+      !checked_mul(tokens, head_values, values_count)) {
+    return invalid(w + " value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(values, values_count, (base + " values").c_str()));
+  if (gate != nullptr) {
+    KRAKEN_TRY(validate_f32(*gate, values_count, (base + " gate").c_str()));
+  }
+  KRAKEN_TRY(validate_f32(weight, head_dim, (base + " weight").c_str()));
+  if (!fits_u32(tokens * heads)) {
+    return invalid(w + " rows exceed uint32 range");
+  }
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_rms_norm_heads(
+    static_cast<float*>(values.data), static_cast<const float*>(weight.data),
+    gate != nullptr ? static_cast<const float*>(gate->data) : nullptr, (uint32_t)tokens,
+    (uint32_t)heads, (uint32_t)head_dim, eps, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (w + " command failed: ").c_str());
+}
+
+// copy_f32_rows / copy_f32_rows_to_f16 / copy_f16_rows host side
+// (mps_backend.mm:9694-9998).
+int copy_rows_entry(kraken_hip_context* ctx, CopyKind kind, const char* what,
+                    const kraken_buffer& source, const kraken_buffer& destination, size_t rows,
+                    size_t row_size, size_t source_stride, size_t source_offset,
+                    size_t destination_stride, size_t destination_offset) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string base(what);
+  size_t source_end = 0, destination_end = 0;
+  KRAKEN_TRY(strided_region_end(source_offset, rows, source_stride, row_size,
+                                (base + " source").c_str(), source_end));
+  KRAKEN_TRY(strided_region_end(destination_offset, rows, destination_stride, row_size,
+                                (base + " destination").c_str(), destination_end));
+  size_t total = 0;
+  if (!checked_mul(rows, row_size, total)) {
+    return invalid("HIP " + base + " value count overflow");
+  }
+  KRAKEN_TRY(check_u32(source_offset, (base + " source offset").c_str()));
+  KRAKEN_TRY(check_u32(destination_offset, (base + " destination offset").c_str()));
+  KRAKEN_TRY(check_u32(source_stride, (base + " source stride").c_str()));
+  KRAKEN_TRY(check_u32(destination_stride, (base + " destination stride").c_str()));
+  KRAKEN_TRY(check_u32(row_size, (base + " row size").c_str()));
+  KRAKEN_TRY(check_u32(total, (base + " total").c_str()));
+  const size_t src_elem = kind == CopyKind::f16 ? sizeof(uint16_t) : sizeof(float);
+  const size_t dst_elem = kind == CopyKind::f32 ? sizeof(float) : sizeof(uint16_t);
+  KRAKEN_TRY(validate_buffer(source, source_end, src_elem, (base + " source").c_str()));
+  KRAKEN_TRY(
+    validate_buffer(destination, destination_end, dst_elem, (base + " destination").c_str()));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e =
+    launch_copy_rows(kind, source.data, destination.data, rows, row_size, source_stride,
+                     source_offset, destination_stride, destination_offset, ctx->stream);
+  if (e != hipSuccess) {
+    return internal("HIP " + base + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, ("HIP " + base + " command failed: ").c_str());
+}
+
+int unary_entry(kraken_hip_context* ctx, UnaryKind kind, const char* what,
+                const kraken_buffer& values, size_t size) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string base(what);
+  KRAKEN_TRY(check_u32(size, (base + " size").c_str()));
+  KRAKEN_TRY(validate_f32(values, size, (base + " values").c_str()));
+  KRAKEN_TRY(begin_launch(ctx));
+  if (size == 0) {
+    return KRAKEN_OK;
+  }
+  const hipError_t e = launch_unary(kind, static_cast<float*>(values.data), size, ctx->stream);
+  if (e != hipSuccess) {
+    return internal("HIP " + base + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, ("HIP " + base + " command failed: ").c_str());
+}
+
+int binary_entry(kraken_hip_context* ctx, BinaryKind kind, const char* what,
+                 const kraken_buffer& target, const kraken_buffer& rhs, size_t rows,
+                 size_t row_size, bool rowwise) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string base(what);
+  size_t total = rows;
+  if (rowwise) {
+    if (rows == 0 || row_size == 0) {
+      return invalid("HIP " + base + " dimensions must be positive");
+    }
+    if (!checked_mul(rows, row_size, total)) {
+      return invalid("HIP " + base + " value count overflow");
+    }
+    KRAKEN_TRY(check_u32(row_size, (base + " row size").c_str()));
+  }
+  KRAKEN_TRY(check_u32(total, (base + " size").c_str()));
+  KRAKEN_TRY(validate_f32(target, total, (base + " target").c_str()));
+  KRAKEN_TRY(validate_f32(rhs, rowwise ? row_size : total, (base + " rhs").c_str()));
+  KRAKEN_TRY(begin_launch(ctx));
+  if (total == 0) {
+    return KRAKEN_OK;
+  }
+  const hipError_t e = launch_binary(kind, static_cast<float*>(target.data),
+                                     static_cast<const float*>(rhs.data), total,
+                                     rowwise ? row_size : 1, ctx->stream);
+  if (e != hipSuccess) {
+    return internal("HIP " + base + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, ("HIP " + base + " command failed: ").c_str());
+}
+
+}  // namespace
+
+extern "C" {
+
+KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key_cache,
+  kraken_buffer value_cache, size_t layer, size_t start_position, size_t tokens,
+  size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim, kraken_buffer output) {
+  return attention_entry(ctx, "F16 KV batched attention", true, query, key_cache, value_cache,
+                         nullptr, layer, start_position, tokens, capacity_tokens, heads,
+                         kv_heads, head_dim, output);
+}
+
+KRAKEN_API int kraken_hip_attention_f32_batched(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key_cache,
+  kraken_buffer value_cache, size_t layer, size_t start_position, size_t tokens,
+  size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim, kraken_buffer output) {
+  return attention_entry(ctx, "batched attention", false, query, key_cache, value_cache,
+                         nullptr, layer, start_position, tokens, capacity_tokens, heads,
+                         kv_heads, head_dim, output);
+}
+
+KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv_gated(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key_cache,
+  kraken_buffer value_cache, kraken_buffer gate, size_t layer, size_t start_position,
+  size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+  kraken_buffer output) {
+  return attention_entry(ctx, "gated F16 KV batched attention", true, query, key_cache,
+                         value_cache, &gate, layer, start_position, tokens, capacity_tokens,
+                         heads, kv_heads, head_dim, output);
+}
+
+KRAKEN_API int kraken_hip_gated_delta_net_f32_batched_in_place_at(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key, kraken_buffer value,
+  kraken_buffer gate, kraken_buffer beta, kraken_buffer state, size_t state_offset,
+  size_t tokens, size_t key_heads, size_t value_heads, size_t head_dim, kraken_buffer output) {
+  return gdn_entry(ctx, "batched gated delta net", query, key, value, gate, beta, state,
+                   state_offset, tokens, key_heads, value_heads, head_dim, output, nullptr,
+                   nullptr, nullptr, nullptr, 0.0f);
+}
+
+KRAKEN_API int kraken_hip_gated_delta_net_f32_batched_in_place(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key, kraken_buffer value,
+  kraken_buffer gate, kraken_buffer beta, kraken_buffer state, size_t tokens, size_t key_heads,
+  size_t value_heads, size_t head_dim, kraken_buffer output) {
+  return gdn_entry(ctx, "batched gated delta net", query, key, value, gate, beta, state, 0,
+                   tokens, key_heads, value_heads, head_dim, output, nullptr, nullptr, nullptr,
+                   nullptr, 0.0f);
+}
+
+KRAKEN_API int kraken_hip_gated_delta_net_f32_in_place_at(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key, kraken_buffer value,
+  kraken_buffer gate, kraken_buffer beta, kraken_buffer state, size_t state_offset,
+  size_t key_heads, size_t value_heads, size_t head_dim, kraken_buffer output) {
+  return gdn_entry(ctx, "gated delta net", query, key, value, gate, beta, state, state_offset,
+                   1, key_heads, value_heads, head_dim, output, nullptr, nullptr, nullptr,
+                   nullptr, 0.0f);
+}
+
+KRAKEN_API int kraken_hip_qwen35_gdn_gated_f32(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key, kraken_buffer value,
+  kraken_buffer alpha, kraken_buffer beta_raw, kraken_buffer dt_bias, kraken_buffer ssm_a,
+  kraken_buffer z, kraken_buffer norm_weight, kraken_buffer state, size_t state_offset,
+  size_t tokens, size_t key_heads, size_t value_heads, size_t head_dim, float eps,
+  kraken_buffer output) {
+  return gdn_entry(ctx, "Qwen3.5 gated GDN", query, key, value, alpha, beta_raw, state,
+                   state_offset, tokens, key_heads, value_heads, head_dim, output, &dt_bias,
+                   &ssm_a, &z, &norm_weight, eps);
+}
+
+// ssm_conv_f32 host side (mps_backend.mm:8703-8799).
+KRAKEN_API int kraken_hip_ssm_conv_f32(kraken_hip_context* ctx, kraken_buffer input,
+                                       kraken_buffer kernel, size_t conv_kernel, size_t channels,
+                                       size_t tokens, size_t sequences, kraken_buffer output) {
+  KRAKEN_TRY(check_context(ctx));
+  if (conv_kernel == 0 || channels == 0 || tokens == 0 || sequences == 0) {
+    return invalid("HIP SSM conv dimensions must be positive");
+  }
+  size_t span = 0;
+  if (!checked_add(conv_kernel - 1u, tokens, span)) {
+    return invalid("HIP SSM conv input span overflow");
+  }
+  size_t input_values = 0, kernel_values = 0, output_values = 0;
+  if (!checked_mul(span, channels, input_values) ||
+      !checked_mul(input_values, sequences, input_values) ||
+      !checked_mul(conv_kernel, channels, kernel_values) ||
+      !checked_mul(channels, tokens, output_values) ||
+      !checked_mul(output_values, sequences, output_values)) {
+    return invalid("HIP SSM conv value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(input, input_values, "SSM conv input"));
+  KRAKEN_TRY(validate_f32(kernel, kernel_values, "SSM conv kernel"));
+  KRAKEN_TRY(validate_f32(output, output_values, "SSM conv output"));
+  KRAKEN_TRY(check_u32(conv_kernel, "SSM conv kernel"));
+  KRAKEN_TRY(check_u32(span, "SSM conv input span"));
+  KRAKEN_TRY(check_u32(channels, "SSM conv channels"));
+  KRAKEN_TRY(check_u32(tokens, "SSM conv tokens"));
+  KRAKEN_TRY(check_u32(sequences, "SSM conv sequences"));
+  KRAKEN_TRY(check_u32(output_values, "SSM conv output values"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_ssm_conv(
+    static_cast<const float*>(input.data), static_cast<const float*>(kernel.data),
+    static_cast<float*>(output.data), (uint32_t)conv_kernel, (uint32_t)channels,
+    (uint32_t)tokens, (uint32_t)sequences, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP SSM conv launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP SSM conv command failed: ");
+}
+
+// build_ssm_conv_state_f32 host side (mps_backend.mm:8801-8912).
+KRAKEN_API int kraken_hip_build_ssm_conv_state_f32(kraken_hip_context* ctx, kraken_buffer state,
+                                                   size_t state_offset, kraken_buffer input,
+                                                   size_t conv_kernel, size_t channels,
+                                                   size_t tokens, kraken_buffer conv_input) {
+  KRAKEN_TRY(check_context(ctx));
+  if (conv_kernel < 2 || channels == 0 || tokens == 0) {
+    return invalid("HIP SSM conv-state dimensions are invalid");
+  }
+  size_t span = 0;
+  if (!checked_add(conv_kernel - 1u, tokens, span)) {
+    return invalid("HIP SSM conv-state input span overflow");
+  }
+  size_t state_values = 0, input_values = 0, conv_input_values = 0;
+  if (!checked_mul(conv_kernel - 1u, channels, state_values) ||
+      !checked_mul(tokens, channels, input_values) ||
+      !checked_mul(span, channels, conv_input_values)) {
+    return invalid("HIP SSM conv-state value count overflow");
+  }
+  KRAKEN_TRY(validate_f32_region(state, state_offset, state_values, "SSM conv-state state"));
+  KRAKEN_TRY(validate_f32(input, input_values, "SSM conv-state input"));
+  KRAKEN_TRY(validate_f32(conv_input, conv_input_values, "SSM conv-state conv input"));
+  KRAKEN_TRY(check_u32(conv_kernel, "SSM conv-state kernel"));
+  KRAKEN_TRY(check_u32(channels, "SSM conv-state channels"));
+  KRAKEN_TRY(check_u32(tokens, "SSM conv-state tokens"));
+  KRAKEN_TRY(check_u32(span, "SSM conv-state input span"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_build_ssm_conv_state(
+    static_cast<float*>(state.data) + state_offset, static_cast<const float*>(input.data),
+    static_cast<float*>(conv_input.data), (uint32_t)conv_kernel, (uint32_t)channels,
+    (uint32_t)tokens, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP SSM conv-state launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP SSM conv-state command failed: ");
+}
+
+// ssm_conv1_f32_stateful_at host side (mps_backend.mm:8914-8990).
+KRAKEN_API int kraken_hip_ssm_conv1_f32_stateful_at(kraken_hip_context* ctx, kraken_buffer state,
+                                                    size_t state_offset, kraken_buffer input,
+                                                    kraken_buffer kernel, size_t conv_kernel,
+                                                    size_t channels, kraken_buffer output) {
+  KRAKEN_TRY(check_context(ctx));
+  if (conv_kernel < 2 || channels == 0) {
+    return invalid("HIP stateful SSM conv dimensions are invalid");
+  }
+  size_t state_values = 0, kernel_values = 0;
+  if (!checked_mul(conv_kernel - 1u, channels, state_values) ||
+      !checked_mul(conv_kernel, channels, kernel_values)) {
+    return invalid("HIP stateful SSM conv value count overflow");
+  }
+  KRAKEN_TRY(validate_f32_region(state, state_offset, state_values, "stateful SSM conv state"));
+  KRAKEN_TRY(validate_f32(input, channels, "stateful SSM conv input"));
+  KRAKEN_TRY(validate_f32(kernel, kernel_values, "stateful SSM conv kernel"));
+  KRAKEN_TRY(validate_f32(output, channels, "stateful SSM conv output"));
+  KRAKEN_TRY(check_u32(conv_kernel, "stateful SSM conv kernel"));
+  KRAKEN_TRY(check_u32(channels, "stateful SSM conv channels"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_ssm_conv1_stateful(
+    static_cast<float*>(state.data) + state_offset, static_cast<const float*>(input.data),
+    static_cast<const float*>(kernel.data), static_cast<float*>(output.data),
+    (uint32_t)conv_kernel, (uint32_t)channels, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP stateful SSM conv launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP stateful SSM conv command failed: ");
+}
+
+// Fused prologue of run_qwen35_linear_layer_chunk (qwen35_runtime.cpp:2746-2796).
+KRAKEN_API int kraken_hip_qwen35_conv_split_l2_f32(
+  kraken_hip_context* ctx, kraken_buffer qkv, kraken_buffer conv_state, size_t state_offset,
+  kraken_buffer conv_kernel_weights, size_t conv_kernel, size_t tokens, size_t key_heads,
+  size_t value_heads, size_t head_dim, float eps, kraken_buffer query, kraken_buffer key,
+  kraken_buffer value) {
+  KRAKEN_TRY(check_context(ctx));
+  if (tokens == 0 || key_heads == 0 || value_heads == 0 || head_dim == 0) {
+    return invalid("HIP Qwen3.5 conv split dimensions must be positive");
+  }
+  if (conv_kernel < 2 || conv_kernel > 8) {
+    return invalid("HIP Qwen3.5 conv split conv_kernel must be in [2, 8]");
+  }
+  if (head_dim > 256u) {
+    return invalid("HIP Qwen3.5 conv split head_dim exceeds 256");
+  }
+  size_t key_dim = 0, value_dim = 0, channels = 0, qkv_values = 0, key_values = 0,
+         value_values = 0, state_values = 0, kernel_values = 0;
+  if (!checked_mul(key_heads, head_dim, key_dim) ||
+      !checked_mul(value_heads, head_dim, value_dim) ||
+      !checked_add(2u * key_dim, value_dim, channels) ||
+      !checked_mul(tokens, channels, qkv_values) || !checked_mul(tokens, key_dim, key_values) ||
+      !checked_mul(tokens, value_dim, value_values) ||
+      !checked_mul(conv_kernel - 1u, channels, state_values) ||
+      !checked_mul(conv_kernel, channels, kernel_values)) {
+    return invalid("HIP Qwen3.5 conv split value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(qkv, qkv_values, "Qwen3.5 conv split qkv"));
+  KRAKEN_TRY(validate_f32_region(conv_state, state_offset, state_values,
+                                 "Qwen3.5 conv split conv state"));
+  KRAKEN_TRY(validate_f32(conv_kernel_weights, kernel_values, "Qwen3.5 conv split kernel"));
+  KRAKEN_TRY(validate_f32(query, key_values, "Qwen3.5 conv split query"));
+  KRAKEN_TRY(validate_f32(key, key_values, "Qwen3.5 conv split key"));
+  KRAKEN_TRY(validate_f32(value, value_values, "Qwen3.5 conv split value"));
+  KRAKEN_TRY(check_u32(tokens, "Qwen3.5 conv split tokens"));
+  KRAKEN_TRY(check_u32(channels, "Qwen3.5 conv split channels"));
+  KRAKEN_TRY(check_u32(qkv_values, "Qwen3.5 conv split qkv values"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_conv_split_l2(
+    static_cast<const float*>(qkv.data), static_cast<float*>(conv_state.data) + state_offset,
+    static_cast<const float*>(conv_kernel_weights.data), (uint32_t)conv_kernel,
+    (uint32_t)tokens, (uint32_t)key_heads, (uint32_t)value_heads, (uint32_t)head_dim, eps,
+    static_cast<float*>(query.data), static_cast<float*>(key.data),
+    static_cast<float*>(value.data), ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP Qwen3.5 conv split launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP Qwen3.5 conv split command failed: ");
+}
+
+// split_qkv_l2_norm_f32_qwen35 host side (mps_backend.mm:8261-8377).
+KRAKEN_API int kraken_hip_split_qkv_l2_norm_f32_qwen35(
+  kraken_hip_context* ctx, kraken_buffer source, kraken_buffer query, kraken_buffer key,
+  kraken_buffer value, size_t tokens, size_t key_heads, size_t value_heads, size_t head_dim,
+  float eps) {
+  KRAKEN_TRY(check_context(ctx));
+  if (tokens == 0 || key_heads == 0 || value_heads == 0 || head_dim == 0) {
+    return invalid("HIP Qwen3.5 split qkv dimensions must be positive");
+  }
+  size_t key_dim = 0, value_dim = 0, doubled = 0, channels = 0;
+  if (!checked_mul(key_heads, head_dim, key_dim) ||
+      !checked_mul(value_heads, head_dim, value_dim) || !checked_mul(2u, key_dim, doubled) ||
+      !checked_add(doubled, value_dim, channels)) {
+    return invalid("HIP Qwen3.5 split qkv channel count overflow");
+  }
+  size_t source_values = 0, key_values = 0, value_values = 0;
+  if (!checked_mul(tokens, channels, source_values) ||
+      !checked_mul(tokens, key_dim, key_values) ||
+      !checked_mul(tokens, value_dim, value_values)) {
+    return invalid("HIP Qwen3.5 split qkv value count overflow");
+  }
+  KRAKEN_TRY(check_u32(tokens, "Qwen3.5 split qkv tokens"));
+  KRAKEN_TRY(check_u32(key_heads, "Qwen3.5 split qkv key heads"));
+  KRAKEN_TRY(check_u32(value_heads, "Qwen3.5 split qkv value heads"));
+  KRAKEN_TRY(check_u32(head_dim, "Qwen3.5 split qkv head dim"));
+  KRAKEN_TRY(check_u32(channels, "Qwen3.5 split qkv conv channels"));
+  KRAKEN_TRY(validate_f32(source, source_values, "Qwen3.5 split qkv source"));
+  KRAKEN_TRY(validate_f32(query, key_values, "Qwen3.5 split qkv query"));
+  KRAKEN_TRY(validate_f32(key, key_values, "Qwen3.5 split qkv key"));
+  KRAKEN_TRY(validate_f32(value, value_values, "Qwen3.5 split qkv value"));
+  if (!fits_u32(tokens * (2u * key_heads + value_heads))) {
+    return invalid("HIP Qwen3.5 split qkv row count exceeds uint32 range");
+  }
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_split_qkv_l2(
+    static_cast<const float*>(source.data), static_cast<float*>(query.data),
+    static_cast<float*>(key.data), static_cast<float*>(value.data), (uint32_t)tokens,
+    (uint32_t)key_heads, (uint32_t)value_heads, (uint32_t)head_dim, eps, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP Qwen3.5 split qkv launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP Qwen3.5 split qkv command failed: ");
+}
+
+// l2_norm_f32_in_place host side (mps_backend.mm:8211-8259).
+KRAKEN_API int kraken_hip_l2_norm_f32_in_place(kraken_hip_context* ctx, kraken_buffer values,
+                                               size_t rows, size_t row_size, float eps) {
+  KRAKEN_TRY(check_context(ctx));
+  if (rows == 0 || row_size == 0) {
+    return invalid("HIP l2 norm dimensions must be positive");
+  }
+  KRAKEN_TRY(check_u32(rows, "l2 norm rows"));
+  KRAKEN_TRY(check_u32(row_size, "l2 norm row size"));
+  size_t total = 0;
+  if (!checked_mul(rows, row_size, total)) {
+    return invalid("HIP l2 norm value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(values, total, "l2 norm values"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_l2_norm(static_cast<float*>(values.data), (uint32_t)rows,
+                                      (uint32_t)row_size, eps, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP l2 norm launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP l2 norm command failed: ");
+}
+
+KRAKEN_API int kraken_hip_qk_norm_f32_f32_batched(kraken_hip_context* ctx, kraken_buffer values,
+                                                  kraken_buffer weight, size_t tokens,
+                                                  size_t heads, size_t head_dim, float eps) {
+  return rms_heads_entry(ctx, "batched qk norm", values, weight, nullptr, tokens, heads,
+                         head_dim, eps);
+}
+
+KRAKEN_API int kraken_hip_qwen35_norm_gated_f32_in_place(kraken_hip_context* ctx,
+                                                         kraken_buffer values,
+                                                         kraken_buffer weight,
+                                                         kraken_buffer gate, size_t tokens,
+                                                         size_t heads, size_t head_dim,
+                                                         float eps) {
+  return rms_heads_entry(ctx, "Qwen3.5 norm-gated", values, weight, &gate, tokens, heads,
+                         head_dim, eps);
+}
+
+// prepare_qwen35_gdn_gate_beta_f32 host side (mps_backend.mm:9468-9540).
+KRAKEN_API int kraken_hip_prepare_qwen35_gdn_gate_beta_f32(
+  kraken_hip_context* ctx, kraken_buffer gate, kraken_buffer beta, kraken_buffer gate_bias,
+  kraken_buffer gate_scale, size_t rows, size_t row_size) {
+  KRAKEN_TRY(check_context(ctx));
+  if (rows == 0 || row_size == 0) {
+    return invalid("HIP Qwen3.5 GDN gate dimensions must be positive");
+  }
+  size_t total = 0;
+  if (!checked_mul(rows, row_size, total)) {
+    return invalid("HIP Qwen3.5 GDN gate value count overflow");
+  }
+  KRAKEN_TRY(check_u32(row_size, "Qwen3.5 GDN gate row size"));
+  KRAKEN_TRY(check_u32(total, "Qwen3.5 GDN gate total"));
+  KRAKEN_TRY(validate_f32(gate, total, "Qwen3.5 GDN gate"));
+  KRAKEN_TRY(validate_f32(beta, total, "Qwen3.5 GDN beta"));
+  KRAKEN_TRY(validate_f32(gate_bias, row_size, "Qwen3.5 GDN gate bias"));
+  KRAKEN_TRY(validate_f32(gate_scale, row_size, "Qwen3.5 GDN gate scale"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_prepare_gate_beta(
+    static_cast<float*>(gate.data), static_cast<float*>(beta.data),
+    static_cast<const float*>(gate_bias.data), static_cast<const float*>(gate_scale.data),
+    (uint32_t)rows, (uint32_t)row_size, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP Qwen3.5 GDN gate launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP Qwen3.5 GDN gate command failed: ");
+}
+
+// mrope_f32_in_place host side (mps_backend.mm:9057-9163).
+KRAKEN_API int kraken_hip_mrope_f32_in_place(kraken_hip_context* ctx, kraken_buffer values,
+                                             kraken_buffer positions, size_t tokens, size_t heads,
+                                             size_t head_dim, size_t n_dims, size_t section_0,
+                                             size_t section_1, size_t section_2,
+                                             size_t section_3, float theta) {
+  KRAKEN_TRY(check_context(ctx));
+  if (tokens == 0 || heads == 0 || head_dim == 0 || n_dims == 0 || n_dims > head_dim ||
+      n_dims % 2u != 0) {
+    return invalid("HIP MRoPE dimensions are invalid");
+  }
+  size_t sections = 0;
+  if (!checked_add(section_0, section_1, sections) ||
+      !checked_add(sections, section_2, sections) ||
+      !checked_add(sections, section_3, sections)) {
+    return invalid("HIP MRoPE sections overflow");
+  }
+  if (sections == 0) {
+    return invalid("HIP MRoPE sections must not all be zero");
+  }
+  size_t value_count = 0;
+  if (!checked_mul(tokens, heads, value_count) ||
+      !checked_mul(value_count, head_dim, value_count)) {
+    return invalid("HIP MRoPE value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(values, value_count, "MRoPE values"));
+  size_t position_count = 0;
+  if (!checked_mul(tokens, 4u, position_count)) {
+    return invalid("HIP MRoPE position count overflow");
+  }
+  if (positions.data == nullptr || positions.byte_size < position_count * sizeof(int32_t)) {
+    return invalid("HIP MRoPE position buffer is too small");
+  }
+  KRAKEN_TRY(check_u32(tokens, "MRoPE tokens"));
+  KRAKEN_TRY(check_u32(heads, "MRoPE heads"));
+  KRAKEN_TRY(check_u32(head_dim, "MRoPE head dim"));
+  KRAKEN_TRY(check_u32(n_dims, "MRoPE n_dims"));
+  KRAKEN_TRY(check_u32(section_0, "MRoPE section 0"));
+  KRAKEN_TRY(check_u32(section_1, "MRoPE section 1"));
+  KRAKEN_TRY(check_u32(section_2, "MRoPE section 2"));
+  KRAKEN_TRY(check_u32(section_3, "MRoPE section 3"));
+  KRAKEN_TRY(check_u32(sections, "MRoPE sections"));
+  size_t pair_count = 0;
+  if (!checked_mul(tokens, heads, pair_count) || !checked_mul(pair_count, n_dims / 2u, pair_count)) {
+    return invalid("HIP MRoPE pair count overflow");
+  }
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_mrope(
+    static_cast<float*>(values.data), static_cast<const int32_t*>(positions.data),
+    (uint32_t)tokens, (uint32_t)heads, (uint32_t)head_dim, (uint32_t)n_dims,
+    (uint32_t)section_0, (uint32_t)section_1, (uint32_t)section_2, (uint32_t)section_3, theta,
+    ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP MRoPE launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP MRoPE command failed: ");
+}
+
+KRAKEN_API int kraken_hip_copy_f32_rows_to_f16(kraken_hip_context* ctx, kraken_buffer source,
+                                               kraken_buffer destination, size_t rows,
+                                               size_t row_size, size_t source_stride,
+                                               size_t source_offset, size_t destination_stride,
+                                               size_t destination_offset) {
+  return copy_rows_entry(ctx, CopyKind::f32_to_f16, "copy rows to f16", source, destination,
+                         rows, row_size, source_stride, source_offset, destination_stride,
+                         destination_offset);
+}
+
+KRAKEN_API int kraken_hip_copy_f32_rows(kraken_hip_context* ctx, kraken_buffer source,
+                                        kraken_buffer destination, size_t rows, size_t row_size,
+                                        size_t source_stride, size_t source_offset,
+                                        size_t destination_stride, size_t destination_offset) {
+  return copy_rows_entry(ctx, CopyKind::f32, "copy rows", source, destination, rows, row_size,
+                         source_stride, source_offset, destination_stride, destination_offset);
+}
+
+KRAKEN_API int kraken_hip_copy_f16_rows(kraken_hip_context* ctx, kraken_buffer source,
+                                        kraken_buffer destination, size_t rows, size_t row_size,
+                                        size_t source_stride, size_t source_offset,
+                                        size_t destination_stride, size_t destination_offset) {
+  return copy_rows_entry(ctx, CopyKind::f16, "copy f16 rows", source, destination, rows,
+                         row_size, source_stride, source_offset, destination_stride,
+                         destination_offset);
+}
+
+KRAKEN_API int kraken_hip_sigmoid_f32_in_place(kraken_hip_context* ctx, kraken_buffer values,
+                                               size_t size) {
+  return unary_entry(ctx, UnaryKind::sigmoid, "sigmoid", values, size);
+}
+
+KRAKEN_API int kraken_hip_softplus_f32_in_place(kraken_hip_context* ctx, kraken_buffer values,
+                                                size_t size) {
+  return unary_entry(ctx, UnaryKind::softplus, "softplus", values, size);
+}
+
+KRAKEN_API int kraken_hip_silu_f32_in_place(kraken_hip_context* ctx, kraken_buffer values,
+                                            size_t size) {
+  return unary_entry(ctx, UnaryKind::silu, "silu", values, size);
+}
+
+KRAKEN_API int kraken_hip_mul_f32_in_place(kraken_hip_context* ctx, kraken_buffer target,
+                                           kraken_buffer rhs, size_t size) {
+  return binary_entry(ctx, BinaryKind::mul, "mul", target, rhs, size, 0, false);
+}
+
+KRAKEN_API int kraken_hip_add_f32_row_in_place(kraken_hip_context* ctx, kraken_buffer target,
+                                               kraken_buffer row, size_t rows, size_t row_size) {
+  return binary_entry(ctx, BinaryKind::add_row, "add row", target, row, rows, row_size, true);
+}
+
+KRAKEN_API int kraken_hip_mul_f32_row_in_place(kraken_hip_context* ctx, kraken_buffer target,
+                                               kraken_buffer row, size_t rows, size_t row_size) {
+  return binary_entry(ctx, BinaryKind::mul_row, "mul row", target, row, rows, row_size, true);
+}
+
+}  // extern "C"

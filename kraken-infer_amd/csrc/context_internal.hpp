@@ -1,0 +1,191 @@
+// Host-side internals shared by the C-ABI translation units: the context
+// object, the status/last-error convention, argument validation helpers, and
+// the launch functions each kernel translation unit provides.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <limits>
+#include <string>
+
+#include "kraken_hip.h"
+
+struct kraken_hip_context {
+  bool validation_only = false;
+  int device = -1;
+  int cu_count = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;  // where work is enqueued (own or caller's)
+  bool graph_active = false;
+  // Device workspace owned by the context (split-K partials, counters).  Grown on
+  // demand outside of any kernel; the reference likewise owns only its flash-tail
+  // scratch (mps_backend.mm:4402-4407).
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+};
+
+namespace kraken {
+
+// --------------------------------------------------------------- status ----
+// Records `message` as this thread's last error and returns `code`.
+int fail(int code, const std::string& message);
+inline int invalid(const std::string& m) { return fail(KRAKEN_INVALID_ARGUMENT, m); }
+inline int unavailable(const std::string& m) { return fail(KRAKEN_UNAVAILABLE, m); }
+inline int internal(const std::string& m) { return fail(KRAKEN_INTERNAL_ERROR, m); }
+
+// Context validity (first check of every op, mps_backend.mm:10625-10627).
+int check_context(const kraken_hip_context* ctx);
+
+// After validation: a validation-only context stops here with KRAKEN_UNAVAILABLE;
+// a live context selects its device.  Returns KRAKEN_OK to proceed.
+int begin_launch(kraken_hip_context* ctx);
+
+// After enqueueing: checks the launch and, outside a graph, waits for the stream
+// (finish_command_buffer, mps_backend.mm:4416-4428).
+int finish_launch(kraken_hip_context* ctx, const char* error_prefix);
+
+// Ensures ctx->workspace holds at least `bytes`; waits for pending work before
+// reallocating.  Returns KRAKEN_OK or an error status.
+int ensure_workspace(kraken_hip_context* ctx, size_t bytes);
+
+// ------------------------------------------------------------ validation ----
+// Restatements of the reference's helpers, mps_backend.mm:4196-4308.
+inline bool checked_mul(size_t a, size_t b, size_t& out) {
+  if (a != 0 && b > std::numeric_limits<size_t>::max() / a) {
+    return false;
+  }
+  out = a * b;
+  return true;
+}
+
+inline bool checked_add(size_t a, size_t b, size_t& out) {
+  if (a > std::numeric_limits<size_t>::max() - b) {
+    return false;
+  }
+  out = a + b;
+  return true;
+}
+
+inline bool fits_u32(size_t v) { return v <= std::numeric_limits<uint32_t>::max(); }
+
+// checked_u32: `name` exceeds uint32 range -> invalid argument.
+int check_u32(size_t value, const char* name);
+
+// validate_f32/f16/i32_buffer: byte count overflow, "not initialized", "too small".
+int validate_buffer(const kraken_buffer& buffer, size_t values, size_t element_bytes,
+                    const char* name);
+inline int validate_f32(const kraken_buffer& b, size_t values, const char* name) {
+  return validate_buffer(b, values, sizeof(float), name);
+}
+inline int validate_f16(const kraken_buffer& b, size_t values, const char* name) {
+  return validate_buffer(b, values, sizeof(uint16_t), name);
+}
+inline int validate_i32(const kraken_buffer& b, size_t values, const char* name) {
+  return validate_buffer(b, values, sizeof(int32_t), name);
+}
+
+// validate_f32_buffer_region: [offset, offset+values) must fit; returns status.
+int validate_f32_region(const kraken_buffer& b, size_t offset, size_t values,
+                        const char* name);
+
+// strided_f32_region_end (mps_backend.mm:4203-4231): end element of a strided
+// row range; invalid argument on zero rows/row_size, stride < row_size, overflow.
+int strided_region_end(size_t offset, size_t rows, size_t stride, size_t row_size,
+                       const char* name, size_t& end);
+
+// -------------------------------------------------------------- launches ----
+// Implemented by the kernel translation units; all enqueue on `stream` and
+// return hipSuccess or the launch error.
+
+struct AttentionArgs {
+  const float* query;
+  const void* key_cache;
+  const void* value_cache;
+  const float* gate;  // nullable: fused sigmoid output gate
+  float* output;
+  uint32_t layer, start_position, tokens, capacity_tokens, heads, kv_heads, head_dim;
+  bool kv_f16;
+};
+
+// Bytes of workspace the split-K decode path needs for these arguments.
+size_t attention_decode_workspace_bytes(const AttentionArgs& a, int cu_count);
+hipError_t launch_attention_decode(const AttentionArgs& a, int cu_count, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
+// Merges per-split (m, l, o) partials (log2-domain m) into the final output,
+// applying the optional sigmoid gate.  Partials are laid out
+// [tokens][kv_heads][splits][group][head_dim] (ml: [...][group][2]).
+struct CombineArgs {
+  const float* partial_o;
+  const float* partial_ml;
+  const float* gate;
+  float* output;
+  uint32_t tokens, heads, kv_heads, splits, head_dim;
+};
+hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream);
+// True when the flash MFMA prefill kernel supports these arguments.
+bool flash_prefill_supported(const AttentionArgs& a);
+size_t attention_flash_workspace_bytes(const AttentionArgs& a, int cu_count);
+hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream);
+
+struct GdnArgs {
+  const float* query;
+  const float* key;
+  const float* value;
+  const float* gate;   // prepared gate (log decay) unless `prepare` is set
+  const float* beta;   // prepared beta unless `prepare` is set
+  float* state;
+  float* output;
+  uint32_t tokens, key_heads, value_heads, head_dim;
+  // Fused prologue/epilogue (kraken_hip_qwen35_gdn_gated_f32); null otherwise.
+  const float* dt_bias;      // prepare: gate = softplus(alpha + dt_bias) * ssm_a
+  const float* ssm_a;        //          beta = sigmoid(beta_raw)
+  const float* z;            // epilogue: out = RMSNorm(y) * norm_weight * silu(z)
+  const float* norm_weight;
+  float eps;
+};
+hipError_t launch_gated_delta_net(const GdnArgs& a, int cu_count, hipStream_t stream);
+
+hipError_t launch_ssm_conv(const float* input, const float* kernel, float* output,
+                           uint32_t conv_kernel, uint32_t channels, uint32_t tokens,
+                           uint32_t sequences, hipStream_t stream);
+hipError_t launch_build_ssm_conv_state(float* state, const float* input, float* conv_input,
+                                       uint32_t conv_kernel, uint32_t channels,
+                                       uint32_t tokens, hipStream_t stream);
+hipError_t launch_ssm_conv1_stateful(float* state, const float* input, const float* kernel,
+                                     float* output, uint32_t conv_kernel, uint32_t channels,
+                                     hipStream_t stream);
+hipError_t launch_conv_split_l2(const float* qkv, float* conv_state, const float* weights,
+                                uint32_t conv_kernel, uint32_t tokens, uint32_t key_heads,
+                                uint32_t value_heads, uint32_t head_dim, float eps,
+                                float* query, float* key, float* value, hipStream_t stream);
+
+hipError_t launch_split_qkv_l2(const float* source, float* q, float* k, float* v,
+                               uint32_t tokens, uint32_t key_heads, uint32_t value_heads,
+                               uint32_t head_dim, float eps, hipStream_t stream);
+hipError_t launch_l2_norm(float* values, uint32_t rows, uint32_t row_size, float eps,
+                          hipStream_t stream);
+hipError_t launch_rms_norm_heads(float* values, const float* weight, const float* gate,
+                                 uint32_t tokens, uint32_t heads, uint32_t head_dim,
+                                 float eps, hipStream_t stream);
+hipError_t launch_prepare_gate_beta(float* gate, float* beta, const float* bias,
+                                    const float* scale, uint32_t rows, uint32_t row_size,
+                                    hipStream_t stream);
+hipError_t launch_mrope(float* values, const int32_t* positions, uint32_t tokens,
+                        uint32_t heads, uint32_t head_dim, uint32_t n_dims, uint32_t s0,
+                        uint32_t s1, uint32_t s2, uint32_t s3, float theta,
+                        hipStream_t stream);
+enum class CopyKind { f32, f32_to_f16, f16 };
+hipError_t launch_copy_rows(CopyKind kind, const void* source, void* destination,
+                            size_t rows, size_t row_size, size_t source_stride,
+                            size_t source_offset, size_t destination_stride,
+                            size_t destination_offset, hipStream_t stream);
+enum class UnaryKind { sigmoid, softplus, silu };
+hipError_t launch_unary(UnaryKind kind, float* values, size_t size, hipStream_t stream);
+enum class BinaryKind { mul, add_row, mul_row };
+hipError_t launch_binary(BinaryKind kind, float* target, const float* rhs, size_t size,
+                         size_t row_size, hipStream_t stream);
+
+}  // namespace kraken

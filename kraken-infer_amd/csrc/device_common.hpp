@@ -1,0 +1,102 @@
+// Device-side helpers shared by the gfx950 kernels: 64-lane wave reductions
+// built from DPP row operations and ds_swizzle, fp16 packing, fast exp2.
+//
+// Lane groups used below (wave64):
+//   reduce8  : lanes sharing (lane >> 3), i.e. 8 consecutive lanes
+//   reduce32 : lanes sharing (lane >> 5)
+//   across8  : lanes sharing (lane & 7) but differing in bits 3..4 (the 4 groups
+//              of 8 within one 32-lane half): lane ^ 8 via row_ror:8, then
+//              lane ^ 16 via ds_swizzle.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kraken {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// DPP control codes (GCN3+/CDNA encoding).
+constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <-> 7-i within 8
+constexpr int kDppRowMirror = 0x140;      // lane i <-> 15-i within 16
+constexpr int kDppRowRor8 = 0x128;        // lane i <-> i^8 within 16 (rotate by 8)
+// ds_swizzle bit mode: and_mask=0x1F, xor_mask=0x10 -> lane ^ 16 within 32.
+constexpr int kSwizzleXor16 = 0x401F;
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(
+    __builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float swizzle_xor16(float x) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), kSwizzleXor16));
+}
+
+// Sum over the 8 lanes of an aligned 8-lane group; result in all 8 lanes.
+__device__ __forceinline__ float reduce8_sum(float x) {
+  x += dpp<kDppQuadXor1>(x);
+  x += dpp<kDppQuadXor2>(x);
+  x += dpp<kDppRowHalfMirror>(x);
+  return x;
+}
+
+__device__ __forceinline__ float reduce8_max(float x) {
+  x = fmaxf(x, dpp<kDppQuadXor1>(x));
+  x = fmaxf(x, dpp<kDppQuadXor2>(x));
+  x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
+  return x;
+}
+
+// Sum over an aligned 32-lane half; result in all 32 lanes.
+__device__ __forceinline__ float reduce32_sum(float x) {
+  x += dpp<kDppQuadXor1>(x);
+  x += dpp<kDppQuadXor2>(x);
+  x += dpp<kDppRowHalfMirror>(x);
+  x += dpp<kDppRowMirror>(x);
+  x += swizzle_xor16(x);
+  return x;
+}
+
+// Combine the four 8-lane groups of each 32-lane half lane-wise (lane bits 3 and
+// 4): every lane ends with the sum over lanes {l, l^8, l^16, l^24}.
+__device__ __forceinline__ float across8_sum(float x) {
+  x += dpp<kDppRowRor8>(x);
+  x += swizzle_xor16(x);
+  return x;
+}
+
+__device__ __forceinline__ float across8_max(float x) {
+  x = fmaxf(x, dpp<kDppRowRor8>(x));
+  x = fmaxf(x, swizzle_xor16(x));
+  return x;
+}
+
+// Wave-uniform combination of the two 32-lane halves of a value that is already
+// uniform within each half.
+__device__ __forceinline__ float halves_sum(float x) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+}
+
+__device__ __forceinline__ float halves_max(float x) {
+  return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)),
+               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32)));
+}
+
+// Full 64-lane sum, result uniform.
+__device__ __forceinline__ float wave_sum(float x) { return halves_sum(reduce32_sum(x)); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace kraken

@@ -1,0 +1,446 @@
+// Gated-delta-net linear attention: recurrent core and the causal conv1d
+// state machinery in front of it.
+//
+// Recurrence (reference MSL gated_delta_net_f32_batched_qwen35 /
+// _batched_in_place, mps_backend.mm:2225-2374), per value head h
+// (key_head = h % key_heads), per token, for every state row r (value dim) over
+// columns c (key dim):
+//     S[r,:] *= exp(g);  sk = S[r,:].k;  delta = (v[r] - sk) * beta;
+//     S[r,:] += k * delta;  y[r] = (S[r,:].q) / sqrt(D)
+// State rows are independent, so the kernel spreads the 16 x 128 rows of a
+// layer over the whole chip: 32 lanes own one row (4 fp32 columns each for
+// D=128) and keep it in registers for the whole chunk; dot products reduce over
+// the 32 lanes with DPP + swizzle.  The next token's k/q/v/g/beta are fetched
+// while the current token computes.  With `prepare` the kernel also forms
+// g = softplus(alpha + dt_bias) * ssm_a and beta = sigmoid(beta_raw)
+// (prepare_qwen35_gdn_gate_beta_f32, mps_backend.mm:2588-2605) on the fly.
+#include <hip/hip_runtime.h>
+
+#include "context_internal.hpp"
+#include "device_common.hpp"
+
+namespace kraken {
+namespace {
+
+constexpr int kGdnRowsPerBlock = 8;  // 4 waves x 2 rows
+
+struct GdnParams {
+  const float* query;
+  const float* key;
+  const float* value;
+  const float* gate;
+  const float* beta;
+  const float* dt_bias;
+  const float* ssm_a;
+  float* state;
+  float* output;
+  uint32_t tokens, key_heads, value_heads, head_dim;
+  float scale;
+};
+
+__device__ __forceinline__ float softplus_ref(float x) {
+  return x > 20.0f ? x : log1pf(expf(x));
+}
+
+template <int CPL, bool kPrepare>
+__global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const uint32_t h = blockIdx.y;
+  const uint32_t row = blockIdx.x * kGdnRowsPerBlock + wave * 2 + (lane >> 5);
+  const uint32_t col0 = (uint32_t)(lane & 31) * CPL;
+  const uint32_t D = p.head_dim;
+  const bool row_ok = row < D;
+  const uint32_t kh = h % p.key_heads;
+
+  float s[CPL];
+  float* srow = p.state + ((size_t)h * D + (row_ok ? row : 0)) * D;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    s[i] = (row_ok && col0 + i < D) ? srow[col0 + i] : 0.0f;
+  }
+
+  auto load_token = [&](uint32_t t, float* k, float* q, float& v, float& g, float& b) {
+    const float* kp = p.key + ((size_t)t * p.key_heads + kh) * D;
+    const float* qp = p.query + ((size_t)t * p.key_heads + kh) * D;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const bool ok = col0 + i < D;
+      k[i] = ok ? kp[col0 + i] : 0.0f;
+      q[i] = ok ? qp[col0 + i] : 0.0f;
+    }
+    v = row_ok ? p.value[((size_t)t * p.value_heads + h) * D + row] : 0.0f;
+    const size_t gi = (size_t)t * p.value_heads + h;
+    g = p.gate[gi];
+    b = p.beta[gi];
+  };
+
+  float kc[CPL], qc[CPL], vc, gc, bc;
+  load_token(0, kc, qc, vc, gc, bc);
+  for (uint32_t t = 0; t < p.tokens; ++t) {
+    float kn[CPL], qn[CPL], vn = 0.0f, gn = 0.0f, bn = 0.0f;
+    if (t + 1 < p.tokens) {
+      load_token(t + 1, kn, qn, vn, gn, bn);
+    }
+    float g = gc;
+    float b = bc;
+    if (kPrepare) {
+      g = softplus_ref(g + p.dt_bias[h]) * p.ssm_a[h];
+      b = 1.0f / (1.0f + expf(-b));
+    }
+    const float decay = expf(g);
+    float sk = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      s[i] *= decay;
+      sk = fmaf(s[i], kc[i], sk);
+    }
+    sk = reduce32_sum(sk);
+    const float delta = (vc - sk) * b;
+    float y = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      s[i] = fmaf(kc[i], delta, s[i]);
+      y = fmaf(s[i], qc[i], y);
+    }
+    y = reduce32_sum(y);
+    if (row_ok && (lane & 31) == 0) {
+      p.output[((size_t)t * p.value_heads + h) * D + row] = y * p.scale;
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      kc[i] = kn[i];
+      qc[i] = qn[i];
+    }
+    vc = vn;
+    gc = gn;
+    bc = bn;
+  }
+  if (row_ok) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      if (col0 + i < D) {
+        srow[col0 + i] = s[i];
+      }
+    }
+  }
+}
+
+template <bool kPrepare>
+hipError_t launch_gdn_cpl(const GdnParams& p, hipStream_t stream) {
+  const dim3 grid((p.head_dim + kGdnRowsPerBlock - 1) / kGdnRowsPerBlock, p.value_heads);
+  const uint32_t cpl = (p.head_dim + 31) / 32;
+  if (cpl <= 1) {
+    gdn_recurrent_kernel<1, kPrepare><<<grid, 256, 0, stream>>>(p);
+  } else if (cpl <= 2) {
+    gdn_recurrent_kernel<2, kPrepare><<<grid, 256, 0, stream>>>(p);
+  } else if (cpl <= 4) {
+    gdn_recurrent_kernel<4, kPrepare><<<grid, 256, 0, stream>>>(p);
+  } else {
+    gdn_recurrent_kernel<8, kPrepare><<<grid, 256, 0, stream>>>(p);
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- conv ------
+
+// build_ssm_conv_state_f32 (mps_backend.mm:2428-2457).  One block per 64
+// channels: thread c < 64 owns channel c's state (old state -> conv_input head,
+// new state <- last K-1 entries of [old state | chunk]); the whole block copies
+// the chunk transposed into conv_input[c][K-1+t].
+__global__ __launch_bounds__(256) void build_conv_state_kernel(float* state, const float* input,
+                                                               float* conv_input,
+                                                               uint32_t conv_kernel,
+                                                               uint32_t channels,
+                                                               uint32_t tokens) {
+  const uint32_t width = conv_kernel - 1u;
+  const size_t span = (size_t)width + tokens;
+  const uint32_t c0 = blockIdx.x * 64u;
+  const uint32_t lc = threadIdx.x & 63u;
+  const uint32_t c = c0 + lc;
+  const uint32_t tlane = threadIdx.x >> 6;
+  if (tlane == 0 && c < channels) {
+    for (uint32_t j = 0; j < width; ++j) {
+      conv_input[c * span + j] = state[(size_t)c * width + j];
+    }
+  }
+  if (c < channels) {
+    for (uint32_t t = tlane; t < tokens; t += 4u) {
+      conv_input[c * span + width + t] = input[(size_t)t * channels + c];
+    }
+  }
+  __syncthreads();
+  if (tlane == 0 && c < channels) {
+    for (uint32_t j = 0; j < width; ++j) {
+      state[(size_t)c * width + j] = conv_input[c * span + tokens + j];
+    }
+  }
+}
+
+// ssm_conv_f32 (mps_backend.mm:2376-2400).
+__global__ void ssm_conv_kernel(const float* input, const float* weights, float* output,
+                                uint32_t conv_kernel, uint32_t channels, uint32_t tokens,
+                                uint32_t sequences) {
+  const size_t span = (size_t)conv_kernel - 1u + tokens;
+  const size_t total = (size_t)sequences * tokens * channels;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t c = (uint32_t)(i % channels);
+    const uint32_t t = (uint32_t)((i / channels) % tokens);
+    const size_t s = i / ((size_t)channels * tokens);
+    const float* x = input + (s * channels + c) * span + t;
+    const float* w = weights + (size_t)c * conv_kernel;
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < conv_kernel; ++j) {
+      acc = fmaf(x[j], w[j], acc);
+    }
+    output[i] = acc;
+  }
+}
+
+// ssm_conv1_f32_stateful (mps_backend.mm:2402-2426).
+__global__ void conv1_stateful_kernel(float* state, const float* input, const float* weights,
+                                      float* output, uint32_t conv_kernel, uint32_t channels) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= channels) {
+    return;
+  }
+  const uint32_t width = conv_kernel - 1u;
+  float* st = state + (size_t)c * width;
+  const float* w = weights + (size_t)c * conv_kernel;
+  const float x = input[c];
+  float acc = 0.0f;
+  for (uint32_t j = 0; j < width; ++j) {
+    acc = fmaf(st[j], w[j], acc);
+  }
+  acc = fmaf(x, w[width], acc);
+  for (uint32_t j = 0; j + 1u < width; ++j) {
+    st[j] = st[j + 1u];
+  }
+  st[width - 1u] = x;
+  output[c] = acc;
+}
+
+// Fused linear-attention prologue (qwen35_runtime.cpp:2746-2796): causal depthwise
+// conv over [old state | chunk] + SiLU + split into q/k/v + L2 norm of q and k.
+// Block = 4 waves = one head-slice of D channels (q head, k head or v head) for a
+// tile of tokens; lane owns CPL channels.  Each wave walks TPW consecutive tokens
+// with a register sliding window of the last K rows.
+constexpr int kConvTokensPerWave = 4;
+constexpr int kConvMaxKernel = 8;
+
+template <int CPL, int K>
+__global__ __launch_bounds__(256) void conv_split_l2_kernel(
+  const float* qkv, const float* conv_state, const float* weights, uint32_t tokens,
+  uint32_t key_heads, uint32_t value_heads, uint32_t head_dim, float eps, float* query,
+  float* key, float* value) {
+  constexpr int W = K - 1;
+  const uint32_t heads_total = 2u * key_heads + value_heads;
+  const uint32_t unit = blockIdx.x % heads_total;  // which q/k/v head
+  const uint32_t tile = blockIdx.x / heads_total;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const size_t channels = (size_t)heads_total * head_dim;
+  const uint32_t cbase = unit * head_dim;  // first channel of this head-slice
+  const uint32_t t_begin = (tile * 4u + wave) * kConvTokensPerWave;
+  if (t_begin >= tokens) {
+    return;
+  }
+  const uint32_t t_end = min(tokens, t_begin + kConvTokensPerWave);
+
+  float w[CPL][K];
+  float win[CPL][W];  // win[.][j] = x[t - W + j]
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const uint32_t d = lane + 64u * i;
+    const bool ok = d < head_dim;
+    const size_t c = cbase + d;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      w[i][j] = ok ? weights[c * K + j] : 0.0f;
+    }
+    // Rows t_begin - W .. t_begin - 1 (conv state rows when negative).
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      float v = 0.0f;
+      if (ok) {
+        const int64_t r = (int64_t)t_begin - W + j;
+        v = r >= 0 ? qkv[(size_t)r * channels + c] : conv_state[c * W + (W + r)];
+      }
+      win[i][j] = v;
+    }
+  }
+
+  const bool is_v = unit >= 2u * key_heads;
+  for (uint32_t t = t_begin; t < t_end; ++t) {
+    float y[CPL];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const uint32_t d = lane + 64u * i;
+      const bool ok = d < head_dim;
+      const float xt = ok ? qkv[(size_t)t * channels + cbase + d] : 0.0f;
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        acc = fmaf(win[i][j], w[i][j], acc);
+      }
+      acc = fmaf(xt, w[i][W], acc);
+#pragma unroll
+      for (int j = 0; j + 1 < W; ++j) {
+        win[i][j] = win[i][j + 1];
+      }
+      win[i][W - 1] = xt;
+      const float sl = acc / (1.0f + expf(-acc));  // SiLU
+      y[i] = ok ? sl : 0.0f;
+      ss = fmaf(y[i], y[i], ss);
+    }
+    if (is_v) {
+      const uint32_t vh = unit - 2u * key_heads;
+      float* dst = value + ((size_t)t * value_heads + vh) * head_dim;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const uint32_t d = lane + 64u * i;
+        if (d < head_dim) {
+          dst[d] = y[i];
+        }
+      }
+    } else {
+      ss = wave_sum(ss);
+      const float inv = 1.0f / fmaxf(sqrtf(ss), eps);
+      const uint32_t part = unit / key_heads;
+      const uint32_t kh = unit % key_heads;
+      float* dst = (part == 0 ? query : key) + ((size_t)t * key_heads + kh) * head_dim;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const uint32_t d = lane + 64u * i;
+        if (d < head_dim) {
+          dst[d] = y[i] * inv;
+        }
+      }
+    }
+  }
+}
+
+// New conv state after the chunk: last K-1 rows of [old state | chunk].  Runs
+// after the conv kernel so no block reads a state row this one overwrites.
+__global__ void conv_state_update_kernel(float* conv_state, const float* qkv,
+                                         uint32_t conv_kernel, uint32_t tokens,
+                                         uint32_t channels) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= channels) {
+    return;
+  }
+  const uint32_t width = conv_kernel - 1u;
+  float old[kConvMaxKernel];
+  for (uint32_t j = 0; j < width; ++j) {
+    old[j] = conv_state[(size_t)c * width + j];
+  }
+  for (uint32_t j = 0; j < width; ++j) {
+    const int64_t r = (int64_t)tokens - (int64_t)width + j;  // row in [old | chunk] - width
+    conv_state[(size_t)c * width + j] =
+      r >= 0 ? qkv[(size_t)r * channels + c] : old[width + r];
+  }
+}
+
+unsigned grid_for(size_t total, unsigned block = 256) {
+  size_t blocks = (total + block - 1) / block;
+  if (blocks < 1) {
+    blocks = 1;
+  }
+  if (blocks > 65535) {
+    blocks = 65535;
+  }
+  return (unsigned)blocks;
+}
+
+}  // namespace
+
+hipError_t launch_gated_delta_net(const GdnArgs& a, int cu_count, hipStream_t stream) {
+  (void)cu_count;
+  GdnParams p{};
+  p.query = a.query;
+  p.key = a.key;
+  p.value = a.value;
+  p.gate = a.gate;
+  p.beta = a.beta;
+  p.dt_bias = a.dt_bias;
+  p.ssm_a = a.ssm_a;
+  p.state = a.state;
+  p.output = a.output;
+  p.tokens = a.tokens;
+  p.key_heads = a.key_heads;
+  p.value_heads = a.value_heads;
+  p.head_dim = a.head_dim;
+  p.scale = 1.0f / sqrtf((float)a.head_dim);
+  hipError_t e = a.dt_bias != nullptr ? launch_gdn_cpl<true>(p, stream)
+                                      : launch_gdn_cpl<false>(p, stream);
+  if (e != hipSuccess || a.z == nullptr) {
+    return e;
+  }
+  // Norm-gated epilogue over each (token, head) row of y.
+  return launch_rms_norm_heads(a.output, a.norm_weight, a.z, a.tokens, a.value_heads,
+                               a.head_dim, a.eps, stream);
+}
+
+hipError_t launch_ssm_conv(const float* input, const float* kernel, float* output,
+                           uint32_t conv_kernel, uint32_t channels, uint32_t tokens,
+                           uint32_t sequences, hipStream_t stream) {
+  const size_t total = (size_t)sequences * tokens * channels;
+  ssm_conv_kernel<<<grid_for(total), 256, 0, stream>>>(input, kernel, output, conv_kernel,
+                                                        channels, tokens, sequences);
+  return hipGetLastError();
+}
+
+hipError_t launch_build_ssm_conv_state(float* state, const float* input, float* conv_input,
+                                       uint32_t conv_kernel, uint32_t channels,
+                                       uint32_t tokens, hipStream_t stream) {
+  const unsigned grid = (channels + 63u) / 64u;
+  build_conv_state_kernel<<<grid, 256, 0, stream>>>(state, input, conv_input, conv_kernel,
+                                                    channels, tokens);
+  return hipGetLastError();
+}
+
+hipError_t launch_ssm_conv1_stateful(float* state, const float* input, const float* kernel,
+                                     float* output, uint32_t conv_kernel, uint32_t channels,
+                                     hipStream_t stream) {
+  conv1_stateful_kernel<<<(channels + 255u) / 256u, 256, 0, stream>>>(state, input, kernel,
+                                                                      output, conv_kernel,
+                                                                      channels);
+  return hipGetLastError();
+}
+
+hipError_t launch_conv_split_l2(const float* qkv, float* conv_state, const float* weights,
+                                uint32_t conv_kernel, uint32_t tokens, uint32_t key_heads,
+                                uint32_t value_heads, uint32_t head_dim, float eps,
+                                float* query, float* key, float* value, hipStream_t stream) {
+  const uint32_t heads_total = 2u * key_heads + value_heads;
+  const uint32_t tokens_per_block = 4u * kConvTokensPerWave;
+  const uint32_t tiles = (tokens + tokens_per_block - 1) / tokens_per_block;
+  const dim3 grid(heads_total * tiles);
+  const uint32_t cpl = (head_dim + 63u) / 64u;
+  const int kk = (int)conv_kernel;
+#define KRAKEN_CONV_CASE(CPLV, KV)                                                        \
+  if (cpl <= CPLV && kk == KV) {                                                          \
+    conv_split_l2_kernel<CPLV, KV><<<grid, 256, 0, stream>>>(                            \
+      qkv, conv_state, weights, tokens, key_heads, value_heads, head_dim, eps, query, key, \
+      value);                                                                             \
+  } else
+#define KRAKEN_CONV_CPL(CPLV)                                                             \
+  KRAKEN_CONV_CASE(CPLV, 2) KRAKEN_CONV_CASE(CPLV, 3) KRAKEN_CONV_CASE(CPLV, 4)          \
+  KRAKEN_CONV_CASE(CPLV, 5) KRAKEN_CONV_CASE(CPLV, 6) KRAKEN_CONV_CASE(CPLV, 7)          \
+  KRAKEN_CONV_CASE(CPLV, 8)
+  KRAKEN_CONV_CPL(1) KRAKEN_CONV_CPL(2) KRAKEN_CONV_CPL(4) { return hipErrorInvalidValue; }
+#undef KRAKEN_CONV_CPL
+#undef KRAKEN_CONV_CASE
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    return e;
+  }
+  const uint32_t channels = heads_total * head_dim;
+  conv_state_update_kernel<<<(channels + 255u) / 256u, 256, 0, stream>>>(
+    conv_state, qkv, conv_kernel, tokens, channels);
+  return hipGetLastError();
+}
+
+}  // namespace kraken

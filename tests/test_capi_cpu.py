@@ -1,0 +1,268 @@
+"""CPU tests of the C ABI: library loads, exports every declared entry point,
+and enforces the reference's argument checks (order and codes) without a GPU.
+
+Checks follow the reference host dispatchers: context validity first
+(`unavailable`), then dimensions, divisibility, bounds, capacity, overflow,
+buffer initialisation and size, uint32 range (`invalid_argument`), e.g.
+mps_backend.mm:10625-10713 for attention.  The validation-only context runs
+every check and answers `unavailable` instead of launching.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+import kraken_hip as kh
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kraken_hip.h")
+ACCEPTED = "validation-only context: arguments accepted"
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"KRAKEN_API[^;]*?\b(kraken_hip_\w+)\s*\(", text, re.S)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_symbols()
+    assert len(names) >= 40
+    lib = kh.lib()
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_no_undeclared_exports():
+    """Every exported kraken_hip_* symbol is declared in the header."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", kh.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\b(kraken_hip_\w+)\b", out))
+    assert exported == set(declared_symbols())
+
+
+def test_python_signatures_cover_header():
+    names = set(declared_symbols())
+    special = {"kraken_hip_context_create", "kraken_hip_context_create_validation_only",
+               "kraken_hip_context_destroy", "kraken_hip_context_stream",
+               "kraken_hip_last_error", "kraken_hip_abort_graph"}
+    assert names - special == set(kh.SIGNATURES)
+
+
+@pytest.fixture()
+def vctx():
+    ctx = kh.Context(validation_only=True)
+    yield ctx
+    ctx.close()
+
+
+def fake(nbytes):
+    """A buffer view that is never dereferenced (validation-only context)."""
+    return kh.KrakenBuffer(0x1000, nbytes)
+
+
+def status(ctx, name, *args):
+    code = ctx.status(name, *args)
+    return code, kh.last_error()
+
+
+def test_null_context_is_unavailable():
+    code = kh.lib().kraken_hip_attention_f32_batched_f16_kv(
+        None, fake(4), fake(4), fake(4), 0, 0, 1, 1, 1, 1, 1, fake(4))
+    assert code == kh.UNAVAILABLE
+    assert "not initialized" in kh.last_error()
+
+
+def test_live_context_without_gpu_is_unavailable():
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU driver is present")
+    with pytest.raises(kh.KrakenError) as e:
+        kh.Context()
+    assert e.value.code == kh.UNAVAILABLE
+
+
+# ------------------------------------------------------------- attention ----
+
+def attn_args(tokens=1, start=4096, cap=4097, heads=8, kv_heads=2, d=256, layer=0,
+              q_bytes=None, kv_bytes=None, out_bytes=None, elem=2):
+    qv = tokens * heads * d
+    kvv = (layer + 1) * cap * kv_heads * d
+    return (fake(q_bytes if q_bytes is not None else 4 * qv),
+            fake(kv_bytes if kv_bytes is not None else elem * kvv),
+            fake(kv_bytes if kv_bytes is not None else elem * kvv),
+            layer, start, tokens, cap, heads, kv_heads, d,
+            fake(out_bytes if out_bytes is not None else 4 * qv))
+
+
+def test_attention_accepts_valid_decode_and_prefill(vctx):
+    for kw in ({}, dict(tokens=1024, start=7168, cap=8192), dict(tokens=65, start=0, cap=65,
+                                                                 heads=2, kv_heads=1)):
+        code, msg = status(vctx, "attention_f32_batched_f16_kv", *attn_args(**kw))
+        assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+@pytest.mark.parametrize("kw,fragment", [
+    (dict(tokens=0), "dimensions must be positive"),
+    (dict(heads=0), "dimensions must be positive"),
+    (dict(kv_heads=0), "dimensions must be positive"),
+    (dict(d=0), "dimensions must be positive"),
+    (dict(cap=0, start=0), "dimensions must be positive"),
+    (dict(heads=6, kv_heads=4), "divisible by kv_heads"),
+    (dict(d=512), "head_dim exceeds 256"),
+    (dict(start=4097), "exceeds KV cache capacity"),
+    (dict(q_bytes=4 * 8 * 256 - 4), "query buffer is too small"),
+    (dict(kv_bytes=2 * 4097 * 512 - 2), "key cache buffer is too small"),
+    (dict(out_bytes=16), "output buffer is too small"),
+    (dict(layer=1, kv_bytes=2 * 4097 * 512), "key cache buffer is too small"),
+])
+def test_attention_rejects(vctx, kw, fragment):
+    code, msg = status(vctx, "attention_f32_batched_f16_kv", *attn_args(**kw))
+    assert code == kh.INVALID_ARGUMENT
+    assert fragment in msg, msg
+
+
+def test_attention_check_order_dimensions_before_buffers(vctx):
+    # Zero tokens and a null query: the dimension check fires first.
+    args = list(attn_args(tokens=0))
+    args[0] = kh.KrakenBuffer(None, 0)
+    code, msg = status(vctx, "attention_f32_batched_f16_kv", *args)
+    assert code == kh.INVALID_ARGUMENT and "dimensions must be positive" in msg
+    args = list(attn_args())
+    args[0] = kh.KrakenBuffer(None, 1 << 20)
+    code, msg = status(vctx, "attention_f32_batched_f16_kv", *args)
+    assert code == kh.INVALID_ARGUMENT and "query buffer is not initialized" in msg
+
+
+def test_attention_overflow_and_u32_range(vctx):
+    big = 1 << 62
+    code, msg = status(vctx, "attention_f32_batched_f16_kv",
+                       *attn_args(tokens=1, start=0, cap=big, heads=8, kv_heads=2, d=256))
+    assert code == kh.INVALID_ARGUMENT and "overflow" in msg
+    # capacity beyond uint32 with buffers large enough on paper
+    cap = (1 << 32) + 1
+    code, msg = status(vctx, "attention_f32_batched_f16_kv",
+                       *attn_args(tokens=1, start=0, cap=cap, heads=1, kv_heads=1, d=1))
+    assert code == kh.INVALID_ARGUMENT and "exceeds uint32 range" in msg
+
+
+def test_f32_kv_twin_validates_f32_cache_sizes(vctx):
+    args = attn_args(tokens=2, start=1, cap=3, heads=1, kv_heads=1, d=2, elem=4)
+    code, msg = status(vctx, "attention_f32_batched", *args)
+    assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED)
+    args = attn_args(tokens=2, start=1, cap=3, heads=1, kv_heads=1, d=2, elem=2)
+    code, msg = status(vctx, "attention_f32_batched", *args)
+    assert code == kh.INVALID_ARGUMENT and "key cache buffer is too small" in msg
+
+
+def test_gated_attention_validates_gate(vctx):
+    q, k, v, *rest = attn_args()
+    code, msg = status(vctx, "attention_f32_batched_f16_kv_gated", q, k, v, fake(8), *rest)
+    assert code == kh.INVALID_ARGUMENT and "gate buffer is too small" in msg
+    code, msg = status(vctx, "attention_f32_batched_f16_kv_gated", q, k, v, fake(4 * 2048),
+                       *rest)
+    assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+# ------------------------------------------------------------------ GDN -----
+
+def gdn_args(tokens=4, hk=16, hv=16, d=128, state_offset=0, state_values=None, **over):
+    kv = tokens * hk * d
+    vv = tokens * hv * d
+    gv = tokens * hv
+    sv = state_values if state_values is not None else state_offset + hv * d * d
+    a = dict(q=fake(4 * kv), k=fake(4 * kv), v=fake(4 * vv), g=fake(4 * gv), b=fake(4 * gv),
+             s=fake(4 * sv), out=fake(4 * vv))
+    a.update(over)
+    return (a["q"], a["k"], a["v"], a["g"], a["b"], a["s"], state_offset, tokens, hk, hv, d,
+            a["out"])
+
+
+def test_gdn_accepts_and_rejects(vctx):
+    name = "gated_delta_net_f32_batched_in_place_at"
+    assert status(vctx, name, *gdn_args()) == (kh.UNAVAILABLE, ACCEPTED)
+    assert status(vctx, name, *gdn_args(state_offset=3 * 16 * 128 * 128)) == (
+        kh.UNAVAILABLE, ACCEPTED)
+    cases = [
+        (gdn_args(tokens=0), "dimensions must be positive"),
+        (gdn_args(hk=3, hv=16), "value heads must repeat key heads"),
+        (gdn_args(d=384), "head_dim exceeds 256"),
+        (gdn_args(q=fake(16)), "query buffer is too small"),
+        (gdn_args(b=kh.KrakenBuffer(None, 0)), "beta buffer is not initialized"),
+        (gdn_args(state_offset=10, state_values=16 * 128 * 128), "state buffer region is too small"),
+        (gdn_args(out=fake(4)), "output buffer is too small"),
+    ]
+    for args, fragment in cases:
+        code, msg = status(vctx, name, *args)
+        assert code == kh.INVALID_ARGUMENT and fragment in msg, (fragment, msg)
+
+
+def test_conv_ops_validation(vctx):
+    # ssm_conv: input [S][C][K-1+T]
+    assert status(vctx, "ssm_conv_f32", fake(4 * 2 * 6), fake(4 * 8), 4, 2, 3, 1,
+                  fake(4 * 6)) == (kh.UNAVAILABLE, ACCEPTED)
+    code, msg = status(vctx, "ssm_conv_f32", fake(4 * 2 * 5), fake(4 * 8), 4, 2, 3, 1, fake(24))
+    assert code == kh.INVALID_ARGUMENT and "SSM conv input buffer is too small" in msg
+    code, msg = status(vctx, "build_ssm_conv_state_f32", fake(24), 0, fake(16), 1, 2, 2, fake(40))
+    assert code == kh.INVALID_ARGUMENT and "conv-state dimensions are invalid" in msg
+    assert status(vctx, "build_ssm_conv_state_f32", fake(24), 0, fake(16), 4, 2, 2,
+                  fake(40)) == (kh.UNAVAILABLE, ACCEPTED)
+    code, msg = status(vctx, "build_ssm_conv_state_f32", fake(24), 1, fake(16), 4, 2, 2, fake(40))
+    assert code == kh.INVALID_ARGUMENT and "region is too small" in msg
+    code, msg = status(vctx, "qwen35_conv_split_l2_f32", fake(4 * 6144), fake(4 * 3 * 6144), 0,
+                       fake(4 * 4 * 6144), 9, 1, 16, 16, 128, 1e-6, fake(8192), fake(8192),
+                       fake(8192))
+    assert code == kh.INVALID_ARGUMENT and "conv_kernel must be in [2, 8]" in msg
+    assert status(vctx, "qwen35_conv_split_l2_f32", fake(4 * 6144), fake(4 * 3 * 6144), 0,
+                  fake(4 * 4 * 6144), 4, 1, 16, 16, 128, 1e-6, fake(8192), fake(8192),
+                  fake(8192)) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+def test_small_ops_validation(vctx):
+    code, msg = status(vctx, "mrope_f32_in_place", fake(64), fake(16), 1, 1, 8, 10, 1, 1, 1, 1,
+                       1e4)
+    assert code == kh.INVALID_ARGUMENT and "MRoPE dimensions are invalid" in msg
+    code, msg = status(vctx, "mrope_f32_in_place", fake(64), fake(16), 1, 1, 8, 8, 0, 0, 0, 0,
+                       1e4)
+    assert code == kh.INVALID_ARGUMENT and "sections must not all be zero" in msg
+    code, msg = status(vctx, "mrope_f32_in_place", fake(64), fake(8), 1, 1, 8, 8, 1, 1, 1, 1, 1e4)
+    assert code == kh.INVALID_ARGUMENT and "position buffer is too small" in msg
+    code, msg = status(vctx, "copy_f32_rows", fake(48), fake(36), 3, 2, 1, 1, 3, 0)
+    assert code == kh.INVALID_ARGUMENT and "stride must be at least row size" in msg
+    code, msg = status(vctx, "copy_f32_rows", fake(40), fake(36), 3, 2, 4, 1, 3, 0)
+    assert code == kh.INVALID_ARGUMENT and "copy rows source buffer is too small" in msg
+    assert status(vctx, "copy_f32_rows", fake(48), fake(36), 3, 2, 4, 1, 3, 0) == (
+        kh.UNAVAILABLE, ACCEPTED)
+    code, msg = status(vctx, "copy_f32_rows_to_f16", fake(48), fake(15), 3, 2, 4, 1, 3, 0)
+    assert code == kh.INVALID_ARGUMENT and "destination buffer is too small" in msg
+    code, msg = status(vctx, "qk_norm_f32_f32_batched", fake(16), fake(4), 2, 1, 2, 0.0)
+    assert code == kh.INVALID_ARGUMENT and "weight buffer is too small" in msg
+    code, msg = status(vctx, "prepare_qwen35_gdn_gate_beta_f32", fake(16), fake(16), fake(8),
+                       fake(8), 0, 2)
+    assert code == kh.INVALID_ARGUMENT and "dimensions must be positive" in msg
+    code, msg = status(vctx, "split_qkv_l2_norm_f32_qwen35", fake(96), fake(32), fake(32),
+                       fake(31), 2, 2, 2, 2, 0.0)
+    assert code == kh.INVALID_ARGUMENT and "split qkv value buffer is too small" in msg
+    code, msg = status(vctx, "sigmoid_f32_in_place", fake(4), 2)
+    assert code == kh.INVALID_ARGUMENT and "sigmoid values buffer is too small" in msg
+
+
+def test_graph_batching_rules(vctx):
+    lib = kh.lib()
+    assert lib.kraken_hip_commit_graph(vctx.handle) == kh.OK  # commit without begin
+    assert lib.kraken_hip_begin_graph(vctx.handle) == kh.OK
+    assert lib.kraken_hip_begin_graph(vctx.handle) == kh.INVALID_ARGUMENT
+    assert "already active" in kh.last_error()
+    vctx.abort_graph()
+    assert lib.kraken_hip_begin_graph(vctx.handle) == kh.OK
+    assert lib.kraken_hip_commit_graph(vctx.handle) == kh.OK
+
+
+def test_copy_rules(vctx):
+    data = (ctypes.c_float * 4)()
+    code, msg = status(vctx, "copy_to_buffer_at", fake(16), 8, ctypes.addressof(data), 12)
+    assert code == kh.INVALID_ARGUMENT and "exceeds destination buffer size" in msg
+    code, msg = status(vctx, "copy_from_buffer", fake(16), None, 4)
+    assert code == kh.INVALID_ARGUMENT and "destination must not be null" in msg
+    code, msg = status(vctx, "zero_buffer", fake(16), 32)
+    assert code == kh.INVALID_ARGUMENT and "zero size exceeds buffer size" in msg

@@ -1,0 +1,264 @@
+"""GPU parity of the attention kernels against the CPU oracle.
+
+Tolerance: fp16-KV outputs within 2e-3 relative /
+1e-3 absolute of the oracle; f32-KV outputs within 1e-4.  Inputs are seeded
+numpy draws (np.random.default_rng(seed)).
+
+Cases:
+  * split-K decode (T=1) at C1's shape (8 Q / 2 KV heads, D=256) for several KV
+    lengths, unsplit and split, with and without the fused sigmoid gate;
+  * short chunks (T<64) with causal masking, GQA group sizes 1/2/4/8,
+    head_dim 64/128/256 and a generic (untuned) head_dim;
+  * flash256 prefill vs the oracle (Q rounded to f16 as the reference does),
+    aligned and unaligned token counts, with a KV prefix, plus C2's full shape
+    through sampled tokens and through agreement with the decode kernel;
+  * the reference smoke test's 64- and 65-token modular-pattern cases.
+"""
+import numpy as np
+import pytest
+
+import kraken_hip as kh
+import oracle
+
+RTOL, ATOL = 2e-3, 1e-3
+
+
+def f16_bits(x):
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+def make_case(seed, tokens, start, cap, heads, kv_heads, d, layers=1, layer=0, scale_kv=1.0):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal(tokens * heads * d).astype(np.float32)
+    k = (rng.standard_normal(layers * cap * kv_heads * d) * scale_kv).astype(np.float32)
+    v = rng.standard_normal(layers * cap * kv_heads * d).astype(np.float32)
+    return q, f16_bits(k), f16_bits(v)
+
+
+def run_hip(ctx, q, kc, vc, layer, start, tokens, cap, heads, kv_heads, d, gate=None):
+    return kh.NumpyOps(ctx).attention_batched(q, kc, vc, layer, start, tokens, cap, heads,
+                                              kv_heads, d, gate=gate)
+
+
+def close(got, ref, rtol=RTOL, atol=ATOL, msg=""):
+    np.testing.assert_allclose(got, ref, rtol=rtol, atol=atol, err_msg=msg)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kv_len", [0, 31, 1024, 4096, 16384])
+def test_decode_c1_shape(hip_ctx, kv_len):
+    heads, kv_heads, d = 8, 2, 256
+    cap = kv_len + 1
+    print(f"decode C1 L={kv_len}", flush=True)
+    q, kc, vc = make_case(1, 1, kv_len, cap, heads, kv_heads, d)
+    got = run_hip(hip_ctx, q, kc, vc, 0, kv_len, 1, cap, heads, kv_heads, d)
+    ref = oracle.attention_batched(q, kc, vc, 0, kv_len, 1, cap, heads, kv_heads, d)
+    close(got, ref, msg=f"L={kv_len}")
+
+
+@pytest.mark.gpu
+def test_decode_gated_matches_separate_gate(hip_ctx):
+    heads, kv_heads, d, kv_len = 8, 2, 256, 4096
+    q, kc, vc = make_case(1, 1, kv_len, kv_len + 1, heads, kv_heads, d)
+    gate = np.random.default_rng(11).standard_normal(heads * d).astype(np.float32)
+    got = run_hip(hip_ctx, q, kc, vc, 0, kv_len, 1, kv_len + 1, heads, kv_heads, d, gate=gate)
+    ref = oracle.sigmoid_gate_mul(
+        oracle.attention_batched(q, kc, vc, 0, kv_len, 1, kv_len + 1, heads, kv_heads, d), gate)
+    close(got, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [
+    # tokens, start, heads, kv_heads, d
+    (1, 0, 8, 2, 256), (7, 100, 8, 2, 256), (33, 500, 8, 8, 256), (63, 2000, 16, 2, 128),
+    (5, 300, 16, 8, 128), (9, 50, 8, 1, 128), (4, 70, 4, 4, 64), (3, 40, 6, 3, 96),
+    (2, 17, 2, 1, 200), (1, 1000, 24, 4, 128),
+])
+def test_decode_chunk_shapes_and_layer_offset(hip_ctx, shape):
+    tokens, start, heads, kv_heads, d = shape
+    cap = start + tokens + 3
+    print(f"decode chunk {shape}", flush=True)
+    q, kc, vc = make_case(2, tokens, start, cap, heads, kv_heads, d, layers=2)
+    got = run_hip(hip_ctx, q, kc, vc, 1, start, tokens, cap, heads, kv_heads, d)
+    ref = oracle.attention_batched(q, kc, vc, 1, start, tokens, cap, heads, kv_heads, d)
+    close(got, ref, msg=str(shape))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(1, 300, 16, 8, 128), (8, 64, 8, 2, 256), (3, 9, 4, 1, 64)])
+def test_f32_kv_twin(hip_ctx, shape):
+    tokens, start, heads, kv_heads, d = shape
+    cap = start + tokens
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal(tokens * heads * d).astype(np.float32)
+    kc = rng.standard_normal(cap * kv_heads * d).astype(np.float32)
+    vc = rng.standard_normal(cap * kv_heads * d).astype(np.float32)
+    got = run_hip(hip_ctx, q, kc, vc, 0, start, tokens, cap, heads, kv_heads, d)
+    ref = oracle.attention_batched(q, kc, vc, 0, start, tokens, cap, heads, kv_heads, d)
+    close(got, ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.gpu
+def test_decode_uniform_average_closed_form(hip_ctx):
+    """q = 0 gives the uniform mean of V over the causal prefix (smoke_test.cpp:1688-1725)."""
+    heads, kv_heads, d, tokens, start = 8, 2, 256, 5, 3000
+    cap = start + tokens
+    rng = np.random.default_rng(4)
+    v = rng.standard_normal(cap * kv_heads * d).astype(np.float32)
+    vb = f16_bits(v)
+    vf = vb.view(np.float16).astype(np.float64).reshape(cap, kv_heads, d)
+    q = np.zeros(tokens * heads * d, np.float32)
+    kb = f16_bits(rng.standard_normal(cap * kv_heads * d))
+    got = run_hip(hip_ctx, q, kb, vb, 0, start, tokens, cap, heads, kv_heads, d)
+    got = got.reshape(tokens, heads, d)
+    for t in range(tokens):
+        mean = vf[:start + t + 1].mean(axis=0)
+        for h in range(heads):
+            close(got[t, h], mean[h // 4], rtol=1e-4, atol=1e-5)
+
+
+# ------------------------------------------------------------------ flash ----
+
+def mrope_l2_inputs(seed, tokens, prefix, heads=8, kv_heads=2, d=256):
+    """C2 inputs: q,k ~ N(0,1) with MRoPE (sections 11,11,10,0; theta 1e7; pos = P+i)
+    then L2-normalised per head; v ~ N(0,1); all fp16-representable."""
+    rng = np.random.default_rng(seed)
+    cap = prefix + tokens
+    q = rng.standard_normal(tokens * heads * d).astype(np.float32)
+    k = rng.standard_normal(cap * kv_heads * d).astype(np.float32)
+    v = rng.standard_normal(cap * kv_heads * d).astype(np.float32)
+    qpos = oracle.make_mrope_positions(prefix, tokens)
+    kpos = oracle.make_mrope_positions(0, cap)
+    q = oracle.mrope(q, qpos, tokens, heads, d, 64, (11, 11, 10, 0), 1e7)
+    k = oracle.mrope(k, kpos, cap, kv_heads, d, 64, (11, 11, 10, 0), 1e7)
+    q = oracle.l2_norm(q, tokens * heads, d, 1e-6)
+    k = oracle.l2_norm(k, cap * kv_heads, d, 1e-6)
+    q = q.astype(np.float16).astype(np.float32)
+    return q, f16_bits(k), f16_bits(v)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [
+    # tokens, start, heads, kv_heads
+    (64, 0, 8, 2), (65, 0, 2, 1), (128, 0, 8, 2), (100, 37, 8, 2), (256, 1000, 8, 2),
+    (96, 7, 8, 8), (70, 3, 4, 2), (64, 64, 8, 1),
+])
+def test_flash_prefill_vs_oracle(hip_ctx, shape):
+    tokens, start, heads, kv_heads = shape
+    d = 256
+    cap = start + tokens + 5
+    print(f"flash {shape}", flush=True)
+    q, kc, vc = make_case(5, tokens, start, cap, heads, kv_heads, d)
+    got = run_hip(hip_ctx, q, kc, vc, 0, start, tokens, cap, heads, kv_heads, d)
+    ref = oracle.attention_batched(q, kc, vc, 0, start, tokens, cap, heads, kv_heads, d,
+                                   round_query_f16=True)
+    close(got, ref, msg=str(shape))
+
+
+@pytest.mark.gpu
+def test_flash_gated(hip_ctx):
+    tokens, start, heads, kv_heads, d = 128, 200, 8, 2, 256
+    cap = start + tokens
+    q, kc, vc = make_case(6, tokens, start, cap, heads, kv_heads, d)
+    gate = np.random.default_rng(12).standard_normal(tokens * heads * d).astype(np.float32)
+    got = run_hip(hip_ctx, q, kc, vc, 0, start, tokens, cap, heads, kv_heads, d, gate=gate)
+    ref = oracle.sigmoid_gate_mul(oracle.attention_batched(
+        q, kc, vc, 0, start, tokens, cap, heads, kv_heads, d, round_query_f16=True), gate)
+    close(got, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("prefix", [0, 3072, 7168])
+def test_flash_c2_full_shape_sampled_tokens(hip_ctx, prefix):
+    """C2 at full size (T=1024, P in {0,3072,7168}); the oracle checks 12 sampled
+    query tokens (first, last, tile edges, random) of every head."""
+    tokens, heads, kv_heads, d = 1024, 8, 2, 256
+    cap = prefix + tokens
+    print(f"flash C2 P={prefix}", flush=True)
+    q, kc, vc = mrope_l2_inputs(2, tokens, prefix)
+    got = run_hip(hip_ctx, q, kc, vc, 0, prefix, tokens, cap, heads, kv_heads, d)
+    got = got.reshape(tokens, heads * d)
+    rng = np.random.default_rng(7)
+    sample = sorted({0, 31, 32, 63, 64, 511, 1022, 1023, *rng.integers(0, tokens, 4).tolist()})
+    for t in sample:
+        ref = oracle.attention_batched(q[t * heads * d:(t + 1) * heads * d], kc, vc, 0,
+                                       prefix + t, 1, cap, heads, kv_heads, d,
+                                       round_query_f16=True)
+        close(got[t], ref, msg=f"P={prefix} t={t}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("prefix", [0, 3072])
+def test_flash_agrees_with_split_decode_unnormalised(hip_ctx, prefix, monkeypatch):
+    """Two independent kernels (MFMA flash and VALU split-K) agree on every
+    output at C2's shape with un-normalised N(0,1) q/k (a sharper softmax than
+    the L2-normalised C2 inputs)."""
+    tokens, heads, kv_heads, d = 1024, 8, 2, 256
+    cap = prefix + tokens
+    q, kc, vc = make_case(8, tokens, prefix, cap, heads, kv_heads, d)
+    q = q.astype(np.float16).astype(np.float32)  # flash rounds Q; give both the same Q
+    flash = run_hip(hip_ctx, q, kc, vc, 0, prefix, tokens, cap, heads, kv_heads, d)
+    monkeypatch.setenv("KRAKEN_QWEN35_FLASH_ATTENTION", "0")
+    split = run_hip(hip_ctx, q, kc, vc, 0, prefix, tokens, cap, heads, kv_heads, d)
+    close(flash, split)
+
+
+def smoke_pattern_case(tokens, heads, kv_heads, d, qa, qm, qo, qs, ka, km, ko, ks, va, vm, vo, vs):
+    """The reference smoke test's modular input patterns (smoke_test.cpp:1744-1753, 1832-1841)."""
+    qv = tokens * heads * d
+    kv = tokens * kv_heads * d
+    i = np.arange(qv)
+    q = (((i * qa) % qm) - qo).astype(np.float32) * np.float32(qs)
+    j = np.arange(kv)
+    k = (((j * ka) % km) - ko).astype(np.float32) * np.float32(ks)
+    v = (((j * va) % vm) - vo).astype(np.float32) * np.float32(vs)
+    return q, k, v
+
+
+@pytest.mark.gpu
+def test_reference_smoke_64_token_flash_equivalence(hip_ctx, monkeypatch):
+    """smoke_test.cpp:1727-1812: 64 tokens, 8/2/256; flash vs default within 1e-5 on f32 KV.
+    Here: F16 flash vs the oracle on the f16-rounded cache, and F32 decode vs oracle."""
+    tokens, heads, kv_heads, d = 64, 8, 2, 256
+    q, k, v = smoke_pattern_case(tokens, heads, kv_heads, d, 13, 31, 15, 0.015, 7, 29, 14,
+                                 0.012, 11, 37, 18, 0.025)
+    ref32 = oracle.attention_batched(q, k, v, 0, 0, tokens, tokens, heads, kv_heads, d)
+    got32 = run_hip(hip_ctx, q, k, v, 0, 0, tokens, tokens, heads, kv_heads, d)
+    close(got32, ref32, rtol=1e-5, atol=1e-5)
+    kb, vb = f16_bits(k), f16_bits(v)
+    got16 = run_hip(hip_ctx, q, kb, vb, 0, 0, tokens, tokens, heads, kv_heads, d)
+    close(got16, ref32, rtol=0, atol=5e-3)
+    ref16 = oracle.attention_batched(q, kb, vb, 0, 0, tokens, tokens, heads, kv_heads, d,
+                                     round_query_f16=True)
+    close(got16, ref16)
+
+
+@pytest.mark.gpu
+def test_reference_smoke_65_token_unaligned(hip_ctx, monkeypatch):
+    """smoke_test.cpp:1814-1972: 65 tokens, 2/1/256, F16 flash vs F32 default within 5e-3,
+    and F16 flash vs F16 default (forced by KRAKEN_QWEN35_FLASH_ATTENTION) within 5e-3."""
+    tokens, heads, kv_heads, d = 65, 2, 1, 256
+    q, k, v = smoke_pattern_case(tokens, heads, kv_heads, d, 17, 43, 21, 0.01, 5, 41, 20,
+                                 0.011, 19, 47, 23, 0.017)
+    ref32 = oracle.attention_batched(q, k, v, 0, 0, tokens, tokens, heads, kv_heads, d)
+    kb, vb = f16_bits(k), f16_bits(v)
+    monkeypatch.setenv("KRAKEN_QWEN35_FLASH_ATTENTION", "1")
+    flash16 = run_hip(hip_ctx, q, kb, vb, 0, 0, tokens, tokens, heads, kv_heads, d)
+    monkeypatch.setenv("KRAKEN_QWEN35_FLASH_ATTENTION", "0")
+    default16 = run_hip(hip_ctx, q, kb, vb, 0, 0, tokens, tokens, heads, kv_heads, d)
+    close(flash16, ref32, rtol=0, atol=5e-3)
+    close(flash16, default16, rtol=0, atol=5e-3)
+
+
+@pytest.mark.gpu
+def test_gqa_heads_with_equal_query_agree(hip_ctx):
+    heads, kv_heads, d, kv_len = 8, 2, 256, 2048
+    rng = np.random.default_rng(9)
+    qh = rng.standard_normal(d).astype(np.float32)
+    q = np.tile(qh, heads)
+    kc = f16_bits(rng.standard_normal((kv_len + 1) * kv_heads * d))
+    vc = f16_bits(rng.standard_normal((kv_len + 1) * kv_heads * d))
+    out = run_hip(hip_ctx, q, kc, vc, 0, kv_len, 1, kv_len + 1, heads, kv_heads, d)
+    out = out.reshape(heads, d)
+    for h in range(heads):
+        np.testing.assert_array_equal(out[h], out[(h // 4) * 4])
