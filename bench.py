@@ -1,0 +1,341 @@
+"""Benchmark of the MI355X Qwen3.5 attention hot path (one GPU).
+
+Headline (`value`): C1 decode attention -- one query token, 8 Q / 2 KV heads,
+head_dim 256, F16 KV cache holding 4096 prior tokens plus the new one, output
+gated by sigmoid(G) -- as algorithmic HBM GB/s:
+    bytes/step = 2048 * (L + 1)  (K and V rows)  +  24 KiB (q, G, out) + 1 KiB
+with the KV sets rotating over > 512 MB so every step reads from HBM, not the
+256 MB Infinity Cache ("cold").  A step is one call of
+kraken_hip_attention_f32_batched_f16_kv_gated.  The timed steps are captured in
+one HIP graph on torch's stream and replayed between HIP events; inputs are
+resident in HBM before the timed region starts.
+
+`details` adds: decode at L = 1024/8192/16384 (cold and warm), flash256 prefill
+(C2: T=1024 chunk after P = 0/3072/7168 prefix tokens, causal FLOP/s vs the
+2.5 PFLOP/s dense fp16 MFMA peak), the GDN recurrence (C3: 1024-token chunk
+prefill tok/s; single-token decode tok/s and GB/s cold over rotating state
+sets) and the fused GDN layer core (conv prologue + gated recurrence).
+
+`cpu_baseline`: the CPU oracle's restatement of the same decode step
+(oracle/kraken_oracle.c, one core), timed on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps 1000] [--warmup 20] [--kv-len 4096]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "kraken-infer_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+HQ, HKV, D = 8, 2, 256
+METRIC = "decode attn HBM GB/s & prefill TFLOP/s (% roofline), GDN tok/s, 1 GPU"
+
+
+def progress(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_bytes(kv_len):
+    return 2048 * (kv_len + 1) + 3 * HQ * D * 4 + 2 * HKV * D * 2
+
+
+def prefill_flops(tokens, prefix):
+    return 8192 * (tokens * prefix + tokens * (tokens + 1) // 2)
+
+
+GDN_DECODE_BYTES = 2 * 16 * 128 * 128 * 4 + 3 * 16 * 128 * 4 + 2 * 16 * 4 + 16 * 128 * 4
+
+
+class Runner:
+    """Captures a list of step launches in one HIP graph and times replays."""
+
+    def __init__(self, torch, ctx):
+        self.torch = torch
+        self.ctx = ctx
+        self.stream = torch.cuda.Stream()
+        ctx.set_stream(self.stream.cuda_stream)
+        ctx.begin_graph()
+
+    def time(self, steps, warmup):
+        """steps: list of zero-arg callables, each enqueueing one step.  Returns
+        ms per step over one replay of the captured list."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for i in range(warmup):
+                steps[i % len(steps)]()
+            self.stream.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=self.stream):
+                for s in steps:
+                    s()
+            graph.replay()  # untimed replay
+            self.stream.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record(self.stream)
+            graph.replay()
+            end.record(self.stream)
+            end.synchronize()
+            torch.cuda.synchronize()
+        return start.elapsed_time(end) / len(steps), graph
+
+    def close(self):
+        self.ctx.commit_graph()
+        self.ctx.set_stream(None)
+
+
+def bench_decode(torch, ctx, run, kv_len, steps, warmup, cold, gen):
+    """Returns dict with ms/step and GB/s for C1 decode at kv_len."""
+    cap = kv_len + 1
+    set_bytes = 2 * cap * HKV * D * 2
+    n_sets = max(1, -(-2 * MALL_BYTES // set_bytes)) if cold else 1
+    dev = "cuda"
+    q = torch.randn(HQ * D, generator=gen, device=dev, dtype=torch.float32)
+    g = torch.randn(HQ * D, generator=gen, device=dev, dtype=torch.float32)
+    out = torch.empty(HQ * D, device=dev, dtype=torch.float32)
+    ks = [torch.randn(cap * HKV * D, generator=gen, device=dev).half() for _ in range(n_sets)]
+    vs = [torch.randn(cap * HKV * D, generator=gen, device=dev).half() for _ in range(n_sets)]
+
+    def step(i):
+        return lambda: ctx.attention_f32_batched_f16_kv_gated(
+            q, ks[i % n_sets], vs[i % n_sets], g, 0, kv_len, 1, cap, HQ, HKV, D, out)
+
+    ms, graph = run.time([step(i) for i in range(steps)], warmup)
+    del graph
+    gbs = decode_bytes(kv_len) / (ms * 1e-3) / 1e9
+    res = {"kv_len": kv_len, "cold": cold, "kv_sets": n_sets, "ms_per_step": ms, "GB_s": gbs,
+           "frac_hbm_peak": gbs / HBM_PEAK_GBS}
+    del ks, vs
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_prefill(torch, ctx, run, prefix, reps, warmup, gen):
+    import kraken_hip as kh
+
+    tokens = 1024
+    cap = prefix + tokens
+    dev = "cuda"
+    q = torch.randn(tokens * HQ * D, generator=gen, device=dev)
+    k = torch.randn(cap * HKV * D, generator=gen, device=dev)
+    v = torch.randn(cap * HKV * D, generator=gen, device=dev)
+    # C2 synthesis with the library's own ops: MRoPE (11,11,10,0; theta 1e7) then
+    # L2 normalisation of q and k; q rounded to fp16 values, K/V stored fp16.
+    pos_q = torch.arange(prefix, prefix + tokens, device=dev, dtype=torch.int32).repeat(4)
+    pos_k = torch.arange(0, cap, device=dev, dtype=torch.int32).repeat(4)
+    ctx.mrope_f32_in_place(q, pos_q, tokens, HQ, D, 64, 11, 11, 10, 0, 1e7)
+    ctx.mrope_f32_in_place(k, pos_k, cap, HKV, D, 64, 11, 11, 10, 0, 1e7)
+    ctx.l2_norm_f32_in_place(q, tokens * HQ, D, 1e-6)
+    ctx.l2_norm_f32_in_place(k, cap * HKV, D, 1e-6)
+    q = q.half().float()
+    kc, vc = k.half(), v.half()
+    out = torch.empty(tokens * HQ * D, device=dev)
+    step = lambda: ctx.attention_f32_batched_f16_kv(q, kc, vc, 0, prefix, tokens, cap, HQ, HKV,
+                                                    D, out)
+    ms, graph = run.time([step] * reps, warmup)
+    del graph
+    flops = prefill_flops(tokens, prefix)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"prefix": prefix, "tokens": tokens, "ms_per_chunk": ms, "TFLOP_s": tflops,
+            "frac_fp16_mfma_peak": tflops / FP16_PEAK_TFLOPS, "tok_s": tokens / (ms * 1e-3),
+            "gflop": flops / 1e9}
+
+
+def bench_gdn(torch, ctx, run, gen):
+    hk = hv = 16
+    d = 128
+    dev = "cuda"
+    res = {}
+
+    def inputs(t):
+        q = torch.nn.functional.normalize(torch.randn(t, hk, d, generator=gen, device=dev), dim=-1)
+        k = torch.nn.functional.normalize(torch.randn(t, hk, d, generator=gen, device=dev), dim=-1)
+        v = torch.randn(t, hv, d, generator=gen, device=dev)
+        g = -torch.nn.functional.softplus(torch.randn(t, hv, generator=gen, device=dev))
+        b = torch.sigmoid(torch.randn(t, hv, generator=gen, device=dev))
+        return [x.contiguous() for x in (q, k, v, g, b)]
+
+    # Prefill: 1024-token chunks through the recurrence.
+    t = 1024
+    q, k, v, g, b = inputs(t)
+    state = torch.zeros(hv * d * d, device=dev)
+    out = torch.empty(t * hv * d, device=dev)
+    step = lambda: ctx.gated_delta_net_f32_batched_in_place_at(q, k, v, g, b, state, 0, t, hk,
+                                                               hv, d, out)
+    ms, graph = run.time([step] * 4, 1)
+    del graph
+    res["prefill"] = {"tokens_per_chunk": t, "ms_per_chunk": ms, "tok_s": t / (ms * 1e-3),
+                      "gflop_s_recurrent_equiv": 1.835e6 * t / (ms * 1e-3) / 1e9}
+
+    # Decode: one token per step, cold over rotating state sets (>512 MB).
+    sets = 512
+    q1, k1, v1, g1, b1 = inputs(1)
+    states = torch.zeros(sets, hv * d * d, device=dev)
+    out1 = torch.empty(hv * d, device=dev)
+
+    def dstep(i):
+        return lambda: ctx.gated_delta_net_f32_batched_in_place_at(
+            q1, k1, v1, g1, b1, states[i % sets], 0, 1, hk, hv, d, out1)
+
+    ms, graph = run.time([dstep(i) for i in range(1024)], 16)
+    del graph
+    gbs = GDN_DECODE_BYTES / (ms * 1e-3) / 1e9
+    res["decode"] = {"ms_per_token_layer": ms, "tok_s": 1 / (ms * 1e-3), "GB_s": gbs,
+                     "frac_hbm_peak": gbs / HBM_PEAK_GBS, "state_sets": sets, "cold": True}
+    del states
+
+    # Fused layer core per decode token: conv/split/L2 prologue + gated recurrence
+    # with norm-gated epilogue (4 kernels), cold over the same state sets.
+    channels = (2 * hk + hv) * d
+    qkv = torch.randn(channels, generator=gen, device=dev)
+    w = 0.5 * torch.randn(channels * 4, generator=gen, device=dev)
+    conv_states = torch.zeros(sets, channels * 3, device=dev)
+    states = torch.zeros(sets, hv * d * d, device=dev)
+    alpha = torch.randn(hv, generator=gen, device=dev)
+    beta = torch.randn(hv, generator=gen, device=dev)
+    dtb = torch.randn(hv, generator=gen, device=dev)
+    ssa = -torch.rand(hv, generator=gen, device=dev)
+    z = torch.randn(hv * d, generator=gen, device=dev)
+    nw = torch.ones(d, device=dev)
+    qb, kb, vb = (torch.empty(hk * d, device=dev), torch.empty(hk * d, device=dev),
+                  torch.empty(hv * d, device=dev))
+
+    def lstep(i):
+        def f():
+            ctx.qwen35_conv_split_l2_f32(qkv, conv_states[i % sets], 0, w, 4, 1, hk, hv, d, 1e-6,
+                                         qb, kb, vb)
+            ctx.qwen35_gdn_gated_f32(qb, kb, vb, alpha, beta, dtb, ssa, z, nw, states[i % sets],
+                                     0, 1, hk, hv, d, 1e-6, out1)
+        return f
+
+    ms, graph = run.time([lstep(i) for i in range(512)], 8)
+    del graph
+    res["decode_layer_core_fused"] = {"ms_per_token_layer": ms, "tok_s": 1 / (ms * 1e-3)}
+    del states, conv_states
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(kv_len, budget_s):
+    """Times the oracle's decode step (one core) on a bounded sample."""
+    import numpy as np
+
+    import oracle
+
+    cap = kv_len + 1
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal(HQ * D).astype(np.float32)
+    kc = rng.standard_normal(cap * HKV * D).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(cap * HKV * D).astype(np.float16).view(np.uint16)
+    gate = rng.standard_normal(HQ * D).astype(np.float32)
+    oracle.lib()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        out = oracle.attention_batched(q, kc, vc, 0, kv_len, 1, cap, HQ, HKV, D)
+        oracle.sigmoid_gate_mul(out, gate)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 2000:
+            break
+    s_per_step = el / n
+    return {"value": decode_bytes(kv_len) / s_per_step / 1e9, "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{n} C1 decode steps at L={kv_len} (oracle_attention_batched + gate, "
+                      f"double accumulation, one thread), {el:.1f} s; "
+                      f"{s_per_step * 1e3:.2f} ms/step",
+            "ms_per_step": s_per_step * 1e3,
+            "host_threads_available": os.cpu_count()}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--kv-len", type=int, default=4096)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--quick", action="store_true", help="headline only, no details")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import kraken_hip as kh
+
+    torch.cuda.init()
+    ctx = kh.Context()
+    run = Runner(torch, ctx)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1)
+
+    # Input generation and our launches share one stream, so they stay ordered.
+    with torch.cuda.stream(run.stream):
+        head = bench_decode(torch, ctx, run, args.kv_len, args.steps, args.warmup, True, gen)
+        progress(f"decode L={args.kv_len} cold: {head['GB_s']:.0f} GB/s")
+        details = {"decode_c1": [head]}
+        if not args.quick:
+            for kv in (1024, 8192, 16384):
+                details["decode_c1"].append(bench_decode(torch, ctx, run, kv, 400, 10, True, gen))
+            for kv in (1024, 4096, 16384):
+                details["decode_c1"].append(bench_decode(torch, ctx, run, kv, 400, 10, False,
+                                                         gen))
+            progress("decode details done")
+            gen.manual_seed(2)
+            details["prefill_c2"] = [bench_prefill(torch, ctx, run, p, 10, 2, gen)
+                                     for p in (0, 3072, 7168)]
+            progress("prefill done")
+            gen.manual_seed(3)
+            details["gdn_c3"] = bench_gdn(torch, ctx, run, gen)
+            progress("gdn done")
+    run.close()
+    ctx.close()
+
+    cpu = cpu_baseline(args.kv_len, args.cpu_seconds)
+    progress("cpu baseline done")
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", "decode_attention_c1_l4096_counters.json")
+    if os.path.exists(prof) and args.kv_len == 4096:
+        with open(prof) as f:
+            traffic = json.load(f).get("hbm_bytes_per_step")
+    line = {
+        "metric": METRIC,
+        "value": head["GB_s"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 KV, f32 accumulate",
+        "data": "synthetic (seeded N(0,1), torch generator seed 1)",
+        "config": {"workload": f"C1 decode attention: 1 query token, 8 Q / 2 KV heads, "
+                               f"head_dim 256, F16 KV cache of {args.kv_len} prior tokens, "
+                               "sigmoid output gate fused; KV sets rotated over >512 MB (cold)",
+                   "kv_len": args.kv_len, "heads": HQ, "kv_heads": HKV, "head_dim": D,
+                   "batch": 1, "kv_sets": head["kv_sets"],
+                   "bytes_per_step": decode_bytes(args.kv_len)},
+        "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": head["GB_s"] / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernels": "attention_split + attention_combine (one decode step)"},
+        "cpu_baseline": cpu,
+        "details": details,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
