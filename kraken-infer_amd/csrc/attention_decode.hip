@@ -8,17 +8,30 @@
 // out *= sigmoid(G) (qwen35_runtime.cpp:3347-3355) in the epilogue.
 //
 // Design (gfx950, wave64):
-//  * Pass 1 (attention_split): one workgroup of 4 waves per (token, kv_head,
-//    key split).  The workgroup serves all G query heads of the GQA group, so
-//    each K/V row is fetched once for G heads.  A wave takes 8 keys per step:
-//    lane = 8*key_slot + chunk, each lane loads 16-byte chunks (chunk + 8*i) of
-//    its key's K and V rows, so one load instruction moves 8 x 128 contiguous
-//    bytes.  Dot products reduce over the 8 lanes of a key with DPP; the online
-//    softmax runs in the log2 domain (q pre-scaled by log2(e)/sqrt(D)) with a
-//    wave-uniform running max.  Waves merge through LDS; the workgroup writes
-//    (m, l, o[G][D]) for its split, or the final (gated) output if unsplit.
-//  * Pass 2 (attention_combine): one workgroup per (token, head) rescales and
-//    sums the split partials, divides by the total denominator, applies the gate.
+//  * A workgroup of 16 waves (1024 threads) owns (token, kv_head, key split) and
+//    serves all G query heads of the GQA group, so each K/V row is fetched once
+//    for G heads.  Splits are sized to put about one workgroup on every CU: the
+//    whole KV stream is requested by the first load of each thread, which is
+//    what saturates HBM for the few MB of one decode step.
+//  * A key row (D elements) is spread over R = D / E lanes, each holding one
+//    16-byte chunk (E elements); a wave takes 64 / R keys per round (2 for the
+//    f16 D=256 cache), the workgroup 16 * 64 / R.  Rows are read through buffer
+//    resources bounded to the split, so lanes past its end get zeros from the
+//    range check without a memory access, every round issues the same loads
+//    with no branch, and the next two rounds are always in flight.
+//  * The query, pre-scaled into the log2 domain, sits in registers (a lane's G
+//    heads x E dims) when that is at most 32 floats, else in LDS.  Dot products
+//    reduce over a row's R lanes with DPP and the gfx950 permlane swaps; each
+//    wave runs its own online softmax against a wave-uniform reference max that
+//    moves only when a score exceeds it by 2^8 (lazy rescale), and stops after
+//    its last round that holds a key.
+//  * Waves merge (m, l, o[G][D]) through LDS with a log-sum-exp rescale.
+//    Unsplit, the workgroup writes the (gated) output directly.  Split, it
+//    stores its partial and a second, wide pass merges them: one workgroup per
+//    16-dim slice of each query head issues all of its partial loads at once,
+//    reduces with lane shuffles and LDS, divides by the denominator and applies
+//    the gate.  The kernel boundary orders the partial stores before the merge,
+//    which needs no atomics or cross-workgroup fences.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -30,10 +43,9 @@
 namespace kraken {
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 16;  // waves per decode workgroup
 constexpr int kThreads = 64 * kWaves;
-constexpr int kKeysPerWaveStep = 8;
-constexpr int kMaxSplits = 1024;
+constexpr int kMaxSplits = 256;  // merge pass: 64 subsets x 4 loads per thread
 
 struct DecodeParams {
   const float* query;
@@ -41,8 +53,8 @@ struct DecodeParams {
   const void* value_cache;
   const float* gate;
   float* output;
-  float* partial_o;   // [tokens][kv_heads][splits][G][D]
-  float* partial_ml;  // [tokens][kv_heads][splits][G][2]
+  float* part_o;   // [tokens][kv_heads][splits][G][D]
+  float* part_ml;  // [tokens][kv_heads][splits][G][2]
   uint32_t layer, start_position, tokens, capacity_tokens, heads, kv_heads;
   uint32_t keys_per_split, splits;
   float scale_log2;
@@ -75,170 +87,315 @@ struct KvTraits<float> {
 
 __device__ __forceinline__ float sigmoidf_acc(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-template <int D, int G, typename KV>
-__global__ __launch_bounds__(kThreads) void attention_split(DecodeParams p) {
-  using T = KvTraits<KV>;
-  constexpr int E = T::kPerChunk;
-  constexpr int kChunksPerRow = D / E;
-  constexpr int kChunksPerLane = kChunksPerRow / 8;
-  constexpr int kDimsPerLane = kChunksPerLane * E;  // == D / 8
-  static_assert(kChunksPerRow % 8 == 0, "row must split into 8 lanes of 16B chunks");
+// Lane geometry of a key row: E elements per 16-byte chunk, R lanes per row,
+// KW keys per wave per round, KPR keys per workgroup round.
+template <int D, typename KV>
+struct RowShape {
+  static constexpr int E = KvTraits<KV>::kPerChunk;
+  static constexpr int R = D / E;
+  static constexpr int KW = 64 / R;
+  static constexpr int KPR = kWaves * KW;
+  static_assert(R >= 8 && R <= 64 && 64 % R == 0, "row must span 8..64 lanes");
+};
 
-  __shared__ float s_o[kWaves][2][G][D];
+// Sum over the R lanes of a row (aligned lane group); result in all of them.
+template <int R>
+__device__ __forceinline__ float row_sum(float x) {
+  x = reduce8_sum(x);
+  if constexpr (R >= 16) {
+    x += dpp<kDppRowMirror>(x);
+  }
+  if constexpr (R >= 32) {
+    x = xor16_sum(x);
+  }
+  if constexpr (R >= 64) {
+    x = xor32_sum(x);
+  }
+  return x;
+}
+
+// Max over the KW key slots of a wave of a value that is uniform within each
+// row's lane group; result wave-uniform.
+template <int R>
+__device__ __forceinline__ float slots_max(float x) {
+  if constexpr (R <= 8) {
+    x = fmaxf(x, dpp<kDppRowRor8>(x));
+  }
+  if constexpr (R <= 16) {
+    x = xor16_max(x);
+  }
+  if constexpr (R <= 32) {
+    x = xor32_max(x);
+  }
+  return x;
+}
+
+// Lane-wise sum over the KW key slots (lanes sharing lane % R).
+template <int R>
+__device__ __forceinline__ float slots_sum(float x) {
+  if constexpr (R <= 8) {
+    x += dpp<kDppRowRor8>(x);
+  }
+  if constexpr (R <= 16) {
+    x = xor16_sum(x);
+  }
+  if constexpr (R <= 32) {
+    x = xor32_sum(x);
+  }
+  return x;
+}
+
+template <int D, int G>
+__device__ __forceinline__ void write_final(const DecodeParams& p, uint32_t token, uint32_t kvh,
+                                            int idx, float den, float acc) {
+  const int g = idx / D;
+  const int d = idx % D;
+  const size_t out_index = ((size_t)token * p.heads + kvh * G + g) * D + d;
+  float r = den == 0.0f ? 0.0f : acc / den;
+  if (p.gate != nullptr) {
+    r *= sigmoidf_acc(p.gate[out_index]);
+  }
+  p.output[out_index] = r;
+}
+
+// Lazy rescale slack (log2 domain): a wave exponentiates against a reference
+// max that moves only when a score exceeds it by more than this, so p <= 2^8
+// (far from f32 overflow) and most rounds skip the rescale of o and l.  The
+// result is exact either way: o and l always share the same reference.
+constexpr float kRescaleSlack = 8.0f;
+
+__device__ __forceinline__ float uniform_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, x)));
+}
+
+template <int D, int G, typename KV>
+__global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams p) {
+  using T = KvTraits<KV>;
+  using S = RowShape<D, KV>;
+  constexpr int E = S::E;
+  constexpr int R = S::R;
+  constexpr int KW = S::KW;
+  constexpr int KPR = S::KPR;
+  // A lane's query slice (G heads x its E dims) lives in registers when small;
+  // otherwise in LDS, read by all lanes that hold the same dims.
+  constexpr bool kQRegs = G * E <= 32;
+  constexpr int kQVec = G * D / 4;
+  constexpr int kOutPerThread = (G * D + kThreads - 1) / kThreads;
+  static_assert(kQVec <= kThreads, "query staging takes one float4 per thread");
+
+  // LDS query: G*D floats plus one float4 of padding that threads past the end
+  // write into, so the store needs no branch (a branch would let the compiler
+  // sink the query load below the K/V loads and wait for all of them).
+  __shared__ __attribute__((aligned(16))) float s_q[kQRegs ? 4 : G * D + 4];
+  __shared__ float s_o[kWaves][G * D];
   __shared__ float s_m[kWaves][G];
   __shared__ float s_l[kWaves][G];
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int slot = lane >> 3;
-  const int c8 = lane & 7;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kslot = lane / R;
+  const int c = lane % R;
   const uint32_t split = blockIdx.x;
   const uint32_t kvh = blockIdx.y;
   const uint32_t token = blockIdx.z;
-  const uint32_t position = p.start_position + token;
-  const uint32_t n_keys = position + 1u;
+  const uint32_t n_keys = p.start_position + token + 1u;
   const uint32_t key_begin = split * p.keys_per_split;
-  uint32_t key_end = key_begin + p.keys_per_split;
-  if (key_end > n_keys) {
-    key_end = n_keys;
-  }
+  const uint32_t key_end = min(n_keys, key_begin + p.keys_per_split);
+  const uint32_t count = key_end > key_begin ? key_end - key_begin : 0u;
 
-  // Query heads kvh*G .. kvh*G+G-1, pre-scaled into the log2 domain.
-  float qv[G][kDimsPerLane];
+  const size_t row_stride = (size_t)p.kv_heads * D;
+  const KV* kbase = static_cast<const KV*>(p.key_cache) +
+                    (size_t)p.layer * p.capacity_tokens * row_stride + (size_t)kvh * D;
+  const KV* vbase = static_cast<const KV*>(p.value_cache) +
+                    (size_t)p.layer * p.capacity_tokens * row_stride + (size_t)kvh * D;
+
+  // The query heads kvh*G .. kvh*G+G-1 (G*D contiguous floats) are loaded
+  // before K/V: vector loads retire in issue order, so using the query waits
+  // only for the query (measured faster than issuing K/V first).
+  const float* qhead = p.query + ((size_t)token * p.heads + kvh * G) * D;
+  float4 qraw[kQRegs ? G * E / 4 : 1];
+  auto load_query = [&]() {
+    if constexpr (kQRegs) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float* qrow = p.query + ((size_t)token * p.heads + kvh * G + g) * D;
+      for (int g = 0; g < G; ++g) {
 #pragma unroll
-    for (int i = 0; i < kChunksPerLane; ++i) {
-      const int d0 = (c8 + 8 * i) * E;
+        for (int e = 0; e < E; e += 4) {
+          qraw[(g * E + e) / 4] = *reinterpret_cast<const float4*>(qhead + g * D + c * E + e);
+        }
+      }
+    } else {
+      qraw[0] = reinterpret_cast<const float4*>(qhead)[tid < kQVec ? tid : 0];
+    }
+  };
+  load_query();
+
+  // K/V rows of the split through buffer resources based at its first row and
+  // ending at its last: lanes and rounds past the end read zeros from the range
+  // check with no memory access (and are masked out of the softmax).
+  const uint32_t row_bytes = (uint32_t)(row_stride * sizeof(KV));
+  const __amdgpu_buffer_rsrc_t krsrc =
+    make_buffer_rsrc(kbase + (size_t)key_begin * row_stride, count * row_bytes);
+  const __amdgpu_buffer_rsrc_t vrsrc =
+    make_buffer_rsrc(vbase + (size_t)key_begin * row_stride, count * row_bytes);
+  const uint32_t wave_first = (uint32_t)(wave * KW);  // wave's first key in a round
+  const uint32_t lane_key = wave_first + (uint32_t)kslot;
+  const uint32_t lane_off = lane_key * row_bytes + 16u * c;
+
+  // Two register sets in ping-pong (A: even rounds, B: odd rounds), each
+  // reloaded in place right after its round computes, so the next two rounds
+  // are always in flight and no loaded register is ever copied (a copy would
+  // have to wait for its load).
+  // The scheduling barriers pin the issue order (K then V, even then odd
+  // round), which the wait counts in the loop below depend on.
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4_t ka = buffer_load_nt_b128(krsrc, lane_off);
+  u32x4_t va = buffer_load_nt_b128(vrsrc, lane_off);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4_t kb_ = buffer_load_nt_b128(krsrc, lane_off + KPR * row_bytes);
+  u32x4_t vb_ = buffer_load_nt_b128(vrsrc, lane_off + KPR * row_bytes);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Query pre-scaled into the log2 domain.
+  float qr[kQRegs ? G : 1][kQRegs ? E : 1];
+  if constexpr (kQRegs) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
 #pragma unroll
       for (int e = 0; e < E; e += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(qrow + d0 + e);
-        qv[g][i * E + e + 0] = v.x * p.scale_log2;
-        qv[g][i * E + e + 1] = v.y * p.scale_log2;
-        qv[g][i * E + e + 2] = v.z * p.scale_log2;
-        qv[g][i * E + e + 3] = v.w * p.scale_log2;
+        const float4 t = qraw[(g * E + e) / 4];
+        qr[g][e + 0] = t.x * p.scale_log2;
+        qr[g][e + 1] = t.y * p.scale_log2;
+        qr[g][e + 2] = t.z * p.scale_log2;
+        qr[g][e + 3] = t.w * p.scale_log2;
       }
     }
+  } else {
+    reinterpret_cast<float4*>(s_q)[tid < kQVec ? tid : kQVec] =
+      make_float4(qraw[0].x * p.scale_log2, qraw[0].y * p.scale_log2, qraw[0].z * p.scale_log2,
+                  qraw[0].w * p.scale_log2);
+    __syncthreads();
   }
 
-  float m[G];
+  float m[G];  // wave-uniform reference max (log2 domain)
   float l[G];
-  float o[G][kDimsPerLane];
+  float o[G][E];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
     l[g] = 0.0f;
 #pragma unroll
-    for (int d = 0; d < kDimsPerLane; ++d) {
-      o[g][d] = 0.0f;
+    for (int e = 0; e < E; ++e) {
+      o[g][e] = 0.0f;
     }
   }
 
-  const size_t row_stride = (size_t)p.kv_heads * D;  // elements between consecutive keys
-  const KV* kbase = static_cast<const KV*>(p.key_cache) +
-                    ((size_t)p.layer * p.capacity_tokens) * row_stride + (size_t)kvh * D;
-  const KV* vbase = static_cast<const KV*>(p.value_cache) +
-                    ((size_t)p.layer * p.capacity_tokens) * row_stride + (size_t)kvh * D;
-
-  for (uint32_t kb = key_begin + wave * kKeysPerWaveStep; kb < key_end;
-       kb += kWaves * kKeysPerWaveStep) {
-    const uint32_t key = kb + slot;
-    const bool valid = key < key_end;
-    u32x4_t kraw[kChunksPerLane];
-    u32x4_t vraw[kChunksPerLane];
-    if (valid) {
-      const u32x4_t* krow = reinterpret_cast<const u32x4_t*>(kbase + (size_t)key * row_stride);
-      const u32x4_t* vrow = reinterpret_cast<const u32x4_t*>(vbase + (size_t)key * row_stride);
-#pragma unroll
-      for (int i = 0; i < kChunksPerLane; ++i) {
-        kraw[i] = __builtin_nontemporal_load(krow + c8 + 8 * i);
-      }
-#pragma unroll
-      for (int i = 0; i < kChunksPerLane; ++i) {
-        vraw[i] = __builtin_nontemporal_load(vrow + c8 + 8 * i);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kChunksPerLane; ++i) {
-        kraw[i] = u32x4_t{0u, 0u, 0u, 0u};
-        vraw[i] = u32x4_t{0u, 0u, 0u, 0u};
-      }
-    }
-    float kf[kDimsPerLane];
-#pragma unroll
-    for (int i = 0; i < kChunksPerLane; ++i) {
-      T::to_float(kraw[i], kf + i * E);
-    }
-    float s[G];
+  // One round: keys [kr, kr + KPR) of the split (relative), this lane's key at
+  // kr + lane_key.
+  auto round = [&](uint32_t kr, const u32x4_t& kraw, const u32x4_t& vraw) {
+    const bool valid = kr + lane_key < count;
+    float kf[E];
+    T::to_float(kraw, kf);
+    float sc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float acc = 0.0f;
+      if constexpr (kQRegs) {
 #pragma unroll
-      for (int d = 0; d < kDimsPerLane; ++d) {
-        acc = fmaf(qv[g][d], kf[d], acc);
+        for (int e = 0; e < E; ++e) {
+          acc = fmaf(qr[g][e], kf[e], acc);
+        }
+      } else {
+        // An opaque zero in the LDS address keeps the compiler from hoisting
+        // the G*E loop-invariant query words into registers across rounds.
+        int qz;
+        __asm__ volatile("v_mov_b32 %0, 0" : "=v"(qz));
+        const float* sq = s_q + qz + g * D + c * E;
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+          const float4 q4 = *reinterpret_cast<const float4*>(sq + e);
+          acc = fmaf(q4.x, kf[e + 0], acc);
+          acc = fmaf(q4.y, kf[e + 1], acc);
+          acc = fmaf(q4.z, kf[e + 2], acc);
+          acc = fmaf(q4.w, kf[e + 3], acc);
+        }
       }
-      acc = reduce8_sum(acc);
-      s[g] = valid ? acc : -INFINITY;
+      // The cross-lane reduction runs for every lane (it cannot sit under a
+      // divergent mask); invalid keys are masked afterwards.
+      const float red = row_sum<R>(acc);
+      sc[g] = valid ? red : -INFINITY;
     }
-    float vf[kDimsPerLane];
-#pragma unroll
-    for (int i = 0; i < kChunksPerLane; ++i) {
-      T::to_float(vraw[i], vf + i * E);
-    }
+    float vf[E];
+    T::to_float(vraw, vf);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float step_max = halves_max(across8_max(s[g]));
-      if (step_max > m[g]) {  // wave-uniform branch
-        const float corr = fast_exp2(m[g] - step_max);
+      const float bmax = uniform_f(slots_max<R>(sc[g]));
+      if (bmax > m[g] + kRescaleSlack) {
+        const float corr = fast_exp2(m[g] - bmax);  // 0 on the first valid round
+        m[g] = bmax;
         l[g] *= corr;
 #pragma unroll
-        for (int d = 0; d < kDimsPerLane; ++d) {
-          o[g][d] *= corr;
+        for (int e = 0; e < E; ++e) {
+          o[g][e] *= corr;
         }
-        m[g] = step_max;
       }
-      const float pr = valid ? fast_exp2(s[g] - m[g]) : 0.0f;
+      const float pr = valid ? fast_exp2(sc[g] - m[g]) : 0.0f;
       l[g] += pr;
 #pragma unroll
-      for (int d = 0; d < kDimsPerLane; ++d) {
-        o[g][d] = fmaf(pr, vf[d], o[g][d]);
+      for (int e = 0; e < E; ++e) {
+        o[g][e] = fmaf(pr, vf[e], o[g][e]);
       }
     }
+  };
+
+  // Each wave stops after its last round holding a key of the split.
+  for (uint32_t kr = 0; kr + wave_first < count; kr += 2 * KPR) {
+    round(kr, ka, va);
+    ka = buffer_load_nt_b128(krsrc, lane_off + (kr + 2 * KPR) * row_bytes);
+    va = buffer_load_nt_b128(vrsrc, lane_off + (kr + 2 * KPR) * row_bytes);
+    if (kr + KPR + wave_first >= count) {
+      break;
+    }
+    round(kr + KPR, kb_, vb_);
+    kb_ = buffer_load_nt_b128(krsrc, lane_off + (kr + 3 * KPR) * row_bytes);
+    vb_ = buffer_load_nt_b128(vrsrc, lane_off + (kr + 3 * KPR) * row_bytes);
   }
 
-  // Merge the 8 key slots of the wave: slots 0..3 and 4..7 within each half via
-  // DPP, the two halves through LDS.
+  // Wave partial: the KW key slots share the wave's running max, so their
+  // accumulators add lane-wise.
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    // l is replicated over the 8 lanes of a slot; sum over slots.
-    const float lw = halves_sum(across8_sum(l[g]));
+    const float lw = slots_sum<R>(l[g]);
 #pragma unroll
-    for (int d = 0; d < kDimsPerLane; ++d) {
-      o[g][d] = across8_sum(o[g][d]);
+    for (int e = 0; e < E; ++e) {
+      o[g][e] = slots_sum<R>(o[g][e]);
     }
     if (lane == 0) {
       s_m[wave][g] = m[g];
       s_l[wave][g] = lw;
     }
-    if ((lane & 31) < 8) {
-      const int half = lane >> 5;
+    if (kslot == 0) {
 #pragma unroll
-      for (int i = 0; i < kChunksPerLane; ++i) {
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          s_o[wave][half][g][(c8 + 8 * i) * E + e] = o[g][i * E + e];
-        }
+      for (int e = 0; e < E; e += 4) {
+        *reinterpret_cast<float4*>(&s_o[wave][g * D + c * E + e]) =
+          make_float4(o[g][e], o[g][e + 1], o[g][e + 2], o[g][e + 3]);
       }
     }
   }
   __syncthreads();
 
-  // Workgroup merge: thread handles (g, d) pairs.
+  // Workgroup merge of the 16 wave partials; thread handles outputs
+  // idx = tid + k*kThreads of the G*D block.
   const size_t tk = (size_t)token * p.kv_heads + kvh;
-  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+  float* po = p.part_o + (tk * p.splits + split) * (size_t)(G * D);
+  float* pml = p.part_ml + (tk * p.splits + split) * (size_t)(G * 2);
+#pragma unroll
+  for (int k = 0; k < kOutPerThread; ++k) {
+    const int idx = tid + k * kThreads;
+    if (idx >= G * D) {
+      continue;
+    }
     const int g = idx / D;
-    const int d = idx % D;
     float mx = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
@@ -249,113 +406,134 @@ __global__ __launch_bounds__(kThreads) void attention_split(DecodeParams p) {
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
       const float wt = s_m[w][g] == -INFINITY ? 0.0f : fast_exp2(s_m[w][g] - mx);
-      acc += wt * (s_o[w][0][g][d] + s_o[w][1][g][d]);
-      den += wt * s_l[w][g];
+      acc = fmaf(wt, s_o[w][idx], acc);
+      den = fmaf(wt, s_l[w][g], den);
     }
     if (p.splits == 1) {
-      const uint32_t head = kvh * G + g;
-      const size_t out_index = ((size_t)token * p.heads + head) * D + d;
-      float r = den == 0.0f ? 0.0f : acc / den;
-      if (p.gate != nullptr) {
-        r *= sigmoidf_acc(p.gate[out_index]);
-      }
-      p.output[out_index] = r;
+      write_final<D, G>(p, token, kvh, idx, den, acc);
     } else {
-      const size_t base = (tk * p.splits + split) * G;
-      p.partial_o[(base + g) * D + d] = acc;
-      if (d == 0) {
-        p.partial_ml[(base + g) * 2 + 0] = mx;
-        p.partial_ml[(base + g) * 2 + 1] = den;
+      po[idx] = acc;
+      if (idx % D == 0) {
+        pml[g * 2 + 0] = mx;
+        pml[g * 2 + 1] = den;
       }
     }
   }
 }
 
-// Pass 2: one workgroup per (token, head).
-template <int D>
-__global__ __launch_bounds__(256) void attention_combine(CombineArgs p) {
-  constexpr int kChunks = D / 4;             // float4 chunks per row
-  constexpr int kSubsets = 256 / kChunks;    // split subsets summed in parallel
-  __shared__ float s_w[kMaxSplits];
-  __shared__ float s_red[256];
-  __shared__ float4 s_acc[kSubsets][kChunks];
+// Split merge: one workgroup per (token, head, 16-dim slice).  256 threads =
+// 4 float4 chunks x 64 split subsets; every thread issues all of its (<= 4)
+// partial loads before using any.  The global max and the weighted sums are
+// reduced across subsets with lane shuffles (lane bits 2..5) and then across
+// the 4 waves through LDS.
+constexpr int kMergeDims = 16;
+constexpr int kMergeChunks = kMergeDims / 4;
+static_assert(kMergeChunks == 4, "merge lane reductions run over lane bits 2..5");
+constexpr int kMergeSubsets = 256 / kMergeChunks;
+constexpr int kMergePerThread = kMaxSplits / kMergeSubsets;
 
+// Reductions over lane bits 2..5 (the split subsets of one chunk): rotations by
+// 4 and 8 within each 16-lane row, then the xor-16 and xor-32 exchanges.
+__device__ __forceinline__ float merge_lanes_max(float x) {
+  x = fmaxf(x, dpp<kDppRowRor4>(x));
+  x = fmaxf(x, dpp<kDppRowRor8>(x));
+  return xor32_max(xor16_max(x));
+}
+
+__device__ __forceinline__ float merge_lanes_sum(float x) {
+  x += dpp<kDppRowRor4>(x);
+  x += dpp<kDppRowRor8>(x);
+  return xor32_sum(xor16_sum(x));
+}
+
+__global__ __launch_bounds__(256) void attention_merge(CombineArgs p) {
+  __shared__ float s_mx[4];
+  __shared__ float s_den[4][kMergeChunks];
+  __shared__ float4 s_acc[4][kMergeChunks];
   const uint32_t group = p.heads / p.kv_heads;
   const uint32_t token = blockIdx.x;
   const uint32_t head = blockIdx.y;
   const uint32_t kvh = head / group;
   const uint32_t g = head % group;
-  const size_t tk = (size_t)token * p.kv_heads + kvh;
+  const uint32_t d0 = blockIdx.z * kMergeDims;
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int chunk = tid % kMergeChunks;
+  const int subset = tid / kMergeChunks;
+  const size_t base = (size_t)token * p.kv_heads + kvh;
 
-  // Global max over splits.
-  float mx = -INFINITY;
-  for (uint32_t s = tid; s < p.splits; s += 256) {
-    mx = fmaxf(mx, p.partial_ml[((tk * p.splits + s) * group + g) * 2]);
-  }
-  s_red[tid] = mx;
-  __syncthreads();
-  for (int stride = 128; stride > 0; stride >>= 1) {
-    if (tid < stride) {
-      s_red[tid] = fmaxf(s_red[tid], s_red[tid + stride]);
-    }
-    __syncthreads();
-  }
-  mx = s_red[0];
-  __syncthreads();
-  float den = 0.0f;
-  for (uint32_t s = tid; s < p.splits; s += 256) {
-    const float* ml = p.partial_ml + ((tk * p.splits + s) * group + g) * 2;
-    const float w = ml[0] == -INFINITY ? 0.0f : fast_exp2(ml[0] - mx);
-    s_w[s] = w;
-    den += w * ml[1];
-  }
-  s_red[tid] = den;
-  __syncthreads();
-  for (int stride = 128; stride > 0; stride >>= 1) {
-    if (tid < stride) {
-      s_red[tid] += s_red[tid + stride];
-    }
-    __syncthreads();
-  }
-  den = s_red[0];
-
-  const int chunk = tid % kChunks;
-  const int subset = tid / kChunks;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  const float4* po = reinterpret_cast<const float4*>(p.partial_o);
-  for (uint32_t s = subset; s < p.splits; s += kSubsets) {
-    const float w = s_w[s];
-    if (w != 0.0f) {
-      const float4 v = po[((tk * p.splits + s) * group + g) * kChunks + chunk];
-      acc.x = fmaf(w, v.x, acc.x);
-      acc.y = fmaf(w, v.y, acc.y);
-      acc.z = fmaf(w, v.z, acc.z);
-      acc.w = fmaf(w, v.w, acc.w);
-    }
-  }
-  s_acc[subset][chunk] = acc;
-  __syncthreads();
-  if (tid < kChunks) {
-    float4 r = s_acc[0][tid];
-    for (int i = 1; i < kSubsets; ++i) {
-      const float4 v = s_acc[i][tid];
-      r.x += v.x;
-      r.y += v.y;
-      r.z += v.z;
-      r.w += v.w;
-    }
-    const float inv = den == 0.0f ? 0.0f : 1.0f / den;
-    const size_t out_index = ((size_t)token * p.heads + head) * D + tid * 4;
-    float out[4] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
-    if (p.gate != nullptr) {
+  float mv[kMergePerThread], lv[kMergePerThread];
+  float4 ov[kMergePerThread];
+  // Unconditional loads from clamped indices (masked below) keep every load in
+  // flight at once.
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        out[e] *= sigmoidf_acc(p.gate[out_index + e]);
-      }
-    }
-    *reinterpret_cast<float4*>(p.output + out_index) = make_float4(out[0], out[1], out[2], out[3]);
+  for (int j = 0; j < kMergePerThread; ++j) {
+    const uint32_t s = min(subset + j * kMergeSubsets, p.splits - 1u);
+    const size_t unit = (base * p.splits + s) * group + g;
+    mv[j] = p.partial_ml[unit * 2];
+    lv[j] = p.partial_ml[unit * 2 + 1];
+    ov[j] = *reinterpret_cast<const float4*>(p.partial_o + unit * p.head_dim + d0 + chunk * 4);
   }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kMergePerThread; ++j) {
+    if (subset + j * kMergeSubsets >= p.splits) {
+      mv[j] = -INFINITY;
+    }
+    mx = fmaxf(mx, mv[j]);
+  }
+  mx = merge_lanes_max(mx);
+  if (lane == 0) {
+    s_mx[wave] = mx;
+  }
+  __syncthreads();
+  const float gmx = fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));
+  float den = 0.0f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < kMergePerThread; ++j) {
+    const float w = mv[j] == -INFINITY ? 0.0f : fast_exp2(mv[j] - gmx);
+    den = fmaf(w, lv[j], den);
+    acc.x = fmaf(w, ov[j].x, acc.x);
+    acc.y = fmaf(w, ov[j].y, acc.y);
+    acc.z = fmaf(w, ov[j].z, acc.z);
+    acc.w = fmaf(w, ov[j].w, acc.w);
+  }
+  den = merge_lanes_sum(den);
+  acc.x = merge_lanes_sum(acc.x);
+  acc.y = merge_lanes_sum(acc.y);
+  acc.z = merge_lanes_sum(acc.z);
+  acc.w = merge_lanes_sum(acc.w);
+  if (lane < kMergeChunks) {
+    s_den[wave][chunk] = den;
+    s_acc[wave][chunk] = acc;
+  }
+  __syncthreads();
+  if (tid >= kMergeChunks) {
+    return;
+  }
+  float tden = 0.0f;
+  float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    tden += s_den[w][chunk];
+    r.x += s_acc[w][chunk].x;
+    r.y += s_acc[w][chunk].y;
+    r.z += s_acc[w][chunk].z;
+    r.w += s_acc[w][chunk].w;
+  }
+
+  const float inv = tden == 0.0f ? 0.0f : 1.0f / tden;
+  const size_t out_index = ((size_t)token * p.heads + head) * p.head_dim + d0 + chunk * 4;
+  float out[4] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
+  if (p.gate != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      out[e] *= sigmoidf_acc(p.gate[out_index + e]);
+    }
+  }
+  *reinterpret_cast<float4*>(p.output + out_index) = make_float4(out[0], out[1], out[2], out[3]);
 }
 
 // Shapes outside the tuned templates: one wave per (token, head), 64 lanes over
@@ -422,25 +600,26 @@ struct SplitPlan {
   uint32_t splits;
 };
 
+// Splits per (token, kv_head) so that the grid puts about one workgroup on each
+// CU; a split may be any number of keys (a partial last round is masked).
 SplitPlan plan_splits(const AttentionArgs& a, int cu_count) {
   const uint64_t max_keys = (uint64_t)a.start_position + a.tokens;  // last query's keys
   const uint64_t units = (uint64_t)a.tokens * a.kv_heads;
-  const uint64_t target_blocks = 2ull * (uint64_t)(cu_count > 0 ? cu_count : 256);
-  uint64_t kps = (units * max_keys + target_blocks - 1) / target_blocks;
-  const uint64_t step = kWaves * kKeysPerWaveStep;
+  const uint64_t slots = (uint64_t)(cu_count > 0 ? cu_count : 256);
+  uint64_t splits_target = slots / units;
+  if (splits_target < 1) {
+    splits_target = 1;
+  }
+  uint64_t kps = (max_keys + splits_target - 1) / splits_target;
   if (const char* env = std::getenv("KRAKEN_DECODE_KEYS_PER_SPLIT")) {
     const long v = std::strtol(env, nullptr, 10);
     if (v > 0) {
       kps = (uint64_t)v;
     }
   }
-  kps = ((kps + step - 1) / step) * step;
-  if (kps < step) {
-    kps = step;
-  }
   uint64_t splits = (max_keys + kps - 1) / kps;
   if (splits > kMaxSplits) {
-    kps = ((max_keys + kMaxSplits - 1) / kMaxSplits + step - 1) / step * step;
+    kps = (max_keys + kMaxSplits - 1) / kMaxSplits;
     splits = (max_keys + kps - 1) / kps;
   }
   return SplitPlan{(uint32_t)kps, (uint32_t)splits};
@@ -448,7 +627,7 @@ SplitPlan plan_splits(const AttentionArgs& a, int cu_count) {
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
-// The tuned kernels move 16-byte chunks; shapes or pointers outside that contract
+// The tuned kernel moves 16-byte chunks; shapes or pointers outside that contract
 // take the generic kernel.
 bool tuned_args(const AttentionArgs& a) {
   const uint32_t d = a.head_dim;
@@ -457,26 +636,29 @@ bool tuned_args(const AttentionArgs& a) {
       !aligned16(a.output)) {
     return false;
   }
-  if (d == 256) {
-    return g == 1 || g == 2 || g == 4;
+  return (d == 256 || d == 128 || d == 64) && (g == 1 || g == 2 || g == 4 || g == 8);
+}
+
+size_t data_bytes(const AttentionArgs& a, const SplitPlan& plan) {
+  if (plan.splits <= 1) {
+    return 0;
   }
-  if (d == 128 || d == 64) {
-    return g == 1 || g == 2 || g == 4 || g == 8;
-  }
-  return false;
+  const size_t g = a.heads / a.kv_heads;
+  const size_t units = (size_t)a.tokens * a.kv_heads;
+  return units * plan.splits * g * (a.head_dim + 2) * sizeof(float);
 }
 
 template <int D, int G, typename KV>
 hipError_t launch_tuned(const DecodeParams& p, hipStream_t stream) {
-  dim3 grid(p.splits, p.kv_heads, p.tokens);
-  attention_split<D, G, KV><<<grid, kThreads, 0, stream>>>(p);
+  const dim3 grid(p.splits, p.kv_heads, p.tokens);
+  attention_decode_kernel<D, G, KV><<<grid, kThreads, 0, stream>>>(p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) {
     return e;
   }
   CombineArgs c{};
-  c.partial_o = p.partial_o;
-  c.partial_ml = p.partial_ml;
+  c.partial_o = p.part_o;
+  c.partial_ml = p.part_ml;
   c.gate = p.gate;
   c.output = p.output;
   c.tokens = p.tokens;
@@ -495,6 +677,7 @@ hipError_t dispatch_kv(const DecodeParams& p, uint32_t d, uint32_t g, bool tuned
       if (g == 1) return launch_tuned<256, 1, KV>(p, stream);
       if (g == 2) return launch_tuned<256, 2, KV>(p, stream);
       if (g == 4) return launch_tuned<256, 4, KV>(p, stream);
+      if (g == 8) return launch_tuned<256, 8, KV>(p, stream);
       break;
     case 128:
       if (g == 1) return launch_tuned<128, 1, KV>(p, stream);
@@ -518,30 +701,32 @@ hipError_t dispatch_kv(const DecodeParams& p, uint32_t d, uint32_t g, bool tuned
 }  // namespace
 
 hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream) {
-  if (c.splits > kMaxSplits) {
+  if (c.splits > kMaxSplits || c.head_dim % kMergeDims != 0) {
     return hipErrorInvalidValue;
   }
-  const dim3 grid(c.tokens, c.heads);
-  switch (c.head_dim) {
-    case 256: attention_combine<256><<<grid, 256, 0, stream>>>(c); break;
-    case 128: attention_combine<128><<<grid, 256, 0, stream>>>(c); break;
-    case 64: attention_combine<64><<<grid, 256, 0, stream>>>(c); break;
-    default: return hipErrorInvalidValue;
-  }
+  const dim3 grid(c.tokens, c.heads, c.head_dim / kMergeDims);
+  attention_merge<<<grid, 256, 0, stream>>>(c);
   return hipGetLastError();
 }
 
+// The tuned kernel's buffer offsets are 32-bit: a split's byte span plus the
+// two prefetched steps past its end must stay below 2^31.
+bool offsets_fit(const AttentionArgs& a, const SplitPlan& plan) {
+  const uint64_t row_bytes = (uint64_t)a.kv_heads * a.head_dim * (a.kv_f16 ? 2u : 4u);
+  // At most 128 keys per round (D=64, f16), two rounds ahead of the last one.
+  return ((uint64_t)plan.keys_per_split + 3u * 128u) * row_bytes < (1ull << 31);
+}
+
+bool use_tuned(const AttentionArgs& a, const SplitPlan& plan) {
+  return tuned_args(a) && offsets_fit(a, plan);
+}
+
 size_t attention_decode_workspace_bytes(const AttentionArgs& a, int cu_count) {
-  const uint32_t g = a.heads / a.kv_heads;
-  if (!tuned_args(a)) {
-    return 0;
-  }
   const SplitPlan plan = plan_splits(a, cu_count);
-  if (plan.splits <= 1) {
+  if (!use_tuned(a, plan)) {
     return 0;
   }
-  const size_t units = (size_t)a.tokens * a.kv_heads * plan.splits * g;
-  return units * (a.head_dim + 2) * sizeof(float);
+  return kCounterRegionBytes + data_bytes(a, plan);
 }
 
 hipError_t launch_attention_decode(const AttentionArgs& a, int cu_count, void* workspace,
@@ -560,23 +745,22 @@ hipError_t launch_attention_decode(const AttentionArgs& a, int cu_count, void* w
   p.heads = a.heads;
   p.kv_heads = a.kv_heads;
   p.scale_log2 = (1.0f / sqrtf((float)a.head_dim)) * kLog2e;
-  if (tuned_args(a)) {
-    const SplitPlan plan = plan_splits(a, cu_count);
+  const SplitPlan plan = plan_splits(a, cu_count);
+  const bool tuned = use_tuned(a, plan);
+  p.splits = 1;
+  if (tuned) {
     p.keys_per_split = plan.keys_per_split;
     p.splits = plan.splits;
     if (plan.splits > 1) {
-      const size_t units = (size_t)a.tokens * a.kv_heads * plan.splits * g;
-      if (workspace == nullptr || workspace_bytes < units * (a.head_dim + 2) * sizeof(float)) {
+      if (workspace == nullptr || workspace_bytes < kCounterRegionBytes + data_bytes(a, plan)) {
         return hipErrorInvalidValue;
       }
-      p.partial_o = static_cast<float*>(workspace);
-      p.partial_ml = p.partial_o + units * a.head_dim;
+      const size_t units = (size_t)a.tokens * a.kv_heads;
+      // Partials follow the counter region, which they must never overlap.
+      p.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterRegionBytes);
+      p.part_ml = p.part_o + units * plan.splits * g * a.head_dim;
     }
-  } else {
-    p.keys_per_split = 0;
-    p.splits = 1;
   }
-  const bool tuned = tuned_args(a);
   return a.kv_f16 ? dispatch_kv<half_t>(p, a.head_dim, g, tuned, stream)
                   : dispatch_kv<float>(p, a.head_dim, g, tuned, stream);
 }

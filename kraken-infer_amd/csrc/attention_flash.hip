@@ -318,7 +318,7 @@ size_t attention_flash_workspace_bytes(const AttentionArgs& a, int cu_count) {
     return 0;
   }
   const size_t units = (size_t)a.tokens * a.heads * plan.splits;
-  return units * (kD + 2) * sizeof(float);
+  return kCounterRegionBytes + units * (kD + 2) * sizeof(float);
 }
 
 hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* workspace,
@@ -343,10 +343,12 @@ hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* wo
   p.scale_log2 = (1.0f / sqrtf(256.0f)) * kLog2e;
   if (plan.splits > 1) {
     const size_t units = (size_t)a.tokens * a.heads * plan.splits;
-    if (workspace == nullptr || workspace_bytes < units * (kD + 2) * sizeof(float)) {
+    if (workspace == nullptr ||
+        workspace_bytes < kCounterRegionBytes + units * (kD + 2) * sizeof(float)) {
       return hipErrorInvalidValue;
     }
-    p.partial_o = static_cast<float*>(workspace);
+    // Partials follow the counter region, which they must never overlap.
+    p.partial_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterRegionBytes);
     p.partial_ml = p.partial_o + units * kD;
   }
   const uint32_t g = a.heads / a.kv_heads;

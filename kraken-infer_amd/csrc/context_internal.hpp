@@ -99,6 +99,12 @@ int strided_region_end(size_t offset, size_t rows, size_t stride, size_t row_siz
 // Implemented by the kernel translation units; all enqueue on `stream` and
 // return hipSuccess or the launch error.
 
+// The context workspace starts with a fixed region of uint32 counters used by
+// in-kernel last-arriver reductions.  Counters start at zero and every kernel
+// that uses one returns it to zero, so the region is never cleared per call and
+// no partial-result buffer may overlap it.
+constexpr size_t kCounterRegionBytes = size_t(1) << 20;
+
 struct AttentionArgs {
   const float* query;
   const void* key_cache;

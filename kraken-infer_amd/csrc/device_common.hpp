@@ -27,6 +27,7 @@ constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141;  // lane i <-> 7-i within 8
 constexpr int kDppRowMirror = 0x140;      // lane i <-> 15-i within 16
+constexpr int kDppRowRor4 = 0x124;        // lane i <- (i+4) mod 16 within 16 (rotate by 4)
 constexpr int kDppRowRor8 = 0x128;        // lane i <-> i^8 within 16 (rotate by 8)
 // ds_swizzle bit mode: and_mask=0x1F, xor_mask=0x10 -> lane ^ 16 within 32.
 constexpr int kSwizzleXor16 = 0x401F;
@@ -39,6 +40,35 @@ __device__ __forceinline__ float dpp(float x) {
 
 __device__ __forceinline__ float swizzle_xor16(float x) {
   return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), kSwizzleXor16));
+}
+
+// gfx950 lane-half exchanges (VALU, no LDS crossbar).  With the same register
+// as both operands, v_permlane32_swap returns the pair (lanes 0-31 broadcast to
+// both halves, lanes 32-63 broadcast to both halves); v_permlane16_swap does
+// the same for the 16-lane rows of each half.  Combining the pair gives every
+// lane op(x[l], x[l ^ 32]) or op(x[l], x[l ^ 16]).
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Sum over the 8 lanes of an aligned 8-lane group; result in all 8 lanes.
@@ -98,5 +128,28 @@ __device__ __forceinline__ float wave_sum(float x) { return halves_sum(reduce32_
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+// Raw (unswizzled, stride 0) buffer resource over `bytes` bytes from `base`;
+// word 3 = 0x00020000 is the gfx9-family data format for raw dword access.
+// A load whose offset is at or past `bytes` returns zeros without a memory
+// access.  Base and size must be wave-uniform (the resource lives in SGPRs).
+// readfirstlane states the uniformity to the compiler, which otherwise may not
+// prove it and wraps every load in a waterfall loop over lanes.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buffer_rsrc(const void* base,
+                                                                  uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* p = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, (int)__builtin_amdgcn_readfirstlane(bytes),
+                                           0x00020000);
+}
+
+// 16-byte buffer load with the nontemporal hint (cache policy bit NT).
+__device__ __forceinline__ u32x4_t buffer_load_nt_b128(__amdgpu_buffer_rsrc_t rsrc,
+                                                       uint32_t offset) {
+  return __builtin_bit_cast(u32x4_t,
+                            __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)offset, 0, 2));
+}
 
 }  // namespace kraken

@@ -18,7 +18,10 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "build", "libkraken_hip.so")
+# KRAKEN_HIP_LIBRARY selects another build of the same library (e.g. an
+# installed copy); the default is the in-tree build.
+LIB_PATH = os.environ.get("KRAKEN_HIP_LIBRARY") or os.path.join(_HERE, "build",
+                                                                "libkraken_hip.so")
 
 OK, INVALID_ARGUMENT, UNAVAILABLE, INTERNAL_ERROR = 0, 1, 2, 3
 STATUS_NAMES = {OK: "ok", INVALID_ARGUMENT: "invalid_argument", UNAVAILABLE: "unavailable",
