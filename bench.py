@@ -256,6 +256,20 @@ def cpu_baseline(kv_len, budget_s):
             "host_threads_available": os.cpu_count()}
 
 
+def decode_traffic():
+    """HBM bytes per C1 (L=4096) decode step from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE of both dispatches, scaled by the plain-copy
+    calibration), or None when it is absent."""
+    path = os.path.join(ROOT, "profiles", "decode_attention_c1_l4096_counters.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_step:"):
+                return int(line.split(":", 1)[1].strip())
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -264,6 +278,10 @@ def main():
     ap.add_argument("--kv-len", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline only, no details")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run torch copies of MIB MiB (20 launches), the known-size "
+                         "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -275,6 +293,15 @@ def main():
     import kraken_hip as kh
 
     torch.cuda.init()
+    if args.copy_calibration:
+        n = args.copy_calibration << 18  # floats
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        progress(f"copy calibration: 20 x {args.copy_calibration} MiB read + written")
+        return
     ctx = kh.Context()
     run = Runner(torch, ctx)
     gen = torch.Generator(device="cuda")
@@ -302,13 +329,9 @@ def main():
     run.close()
     ctx.close()
 
-    cpu = cpu_baseline(args.kv_len, args.cpu_seconds)
+    cpu = None if args.no_cpu else cpu_baseline(args.kv_len, args.cpu_seconds)
     progress("cpu baseline done")
-    traffic = None
-    prof = os.path.join(ROOT, "profiles", "decode_attention_c1_l4096_counters.json")
-    if os.path.exists(prof) and args.kv_len == 4096:
-        with open(prof) as f:
-            traffic = json.load(f).get("hbm_bytes_per_step")
+    traffic = decode_traffic() if args.kv_len == 4096 else None
     line = {
         "metric": METRIC,
         "value": head["GB_s"],
@@ -330,7 +353,8 @@ def main():
                    "bytes_per_step": decode_bytes(args.kv_len)},
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": head["GB_s"] / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernels": "attention_split + attention_combine (one decode step)"},
+                     "kernels": "attention_decode_kernel<256,4,f16> + attention_merge "
+                                "(the two dispatches of one decode step, timed together)"},
         "cpu_baseline": cpu,
         "details": details,
     }

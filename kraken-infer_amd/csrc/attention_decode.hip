@@ -700,9 +700,77 @@ hipError_t dispatch_kv(const DecodeParams& p, uint32_t d, uint32_t g, bool tuned
 
 }  // namespace
 
+// Few splits (chunked prefill): one thread per (token, head, 4 dims) with all of
+// its <= S partial loads in flight (clamped indices, masked), no LDS.
+template <int S>
+__global__ __launch_bounds__(256) void attention_merge_narrow(CombineArgs p) {
+  const uint32_t chunks = p.head_dim / 4;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)p.tokens * p.heads * chunks) {
+    return;
+  }
+  const uint32_t chunk = (uint32_t)(idx % chunks);
+  const size_t th = idx / chunks;  // token * heads + head
+  const uint32_t head = (uint32_t)(th % p.heads);
+  const uint32_t token = (uint32_t)(th / p.heads);
+  const uint32_t group = p.heads / p.kv_heads;
+  const uint32_t kvh = head / group;
+  const uint32_t g = head % group;
+  const size_t base = (size_t)token * p.kv_heads + kvh;
+  float mv[S], lv[S];
+  float4 ov[S];
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const uint32_t s = min((uint32_t)j, p.splits - 1u);
+    const size_t unit = (base * p.splits + s) * group + g;
+    mv[j] = p.partial_ml[unit * 2];
+    lv[j] = p.partial_ml[unit * 2 + 1];
+    ov[j] = *reinterpret_cast<const float4*>(p.partial_o + unit * p.head_dim + chunk * 4);
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    if ((uint32_t)j >= p.splits) {
+      mv[j] = -INFINITY;
+    }
+    mx = fmaxf(mx, mv[j]);
+  }
+  float den = 0.0f;
+  float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const float w = mv[j] == -INFINITY ? 0.0f : fast_exp2(mv[j] - mx);
+    den = fmaf(w, lv[j], den);
+    r.x = fmaf(w, ov[j].x, r.x);
+    r.y = fmaf(w, ov[j].y, r.y);
+    r.z = fmaf(w, ov[j].z, r.z);
+    r.w = fmaf(w, ov[j].w, r.w);
+  }
+  const float inv = den == 0.0f ? 0.0f : 1.0f / den;
+  const size_t out_index = th * p.head_dim + chunk * 4;
+  float out[4] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
+  if (p.gate != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      out[e] *= sigmoidf_acc(p.gate[out_index + e]);
+    }
+  }
+  *reinterpret_cast<float4*>(p.output + out_index) = make_float4(out[0], out[1], out[2], out[3]);
+}
+
 hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream) {
   if (c.splits > kMaxSplits || c.head_dim % kMergeDims != 0) {
     return hipErrorInvalidValue;
+  }
+  if (c.splits <= 16) {
+    const size_t threads = (size_t)c.tokens * c.heads * (c.head_dim / 4);
+    const dim3 grid((uint32_t)((threads + 255) / 256));
+    if (c.splits <= 4) {
+      attention_merge_narrow<4><<<grid, 256, 0, stream>>>(c);
+    } else {
+      attention_merge_narrow<16><<<grid, 256, 0, stream>>>(c);
+    }
+    return hipGetLastError();
   }
   const dim3 grid(c.tokens, c.heads, c.head_dim / kMergeDims);
   attention_merge<<<grid, 256, 0, stream>>>(c);
