@@ -353,6 +353,51 @@ class HipContext {
       value_heads, head_dim, eps, output.raw()));
   }
 
+  // Ragged multi-sequence decode (no counterparts in the reference, which
+  // serves one sequence per context): row b of each [sequences][...] operand
+  // belongs to sequence b; per-sequence tables are device buffers of uint64
+  // element offsets into caller pools and uint32 positions.  A HipBuffer with
+  // no data stands for an absent gate.
+  [[nodiscard]] Status attention_f32_ragged_f16_kv(
+    const HipBuffer& query, const HipBuffer& key_pool, const HipBuffer& value_pool,
+    const HipBuffer& gate, const HipBuffer& seq_kv_offsets, const HipBuffer& seq_positions,
+    std::size_t sequences, std::size_t max_position, std::size_t heads, std::size_t kv_heads,
+    std::size_t head_dim, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_attention_f32_ragged_f16_kv(
+      ctx_, query.raw(), key_pool.raw(), value_pool.raw(), gate.raw(), seq_kv_offsets.raw(),
+      seq_positions.raw(), sequences, max_position, heads, kv_heads, head_dim, output.raw()));
+  }
+  [[nodiscard]] Status append_kv_ragged_f16(const HipBuffer& key_rows,
+                                            const HipBuffer& value_rows, HipBuffer& key_pool,
+                                            HipBuffer& value_pool,
+                                            const HipBuffer& seq_kv_offsets,
+                                            const HipBuffer& seq_positions,
+                                            std::size_t sequences,
+                                            std::size_t row_size) const {
+    return Status::from_code(kraken_hip_append_kv_ragged_f16(
+      ctx_, key_rows.raw(), value_rows.raw(), key_pool.raw(), value_pool.raw(),
+      seq_kv_offsets.raw(), seq_positions.raw(), sequences, row_size));
+  }
+  [[nodiscard]] Status gated_delta_net_f32_ragged_decode(
+    const HipBuffer& query, const HipBuffer& key, const HipBuffer& value,
+    const HipBuffer& gate, const HipBuffer& beta, HipBuffer& state_pool,
+    const HipBuffer& seq_state_offsets, std::size_t sequences, std::size_t key_heads,
+    std::size_t value_heads, std::size_t head_dim, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_gated_delta_net_f32_ragged_decode(
+      ctx_, query.raw(), key.raw(), value.raw(), gate.raw(), beta.raw(), state_pool.raw(),
+      seq_state_offsets.raw(), sequences, key_heads, value_heads, head_dim, output.raw()));
+  }
+  [[nodiscard]] Status qwen35_conv_split_l2_ragged_decode_f32(
+    const HipBuffer& qkv, HipBuffer& conv_pool, const HipBuffer& seq_conv_offsets,
+    const HipBuffer& conv_kernel_weights, std::size_t conv_kernel, std::size_t sequences,
+    std::size_t key_heads, std::size_t value_heads, std::size_t head_dim, float eps,
+    HipBuffer& query, HipBuffer& key, HipBuffer& value) const {
+    return Status::from_code(kraken_hip_qwen35_conv_split_l2_ragged_decode_f32(
+      ctx_, qkv.raw(), conv_pool.raw(), seq_conv_offsets.raw(), conv_kernel_weights.raw(),
+      conv_kernel, sequences, key_heads, value_heads, head_dim, eps, query.raw(), key.raw(),
+      value.raw()));
+  }
+
   // Norms and elementwise ops (mps_backend.hpp:252-376).
   [[nodiscard]] Status split_qkv_l2_norm_f32_qwen35(
     const HipBuffer& source, HipBuffer& query, HipBuffer& key, HipBuffer& value,

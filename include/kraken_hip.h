@@ -310,6 +310,59 @@ KRAKEN_API int kraken_hip_mul_f32_row_in_place(kraken_hip_context* context,
                                                kraken_buffer target, kraken_buffer row,
                                                size_t rows, size_t row_size);
 
+/* ---- Ragged multi-sequence decode ------------------------------------------
+ * No counterpart in the reference, which serves one sequence per context
+ * (README.md:540); for callers that batch the decode step of many sequences
+ * (the layer drivers run_qwen35_full_attention_layer_chunk /
+ * run_qwen35_linear_layer_chunk, qwen35_runtime.cpp:2634-3423, applied to one
+ * token of each sequence).  Sequence b contributes row b of every [sequences][...]
+ * operand.  Per-sequence tables are device buffers: seq_*_offsets are uint64
+ * element offsets into caller-owned pools, seq_positions are uint32 positions
+ * (the query at position p attends keys 0..p; the new key/value row is row p).
+ * Kernels bound every access to its pool: an offset outside it reads zeros
+ * (KV) or skips that sequence (states, appends). */
+
+/* Decode attention over per-sequence F16 K/V rows [position][kv_heads][head_dim]
+ * at seq_kv_offsets[b] of key_pool / value_pool (same size); optional fused
+ * output gate (gate.data == NULL: none); max_position bounds every position.
+ * Semantics per sequence: attention_f32_batched_f16_kv with tokens = 1
+ * (mps_backend.hpp:415-420; mps_backend.mm:2943-3008) and, with a gate,
+ * out *= sigmoid(gate) (qwen35_runtime.cpp:3347-3355).  head_dim 64/128/256,
+ * 1/2/4/8 query heads per KV head, 16-byte aligned buffers. */
+KRAKEN_API int kraken_hip_attention_f32_ragged_f16_kv(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key_pool,
+  kraken_buffer value_pool, kraken_buffer gate, kraken_buffer seq_kv_offsets,
+  kraken_buffer seq_positions, size_t sequences, size_t max_position, size_t heads,
+  size_t kv_heads, size_t head_dim, kraken_buffer output);
+
+/* KV append: f32 rows [sequences][row_size] -> f16 row seq_positions[b] of each
+ * sequence's K and V (copy_f32_rows_to_f16, mps_backend.hpp:372-376, at the
+ * per-sequence destination). */
+KRAKEN_API int kraken_hip_append_kv_ragged_f16(kraken_hip_context* context,
+                                               kraken_buffer key_rows, kraken_buffer value_rows,
+                                               kraken_buffer key_pool, kraken_buffer value_pool,
+                                               kraken_buffer seq_kv_offsets,
+                                               kraken_buffer seq_positions, size_t sequences,
+                                               size_t row_size);
+
+/* One recurrent step per sequence: gated_delta_net_f32_batched_in_place_at with
+ * tokens = 1 (mps_backend.hpp:296-300) on the state [value_heads][D][D] at
+ * seq_state_offsets[b] of state_pool. */
+KRAKEN_API int kraken_hip_gated_delta_net_f32_ragged_decode(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key, kraken_buffer value,
+  kraken_buffer gate, kraken_buffer beta, kraken_buffer state_pool,
+  kraken_buffer seq_state_offsets, size_t sequences, size_t key_heads, size_t value_heads,
+  size_t head_dim, kraken_buffer output);
+
+/* Fused linear-attention prologue for one token per sequence
+ * (kraken_hip_qwen35_conv_split_l2_f32 semantics) with the conv state
+ * [channels][conv_kernel - 1] of sequence b at seq_conv_offsets[b] of conv_pool. */
+KRAKEN_API int kraken_hip_qwen35_conv_split_l2_ragged_decode_f32(
+  kraken_hip_context* context, kraken_buffer qkv, kraken_buffer conv_pool,
+  kraken_buffer seq_conv_offsets, kraken_buffer conv_kernel_weights, size_t conv_kernel,
+  size_t sequences, size_t key_heads, size_t value_heads, size_t head_dim, float eps,
+  kraken_buffer query, kraken_buffer key, kraken_buffer value);
+
 #ifdef __cplusplus
 }
 #endif

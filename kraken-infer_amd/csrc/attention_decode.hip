@@ -58,7 +58,21 @@ struct DecodeParams {
   uint32_t layer, start_position, tokens, capacity_tokens, heads, kv_heads;
   uint32_t keys_per_split, splits;
   float scale_log2;
+  // Ragged multi-sequence mode (see AttentionArgs): per-token K/V element
+  // offsets and positions, and the pools' element count.
+  const uint64_t* seq_kv_offsets;
+  const uint32_t* seq_positions;
+  uint64_t pool_elems;
 };
+
+// Keys of token t (positions table in ragged mode); at least 1 (a position of
+// 2^32 - 1 saturates instead of wrapping to 0).
+__device__ __forceinline__ uint32_t token_keys(const uint32_t* positions, uint32_t start,
+                                               uint32_t token) {
+  const uint64_t keys = positions != nullptr ? (uint64_t)positions[token] + 1u
+                                             : (uint64_t)start + token + 1u;
+  return (uint32_t)min(keys, (uint64_t)0xffffffffu);
+}
 
 template <typename KV>
 struct KvTraits;
@@ -199,16 +213,21 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams
   const uint32_t split = blockIdx.x;
   const uint32_t kvh = blockIdx.y;
   const uint32_t token = blockIdx.z;
-  const uint32_t n_keys = p.start_position + token + 1u;
+  const bool ragged = p.seq_positions != nullptr;
+  const uint32_t n_keys = token_keys(p.seq_positions, p.start_position, token);
   const uint32_t key_begin = split * p.keys_per_split;
+  if (key_begin >= n_keys) {
+    return;  // empty split (whole workgroup): the merge reads only this token's splits
+  }
   const uint32_t key_end = min(n_keys, key_begin + p.keys_per_split);
-  const uint32_t count = key_end > key_begin ? key_end - key_begin : 0u;
+  const uint32_t count = key_end - key_begin;
 
   const size_t row_stride = (size_t)p.kv_heads * D;
-  const KV* kbase = static_cast<const KV*>(p.key_cache) +
-                    (size_t)p.layer * p.capacity_tokens * row_stride + (size_t)kvh * D;
-  const KV* vbase = static_cast<const KV*>(p.value_cache) +
-                    (size_t)p.layer * p.capacity_tokens * row_stride + (size_t)kvh * D;
+  const uint64_t seq_elem = ragged ? p.seq_kv_offsets[token]
+                                   : (uint64_t)p.layer * p.capacity_tokens * row_stride;
+  const uint64_t first_elem = seq_elem + (uint64_t)kvh * D;
+  const KV* kbase = static_cast<const KV*>(p.key_cache) + first_elem;
+  const KV* vbase = static_cast<const KV*>(p.value_cache) + first_elem;
 
   // The query heads kvh*G .. kvh*G+G-1 (G*D contiguous floats) are loaded
   // before K/V: vector loads retire in issue order, so using the query waits
@@ -234,10 +253,21 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams
   // ending at its last: lanes and rounds past the end read zeros from the range
   // check with no memory access (and are masked out of the softmax).
   const uint32_t row_bytes = (uint32_t)(row_stride * sizeof(KV));
+  uint32_t span_bytes = count * row_bytes;
+  if (ragged) {
+    // Device-side offsets are not checked on the host: the range also ends at
+    // the pool's end, so a bad offset reads zeros instead of faulting.
+    // An offset that is not a whole 16-byte chunk (misaligned rows) reads zeros too.
+    const uint64_t split_elem = first_elem + (uint64_t)key_begin * row_stride;
+    const uint64_t avail =
+      split_elem < p.pool_elems ? (p.pool_elems - split_elem) * sizeof(KV) : 0u;
+    span_bytes = (seq_elem * sizeof(KV)) % 16u != 0 ? 0u
+                                                   : (uint32_t)min((uint64_t)span_bytes, avail);
+  }
   const __amdgpu_buffer_rsrc_t krsrc =
-    make_buffer_rsrc(kbase + (size_t)key_begin * row_stride, count * row_bytes);
+    make_buffer_rsrc(kbase + (size_t)key_begin * row_stride, span_bytes);
   const __amdgpu_buffer_rsrc_t vrsrc =
-    make_buffer_rsrc(vbase + (size_t)key_begin * row_stride, count * row_bytes);
+    make_buffer_rsrc(vbase + (size_t)key_begin * row_stride, span_bytes);
   const uint32_t wave_first = (uint32_t)(wave * KW);  // wave's first key in a round
   const uint32_t lane_key = wave_first + (uint32_t)kslot;
   const uint32_t lane_off = lane_key * row_bytes + 16u * c;
@@ -432,6 +462,16 @@ static_assert(kMergeChunks == 4, "merge lane reductions run over lane bits 2..5"
 constexpr int kMergeSubsets = 256 / kMergeChunks;
 constexpr int kMergePerThread = kMaxSplits / kMergeSubsets;
 
+// Number of splits holding partials for `token` (>= 1: every token has a key).
+__device__ __forceinline__ uint32_t token_splits(const CombineArgs& p, uint32_t token) {
+  if (p.keys_per_split == 0) {
+    return p.splits;
+  }
+  const uint64_t keys = token_keys(p.positions, p.start_position, token);
+  const uint64_t needed = (keys + p.keys_per_split - 1u) / p.keys_per_split;
+  return (uint32_t)max((uint64_t)1, min((uint64_t)p.splits, needed));
+}
+
 // Reductions over lane bits 2..5 (the split subsets of one chunk): rotations by
 // 4 and 8 within each 16-lane row, then the xor-16 and xor-32 exchanges.
 __device__ __forceinline__ float merge_lanes_max(float x) {
@@ -462,6 +502,7 @@ __global__ __launch_bounds__(256) void attention_merge(CombineArgs p) {
   const int chunk = tid % kMergeChunks;
   const int subset = tid / kMergeChunks;
   const size_t base = (size_t)token * p.kv_heads + kvh;
+  const uint32_t nsp = token_splits(p, token);
 
   float mv[kMergePerThread], lv[kMergePerThread];
   float4 ov[kMergePerThread];
@@ -469,7 +510,7 @@ __global__ __launch_bounds__(256) void attention_merge(CombineArgs p) {
   // flight at once.
 #pragma unroll
   for (int j = 0; j < kMergePerThread; ++j) {
-    const uint32_t s = min(subset + j * kMergeSubsets, p.splits - 1u);
+    const uint32_t s = min(subset + j * kMergeSubsets, nsp - 1u);
     const size_t unit = (base * p.splits + s) * group + g;
     mv[j] = p.partial_ml[unit * 2];
     lv[j] = p.partial_ml[unit * 2 + 1];
@@ -478,7 +519,7 @@ __global__ __launch_bounds__(256) void attention_merge(CombineArgs p) {
   float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < kMergePerThread; ++j) {
-    if (subset + j * kMergeSubsets >= p.splits) {
+    if (subset + j * kMergeSubsets >= nsp) {
       mv[j] = -INFINITY;
     }
     mx = fmaxf(mx, mv[j]);
@@ -602,15 +643,22 @@ struct SplitPlan {
 
 // Splits per (token, kv_head) so that the grid puts about one workgroup on each
 // CU; a split may be any number of keys (a partial last round is masked).
+// Ragged decode: a fixed split size, so sequences of any length divide into
+// equal pieces of work (the grid covers the longest; empty splits exit).
+constexpr uint64_t kRaggedKeysPerSplit = 1024;
+
 SplitPlan plan_splits(const AttentionArgs& a, int cu_count) {
-  const uint64_t max_keys = (uint64_t)a.start_position + a.tokens;  // last query's keys
+  const bool ragged = a.seq_positions != nullptr;
+  // Keys of the longest query.
+  const uint64_t max_keys =
+    ragged ? (uint64_t)a.max_position + 1 : (uint64_t)a.start_position + a.tokens;
   const uint64_t units = (uint64_t)a.tokens * a.kv_heads;
   const uint64_t slots = (uint64_t)(cu_count > 0 ? cu_count : 256);
   uint64_t splits_target = slots / units;
   if (splits_target < 1) {
     splits_target = 1;
   }
-  uint64_t kps = (max_keys + splits_target - 1) / splits_target;
+  uint64_t kps = ragged ? kRaggedKeysPerSplit : (max_keys + splits_target - 1) / splits_target;
   if (const char* env = std::getenv("KRAKEN_DECODE_KEYS_PER_SPLIT")) {
     const long v = std::strtol(env, nullptr, 10);
     if (v > 0) {
@@ -666,6 +714,9 @@ hipError_t launch_tuned(const DecodeParams& p, hipStream_t stream) {
   c.kv_heads = p.kv_heads;
   c.splits = p.splits;
   c.head_dim = D;
+  c.positions = p.seq_positions;
+  c.start_position = p.start_position;
+  c.keys_per_split = p.keys_per_split;
   return launch_attention_combine(c, stream);
 }
 
@@ -717,11 +768,12 @@ __global__ __launch_bounds__(256) void attention_merge_narrow(CombineArgs p) {
   const uint32_t kvh = head / group;
   const uint32_t g = head % group;
   const size_t base = (size_t)token * p.kv_heads + kvh;
+  const uint32_t nsp = token_splits(p, token);
   float mv[S], lv[S];
   float4 ov[S];
 #pragma unroll
   for (int j = 0; j < S; ++j) {
-    const uint32_t s = min((uint32_t)j, p.splits - 1u);
+    const uint32_t s = min((uint32_t)j, nsp - 1u);
     const size_t unit = (base * p.splits + s) * group + g;
     mv[j] = p.partial_ml[unit * 2];
     lv[j] = p.partial_ml[unit * 2 + 1];
@@ -730,7 +782,7 @@ __global__ __launch_bounds__(256) void attention_merge_narrow(CombineArgs p) {
   float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < S; ++j) {
-    if ((uint32_t)j >= p.splits) {
+    if ((uint32_t)j >= nsp) {
       mv[j] = -INFINITY;
     }
     mx = fmaxf(mx, mv[j]);
@@ -813,8 +865,14 @@ hipError_t launch_attention_decode(const AttentionArgs& a, int cu_count, void* w
   p.heads = a.heads;
   p.kv_heads = a.kv_heads;
   p.scale_log2 = (1.0f / sqrtf((float)a.head_dim)) * kLog2e;
+  p.seq_kv_offsets = a.seq_kv_offsets;
+  p.seq_positions = a.seq_positions;
+  p.pool_elems = a.pool_elems;
   const SplitPlan plan = plan_splits(a, cu_count);
   const bool tuned = use_tuned(a, plan);
+  if (a.seq_positions != nullptr && !tuned) {
+    return hipErrorInvalidValue;  // ragged decode runs on the tuned kernel only
+  }
   p.splits = 1;
   if (tuned) {
     p.keys_per_split = plan.keys_per_split;

@@ -373,6 +373,9 @@ hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* wo
   c.kv_heads = a.kv_heads;
   c.splits = plan.splits;
   c.head_dim = kD;
+  c.positions = nullptr;
+  c.start_position = a.start_position;
+  c.keys_per_split = plan.keys_per_split;
   return launch_attention_combine(c, stream);
 }
 

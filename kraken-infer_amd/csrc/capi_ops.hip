@@ -792,3 +792,276 @@ KRAKEN_API int kraken_hip_mul_f32_row_in_place(kraken_hip_context* ctx, kraken_b
 }
 
 }  // extern "C"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Ragged multi-sequence decode (no counterpart in the reference, which serves
+// one sequence per context; README.md:540).  Each sequence contributes one
+// token.  Per-sequence tables live in device memory (u64 element offsets into
+// caller-owned pools, u32 positions) so a captured step can be replayed while
+// the caller advances them on the device.  Offsets are not readable on the
+// host: kernels bound every access to the pool instead (an offset outside it
+// skips that sequence's state, or reads zeros from the KV pool).
+
+// Elements of a pool buffer of `elem` bytes per element; invalid when the byte
+// size is not a whole number of elements.
+int pool_elems_of(const kraken_buffer& pool, size_t elem, size_t at_least, const std::string& w,
+                  const char* name, uint64_t& elems) {
+  KRAKEN_TRY(validate_buffer(pool, at_least, elem, name));
+  if (pool.byte_size % elem != 0) {
+    return invalid(w + " " + name + " size is not a whole number of elements");
+  }
+  elems = pool.byte_size / elem;
+  return KRAKEN_OK;
+}
+
+int ragged_attention_entry(kraken_hip_context* ctx, const kraken_buffer& query,
+                           const kraken_buffer& key_pool, const kraken_buffer& value_pool,
+                           const kraken_buffer* gate, const kraken_buffer& seq_kv_offsets,
+                           const kraken_buffer& seq_positions, size_t sequences,
+                           size_t max_position, size_t heads, size_t kv_heads, size_t head_dim,
+                           const kraken_buffer& output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string w = "HIP ragged attention";
+  if (sequences == 0 || heads == 0 || kv_heads == 0 || head_dim == 0) {
+    return invalid(w + " dimensions must be positive");
+  }
+  if (heads % kv_heads != 0) {
+    return invalid(w + " heads must be divisible by kv_heads");
+  }
+  const size_t group = heads / kv_heads;
+  if ((head_dim != 64 && head_dim != 128 && head_dim != 256) ||
+      (group != 1 && group != 2 && group != 4 && group != 8)) {
+    return invalid(w + " supports head_dim 64/128/256 and 1/2/4/8 query heads per kv head");
+  }
+  if (((uintptr_t)query.data | (uintptr_t)key_pool.data | (uintptr_t)value_pool.data |
+       (uintptr_t)output.data) & 15u) {
+    return invalid(w + " buffers must be 16-byte aligned");
+  }
+  size_t attn_dim = 0, kv_dim = 0, query_values = 0, one_sequence = 0;
+  if (max_position >= 0xffffffffu || !checked_mul(heads, head_dim, attn_dim) ||
+      !checked_mul(kv_heads, head_dim, kv_dim) ||
+      !checked_mul(sequences, attn_dim, query_values) ||
+      !checked_mul(max_position + 1u, kv_dim, one_sequence)) {
+    return invalid(w + " value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(query, query_values, "ragged attention query"));
+  uint64_t pool_elems = 0, value_elems = 0;
+  KRAKEN_TRY(pool_elems_of(key_pool, sizeof(uint16_t), kv_dim, w, "ragged attention key pool",
+                           pool_elems));
+  KRAKEN_TRY(pool_elems_of(value_pool, sizeof(uint16_t), kv_dim, w,
+                           "ragged attention value pool", value_elems));
+  if (value_elems != pool_elems) {
+    return invalid(w + " key and value pools differ in size");
+  }
+  if (gate != nullptr) {
+    KRAKEN_TRY(validate_f32(*gate, query_values, "ragged attention gate"));
+  }
+  KRAKEN_TRY(validate_buffer(seq_kv_offsets, sequences, sizeof(uint64_t),
+                             "ragged attention kv offsets"));
+  KRAKEN_TRY(validate_buffer(seq_positions, sequences, sizeof(uint32_t),
+                             "ragged attention positions"));
+  KRAKEN_TRY(validate_f32(output, query_values, "ragged attention output"));
+  KRAKEN_TRY(check_u32(sequences, "ragged attention sequences"));
+  KRAKEN_TRY(check_u32(heads, "ragged attention heads"));
+  KRAKEN_TRY(check_u32(kv_heads, "ragged attention kv_heads"));
+
+  AttentionArgs a{};
+  a.query = static_cast<const float*>(query.data);
+  a.key_cache = key_pool.data;
+  a.value_cache = value_pool.data;
+  a.gate = gate != nullptr ? static_cast<const float*>(gate->data) : nullptr;
+  a.output = static_cast<float*>(output.data);
+  a.tokens = (uint32_t)sequences;
+  a.heads = (uint32_t)heads;
+  a.kv_heads = (uint32_t)kv_heads;
+  a.head_dim = (uint32_t)head_dim;
+  a.kv_f16 = true;
+  a.seq_kv_offsets = static_cast<const uint64_t*>(seq_kv_offsets.data);
+  a.seq_positions = static_cast<const uint32_t*>(seq_positions.data);
+  a.pool_elems = pool_elems;
+  a.max_position = (uint32_t)max_position;
+  KRAKEN_TRY(begin_launch(ctx));
+  KRAKEN_TRY(ensure_workspace(ctx, attention_decode_workspace_bytes(a, ctx->cu_count)));
+  const hipError_t e = launch_attention_decode(a, ctx->cu_count, ctx->workspace,
+                                               ctx->workspace_bytes, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (w + " command failed: ").c_str());
+}
+
+}  // namespace
+
+extern "C" {
+
+KRAKEN_API int kraken_hip_attention_f32_ragged_f16_kv(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key_pool, kraken_buffer value_pool,
+  kraken_buffer gate, kraken_buffer seq_kv_offsets, kraken_buffer seq_positions,
+  size_t sequences, size_t max_position, size_t heads, size_t kv_heads, size_t head_dim,
+  kraken_buffer output) {
+  return ragged_attention_entry(ctx, query, key_pool, value_pool,
+                                gate.data != nullptr ? &gate : nullptr, seq_kv_offsets,
+                                seq_positions, sequences, max_position, heads, kv_heads,
+                                head_dim, output);
+}
+
+KRAKEN_API int kraken_hip_append_kv_ragged_f16(kraken_hip_context* ctx, kraken_buffer key_rows,
+                                               kraken_buffer value_rows, kraken_buffer key_pool,
+                                               kraken_buffer value_pool,
+                                               kraken_buffer seq_kv_offsets,
+                                               kraken_buffer seq_positions, size_t sequences,
+                                               size_t row_size) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string w = "HIP ragged KV append";
+  if (sequences == 0 || row_size == 0) {
+    return invalid(w + " dimensions must be positive");
+  }
+  size_t values = 0;
+  if (!checked_mul(sequences, row_size, values)) {
+    return invalid(w + " value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(key_rows, values, "ragged KV append key rows"));
+  KRAKEN_TRY(validate_f32(value_rows, values, "ragged KV append value rows"));
+  uint64_t pool_elems = 0, value_elems = 0;
+  KRAKEN_TRY(pool_elems_of(key_pool, sizeof(uint16_t), row_size, w, "ragged KV append key pool",
+                           pool_elems));
+  KRAKEN_TRY(pool_elems_of(value_pool, sizeof(uint16_t), row_size, w,
+                           "ragged KV append value pool", value_elems));
+  if (value_elems != pool_elems) {
+    return invalid(w + " key and value pools differ in size");
+  }
+  KRAKEN_TRY(validate_buffer(seq_kv_offsets, sequences, sizeof(uint64_t),
+                             "ragged KV append kv offsets"));
+  KRAKEN_TRY(validate_buffer(seq_positions, sequences, sizeof(uint32_t),
+                             "ragged KV append positions"));
+  KRAKEN_TRY(check_u32(sequences, "ragged KV append sequences"));
+  KRAKEN_TRY(check_u32(row_size, "ragged KV append row size"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_append_kv_ragged(
+    static_cast<const float*>(key_rows.data), static_cast<const float*>(value_rows.data),
+    key_pool.data, value_pool.data, static_cast<const uint64_t*>(seq_kv_offsets.data),
+    static_cast<const uint32_t*>(seq_positions.data), pool_elems, (uint32_t)sequences,
+    (uint32_t)row_size, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (w + " command failed: ").c_str());
+}
+
+KRAKEN_API int kraken_hip_gated_delta_net_f32_ragged_decode(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key, kraken_buffer value,
+  kraken_buffer gate, kraken_buffer beta, kraken_buffer state_pool,
+  kraken_buffer seq_state_offsets, size_t sequences, size_t key_heads, size_t value_heads,
+  size_t head_dim, kraken_buffer output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string w = "HIP ragged gated delta net";
+  if (sequences == 0 || key_heads == 0 || value_heads == 0 || head_dim == 0) {
+    return invalid(w + " dimensions must be positive");
+  }
+  if (value_heads % key_heads != 0) {
+    return invalid(w + " value heads must repeat key heads");
+  }
+  if (head_dim > 256u) {
+    return invalid(w + " head_dim exceeds 256");
+  }
+  size_t kvpt = 0, vvpt = 0, key_values = 0, value_values = 0, gate_values = 0,
+         state_values = 0;
+  if (!checked_mul(key_heads, head_dim, kvpt) || !checked_mul(value_heads, head_dim, vvpt) ||
+      !checked_mul(sequences, kvpt, key_values) || !checked_mul(sequences, vvpt, value_values) ||
+      !checked_mul(sequences, value_heads, gate_values) ||
+      !checked_mul(vvpt, head_dim, state_values)) {
+    return invalid(w + " value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(query, key_values, "ragged gated delta net query"));
+  KRAKEN_TRY(validate_f32(key, key_values, "ragged gated delta net key"));
+  KRAKEN_TRY(validate_f32(value, value_values, "ragged gated delta net value"));
+  KRAKEN_TRY(validate_f32(gate, gate_values, "ragged gated delta net gate"));
+  KRAKEN_TRY(validate_f32(beta, gate_values, "ragged gated delta net beta"));
+  uint64_t pool_elems = 0;
+  KRAKEN_TRY(pool_elems_of(state_pool, sizeof(float), state_values, w,
+                           "ragged gated delta net state pool", pool_elems));
+  KRAKEN_TRY(validate_buffer(seq_state_offsets, sequences, sizeof(uint64_t),
+                             "ragged gated delta net state offsets"));
+  KRAKEN_TRY(validate_f32(output, value_values, "ragged gated delta net output"));
+  KRAKEN_TRY(check_u32(sequences, "ragged gated delta net sequences"));
+  KRAKEN_TRY(check_u32(key_heads, "ragged gated delta net key_heads"));
+  KRAKEN_TRY(check_u32(value_heads, "ragged gated delta net value_heads"));
+  KRAKEN_TRY(begin_launch(ctx));
+  GdnArgs a{};
+  a.query = static_cast<const float*>(query.data);
+  a.key = static_cast<const float*>(key.data);
+  a.value = static_cast<const float*>(value.data);
+  a.gate = static_cast<const float*>(gate.data);
+  a.beta = static_cast<const float*>(beta.data);
+  a.state = static_cast<float*>(state_pool.data);
+  a.output = static_cast<float*>(output.data);
+  a.tokens = (uint32_t)sequences;
+  a.key_heads = (uint32_t)key_heads;
+  a.value_heads = (uint32_t)value_heads;
+  a.head_dim = (uint32_t)head_dim;
+  a.seq_state_offsets = static_cast<const uint64_t*>(seq_state_offsets.data);
+  a.pool_elems = pool_elems;
+  const hipError_t e = launch_gated_delta_net(a, ctx->cu_count, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (w + " command failed: ").c_str());
+}
+
+KRAKEN_API int kraken_hip_qwen35_conv_split_l2_ragged_decode_f32(
+  kraken_hip_context* ctx, kraken_buffer qkv, kraken_buffer conv_pool,
+  kraken_buffer seq_conv_offsets, kraken_buffer conv_kernel_weights, size_t conv_kernel,
+  size_t sequences, size_t key_heads, size_t value_heads, size_t head_dim, float eps,
+  kraken_buffer query, kraken_buffer key, kraken_buffer value) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string w = "HIP ragged Qwen3.5 conv split";
+  if (sequences == 0 || key_heads == 0 || value_heads == 0 || head_dim == 0) {
+    return invalid(w + " dimensions must be positive");
+  }
+  if (conv_kernel < 2 || conv_kernel > 8) {
+    return invalid(w + " conv_kernel must be in [2, 8]");
+  }
+  if (head_dim > 256u) {
+    return invalid(w + " head_dim exceeds 256");
+  }
+  size_t key_dim = 0, value_dim = 0, channels = 0, qkv_values = 0, key_values = 0,
+         value_values = 0, state_values = 0, kernel_values = 0;
+  if (!checked_mul(key_heads, head_dim, key_dim) ||
+      !checked_mul(value_heads, head_dim, value_dim) ||
+      !checked_add(2u * key_dim, value_dim, channels) ||
+      !checked_mul(sequences, channels, qkv_values) ||
+      !checked_mul(sequences, key_dim, key_values) ||
+      !checked_mul(sequences, value_dim, value_values) ||
+      !checked_mul(conv_kernel - 1u, channels, state_values) ||
+      !checked_mul(conv_kernel, channels, kernel_values)) {
+    return invalid(w + " value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(qkv, qkv_values, "ragged Qwen3.5 conv split qkv"));
+  uint64_t pool_elems = 0;
+  KRAKEN_TRY(pool_elems_of(conv_pool, sizeof(float), state_values, w,
+                           "ragged Qwen3.5 conv split conv pool", pool_elems));
+  KRAKEN_TRY(validate_buffer(seq_conv_offsets, sequences, sizeof(uint64_t),
+                             "ragged Qwen3.5 conv split conv offsets"));
+  KRAKEN_TRY(validate_f32(conv_kernel_weights, kernel_values, "ragged Qwen3.5 conv split kernel"));
+  KRAKEN_TRY(validate_f32(query, key_values, "ragged Qwen3.5 conv split query"));
+  KRAKEN_TRY(validate_f32(key, key_values, "ragged Qwen3.5 conv split key"));
+  KRAKEN_TRY(validate_f32(value, value_values, "ragged Qwen3.5 conv split value"));
+  KRAKEN_TRY(check_u32(sequences, "ragged Qwen3.5 conv split sequences"));
+  KRAKEN_TRY(check_u32(channels, "ragged Qwen3.5 conv split channels"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_conv_split_l2_ragged(
+    static_cast<const float*>(qkv.data), static_cast<float*>(conv_pool.data),
+    static_cast<const uint64_t*>(seq_conv_offsets.data), pool_elems,
+    static_cast<const float*>(conv_kernel_weights.data), (uint32_t)conv_kernel,
+    (uint32_t)sequences, (uint32_t)key_heads, (uint32_t)value_heads, (uint32_t)head_dim, eps,
+    static_cast<float*>(query.data), static_cast<float*>(key.data),
+    static_cast<float*>(value.data), ctx->stream);
+  if (e != hipSuccess) {
+    return internal(w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (w + " command failed: ").c_str());
+}
+
+}  // extern "C"

@@ -113,6 +113,15 @@ struct AttentionArgs {
   float* output;
   uint32_t layer, start_position, tokens, capacity_tokens, heads, kv_heads, head_dim;
   bool kv_f16;
+  // Ragged multi-sequence decode (set together, else null/0): token t is the
+  // one query token of sequence t, at position seq_positions[t] (it attends
+  // keys 0..position), whose K/V rows [position][kv_heads][head_dim] start at
+  // element seq_kv_offsets[t] of key_cache/value_cache (pools of pool_elems
+  // elements each).  max_position bounds every position (sizes the grid).
+  const uint64_t* seq_kv_offsets = nullptr;
+  const uint32_t* seq_positions = nullptr;
+  uint64_t pool_elems = 0;
+  uint32_t max_position = 0;
 };
 
 // Bytes of workspace the split-K decode path needs for these arguments.
@@ -128,6 +137,12 @@ struct CombineArgs {
   const float* gate;
   float* output;
   uint32_t tokens, heads, kv_heads, splits, head_dim;
+  // Split s covers keys [s*keys_per_split, (s+1)*keys_per_split); token t has
+  // positions[t] + 1 keys (ragged) or start_position + t + 1, so only its first
+  // ceil(keys / keys_per_split) splits hold partials.  keys_per_split == 0:
+  // all `splits` partials are valid for every token.
+  const uint32_t* positions;
+  uint32_t start_position, keys_per_split;
 };
 hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream);
 // True when the flash MFMA prefill kernel supports these arguments.
@@ -151,6 +166,11 @@ struct GdnArgs {
   const float* z;            // epilogue: out = RMSNorm(y) * norm_weight * silu(z)
   const float* norm_weight;
   float eps;
+  // Ragged decode: `tokens` sequences with one token each; sequence b's state
+  // [value_heads][D][D] at element seq_state_offsets[b] of `state` (a pool of
+  // pool_elems elements).  Null for the single-sequence form.
+  const uint64_t* seq_state_offsets = nullptr;
+  uint64_t pool_elems = 0;
 };
 hipError_t launch_gated_delta_net(const GdnArgs& a, int cu_count, hipStream_t stream);
 
@@ -167,6 +187,21 @@ hipError_t launch_conv_split_l2(const float* qkv, float* conv_state, const float
                                 uint32_t conv_kernel, uint32_t tokens, uint32_t key_heads,
                                 uint32_t value_heads, uint32_t head_dim, float eps,
                                 float* query, float* key, float* value, hipStream_t stream);
+// Ragged decode form: one token per sequence, per-sequence conv state offsets.
+hipError_t launch_conv_split_l2_ragged(const float* qkv, float* conv_pool,
+                                       const uint64_t* seq_conv_offsets, uint64_t pool_elems,
+                                       const float* weights, uint32_t conv_kernel,
+                                       uint32_t sequences, uint32_t key_heads,
+                                       uint32_t value_heads, uint32_t head_dim, float eps,
+                                       float* query, float* key, float* value,
+                                       hipStream_t stream);
+// Ragged KV append: rows[b] (f32, row_size) -> f16 at element
+// seq_offsets[b] + seq_positions[b] * row_size of the pool, for K and V.
+hipError_t launch_append_kv_ragged(const float* key_rows, const float* value_rows,
+                                   void* key_pool, void* value_pool,
+                                   const uint64_t* seq_offsets, const uint32_t* seq_positions,
+                                   uint64_t pool_elems, uint32_t sequences, uint32_t row_size,
+                                   hipStream_t stream);
 
 hipError_t launch_split_qkv_l2(const float* source, float* q, float* k, float* v,
                                uint32_t tokens, uint32_t key_heads, uint32_t value_heads,

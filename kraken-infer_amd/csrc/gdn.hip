@@ -36,6 +36,10 @@ struct GdnParams {
   float* output;
   uint32_t tokens, key_heads, value_heads, head_dim;
   float scale;
+  // Ragged decode (blockIdx.z = sequence, one token each): state of sequence b
+  // at element seq_state_offsets[b] of a pool of pool_elems elements.
+  const uint64_t* seq_state_offsets;
+  uint64_t pool_elems;
 };
 
 __device__ __forceinline__ float softplus_ref(float x) {
@@ -53,8 +57,23 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnParams p) {
   const bool row_ok = row < D;
   const uint32_t kh = h % p.key_heads;
 
+  // Token rows [t_first, t_first + n_tokens) and the state they update.
+  float* state = p.state;
+  uint32_t t_first = 0;
+  uint32_t n_tokens = p.tokens;
+  if (p.seq_state_offsets != nullptr) {
+    const uint32_t seq = blockIdx.z;
+    const uint64_t off = p.seq_state_offsets[seq];
+    if (off > p.pool_elems || p.pool_elems - off < (uint64_t)p.value_heads * D * D) {
+      return;  // offset outside the pool: this sequence is skipped, nothing touched
+    }
+    state += off;
+    t_first = seq;
+    n_tokens = 1;
+  }
+
   float s[CPL];
-  float* srow = p.state + ((size_t)h * D + (row_ok ? row : 0)) * D;
+  float* srow = state + ((size_t)h * D + (row_ok ? row : 0)) * D;
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     s[i] = (row_ok && col0 + i < D) ? srow[col0 + i] : 0.0f;
@@ -76,10 +95,11 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnParams p) {
   };
 
   float kc[CPL], qc[CPL], vc, gc, bc;
-  load_token(0, kc, qc, vc, gc, bc);
-  for (uint32_t t = 0; t < p.tokens; ++t) {
+  const uint32_t t_end = t_first + n_tokens;
+  load_token(t_first, kc, qc, vc, gc, bc);
+  for (uint32_t t = t_first; t < t_end; ++t) {
     float kn[CPL], qn[CPL], vn = 0.0f, gn = 0.0f, bn = 0.0f;
-    if (t + 1 < p.tokens) {
+    if (t + 1 < t_end) {
       load_token(t + 1, kn, qn, vn, gn, bn);
     }
     float g = gc;
@@ -128,7 +148,8 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnParams p) {
 
 template <bool kPrepare>
 hipError_t launch_gdn_cpl(const GdnParams& p, hipStream_t stream) {
-  const dim3 grid((p.head_dim + kGdnRowsPerBlock - 1) / kGdnRowsPerBlock, p.value_heads);
+  const dim3 grid((p.head_dim + kGdnRowsPerBlock - 1) / kGdnRowsPerBlock, p.value_heads,
+                  p.seq_state_offsets != nullptr ? p.tokens : 1u);
   const uint32_t cpl = (p.head_dim + 31) / 32;
   if (cpl <= 1) {
     gdn_recurrent_kernel<1, kPrepare><<<grid, 256, 0, stream>>>(p);
@@ -343,6 +364,82 @@ __global__ void conv_state_update_kernel(float* conv_state, const float* qkv,
   }
 }
 
+// Ragged decode form of the fused prologue: one token per sequence, sequence b's
+// conv state R_b [channels][K-1] at element seq_conv_offsets[b] of a pool.  One
+// wave per (head-slice, sequence); lane owns CPL channels.  The state update is
+// fused (each channel's state is read and rewritten by the one lane that owns it).
+template <int CPL, int K>
+__global__ __launch_bounds__(64) void conv_split_l2_ragged_kernel(
+  const float* qkv, float* conv_pool, const uint64_t* seq_conv_offsets, uint64_t pool_elems,
+  const float* weights, uint32_t key_heads, uint32_t value_heads, uint32_t head_dim, float eps,
+  float* query, float* key, float* value) {
+  constexpr int W = K - 1;
+  const uint32_t heads_total = 2u * key_heads + value_heads;
+  const uint32_t unit = blockIdx.x;  // which q/k/v head
+  const uint32_t seq = blockIdx.y;
+  const int lane = threadIdx.x;
+  const size_t channels = (size_t)heads_total * head_dim;
+  const uint64_t off = seq_conv_offsets[seq];
+  if (off > pool_elems || pool_elems - off < channels * W) {
+    return;  // offset outside the pool: this sequence is skipped, nothing touched
+  }
+  float* state = conv_pool + off;
+  const uint32_t cbase = unit * head_dim;
+  float y[CPL];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const uint32_t d = lane + 64u * i;
+    const bool ok = d < head_dim;
+    const size_t c = cbase + (ok ? d : 0u);
+    float win[W];
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      win[j] = ok ? state[c * W + j] : 0.0f;
+    }
+    const float xt = ok ? qkv[(size_t)seq * channels + c] : 0.0f;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      acc = fmaf(win[j], ok ? weights[c * K + j] : 0.0f, acc);
+    }
+    acc = fmaf(xt, ok ? weights[c * K + W] : 0.0f, acc);
+    if (ok) {
+#pragma unroll
+      for (int j = 0; j + 1 < W; ++j) {
+        state[c * W + j] = win[j + 1];
+      }
+      state[c * W + (W - 1)] = xt;
+    }
+    const float sl = acc / (1.0f + expf(-acc));  // SiLU
+    y[i] = ok ? sl : 0.0f;
+    ss = fmaf(y[i], y[i], ss);
+  }
+  if (unit >= 2u * key_heads) {
+    float* dst = value + ((size_t)seq * value_heads + (unit - 2u * key_heads)) * head_dim;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const uint32_t d = lane + 64u * i;
+      if (d < head_dim) {
+        dst[d] = y[i];
+      }
+    }
+    return;
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / fmaxf(sqrtf(ss), eps);
+  const uint32_t part = unit / key_heads;
+  const uint32_t kh = unit % key_heads;
+  float* dst = (part == 0 ? query : key) + ((size_t)seq * key_heads + kh) * head_dim;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const uint32_t d = lane + 64u * i;
+    if (d < head_dim) {
+      dst[d] = y[i] * inv;
+    }
+  }
+}
+
 unsigned grid_for(size_t total, unsigned block = 256) {
   size_t blocks = (total + block - 1) / block;
   if (blocks < 1) {
@@ -373,6 +470,8 @@ hipError_t launch_gated_delta_net(const GdnArgs& a, int cu_count, hipStream_t st
   p.value_heads = a.value_heads;
   p.head_dim = a.head_dim;
   p.scale = 1.0f / sqrtf((float)a.head_dim);
+  p.seq_state_offsets = a.seq_state_offsets;
+  p.pool_elems = a.pool_elems;
   hipError_t e = a.dt_bias != nullptr ? launch_gdn_cpl<true>(p, stream)
                                       : launch_gdn_cpl<false>(p, stream);
   if (e != hipSuccess || a.z == nullptr) {
@@ -440,6 +539,32 @@ hipError_t launch_conv_split_l2(const float* qkv, float* conv_state, const float
   const uint32_t channels = heads_total * head_dim;
   conv_state_update_kernel<<<(channels + 255u) / 256u, 256, 0, stream>>>(
     conv_state, qkv, conv_kernel, tokens, channels);
+  return hipGetLastError();
+}
+
+hipError_t launch_conv_split_l2_ragged(const float* qkv, float* conv_pool,
+                                       const uint64_t* seq_conv_offsets, uint64_t pool_elems,
+                                       const float* weights, uint32_t conv_kernel,
+                                       uint32_t sequences, uint32_t key_heads,
+                                       uint32_t value_heads, uint32_t head_dim, float eps,
+                                       float* query, float* key, float* value,
+                                       hipStream_t stream) {
+  const dim3 grid(2u * key_heads + value_heads, sequences);
+  const uint32_t cpl = (head_dim + 63u) / 64u;
+  const int kk = (int)conv_kernel;
+#define KRAKEN_CONV_CASE(CPLV, KV)                                                           \
+  if (cpl <= CPLV && kk == KV) {                                                             \
+    conv_split_l2_ragged_kernel<CPLV, KV><<<grid, 64, 0, stream>>>(                          \
+      qkv, conv_pool, seq_conv_offsets, pool_elems, weights, key_heads, value_heads, head_dim, \
+      eps, query, key, value);                                                               \
+  } else
+#define KRAKEN_CONV_CPL(CPLV)                                                                \
+  KRAKEN_CONV_CASE(CPLV, 2) KRAKEN_CONV_CASE(CPLV, 3) KRAKEN_CONV_CASE(CPLV, 4)             \
+  KRAKEN_CONV_CASE(CPLV, 5) KRAKEN_CONV_CASE(CPLV, 6) KRAKEN_CONV_CASE(CPLV, 7)             \
+  KRAKEN_CONV_CASE(CPLV, 8)
+  KRAKEN_CONV_CPL(1) KRAKEN_CONV_CPL(2) KRAKEN_CONV_CPL(4) { return hipErrorInvalidValue; }
+#undef KRAKEN_CONV_CPL
+#undef KRAKEN_CONV_CASE
   return hipGetLastError();
 }
 

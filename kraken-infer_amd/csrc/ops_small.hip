@@ -185,6 +185,28 @@ __global__ void copy_rows_kernel(const Src* source, Dst* destination, size_t tot
   }
 }
 
+// Ragged KV append (one new row per sequence): the f32 -> f16 row copy of
+// copy_f32_rows_to_f16 (mps_backend.mm:2655-2666) with the destination row taken
+// from per-sequence tables.  A row that would land outside the pool is skipped.
+__global__ void append_kv_ragged_kernel(const float* key_rows, const float* value_rows,
+                                        half_t* key_pool, half_t* value_pool,
+                                        const uint64_t* seq_offsets,
+                                        const uint32_t* seq_positions, uint64_t pool_elems,
+                                        uint32_t sequences, uint32_t row_size) {
+  const size_t total = (size_t)sequences * row_size;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t b = i / row_size;
+    const size_t c = i % row_size;
+    const uint64_t row0 = seq_offsets[b] + (uint64_t)seq_positions[b] * row_size;
+    if (row0 > pool_elems || pool_elems - row0 < row_size) {
+      continue;
+    }
+    key_pool[row0 + c] = static_cast<half_t>(key_rows[i]);
+    value_pool[row0 + c] = static_cast<half_t>(value_rows[i]);
+  }
+}
+
 // sigmoid/softplus/silu_f32_in_place (mps_backend.mm:2569-2618).
 template <UnaryKind K>
 __global__ void unary_kernel(float* values, size_t size) {
@@ -302,6 +324,18 @@ hipError_t launch_copy_rows(CopyKind kind, const void* source, void* destination
         source_stride, source_offset, destination_stride, destination_offset);
       break;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_append_kv_ragged(const float* key_rows, const float* value_rows,
+                                   void* key_pool, void* value_pool,
+                                   const uint64_t* seq_offsets, const uint32_t* seq_positions,
+                                   uint64_t pool_elems, uint32_t sequences, uint32_t row_size,
+                                   hipStream_t stream) {
+  const size_t total = (size_t)sequences * row_size;
+  append_kv_ragged_kernel<<<grid_for(total), 256, 0, stream>>>(
+    key_rows, value_rows, static_cast<half_t*>(key_pool), static_cast<half_t*>(value_pool),
+    seq_offsets, seq_positions, pool_elems, sequences, row_size);
   return hipGetLastError();
 }
 

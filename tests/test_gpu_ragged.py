@@ -1,0 +1,231 @@
+"""Ragged multi-sequence decode on the GPU against the CPU oracle, sequence by
+sequence.
+
+Each sequence contributes one token.  Its result must equal the single-sequence
+op's on its own data:
+- attention: oracle_attention_batched with tokens = 1, start = position, f16 KV
+  (mps_backend.mm:2943-3008), then sigmoid(G) when gated
+  (qwen35_runtime.cpp:3347-3355);
+- GDN: oracle_gated_delta_net with tokens = 1 (mps_backend.mm:2307-2374);
+- conv prologue: oracle build_ssm_conv_state + ssm_conv + SiLU + split/L2
+  (mps_backend.mm:2097-2153, 2376-2457).
+Pools hold the sequences at scattered offsets with gaps.  Out-of-pool and
+misaligned offsets must leave memory untouched or read zeros, never fault.
+Tolerances: 2e-3 rel / 1e-3 abs (f16 KV); 1e-4 abs on f32 GDN state and
+outputs; 1e-5 on the conv prologue.
+"""
+import numpy as np
+import pytest
+
+import kraken_hip as kh
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def scattered_offsets(rng, rows, row_elems, align=8):
+    """Element offsets of sequences with `rows[i]` rows each, in order, with random
+    aligned gaps; returns (offsets, total elements)."""
+    offsets, cur = [], 0
+    for r in rows:
+        cur += int(rng.integers(0, 4)) * align
+        offsets.append(cur)
+        cur += r * row_elems
+        cur = (cur + align - 1) // align * align
+    return np.array(offsets, np.uint64), cur + 4 * align
+
+
+def attention_reference(q, kpool, vpool, offsets, positions, heads, kv_heads, d, gate=None):
+    kv_dim = kv_heads * d
+    out = []
+    for b, (off, pos) in enumerate(zip(offsets, positions)):
+        rows = int(pos) + 1
+        kc = kpool[int(off):int(off) + rows * kv_dim].view(np.uint16)
+        vc = vpool[int(off):int(off) + rows * kv_dim].view(np.uint16)
+        qb = q[b * heads * d:(b + 1) * heads * d]
+        r = oracle.attention_batched(qb, kc, vc, 0, int(pos), 1, rows, heads, kv_heads, d)
+        if gate is not None:
+            r = oracle.sigmoid_gate_mul(r, gate[b * heads * d:(b + 1) * heads * d])
+        out.append(r)
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("d,heads,kv_heads", [(256, 8, 2), (128, 8, 4), (64, 16, 2)])
+@pytest.mark.parametrize("gated", [False, True])
+def test_ragged_attention_matches_oracle(hip_ctx, d, heads, kv_heads, gated):
+    rng = np.random.default_rng(40 + d + heads)
+    # Positions around the 1024-key split boundary, tiny and long ones.
+    positions = np.array([0, 1, 31, 1023, 1024, 1025, 2047, 3000, 5], np.uint32)
+    b = len(positions)
+    kv_dim = kv_heads * d
+    offsets, total = scattered_offsets(rng, positions.astype(np.int64) + 1, kv_dim)
+    kpool = rng.standard_normal(total).astype(np.float16)
+    vpool = rng.standard_normal(total).astype(np.float16)
+    q = rng.standard_normal(b * heads * d).astype(np.float32)
+    gate = rng.standard_normal(b * heads * d).astype(np.float32) if gated else None
+    ctx = hip_ctx
+    kb, vb = ctx.buffer(kpool.view(np.uint16)), ctx.buffer(vpool.view(np.uint16))
+    qb, ob = ctx.buffer(q), ctx.buffer(byte_size=4 * q.size)
+    gb = ctx.buffer(gate) if gated else None
+    ctx.attention_f32_ragged_f16_kv(qb, kb, vb, gb, ctx.buffer(offsets), ctx.buffer(positions),
+                                    b, int(positions.max()), heads, kv_heads, d, ob)
+    got = ob.download()
+    ref = attention_reference(q, kpool, vpool, offsets, positions, heads, kv_heads, d, gate)
+    np.testing.assert_allclose(got, ref, rtol=2e-3, atol=1e-3)
+
+
+def test_ragged_attention_bad_offsets_read_zeros(hip_ctx):
+    """An offset outside the pool, or not a whole 16-byte chunk, reads zeros: the
+    output is the uniform mean of zero values (0); other sequences are unaffected."""
+    rng = np.random.default_rng(7)
+    heads, kv_heads, d = 8, 2, 256
+    kv_dim = kv_heads * d
+    positions = np.array([100, 200, 300, 50], np.uint32)
+    offsets, total = scattered_offsets(rng, positions.astype(np.int64) + 1, kv_dim)
+    good = offsets.copy()
+    offsets[1] = np.uint64(total + 1024)          # past the pool
+    offsets[3] = np.uint64(int(offsets[3]) + 3)   # misaligned rows
+    kpool = rng.standard_normal(total).astype(np.float16)
+    vpool = rng.standard_normal(total).astype(np.float16)
+    q = rng.standard_normal(4 * heads * d).astype(np.float32)
+    ctx = hip_ctx
+    ob = ctx.buffer(byte_size=4 * q.size)
+    ctx.attention_f32_ragged_f16_kv(ctx.buffer(q), ctx.buffer(kpool.view(np.uint16)),
+                                    ctx.buffer(vpool.view(np.uint16)), None,
+                                    ctx.buffer(offsets), ctx.buffer(positions), 4, 300, heads,
+                                    kv_heads, d, ob)
+    got = ob.download().reshape(4, heads * d)
+    ref = attention_reference(q, kpool, vpool, good, positions, heads, kv_heads, d)
+    ref = ref.reshape(4, heads * d)
+    np.testing.assert_array_equal(got[1], 0.0)
+    np.testing.assert_array_equal(got[3], 0.0)
+    np.testing.assert_allclose(got[[0, 2]], ref[[0, 2]], rtol=2e-3, atol=1e-3)
+
+
+def test_ragged_kv_append(hip_ctx):
+    rng = np.random.default_rng(8)
+    kv_dim = 512
+    positions = np.array([0, 7, 1500, 3], np.uint32)
+    offsets, total = scattered_offsets(rng, positions.astype(np.int64) + 1, kv_dim)
+    kpool = rng.standard_normal(total).astype(np.float16)
+    vpool = rng.standard_normal(total).astype(np.float16)
+    krows = rng.standard_normal(4 * kv_dim).astype(np.float32)
+    vrows = rng.standard_normal(4 * kv_dim).astype(np.float32)
+    ctx = hip_ctx
+    kb, vb = ctx.buffer(kpool.view(np.uint16)), ctx.buffer(vpool.view(np.uint16))
+    ctx.append_kv_ragged_f16(ctx.buffer(krows), ctx.buffer(vrows), kb, vb, ctx.buffer(offsets),
+                             ctx.buffer(positions), 4, kv_dim)
+    ek, ev = kpool.copy(), vpool.copy()
+    for b in range(4):
+        row = int(offsets[b]) + int(positions[b]) * kv_dim
+        ek[row:row + kv_dim] = krows[b * kv_dim:(b + 1) * kv_dim].astype(np.float16)
+        ev[row:row + kv_dim] = vrows[b * kv_dim:(b + 1) * kv_dim].astype(np.float16)
+    np.testing.assert_array_equal(kb.download(dtype=np.uint16), ek.view(np.uint16))
+    np.testing.assert_array_equal(vb.download(dtype=np.uint16), ev.view(np.uint16))
+
+
+def gdn_inputs(rng, b, hk, hv, dd):
+    def unit(n):
+        x = rng.standard_normal((n, dd)).astype(np.float32)
+        return (x / np.linalg.norm(x, axis=1, keepdims=True)).astype(np.float32).ravel()
+    q, k = unit(b * hk), unit(b * hk)
+    v = rng.standard_normal(b * hv * dd).astype(np.float32)
+    g = (-np.logaddexp(0, rng.standard_normal(b * hv))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal(b * hv)))).astype(np.float32)
+    return q, k, v, g, beta
+
+
+def test_ragged_gdn_decode_matches_oracle(hip_ctx):
+    rng = np.random.default_rng(9)
+    b, hk, hv, dd = 6, 16, 16, 128
+    state_elems = hv * dd * dd
+    offsets, total = scattered_offsets(rng, [1] * b, state_elems, align=dd)
+    offsets[4] = np.uint64(total + 7)  # outside the pool: skipped, nothing touched
+    pool = (0.1 * rng.standard_normal(total)).astype(np.float32)
+    q, k, v, g, beta = gdn_inputs(rng, b, hk, hv, dd)
+    ctx = hip_ctx
+    sb = ctx.buffer(pool)
+    sentinel = np.full(b * hv * dd, 7.0, np.float32)
+    ob = ctx.buffer(sentinel)
+    ctx.gated_delta_net_f32_ragged_decode(ctx.buffer(q), ctx.buffer(k), ctx.buffer(v),
+                                          ctx.buffer(g), ctx.buffer(beta), sb,
+                                          ctx.buffer(offsets), b, hk, hv, dd, ob)
+    got_out = ob.download().reshape(b, hv * dd)
+    got_pool = sb.download()
+    exp_pool = pool.copy()
+    for i in range(b):
+        if i == 4:
+            np.testing.assert_array_equal(got_out[i], 7.0)
+            continue
+        off = int(offsets[i])
+        s = pool[off:off + state_elems].copy()
+        sl = slice(i * hk * dd, (i + 1) * hk * dd)
+        vl = slice(i * hv * dd, (i + 1) * hv * dd)
+        gl = slice(i * hv, (i + 1) * hv)
+        out, st = oracle.gated_delta_net(q[sl], k[sl], v[vl], g[gl], beta[gl], s, 1, hk, hv, dd)
+        np.testing.assert_allclose(got_out[i], out, rtol=0, atol=1e-4)
+        exp_pool[off:off + state_elems] = st
+    np.testing.assert_allclose(got_pool, exp_pool, rtol=0, atol=1e-4)
+
+
+def test_ragged_conv_split_matches_oracle(hip_ctx):
+    rng = np.random.default_rng(10)
+    b, hk, hv, dd, kk = 5, 16, 16, 128, 4
+    ch = (2 * hk + hv) * dd
+    state_elems = ch * (kk - 1)
+    offsets, total = scattered_offsets(rng, [1] * b, state_elems, align=64)
+    pool = rng.standard_normal(total).astype(np.float32)
+    x = rng.standard_normal(b * ch).astype(np.float32)
+    w = (0.5 * rng.standard_normal(ch * kk)).astype(np.float32)
+    ctx = hip_ctx
+    pb = ctx.buffer(pool)
+    qb, kb = ctx.buffer(byte_size=4 * b * hk * dd), ctx.buffer(byte_size=4 * b * hk * dd)
+    vb = ctx.buffer(byte_size=4 * b * hv * dd)
+    ctx.qwen35_conv_split_l2_ragged_decode_f32(ctx.buffer(x), pb, ctx.buffer(offsets),
+                                               ctx.buffer(w), kk, b, hk, hv, dd, 1e-6, qb, kb,
+                                               vb)
+    gq, gk, gv = qb.download(), kb.download(), vb.download()
+    got_pool = pb.download()
+    exp_pool = pool.copy()
+    for i in range(b):
+        off = int(offsets[i])
+        st = pool[off:off + state_elems].copy()
+        xi = x[i * ch:(i + 1) * ch]
+        ci, new_state = oracle.build_ssm_conv_state(st, xi, kk, ch, 1)
+        y = oracle.silu(oracle.ssm_conv(ci, w, kk, ch, 1, 1))
+        rq, rk, rv = oracle.split_qkv_l2_norm(y, 1, hk, hv, dd, 1e-6)
+        np.testing.assert_allclose(gq[i * hk * dd:(i + 1) * hk * dd], rq, rtol=0, atol=1e-5)
+        np.testing.assert_allclose(gk[i * hk * dd:(i + 1) * hk * dd], rk, rtol=0, atol=1e-5)
+        np.testing.assert_allclose(gv[i * hv * dd:(i + 1) * hv * dd], rv, rtol=0, atol=1e-5)
+        exp_pool[off:off + state_elems] = new_state
+    np.testing.assert_array_equal(got_pool, exp_pool)
+
+
+def test_ragged_attention_c4_shape_sampled(hip_ctx):
+    """C4 attention layer shape: 64 sequences, lengths in [512, 32768]; eight
+    sequences (shortest, longest and six others) checked against the oracle."""
+    rng = np.random.default_rng(4)
+    heads, kv_heads, d = 8, 2, 256
+    kv_dim = kv_heads * d
+    b = 64
+    positions = rng.integers(512, 32769, b).astype(np.uint32)
+    offsets, total = scattered_offsets(rng, positions.astype(np.int64) + 1, kv_dim)
+    # ~1 GB per pool: a random 1M-element block repeated (period ~2048 rows).
+    block = 1 << 20
+    kpool = np.resize(rng.standard_normal(block).astype(np.float16), total)
+    vpool = np.resize(rng.standard_normal(block + 8).astype(np.float16), total)
+    q = rng.standard_normal(b * heads * d).astype(np.float32)
+    gate = rng.standard_normal(b * heads * d).astype(np.float32)
+    ctx = hip_ctx
+    ob = ctx.buffer(byte_size=4 * q.size)
+    ctx.attention_f32_ragged_f16_kv(ctx.buffer(q), ctx.buffer(kpool.view(np.uint16)),
+                                    ctx.buffer(vpool.view(np.uint16)), ctx.buffer(gate),
+                                    ctx.buffer(offsets), ctx.buffer(positions), b,
+                                    int(positions.max()), heads, kv_heads, d, ob)
+    got = ob.download().reshape(b, heads * d)
+    pick = sorted({int(np.argmin(positions)), int(np.argmax(positions)), 3, 17, 29, 40, 51, 63})
+    for i in pick:
+        sl = slice(i * heads * d, (i + 1) * heads * d)
+        ref = attention_reference(q[sl], kpool, vpool, offsets[i:i + 1], positions[i:i + 1],
+                                  heads, kv_heads, d, gate[sl])
+        np.testing.assert_allclose(got[i], ref, rtol=2e-3, atol=1e-3, err_msg=f"sequence {i}")
