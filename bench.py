@@ -224,6 +224,138 @@ def bench_gdn(torch, ctx, run, gen):
     return res
 
 
+def mt19937_64(seed):
+    """64-bit Mersenne Twister (Matsumoto & Nishimura, 2004), std::mt19937_64."""
+    mask = (1 << 64) - 1
+    n, m = 312, 156
+    mt = [seed & mask] + [0] * (n - 1)
+    for i in range(1, n):
+        mt[i] = (6364136223846793005 * (mt[i - 1] ^ (mt[i - 1] >> 62)) + i) & mask
+    idx = n
+    while True:
+        if idx >= n:
+            for i in range(n):
+                x = (mt[i] & 0xFFFFFFFF80000000) | (mt[(i + 1) % n] & 0x7FFFFFFF)
+                xa = x >> 1
+                if x & 1:
+                    xa ^= 0xB5026F5AA96619E9
+                mt[i] = mt[(i + m) % n] ^ xa
+            idx = 0
+        y = mt[idx]
+        idx += 1
+        y ^= (y >> 29) & 0x5555555555555555
+        y ^= (y << 17) & 0x71D67FFFEDA60000
+        y ^= (y << 37) & 0xFFF7EEE000000000
+        y ^= y >> 43
+        yield y & mask
+
+
+C4_SEQUENCES = 64
+C4_GDN_LAYERS = 3
+
+
+def c4_lengths():
+    """KV lengths L_i in [512, 32768]: 512 + (mt19937_64(seed 4) output mod 32257)."""
+    g = mt19937_64(4)
+    return [512 + next(g) % 32257 for _ in range(C4_SEQUENCES)]
+
+
+def bench_c4(torch, ctx, run, gen, steps=20):
+    """C4: 64 sequences, one token each per step, each running one hybrid block of
+    3 GDN layers (fused conv prologue, recurrence, norm-gated epilogue) and one
+    full-attention layer (KV append + gated attention) through the ragged
+    multi-sequence entry points."""
+    dev = "cuda"
+    b = C4_SEQUENCES
+    hk = hv = 16
+    dg = 128
+    ch = (2 * hk + hv) * dg
+    kv_dim = HKV * D
+    lengths = c4_lengths()
+    # Sequence i owns rows [0, L_i + 1) of its K/V (the new token at row L_i).
+    rows = [l + 1 for l in lengths]
+    kv_off, cur = [], 0
+    for r in rows:
+        kv_off.append(cur)
+        cur += r * kv_dim
+    kpool = torch.randn(cur, generator=gen, device=dev).half()
+    vpool = torch.randn(cur, generator=gen, device=dev).half()
+    kv_off_t = torch.tensor(kv_off, dtype=torch.int64, device=dev)
+    pos_t = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    state_elems = hv * dg * dg
+    state_pool = torch.zeros(C4_GDN_LAYERS * b * state_elems, device=dev)
+    conv_pool = torch.zeros(C4_GDN_LAYERS * b * ch * 3, device=dev)
+    state_off = [torch.arange(b, device=dev, dtype=torch.int64) * state_elems
+                 + l * b * state_elems for l in range(C4_GDN_LAYERS)]
+    conv_off = [torch.arange(b, device=dev, dtype=torch.int64) * ch * 3 + l * b * ch * 3
+                for l in range(C4_GDN_LAYERS)]
+    qkv = [torch.randn(b * ch, generator=gen, device=dev) for _ in range(C4_GDN_LAYERS)]
+    w = [0.5 * torch.randn(ch * 4, generator=gen, device=dev) for _ in range(C4_GDN_LAYERS)]
+    g = [-torch.nn.functional.softplus(torch.randn(b * hv, generator=gen, device=dev))
+         for _ in range(C4_GDN_LAYERS)]
+    beta = [torch.sigmoid(torch.randn(b * hv, generator=gen, device=dev))
+            for _ in range(C4_GDN_LAYERS)]
+    z = [torch.randn(b * hv * dg, generator=gen, device=dev) for _ in range(C4_GDN_LAYERS)]
+    norm_w = torch.ones(dg, device=dev)
+    q = torch.empty(b * hk * dg, device=dev)
+    k = torch.empty(b * hk * dg, device=dev)
+    v = torch.empty(b * hv * dg, device=dev)
+    y = torch.empty(b * hv * dg, device=dev)
+    knew = torch.randn(b * kv_dim, generator=gen, device=dev)
+    vnew = torch.randn(b * kv_dim, generator=gen, device=dev)
+    aq = torch.randn(b * HQ * D, generator=gen, device=dev)
+    agate = torch.randn(b * HQ * D, generator=gen, device=dev)
+    aout = torch.empty(b * HQ * D, device=dev)
+    maxpos = max(lengths)
+
+    def gdn_layer(l, core_only=False):
+        if not core_only:
+            ctx.qwen35_conv_split_l2_ragged_decode_f32(qkv[l], conv_pool, conv_off[l], w[l], 4, b,
+                                                       hk, hv, dg, 1e-6, q, k, v)
+        ctx.gated_delta_net_f32_ragged_decode(q, k, v, g[l], beta[l], state_pool, state_off[l],
+                                              b, hk, hv, dg, y)
+        if not core_only:
+            ctx.qwen35_norm_gated_f32_in_place(y, norm_w, z[l], b, hv, dg, 1e-6)
+
+    def attention_layer(append=True):
+        if append:
+            ctx.append_kv_ragged_f16(knew, vnew, kpool, vpool, kv_off_t, pos_t, b, kv_dim)
+        ctx.attention_f32_ragged_f16_kv(aq, kpool, vpool, agate, kv_off_t, pos_t, b, maxpos, HQ,
+                                        HKV, D, aout)
+
+    def block():
+        for l in range(C4_GDN_LAYERS):
+            gdn_layer(l)
+        attention_layer()
+
+    # Warm the q/k/v inputs of the core-only timing with one full layer.
+    gdn_layer(0)
+    kv_bytes = sum(2048 * r for r in rows)
+    gdn_bytes = b * C4_GDN_LAYERS * GDN_DECODE_BYTES
+    res = {"sequences": b, "kv_len_min": min(lengths), "kv_len_max": maxpos,
+           "kv_len_mean": sum(lengths) / b, "kv_bytes_per_step": kv_bytes,
+           "gdn_core_bytes_per_step": gdn_bytes,
+           "lengths": "512 + mt19937_64(seed 4) mod 32257"}
+    ms, graph = run.time([block] * steps, 2)
+    del graph
+    res["block"] = {"ms_per_step": ms, "tok_s": b / (ms * 1e-3),
+                    "kv_GB_s": kv_bytes / (ms * 1e-3) / 1e9,
+                    "GB_s": (kv_bytes + gdn_bytes) / (ms * 1e-3) / 1e9,
+                    "frac_hbm_peak": (kv_bytes + gdn_bytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    ms, graph = run.time([lambda: attention_layer(False)] * steps, 2)
+    del graph
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    res["attention"] = {"ms_per_step": ms, "GB_s": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS}
+    ms, graph = run.time([lambda: [gdn_layer(l, True) for l in range(C4_GDN_LAYERS)]] * steps, 2)
+    del graph
+    gbs = gdn_bytes / (ms * 1e-3) / 1e9
+    res["gdn_core"] = {"ms_per_step": ms, "GB_s": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
+                       "tok_s": b * C4_GDN_LAYERS / (ms * 1e-3)}
+    del kpool, vpool, state_pool, conv_pool
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(kv_len, budget_s):
     """Times the oracle's decode step (one core) on a bounded sample."""
     import numpy as np
@@ -326,6 +458,9 @@ def main():
             gen.manual_seed(3)
             details["gdn_c3"] = bench_gdn(torch, ctx, run, gen)
             progress("gdn done")
+            gen.manual_seed(4)
+            details["ragged_c4"] = bench_c4(torch, ctx, run, gen)
+            progress("ragged c4 done")
     run.close()
     ctx.close()
 

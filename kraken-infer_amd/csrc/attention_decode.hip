@@ -43,8 +43,6 @@
 namespace kraken {
 namespace {
 
-constexpr int kWaves = 16;  // waves per decode workgroup
-constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxSplits = 256;  // merge pass: 64 subsets x 4 loads per thread
 
 struct DecodeParams {
@@ -63,6 +61,9 @@ struct DecodeParams {
   const uint64_t* seq_kv_offsets;
   const uint32_t* seq_positions;
   uint64_t pool_elems;
+  // Ragged mode: dense work list, one item per workgroup (blockIdx.x):
+  // {token, kv_head << 16 | split}, token 0xffffffff past the last item.
+  const uint2* work_items;
 };
 
 // Keys of token t (positions table in ragged mode); at least 1 (a position of
@@ -101,14 +102,21 @@ struct KvTraits<float> {
 
 __device__ __forceinline__ float sigmoidf_acc(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Lane geometry of a key row: E elements per 16-byte chunk, R lanes per row,
-// KW keys per wave per round, KPR keys per workgroup round.
-template <int D, typename KV>
+// Lane geometry of a key row: a lane holds C consecutive 16-byte chunks of E
+// elements (EL = E*C elements), R = D/EL lanes span a row, a wave takes
+// KW = 64/R keys per round, a workgroup of W = 16/C waves takes KPR = W*KW.
+// More chunks per lane amortise the per-key cross-lane reductions and softmax
+// bookkeeping over more FMAs; the workgroup shrinks so the larger per-lane
+// query and accumulator slices fit the register file.
+template <int D, typename KV, int C>
 struct RowShape {
   static constexpr int E = KvTraits<KV>::kPerChunk;
-  static constexpr int R = D / E;
+  static constexpr int EL = E * C;
+  static constexpr int R = D / EL;
   static constexpr int KW = 64 / R;
-  static constexpr int KPR = kWaves * KW;
+  static constexpr int W = 16 / C;
+  static constexpr int KPR = W * KW;
+  static_assert(C == 1 || C == 2, "one or two chunks per lane");
   static_assert(R >= 8 && R <= 64 && 64 % R == 0, "row must span 8..64 lanes");
 };
 
@@ -182,17 +190,23 @@ __device__ __forceinline__ float uniform_f(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, x)));
 }
 
-template <int D, int G, typename KV>
-__global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams p) {
+template <int D, int G, typename KV, int C, int P>
+__global__ __launch_bounds__((64 * RowShape<D, KV, C>::W)) void attention_decode_kernel(
+  DecodeParams p) {
+  static_assert(P == 2 || P == 4, "prefetch depth 2 or 4");
   using T = KvTraits<KV>;
-  using S = RowShape<D, KV>;
+  using S = RowShape<D, KV, C>;
   constexpr int E = S::E;
+  constexpr int EL = S::EL;
   constexpr int R = S::R;
   constexpr int KW = S::KW;
   constexpr int KPR = S::KPR;
-  // A lane's query slice (G heads x its E dims) lives in registers when small;
-  // otherwise in LDS, read by all lanes that hold the same dims.
-  constexpr bool kQRegs = G * E <= 32;
+  constexpr int kWaves = S::W;
+  constexpr int kThreads = 64 * kWaves;
+  // A lane's query slice (G heads x its EL dims) lives in registers when it
+  // fits beside the accumulators; otherwise in LDS, read by all lanes that hold
+  // the same dims.
+  constexpr bool kQRegs = G * EL <= (C == 2 ? 64 : 32);
   constexpr int kQVec = G * D / 4;
   constexpr int kOutPerThread = (G * D + kThreads - 1) / kThreads;
   static_assert(kQVec <= kThreads, "query staging takes one float4 per thread");
@@ -210,10 +224,19 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kslot = lane / R;
   const int c = lane % R;
-  const uint32_t split = blockIdx.x;
-  const uint32_t kvh = blockIdx.y;
-  const uint32_t token = blockIdx.z;
+  uint32_t split = blockIdx.x;
+  uint32_t kvh = blockIdx.y;
+  uint32_t token = blockIdx.z;
   const bool ragged = p.seq_positions != nullptr;
+  if (ragged) {
+    const uint2 item = p.work_items[blockIdx.x];
+    if (item.x == 0xffffffffu) {
+      return;  // past the last work item
+    }
+    token = item.x;
+    kvh = item.y >> 16;
+    split = item.y & 0xffffu;
+  }
   const uint32_t n_keys = token_keys(p.seq_positions, p.start_position, token);
   const uint32_t key_begin = split * p.keys_per_split;
   if (key_begin >= n_keys) {
@@ -233,21 +256,18 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams
   // before K/V: vector loads retire in issue order, so using the query waits
   // only for the query (measured faster than issuing K/V first).
   const float* qhead = p.query + ((size_t)token * p.heads + kvh * G) * D;
-  float4 qraw[kQRegs ? G * E / 4 : 1];
-  auto load_query = [&]() {
-    if constexpr (kQRegs) {
+  float4 qraw[kQRegs ? G * EL / 4 : 1];
+  if constexpr (kQRegs) {
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
+    for (int g = 0; g < G; ++g) {
 #pragma unroll
-        for (int e = 0; e < E; e += 4) {
-          qraw[(g * E + e) / 4] = *reinterpret_cast<const float4*>(qhead + g * D + c * E + e);
-        }
+      for (int e = 0; e < EL; e += 4) {
+        qraw[(g * EL + e) / 4] = *reinterpret_cast<const float4*>(qhead + g * D + c * EL + e);
       }
-    } else {
-      qraw[0] = reinterpret_cast<const float4*>(qhead)[tid < kQVec ? tid : 0];
     }
-  };
-  load_query();
+  } else {
+    qraw[0] = reinterpret_cast<const float4*>(qhead)[tid < kQVec ? tid : 0];
+  }
 
   // K/V rows of the split through buffer resources based at its first row and
   // ending at its last: lanes and rounds past the end read zeros from the range
@@ -270,30 +290,40 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams
     make_buffer_rsrc(vbase + (size_t)key_begin * row_stride, span_bytes);
   const uint32_t wave_first = (uint32_t)(wave * KW);  // wave's first key in a round
   const uint32_t lane_key = wave_first + (uint32_t)kslot;
-  const uint32_t lane_off = lane_key * row_bytes + 16u * c;
+  const uint32_t lane_off = lane_key * row_bytes + 16u * C * c;
 
-  // Two register sets in ping-pong (A: even rounds, B: odd rounds), each
-  // reloaded in place right after its round computes, so the next two rounds
-  // are always in flight and no loaded register is ever copied (a copy would
-  // have to wait for its load).
-  // The scheduling barriers pin the issue order (K then V, even then odd
-  // round), which the wait counts in the loop below depend on.
-  __builtin_amdgcn_sched_barrier(0);
-  u32x4_t ka = buffer_load_nt_b128(krsrc, lane_off);
-  u32x4_t va = buffer_load_nt_b128(vrsrc, lane_off);
-  __builtin_amdgcn_sched_barrier(0);
-  u32x4_t kb_ = buffer_load_nt_b128(krsrc, lane_off + KPR * row_bytes);
-  u32x4_t vb_ = buffer_load_nt_b128(vrsrc, lane_off + KPR * row_bytes);
+  // A ring of P register sets (round r uses set r % P), each reloaded in place
+  // right after its round computes, so the next P rounds are always in flight
+  // and no loaded register is ever copied (a copy would have to wait for its
+  // load).  The scheduling barriers pin the issue order (K then V, set by
+  // set), which the wait counts in the loop below depend on.
+  u32x4_t kset[P][C], vset[P][C];
+  auto load_set = [&](uint32_t ki, u32x4_t* kreg, u32x4_t* vreg) {
+    const uint32_t off = lane_off + ki * row_bytes;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      kreg[j] = buffer_load_nt_b128(krsrc, off + 16u * j);
+    }
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      vreg[j] = buffer_load_nt_b128(vrsrc, off + 16u * j);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    __builtin_amdgcn_sched_barrier(0);
+    load_set((uint32_t)i * KPR, kset[i], vset[i]);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // Query pre-scaled into the log2 domain.
-  float qr[kQRegs ? G : 1][kQRegs ? E : 1];
+  float qr[kQRegs ? G : 1][kQRegs ? EL : 1];
   if constexpr (kQRegs) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int e = 0; e < E; e += 4) {
-        const float4 t = qraw[(g * E + e) / 4];
+      for (int e = 0; e < EL; e += 4) {
+        const float4 t = qraw[(g * EL + e) / 4];
         qr[g][e + 0] = t.x * p.scale_log2;
         qr[g][e + 1] = t.y * p.scale_log2;
         qr[g][e + 2] = t.z * p.scale_log2;
@@ -309,40 +339,43 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams
 
   float m[G];  // wave-uniform reference max (log2 domain)
   float l[G];
-  float o[G][E];
+  float o[G][EL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
     l[g] = 0.0f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
+    for (int e = 0; e < EL; ++e) {
       o[g][e] = 0.0f;
     }
   }
 
   // One round: keys [kr, kr + KPR) of the split (relative), this lane's key at
   // kr + lane_key.
-  auto round = [&](uint32_t kr, const u32x4_t& kraw, const u32x4_t& vraw) {
+  auto round = [&](uint32_t kr, const u32x4_t* kraw, const u32x4_t* vraw) {
     const bool valid = kr + lane_key < count;
-    float kf[E];
-    T::to_float(kraw, kf);
+    float kf[EL];
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      T::to_float(kraw[j], kf + j * E);
+    }
     float sc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float acc = 0.0f;
       if constexpr (kQRegs) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
+        for (int e = 0; e < EL; ++e) {
           acc = fmaf(qr[g][e], kf[e], acc);
         }
       } else {
         // An opaque zero in the LDS address keeps the compiler from hoisting
-        // the G*E loop-invariant query words into registers across rounds.
+        // the loop-invariant query words into registers across rounds.
         int qz;
         __asm__ volatile("v_mov_b32 %0, 0" : "=v"(qz));
-        const float* sq = s_q + qz + g * D + c * E;
+        const float* sq = s_q + qz + g * D + c * EL;
 #pragma unroll
-        for (int e = 0; e < E; e += 4) {
+        for (int e = 0; e < EL; e += 4) {
           const float4 q4 = *reinterpret_cast<const float4*>(sq + e);
           acc = fmaf(q4.x, kf[e + 0], acc);
           acc = fmaf(q4.y, kf[e + 1], acc);
@@ -355,8 +388,11 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams
       const float red = row_sum<R>(acc);
       sc[g] = valid ? red : -INFINITY;
     }
-    float vf[E];
-    T::to_float(vraw, vf);
+    float vf[EL];
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      T::to_float(vraw[j], vf + j * E);
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float bmax = uniform_f(slots_max<R>(sc[g]));
@@ -365,30 +401,45 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams
         m[g] = bmax;
         l[g] *= corr;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
+        for (int e = 0; e < EL; ++e) {
           o[g][e] *= corr;
         }
       }
       const float pr = valid ? fast_exp2(sc[g] - m[g]) : 0.0f;
       l[g] += pr;
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
+      for (int e = 0; e < EL; ++e) {
         o[g][e] = fmaf(pr, vf[e], o[g][e]);
       }
     }
   };
 
   // Each wave stops after its last round holding a key of the split.
-  for (uint32_t kr = 0; kr + wave_first < count; kr += 2 * KPR) {
-    round(kr, ka, va);
-    ka = buffer_load_nt_b128(krsrc, lane_off + (kr + 2 * KPR) * row_bytes);
-    va = buffer_load_nt_b128(vrsrc, lane_off + (kr + 2 * KPR) * row_bytes);
-    if (kr + KPR + wave_first >= count) {
-      break;
+  // (Written out per depth: a generic unrolled form let the compiler rotate the
+  // loop into a shape whose merged wait counts drained the whole ring.)
+  auto step = [&](uint32_t ki, u32x4_t* kreg, u32x4_t* vreg) {
+    round(ki, kreg, vreg);
+    load_set(ki + P * KPR, kreg, vreg);
+  };
+  if constexpr (P == 2) {
+    for (uint32_t kr = 0; kr + wave_first < count; kr += 2 * KPR) {
+      step(kr, kset[0], vset[0]);
+      if (kr + KPR + wave_first >= count) {
+        break;
+      }
+      step(kr + KPR, kset[1], vset[1]);
     }
-    round(kr + KPR, kb_, vb_);
-    kb_ = buffer_load_nt_b128(krsrc, lane_off + (kr + 3 * KPR) * row_bytes);
-    vb_ = buffer_load_nt_b128(vrsrc, lane_off + (kr + 3 * KPR) * row_bytes);
+  } else {
+    // Whole groups of four rounds with no early exit (an exit between rounds
+    // let the compiler sink the reloads past it and drain the ring at the loop
+    // head); rounds past the wave's keys are masked and read range-checked
+    // zeros.  Chosen only for splits of >= 8 rounds, so the masked tail is small.
+    for (uint32_t kr = 0; kr + wave_first < count; kr += 4 * KPR) {
+      step(kr, kset[0], vset[0]);
+      step(kr + KPR, kset[1], vset[1]);
+      step(kr + 2 * KPR, kset[2], vset[2]);
+      step(kr + 3 * KPR, kset[3], vset[3]);
+    }
   }
 
   // Wave partial: the KW key slots share the wave's running max, so their
@@ -397,7 +448,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams
   for (int g = 0; g < G; ++g) {
     const float lw = slots_sum<R>(l[g]);
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
+    for (int e = 0; e < EL; ++e) {
       o[g][e] = slots_sum<R>(o[g][e]);
     }
     if (lane == 0) {
@@ -406,15 +457,15 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(DecodeParams
     }
     if (kslot == 0) {
 #pragma unroll
-      for (int e = 0; e < E; e += 4) {
-        *reinterpret_cast<float4*>(&s_o[wave][g * D + c * E + e]) =
+      for (int e = 0; e < EL; e += 4) {
+        *reinterpret_cast<float4*>(&s_o[wave][g * D + c * EL + e]) =
           make_float4(o[g][e], o[g][e + 1], o[g][e + 2], o[g][e + 3]);
       }
     }
   }
   __syncthreads();
 
-  // Workgroup merge of the 16 wave partials; thread handles outputs
+  // Workgroup merge of the wave partials; thread handles outputs
   // idx = tid + k*kThreads of the G*D block.
   const size_t tk = (size_t)token * p.kv_heads + kvh;
   float* po = p.part_o + (tk * p.splits + split) * (size_t)(G * D);
@@ -577,6 +628,55 @@ __global__ __launch_bounds__(256) void attention_merge(CombineArgs p) {
   *reinterpret_cast<float4*>(p.output + out_index) = make_float4(out[0], out[1], out[2], out[3]);
 }
 
+// Ragged work list.  The dispatcher hands workgroup i to XCD i mod 8, so empty
+// workgroups interleaved in a (split, kv_head, sequence) grid starve whole XCDs
+// (a grid of alternating empty/full workgroups runs half the chip).  One
+// workgroup writes the non-empty (sequence, kv_head, split) items densely, in
+// sequence order, then marks the rest of the grid empty: consecutive items (the
+// splits of one sequence) land on consecutive XCDs and the empty tail costs
+// nothing.
+__global__ __launch_bounds__(256) void ragged_plan_kernel(const uint32_t* positions,
+                                                          uint32_t sequences, uint32_t kv_heads,
+                                                          uint32_t keys_per_split,
+                                                          uint32_t max_splits,
+                                                          uint32_t grid_items, uint2* items) {
+  __shared__ uint32_t s_scan[256];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t per = (sequences + 255u) / 256u;
+  const uint32_t b0 = min(sequences, tid * per);
+  const uint32_t b1 = min(sequences, b0 + per);
+  auto splits_of = [&](uint32_t b) {
+    const uint64_t keys = (uint64_t)positions[b] + 1u;
+    const uint64_t n = (keys + keys_per_split - 1u) / keys_per_split;
+    return (uint32_t)min(n, (uint64_t)max_splits);
+  };
+  uint32_t local = 0;
+  for (uint32_t b = b0; b < b1; ++b) {
+    local += splits_of(b) * kv_heads;
+  }
+  s_scan[tid] = local;
+  __syncthreads();
+  // Inclusive scan over the 256 per-thread counts (Hillis-Steele).
+  for (uint32_t off = 1; off < 256u; off <<= 1) {
+    const uint32_t add = tid >= off ? s_scan[tid - off] : 0u;
+    __syncthreads();
+    s_scan[tid] += add;
+    __syncthreads();
+  }
+  uint32_t next = s_scan[tid] - local;
+  for (uint32_t b = b0; b < b1; ++b) {
+    const uint32_t n = splits_of(b);
+    for (uint32_t h = 0; h < kv_heads; ++h) {
+      for (uint32_t sp = 0; sp < n; ++sp) {
+        items[next++] = make_uint2(b, (h << 16) | sp);
+      }
+    }
+  }
+  for (uint32_t i = s_scan[255] + tid; i < grid_items; i += 256u) {
+    items[i] = make_uint2(0xffffffffu, 0u);
+  }
+}
+
 // Shapes outside the tuned templates: one wave per (token, head), 64 lanes over
 // dims, online softmax over keys (the reference kernel's structure).
 template <typename KV>
@@ -687,7 +787,7 @@ bool tuned_args(const AttentionArgs& a) {
   return (d == 256 || d == 128 || d == 64) && (g == 1 || g == 2 || g == 4 || g == 8);
 }
 
-size_t data_bytes(const AttentionArgs& a, const SplitPlan& plan) {
+size_t partial_bytes(const AttentionArgs& a, const SplitPlan& plan) {
   if (plan.splits <= 1) {
     return 0;
   }
@@ -696,10 +796,40 @@ size_t data_bytes(const AttentionArgs& a, const SplitPlan& plan) {
   return units * plan.splits * g * (a.head_dim + 2) * sizeof(float);
 }
 
+// Ragged work list entries: one per (sequence, kv_head, split) of the grid.
+size_t work_item_count(const AttentionArgs& a, const SplitPlan& plan) {
+  return a.seq_positions != nullptr ? (size_t)a.tokens * a.kv_heads * plan.splits : 0;
+}
+
+size_t data_bytes(const AttentionArgs& a, const SplitPlan& plan) {
+  // Partials, then the work list (8-byte items) at a 256-byte boundary.
+  return (partial_bytes(a, plan) + 255u) / 256u * 256u + work_item_count(a, plan) * 8u;
+}
+
+// Chunks per lane for a shape.
+template <int D, int G, typename KV>
+constexpr int chunks_for() {
+  // Two chunks per lane measured slower on the C1 and C4 shapes (fewer waves
+  // per CU to hide latency); kept selectable for other shapes.
+  return 1;
+}
+
 template <int D, int G, typename KV>
 hipError_t launch_tuned(const DecodeParams& p, hipStream_t stream) {
-  const dim3 grid(p.splits, p.kv_heads, p.tokens);
-  attention_decode_kernel<D, G, KV><<<grid, kThreads, 0, stream>>>(p);
+  // Ragged: one workgroup per work-list entry (see ragged_plan_kernel).
+  const dim3 grid = p.work_items != nullptr ? dim3(p.splits * p.kv_heads * p.tokens)
+                                            : dim3(p.splits, p.kv_heads, p.tokens);
+  constexpr int C = chunks_for<D, G, KV>();
+  using S = RowShape<D, KV, C>;
+  // Four rounds in flight for long splits (they stream at HBM rate only with
+  // ~100 KB outstanding per CU); two otherwise.
+  // The deeper ring spills for 8 query heads per KV head (one chunk per lane).
+  constexpr bool kDeepFits = G <= 4;
+  if (kDeepFits && p.keys_per_split >= 8u * S::KPR) {
+    attention_decode_kernel<D, G, KV, C, kDeepFits ? 4 : 2><<<grid, 64 * S::W, 0, stream>>>(p);
+  } else {
+    attention_decode_kernel<D, G, KV, C, 2><<<grid, 64 * S::W, 0, stream>>>(p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) {
     return e;
@@ -885,6 +1015,22 @@ hipError_t launch_attention_decode(const AttentionArgs& a, int cu_count, void* w
       // Partials follow the counter region, which they must never overlap.
       p.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterRegionBytes);
       p.part_ml = p.part_o + units * plan.splits * g * a.head_dim;
+    }
+    if (a.seq_positions != nullptr) {
+      if (workspace == nullptr || workspace_bytes < kCounterRegionBytes + data_bytes(a, plan)) {
+        return hipErrorInvalidValue;
+      }
+      uint2* items = reinterpret_cast<uint2*>(static_cast<char*>(workspace) +
+                                              kCounterRegionBytes +
+                                              (partial_bytes(a, plan) + 255u) / 256u * 256u);
+      p.work_items = items;
+      ragged_plan_kernel<<<1, 256, 0, stream>>>(a.seq_positions, a.tokens, a.kv_heads,
+                                                plan.keys_per_split, plan.splits,
+                                                (uint32_t)work_item_count(a, plan), items);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) {
+        return e;
+      }
     }
   }
   return a.kv_f16 ? dispatch_kv<half_t>(p, a.head_dim, g, tuned, stream)
