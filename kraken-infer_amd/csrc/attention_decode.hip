@@ -102,21 +102,19 @@ struct KvTraits<float> {
 
 __device__ __forceinline__ float sigmoidf_acc(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Lane geometry of a key row: a lane holds C consecutive 16-byte chunks of E
-// elements (EL = E*C elements), R = D/EL lanes span a row, a wave takes
-// KW = 64/R keys per round, a workgroup of W = 16/C waves takes KPR = W*KW.
-// More chunks per lane amortise the per-key cross-lane reductions and softmax
-// bookkeeping over more FMAs; the workgroup shrinks so the larger per-lane
-// query and accumulator slices fit the register file.
-template <int D, typename KV, int C>
+// Lane geometry of a key row: a lane holds one 16-byte chunk of E elements
+// (EL = E), R = D/E lanes span a row, a wave takes KW = 64/R keys per round, a
+// workgroup of W = 16 waves takes KPR = W*KW.  (Two chunks per lane in 8-wave
+// workgroups, and a four-deep prefetch ring, both measured slower on the C1
+// and C4 shapes once the ragged grid keeps every XCD busy.)
+template <int D, typename KV>
 struct RowShape {
   static constexpr int E = KvTraits<KV>::kPerChunk;
-  static constexpr int EL = E * C;
+  static constexpr int EL = E;
   static constexpr int R = D / EL;
   static constexpr int KW = 64 / R;
-  static constexpr int W = 16 / C;
+  static constexpr int W = 16;
   static constexpr int KPR = W * KW;
-  static_assert(C == 1 || C == 2, "one or two chunks per lane");
   static_assert(R >= 8 && R <= 64 && 64 % R == 0, "row must span 8..64 lanes");
 };
 
@@ -190,12 +188,13 @@ __device__ __forceinline__ float uniform_f(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, x)));
 }
 
-template <int D, int G, typename KV, int C, int P>
-__global__ __launch_bounds__((64 * RowShape<D, KV, C>::W)) void attention_decode_kernel(
+template <int D, int G, typename KV>
+__global__ __launch_bounds__((64 * RowShape<D, KV>::W)) void attention_decode_kernel(
   DecodeParams p) {
-  static_assert(P == 2 || P == 4, "prefetch depth 2 or 4");
+  constexpr int C = 1;  // 16-byte chunks per lane
+  constexpr int P = 2;  // rounds in flight (ring depth)
   using T = KvTraits<KV>;
-  using S = RowShape<D, KV, C>;
+  using S = RowShape<D, KV>;
   constexpr int E = S::E;
   constexpr int EL = S::EL;
   constexpr int R = S::R;
@@ -414,32 +413,19 @@ __global__ __launch_bounds__((64 * RowShape<D, KV, C>::W)) void attention_decode
     }
   };
 
-  // Each wave stops after its last round holding a key of the split.
-  // (Written out per depth: a generic unrolled form let the compiler rotate the
-  // loop into a shape whose merged wait counts drained the whole ring.)
+  // Each wave stops after its last round holding a key of the split.  Written
+  // as an explicit two-step body: exits leave the loop directly, so the
+  // compiler's wait counts stay exact (a round waits only for its own set).
   auto step = [&](uint32_t ki, u32x4_t* kreg, u32x4_t* vreg) {
     round(ki, kreg, vreg);
     load_set(ki + P * KPR, kreg, vreg);
   };
-  if constexpr (P == 2) {
-    for (uint32_t kr = 0; kr + wave_first < count; kr += 2 * KPR) {
-      step(kr, kset[0], vset[0]);
-      if (kr + KPR + wave_first >= count) {
-        break;
-      }
-      step(kr + KPR, kset[1], vset[1]);
+  for (uint32_t kr = 0; kr + wave_first < count; kr += 2 * KPR) {
+    step(kr, kset[0], vset[0]);
+    if (kr + KPR + wave_first >= count) {
+      break;
     }
-  } else {
-    // Whole groups of four rounds with no early exit (an exit between rounds
-    // let the compiler sink the reloads past it and drain the ring at the loop
-    // head); rounds past the wave's keys are masked and read range-checked
-    // zeros.  Chosen only for splits of >= 8 rounds, so the masked tail is small.
-    for (uint32_t kr = 0; kr + wave_first < count; kr += 4 * KPR) {
-      step(kr, kset[0], vset[0]);
-      step(kr + KPR, kset[1], vset[1]);
-      step(kr + 2 * KPR, kset[2], vset[2]);
-      step(kr + 3 * KPR, kset[3], vset[3]);
-    }
+    step(kr + KPR, kset[1], vset[1]);
   }
 
   // Wave partial: the KW key slots share the wave's running max, so their
@@ -806,30 +792,12 @@ size_t data_bytes(const AttentionArgs& a, const SplitPlan& plan) {
   return (partial_bytes(a, plan) + 255u) / 256u * 256u + work_item_count(a, plan) * 8u;
 }
 
-// Chunks per lane for a shape.
-template <int D, int G, typename KV>
-constexpr int chunks_for() {
-  // Two chunks per lane measured slower on the C1 and C4 shapes (fewer waves
-  // per CU to hide latency); kept selectable for other shapes.
-  return 1;
-}
-
 template <int D, int G, typename KV>
 hipError_t launch_tuned(const DecodeParams& p, hipStream_t stream) {
   // Ragged: one workgroup per work-list entry (see ragged_plan_kernel).
   const dim3 grid = p.work_items != nullptr ? dim3(p.splits * p.kv_heads * p.tokens)
                                             : dim3(p.splits, p.kv_heads, p.tokens);
-  constexpr int C = chunks_for<D, G, KV>();
-  using S = RowShape<D, KV, C>;
-  // Four rounds in flight for long splits (they stream at HBM rate only with
-  // ~100 KB outstanding per CU); two otherwise.
-  // The deeper ring spills for 8 query heads per KV head (one chunk per lane).
-  constexpr bool kDeepFits = G <= 4;
-  if (kDeepFits && p.keys_per_split >= 8u * S::KPR) {
-    attention_decode_kernel<D, G, KV, C, kDeepFits ? 4 : 2><<<grid, 64 * S::W, 0, stream>>>(p);
-  } else {
-    attention_decode_kernel<D, G, KV, C, 2><<<grid, 64 * S::W, 0, stream>>>(p);
-  }
+  attention_decode_kernel<D, G, KV><<<grid, 64 * RowShape<D, KV>::W, 0, stream>>>(p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) {
     return e;

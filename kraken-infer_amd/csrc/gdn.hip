@@ -146,11 +146,115 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnParams p) {
   }
 }
 
+// One token per state (decode: a single sequence with tokens == 1, or ragged
+// decode with one token per sequence, blockIdx.z = sequence), head_dim 128.
+// The recurrence step of gdn_recurrent_kernel for T = 1, laid out to stream the
+// state: a 32-lane group owns RPL state rows (4 columns = one 16-byte vector per
+// lane per row), a workgroup 8 groups = 8*RPL rows.  Shapes are exact (no
+// bounds branches) and every load is a 16-byte vector issued before any math,
+// so each lane has RPL*16 bytes of state in flight; the RPL row reductions
+// interleave.  The host checks 16-byte alignment of q/k/v/state; ragged state
+// offsets must be multiples of 4 elements (others are skipped like offsets
+// outside the pool).
+template <bool kPrepare, int RPL>
+__global__ __launch_bounds__(256) void gdn_decode_kernel(GdnParams p) {
+  constexpr uint32_t D = 128;
+  constexpr int CPL = 4;
+  const int lane = threadIdx.x & 63;
+  const int grp = threadIdx.x >> 5;  // 8 groups of 32 lanes
+  const uint32_t h = blockIdx.y;
+  const uint32_t row0 = (blockIdx.x * 8u + grp) * RPL;
+  const uint32_t col0 = (uint32_t)(lane & 31) * CPL;
+  const uint32_t kh = h % p.key_heads;
+
+  float* state = p.state;
+  uint32_t t = 0;
+  if (p.seq_state_offsets != nullptr) {
+    const uint32_t seq = blockIdx.z;
+    const uint64_t off = p.seq_state_offsets[seq];
+    if ((off & 3u) != 0 || off > p.pool_elems ||
+        p.pool_elems - off < (uint64_t)p.value_heads * D * D) {
+      return;  // misaligned or outside the pool: this sequence is skipped, nothing touched
+    }
+    state += off;
+    t = seq;
+  }
+  float* shead = state + (size_t)h * D * D;
+
+  float4 s[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    s[j] = *reinterpret_cast<const float4*>(shead + (size_t)(row0 + j) * D + col0);
+  }
+  const float4 k = *reinterpret_cast<const float4*>(p.key + ((size_t)t * p.key_heads + kh) * D +
+                                                    col0);
+  const float4 q = *reinterpret_cast<const float4*>(
+    p.query + ((size_t)t * p.key_heads + kh) * D + col0);
+  const float4 v4 =
+    *reinterpret_cast<const float4*>(p.value + ((size_t)t * p.value_heads + h) * D + row0);
+  const size_t gi = (size_t)t * p.value_heads + h;
+  float g = p.gate[gi];
+  float b = p.beta[gi];
+  if (kPrepare) {
+    g = softplus_ref(g + p.dt_bias[h]) * p.ssm_a[h];
+    b = 1.0f / (1.0f + expf(-b));
+  }
+  const float decay = expf(g);
+  const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+
+  float sk[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    s[j].x *= decay;
+    s[j].y *= decay;
+    s[j].z *= decay;
+    s[j].w *= decay;
+    sk[j] = fmaf(s[j].x, k.x, fmaf(s[j].y, k.y, fmaf(s[j].z, k.z, s[j].w * k.w)));
+  }
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    sk[j] = reduce32_sum(sk[j]);
+  }
+  float y[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    const float delta = (v[j] - sk[j]) * b;
+    s[j].x = fmaf(k.x, delta, s[j].x);
+    s[j].y = fmaf(k.y, delta, s[j].y);
+    s[j].z = fmaf(k.z, delta, s[j].z);
+    s[j].w = fmaf(k.w, delta, s[j].w);
+    y[j] = fmaf(s[j].x, q.x, fmaf(s[j].y, q.y, fmaf(s[j].z, q.z, s[j].w * q.w)));
+  }
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    y[j] = reduce32_sum(y[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    *reinterpret_cast<float4*>(shead + (size_t)(row0 + j) * D + col0) = s[j];
+  }
+  // Lanes 0..RPL-1 of the group write the RPL outputs (one 16-byte store).
+  if ((lane & 31) == 0) {
+    *reinterpret_cast<float4*>(p.output + ((size_t)t * p.value_heads + h) * D + row0) =
+      make_float4(y[0] * p.scale, y[1] * p.scale, y[2] * p.scale, y[3] * p.scale);
+  }
+}
+
 template <bool kPrepare>
 hipError_t launch_gdn_cpl(const GdnParams& p, hipStream_t stream) {
+  const bool one_token = p.seq_state_offsets != nullptr || p.tokens == 1;
+  const uint32_t cpl = (p.head_dim + 31) / 32;
+  const bool aligned = ((uintptr_t)p.query | (uintptr_t)p.key | (uintptr_t)p.value |
+                        (uintptr_t)p.state | (uintptr_t)p.output) % 16u == 0;
+  if (one_token && p.head_dim == 128 && aligned) {
+    constexpr int kRpl = 4;
+    const dim3 grid(128 / (8 * kRpl), p.value_heads,
+                    p.seq_state_offsets != nullptr ? p.tokens : 1u);
+    gdn_decode_kernel<kPrepare, kRpl><<<grid, 256, 0, stream>>>(p);
+    return hipGetLastError();
+  }
   const dim3 grid((p.head_dim + kGdnRowsPerBlock - 1) / kGdnRowsPerBlock, p.value_heads,
                   p.seq_state_offsets != nullptr ? p.tokens : 1u);
-  const uint32_t cpl = (p.head_dim + 31) / 32;
   if (cpl <= 1) {
     gdn_recurrent_kernel<1, kPrepare><<<grid, 256, 0, stream>>>(p);
   } else if (cpl <= 2) {
