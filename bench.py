@@ -410,6 +410,9 @@ def main():
     ap.add_argument("--kv-len", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline only, no details")
+    ap.add_argument("--sections", default="decode,prefill,gdn,c4",
+                    help="comma-separated detail sections to run after the headline "
+                         "(decode, prefill, gdn, c4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run torch copies of MIB MiB (20 launches), the known-size "
@@ -444,20 +447,24 @@ def main():
         head = bench_decode(torch, ctx, run, args.kv_len, args.steps, args.warmup, True, gen)
         progress(f"decode L={args.kv_len} cold: {head['GB_s']:.0f} GB/s")
         details = {"decode_c1": [head]}
-        if not args.quick:
+        sections = set() if args.quick else set(args.sections.split(","))
+        if "decode" in sections:
             for kv in (1024, 8192, 16384):
                 details["decode_c1"].append(bench_decode(torch, ctx, run, kv, 400, 10, True, gen))
             for kv in (1024, 4096, 16384):
                 details["decode_c1"].append(bench_decode(torch, ctx, run, kv, 400, 10, False,
                                                          gen))
             progress("decode details done")
+        if "prefill" in sections:
             gen.manual_seed(2)
             details["prefill_c2"] = [bench_prefill(torch, ctx, run, p, 10, 2, gen)
                                      for p in (0, 3072, 7168)]
             progress("prefill done")
+        if "gdn" in sections:
             gen.manual_seed(3)
             details["gdn_c3"] = bench_gdn(torch, ctx, run, gen)
             progress("gdn done")
+        if "c4" in sections:
             gen.manual_seed(4)
             details["ragged_c4"] = bench_c4(torch, ctx, run, gen)
             progress("ragged c4 done")

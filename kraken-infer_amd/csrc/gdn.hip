@@ -16,11 +16,22 @@
 // (prepare_qwen35_gdn_gate_beta_f32, mps_backend.mm:2588-2605) on the fly.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+#include <cstring>
+
 #include "context_internal.hpp"
 #include "device_common.hpp"
 
 namespace kraken {
 namespace {
+
+// KRAKEN_GDN_PREFILL=generic selects the generic recurrence kernel for
+// multi-token calls (the LDS-staged head_dim-128 kernel is the default); used to
+// compare the two on the same inputs.
+bool gdn_prefill_disabled() {
+  const char* v = std::getenv("KRAKEN_GDN_PREFILL");
+  return v != nullptr && std::strcmp(v, "generic") == 0;
+}
 
 constexpr int kGdnRowsPerBlock = 8;  // 4 waves x 2 rows
 
@@ -240,12 +251,175 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnParams p) {
   }
 }
 
+// Sum over the 32 lanes of each wave half, VALU only: DPP within each 16-lane
+// row, then v_permlane16_swap across the two rows of the half.
+__device__ __forceinline__ float half_sum32(float x) {
+  x += dpp<kDppQuadXor1>(x);
+  x += dpp<kDppQuadXor2>(x);
+  x += dpp<kDppRowHalfMirror>(x);
+  x += dpp<kDppRowMirror>(x);
+  return xor16_sum(x);
+}
+
+// Multi-token (prefill) form of the recurrence for head_dim 128.  Same lane
+// layout as gdn_recurrent_kernel (32 lanes own one state row, one 16-byte
+// vector of 4 columns per lane; a workgroup = 4 waves = 8 rows of one head,
+// 16 workgroups per head), but the per-token inputs come from LDS: the
+// workgroup stages kGdnChunk tokens of k, q (the whole 128-wide rows), its 8
+// values of v, and the per-token decay exp(g) and beta (prepared once per token
+// here rather than per lane) into one of two LDS buffers while the other is
+// consumed, so no token waits on global memory.  The per-token arithmetic is
+// the reference's, in its order: S *= exp(g); sk = S.k; delta = (v - sk) beta;
+// S += k delta; y = S.q / sqrt(D).  The host checks 16-byte alignment of
+// q/k/v/state and value_heads * 128 % 4 == 0 (always true for D = 128).
+constexpr int kGdnChunk = 64;
+
+template <bool kPrepare>
+__global__ __launch_bounds__(256) void gdn_prefill_kernel(GdnParams p) {
+  constexpr uint32_t D = 128;
+  constexpr int TC = kGdnChunk;
+  constexpr int kRows = 8;
+  __shared__ float4 s_k[2][TC][D / 4];
+  __shared__ float4 s_q[2][TC][D / 4];
+  __shared__ float s_v[2][TC][kRows];
+  __shared__ float s_decay[2][TC];
+  __shared__ float s_beta[2][TC];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int lrow = (tid >> 6) * 2 + (lane >> 5);  // local row 0..7
+  const int c4 = lane & 31;                        // columns 4*c4 .. 4*c4+3
+  const uint32_t h = blockIdx.y;
+  const uint32_t row0 = blockIdx.x * kRows;
+  const uint32_t row = row0 + lrow;
+  const uint32_t kh = h % p.key_heads;
+  const uint32_t tokens = p.tokens;
+  const uint32_t chunks = (tokens + TC - 1) / TC;
+
+  float* srow = p.state + ((size_t)h * D + row) * D + 4 * c4;
+  float4 s = *reinterpret_cast<const float4*>(srow);
+
+  // Staging registers for one chunk: thread tid carries k/q vectors
+  // tid + 256 i (token (tid + 256 i) / 32, vector (tid + 256 i) % 32), v vector
+  // tid < 128 (token tid / 2, rows 4 (tid % 2) ..), and g/beta of token tid - 128
+  // for 128 <= tid < 192.
+  float4 kr[TC * 32 / 256], qr[TC * 32 / 256], vr = make_float4(0, 0, 0, 0);
+  float dr = 0.0f, br = 0.0f;
+  auto load_chunk = [&](uint32_t c) {
+    const uint32_t tb = c * TC;
+    const uint32_t n = min((uint32_t)TC, tokens - tb);
+#pragma unroll
+    for (int i = 0; i < TC * 32 / 256; ++i) {
+      const uint32_t idx = tid + 256u * i;
+      const uint32_t t = idx >> 5;
+      const uint32_t v4 = idx & 31u;
+      const size_t off = ((size_t)(tb + t) * p.key_heads + kh) * D + 4 * v4;
+      kr[i] = t < n ? *reinterpret_cast<const float4*>(p.key + off) : make_float4(0, 0, 0, 0);
+      qr[i] = t < n ? *reinterpret_cast<const float4*>(p.query + off) : make_float4(0, 0, 0, 0);
+    }
+    if (tid < 2 * TC) {
+      const uint32_t t = tid >> 1;
+      if (t < n) {
+        vr = *reinterpret_cast<const float4*>(
+          p.value + ((size_t)(tb + t) * p.value_heads + h) * D + row0 + 4 * (tid & 1));
+      }
+    } else if (tid < 3 * TC) {
+      const uint32_t t = tid - 2 * TC;
+      if (t < n) {
+        const size_t gi = (size_t)(tb + t) * p.value_heads + h;
+        float g = p.gate[gi];
+        float b = p.beta[gi];
+        if (kPrepare) {
+          g = softplus_ref(g + p.dt_bias[h]) * p.ssm_a[h];
+          b = 1.0f / (1.0f + expf(-b));
+        }
+        dr = expf(g);
+        br = b;
+      }
+    }
+  };
+  auto store_chunk = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TC * 32 / 256; ++i) {
+      const uint32_t idx = tid + 256u * i;
+      s_k[buf][idx >> 5][idx & 31u] = kr[i];
+      s_q[buf][idx >> 5][idx & 31u] = qr[i];
+    }
+    if (tid < 2 * TC) {
+      *reinterpret_cast<float4*>(&s_v[buf][tid >> 1][4 * (tid & 1)]) = vr;
+    } else if (tid < 3 * TC) {
+      s_decay[buf][tid - 2 * TC] = dr;
+      s_beta[buf][tid - 2 * TC] = br;
+    }
+  };
+
+  load_chunk(0);
+  store_chunk(0);
+  __syncthreads();
+  for (uint32_t c = 0; c < chunks; ++c) {
+    const int buf = (int)(c & 1u);
+    if (c + 1 < chunks) {
+      load_chunk(c + 1);  // lands while this chunk computes
+    }
+    const uint32_t tb = c * TC;
+    const int n = (int)min((uint32_t)TC, tokens - tb);
+    float* out = p.output + ((size_t)tb * p.value_heads + h) * D + row;
+    const size_t out_stride = (size_t)p.value_heads * D;
+    float4 k = s_k[buf][0][c4];
+    float4 q = s_q[buf][0][c4];
+    float v = s_v[buf][0][lrow];
+    float decay = s_decay[buf][0];
+    float b = s_beta[buf][0];
+    for (int t = 0; t < n; ++t) {
+      // Next token's inputs (clamped at the chunk end) before this token's math.
+      const int tn = t + 1 < n ? t + 1 : t;
+      const float4 k_n = s_k[buf][tn][c4];
+      const float4 q_n = s_q[buf][tn][c4];
+      const float v_n = s_v[buf][tn][lrow];
+      const float decay_n = s_decay[buf][tn];
+      const float b_n = s_beta[buf][tn];
+
+      s.x *= decay;
+      s.y *= decay;
+      s.z *= decay;
+      s.w *= decay;
+      float sk = fmaf(s.w, k.w, fmaf(s.z, k.z, fmaf(s.y, k.y, s.x * k.x)));
+      sk = half_sum32(sk);
+      const float delta = (v - sk) * b;
+      s.x = fmaf(k.x, delta, s.x);
+      s.y = fmaf(k.y, delta, s.y);
+      s.z = fmaf(k.z, delta, s.z);
+      s.w = fmaf(k.w, delta, s.w);
+      float y = fmaf(s.w, q.w, fmaf(s.z, q.z, fmaf(s.y, q.y, s.x * q.x)));
+      y = half_sum32(y);
+      if (c4 == 0) {
+        out[(size_t)t * out_stride] = y * p.scale;
+      }
+      k = k_n;
+      q = q_n;
+      v = v_n;
+      decay = decay_n;
+      b = b_n;
+    }
+    if (c + 1 < chunks) {
+      store_chunk(buf ^ 1);  // buffer buf ^ 1 was last read before the previous barrier
+    }
+    __syncthreads();
+  }
+  *reinterpret_cast<float4*>(srow) = s;
+}
+
 template <bool kPrepare>
 hipError_t launch_gdn_cpl(const GdnParams& p, hipStream_t stream) {
   const bool one_token = p.seq_state_offsets != nullptr || p.tokens == 1;
   const uint32_t cpl = (p.head_dim + 31) / 32;
   const bool aligned = ((uintptr_t)p.query | (uintptr_t)p.key | (uintptr_t)p.value |
                         (uintptr_t)p.state | (uintptr_t)p.output) % 16u == 0;
+  if (!one_token && p.head_dim == 128 && aligned && !gdn_prefill_disabled()) {
+    const dim3 grid(128 / 8, p.value_heads);
+    gdn_prefill_kernel<kPrepare><<<grid, 256, 0, stream>>>(p);
+    return hipGetLastError();
+  }
   if (one_token && p.head_dim == 128 && aligned) {
     constexpr int kRpl = 4;
     const dim3 grid(128 / (8 * kRpl), p.value_heads,

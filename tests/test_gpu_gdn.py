@@ -31,7 +31,8 @@ def gdn_inputs(seed, tokens, hk=16, hv=16, d=128, state_scale=0.0):
 @pytest.mark.parametrize("shape", [
     # tokens, key_heads, value_heads, head_dim
     (1, 16, 16, 128), (7, 16, 16, 128), (64, 2, 4, 128), (33, 1, 3, 64), (5, 2, 2, 40),
-    (9, 1, 1, 256), (3, 4, 8, 96),
+    (9, 1, 1, 256), (3, 4, 8, 96), (2, 16, 16, 128), (65, 16, 16, 128), (130, 2, 6, 128),
+    (200, 16, 16, 128),
 ])
 def test_gdn_shapes(hip_ctx, shape):
     tokens, hk, hv, d = shape
@@ -57,6 +58,41 @@ def test_gdn_state_offset_and_neighbours_untouched(hip_ctx):
     np.testing.assert_allclose(st[off:2 * off], st1, rtol=0, atol=ATOL)
     np.testing.assert_array_equal(st[:off], big[:off])
     np.testing.assert_array_equal(st[2 * off:], big[2 * off:])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("offset_extra", [0, 1])
+def test_gdn_prefill_state_offset_d128(hip_ctx, offset_extra):
+    """head_dim 128 multi-token calls at a state offset: a 16-byte aligned offset
+    takes the LDS-staged prefill kernel, an odd one the generic kernel; both must
+    update exactly their own state block."""
+    tokens, h, d = 97, 4, 128
+    q, k, v, g, b, _ = gdn_inputs(12, tokens, h, h, d)
+    blk = h * d * d
+    big = (0.1 * np.random.default_rng(13).standard_normal(3 * blk + 4)).astype(np.float32)
+    off = blk + offset_extra
+    out, st = kh.NumpyOps(hip_ctx).gated_delta_net(q, k, v, g, b, big, tokens, h, h, d,
+                                                   state_offset=off)
+    out_ref, st1 = oracle.gated_delta_net(q, k, v, g, b, big[off:off + blk], tokens, h, h, d)
+    np.testing.assert_allclose(out, out_ref, rtol=0, atol=ATOL)
+    np.testing.assert_allclose(st[off:off + blk], st1, rtol=0, atol=ATOL)
+    np.testing.assert_array_equal(st[:off], big[:off])
+    np.testing.assert_array_equal(st[off + blk:], big[off + blk:])
+
+
+@pytest.mark.gpu
+def test_gdn_prefill_staged_equals_generic_kernel(hip_ctx, monkeypatch):
+    """The LDS-staged head_dim-128 prefill kernel and the generic recurrence
+    kernel (KRAKEN_GDN_PREFILL=generic) give the same outputs and state."""
+    tokens, hk, hv, d = 257, 16, 16, 128
+    q, k, v, g, b, s = gdn_inputs(14, tokens, hk, hv, d, state_scale=0.1)
+    ops = kh.NumpyOps(hip_ctx)
+    out_a, st_a = ops.gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
+    monkeypatch.setenv("KRAKEN_GDN_PREFILL", "generic")
+    out_b, st_b = ops.gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
+    monkeypatch.delenv("KRAKEN_GDN_PREFILL")
+    np.testing.assert_allclose(out_a, out_b, rtol=0, atol=1e-5)
+    np.testing.assert_allclose(st_a, st_b, rtol=0, atol=1e-5)
 
 
 @pytest.mark.gpu
