@@ -156,6 +156,25 @@ def test_flash_prefill_vs_oracle(hip_ctx, shape):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("q_scale,splits", [(8.0, None), (30.0, None), (8.0, "1"), (8.0, "3")])
+def test_flash_sharp_softmax_and_split_counts(hip_ctx, q_scale, splits, monkeypatch):
+    """Scaled queries make the running max jump by far more than the lazy-rescale
+    slack many times along the key axis; forced split counts move the split
+    boundaries (KRAKEN_FLASH_SPLITS)."""
+    tokens, start, heads, kv_heads, d = 160, 300, 8, 2, 256
+    cap = start + tokens
+    if splits is not None:
+        monkeypatch.setenv("KRAKEN_FLASH_SPLITS", splits)
+    print(f"flash sharp q_scale={q_scale} splits={splits}", flush=True)
+    q, kc, vc = make_case(21, tokens, start, cap, heads, kv_heads, d)
+    q = (q * q_scale).astype(np.float16).astype(np.float32)
+    got = run_hip(hip_ctx, q, kc, vc, 0, start, tokens, cap, heads, kv_heads, d)
+    ref = oracle.attention_batched(q, kc, vc, 0, start, tokens, cap, heads, kv_heads, d,
+                                   round_query_f16=True)
+    close(got, ref, msg=f"q_scale={q_scale} splits={splits}")
+
+
+@pytest.mark.gpu
 def test_flash_gated(hip_ctx):
     tokens, start, heads, kv_heads, d = 128, 200, 8, 2, 256
     cap = start + tokens
