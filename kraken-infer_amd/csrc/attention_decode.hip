@@ -917,6 +917,8 @@ hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream) {
     const dim3 grid((uint32_t)((threads + 255) / 256));
     if (c.splits <= 4) {
       attention_merge_narrow<4><<<grid, 256, 0, stream>>>(c);
+    } else if (c.splits <= 8) {
+      attention_merge_narrow<8><<<grid, 256, 0, stream>>>(c);
     } else {
       attention_merge_narrow<16><<<grid, 256, 0, stream>>>(c);
     }
