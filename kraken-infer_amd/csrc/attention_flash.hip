@@ -11,30 +11,26 @@
 //
 // Layout of the work (gfx950, wave64):
 //  * A workgroup takes one KV head, up to four query heads of its GQA group
-//    ("head slots"), a tile of 32 query tokens and a key split.  It has two
-//    waves per head slot, so a CU runs one workgroup of 8 waves, two per SIMD.
-//    Wave dh of a pair computes the scores of keys 32 dh .. 32 dh + 31 of every
-//    64-key tile and accumulates output dims 128 dh .. 128 dh + 127 over all 64
-//    keys: the pair swaps its tile maxima and its P halves through LDS.  The
-//    split of O by dims keeps each wave within the 256 registers that two waves
-//    per SIMD allow (Q 64 + O 64 + scores and P 32, with room for the fragment
-//    read pipeline); both waves of a pair make the same softmax decisions from
-//    the same maxima, so they share one reference max per query.
-//  * K/V tiles are copied global -> LDS by the gfx950 direct-to-LDS buffer loads
-//    (buffer_load_dwordx4 ... lds), double-buffered: the next tile's copy is in
-//    flight while the current one is consumed, and no register holds staging
-//    data.  Rows stay in their row-major layout (512 bytes per key); the 16-byte
-//    chunks of each row are XOR-swizzled (K by row % 16, V by 4 * (row % 4)) by
-//    choosing which global chunk each lane fetches, which keeps the fragment
-//    reads below free of bank conflicts.
-//  * Per tile a wave computes S^T = K Q^T for its 32 keys (keys x queries, one
-//    32x32 MFMA tile over 16 k-steps of 16 dims; lane l owns query column l%32).
-//    The accumulator's registers are already the B operand of the next product,
-//    O^T = V^T P^T (dims x queries, 4 tiles of 32 dims, 4 k-steps of 16 keys): a
-//    lane's P values are the B operand as they stand, and the partner's P comes
-//    from the same lane of the partner, so P never moves between lanes.  The V^T
-//    operand comes straight from the row-major V tile through the gfx950
-//    transposing LDS read ds_read_b64_tr_b16.
+//    ("head slots"), a tile of 32 query tokens and a key split: one wave per
+//    head slot, one workgroup (128 KB of LDS) per CU, so each wave owns a SIMD
+//    and its 512 registers (Q 64, O 128, two score tiles 64, P 16, fragment read
+//    pipelines).
+//  * K and V tiles (64 keys) are copied global -> LDS by the gfx950
+//    direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds), double buffered:
+//    at the top of iteration t the copies of tile t+1 are issued, so every copy
+//    has a whole iteration to land and no register holds staging data.  Rows stay row-major (512 bytes per key); the 16-byte chunks
+//    of each row are XOR-swizzled (K by row % 16, V by 4 * (row % 4)) by choosing
+//    which global chunk each lane fetches, which keeps the fragment reads below
+//    free of bank conflicts.  One barrier per tile publishes the copies.
+//  * Per tile a wave computes S^T = K Q^T, the softmax, then PV; the LDS
+//    fragment reads of both products run several MFMAs ahead through explicit
+//    register rings so that LDS latency stays off the MFMA issue.  S^T per 32 keys
+//    (keys x queries, one 32x32 MFMA tile over 16 k-steps of 16 dims; lane l
+//    owns query column l%32).  The accumulator's registers are already the B
+//    operand of O^T = V^T P^T (dims x queries, 8 tiles of 32 dims, 4 k-steps of
+//    16 keys), so P never moves between lanes.  The V^T operand comes straight
+//    from the row-major V tile through the transposing LDS read
+//    ds_read_b64_tr_b16.
 //  * Lazy rescale: scores live in the log2 domain with the 1/sqrt(D) scale
 //    folded into the exp2 argument; a query's reference max moves (and O, l are
 //    rescaled) only when a tile's max exceeds it by more than 8, so P <= 2^8.
@@ -105,24 +101,25 @@ __device__ __forceinline__ float sigmoid_acc(float x) { return 1.0f / (1.0f + ex
 // Row of C (32x32 accumulator) held in register r by a lane in half h.
 __device__ __forceinline__ int c_row(int r, int h) { return (r >> 2) * 8 + h * 4 + (r & 3); }
 
-// Scheduling constraint for a run of N (LDS fragment reads, MFMA) groups: the
-// first kLookahead groups of reads, then one MFMA per group, then the last
-// MFMAs.  Keeps kLookahead fragments in flight instead of all N
-// (sched_group_barrier masks: 0x008 MFMA, 0x100 LDS read).
-template <int N, int kLookahead, int kReadsPerMfma>
-__device__ __forceinline__ void pipeline_reads_and_mfma() {
+// Scheduling constraints (sched_group_barrier masks: 0x002 VALU, 0x008 MFMA,
+// 0x100 LDS read, 0x400 transcendental).  A run of N MFMAs, each fed by
+// kReadsPerMfma LDS fragment reads issued kLookahead MFMAs ahead, with up to
+// kValuPerMfma VALU instructions placed after each MFMA.
+template <int N, int kLookahead, int kReadsPerMfma, int kValuPerMfma>
+__device__ __forceinline__ void pipeline_mfma() {
 #pragma unroll
   for (int i = 0; i < kLookahead; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x100, kReadsPerMfma, 0);
   }
 #pragma unroll
-  for (int i = 0; i < N - kLookahead; ++i) {
+  for (int i = 0; i < N; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, kReadsPerMfma, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < kLookahead; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (i + kLookahead < N) {
+      __builtin_amdgcn_sched_group_barrier(0x100, kReadsPerMfma, 0);
+    }
+    if (kValuPerMfma > 0) {
+      __builtin_amdgcn_sched_group_barrier(0x402, kValuPerMfma, 0);
+    }
   }
 }
 
@@ -145,7 +142,11 @@ __device__ __forceinline__ i32x4_t rsrc_words(const void* base, uint32_t bytes) 
 // not make every later LDS read wait for it (it cannot tell the copy's target
 // from the stage being read); completion is awaited explicitly by
 // wait_tile_copies() before the barrier that publishes a stage.  M0 is set in the
-// same statement, with the one wait state the M0 -> LDS-DMA hazard needs.
+// same statement, with the one wait state the M0 -> LDS-DMA hazard needs; the
+// kernel has no other M0 user (checked in its ISA), so declaring the reserved
+// register clobbered is safe here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t voffset, const half_t* lds) {
   const uint32_t m0 =
     __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds);
@@ -154,25 +155,56 @@ __device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t voffset, co
                : "s"(m0), "v"(voffset), "s"(rsrc)
                : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
-// Copies one 64-key K and V tile (keys kt..kt+63) into an LDS stage.  Row pair
-// rp (rows 2 rp, 2 rp + 1: 1 KB) is one wave instruction; lane l fills physical
-// chunk l % 32 of row 2 rp + l / 32 with the logical chunk that the row's
-// swizzle puts there.
+// Per-lane byte offsets of the tile copies (loop invariant): copy i of wave w
+// fills rows 2 (i W + w) + l / 32 (l = lane) of the stage, physical chunk
+// l % 32, from logical chunk (l % 32) ^ swizzle(row).  The row's swizzle
+// depends on i only through i mod (8 / W) for K (row % 16) and i mod 2 for V
+// (row % 4, only when W = 1), so kK and kV offsets per lane cover every copy;
+// the row pair 2 i W and the tile's first row enter through the buffer base.
 template <int W>
-__device__ __forceinline__ void issue_tile_copy(i32x4_t krsrc, i32x4_t vrsrc, half_t* k_stage,
-                                                half_t* v_stage, uint32_t kt, uint32_t row_bytes,
-                                                uint32_t head_bytes, int wave, int lane) {
+struct CopyOffsets {
+  static constexpr int kK = 8 / W;
+  static constexpr int kV = W == 1 ? 2 : 1;
+  uint32_t k[kK];
+  uint32_t v[kV];
+};
+
+template <int W>
+__device__ __forceinline__ CopyOffsets<W> copy_offsets(uint32_t row_bytes, uint32_t head_bytes,
+                                                       int wave, int lane) {
+  CopyOffsets<W> c;
   const int p = lane & 31;
+  const uint32_t row_in_copy = (uint32_t)(2 * wave + (lane >> 5));
+#pragma unroll
+  for (int j = 0; j < CopyOffsets<W>::kK; ++j) {
+    const int r = 2 * (j * W + wave) + (lane >> 5);
+    c.k[j] = row_in_copy * row_bytes + head_bytes + 16u * (uint32_t)(p ^ (r & 15));
+  }
+#pragma unroll
+  for (int j = 0; j < CopyOffsets<W>::kV; ++j) {
+    const int r = 2 * (j * W + wave) + (lane >> 5);
+    c.v[j] = row_in_copy * row_bytes + head_bytes + 16u * (uint32_t)(p ^ (4 * (r & 3)));
+  }
+  return c;
+}
+
+// Copies one 64-key tile (keys kt..kt+63) of K (kV false) or V into an LDS
+// stage.  Copy i reads through a resource based at row kt + 2 i W whose byte
+// count ends at key_end, so rows at or past key_end read as zeros; all of the
+// per-copy arithmetic is scalar.
+template <int W, bool kV>
+__device__ __forceinline__ void issue_tile_copy(const half_t* layer_base, half_t* stage,
+                                                uint32_t kt, uint32_t key_end, uint32_t row_bytes,
+                                                const CopyOffsets<W>& off, int wave) {
 #pragma unroll
   for (int i = 0; i < (kKTile / 2) / W; ++i) {
-    const int rp = i * W + wave;
-    const int r = 2 * rp + (lane >> 5);
-    const uint32_t row_off = (kt + r) * row_bytes + head_bytes;
-    const int kc = p ^ (r & 15);
-    const int vc = p ^ (4 * (r & 3));
-    copy16_to_lds(krsrc, row_off + 16u * kc, k_stage + rp * 2 * kRowHalfs);
-    copy16_to_lds(vrsrc, row_off + 16u * vc, v_stage + rp * 2 * kRowHalfs);
+    const uint32_t row0 = kt + 2u * i * W;
+    const uint32_t bytes = key_end > row0 ? (key_end - row0) * row_bytes : 0u;
+    const i32x4_t rsrc = rsrc_words(layer_base + (size_t)row0 * (row_bytes / 2u), bytes);
+    const uint32_t voff = kV ? off.v[i % CopyOffsets<W>::kV] : off.k[i % CopyOffsets<W>::kK];
+    copy16_to_lds(rsrc, voff, stage + (i * W + wave) * 2 * kRowHalfs);
   }
 }
 
@@ -181,20 +213,16 @@ __device__ __forceinline__ void wait_tile_copies() {
 }
 
 template <int GW>
-__global__ __launch_bounds__(128 * GW) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(64 * GW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flash256_kernel(FlashParams p) {
-  // Two stages of K and V tiles (128 KB); the pair exchange slots for tile maxima
-  // (per query) and P (16 halves per lane).
-  __shared__ __attribute__((aligned(16))) half_t s_tiles[2 * 2 * kTileHalfs];
-  __shared__ float s_mx[GW][2][32];
-  __shared__ __attribute__((aligned(16))) half8_t s_p[GW][2][64][2];
+  // K and V tiles, two stages each (128 KB).
+  __shared__ __attribute__((aligned(16))) half_t s_k[2 * kTileHalfs];
+  __shared__ __attribute__((aligned(16))) half_t s_v[2 * kTileHalfs];
 
-  constexpr int W = 2 * GW;  // waves
+  constexpr int W = GW;  // waves
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int slot = wave % GW;    // head slot
-  const int dh = wave / GW;      // key half for scores, dim half for O
+  const int wave = tid >> 6;     // head slot
   const int h = lane >> 5;       // lane half
   const int n = lane & 31;       // query column owned by this lane
   const uint32_t G = p.heads / p.kv_heads;
@@ -212,7 +240,7 @@ void flash256_kernel(FlashParams p) {
   const uint32_t split = (item / p.q_tiles) % p.splits;
   const uint32_t hg = (item / (p.q_tiles * p.splits)) % p.head_groups;
   const uint32_t kvh = item / (p.q_tiles * p.splits * p.head_groups);
-  const uint32_t g_in_group = hg * GW + slot;
+  const uint32_t g_in_group = hg * GW + wave;
   const uint32_t head = kvh * G + g_in_group;
   const uint32_t t0 = q_tile * kQTile;
   const uint32_t token = t0 + n;
@@ -236,19 +264,20 @@ void flash256_kernel(FlashParams p) {
     // include this one, so nothing is written.
     return;
   }
+  const uint32_t ntiles = (key_end - key_begin + kKTile - 1) / kKTile;
 
   // K/V rows of this layer through range-checked buffer resources: rows at or
   // past key_end read as zeros without a memory access (the host keeps every
   // byte offset below 2^31).
   const uint32_t row_bytes = p.kv_heads * kD * 2u;
   const size_t layer_elems = (size_t)p.layer * p.capacity_tokens * p.kv_heads * kD;
-  const i32x4_t krsrc = rsrc_words(p.key_cache + layer_elems, key_end * row_bytes);
-  const i32x4_t vrsrc = rsrc_words(p.value_cache + layer_elems, key_end * row_bytes);
-  const uint32_t head_bytes = kvh * kD * 2u;
+  const half_t* k_layer = p.key_cache + layer_elems;
+  const half_t* v_layer = p.value_cache + layer_elems;
+  const CopyOffsets<W> coff = copy_offsets<W>(row_bytes, kvh * kD * 2u, wave, lane);
 
-  // The first tile's copy goes out before the query is loaded.
-  issue_tile_copy<W>(krsrc, vrsrc, s_tiles, s_tiles + kTileHalfs, key_begin, row_bytes,
-                     head_bytes, wave, lane);
+  // Tile 0's copies go out before the query is loaded.
+  issue_tile_copy<W, false>(k_layer, s_k, key_begin, key_end, row_bytes, coff, wave);
+  issue_tile_copy<W, true>(v_layer, s_v, key_begin, key_end, row_bytes, coff, wave);
 
   // Q^T as the B operand of S^T = K Q^T: lane holds query n, dims 16*step + 8*h + j.
   half8_t qf[kD / 16];
@@ -268,147 +297,172 @@ void flash256_kernel(FlashParams p) {
     }
   }
 
-  constexpr int kDt = kD / 64;  // O^T tiles of 32 dims per wave (half of D)
-  float16_t o[kDt];  // O^T tiles: dims 128*dh + 32*dt + c_row(r, h), query n
+  float16_t o[kD / 32];  // O^T tiles: dims 32*dt + c_row(r, h), query n
 #pragma unroll
-  for (int dt = 0; dt < kDt; ++dt) {
+  for (int dt = 0; dt < kD / 32; ++dt) {
     o[dt] = float16_t{};
   }
   float m = -INFINITY;  // reference max (log2 domain, scaled) of query n
-  float l = 0.0f;       // this lane's share (own keys) of the denominator, relative to m
+  float l = 0.0f;       // this lane's share of the denominator (relative to m)
   const float c = p.scale_log2;
 
-  // K fragment reads: row dh*32 + n, logical chunk 2*step + h at physical chunk
-  // (2*step + h) ^ (n % 16) = 2*step ^ u.
+  // K fragment reads: row 32*half + n, logical chunk 2*step + h at physical
+  // chunk (2*step + h) ^ (row % 16) = 2*step ^ u.
   const int u = h ^ (n & 15);
-  const int k_row = (dh * 32 + n) * kRowHalfs;
+  const int k_lane = n * kRowHalfs;
   // V^T fragment reads (ds_read_b64_tr_b16): lane L = 16 g + 4 e + q of group g
-  // (h = g / 2, 16-dim group gd = g % 2) supplies row 4h + e (+8 for the high
-  // four keys, +16 per k-step, +32 for the second key half), dims
-  // 128 dh + 32 dt + 16 gd + 4q, i.e. physical chunk (16 dh + 4 dt + 2 gd + q/2)
-  // ^ 4e: 128 dh + 32 (dt ^ e) + 16 gd + 4q halfs.
+  // (h = g / 2, 16-dim group gd = g % 2) supplies row 16 ks + 4h + e (+8 for the
+  // high four keys), dims 32 dt + 16 gd + 4q, i.e. physical chunk
+  // (4 dt + 2 gd + q/2) ^ 4e: 32 (dt ^ e) + 16 gd + 4q halfs (dt < 4; +128 for
+  // dt >= 4).
   const int e = (lane >> 2) & 3;
-  const int v_lane = (4 * h + e) * kRowHalfs + 128 * dh + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int v_lane = (4 * h + e) * kRowHalfs + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   int v_addr[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     v_addr[b] = v_lane + 32 * (b ^ e);
   }
 
-  int stage = 0;
-  for (uint32_t kt = key_begin; kt < key_end; kt += kKTile, stage ^= 1) {
-    wait_tile_copies();
-    __syncthreads();  // tile kt is in `stage`; every wave is done with the other stage
-    if (kt + kKTile < key_end) {
-      half_t* nk = s_tiles + (stage ^ 1) * 2 * kTileHalfs;
-      issue_tile_copy<W>(krsrc, vrsrc, nk, nk + kTileHalfs, kt + kKTile, row_bytes, head_bytes,
-                         wave, lane);
-    }
-    const half_t* ks_base = s_tiles + stage * 2 * kTileHalfs;
-    const half_t* vs_base = ks_base + kTileHalfs;
-    const uint32_t k0 = kt + dh * 32;  // first key of this wave's score half
-
-    // ---- S^T = K Q^T for 32 keys x 32 queries ----
-    float16_t s = float16_t{};
+  // S^T of one 64-key tile: s0 = keys 0..31, s1 = keys 32..63.  The 32 fragment
+  // reads run kRing MFMAs ahead through an explicit register ring, which keeps
+  // the LDS latency off the MFMA issue.
+  constexpr int kRing = 6;   // K fragment reads in flight
+  constexpr int kVRing = 4;  // V fragment read pairs in flight
+  auto scores = [&](const half_t* kst, float16_t& s0, float16_t& s1) {
+    s0 = float16_t{};
+    s1 = float16_t{};
+    // The swizzled offsets are recomputed here (two VALU ops per read) rather
+    // than hoisted out of the tile loop, where 16 of them would pin registers.
+    int uu = u;
+    asm volatile("" : "+v"(uu));
+    auto frag = [&](int i) {  // read i: step i / 2, key half i % 2
+      const int off = 8 * ((2 * (i >> 1)) ^ uu) + (i & 1) * 32 * kRowHalfs;
+      return *reinterpret_cast<const half8_t*>(&kst[k_lane + off]);
+    };
+    // Scheduling barriers keep this block in source order: the machine
+    // scheduler would otherwise sink every read to just before its MFMA.
+    half8_t ring[kRing];
 #pragma unroll
-    for (int step = 0; step < kD / 16; ++step) {
-      const half8_t a =
-        *reinterpret_cast<const half8_t*>(&ks_base[k_row + 8 * ((2 * step) ^ u)]);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[step], s, 0, 0, 0);
+    for (int i = 0; i < kRing; ++i) {
+      ring[i] = frag(i);
     }
-    pipeline_reads_and_mfma<kD / 16, 3, 1>();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kD / 8; ++i) {
+      const half8_t a = ring[i % kRing];
+      if (i + kRing < kD / 8) {
+        ring[i % kRing] = frag(i + kRing);
+      }
+      if (i & 1) {
+        s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[i >> 1], s1, 0, 0, 0);
+      } else {
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[i >> 1], s0, 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 
-    // ---- mask; tile max shared with the partner wave ----
-    const bool full = k0 + 32 <= key_end && k0 + 31 <= first_position;
+  // Iteration t: publish tile t's K/V copies, start the copies of tile t+1, then
+  // S^T of tile t, its softmax, and its PV.
+  auto iteration = [&](uint32_t t) __attribute__((always_inline)) {
+    wait_tile_copies();
+    __syncthreads();
+    const uint32_t kt = key_begin + t * kKTile;
+    if (t + 1 < ntiles) {
+      issue_tile_copy<W, false>(k_layer, s_k + ((t + 1) & 1) * kTileHalfs, kt + kKTile, key_end,
+                                row_bytes, coff, wave);
+      issue_tile_copy<W, true>(v_layer, s_v + ((t + 1) & 1) * kTileHalfs, kt + kKTile, key_end,
+                               row_bytes, coff, wave);
+    }
+    float16_t c0, c1;
+    scores(s_k + (t & 1) * kTileHalfs, c0, c1);
+
+    // ---- mask and max of tile t ----
+    const bool full = kt + kKTile <= key_end && kt + kKTile - 1u <= first_position;
     if (!full) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const uint32_t key = k0 + c_row(r, h);
-        const bool valid = key < key_end && key <= position;
-        s[r] = valid ? s[r] : -INFINITY;
+        const uint32_t k0 = kt + c_row(r, h);
+        const uint32_t k1 = k0 + 32;
+        c0[r] = (k0 < key_end && k0 <= position) ? c0[r] : -INFINITY;
+        c1[r] = (k1 < key_end && k1 <= position) ? c1[r] : -INFINITY;
       }
     }
-    float mx = s[0];
+    float mx = fmaxf(c0[0], c1[0]);
 #pragma unroll
     for (int r = 1; r < 16; ++r) {
-      mx = fmaxf(mx, s[r]);
+      mx = fmaxf(mx, fmaxf(c0[r], c1[r]));
     }
-    mx = xor32_max(mx);  // this wave's 32 keys, query n (both lane halves)
-    if (h == 0) {
-      s_mx[slot][dh][n] = mx;
-    }
-    __syncthreads();
-    mx = fmaxf(s_mx[slot][0][n], s_mx[slot][1][n]) * c;  // the tile's max, same in both waves
-
-    // ---- lazy online softmax (log2 domain) ----
+    mx = xor32_max(mx) * c;  // tile max for query n (both lane halves)
     const bool need = mx > m + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(need) != 0) {
       const float m_new = need ? mx : m;
       const float corr = need ? fast_exp2(m - m_new) : 1.0f;  // m = -inf -> 0
       l *= corr;
 #pragma unroll
-      for (int dt = 0; dt < kDt; ++dt) {
+      for (int dt = 0; dt < kD / 32; ++dt) {
         o[dt] *= corr;
       }
       m = m_new;
     }
     // A query with no valid key yet keeps m = -inf; its scores are all -inf.
     const float neg_m = m == -INFINITY ? 0.0f : -m;
-    half8_t pb[2];
+    half8_t pb[4];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float pr = fast_exp2(fmaf(s[r], c, neg_m));
-      l += pr;
-      pb[r >> 3][r & 7] = (half_t)pr;
+      const float p0 = fast_exp2(fmaf(c0[r], c, neg_m));
+      const float p1 = fast_exp2(fmaf(c1[r], c, neg_m));
+      l += p0 + p1;
+      pb[r >> 3][r & 7] = (half_t)p0;
+      pb[2 + (r >> 3)][r & 7] = (half_t)p1;
     }
-    s_p[slot][dh][lane][0] = pb[0];
-    s_p[slot][dh][lane][1] = pb[1];
-    __syncthreads();
-    const half8_t po0 = s_p[slot][dh ^ 1][lane][0];
-    const half8_t po1 = s_p[slot][dh ^ 1][lane][1];
-    // P of keys 0..31 and 32..63 of the tile, as B operands (k-steps of 16 keys).
-    half8_t pk[4];
-    pk[0] = dh == 0 ? pb[0] : po0;
-    pk[1] = dh == 0 ? pb[1] : po1;
-    pk[2] = dh == 0 ? po0 : pb[0];
-    pk[3] = dh == 0 ? po1 : pb[1];
 
-    // ---- O^T += V^T P^T over the 64 keys (4 k-steps), this wave's 128 dims ----
+    // ---- O^T += V^T P^T over the tile's 64 keys (4 k-steps of 16) ----
+    const half_t* vst = s_v + (t & 1) * kTileHalfs;
+    auto vfrag = [&](int i) {  // read i: k-step i / 8, dim tile i % 8
+      const int ks = i >> 3;
+      const int dt = i & 7;
+      const half_t* vp = vst + v_addr[dt & 3] + 128 * (dt >> 2) + 16 * ks * kRowHalfs;
+      const half4_t lo = read_tr16(vp);
+      const half4_t hi = read_tr16(vp + 8 * kRowHalfs);
+      return half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    half8_t vring[kVRing];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int i = 0; i < kVRing; ++i) {
+      vring[i] = vfrag(i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int dt = 0; dt < kDt; ++dt) {
-        const half_t* vp = vs_base + v_addr[dt] + 16 * ks * kRowHalfs;
-        const half4_t lo = read_tr16(vp);
-        const half4_t hi = read_tr16(vp + 8 * kRowHalfs);
-        const half8_t a = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pk[ks], o[dt], 0, 0, 0);
+    for (int i = 0; i < 4 * (kD / 32); ++i) {
+      const half8_t a = vring[i % kVRing];
+      if (i + kVRing < 4 * (kD / 32)) {
+        vring[i % kVRing] = vfrag(i + kVRing);
       }
+      o[i & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[i >> 3], o[i & 7], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    pipeline_reads_and_mfma<4 * kDt, 2, 2>();
+  };
+
+  // Prologue: tile 0's copies were issued above.
+  for (uint32_t t = 0; t < ntiles; ++t) {
+    iteration(t);
   }
 
-  // ---- denominator: own keys (both lane halves) plus the partner's keys ----
-  l = xor32_sum(l);
-  __syncthreads();  // every wave is past its last read of s_mx
-  if (h == 0) {
-    s_mx[slot][dh][n] = l;
-  }
-  __syncthreads();
-  l += s_mx[slot][dh ^ 1][n];
+  l = xor32_sum(l);  // both lane halves hold keys of query n
   if (!token_ok) {
     return;
   }
-  // ---- epilogue: lane owns query n; dims 128*dh + 32*dt + c_row(r, h) ----
+  // ---- epilogue: lane owns query n; dims 32*dt + c_row(r, h) ----
   if (p.splits == 1) {
     const float inv = l == 0.0f ? 0.0f : 1.0f / l;
     float* orow = p.output + ((size_t)token * p.heads + head) * kD;
     const float* grow = p.gate != nullptr ? p.gate + ((size_t)token * p.heads + head) * kD : nullptr;
 #pragma unroll
-    for (int dt = 0; dt < kDt; ++dt) {
+    for (int dt = 0; dt < kD / 32; ++dt) {
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        const int d = dh * 128 + dt * 32 + r4 * 8 + h * 4;
+        const int d = dt * 32 + r4 * 8 + h * 4;
         float4 v = make_float4(o[dt][r4 * 4 + 0] * inv, o[dt][r4 * 4 + 1] * inv,
                                o[dt][r4 * 4 + 2] * inv, o[dt][r4 * 4 + 3] * inv);
         if (grow != nullptr) {
@@ -425,15 +479,15 @@ void flash256_kernel(FlashParams p) {
     const size_t base = (((size_t)token * p.kv_heads + kvh) * p.splits + split) * G + g_in_group;
     float* po = p.partial_o + base * kD;
 #pragma unroll
-    for (int dt = 0; dt < kDt; ++dt) {
+    for (int dt = 0; dt < kD / 32; ++dt) {
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        const int d = dh * 128 + dt * 32 + r4 * 8 + h * 4;
+        const int d = dt * 32 + r4 * 8 + h * 4;
         *reinterpret_cast<float4*>(po + d) =
           make_float4(o[dt][r4 * 4 + 0], o[dt][r4 * 4 + 1], o[dt][r4 * 4 + 2], o[dt][r4 * 4 + 3]);
       }
     }
-    if (h == 0 && dh == 0) {
+    if (h == 0) {
       p.partial_ml[base * 2 + 0] = m;
       p.partial_ml[base * 2 + 1] = l;
     }
@@ -453,7 +507,7 @@ FlashPlan plan_flash(const AttentionArgs& a, int cu_count) {
   plan.head_groups = g > 4 ? g / 4 : 1;
   const uint32_t key_count = a.start_position + a.tokens;
   const uint64_t units = (uint64_t)plan.q_tiles * a.kv_heads * plan.head_groups;
-  // One workgroup (8 waves, 128 KB of LDS) per CU.
+  // One workgroup (one wave per SIMD, 128 KB of LDS) per CU.
   const uint64_t target = (uint64_t)(cu_count > 0 ? cu_count : 256);
   uint64_t splits = (target + units - 1) / units;
   // A split should hold enough key tiles to amortise its query load and
@@ -481,7 +535,7 @@ FlashPlan plan_flash(const AttentionArgs& a, int cu_count) {
 template <int GW>
 hipError_t launch_g(const FlashParams& p, hipStream_t stream) {
   const dim3 grid(p.q_tiles * p.kv_heads * p.head_groups * p.splits);
-  flash256_kernel<GW><<<grid, 128 * GW, 0, stream>>>(p);
+  flash256_kernel<GW><<<grid, 64 * GW, 0, stream>>>(p);
   return hipGetLastError();
 }
 
