@@ -199,7 +199,9 @@ int gdn_entry(kraken_hip_context* ctx, const char* what, const kraken_buffer& qu
     a.norm_weight = static_cast<const float*>(norm_w->data);
     a.eps = eps;
   }
-  const hipError_t e = launch_gated_delta_net(a, ctx->cu_count, ctx->stream);
+  KRAKEN_TRY(ensure_workspace(ctx, gdn_workspace_bytes(a)));
+  const hipError_t e = launch_gated_delta_net(a, ctx->cu_count, ctx->workspace,
+                                              ctx->workspace_bytes, ctx->stream);
   if (e != hipSuccess) {
     return internal(w + " launch failed: " + hipGetErrorString(e));
   }
@@ -1003,7 +1005,7 @@ KRAKEN_API int kraken_hip_gated_delta_net_f32_ragged_decode(
   a.head_dim = (uint32_t)head_dim;
   a.seq_state_offsets = static_cast<const uint64_t*>(seq_state_offsets.data);
   a.pool_elems = pool_elems;
-  const hipError_t e = launch_gated_delta_net(a, ctx->cu_count, ctx->stream);
+  const hipError_t e = launch_gated_delta_net(a, ctx->cu_count, nullptr, 0, ctx->stream);
   if (e != hipSuccess) {
     return internal(w + " launch failed: " + hipGetErrorString(e));
   }

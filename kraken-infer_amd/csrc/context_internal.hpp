@@ -172,7 +172,16 @@ struct GdnArgs {
   const uint64_t* seq_state_offsets = nullptr;
   uint64_t pool_elems = 0;
 };
-hipError_t launch_gated_delta_net(const GdnArgs& a, int cu_count, hipStream_t stream);
+// Multi-token calls at head_dim 128 take the chunked (WY) path, which needs
+// gdn_workspace_bytes() of context workspace; other calls need none.
+size_t gdn_workspace_bytes(const GdnArgs& a);
+hipError_t launch_gated_delta_net(const GdnArgs& a, int cu_count, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream);
+// Chunked prefill (csrc/gdn_chunked.hip).
+bool gdn_chunked_supported(const GdnArgs& a);
+size_t gdn_chunked_workspace_bytes(const GdnArgs& a);
+hipError_t launch_gdn_chunked(const GdnArgs& a, void* workspace, size_t workspace_bytes,
+                              hipStream_t stream);
 
 hipError_t launch_ssm_conv(const float* input, const float* kernel, float* output,
                            uint32_t conv_kernel, uint32_t channels, uint32_t tokens,

@@ -25,13 +25,15 @@
 namespace kraken {
 namespace {
 
-// KRAKEN_GDN_PREFILL=generic selects the generic recurrence kernel for
-// multi-token calls (the LDS-staged head_dim-128 kernel is the default); used to
-// compare the two on the same inputs.
+// KRAKEN_GDN_PREFILL selects the multi-token kernel for head_dim 128:
+// "sequential" the LDS-staged recurrence, "generic" the generic recurrence
+// kernel; unset, the chunked (WY) kernels of gdn_chunked.hip run.  Used to
+// compare the three on the same inputs.
 bool gdn_prefill_disabled() {
   const char* v = std::getenv("KRAKEN_GDN_PREFILL");
   return v != nullptr && std::strcmp(v, "generic") == 0;
 }
+// (The chunked path's own selection is gdn_chunked_supported.)
 
 constexpr int kGdnRowsPerBlock = 8;  // 4 waves x 2 rows
 
@@ -731,8 +733,21 @@ unsigned grid_for(size_t total, unsigned block = 256) {
 
 }  // namespace
 
-hipError_t launch_gated_delta_net(const GdnArgs& a, int cu_count, hipStream_t stream) {
+size_t gdn_workspace_bytes(const GdnArgs& a) {
+  return gdn_chunked_supported(a) ? gdn_chunked_workspace_bytes(a) : 0;
+}
+
+hipError_t launch_gated_delta_net(const GdnArgs& a, int cu_count, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
   (void)cu_count;
+  if (gdn_chunked_supported(a)) {
+    const hipError_t e = launch_gdn_chunked(a, workspace, workspace_bytes, stream);
+    if (e != hipSuccess || a.z == nullptr) {
+      return e;
+    }
+    return launch_rms_norm_heads(a.output, a.norm_weight, a.z, a.tokens, a.value_heads,
+                                 a.head_dim, a.eps, stream);
+  }
   GdnParams p{};
   p.query = a.query;
   p.key = a.key;

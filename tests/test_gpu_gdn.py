@@ -81,18 +81,46 @@ def test_gdn_prefill_state_offset_d128(hip_ctx, offset_extra):
 
 
 @pytest.mark.gpu
-def test_gdn_prefill_staged_equals_generic_kernel(hip_ctx, monkeypatch):
-    """The LDS-staged head_dim-128 prefill kernel and the generic recurrence
-    kernel (KRAKEN_GDN_PREFILL=generic) give the same outputs and state."""
-    tokens, hk, hv, d = 257, 16, 16, 128
+@pytest.mark.parametrize("tokens", [64, 257, 1024])
+def test_gdn_prefill_kernels_agree(hip_ctx, monkeypatch, tokens):
+    """The three multi-token kernels for head_dim 128 -- chunked WY (default),
+    LDS-staged sequential (KRAKEN_GDN_PREFILL=sequential) and the generic
+    recurrence (KRAKEN_GDN_PREFILL=generic) -- give the same outputs and state,
+    and each matches the oracle."""
+    hk = hv = 16
+    d = 128
     q, k, v, g, b, s = gdn_inputs(14, tokens, hk, hv, d, state_scale=0.1)
     ops = kh.NumpyOps(hip_ctx)
-    out_a, st_a = ops.gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
-    monkeypatch.setenv("KRAKEN_GDN_PREFILL", "generic")
-    out_b, st_b = ops.gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
-    monkeypatch.delenv("KRAKEN_GDN_PREFILL")
-    np.testing.assert_allclose(out_a, out_b, rtol=0, atol=1e-5)
-    np.testing.assert_allclose(st_a, st_b, rtol=0, atol=1e-5)
+    out_ref, st_ref = oracle.gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
+    results = {}
+    for mode in (None, "sequential", "generic"):
+        if mode is None:
+            monkeypatch.delenv("KRAKEN_GDN_PREFILL", raising=False)
+        else:
+            monkeypatch.setenv("KRAKEN_GDN_PREFILL", mode)
+        results[mode] = ops.gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
+        np.testing.assert_allclose(results[mode][0], out_ref, rtol=0, atol=ATOL, err_msg=str(mode))
+        np.testing.assert_allclose(results[mode][1], st_ref, rtol=0, atol=ATOL, err_msg=str(mode))
+    monkeypatch.delenv("KRAKEN_GDN_PREFILL", raising=False)
+    for mode in ("sequential", "generic"):
+        np.testing.assert_allclose(results[None][0], results[mode][0], rtol=0, atol=2e-5)
+        np.testing.assert_allclose(results[None][1], results[mode][1], rtol=0, atol=2e-5)
+
+
+@pytest.mark.gpu
+def test_gdn_chunked_decay_and_beta_extremes(hip_ctx):
+    """Chunked path with strong decay (g down to -8, exp(g) ~ 3e-4), beta near
+    0 and 1, and a large initial state: the per-chunk factors exp(G_t - G_j)
+    span many orders of magnitude."""
+    tokens, hk, hv, d = 192, 4, 8, 128
+    rng = np.random.default_rng(15)
+    q, k, v, _, _, s = gdn_inputs(15, tokens, hk, hv, d, state_scale=1.0)
+    g = (-8.0 * rng.random(tokens * hv)).astype(np.float32)
+    b = np.where(rng.random(tokens * hv) < 0.5, 0.999, 0.001).astype(np.float32)
+    out, st = kh.NumpyOps(hip_ctx).gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
+    out_ref, st_ref = oracle.gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
+    np.testing.assert_allclose(out, out_ref, rtol=0, atol=ATOL)
+    np.testing.assert_allclose(st, st_ref, rtol=0, atol=ATOL)
 
 
 @pytest.mark.gpu
