@@ -108,16 +108,21 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
   float* blk = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats;
 
   // ---- stage K, Q, V (rows past the chunk's tokens are zero) ----
-  for (int idx = tid; idx < kC * (kDim / 4); idx += 256) {
+  // Unconditional loads from a valid row (the chunk's first token stands in for
+  // rows past its end), zeroed afterwards, so all of them are in flight at once.
+#pragma unroll
+  for (int it = 0; it < kC * (kDim / 4) / 256; ++it) {
+    const int idx = tid + 256 * it;
     const int t = idx >> 5;
     const int c4 = (idx & 31) * 4;
-    float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), qq = kk, vv = kk;
-    if ((uint32_t)t < n) {
-      const size_t ko = ((size_t)(t0 + t) * p.key_heads + kh) * kDim + c4;
-      kk = *reinterpret_cast<const float4*>(p.key + ko);
-      qq = *reinterpret_cast<const float4*>(p.query + ko);
-      vv = *reinterpret_cast<const float4*>(p.value + ((size_t)(t0 + t) * p.value_heads + h) * kDim +
-                                            c4);
+    const bool ok = (uint32_t)t < n;
+    const uint32_t tr = t0 + (ok ? t : 0);
+    const size_t ko = ((size_t)tr * p.key_heads + kh) * kDim + c4;
+    float4 kk = *reinterpret_cast<const float4*>(p.key + ko);
+    float4 qq = *reinterpret_cast<const float4*>(p.query + ko);
+    float4 vv = *reinterpret_cast<const float4*>(p.value + ((size_t)tr * p.value_heads + h) * kDim + c4);
+    if (!ok) {
+      kk = qq = vv = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     *reinterpret_cast<float4*>(&Ks[t][c4]) = kk;
     *reinterpret_cast<float4*>(&Qs[t][c4]) = qq;
@@ -155,26 +160,20 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
   const float g_last = Gs[kC - 1];  // padded tokens carry g = 0
 
   // ---- Gram matrices: tiles (I, J), J <= I, of K K^T (A) and Q K^T (M) ----
-  for (int job = wave; job < 20; job += 4) {
-    const bool is_q = job >= 10;
+  // Jobs 0..9: the ten lower tiles of K K^T, 10..19: of Q K^T.  A wave runs two
+  // jobs per pass with independent accumulators (LDS reads of one overlap the
+  // MFMAs of the other).
+  auto gram_tile = [&](int job, int& I, int& J, bool& is_q) __attribute__((always_inline)) {
+    is_q = job >= 10;
     int jj = is_q ? job - 10 : job;  // lower-triangular tile index
-    int I = 0;
+    I = 0;
     while (jj > I) {
       jj -= I + 1;
       ++I;
     }
-    const int J = jj;
-    const float(*X)[kRowPad] = is_q ? Qs : Ks;
-    float4_v acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4) {
-      const float4 a = *reinterpret_cast<const float4*>(&X[16 * I + li][32 * kq + 4 * s4]);
-      const float4 b = *reinterpret_cast<const float4*>(&Ks[16 * J + li][32 * kq + 4 * s4]);
-      acc = mfma4(a.x, b.x, acc);
-      acc = mfma4(a.y, b.y, acc);
-      acc = mfma4(a.z, b.z, acc);
-      acc = mfma4(a.w, b.w, acc);
-    }
+    J = jj;
+  };
+  auto gram_store = [&](int I, int J, bool is_q, const float4_v& acc) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * I + 4 * kq + r;
@@ -185,6 +184,35 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
       } else {
         As[t][j] = j < t ? Bs[t] * decay * acc[r] : 0.0f;
       }
+    }
+  };
+  for (int job = wave; job < 20; job += 8) {
+    int I0, J0, I1, J1;
+    bool q0, q1;
+    gram_tile(job, I0, J0, q0);
+    const bool two = job + 4 < 20;
+    gram_tile(two ? job + 4 : job, I1, J1, q1);
+    const float(*X0)[kRowPad] = q0 ? Qs : Ks;
+    const float(*X1)[kRowPad] = q1 ? Qs : Ks;
+    float4_v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+      const float4 a0 = *reinterpret_cast<const float4*>(&X0[16 * I0 + li][32 * kq + 4 * s4]);
+      const float4 b0 = *reinterpret_cast<const float4*>(&Ks[16 * J0 + li][32 * kq + 4 * s4]);
+      const float4 a1 = *reinterpret_cast<const float4*>(&X1[16 * I1 + li][32 * kq + 4 * s4]);
+      const float4 b1 = *reinterpret_cast<const float4*>(&Ks[16 * J1 + li][32 * kq + 4 * s4]);
+      acc0 = mfma4(a0.x, b0.x, acc0);
+      acc1 = mfma4(a1.x, b1.x, acc1);
+      acc0 = mfma4(a0.y, b0.y, acc0);
+      acc1 = mfma4(a1.y, b1.y, acc1);
+      acc0 = mfma4(a0.z, b0.z, acc0);
+      acc1 = mfma4(a1.z, b1.z, acc1);
+      acc0 = mfma4(a0.w, b0.w, acc0);
+      acc1 = mfma4(a1.w, b1.w, acc1);
+    }
+    gram_store(I0, J0, q0, acc0);
+    if (two) {
+      gram_store(I1, J1, q1, acc1);
     }
   }
   // Upper tiles of M are zero.
@@ -300,27 +328,40 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
   }
   __syncthreads();
 
-  // ---- U = T V', W = T K' (C x D): 2 x 32 output tiles ----
-  for (int job = wave; job < 64; job += 4) {
-    const bool is_w = job >= 32;
-    const int tile = is_w ? job - 32 : job;
-    const int R = tile >> 3;   // token row block
-    const int Cb = tile & 7;   // dim column block
-    const float(*X)[kRowPad] = is_w ? Ks : Vs;
-    float4_v acc = {0.f, 0.f, 0.f, 0.f};
+  // ---- U = T V', W = T K' (C x D): 2 x 32 output tiles, four per pass ----
+  for (int job0 = 4 * wave; job0 < 64; job0 += 16) {
+    float4_v acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc[u] = float4_v{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
-      const float4 a = *reinterpret_cast<const float4*>(&Ts[16 * R + li][16 * kq + 4 * s4]);
       const int k0 = 16 * kq + 4 * s4;
-      acc = mfma4(a.x, X[k0 + 0][16 * Cb + li], acc);
-      acc = mfma4(a.y, X[k0 + 1][16 * Cb + li], acc);
-      acc = mfma4(a.z, X[k0 + 2][16 * Cb + li], acc);
-      acc = mfma4(a.w, X[k0 + 3][16 * Cb + li], acc);
-    }
-    float* dst = blk + (is_w ? kOffW : kOffU);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      dst[(16 * R + 4 * kq + r) * kDim + 16 * Cb + li] = acc[r];
+      for (int u = 0; u < 4; ++u) {
+        const int job = job0 + u;
+        const bool is_w = job >= 32;
+        const int tile = job & 31;
+        const int R = tile >> 3;   // token row block
+        const int Cb = tile & 7;   // dim column block
+        const float(*X)[kRowPad] = is_w ? Ks : Vs;
+        const float4 a = *reinterpret_cast<const float4*>(&Ts[16 * R + li][k0]);
+        acc[u] = mfma4(a.x, X[k0 + 0][16 * Cb + li], acc[u]);
+        acc[u] = mfma4(a.y, X[k0 + 1][16 * Cb + li], acc[u]);
+        acc[u] = mfma4(a.z, X[k0 + 2][16 * Cb + li], acc[u]);
+        acc[u] = mfma4(a.w, X[k0 + 3][16 * Cb + li], acc[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int job = job0 + u;
+      const int tile = job & 31;
+      float* dst = blk + (job >= 32 ? kOffW : kOffU);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        dst[(16 * (tile >> 3) + 4 * kq + r) * kDim + 16 * (tile & 7) + li] = acc[u][r];
+      }
     }
   }
 }
