@@ -18,16 +18,22 @@
 // identities term by term; they are checked against the sequential kernel and
 // the CPU oracle by the tests.  All decay factors are <= 1.
 //
-// Two kernels:
+// Three kernels:
 //  * gdn_chunk_prep_kernel, one workgroup per (chunk, value head), all chunks
 //    in parallel: stages K, Q, V of the chunk in LDS, forms G, the Gram
 //    matrices K K^T and Q K^T (MFMA), A and M, inverts I + A (diagonal 16 x 16
 //    blocks by substitution, off-diagonal blocks by block substitution), then
 //    U, W (MFMA), Qtil = diag(gamma) Q and Ktil^T into a workspace block.
 //  * gdn_chunk_scan_kernel, one workgroup per (16 state rows, value head),
-//    sequential over the chunks: the 16 x 128 state slice lives in LDS; per
-//    chunk it forms [W; Qtil] S_0^T (MFMA, the state as the B operand in
-//    registers), delta, Y = Z + M delta, and S_C = gamma_C S_0 + Ktil^T delta.
+//    sequential over the chunks, holds only the recurrence: the 16 x 128 state
+//    slice lives in LDS; per chunk it stores S_0 and forms delta = U - W S_0^T
+//    (stored too) and S_C = gamma_C S_0 + Ktil^T delta (MFMA).  The next
+//    chunk's operands are loaded between the MFMAs of the current one.
+//  * gdn_chunk_out_kernel, one workgroup per (chunk, value head, 64 state
+//    rows), all in parallel: Y = scale (Qtil S_0^T + M delta).
+// Taking Y out of the sequential kernel matters because each of its
+// workgroups reads the chunk's operands through one CU's load path (about
+// 30 bytes per clock measured), which then bounds the chunk's latency.
 // MFMA operand layout of v_mfma_f32_16x16x4f32 (checked on the device): A[i][k]
 // in lane i + 16 k, B[k][j] in lane j + 16 k, D[i][j] in lane j + 16 (i / 4),
 // register i % 4.  The k index is relabelled per lane group (lane / 16 = kq
@@ -51,12 +57,14 @@ constexpr int kScanRows = 16;  // state rows per scan workgroup
 // Workspace block per (chunk, value head), in floats.
 constexpr size_t kOffW = 0;                     // W     [C][D]
 constexpr size_t kOffQ = kOffW + kC * kDim;     // Qtil  [C][D]
-constexpr size_t kOffU = kOffQ + kC * kDim;     // U     [C][D]
+constexpr size_t kOffU = kOffQ + kC * kDim;     // U^T   [D][C]
 constexpr size_t kOffKT = kOffU + kC * kDim;    // Ktil^T [D][C]
 constexpr size_t kOffM = kOffKT + kDim * kC;    // M     [C][C]
-constexpr size_t kOffGammaC = kOffM + kC * kC;  // gamma_C
+constexpr size_t kOffS0 = kOffM + kC * kC;     // S_0   [D][D] (state before the chunk)
+constexpr size_t kOffDT = kOffS0 + kDim * kDim; // delta^T [D][C]
+constexpr size_t kOffGammaC = kOffDT + kDim * kC;  // gamma_C
 constexpr size_t kBlockFloats = kOffGammaC + 4;
-// Chunks per prep/scan pair: bounds the workspace (per value head 9.4 MB).
+// Chunks per prep/scan/out pass: bounds the workspace (per value head 15.6 MB).
 constexpr uint32_t kSlabChunks = 64;
 
 typedef float float4_v __attribute__((ext_vector_type(4)));
@@ -197,10 +205,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
     float4_v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
 #pragma unroll
     for (int s4 = 0; s4 < 8; ++s4) {
-      const float4 a0 = *reinterpret_cast<const float4*>(&X0[16 * I0 + li][32 * kq + 4 * s4]);
-      const float4 b0 = *reinterpret_cast<const float4*>(&Ks[16 * J0 + li][32 * kq + 4 * s4]);
-      const float4 a1 = *reinterpret_cast<const float4*>(&X1[16 * I1 + li][32 * kq + 4 * s4]);
-      const float4 b1 = *reinterpret_cast<const float4*>(&Ks[16 * J1 + li][32 * kq + 4 * s4]);
+      const float4 a0 = *reinterpret_cast<const float4*>(&X0[16 * I0 + li][16 * s4 + 4 * kq]);
+      const float4 b0 = *reinterpret_cast<const float4*>(&Ks[16 * J0 + li][16 * s4 + 4 * kq]);
+      const float4 a1 = *reinterpret_cast<const float4*>(&X1[16 * I1 + li][16 * s4 + 4 * kq]);
+      const float4 b1 = *reinterpret_cast<const float4*>(&Ks[16 * J1 + li][16 * s4 + 4 * kq]);
       acc0 = mfma4(a0.x, b0.x, acc0);
       acc1 = mfma4(a1.x, b1.x, acc1);
       acc0 = mfma4(a0.y, b0.y, acc0);
@@ -337,7 +345,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
     }
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
-      const int k0 = 16 * kq + 4 * s4;
+      const int k0 = 16 * s4 + 4 * kq;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int job = job0 + u;
@@ -356,11 +364,16 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int job = job0 + u;
-      const int tile = job & 31;
-      float* dst = blk + (job >= 32 ? kOffW : kOffU);
+      const int R = (job & 31) >> 3;
+      const int Cb = job & 7;
+      if (job >= 32) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        dst[(16 * (tile >> 3) + 4 * kq + r) * kDim + 16 * (tile & 7) + li] = acc[u][r];
+        for (int r = 0; r < 4; ++r) {
+          blk[kOffW + (16 * R + 4 * kq + r) * kDim + 16 * Cb + li] = acc[u][r];
+        }
+      } else {  // U transposed: the four tokens of a lane are contiguous
+        *reinterpret_cast<float4*>(blk + kOffU + (16 * Cb + li) * kC + 16 * R + 4 * kq) =
+          make_float4(acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
       }
     }
   }
@@ -368,10 +381,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
 
 // Global operands of one scan chunk for one lane (see gdn_chunk_scan_kernel).
 struct ScanOps {
-  float4 x[2][8];   // [W; Qtil] rows of the wave's two tiles, 32 k values each
-  float4 kt[2][4];  // Ktil^T rows of the wave's two state tiles, 16 tokens each
-  float4 m[2][4];   // M rows of the wave's two output tiles (waves 2, 3)
-  float u[2][4];    // U values of the wave's delta entries (waves 0, 1)
+  // Lane (i, kq) holds, of row i, the values 16 s + 4 kq .. 16 s + 4 kq + 3 in
+  // entry s: one load instruction reads 64 contiguous bytes of each of 16 rows.
+  float4 x[8];      // W rows of the wave's 16 tokens (32 values)
+  float4 kt[2][4];  // Ktil^T rows of the wave's two state tiles (16 tokens)
+  float4 u;         // U entries of the lane's four delta values
   float gamma_c;
 };
 
@@ -384,8 +398,14 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ChunkParams p) {
   const int wave = tid >> 6;
   const int li = lane & 15;
   const int kq = lane >> 4;
-  const uint32_t row0 = blockIdx.x * kScanRows;
-  const uint32_t h = blockIdx.y;
+  // Workgroup i runs on XCD i % 8.  The (head, row block) pairs are numbered
+  // so that the eight row blocks of a head share an XCD and its L2, which then
+  // fetches the head's chunk operands once instead of eight times.
+  constexpr uint32_t kXcds = 8;
+  static_assert(kDim / kScanRows == kXcds, "grid of value_heads * kXcds workgroups");
+  const uint32_t q = (blockIdx.x % kXcds) * p.value_heads + blockIdx.x / kXcds;
+  const uint32_t row0 = (q % (kDim / kScanRows)) * kScanRows;
+  const uint32_t h = q / (kDim / kScanRows);
   float* shead = p.state + ((size_t)h * kDim + row0) * kDim;
 
   for (int idx = tid; idx < kScanRows * (kDim / 4); idx += 256) {
@@ -395,144 +415,124 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ChunkParams p) {
       *reinterpret_cast<const float4*>(shead + (size_t)r * kDim + c4);
   }
 
-  // Loads every global operand of chunk cl that this lane uses (issued one
-  // chunk ahead, so the chunk loop never waits on memory).
-  auto load_ops = [&](uint32_t cl, ScanOps& o) __attribute__((always_inline)) {
+  // Global operands of chunk cl that this lane uses, in two parts (W rows,
+  // then U, gamma_C, Ktil^T), issued for the next chunk between the MFMAs of
+  // the current one: the per-CU load path moves about as many cycles' worth of
+  // bytes per chunk as the MFMAs take, and an in-order wave stalled on a burst
+  // of loads issues no MFMAs.
+  auto load_x = [&](uint32_t cl, ScanOps& o) __attribute__((always_inline)) {
+    const float* xr = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats + kOffW +
+                      (size_t)(16 * wave + li) * kDim + 4 * kq;
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+      o.x[s4] = *reinterpret_cast<const float4*>(xr + 16 * s4);
+    }
+  };
+  auto load_rest = [&](uint32_t cl, ScanOps& o) __attribute__((always_inline)) {
     const float* blk = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats;
-    const float* X = blk + (wave < 2 ? kOffW : kOffQ) + (size_t)(32 * (wave & 1)) * kDim;
+    o.u = *reinterpret_cast<const float4*>(blk + kOffU + (size_t)(row0 + li) * kC + 16 * wave + 4 * kq);
+    o.gamma_c = blk[kOffGammaC];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const float* xr = X + (size_t)(16 * tt + li) * kDim + 32 * kq;
-#pragma unroll
-      for (int s4 = 0; s4 < 8; ++s4) {
-        o.x[tt][s4] = *reinterpret_cast<const float4*>(xr + 4 * s4);
-      }
-      const float* kr = blk + kOffKT + (size_t)(32 * wave + 16 * tt + li) * kC + 16 * kq;
+      const float* kr = blk + kOffKT + (size_t)(32 * wave + 16 * tt + li) * kC + 4 * kq;
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        o.kt[tt][s4] = *reinterpret_cast<const float4*>(kr + 4 * s4);
-      }
-      if (wave >= 2) {
-        const float* mr = blk + kOffM + (size_t)(32 * (wave - 2) + 16 * tt + li) * kC + 16 * kq;
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-          o.m[tt][s4] = *reinterpret_cast<const float4*>(mr + 4 * s4);
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 32 * wave + 16 * tt + 4 * kq + r;
-          o.u[tt][r] = blk[kOffU + (size_t)t * kDim + row0 + li];
-        }
+        o.kt[tt][s4] = *reinterpret_cast<const float4*>(kr + 16 * s4);
       }
     }
-    o.gamma_c = blk[kOffGammaC];
   };
 
-  auto chunk = [&](uint32_t cl, const ScanOps& o) __attribute__((always_inline)) {
-    const uint32_t t0 = (p.chunk0 + cl) * kC;
-    const uint32_t n = min((uint32_t)kC, p.tokens - t0);
-    // State slice as the B operand: lane (j, kq) holds S[j][32 kq .. 32 kq + 31].
+  // Chunk cl with operands o; loads chunk ncl's operands into nx meanwhile.
+  auto chunk = [&](uint32_t cl, const ScanOps& o, uint32_t ncl, ScanOps& nx)
+                 __attribute__((always_inline)) {
+    float* blk = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats;
+    // State slice as the B operand: lane (j, kq) holds S[j][16 s + 4 kq + c],
+    // s < 8, c < 4 (k = 16 s + 4 kq + c in MFMA 4 s + c, for A and B alike).
     float sb[32];
 #pragma unroll
     for (int s4 = 0; s4 < 8; ++s4) {
-      const float4 v = *reinterpret_cast<const float4*>(&Sl[li][32 * kq + 4 * s4]);
+      const float4 v = *reinterpret_cast<const float4*>(&Sl[li][16 * s4 + 4 * kq]);
       sb[4 * s4 + 0] = v.x;
       sb[4 * s4 + 1] = v.y;
       sb[4 * s4 + 2] = v.z;
       sb[4 * s4 + 3] = v.w;
     }
-    // [W; Qtil] S_0^T: waves 0, 1 take W rows 32 w .., waves 2, 3 Qtil rows.
-    float4_v acc[2];
+    // S_0 of this chunk, for the output kernel.
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      acc[tt] = float4_v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s4 = 0; s4 < 8; ++s4) {
-        const float4 a = o.x[tt][s4];
-        acc[tt] = mfma4(a.x, sb[4 * s4 + 0], acc[tt]);
-        acc[tt] = mfma4(a.y, sb[4 * s4 + 1], acc[tt]);
-        acc[tt] = mfma4(a.z, sb[4 * s4 + 2], acc[tt]);
-        acc[tt] = mfma4(a.w, sb[4 * s4 + 3], acc[tt]);
-      }
+    for (int it = 0; it < kScanRows * (kDim / 4) / 256; ++it) {
+      const int idx = tid + 256 * it;
+      const int r = idx >> 5;
+      const int c4 = (idx & 31) * 4;
+      *reinterpret_cast<float4*>(blk + kOffS0 + (size_t)(row0 + r) * kDim + c4) =
+        *reinterpret_cast<const float4*>(&Sl[r][c4]);
     }
-    if (wave < 2) {
-      // delta = U - W S_0^T, stored transposed (rows j, tokens t).
+    load_x(ncl, nx);
+    // W S_0^T for tokens 16 w .. 16 w + 15.
+    float4_v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          dT[li][32 * wave + 16 * tt + 4 * kq + r] = o.u[tt][r] - acc[tt][r];
-        }
-      }
+    for (int s4 = 0; s4 < 8; ++s4) {
+      const float4 a = o.x[s4];
+      acc = mfma4(a.x, sb[4 * s4 + 0], acc);
+      acc = mfma4(a.y, sb[4 * s4 + 1], acc);
+      acc = mfma4(a.z, sb[4 * s4 + 2], acc);
+      acc = mfma4(a.w, sb[4 * s4 + 3], acc);
     }
+    // Schedule: the state reads, then one load per four MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
+    // delta = U - W S_0^T, kept transposed (rows j, tokens t) in LDS and in
+    // the block.
+    const float4 d = make_float4(o.u.x - acc[0], o.u.y - acc[1], o.u.z - acc[2], o.u.w - acc[3]);
+    *reinterpret_cast<float4*>(&dT[li][16 * wave + 4 * kq]) = d;
+    *reinterpret_cast<float4*>(blk + kOffDT + (size_t)(row0 + li) * kC + 16 * wave + 4 * kq) = d;
     __syncthreads();
-    if (wave >= 2) {
-      // Y = scale (Qtil S_0^T + M delta) for tokens 32 (w - 2) ..
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int tb = 32 * (wave - 2) + 16 * tt;
-        float4_v y = acc[tt];
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-          const float4 a = o.m[tt][s4];
-          const float4 b = *reinterpret_cast<const float4*>(&dT[li][16 * kq + 4 * s4]);
-          y = mfma4(a.x, b.x, y);
-          y = mfma4(a.y, b.y, y);
-          y = mfma4(a.z, b.z, y);
-          y = mfma4(a.w, b.w, y);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t t = tb + 4 * kq + r;
-          if (t < n) {
-            p.output[((size_t)(t0 + t) * p.value_heads + h) * kDim + row0 + li] = y[r] * p.scale;
-          }
-        }
-      }
-    }
+    load_rest(ncl, nx);
     // S_C^T rows (key dims) 32 w .. 32 w + 31 = gamma_C S_0^T + Ktil^T delta.
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       const int kb = 32 * wave + 16 * tt;
-      float4_v s;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        s[r] = o.gamma_c * Sl[li][kb + 4 * kq + r];
-      }
+      const float4 s0 = *reinterpret_cast<const float4*>(&Sl[li][kb + 4 * kq]);
+      float4_v s = {o.gamma_c * s0.x, o.gamma_c * s0.y, o.gamma_c * s0.z, o.gamma_c * s0.w};
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
         const float4 a = o.kt[tt][s4];
-        const float4 b = *reinterpret_cast<const float4*>(&dT[li][16 * kq + 4 * s4]);
+        const float4 b = *reinterpret_cast<const float4*>(&dT[li][16 * s4 + 4 * kq]);
         s = mfma4(a.x, b.x, s);
         s = mfma4(a.y, b.y, s);
         s = mfma4(a.z, b.z, s);
         s = mfma4(a.w, b.w, s);
       }
+      *reinterpret_cast<float4*>(&Sl[li][kb + 4 * kq]) = make_float4(s[0], s[1], s[2], s[3]);
+    }
+    // Schedule: the delta and state reads, then one load per three MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        Sl[li][kb + 4 * kq + r] = s[r];
-      }
+    for (int i = 0; i < 10; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
     }
     __syncthreads();
   };
 
+  // Two chunks per iteration with the operand sets swapped: the next chunk's
+  // loads (clamped to the last chunk, so always in range) are in flight during
+  // the current chunk.
   ScanOps ops_a, ops_b;
-  load_ops(0, ops_a);
+  load_x(0, ops_a);
+  load_rest(0, ops_a);
   __syncthreads();  // state slice staged
-  // Two chunks per iteration with the operand sets swapped, so the next
-  // chunk's loads are always in flight during the current chunk.
-  for (uint32_t cl = 0; cl < p.chunks; cl += 2) {
-    if (cl + 1 < p.chunks) {
-      load_ops(cl + 1, ops_b);
-    }
-    chunk(cl, ops_a);
-    if (cl + 1 < p.chunks) {
-      if (cl + 2 < p.chunks) {
-        load_ops(cl + 2, ops_a);
-      }
-      chunk(cl + 1, ops_b);
-    }
+  const uint32_t last = p.chunks - 1;
+  uint32_t cl = 0;
+  for (; cl + 1 < p.chunks; cl += 2) {
+    chunk(cl, ops_a, cl + 1, ops_b);
+    chunk(cl + 1, ops_b, min(cl + 2, last), ops_a);
+  }
+  if (cl < p.chunks) {
+    chunk(cl, ops_a, last, ops_b);
   }
 
   for (int idx = tid; idx < kScanRows * (kDim / 4); idx += 256) {
@@ -540,6 +540,102 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ChunkParams p) {
     const int c4 = (idx & 31) * 4;
     *reinterpret_cast<float4*>(shead + (size_t)r * kDim + c4) =
       *reinterpret_cast<const float4*>(&Sl[r][c4]);
+  }
+}
+
+constexpr int kOutRows = 64;  // state rows per output workgroup
+
+// Y = scale (Qtil S_0^T + M delta) for one (chunk, value head, 64 state rows).
+// Wave w takes tokens 16 w .. 16 w + 15 against four 16-row tiles; S_0 and
+// delta^T rows are staged in LDS (shared by the four waves), the Qtil and M
+// rows of the wave's tokens are the A operands in registers.
+__global__ __launch_bounds__(256) void gdn_chunk_out_kernel(ChunkParams p) {
+  __shared__ __attribute__((aligned(16))) float S0s[kOutRows][kRowPad];
+  __shared__ __attribute__((aligned(16))) float Ds[kOutRows][kCPad];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int li = lane & 15;
+  const int kq = lane >> 4;
+  // Workgroups i and i + 8 (same XCD) take the two row halves of one
+  // (chunk, head) unit and share its Qtil and M through that XCD's L2.
+  constexpr uint32_t kHalves = kDim / kOutRows;
+  static_assert(kHalves == 2, "two row halves per unit");
+  const uint32_t unit = (blockIdx.x / 16) * 8 + blockIdx.x % 8;
+  const uint32_t half = (blockIdx.x / 8) % 2;
+  if (unit >= p.chunks * p.value_heads) {
+    return;  // grid padding (whole workgroup)
+  }
+  const uint32_t cl = unit / p.value_heads;
+  const uint32_t h = unit % p.value_heads;
+  const uint32_t r0 = half * kOutRows;
+  const float* blk = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats;
+
+  // A operands first (global, in flight while S_0 and delta are staged).
+  const float* qr = blk + kOffQ + (size_t)(16 * wave + li) * kDim + 4 * kq;
+  const float* mr = blk + kOffM + (size_t)(16 * wave + li) * kC + 4 * kq;
+  float4 qa[8], ma[4];
+#pragma unroll
+  for (int s4 = 0; s4 < 8; ++s4) {
+    qa[s4] = *reinterpret_cast<const float4*>(qr + 16 * s4);
+  }
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) {
+    ma[s4] = *reinterpret_cast<const float4*>(mr + 16 * s4);
+  }
+#pragma unroll
+  for (int it = 0; it < kOutRows * (kDim / 4) / 256; ++it) {
+    const int idx = tid + 256 * it;
+    const int r = idx >> 5;
+    const int c4 = (idx & 31) * 4;
+    *reinterpret_cast<float4*>(&S0s[r][c4]) =
+      *reinterpret_cast<const float4*>(blk + kOffS0 + (size_t)(r0 + r) * kDim + c4);
+  }
+#pragma unroll
+  for (int it = 0; it < kOutRows * (kC / 4) / 256; ++it) {
+    const int idx = tid + 256 * it;
+    const int r = idx >> 4;
+    const int c4 = (idx & 15) * 4;
+    *reinterpret_cast<float4*>(&Ds[r][c4]) =
+      *reinterpret_cast<const float4*>(blk + kOffDT + (size_t)(r0 + r) * kC + c4);
+  }
+  __syncthreads();
+
+  const uint32_t t0 = (p.chunk0 + cl) * kC;
+  const uint32_t n = min((uint32_t)kC, p.tokens - t0);
+  const size_t row_floats = (size_t)p.value_heads * kDim;
+  // Rows at or past the chunk's last token fall outside the resource and are
+  // dropped.
+  const __amdgpu_buffer_rsrc_t out =
+    make_buffer_rsrc(p.output + (size_t)t0 * row_floats, n * (uint32_t)row_floats * 4u);
+#pragma unroll
+  for (int nt = 0; nt < kOutRows / 16; ++nt) {
+    const int j = 16 * nt + li;
+    float4_v y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+      const float4 b = *reinterpret_cast<const float4*>(&S0s[j][16 * s4 + 4 * kq]);
+      y = mfma4(qa[s4].x, b.x, y);
+      y = mfma4(qa[s4].y, b.y, y);
+      y = mfma4(qa[s4].z, b.z, y);
+      y = mfma4(qa[s4].w, b.w, y);
+    }
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const float4 b = *reinterpret_cast<const float4*>(&Ds[j][16 * s4 + 4 * kq]);
+      y = mfma4(ma[s4].x, b.x, y);
+      y = mfma4(ma[s4].y, b.y, y);
+      y = mfma4(ma[s4].z, b.z, y);
+      y = mfma4(ma[s4].w, b.w, y);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t t = 16 * wave + 4 * kq + r;
+      const uint32_t off = ((t * p.value_heads + h) * kDim + r0 + j) * 4u;
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y[r] * p.scale), out,
+                                            (int)off, 0, 0);
+    }
   }
 }
 
@@ -597,7 +693,16 @@ hipError_t launch_gdn_chunked(const GdnArgs& a, void* workspace, size_t workspac
     if (e != hipSuccess) {
       return e;
     }
-    gdn_chunk_scan_kernel<<<dim3(kDim / kScanRows, a.value_heads), 256, 0, stream>>>(p);
+    // One workgroup per (head, 16-row block); the kernel maps the linear index
+    // (value_heads * 8 of them, a multiple of the XCD count) to the pair.
+    gdn_chunk_scan_kernel<<<a.value_heads * (kDim / kScanRows), 256, 0, stream>>>(p);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+      return e;
+    }
+    // Two workgroups per (chunk, head) unit, padded to a multiple of 16.
+    const uint32_t units = p.chunks * a.value_heads;
+    gdn_chunk_out_kernel<<<(units + 7) / 8 * 16, 256, 0, stream>>>(p);
     e = hipGetLastError();
     if (e != hipSuccess) {
       return e;
