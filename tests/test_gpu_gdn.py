@@ -108,6 +108,25 @@ def test_gdn_prefill_kernels_agree(hip_ctx, monkeypatch, tokens):
 
 
 @pytest.mark.gpu
+def test_gdn_chunked_crosses_pass_boundary(hip_ctx, monkeypatch):
+    """The chunked path works through the tokens in passes of 64 chunks (4096
+    tokens) with the state carried between passes; 4166 tokens make a second,
+    ragged pass.  Grouped heads (key_heads < value_heads)."""
+    tokens, hk, hv, d = 64 * 64 + 70, 2, 4, 128
+    q, k, v, g, b, s = gdn_inputs(16, tokens, hk, hv, d, state_scale=0.1)
+    ops = kh.NumpyOps(hip_ctx)
+    monkeypatch.delenv("KRAKEN_GDN_PREFILL", raising=False)
+    out, st = ops.gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
+    out_ref, st_ref = oracle.gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
+    np.testing.assert_allclose(out, out_ref, rtol=0, atol=ATOL)
+    np.testing.assert_allclose(st, st_ref, rtol=0, atol=ATOL)
+    monkeypatch.setenv("KRAKEN_GDN_PREFILL", "sequential")
+    out_s, st_s = ops.gated_delta_net(q, k, v, g, b, s, tokens, hk, hv, d)
+    np.testing.assert_allclose(out, out_s, rtol=0, atol=2e-5)
+    np.testing.assert_allclose(st, st_s, rtol=0, atol=2e-5)
+
+
+@pytest.mark.gpu
 def test_gdn_chunked_decay_and_beta_extremes(hip_ctx):
     """Chunked path with strong decay (g down to -8, exp(g) ~ 3e-4), beta near
     0 and 1, and a large initial state: the per-chunk factors exp(G_t - G_j)
