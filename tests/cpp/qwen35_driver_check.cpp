@@ -1,0 +1,386 @@
+// Drives the Qwen3.5 plan and layer drivers (include/kraken/qwen35_plan.hpp,
+// include/kraken/qwen35_layers.hpp) for tests/test_qwen35_driver.py.
+//
+//   qwen35_driver_check plan
+//       No GPU needed.  Prints the execution plan of Qwen3.5-0.8B for the
+//       reference smoke test's request (11000 prompt tokens, chunks of 512) as
+//       key=value lines and the formatted summary, the Status of the plan's
+//       argument checks, and the layer walk of the decode loop.
+//   qwen35_driver_check linear <dir> <reference|fused>
+//   qwen35_driver_check full <dir> <reference|fused>
+//       On a GPU.  Reads the chunk's projection outputs, weights and initial
+//       caches from raw files in <dir> (written by the test), runs one layer
+//       driver on the 0.8B plan and writes the output and the final caches
+//       back to <dir>.
+// Exits non-zero on the first failure.
+#include <array>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <iterator>
+#include <string>
+#include <vector>
+
+#include "kraken/qwen35_layers.hpp"
+
+using kraken::hip::HipBuffer;
+using kraken::hip::HipContext;
+using kraken::hip::Status;
+namespace q35 = kraken::qwen35;
+
+namespace {
+
+const char* code_name(kraken::hip::StatusCode c) {
+  switch (c) {
+    case kraken::hip::StatusCode::ok:
+      return "ok";
+    case kraken::hip::StatusCode::invalid_argument:
+      return "invalid_argument";
+    case kraken::hip::StatusCode::unavailable:
+      return "unavailable";
+    default:
+      return "internal_error";
+  }
+}
+
+const char* kind_name(q35::LayerKind k) {
+  switch (k) {
+    case q35::LayerKind::full_attention:
+      return "full_attention";
+    case q35::LayerKind::linear_attention:
+      return "linear_attention";
+    default:
+      return "mtp";
+  }
+}
+
+void print_status(const char* label, const Status& s) {
+  std::printf("status %s: %s %s\n", label, code_name(s.code()), s.message().c_str());
+}
+
+int run_plan() {
+  q35::RuntimeOptions options;
+  options.decode_tokens = 1;
+  options.prefill_chunk_tokens = 512;
+  const q35::ModelShape shape = q35::qwen35_0_8b_shape();
+  auto plan = q35::build_execution_plan(shape, 11000, options);
+  if (!plan.is_ok()) {
+    print_status("plan", plan.status());
+    return 1;
+  }
+  const q35::ExecutionPlan& p = plan.value();
+  const q35::CachePlan& c = p.cache;
+  std::printf("main_layers=%zu\n", p.main_layers);
+  std::printf("full_attention_layers=%zu\n", c.full_attention_layers);
+  std::printf("linear_attention_layers=%zu\n", c.linear_attention_layers);
+  std::printf("kv_dim=%zu\n", c.kv_dim);
+  std::printf("recurrent_r_elements_per_layer=%zu\n", c.recurrent_r_elements_per_layer);
+  std::printf("recurrent_s_elements_per_layer=%zu\n", c.recurrent_s_elements_per_layer);
+  std::printf("attention_capacity_tokens=%zu\n", c.attention_capacity_tokens);
+  std::printf("chunk_count=%zu\n", p.prefill.chunk_count);
+  std::printf("final_chunk_tokens=%zu\n", p.prefill.final_chunk_tokens);
+  std::printf("output_only_last_token=%d\n", p.prefill.output_only_last_token ? 1 : 0);
+  std::printf("kv_cache_bytes=%llu\n", (unsigned long long)c.kv_cache_bytes);
+  std::printf("recurrent_r_cache_bytes=%llu\n", (unsigned long long)c.recurrent_r_cache_bytes);
+  std::printf("recurrent_s_cache_bytes=%llu\n", (unsigned long long)c.recurrent_s_cache_bytes);
+  std::printf("total_cache_bytes=%llu\n", (unsigned long long)c.total_cache_bytes);
+  for (std::size_t i = 0; i < p.layer_kinds.size(); ++i) {
+    std::printf("layer_kind %zu %s\n", i, kind_name(p.layer_kinds[i]));
+  }
+  std::printf("--- summary\n%s--- end\n", q35::format_execution_plan(p).c_str());
+
+  // The plan's argument checks, in the reference's order.
+  print_status("prompt_zero", q35::build_execution_plan(shape, 0, options).status());
+  q35::RuntimeOptions bad = options;
+  bad.prefill_chunk_tokens = 0;
+  print_status("chunk_zero", q35::build_execution_plan(shape, 8, bad).status());
+  bad = options;
+  bad.sequence_slots = 0;
+  print_status("slots_zero", q35::build_execution_plan(shape, 8, bad).status());
+  q35::ModelShape s2 = shape;
+  s2.hidden_size = 0;
+  s2.head_dim = -1;
+  print_status("hidden_zero", q35::build_execution_plan(s2, 8, options).status());
+  s2 = shape;
+  s2.head_dim = -1;
+  print_status("head_dim_negative", q35::build_execution_plan(s2, 8, options).status());
+  s2 = shape;
+  s2.linear_inner_size = 2047;
+  print_status("inner_indivisible", q35::build_execution_plan(s2, 8, options).status());
+  s2 = shape;
+  s2.layer_kinds.resize(23);
+  print_status("kinds_short", q35::build_execution_plan(s2, 8, options).status());
+  bad = options;
+  bad.context_tokens = (std::size_t)1 << 62;
+  print_status("kv_overflow", q35::build_execution_plan(shape, 8, bad).status());
+
+  // Options that change every cache term.
+  q35::RuntimeOptions o2;
+  o2.context_tokens = 262144;
+  o2.decode_tokens = 64;
+  o2.prefill_chunk_tokens = 1000;
+  o2.sequence_slots = 2;
+  o2.recurrent_snapshot_count = 3;
+  o2.kv_cache_f16 = false;
+  o2.output_all_prompt_logits = true;
+  auto plan2 = q35::build_execution_plan(shape, 3000, o2);
+  if (!plan2.is_ok()) {
+    print_status("plan2", plan2.status());
+    return 1;
+  }
+  std::printf("--- summary2\n%s--- end\n", q35::format_execution_plan(plan2.value()).c_str());
+
+  // A model with one MTP layer past the main ones: counted in neither cache.
+  q35::ModelShape s3 = shape;
+  s3.total_layer_count = 25;
+  s3.layer_kinds = q35::default_layer_kinds(24, 25);
+  auto plan3 = q35::build_execution_plan(s3, 16, options);
+  std::printf("mtp_model: %s main=%zu total=%zu full=%zu linear=%zu\n",
+              code_name(plan3.status().code()), plan3.value().main_layers,
+              plan3.value().total_layers, plan3.value().cache.full_attention_layers,
+              plan3.value().cache.linear_attention_layers);
+
+  // The decode loop's layer walk.
+  const Status walk = q35::for_each_main_layer(
+    p, [](std::size_t i, q35::LayerKind k, std::size_t kind_index) {
+      std::printf("walk %zu %s %zu\n", i, kind_name(k), kind_index);
+      return Status::ok();
+    });
+  print_status("walk", walk);
+  q35::ExecutionPlan p4 = p;
+  p4.layer_kinds[5] = q35::LayerKind::mtp;
+  print_status("walk_mtp", q35::for_each_main_layer(p4, [](std::size_t, q35::LayerKind,
+                                                           std::size_t) { return Status::ok(); }));
+  q35::ExecutionPlan p5 = p;
+  p5.layer_kinds[4] = q35::LayerKind::full_attention;
+  print_status("walk_count", q35::for_each_main_layer(p5, [](std::size_t, q35::LayerKind,
+                                                             std::size_t) { return Status::ok(); }));
+  std::printf("plan done\n");
+  return 0;
+}
+
+template <typename T>
+bool read_file(const std::string& path, std::vector<T>& out) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) {
+    std::printf("FAIL cannot read %s\n", path.c_str());
+    return false;
+  }
+  std::vector<char> bytes((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+  out.resize(bytes.size() / sizeof(T));
+  std::memcpy(out.data(), bytes.data(), out.size() * sizeof(T));
+  return true;
+}
+
+template <typename T>
+bool write_file(const std::string& path, const std::vector<T>& data) {
+  std::ofstream f(path, std::ios::binary);
+  f.write(reinterpret_cast<const char*>(data.data()), (std::streamsize)(data.size() * sizeof(T)));
+  return (bool)f;
+}
+
+bool check(const Status& s, const char* what) {
+  if (!s.is_ok()) {
+    std::printf("FAIL %s: %s %s\n", what, code_name(s.code()), s.message().c_str());
+    return false;
+  }
+  return true;
+}
+
+// Device buffer holding `host`.
+template <typename T>
+bool upload(const HipContext& ctx, const std::vector<T>& host, HipBuffer& out) {
+  auto b = ctx.make_buffer(host.size() * sizeof(T));
+  if (!check(b.status(), "make_buffer")) {
+    return false;
+  }
+  out = std::move(b.value());
+  return check(ctx.copy_to_buffer(out, host.data(), host.size() * sizeof(T)), "upload");
+}
+
+template <typename T>
+bool download(const HipContext& ctx, const HipBuffer& b, std::vector<T>& host) {
+  host.resize(b.byte_size() / sizeof(T));
+  return check(ctx.copy_from_buffer(b, host.data(), host.size() * sizeof(T)), "download");
+}
+
+// meta.txt: whitespace-separated integers.
+bool read_meta(const std::string& dir, std::vector<long long>& meta) {
+  std::ifstream f(dir + "/meta.txt");
+  long long v;
+  while (f >> v) {
+    meta.push_back(v);
+  }
+  return !meta.empty();
+}
+
+int run_linear(const std::string& dir, q35::OpOrder order) {
+  std::vector<long long> meta;  // tokens, linear_layer
+  if (!read_meta(dir, meta) || meta.size() < 2) {
+    std::printf("FAIL meta\n");
+    return 1;
+  }
+  const std::size_t tokens = (std::size_t)meta[0];
+  const std::size_t layer = (std::size_t)meta[1];
+  auto ctx_r = HipContext::create();
+  if (!check(ctx_r.status(), "create")) {
+    return 1;
+  }
+  const HipContext& ctx = ctx_r.value();
+  q35::RuntimeOptions options;
+  auto plan = q35::build_execution_plan(q35::qwen35_0_8b_shape(), tokens, options);
+  if (!check(plan.status(), "plan")) {
+    return 1;
+  }
+  auto cache = q35::allocate_device_cache(ctx, plan.value());
+  if (!check(cache.status(), "allocate_device_cache")) {
+    return 1;
+  }
+  std::vector<float> qkv, z, beta, alpha, conv1d, dt_bias, ssm_a, norm, r0, s0;
+  const std::pair<const char*, std::vector<float>*> inputs[] = {
+    {"qkv", &qkv},         {"z", &z},         {"beta", &beta}, {"alpha", &alpha},
+    {"conv1d", &conv1d},   {"dt_bias", &dt_bias}, {"ssm_a", &ssm_a},
+    {"ssm_norm", &norm},   {"r0", &r0},       {"s0", &s0},
+  };
+  for (const auto& in : inputs) {
+    if (!read_file(dir + "/" + in.first + ".f32", *in.second)) {
+      return 1;
+    }
+  }
+  HipBuffer qkv_b, z_b, beta_b, alpha_b, conv_b, dtb_b, a_b, norm_b;
+  if (!upload(ctx, qkv, qkv_b) || !upload(ctx, z, z_b) || !upload(ctx, beta, beta_b) ||
+      !upload(ctx, alpha, alpha_b) || !upload(ctx, conv1d, conv_b) ||
+      !upload(ctx, dt_bias, dtb_b) || !upload(ctx, ssm_a, a_b) || !upload(ctx, norm, norm_b)) {
+    return 1;
+  }
+  q35::DeviceCache& dc = cache.value();
+  if (r0.size() * 4 != dc.recurrent_r_cache.byte_size() ||
+      s0.size() * 4 != dc.recurrent_s_cache.byte_size()) {
+    std::printf("FAIL initial cache sizes\n");
+    return 1;
+  }
+  if (!check(ctx.copy_to_buffer(dc.recurrent_r_cache, r0.data(), r0.size() * 4), "r0") ||
+      !check(ctx.copy_to_buffer(dc.recurrent_s_cache, s0.data(), s0.size() * 4), "s0")) {
+    return 1;
+  }
+  auto out = ctx.make_buffer(tokens * plan.value().linear_inner_size * 4);
+  if (!check(out.status(), "output")) {
+    return 1;
+  }
+  q35::LinearAttentionWeights w{&conv_b, &dtb_b, &a_b, &norm_b};
+  q35::LayerWorkspace ws;
+  if (!check(q35::run_linear_attention_chunk(ctx, plan.value(), dc, w, layer, 0, qkv_b, z_b,
+                                             beta_b, alpha_b, tokens, 1e-6f, order, ws,
+                                             out.value()),
+             "run_linear_attention_chunk")) {
+    return 1;
+  }
+  std::vector<float> y, r1, s1;
+  if (!download(ctx, out.value(), y) || !download(ctx, dc.recurrent_r_cache, r1) ||
+      !download(ctx, dc.recurrent_s_cache, s1)) {
+    return 1;
+  }
+  write_file(dir + "/out.f32", y);
+  write_file(dir + "/r1.f32", r1);
+  write_file(dir + "/s1.f32", s1);
+  std::printf("linear done\n");
+  return 0;
+}
+
+int run_full(const std::string& dir, q35::OpOrder order) {
+  std::vector<long long> meta;  // tokens, start_position, attention_layer, capacity
+  if (!read_meta(dir, meta) || meta.size() < 4) {
+    std::printf("FAIL meta\n");
+    return 1;
+  }
+  const std::size_t tokens = (std::size_t)meta[0];
+  const std::size_t start = (std::size_t)meta[1];
+  const std::size_t layer = (std::size_t)meta[2];
+  auto ctx_r = HipContext::create();
+  if (!check(ctx_r.status(), "create")) {
+    return 1;
+  }
+  const HipContext& ctx = ctx_r.value();
+  q35::RuntimeOptions options;
+  options.context_tokens = (std::size_t)meta[3];
+  auto plan = q35::build_execution_plan(q35::qwen35_0_8b_shape(), start + tokens, options);
+  if (!check(plan.status(), "plan")) {
+    return 1;
+  }
+  auto cache = q35::allocate_device_cache(ctx, plan.value());
+  if (!check(cache.status(), "allocate_device_cache")) {
+    return 1;
+  }
+  std::vector<float> qg, key, value, qn, kn;
+  std::vector<std::uint16_t> kc0, vc0;
+  if (!read_file(dir + "/qg.f32", qg) || !read_file(dir + "/key.f32", key) ||
+      !read_file(dir + "/value.f32", value) || !read_file(dir + "/q_norm.f32", qn) ||
+      !read_file(dir + "/k_norm.f32", kn) || !read_file(dir + "/kc0.u16", kc0) ||
+      !read_file(dir + "/vc0.u16", vc0)) {
+    return 1;
+  }
+  q35::DeviceCache& dc = cache.value();
+  if (kc0.size() * 2 != dc.key_cache.byte_size() || vc0.size() * 2 != dc.value_cache.byte_size()) {
+    std::printf("FAIL initial cache sizes\n");
+    return 1;
+  }
+  if (!check(ctx.copy_to_buffer(dc.key_cache, kc0.data(), kc0.size() * 2), "kc0") ||
+      !check(ctx.copy_to_buffer(dc.value_cache, vc0.data(), vc0.size() * 2), "vc0")) {
+    return 1;
+  }
+  HipBuffer qg_b, key_b, value_b, qn_b, kn_b;
+  if (!upload(ctx, qg, qg_b) || !upload(ctx, key, key_b) || !upload(ctx, value, value_b) ||
+      !upload(ctx, qn, qn_b) || !upload(ctx, kn, kn_b)) {
+    return 1;
+  }
+  const q35::ExecutionPlan& p = plan.value();
+  auto out = ctx.make_buffer(tokens * p.attention_heads * p.head_dim * 4);
+  if (!check(out.status(), "output")) {
+    return 1;
+  }
+  q35::FullAttentionWeights w{&qn_b, &kn_b};
+  q35::LayerWorkspace ws;
+  // Qwen3.5 MRoPE sections and rope theta (qwen3-5-0-8b-llama-cpp-ops.md:64).
+  const std::array<std::size_t, 4> sections{11, 11, 10, 0};
+  if (!check(q35::run_full_attention_chunk(ctx, p, dc, w, layer, qg_b, key_b, value_b, tokens,
+                                           start, start, sections, 1e7f, 1e-6f, nullptr, order,
+                                           ws, out.value()),
+             "run_full_attention_chunk")) {
+    return 1;
+  }
+  std::vector<float> y;
+  std::vector<std::uint16_t> kc1, vc1;
+  if (!download(ctx, out.value(), y) || !download(ctx, dc.key_cache, kc1) ||
+      !download(ctx, dc.value_cache, vc1)) {
+    return 1;
+  }
+  write_file(dir + "/out.f32", y);
+  write_file(dir + "/kc1.u16", kc1);
+  write_file(dir + "/vc1.u16", vc1);
+  std::printf("full done\n");
+  return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const std::string mode = argc > 1 ? argv[1] : "plan";
+  if (mode == "plan") {
+    return run_plan();
+  }
+  if (argc < 4) {
+    std::printf("usage: qwen35_driver_check plan | linear <dir> <order> | full <dir> <order>\n");
+    return 2;
+  }
+  const q35::OpOrder order =
+    std::string(argv[3]) == "fused" ? q35::OpOrder::fused : q35::OpOrder::reference;
+  if (mode == "linear") {
+    return run_linear(argv[2], order);
+  }
+  if (mode == "full") {
+    return run_full(argv[2], order);
+  }
+  std::printf("unknown mode %s\n", mode.c_str());
+  return 2;
+}
