@@ -258,7 +258,11 @@ namespace detail {
 // attention output that feeds attn_output:
 //   q_gate [tokens][heads][2 * head_dim] (per head the query, then its gate:
 //   the GGUF's interleaved layout); key, value [tokens][kv_heads * head_dim]
-//   (key is normalised and rotated in place); output [tokens][heads * head_dim].
+//   (with OpOrder::reference key is normalised and rotated in place, as in the
+//   reference; OpOrder::fused with an F16 cache leaves it unchanged); output
+//   [tokens][heads * head_dim].
+// OpOrder::fused with an F16 cache issues two launches: the fused prologue
+// (split, q/k RMSNorm, MRoPE, K/V append) and attention with the output gate.
 // K and V are appended to full-attention layer `attention_layer` of the cache
 // at positions start_position .. start_position + tokens - 1, and attention
 // runs causally over positions 0 .. start_position + t.  `positions` (int32
@@ -309,6 +313,21 @@ namespace detail {
   }
   HipBuffer& qb = *query.value();
   HipBuffer& gb = *gate.value();
+
+  if (order == OpOrder::fused && cache.kv_cache_f16) {
+    const HipBuffer none;
+    Status s = ctx.qwen35_attention_prologue_f16_kv(
+      q_gate, key, value, *w.q_norm, *w.k_norm, positions != nullptr ? *positions : none,
+      mrope_start_position, cache.key_cache, cache.value_cache, attention_layer, start_position,
+      tokens, capacity, heads, kv_heads, head_dim, mrope_dims, mrope_sections[0],
+      mrope_sections[1], mrope_sections[2], mrope_sections[3], rope_theta, rms_eps, qb, gb);
+    if (!s.is_ok()) {
+      return s;
+    }
+    return ctx.attention_f32_batched_f16_kv_gated(qb, cache.key_cache, cache.value_cache, gb,
+                                                  attention_layer, start_position, tokens,
+                                                  capacity, heads, kv_heads, head_dim, output);
+  }
 
   // :3229-3268 split of the joint projection, q and k RMSNorm.
   Status s = ctx.copy_f32_rows(q_gate, qb, tokens * heads, head_dim, 2 * head_dim, 0, head_dim, 0);
@@ -371,11 +390,6 @@ namespace detail {
     return s;
   }
   // :3328-3355 attention, then the sigmoid output gate.
-  if (order == OpOrder::fused && cache.kv_cache_f16) {
-    return ctx.attention_f32_batched_f16_kv_gated(qb, cache.key_cache, cache.value_cache, gb,
-                                                  attention_layer, start_position, tokens,
-                                                  capacity, heads, kv_heads, head_dim, output);
-  }
   s = cache.kv_cache_f16
         ? ctx.attention_f32_batched_f16_kv(qb, cache.key_cache, cache.value_cache, attention_layer,
                                            start_position, tokens, capacity, heads, kv_heads,

@@ -155,6 +155,26 @@ KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv_gated(
   size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim,
   kraken_buffer output);
 
+/* The full-attention prologue of run_qwen35_full_attention_layer_chunk
+ * (qwen35_runtime.cpp:3229-3326) fused into one launch; no single MpsContext
+ * method corresponds.  It replaces, with the same arithmetic:
+ *   copy_f32_rows x2 (split of q_gate [tokens][heads][2*head_dim], per head the
+ *   query then its gate) -> query_out, gate_out [tokens][heads][head_dim];
+ *   qk_norm_f32_f32_batched of the query (q_norm) and key (k_norm) rows;
+ *   mrope_f32_in_place of both (n_dims, sections, theta);
+ *   copy_f32_rows_to_f16 of key and value [tokens][kv_heads*head_dim] into the
+ *   F16 caches at element (layer*capacity_tokens + start_position)*kv_dim.
+ * positions is int32 [4][tokens]; with positions.data == NULL every row holds
+ * mrope_start_position + t (make_qwen35_mrope_positions, qwen35_runtime.cpp:
+ * 1848-1877).  key and value are not modified.  head_dim <= 256. */
+KRAKEN_API int kraken_hip_qwen35_attention_prologue_f16_kv(
+  kraken_hip_context* context, kraken_buffer q_gate, kraken_buffer key, kraken_buffer value,
+  kraken_buffer q_norm, kraken_buffer k_norm, kraken_buffer positions,
+  size_t mrope_start_position, kraken_buffer key_cache, kraken_buffer value_cache, size_t layer,
+  size_t start_position, size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads,
+  size_t head_dim, size_t n_dims, size_t section_0, size_t section_1, size_t section_2,
+  size_t section_3, float theta, float eps, kraken_buffer query_out, kraken_buffer gate_out);
+
 /* ------------------------------------------------------ gated delta net -- */
 
 /* MpsContext::gated_delta_net_f32_batched_in_place_at (mps_backend.hpp:296-300;

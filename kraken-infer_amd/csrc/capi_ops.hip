@@ -736,6 +736,105 @@ KRAKEN_API int kraken_hip_mrope_f32_in_place(kraken_hip_context* ctx, kraken_buf
   return finish_launch(ctx, "HIP MRoPE command failed: ");
 }
 
+KRAKEN_API int kraken_hip_qwen35_attention_prologue_f16_kv(
+  kraken_hip_context* ctx, kraken_buffer q_gate, kraken_buffer key, kraken_buffer value,
+  kraken_buffer q_norm, kraken_buffer k_norm, kraken_buffer positions,
+  size_t mrope_start_position, kraken_buffer key_cache, kraken_buffer value_cache, size_t layer,
+  size_t start_position, size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads,
+  size_t head_dim, size_t n_dims, size_t section_0, size_t section_1, size_t section_2,
+  size_t section_3, float theta, float eps, kraken_buffer query_out, kraken_buffer gate_out) {
+  KRAKEN_TRY(check_context(ctx));
+  if (tokens == 0 || heads == 0 || kv_heads == 0 || head_dim == 0 || capacity_tokens == 0) {
+    return invalid("HIP attention prologue dimensions must be positive");
+  }
+  if (heads % kv_heads != 0) {
+    return invalid("HIP attention prologue heads must be divisible by kv_heads");
+  }
+  if (head_dim > 256u) {
+    return invalid("HIP attention prologue head_dim exceeds 256");
+  }
+  if (n_dims == 0 || n_dims > head_dim || n_dims % 2u != 0) {
+    return invalid("HIP MRoPE dimensions are invalid");
+  }
+  size_t sections = 0;
+  if (!checked_add(section_0, section_1, sections) ||
+      !checked_add(sections, section_2, sections) ||
+      !checked_add(sections, section_3, sections)) {
+    return invalid("HIP MRoPE sections overflow");
+  }
+  if (sections == 0) {
+    return invalid("HIP MRoPE sections must not all be zero");
+  }
+  size_t key_count = 0;
+  if (!checked_add(start_position, tokens, key_count) || key_count > capacity_tokens) {
+    return invalid("HIP attention prologue chunk exceeds KV cache capacity");
+  }
+  size_t attn_dim = 0, kv_dim = 0, query_values = 0, kv_values = 0, cache_rows = 0,
+         cache_values = 0, joint_values = 0, position_count = 0;
+  if (!checked_mul(heads, head_dim, attn_dim) || !checked_mul(kv_heads, head_dim, kv_dim) ||
+      !checked_mul(tokens, attn_dim, query_values) ||
+      !checked_mul(query_values, 2u, joint_values) ||
+      !checked_mul(tokens, kv_dim, kv_values) || layer == SIZE_MAX ||
+      !checked_mul(layer + 1u, capacity_tokens, cache_rows) ||
+      !checked_mul(cache_rows, kv_dim, cache_values) || !checked_mul(tokens, 4u, position_count)) {
+    return invalid("HIP attention prologue value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(q_gate, joint_values, "attention prologue q_gate"));
+  KRAKEN_TRY(validate_f32(key, kv_values, "attention prologue key"));
+  KRAKEN_TRY(validate_f32(value, kv_values, "attention prologue value"));
+  KRAKEN_TRY(validate_f32(q_norm, head_dim, "attention prologue q_norm"));
+  KRAKEN_TRY(validate_f32(k_norm, head_dim, "attention prologue k_norm"));
+  if (positions.data != nullptr) {
+    KRAKEN_TRY(validate_i32(positions, position_count, "attention prologue positions"));
+  }
+  KRAKEN_TRY(validate_f16(key_cache, cache_values, "attention prologue key cache"));
+  KRAKEN_TRY(validate_f16(value_cache, cache_values, "attention prologue value cache"));
+  KRAKEN_TRY(validate_f32(query_out, query_values, "attention prologue query output"));
+  KRAKEN_TRY(validate_f32(gate_out, query_values, "attention prologue gate output"));
+  KRAKEN_TRY(check_u32(tokens, "attention prologue tokens"));
+  KRAKEN_TRY(check_u32(heads + 2u * kv_heads, "attention prologue head slots"));
+  KRAKEN_TRY(check_u32(n_dims, "MRoPE n_dims"));
+  KRAKEN_TRY(check_u32(sections, "MRoPE sections"));
+  if (positions.data == nullptr) {
+    size_t last = 0;
+    if (!checked_add(mrope_start_position, tokens - 1u, last) ||
+        last > (size_t)std::numeric_limits<int32_t>::max()) {
+      return invalid("Qwen3.5 batched MRoPE position exceeds int32 range");
+    }
+  }
+
+  PrologueArgs a{};
+  a.q_gate = static_cast<const float*>(q_gate.data);
+  a.key = static_cast<const float*>(key.data);
+  a.value = static_cast<const float*>(value.data);
+  a.q_norm = static_cast<const float*>(q_norm.data);
+  a.k_norm = static_cast<const float*>(k_norm.data);
+  a.positions = static_cast<const int32_t*>(positions.data);
+  a.mrope_start = (uint32_t)mrope_start_position;
+  a.key_cache = static_cast<_Float16*>(key_cache.data);
+  a.value_cache = static_cast<_Float16*>(value_cache.data);
+  a.cache_offset = (layer * capacity_tokens + start_position) * kv_dim;
+  a.query_out = static_cast<float*>(query_out.data);
+  a.gate_out = static_cast<float*>(gate_out.data);
+  a.tokens = (uint32_t)tokens;
+  a.heads = (uint32_t)heads;
+  a.kv_heads = (uint32_t)kv_heads;
+  a.head_dim = (uint32_t)head_dim;
+  a.n_dims = (uint32_t)n_dims;
+  a.s0 = (uint32_t)section_0;
+  a.s1 = (uint32_t)section_1;
+  a.s2 = (uint32_t)section_2;
+  a.s3 = (uint32_t)section_3;
+  a.theta = theta;
+  a.eps = eps;
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_attention_prologue(a, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP attention prologue launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP attention prologue command failed: ");
+}
+
 KRAKEN_API int kraken_hip_copy_f32_rows_to_f16(kraken_hip_context* ctx, kraken_buffer source,
                                                kraken_buffer destination, size_t rows,
                                                size_t row_size, size_t source_stride,

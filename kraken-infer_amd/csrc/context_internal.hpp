@@ -217,6 +217,26 @@ hipError_t launch_split_qkv_l2(const float* source, float* q, float* k, float* v
                                uint32_t head_dim, float eps, hipStream_t stream);
 hipError_t launch_l2_norm(float* values, uint32_t rows, uint32_t row_size, float eps,
                           hipStream_t stream);
+// Fused full-attention prologue (attention_prologue.hip): Q/gate split, q and k
+// RMSNorm, MRoPE of q and k, K/V append to the F16 cache.
+struct PrologueArgs {
+  const float* q_gate;       // [tokens][heads][2 * head_dim] (query, then gate)
+  const float* key;          // [tokens][kv_heads * head_dim]
+  const float* value;        // [tokens][kv_heads * head_dim]
+  const float* q_norm;       // [head_dim]
+  const float* k_norm;       // [head_dim]
+  const int32_t* positions;  // [4][tokens], or null: mrope_start + t in every row
+  uint32_t mrope_start;
+  _Float16* key_cache;       // f16; rows written from element cache_offset
+  _Float16* value_cache;
+  size_t cache_offset;       // (layer * capacity + start_position) * kv_dim
+  float* query_out;          // [tokens][heads][head_dim]
+  float* gate_out;           // [tokens][heads][head_dim]
+  uint32_t tokens, heads, kv_heads, head_dim, n_dims, s0, s1, s2, s3;
+  float theta, eps;
+};
+hipError_t launch_attention_prologue(const PrologueArgs& a, hipStream_t stream);
+
 hipError_t launch_rms_norm_heads(float* values, const float* weight, const float* gate,
                                  uint32_t tokens, uint32_t heads, uint32_t head_dim,
                                  float eps, hipStream_t stream);

@@ -266,3 +266,54 @@ def test_copy_rules(vctx):
     assert code == kh.INVALID_ARGUMENT and "destination must not be null" in msg
     code, msg = status(vctx, "zero_buffer", fake(16), 32)
     assert code == kh.INVALID_ARGUMENT and "zero size exceeds buffer size" in msg
+
+
+# ------------------------------------------------ fused attention prologue --
+
+def prologue_args(tokens=4, start=10, cap=16, heads=8, kv_heads=2, d=256, layer=1, n_dims=64,
+                  sections=(11, 11, 10, 0), positions=True, **sizes):
+    qv = tokens * heads * d
+    kvv = tokens * kv_heads * d
+    cache = (layer + 1) * cap * kv_heads * d
+
+    def b(name, n):
+        return fake(sizes.get(name, n))
+
+    pos = b("pos", 4 * 4 * tokens) if positions else kh.KrakenBuffer(None, 0)
+    return (b("qg", 4 * 2 * qv), b("k", 4 * kvv), b("v", 4 * kvv), b("qn", 4 * d),
+            b("kn", 4 * d), pos, start, b("kc", 2 * cache), b("vc", 2 * cache), layer, start,
+            tokens, cap, heads, kv_heads, d, n_dims, *sections, 1e7, 1e-6, b("qo", 4 * qv),
+            b("go", 4 * qv))
+
+
+def test_prologue_accepts_valid(vctx):
+    for kw in ({}, dict(positions=False), dict(tokens=1, start=15), dict(d=128, n_dims=128,
+                                                                         heads=4, kv_heads=4)):
+        code, msg = status(vctx, "qwen35_attention_prologue_f16_kv", *prologue_args(**kw))
+        assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED), kw
+
+
+@pytest.mark.parametrize("kw,fragment", [
+    (dict(tokens=0), "dimensions must be positive"),
+    (dict(heads=6, kv_heads=4), "divisible by kv_heads"),
+    (dict(d=512, n_dims=64), "head_dim exceeds 256"),
+    (dict(n_dims=63), "MRoPE dimensions are invalid"),
+    (dict(n_dims=258), "MRoPE dimensions are invalid"),
+    (dict(sections=(0, 0, 0, 0)), "sections must not all be zero"),
+    (dict(start=13), "exceeds KV cache capacity"),
+    (dict(qg=4 * 2 * 4 * 8 * 256 - 4), "q_gate buffer is too small"),
+    (dict(kc=2 * 2 * 16 * 512 - 2), "key cache buffer is too small"),
+    (dict(pos=4 * 4 * 4 - 4), "positions buffer is too small"),
+    (dict(go=16), "gate output buffer is too small"),
+])
+def test_prologue_rejects(vctx, kw, fragment):
+    code, msg = status(vctx, "qwen35_attention_prologue_f16_kv", *prologue_args(**kw))
+    assert code == kh.INVALID_ARGUMENT
+    assert fragment in msg, msg
+
+
+def test_prologue_generated_positions_must_fit_int32(vctx):
+    args = list(prologue_args(positions=False))
+    args[6] = (1 << 31) - 2  # mrope_start_position: the last of 4 tokens exceeds int32
+    code, msg = status(vctx, "qwen35_attention_prologue_f16_kv", *args)
+    assert code == kh.INVALID_ARGUMENT and "exceeds int32 range" in msg
