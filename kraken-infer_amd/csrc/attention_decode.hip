@@ -36,6 +36,8 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
+#include <type_traits>
 
 #include "context_internal.hpp"
 #include "device_common.hpp"
@@ -488,6 +490,296 @@ __global__ __launch_bounds__((64 * RowShape<D, KV>::W)) void attention_decode_ke
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA variant: head_dim 256, f16 cache, G <= 4 query heads per KV head.
+//
+// The vector kernel above spends about 80 VALU operations per 16-byte K/V
+// chunk (f16 -> f32 conversions, G dot-product FMAs and 32-lane reductions,
+// G P*V FMAs).  With every SIMD busy it tops out near 5.2 TB/s on a large
+// batched decode (VALU active 75% of the time, measured).  This kernel moves
+// the arithmetic onto the matrix cores so that the stream is bound by memory.
+//  * A workgroup of 4 waves owns one (token, kv_head, key split) work item, as
+//    above; wave w takes the split's 16-key tiles w, w + 4, ...  Each wave
+//    copies its tiles' K and V rows straight into two LDS stages of its own
+//    (buffer_load ... lds), so the loop has no barriers and the compiler's wait
+//    counts are not involved: the kernel awaits the copies itself.
+//  * S^T = K Q^T on v_mfma_f32_16x16x32_f16.  A = the tile's 16 key rows (k =
+//    head dims, 16-byte LDS fragments), B = the G query heads as columns.  The
+//    query, pre-scaled into the log2 domain, is split into f16 hi + lo (lo =
+//    q - hi, rounded again), so K (exact in f16) times hi + lo reproduces the
+//    f32 dot product to about 2^-22 relative.
+//  * The S^T accumulator (lane l: head l % 16, keys 4 (l / 16) + r) is already
+//    the A operand of O += P V on v_mfma_f32_16x16x16_f16 (k = keys), with P
+//    split into f16 hi + lo the same way.  V^T fragments come from LDS through
+//    the transposing read ds_read_b64_tr_b16.
+//  * Online softmax per head with the vector kernel's wave-uniform lazy
+//    rescale; wave partials merge through LDS and splits in the same second
+//    pass, in the same partial format.
+// LDS rows are XOR-swizzled in 16-byte chunks (K: chunk ^ (row & 7); V: chunk ^
+// 2 (row & 3)) so that both fragment reads are free of bank conflicts.
+// ---------------------------------------------------------------------------
+constexpr int kMD = 256;
+constexpr int kMTile = 16;                        // keys per tile
+constexpr int kMWaves = 4;
+constexpr int kMStages = 2;                       // tiles in flight per wave
+constexpr int kMTileHalfs = kMTile * kMD;         // 8 KB per K or V tile
+constexpr int kMCopiesPerTile = kMTile;           // 1 KB copies per tile: 8 for K, 8 for V
+
+typedef float float4v_t __attribute__((ext_vector_type(4)));
+
+template <int G>
+__global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(DecodeParams p) {
+  static_assert(G == 1 || G == 2 || G == 4, "query heads per KV head (rows 0..3 of a tile)");
+  // Per wave and stage: the K tile, then the V tile.  After the key loop the
+  // region holds the wave partials for the merge.
+  __shared__ __attribute__((aligned(16))) half_t s_kv[kMWaves][kMStages][2][kMTileHalfs];
+  __shared__ float s_m[kMWaves][G];
+  __shared__ float s_l[kMWaves][G];
+  static_assert(sizeof(float) * kMWaves * G * kMD <= sizeof(s_kv), "merge area");
+  float(*s_o)[G * kMD] = reinterpret_cast<float(*)[G * kMD]>(&s_kv[0][0][0][0]);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  uint32_t split = blockIdx.x;
+  uint32_t kvh = blockIdx.y;
+  uint32_t token = blockIdx.z;
+  const bool ragged = p.seq_positions != nullptr;
+  if (ragged) {
+    const uint2 item = p.work_items[blockIdx.x];
+    if (item.x == 0xffffffffu) {
+      return;  // past the last work item
+    }
+    token = item.x;
+    kvh = item.y >> 16;
+    split = item.y & 0xffffu;
+  }
+  const uint32_t n_keys = token_keys(p.seq_positions, p.start_position, token);
+  const uint32_t key_begin = split * p.keys_per_split;
+  if (key_begin >= n_keys) {
+    return;  // empty split (whole workgroup)
+  }
+  const uint32_t count = min(n_keys, key_begin + p.keys_per_split) - key_begin;
+
+  const size_t row_stride = (size_t)p.kv_heads * kMD;
+  const uint32_t row_bytes = (uint32_t)(row_stride * sizeof(half_t));
+  const uint64_t seq_elem = ragged ? p.seq_kv_offsets[token]
+                                   : (uint64_t)p.layer * p.capacity_tokens * row_stride;
+  const uint64_t first_elem = seq_elem + (uint64_t)kvh * kMD;
+  uint32_t span_bytes = count * row_bytes;
+  if (ragged) {
+    // Device-side offsets are not checked on the host: the range also ends at
+    // the pool's end (and is empty for rows that are not whole 16-byte chunks),
+    // so a bad offset reads zeros instead of faulting.
+    const uint64_t split_elem = first_elem + (uint64_t)key_begin * row_stride;
+    const uint64_t avail =
+      split_elem < p.pool_elems ? (p.pool_elems - split_elem) * sizeof(half_t) : 0u;
+    span_bytes = (seq_elem * sizeof(half_t)) % 16u != 0
+                   ? 0u
+                   : (uint32_t)min((uint64_t)span_bytes, avail);
+  }
+  const half_t* kbase =
+    static_cast<const half_t*>(p.key_cache) + first_elem + (size_t)key_begin * row_stride;
+  const half_t* vbase =
+    static_cast<const half_t*>(p.value_cache) + first_elem + (size_t)key_begin * row_stride;
+  const i32x4_t krs = rsrc_words(kbase, span_bytes);
+  const i32x4_t vrs = rsrc_words(vbase, span_bytes);
+
+  // Query fragments (B operand of S^T): lane (head r16, kq) holds dims
+  // 32 s + 8 kq .. + 7 of step s, scaled into the log2 domain, as hi + lo.
+  half8_t qhi[8], qlo[8];
+  {
+    const int g = r16 < G ? r16 : 0;
+    const float qscale = r16 < G ? p.scale_log2 : 0.0f;
+    const float* qh = p.query + ((size_t)token * p.heads + kvh * G + g) * kMD + 8 * kq;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const float4 a = *reinterpret_cast<const float4*>(qh + 32 * s);
+      const float4 b = *reinterpret_cast<const float4*>(qh + 32 * s + 4);
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float x = v[j] * qscale;
+        const half_t hi = static_cast<half_t>(x);
+        qhi[s][j] = hi;
+        qlo[s][j] = static_cast<half_t>(x - static_cast<float>(hi));
+      }
+    }
+  }
+
+  // Copies tile t (keys 16 t .. 16 t + 15 of the split) of K and V into stage
+  // st of this wave: 8 + 8 copies of 1 KB, copy c filling rows 2 c, 2 c + 1.
+  // Rows at or past the split's end read as zeros (resource range check).
+  const uint32_t copy_row = (uint32_t)(lane >> 5);
+  const uint32_t chunk = (uint32_t)(lane & 31);
+  auto issue_tile = [&](uint32_t t, int st) __attribute__((always_inline)) {
+    half_t* kdst = &s_kv[wave][st][0][0];
+    half_t* vdst = &s_kv[wave][st][1][0];
+#pragma unroll
+    for (int c = 0; c < kMTile / 2; ++c) {
+      const uint32_t row = 2u * c + copy_row;
+      const uint32_t base = (kMTile * t + row) * row_bytes;
+      copy16_to_lds(krs, base + 16u * (chunk ^ (row & 7u)), kdst + c * 2 * kMD);
+      copy16_to_lds(vrs, base + 16u * (chunk ^ (2u * (row & 3u))), vdst + c * 2 * kMD);
+    }
+  };
+
+  float m[G];  // wave-uniform reference max per head (log2 domain)
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+  }
+  float lpart = 0.0f;  // this lane's share of head r16's denominator
+  float4v_t o[16];     // O tile n: lane l holds dim 16 n + l % 16 of heads 4 (l / 16) + r
+#pragma unroll
+  for (int n = 0; n < 16; ++n) {
+    o[n] = float4v_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const uint32_t ntiles = (count + kMTile - 1) / kMTile;
+  issue_tile((uint32_t)wave, 0);
+  issue_tile((uint32_t)wave + kMWaves, 1);
+  int st = 0;
+  for (uint32_t t = (uint32_t)wave; t < ntiles; t += kMWaves) {
+    // Stage st holds tile t once only the other stage's copies are in flight.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kMCopiesPerTile) : "memory");
+    const half_t* ks = &s_kv[wave][st][0][0];
+    const half_t* vs = &s_kv[wave][st][1][0];
+
+    // S^T = K Q^T (keys x heads).
+    float4v_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const half8_t kf = *reinterpret_cast<const half8_t*>(
+        ks + r16 * kMD + 8 * ((4 * s + kq) ^ (r16 & 7)));
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qhi[s], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qlo[s], sacc, 0, 0, 0);
+    }
+
+    // Softmax: lane holds keys 16 t + 4 kq + r of head r16.
+    float sc[4];
+    bool valid[4];
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      valid[r] = r16 < G && kMTile * t + 4u * kq + r < count;
+      sc[r] = valid[r] ? sacc[r] : -INFINITY;
+      cmax = fmaxf(cmax, sc[r]);
+    }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+    float corr_lane = 1.0f;
+    float m_lane = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float bm = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                   __builtin_bit_cast(int, cmax), g));
+      if (bm > m[g] + kRescaleSlack) {  // wave-uniform
+        const float corr = fast_exp2(m[g] - bm);  // 0 on the head's first valid tile
+        m[g] = bm;
+#pragma unroll
+        for (int n = 0; n < 16; ++n) {
+          o[n][g] *= corr;  // head g is row g: register g of lanes 0..15
+        }
+        corr_lane = r16 == g ? corr : corr_lane;
+      }
+      m_lane = r16 == g ? m[g] : m_lane;
+    }
+    lpart *= corr_lane;
+    half4_t phi, plo;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pr = valid[r] ? fast_exp2(sc[r] - m_lane) : 0.0f;
+      lpart += pr;
+      const half_t h = static_cast<half_t>(pr);
+      phi[r] = h;
+      plo[r] = static_cast<half_t>(pr - static_cast<float>(h));
+    }
+
+    // O += P V: lane 4 e + q of group kq points at row 4 kq + e, columns
+    // 16 n + 4 q .. + 3; the transposing read returns column 16 n + l % 16
+    // of rows 4 kq .. 4 kq + 3.
+    const int vrow = 4 * kq + (r16 >> 2);
+    const int q = r16 & 3;
+    const half_t* vrow_p = vs + vrow * kMD + 4 * (q & 1);
+    const int vswz = 2 * (vrow & 3);
+#pragma unroll
+    for (int n = 0; n < 16; ++n) {
+      const half4_t vf = read_tr16(vrow_p + 8 * ((2 * n + (q >> 1)) ^ vswz));
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, vf, o[n], 0, 0, 0);
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, vf, o[n], 0, 0, 0);
+    }
+
+    // Refill this stage with tile t + 8 once its LDS reads have returned.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    issue_tile(t + kMStages * kMWaves, st);
+    st ^= 1;
+  }
+  // No copy may land in a stage after the stages are reused below.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // Wave partial: head r16's denominator over the four lane groups.
+  float lw = lpart;
+  lw += __shfl_xor(lw, 16, 64);
+  lw += __shfl_xor(lw, 32, 64);
+  __syncthreads();  // every wave is done with its stages
+  if (lane < G) {
+    s_l[wave][lane] = lw;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      s_m[wave][g] = m[g];
+    }
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int n = 0; n < 16; ++n) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        s_o[wave][g * kMD + 16 * n + lane] = o[n][g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Workgroup merge of the wave partials, as in the vector kernel.
+  constexpr int kThreads = 64 * kMWaves;
+  constexpr int kOutPerThread = G * kMD / kThreads;
+  const size_t tk = (size_t)token * p.kv_heads + kvh;
+  float* po = p.part_o + (tk * p.splits + split) * (size_t)(G * kMD);
+  float* pml = p.part_ml + (tk * p.splits + split) * (size_t)(G * 2);
+#pragma unroll
+  for (int k = 0; k < kOutPerThread; ++k) {
+    const int idx = tid + k * kThreads;
+    const int g = idx / kMD;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kMWaves; ++w) {
+      mx = fmaxf(mx, s_m[w][g]);
+    }
+    float acc = 0.0f;
+    float den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kMWaves; ++w) {
+      const float wt = s_m[w][g] == -INFINITY ? 0.0f : fast_exp2(s_m[w][g] - mx);
+      acc = fmaf(wt, s_o[w][idx], acc);
+      den = fmaf(wt, s_l[w][g], den);
+    }
+    if (p.splits == 1) {
+      write_final<kMD, G>(p, token, kvh, idx, den, acc);
+    } else {
+      po[idx] = acc;
+      if (idx % kMD == 0) {
+        pml[g * 2 + 0] = mx;
+        pml[g * 2 + 1] = den;
+      }
+    }
+  }
+}
+
 // Split merge: one workgroup per (token, head, 16-dim slice).  256 threads =
 // 4 float4 chunks x 64 split subsets; every thread issues all of its (<= 4)
 // partial loads before using any.  The global max and the weighted sums are
@@ -792,12 +1084,40 @@ size_t data_bytes(const AttentionArgs& a, const SplitPlan& plan) {
   return (partial_bytes(a, plan) + 255u) / 256u * 256u + work_item_count(a, plan) * 8u;
 }
 
+// The MFMA kernel serves head_dim 256 with an f16 cache and up to 4 query heads
+// per KV head, for splits of at least kMfmaMinKeys keys (8 tiles per wave).
+// On shorter splits (batch-1 decode, where a split is a few dozen keys) the
+// vector kernel's single 1024-thread pass is faster: the MFMA kernel's copy,
+// wait and merge chain is then its whole run time (measured: 11.0 vs 12.5 us
+// per C1 step at 4096 keys).  KRAKEN_DECODE_KERNEL=mfma or =vector forces one.
+constexpr uint32_t kMfmaMinKeys = 512;
+
+bool mfma_decode_enabled(uint32_t keys_per_split) {
+  const char* v = std::getenv("KRAKEN_DECODE_KERNEL");
+  if (v != nullptr && std::strcmp(v, "vector") == 0) {
+    return false;
+  }
+  if (v != nullptr && std::strcmp(v, "mfma") == 0) {
+    return true;
+  }
+  return keys_per_split >= kMfmaMinKeys;
+}
+
 template <int D, int G, typename KV>
 hipError_t launch_tuned(const DecodeParams& p, hipStream_t stream) {
   // Ragged: one workgroup per work-list entry (see ragged_plan_kernel).
   const dim3 grid = p.work_items != nullptr ? dim3(p.splits * p.kv_heads * p.tokens)
                                             : dim3(p.splits, p.kv_heads, p.tokens);
-  attention_decode_kernel<D, G, KV><<<grid, 64 * RowShape<D, KV>::W, 0, stream>>>(p);
+  bool mfma = false;
+  if constexpr (D == kMD && std::is_same_v<KV, half_t> && (G == 1 || G == 2 || G == 4)) {
+    mfma = mfma_decode_enabled(p.keys_per_split);
+    if (mfma) {
+      attention_decode_mfma_kernel<G><<<grid, 64 * kMWaves, 0, stream>>>(p);
+    }
+  }
+  if (!mfma) {
+    attention_decode_kernel<D, G, KV><<<grid, 64 * RowShape<D, KV>::W, 0, stream>>>(p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) {
     return e;

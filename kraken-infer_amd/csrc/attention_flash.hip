@@ -73,16 +73,6 @@ constexpr int kRowHalfs = kD;          // an LDS row is a whole 512-byte key row
 constexpr int kTileHalfs = kKTile * kRowHalfs;  // 32 KB per K or V tile
 constexpr float kRescaleSlack = 8.0f;  // log2 headroom before O is rescaled
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef short short4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) short4_t lds_short4_t;
-
-// Transposing 8-byte LDS read (ds_read_b64_tr_b16) of four 16-bit values.
-__device__ __forceinline__ half4_t read_tr16(const half_t* lds_address) {
-  return __builtin_bit_cast(half4_t,
-                            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)lds_address));
-}
-
 struct FlashParams {
   const float* query;
   const half_t* key_cache;
@@ -122,40 +112,6 @@ __device__ __forceinline__ void pipeline_mfma() {
     }
   }
 }
-
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-// Buffer resource words (raw, stride 0) over `bytes` bytes from `base`, for the
-// inline-asm copies below; base and size are made wave-uniform.
-__device__ __forceinline__ i32x4_t rsrc_words(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  i32x4_t r;
-  r[0] = (int)__builtin_amdgcn_readfirstlane((uint32_t)a);
-  r[1] = (int)(__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xFFFFu);
-  r[2] = (int)__builtin_amdgcn_readfirstlane(bytes);
-  r[3] = 0x00020000;
-  return r;
-}
-
-// One direct-to-LDS 16-byte-per-lane copy (buffer_load_dwordx4 ... lds) to the
-// wave-uniform LDS address `lds`.  Issued as inline asm so that the compiler does
-// not make every later LDS read wait for it (it cannot tell the copy's target
-// from the stage being read); completion is awaited explicitly by
-// wait_tile_copies() before the barrier that publishes a stage.  M0 is set in the
-// same statement, with the one wait state the M0 -> LDS-DMA hazard needs; the
-// kernel has no other M0 user (checked in its ISA), so declaring the reserved
-// register clobbered is safe here.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t voffset, const half_t* lds) {
-  const uint32_t m0 =
-    __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(m0), "v"(voffset), "s"(rsrc)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 // Per-lane byte offsets of the tile copies (loop invariant): copy i of wave w
 // fills rows 2 (i W + w) + l / 32 (l = lane) of the stage, physical chunk

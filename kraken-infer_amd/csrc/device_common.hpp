@@ -145,6 +145,54 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buffer_rsrc(const void* b
                                            0x00020000);
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Transposing 8-byte LDS read (ds_read_b64_tr_b16, gfx950) of four 16-bit
+// values.  Within each group of 16 lanes, result lane l' gets element e (e < 4)
+// = the 16-bit value at (address supplied by lane 4e + l'/4 of the group) +
+// (l' % 4); so if lane 4e + q points at row e, columns 4q..4q+3 of a 4 x 16
+// block, lane l' receives column l' of that block (checked on the device).
+__device__ __forceinline__ half4_t read_tr16(const half_t* lds_address) {
+  return __builtin_bit_cast(half4_t,
+                            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)lds_address));
+}
+
+// Buffer resource words (raw, stride 0) over `bytes` bytes from `base`, for the
+// inline-asm copies below; base and size are made wave-uniform.
+__device__ __forceinline__ i32x4_t rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r[0] = (int)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  r[1] = (int)(__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xFFFFu);
+  r[2] = (int)__builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// One direct-to-LDS 16-byte-per-lane copy (buffer_load_dwordx4 ... lds, gfx950):
+// lane l's 16 bytes land at the wave-uniform LDS address `lds` + 16 l; an offset
+// at or past the resource's byte count writes zeros without a memory access.
+// Issued as inline asm so that the compiler does not make every later LDS read
+// wait for it (it cannot tell the copy's target from the LDS being read); the
+// caller awaits completion with an explicit s_waitcnt vmcnt.  M0 is set in the
+// same statement, with the one wait state the M0 -> LDS-DMA hazard needs.  A
+// kernel using this must have no other M0 user (its ISA is checked for one), so
+// declaring the reserved register clobbered is safe there.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t voffset, const half_t* lds) {
+  const uint32_t m0 =
+    __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // 16-byte buffer load with the nontemporal hint (cache policy bit NT).
 __device__ __forceinline__ u32x4_t buffer_load_nt_b128(__amdgpu_buffer_rsrc_t rsrc,
                                                        uint32_t offset) {

@@ -85,6 +85,36 @@ def test_decode_chunk_shapes_and_layer_offset(hip_ctx, shape):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("shape", [
+    # tokens, start, heads, kv_heads (head_dim 256, f16 cache: the MFMA decode kernel)
+    (1, 4096, 8, 2), (1, 0, 8, 2), (1, 15, 8, 2), (1, 16, 8, 2), (1, 2047, 4, 2),
+    (7, 100, 8, 2), (33, 500, 4, 4), (5, 20, 2, 1), (1, 30000, 8, 2),
+])
+@pytest.mark.parametrize("q_scale", [1.0, 12.0])
+def test_decode_mfma_matches_vector_kernel_and_oracle(hip_ctx, monkeypatch, shape, q_scale):
+    """The MFMA decode kernel (head_dim 256, f16 KV, up to 4 query heads per KV
+    head; forced with KRAKEN_DECODE_KERNEL=mfma, since by default it takes only
+    splits of 512 keys or more) against the oracle and against the vector
+    kernel (KRAKEN_DECODE_KERNEL=vector), including keys that are not a
+    multiple of its 16-key tiles, GQA groups 1/2/4 and a sharp softmax (q
+    scaled by 12)."""
+    tokens, start, heads, kv_heads = shape
+    d = 256
+    cap = start + tokens + 2
+    print(f"decode mfma {shape} q_scale={q_scale}", flush=True)
+    q, kc, vc = make_case(6, tokens, start, cap, heads, kv_heads, d, layers=2)
+    q = (q * q_scale).astype(np.float32)
+    ref = oracle.attention_batched(q, kc, vc, 1, start, tokens, cap, heads, kv_heads, d)
+    monkeypatch.setenv("KRAKEN_DECODE_KERNEL", "mfma")
+    got = run_hip(hip_ctx, q, kc, vc, 1, start, tokens, cap, heads, kv_heads, d)
+    close(got, ref, msg=f"mfma {shape}")
+    monkeypatch.setenv("KRAKEN_DECODE_KERNEL", "vector")
+    vec = run_hip(hip_ctx, q, kc, vc, 1, start, tokens, cap, heads, kv_heads, d)
+    close(vec, ref, msg=f"vector {shape}")
+    close(got, vec, rtol=1e-3, atol=5e-4, msg=f"mfma vs vector {shape}")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("shape", [(1, 300, 16, 8, 128), (8, 64, 8, 2, 256), (3, 9, 4, 1, 64)])
 def test_f32_kv_twin(hip_ctx, shape):
     tokens, start, heads, kv_heads, d = shape

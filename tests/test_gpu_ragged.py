@@ -50,9 +50,17 @@ def attention_reference(q, kpool, vpool, offsets, positions, heads, kv_heads, d,
     return np.concatenate(out)
 
 
-@pytest.mark.parametrize("d,heads,kv_heads", [(256, 8, 2), (128, 8, 4), (64, 16, 2)])
+@pytest.mark.parametrize("d,heads,kv_heads,kernel", [
+    (256, 8, 2, None), (256, 8, 2, "vector"), (256, 4, 4, None), (128, 8, 4, None),
+    (64, 16, 2, None)])
 @pytest.mark.parametrize("gated", [False, True])
-def test_ragged_attention_matches_oracle(hip_ctx, d, heads, kv_heads, gated):
+def test_ragged_attention_matches_oracle(hip_ctx, monkeypatch, d, heads, kv_heads, kernel, gated):
+    """Head_dim 256 with an f16 pool takes the MFMA decode kernel by default (1024-key
+    splits); kernel "vector" forces the vector kernel on the same case."""
+    if kernel is None:
+        monkeypatch.delenv("KRAKEN_DECODE_KERNEL", raising=False)
+    else:
+        monkeypatch.setenv("KRAKEN_DECODE_KERNEL", kernel)
     rng = np.random.default_rng(40 + d + heads)
     # Positions around the 1024-key split boundary, tiny and long ones.
     positions = np.array([0, 1, 31, 1023, 1024, 1025, 2047, 3000, 5], np.uint32)
