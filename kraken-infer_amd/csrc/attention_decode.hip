@@ -502,7 +502,10 @@ __global__ __launch_bounds__((64 * RowShape<D, KV>::W)) void attention_decode_ke
 //    above; wave w takes the split's 16-key tiles w, w + 4, ...  Each wave
 //    copies its tiles' K and V rows straight into two LDS stages of its own
 //    (buffer_load ... lds), so the loop has no barriers and the compiler's wait
-//    counts are not involved: the kernel awaits the copies itself.
+//    counts are not involved: the kernel awaits the copies itself.  The copies
+//    carry the nontemporal hint: the KV stream is read once, and keeping it out
+//    of the caches was measured at 8% faster attention and 13% faster for the
+//    C4 block, whose GDN state then stays cached.
 //  * S^T = K Q^T on v_mfma_f32_16x16x32_f16.  A = the tile's 16 key rows (k =
 //    head dims, 16-byte LDS fragments), B = the G query heads as columns.  The
 //    query, pre-scaled into the log2 domain, is split into f16 hi + lo (lo =
@@ -621,8 +624,8 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
     for (int c = 0; c < kMTile / 2; ++c) {
       const uint32_t row = 2u * c + copy_row;
       const uint32_t base = (kMTile * t + row) * row_bytes;
-      copy16_to_lds(krs, base + 16u * (chunk ^ (row & 7u)), kdst + c * 2 * kMD);
-      copy16_to_lds(vrs, base + 16u * (chunk ^ (2u * (row & 3u))), vdst + c * 2 * kMD);
+      copy16_to_lds_nt(krs, base + 16u * (chunk ^ (row & 7u)), kdst + c * 2 * kMD);
+      copy16_to_lds_nt(vrs, base + 16u * (chunk ^ (2u * (row & 3u))), vdst + c * 2 * kMD);
     }
   };
 

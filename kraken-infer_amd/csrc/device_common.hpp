@@ -191,6 +191,17 @@ __device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t voffset, co
                : "s"(m0), "v"(voffset), "s"(rsrc)
                : "memory", "m0");
 }
+
+// The same copy with the nontemporal hint, for data read once (a KV stream).
+__device__ __forceinline__ void copy16_to_lds_nt(i32x4_t rsrc, uint32_t voffset,
+                                                 const half_t* lds) {
+  const uint32_t m0 =
+    __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :
+               : "s"(m0), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // 16-byte buffer load with the nontemporal hint (cache policy bit NT).
