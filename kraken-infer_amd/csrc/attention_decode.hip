@@ -1231,6 +1231,78 @@ __global__ __launch_bounds__(256) void attention_merge_narrow(CombineArgs p) {
   *reinterpret_cast<float4*>(p.output + out_index) = make_float4(out[0], out[1], out[2], out[3]);
 }
 
+// Many tokens with more than 16 splits (ragged batched decode): the same
+// per-thread layout as attention_merge_narrow, walking a token's splits in
+// batches of 8 (all loads of a batch in flight) with an online log-sum-exp, so
+// a token reads only its own splits' partials.  The wide merge's thousands of
+// small workgroups cost more than the partials they read at this shape.
+__global__ __launch_bounds__(256) void attention_merge_tokens(CombineArgs p) {
+  constexpr int B = 8;
+  const uint32_t chunks = p.head_dim / 4;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)p.tokens * p.heads * chunks) {
+    return;
+  }
+  const uint32_t chunk = (uint32_t)(idx % chunks);
+  const size_t th = idx / chunks;  // token * heads + head
+  const uint32_t head = (uint32_t)(th % p.heads);
+  const uint32_t token = (uint32_t)(th / p.heads);
+  const uint32_t group = p.heads / p.kv_heads;
+  const uint32_t kvh = head / group;
+  const uint32_t g = head % group;
+  const size_t base = (size_t)token * p.kv_heads + kvh;
+  const uint32_t nsp = token_splits(p, token);
+  float mx = -INFINITY;
+  float den = 0.0f;
+  float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (uint32_t s0 = 0; s0 < nsp; s0 += B) {
+    float mv[B], lv[B];
+    float4 ov[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const uint32_t s = min(s0 + j, nsp - 1u);
+      const size_t unit = (base * p.splits + s) * group + g;
+      mv[j] = p.partial_ml[unit * 2];
+      lv[j] = p.partial_ml[unit * 2 + 1];
+      ov[j] = *reinterpret_cast<const float4*>(p.partial_o + unit * p.head_dim + chunk * 4);
+    }
+    float bmx = mx;
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      if (s0 + j >= nsp) {
+        mv[j] = -INFINITY;
+      }
+      bmx = fmaxf(bmx, mv[j]);
+    }
+    const float f = mx == -INFINITY ? 0.0f : fast_exp2(mx - bmx);
+    den *= f;
+    r.x *= f;
+    r.y *= f;
+    r.z *= f;
+    r.w *= f;
+    mx = bmx;
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const float w = mv[j] == -INFINITY ? 0.0f : fast_exp2(mv[j] - mx);
+      den = fmaf(w, lv[j], den);
+      r.x = fmaf(w, ov[j].x, r.x);
+      r.y = fmaf(w, ov[j].y, r.y);
+      r.z = fmaf(w, ov[j].z, r.z);
+      r.w = fmaf(w, ov[j].w, r.w);
+    }
+  }
+  const float inv = den == 0.0f ? 0.0f : 1.0f / den;
+  const size_t out_index = th * p.head_dim + chunk * 4;
+  float out[4] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
+  if (p.gate != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      out[e] *= sigmoidf_acc(p.gate[out_index + e]);
+    }
+  }
+  *reinterpret_cast<float4*>(p.output + out_index) = make_float4(out[0], out[1], out[2], out[3]);
+}
+
 hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream) {
   if (c.splits > kMaxSplits || c.head_dim % kMergeDims != 0) {
     return hipErrorInvalidValue;
@@ -1245,6 +1317,14 @@ hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream) {
     } else {
       attention_merge_narrow<16><<<grid, 256, 0, stream>>>(c);
     }
+    return hipGetLastError();
+  }
+  // Enough (token, head) rows to fill the chip with one thread per 4 dims:
+  // walk each token's splits; otherwise spread one token's splits over a
+  // workgroup per 16-dim slice.
+  const size_t threads = (size_t)c.tokens * c.heads * (c.head_dim / 4);
+  if (threads >= 256u * 64u) {
+    attention_merge_tokens<<<dim3((uint32_t)((threads + 255) / 256)), 256, 0, stream>>>(c);
     return hipGetLastError();
   }
   const dim3 grid(c.tokens, c.heads, c.head_dim / kMergeDims);
