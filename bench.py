@@ -262,9 +262,9 @@ def c4_lengths():
 
 def bench_c4(torch, ctx, run, gen, steps=20):
     """C4: 64 sequences, one token each per step, each running one hybrid block of
-    3 GDN layers (fused conv prologue, recurrence, norm-gated epilogue) and one
-    full-attention layer (KV append + gated attention) through the ragged
-    multi-sequence entry points."""
+    3 GDN layers (conv prologue, recurrence and norm-gated epilogue, one launch
+    per layer) and one full-attention layer (KV append + gated attention)
+    through the ragged multi-sequence entry points."""
     dev = "cuda"
     b = C4_SEQUENCES
     hk = hv = 16
@@ -309,13 +309,14 @@ def bench_c4(torch, ctx, run, gen, steps=20):
     maxpos = max(lengths)
 
     def gdn_layer(l, core_only=False):
-        if not core_only:
-            ctx.qwen35_conv_split_l2_ragged_decode_f32(qkv[l], conv_pool, conv_off[l], w[l], 4, b,
-                                                       hk, hv, dg, 1e-6, q, k, v)
-        ctx.gated_delta_net_f32_ragged_decode(q, k, v, g[l], beta[l], state_pool, state_off[l],
-                                              b, hk, hv, dg, y)
-        if not core_only:
-            ctx.qwen35_norm_gated_f32_in_place(y, norm_w, z[l], b, hv, dg, 1e-6)
+        if core_only:
+            ctx.gated_delta_net_f32_ragged_decode(q, k, v, g[l], beta[l], state_pool,
+                                                  state_off[l], b, hk, hv, dg, y)
+        else:
+            # Conv prologue, recurrence and norm-gated epilogue in one launch.
+            ctx.qwen35_gdn_layer_ragged_decode_f32(qkv[l], conv_pool, conv_off[l], w[l], 4, g[l],
+                                                   beta[l], None, None, z[l], norm_w, state_pool,
+                                                   state_off[l], b, hk, hv, dg, 1e-6, y)
 
     def attention_layer(append=True):
         if append:
@@ -328,8 +329,9 @@ def bench_c4(torch, ctx, run, gen, steps=20):
             gdn_layer(l)
         attention_layer()
 
-    # Warm the q/k/v inputs of the core-only timing with one full layer.
-    gdn_layer(0)
+    # q/k/v inputs of the core-only timing: one conv prologue.
+    ctx.qwen35_conv_split_l2_ragged_decode_f32(qkv[0], conv_pool, conv_off[0], w[0], 4, b, hk, hv,
+                                               dg, 1e-6, q, k, v)
     kv_bytes = sum(2048 * r for r in rows)
     gdn_bytes = b * C4_GDN_LAYERS * GDN_DECODE_BYTES
     res = {"sequences": b, "kv_len_min": min(lengths), "kv_len_max": maxpos,

@@ -418,6 +418,23 @@ class HipContext {
   }
 
   // Norms and elementwise ops (mps_backend.hpp:252-376).
+  // One decode step of the linear-attention core for many sequences (no
+  // MpsContext counterpart; see kraken_hip.h).  dt_bias/ssm_a may be invalid
+  // (default) buffers: gate and beta are then already prepared.
+  [[nodiscard]] Status qwen35_gdn_layer_ragged_decode_f32(
+    const HipBuffer& qkv, HipBuffer& conv_pool, const HipBuffer& seq_conv_offsets,
+    const HipBuffer& conv_kernel_weights, std::size_t conv_kernel, const HipBuffer& gate,
+    const HipBuffer& beta, const HipBuffer& dt_bias, const HipBuffer& ssm_a, const HipBuffer& z,
+    const HipBuffer& norm_weight, HipBuffer& state_pool, const HipBuffer& seq_state_offsets,
+    std::size_t sequences, std::size_t key_heads, std::size_t value_heads, std::size_t head_dim,
+    float eps, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_qwen35_gdn_layer_ragged_decode_f32(
+      ctx_, qkv.raw(), conv_pool.raw(), seq_conv_offsets.raw(), conv_kernel_weights.raw(),
+      conv_kernel, gate.raw(), beta.raw(), dt_bias.raw(), ssm_a.raw(), z.raw(), norm_weight.raw(),
+      state_pool.raw(), seq_state_offsets.raw(), sequences, key_heads, value_heads, head_dim,
+      eps, output.raw()));
+  }
+
   [[nodiscard]] Status split_qkv_l2_norm_f32_qwen35(
     const HipBuffer& source, HipBuffer& query, HipBuffer& key, HipBuffer& value,
     std::size_t tokens, std::size_t key_heads, std::size_t value_heads, std::size_t head_dim,

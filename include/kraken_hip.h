@@ -383,6 +383,30 @@ KRAKEN_API int kraken_hip_qwen35_conv_split_l2_ragged_decode_f32(
   size_t sequences, size_t key_heads, size_t value_heads, size_t head_dim, float eps,
   kraken_buffer query, kraken_buffer key, kraken_buffer value);
 
+/* One decode step of the Qwen3.5 linear-attention core for `sequences`
+ * sequences (one token each): the ragged conv prologue
+ * (kraken_hip_qwen35_conv_split_l2_ragged_decode_f32), the ragged gated delta
+ * rule (kraken_hip_gated_delta_net_f32_ragged_decode) and the norm-gated
+ * epilogue (qwen35_norm_gated_f32_in_place), i.e. qwen35_runtime.cpp:2740-3008
+ * between the projections.  No single MpsContext method corresponds.
+ * qkv, conv_pool, seq_conv_offsets and conv_kernel_weights as for the ragged conv
+ * prologue; gate/beta [sequences][value_heads] are the raw alpha/beta
+ * projections when dt_bias and ssm_a [value_heads] are given (both or neither;
+ * prepared as in prepare_qwen35_gdn_gate_beta_f32), else the prepared decay
+ * and beta; z [sequences][value_heads][head_dim]; norm_weight [head_dim];
+ * state_pool and seq_state_offsets as for the ragged gated delta net.  output
+ * [sequences][value_heads][head_dim] receives RMSNorm(y) * norm_weight * silu(z).
+ * One kernel for head_dim 128, conv_kernel 4 and key_heads == value_heads
+ * (bit-identical to the chain); other shapes run the three kernels, using
+ * context workspace.  A sequence whose offsets are outside a pool is skipped. */
+KRAKEN_API int kraken_hip_qwen35_gdn_layer_ragged_decode_f32(
+  kraken_hip_context* context, kraken_buffer qkv, kraken_buffer conv_pool,
+  kraken_buffer seq_conv_offsets, kraken_buffer conv_kernel_weights, size_t conv_kernel,
+  kraken_buffer gate, kraken_buffer beta, kraken_buffer dt_bias, kraken_buffer ssm_a,
+  kraken_buffer z, kraken_buffer norm_weight, kraken_buffer state_pool,
+  kraken_buffer seq_state_offsets, size_t sequences, size_t key_heads, size_t value_heads,
+  size_t head_dim, float eps, kraken_buffer output);
+
 #ifdef __cplusplus
 }
 #endif

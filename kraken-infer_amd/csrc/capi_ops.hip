@@ -1165,4 +1165,151 @@ KRAKEN_API int kraken_hip_qwen35_conv_split_l2_ragged_decode_f32(
   return finish_launch(ctx, (w + " command failed: ").c_str());
 }
 
+// One decode step of the Qwen3.5 linear-attention core for many sequences: the
+// ragged conv prologue, gated delta rule and norm-gated epilogue
+// (qwen35_runtime.cpp:2740-3008 between the projections) in one kernel where
+// the shape allows, else as the three-kernel chain.  No single MpsContext
+// method corresponds.
+KRAKEN_API int kraken_hip_qwen35_gdn_layer_ragged_decode_f32(
+  kraken_hip_context* ctx, kraken_buffer qkv, kraken_buffer conv_pool,
+  kraken_buffer seq_conv_offsets, kraken_buffer conv_kernel_weights, size_t conv_kernel,
+  kraken_buffer gate, kraken_buffer beta, kraken_buffer dt_bias, kraken_buffer ssm_a,
+  kraken_buffer z, kraken_buffer norm_weight, kraken_buffer state_pool,
+  kraken_buffer seq_state_offsets, size_t sequences, size_t key_heads, size_t value_heads,
+  size_t head_dim, float eps, kraken_buffer output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string w = "HIP ragged Qwen3.5 GDN layer";
+  if (sequences == 0 || key_heads == 0 || value_heads == 0 || head_dim == 0) {
+    return invalid(w + " dimensions must be positive");
+  }
+  if (value_heads % key_heads != 0) {
+    return invalid(w + " value heads must repeat key heads");
+  }
+  if (conv_kernel < 2 || conv_kernel > 8) {
+    return invalid(w + " conv_kernel must be in [2, 8]");
+  }
+  if (head_dim > 256u) {
+    return invalid(w + " head_dim exceeds 256");
+  }
+  if ((dt_bias.data == nullptr) != (ssm_a.data == nullptr)) {
+    return invalid(w + " dt_bias and ssm_a must be given together");
+  }
+  size_t key_dim = 0, value_dim = 0, channels = 0, qkv_values = 0, key_values = 0,
+         value_values = 0, conv_state_values = 0, kernel_values = 0, gate_values = 0,
+         state_values = 0;
+  if (!checked_mul(key_heads, head_dim, key_dim) ||
+      !checked_mul(value_heads, head_dim, value_dim) ||
+      !checked_add(2u * key_dim, value_dim, channels) ||
+      !checked_mul(sequences, channels, qkv_values) ||
+      !checked_mul(sequences, key_dim, key_values) ||
+      !checked_mul(sequences, value_dim, value_values) ||
+      !checked_mul(conv_kernel - 1u, channels, conv_state_values) ||
+      !checked_mul(conv_kernel, channels, kernel_values) ||
+      !checked_mul(sequences, value_heads, gate_values) ||
+      !checked_mul(value_dim, head_dim, state_values)) {
+    return invalid(w + " value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(qkv, qkv_values, "ragged Qwen3.5 GDN layer qkv"));
+  uint64_t conv_elems = 0, state_elems = 0;
+  KRAKEN_TRY(pool_elems_of(conv_pool, sizeof(float), conv_state_values, w,
+                           "ragged Qwen3.5 GDN layer conv pool", conv_elems));
+  KRAKEN_TRY(validate_buffer(seq_conv_offsets, sequences, sizeof(uint64_t),
+                             "ragged Qwen3.5 GDN layer conv offsets"));
+  KRAKEN_TRY(validate_f32(conv_kernel_weights, kernel_values, "ragged Qwen3.5 GDN layer kernel"));
+  KRAKEN_TRY(validate_f32(gate, gate_values, "ragged Qwen3.5 GDN layer gate"));
+  KRAKEN_TRY(validate_f32(beta, gate_values, "ragged Qwen3.5 GDN layer beta"));
+  if (dt_bias.data != nullptr) {
+    KRAKEN_TRY(validate_f32(dt_bias, value_heads, "ragged Qwen3.5 GDN layer dt_bias"));
+    KRAKEN_TRY(validate_f32(ssm_a, value_heads, "ragged Qwen3.5 GDN layer ssm_a"));
+  }
+  KRAKEN_TRY(validate_f32(z, value_values, "ragged Qwen3.5 GDN layer z"));
+  KRAKEN_TRY(validate_f32(norm_weight, head_dim, "ragged Qwen3.5 GDN layer norm weight"));
+  KRAKEN_TRY(pool_elems_of(state_pool, sizeof(float), state_values, w,
+                           "ragged Qwen3.5 GDN layer state pool", state_elems));
+  KRAKEN_TRY(validate_buffer(seq_state_offsets, sequences, sizeof(uint64_t),
+                             "ragged Qwen3.5 GDN layer state offsets"));
+  KRAKEN_TRY(validate_f32(output, value_values, "ragged Qwen3.5 GDN layer output"));
+  KRAKEN_TRY(check_u32(sequences, "ragged Qwen3.5 GDN layer sequences"));
+  KRAKEN_TRY(check_u32(channels, "ragged Qwen3.5 GDN layer channels"));
+  KRAKEN_TRY(check_u32(value_heads, "ragged Qwen3.5 GDN layer value_heads"));
+
+  const auto* dtb = static_cast<const float*>(dt_bias.data);
+  const auto* ssa = static_cast<const float*>(ssm_a.data);
+  if (gdn_layer_fused_supported((uint32_t)head_dim, (uint32_t)conv_kernel, (uint32_t)key_heads,
+                                (uint32_t)value_heads)) {
+    KRAKEN_TRY(begin_launch(ctx));
+    GdnLayerArgs a{};
+    a.qkv = static_cast<const float*>(qkv.data);
+    a.conv_pool = static_cast<float*>(conv_pool.data);
+    a.seq_conv_offsets = static_cast<const uint64_t*>(seq_conv_offsets.data);
+    a.conv_pool_elems = conv_elems;
+    a.conv_weights = static_cast<const float*>(conv_kernel_weights.data);
+    a.gate = static_cast<const float*>(gate.data);
+    a.beta = static_cast<const float*>(beta.data);
+    a.dt_bias = dtb;
+    a.ssm_a = ssa;
+    a.z = static_cast<const float*>(z.data);
+    a.norm_weight = static_cast<const float*>(norm_weight.data);
+    a.state_pool = static_cast<float*>(state_pool.data);
+    a.seq_state_offsets = static_cast<const uint64_t*>(seq_state_offsets.data);
+    a.state_pool_elems = state_elems;
+    a.output = static_cast<float*>(output.data);
+    a.sequences = (uint32_t)sequences;
+    a.heads = (uint32_t)value_heads;
+    a.eps = eps;
+    const hipError_t e = launch_gdn_layer_ragged(a, ctx->stream);
+    if (e != hipSuccess) {
+      return internal(w + " launch failed: " + hipGetErrorString(e));
+    }
+    return finish_launch(ctx, (w + " command failed: ").c_str());
+  }
+
+  // Three-kernel chain: q/k/v in the context workspace, after its counter region.
+  size_t tmp_bytes = 0;
+  if (!checked_mul(2u * key_values + value_values, sizeof(float), tmp_bytes) ||
+      !checked_add(tmp_bytes, kCounterRegionBytes, tmp_bytes)) {
+    return invalid(w + " value count overflow");
+  }
+  KRAKEN_TRY(ensure_workspace(ctx, tmp_bytes));
+  KRAKEN_TRY(begin_launch(ctx));
+  float* qb = reinterpret_cast<float*>(static_cast<char*>(ctx->workspace) + kCounterRegionBytes);
+  float* kb = qb + key_values;
+  float* vb = kb + key_values;
+  hipError_t e = launch_conv_split_l2_ragged(
+    static_cast<const float*>(qkv.data), static_cast<float*>(conv_pool.data),
+    static_cast<const uint64_t*>(seq_conv_offsets.data), conv_elems,
+    static_cast<const float*>(conv_kernel_weights.data), (uint32_t)conv_kernel,
+    (uint32_t)sequences, (uint32_t)key_heads, (uint32_t)value_heads, (uint32_t)head_dim, eps,
+    qb, kb, vb, ctx->stream);
+  if (e == hipSuccess) {
+    GdnArgs a{};
+    a.query = qb;
+    a.key = kb;
+    a.value = vb;
+    a.gate = static_cast<const float*>(gate.data);
+    a.beta = static_cast<const float*>(beta.data);
+    a.state = static_cast<float*>(state_pool.data);
+    a.output = static_cast<float*>(output.data);
+    a.tokens = (uint32_t)sequences;
+    a.key_heads = (uint32_t)key_heads;
+    a.value_heads = (uint32_t)value_heads;
+    a.head_dim = (uint32_t)head_dim;
+    a.dt_bias = dtb;
+    a.ssm_a = ssa;
+    a.seq_state_offsets = static_cast<const uint64_t*>(seq_state_offsets.data);
+    a.pool_elems = state_elems;
+    e = launch_gated_delta_net(a, ctx->cu_count, nullptr, 0, ctx->stream);
+  }
+  if (e == hipSuccess) {
+    e = launch_rms_norm_heads(static_cast<float*>(output.data),
+                              static_cast<const float*>(norm_weight.data),
+                              static_cast<const float*>(z.data), (uint32_t)sequences,
+                              (uint32_t)value_heads, (uint32_t)head_dim, eps, ctx->stream);
+  }
+  if (e != hipSuccess) {
+    return internal(w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (w + " command failed: ").c_str());
+}
+
 }  // extern "C"

@@ -183,6 +183,34 @@ size_t gdn_chunked_workspace_bytes(const GdnArgs& a);
 hipError_t launch_gdn_chunked(const GdnArgs& a, void* workspace, size_t workspace_bytes,
                               hipStream_t stream);
 
+// Ragged decode of a whole Qwen3.5 linear-attention core in one kernel
+// (kraken_hip_qwen35_gdn_layer_ragged_decode_f32): conv prologue, gated delta
+// rule and norm-gated epilogue, one workgroup per (sequence, value head).
+struct GdnLayerArgs {
+  const float* qkv;           // [sequences][3 * heads * 128]
+  float* conv_pool;           // per sequence [channels][3] at seq_conv_offsets[b]
+  const uint64_t* seq_conv_offsets;
+  uint64_t conv_pool_elems;
+  const float* conv_weights;  // [channels][4]
+  const float* gate;          // [sequences][heads] (raw alpha when dt_bias is set)
+  const float* beta;          // [sequences][heads] (raw when dt_bias is set)
+  const float* dt_bias;       // null: gate and beta are prepared
+  const float* ssm_a;
+  const float* z;             // [sequences][heads][128]
+  const float* norm_weight;   // [128]
+  float* state_pool;          // per sequence [heads][128][128] at seq_state_offsets[b]
+  const uint64_t* seq_state_offsets;
+  uint64_t state_pool_elems;
+  float* output;              // [sequences][heads][128]
+  uint32_t sequences, heads;
+  float eps;
+};
+// True when the one-kernel layer supports the shape (head_dim 128, conv kernel
+// 4, key_heads == value_heads).
+bool gdn_layer_fused_supported(uint32_t head_dim, uint32_t conv_kernel, uint32_t key_heads,
+                               uint32_t value_heads);
+hipError_t launch_gdn_layer_ragged(const GdnLayerArgs& a, hipStream_t stream);
+
 hipError_t launch_ssm_conv(const float* input, const float* kernel, float* output,
                            uint32_t conv_kernel, uint32_t channels, uint32_t tokens,
                            uint32_t sequences, hipStream_t stream);

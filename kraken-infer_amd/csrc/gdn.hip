@@ -720,6 +720,173 @@ __global__ __launch_bounds__(64) void conv_split_l2_ragged_kernel(
   }
 }
 
+// Ragged decode of a whole Qwen3.5 linear-attention core (the op sequence of
+// run_qwen35_linear_layer_chunk between its projections, qwen35_runtime.cpp:
+// 2740-3008, for one token per sequence) in one launch: one workgroup per
+// (sequence, value head) runs, in order,
+//  * the conv prologue of conv_split_l2_ragged_kernel for the head's q, k and v
+//    channels (waves 0, 1, 2: one unit each, with that kernel's lane mapping
+//    and reduction order) into LDS, updating the conv state;
+//  * the gated delta rule of gdn_decode_kernel on the head's 128 x 128 state
+//    (8 groups of 32 lanes, 16 rows each; the state loads are issued first, so
+//    they are in flight during the conv);
+//  * the norm-gated epilogue of rms_norm_heads_kernel (wave 0).
+// Each step repeats the replaced kernel's arithmetic, so the result equals the
+// three-kernel chain bit for bit.  key_heads == value_heads: every workgroup
+// owns its q/k channels, and the conv-state update has one writer.  A sequence
+// whose state or conv offset is misaligned or outside its pool is skipped
+// (nothing is read or written for it).
+template <bool kPrepare>
+__global__ __launch_bounds__(256) void gdn_layer_ragged_kernel(GdnLayerArgs p) {
+  constexpr uint32_t D = 128;
+  constexpr int K = 4;
+  constexpr int W = K - 1;
+  constexpr int RPL = 16;  // state rows per 32-lane group
+  constexpr int CPL = 2;   // conv channels per lane (D / 64)
+  __shared__ float qs[D], ks[D], vs[D], ys[D];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int grp = tid >> 5;
+  const uint32_t h = blockIdx.x;
+  const uint32_t seq = blockIdx.y;
+  const uint32_t H = p.heads;
+  const size_t channels = (size_t)3 * H * D;
+
+  const uint64_t soff = p.seq_state_offsets[seq];
+  const uint64_t coff = p.seq_conv_offsets[seq];
+  if ((soff & 3u) != 0 || soff > p.state_pool_elems ||
+      p.state_pool_elems - soff < (uint64_t)H * D * D || coff > p.conv_pool_elems ||
+      p.conv_pool_elems - coff < channels * W) {
+    return;  // whole workgroup, before any barrier
+  }
+  float* shead = p.state_pool + soff + (size_t)h * D * D;
+  const uint32_t row0 = (uint32_t)grp * RPL;
+  const uint32_t col0 = (uint32_t)(lane & 31) * 4;
+  float4 s[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    s[j] = *reinterpret_cast<const float4*>(shead + (size_t)(row0 + j) * D + col0);
+  }
+
+  if (wave < 3) {
+    // Unit wave * H + h: the q, k or v channels of this head.
+    float* state = p.conv_pool + coff;
+    const uint32_t cbase = ((uint32_t)wave * H + h) * D;
+    float y[CPL];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const size_t c = cbase + lane + 64u * i;
+      float win[W];
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        win[j] = state[c * W + j];
+      }
+      const float xt = p.qkv[(size_t)seq * channels + c];
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        acc = fmaf(win[j], p.conv_weights[c * K + j], acc);
+      }
+      acc = fmaf(xt, p.conv_weights[c * K + W], acc);
+#pragma unroll
+      for (int j = 0; j + 1 < W; ++j) {
+        state[c * W + j] = win[j + 1];
+      }
+      state[c * W + (W - 1)] = xt;
+      y[i] = acc / (1.0f + expf(-acc));  // SiLU
+      ss = fmaf(y[i], y[i], ss);
+    }
+    float* dst = wave == 0 ? qs : (wave == 1 ? ks : vs);
+    float inv = 1.0f;
+    if (wave < 2) {
+      ss = wave_sum(ss);
+      inv = 1.0f / fmaxf(sqrtf(ss), p.eps);
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      dst[lane + 64 * i] = wave < 2 ? y[i] * inv : y[i];
+    }
+  }
+  const size_t gi = (size_t)seq * H + h;
+  float g = p.gate[gi];
+  float b = p.beta[gi];
+  if (kPrepare) {
+    g = softplus_ref(g + p.dt_bias[h]) * p.ssm_a[h];
+    b = 1.0f / (1.0f + expf(-b));
+  }
+  const float decay = expf(g);
+  __syncthreads();
+
+  const float4 k = *reinterpret_cast<const float4*>(&ks[col0]);
+  const float4 q = *reinterpret_cast<const float4*>(&qs[col0]);
+  const float scale = 1.0f / sqrtf((float)D);
+  float sk[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    s[j].x *= decay;
+    s[j].y *= decay;
+    s[j].z *= decay;
+    s[j].w *= decay;
+    sk[j] = fmaf(s[j].x, k.x, fmaf(s[j].y, k.y, fmaf(s[j].z, k.z, s[j].w * k.w)));
+  }
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    sk[j] = reduce32_sum(sk[j]);
+  }
+  float yv[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    const float delta = (vs[row0 + j] - sk[j]) * b;
+    s[j].x = fmaf(k.x, delta, s[j].x);
+    s[j].y = fmaf(k.y, delta, s[j].y);
+    s[j].z = fmaf(k.z, delta, s[j].z);
+    s[j].w = fmaf(k.w, delta, s[j].w);
+    yv[j] = fmaf(s[j].x, q.x, fmaf(s[j].y, q.y, fmaf(s[j].z, q.z, s[j].w * q.w)));
+  }
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    yv[j] = reduce32_sum(yv[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    *reinterpret_cast<float4*>(shead + (size_t)(row0 + j) * D + col0) = s[j];
+  }
+  if ((lane & 31) == 0) {
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+      ys[row0 + j] = yv[j] * scale;
+    }
+  }
+  __syncthreads();
+
+  if (wave == 0) {
+    // Norm-gated epilogue: y <- y * rsqrt(mean(y^2) + eps) * w * silu(z).
+    float v[4];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t d = lane + 64u * i;
+      v[i] = d < D ? ys[d] : 0.0f;
+      sum = fmaf(v[i], v[i], sum);
+    }
+    sum = wave_sum(sum);
+    const float nscale = 1.0f / sqrtf(sum / (float)D + p.eps);
+    const size_t rowoff = gi * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t d = lane + 64u * i;
+      if (d < D) {
+        float r = v[i] * nscale * p.norm_weight[d];
+        const float zz = p.z[rowoff + d];
+        r *= zz * (1.0f / (1.0f + expf(-zz)));
+        p.output[rowoff + d] = r;
+      }
+    }
+  }
+}
+
 unsigned grid_for(size_t total, unsigned block = 256) {
   size_t blocks = (total + block - 1) / block;
   if (blocks < 1) {
@@ -858,6 +1025,21 @@ hipError_t launch_conv_split_l2_ragged(const float* qkv, float* conv_pool,
   KRAKEN_CONV_CPL(1) KRAKEN_CONV_CPL(2) KRAKEN_CONV_CPL(4) { return hipErrorInvalidValue; }
 #undef KRAKEN_CONV_CPL
 #undef KRAKEN_CONV_CASE
+  return hipGetLastError();
+}
+
+bool gdn_layer_fused_supported(uint32_t head_dim, uint32_t conv_kernel, uint32_t key_heads,
+                               uint32_t value_heads) {
+  return head_dim == 128 && conv_kernel == 4 && key_heads == value_heads;
+}
+
+hipError_t launch_gdn_layer_ragged(const GdnLayerArgs& a, hipStream_t stream) {
+  const dim3 grid(a.heads, a.sequences);
+  if (a.dt_bias != nullptr) {
+    gdn_layer_ragged_kernel<true><<<grid, 256, 0, stream>>>(a);
+  } else {
+    gdn_layer_ragged_kernel<false><<<grid, 256, 0, stream>>>(a);
+  }
   return hipGetLastError();
 }
 

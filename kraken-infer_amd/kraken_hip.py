@@ -60,6 +60,8 @@ SIGNATURES = {
     "kraken_hip_append_kv_ragged_f16": [_B] * 6 + [_sz] * 2,
     "kraken_hip_gated_delta_net_f32_ragged_decode": [_B] * 7 + [_sz] * 4 + [_B],
     "kraken_hip_qwen35_conv_split_l2_ragged_decode_f32": [_B] * 4 + [_sz] * 5 + [_f, _B, _B, _B],
+    "kraken_hip_qwen35_gdn_layer_ragged_decode_f32": [_B] * 4 + [_sz] + [_B] * 8 + [_sz] * 4
+                                                     + [_f, _B],
     "kraken_hip_qwen35_gdn_gated_f32": [_B] * 10 + [_sz] * 5 + [_f, _B],
     "kraken_hip_split_qkv_l2_norm_f32_qwen35": [_B] * 4 + [_sz] * 4 + [_f],
     "kraken_hip_l2_norm_f32_in_place": [_B, _sz, _sz, _f],

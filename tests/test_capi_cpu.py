@@ -317,3 +317,49 @@ def test_prologue_generated_positions_must_fit_int32(vctx):
     args[6] = (1 << 31) - 2  # mrope_start_position: the last of 4 tokens exceeds int32
     code, msg = status(vctx, "qwen35_attention_prologue_f16_kv", *args)
     assert code == kh.INVALID_ARGUMENT and "exceeds int32 range" in msg
+
+
+# ------------------------------------------------ fused ragged GDN layer --
+
+def gdn_layer_args(b=4, hk=16, hv=16, d=128, k=4, prepare=True, **sizes):
+    ch = (2 * hk + hv) * d
+
+    def buf(name, n):
+        return fake(sizes.get(name, n))
+
+    dtb = buf("dtb", 4 * hv) if prepare else kh.KrakenBuffer(None, 0)
+    ssa = buf("ssa", 4 * hv) if prepare else kh.KrakenBuffer(None, 0)
+    return (buf("qkv", 4 * b * ch), buf("cp", 4 * ch * (k - 1)), buf("co", 8 * b),
+            buf("w", 4 * ch * k), k, buf("g", 4 * b * hv), buf("beta", 4 * b * hv), dtb, ssa,
+            buf("z", 4 * b * hv * d), buf("nw", 4 * d), buf("sp", 4 * hv * d * d),
+            buf("so", 8 * b), b, hk, hv, d, 1e-6, buf("out", 4 * b * hv * d))
+
+
+def test_gdn_layer_accepts_valid(vctx):
+    for kw in ({}, dict(prepare=False), dict(hk=2, hv=4, d=64, k=3)):
+        code, msg = status(vctx, "qwen35_gdn_layer_ragged_decode_f32", *gdn_layer_args(**kw))
+        assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED), kw
+
+
+@pytest.mark.parametrize("kw,fragment", [
+    (dict(b=0), "dimensions must be positive"),
+    (dict(hk=3, hv=4), "value heads must repeat key heads"),
+    (dict(k=1), "conv_kernel must be in [2, 8]"),
+    (dict(d=512), "head_dim exceeds 256"),
+    (dict(qkv=16), "qkv buffer is too small"),
+    (dict(cp=16), "conv pool buffer is too small"),
+    (dict(sp=16), "state pool buffer is too small"),
+    (dict(z=16), "z buffer is too small"),
+    (dict(out=16), "output buffer is too small"),
+])
+def test_gdn_layer_rejects(vctx, kw, fragment):
+    code, msg = status(vctx, "qwen35_gdn_layer_ragged_decode_f32", *gdn_layer_args(**kw))
+    assert code == kh.INVALID_ARGUMENT
+    assert fragment in msg, msg
+
+
+def test_gdn_layer_dt_bias_and_ssm_a_together(vctx):
+    args = list(gdn_layer_args())
+    args[8] = kh.KrakenBuffer(None, 0)  # ssm_a missing, dt_bias given
+    code, msg = status(vctx, "qwen35_gdn_layer_ragged_decode_f32", *args)
+    assert code == kh.INVALID_ARGUMENT and "given together" in msg

@@ -237,3 +237,119 @@ def test_ragged_attention_c4_shape_sampled(hip_ctx):
         ref = attention_reference(q[sl], kpool, vpool, offsets[i:i + 1], positions[i:i + 1],
                                   heads, kv_heads, d, gate[sl])
         np.testing.assert_allclose(got[i], ref, rtol=2e-3, atol=1e-3, err_msg=f"sequence {i}")
+
+
+def _gdn_layer_case(rng, b, hk, hv, dd, kk, prepare):
+    ch = (2 * hk + hv) * dd
+    conv_elems = ch * (kk - 1)
+    state_elems = hv * dd * dd
+    coffs, ctotal = scattered_offsets(rng, [1] * b, conv_elems, align=64)
+    soffs, stotal = scattered_offsets(rng, [1] * b, state_elems, align=dd)
+    c = dict(
+        qkv=rng.standard_normal(b * ch).astype(np.float32),
+        conv_pool=rng.standard_normal(ctotal).astype(np.float32),
+        w=(0.5 * rng.standard_normal(ch * kk)).astype(np.float32),
+        gate=rng.standard_normal(b * hv).astype(np.float32),
+        beta=rng.standard_normal(b * hv).astype(np.float32),
+        z=rng.standard_normal(b * hv * dd).astype(np.float32),
+        nw=(1 + 0.1 * rng.standard_normal(dd)).astype(np.float32),
+        state_pool=(0.1 * rng.standard_normal(stotal)).astype(np.float32),
+        coffs=coffs, soffs=soffs)
+    if prepare:
+        c["dtb"] = rng.standard_normal(hv).astype(np.float32)
+        c["ssa"] = (-rng.random(hv)).astype(np.float32)
+    else:
+        c["gate"] = (-np.logaddexp(0, c["gate"])).astype(np.float32)
+        c["beta"] = (1 / (1 + np.exp(-c["beta"]))).astype(np.float32)
+    return c
+
+
+def _run_gdn_layer(ctx, c, b, hk, hv, dd, kk):
+    cp, sp = ctx.buffer(c["conv_pool"]), ctx.buffer(c["state_pool"])
+    ob = ctx.buffer(np.full(b * hv * dd, 7.0, np.float32))
+    dtb = ctx.buffer(c["dtb"]) if "dtb" in c else None
+    ssa = ctx.buffer(c["ssa"]) if "ssa" in c else None
+    ctx.qwen35_gdn_layer_ragged_decode_f32(
+        ctx.buffer(c["qkv"]), cp, ctx.buffer(c["coffs"]), ctx.buffer(c["w"]), kk,
+        ctx.buffer(c["gate"]), ctx.buffer(c["beta"]), dtb, ssa, ctx.buffer(c["z"]),
+        ctx.buffer(c["nw"]), sp, ctx.buffer(c["soffs"]), b, hk, hv, dd, 1e-6, ob)
+    return ob.download(), cp.download(), sp.download()
+
+
+def _run_gdn_chain(ctx, c, b, hk, hv, dd, kk):
+    """The same step as the separate ragged ops (gate/beta prepared on the device)."""
+    cp, sp = ctx.buffer(c["conv_pool"]), ctx.buffer(c["state_pool"])
+    qb, kb = ctx.buffer(byte_size=4 * b * hk * dd), ctx.buffer(byte_size=4 * b * hk * dd)
+    vb = ctx.buffer(byte_size=4 * b * hv * dd)
+    ctx.qwen35_conv_split_l2_ragged_decode_f32(ctx.buffer(c["qkv"]), cp, ctx.buffer(c["coffs"]),
+                                               ctx.buffer(c["w"]), kk, b, hk, hv, dd, 1e-6, qb,
+                                               kb, vb)
+    gb, bb = ctx.buffer(c["gate"]), ctx.buffer(c["beta"])
+    if "dtb" in c:
+        ctx.prepare_qwen35_gdn_gate_beta_f32(gb, bb, ctx.buffer(c["dtb"]), ctx.buffer(c["ssa"]),
+                                             b, hv)
+    ob = ctx.buffer(byte_size=4 * b * hv * dd)
+    ctx.gated_delta_net_f32_ragged_decode(qb, kb, vb, gb, bb, sp, ctx.buffer(c["soffs"]), b, hk,
+                                          hv, dd, ob)
+    ctx.qwen35_norm_gated_f32_in_place(ob, ctx.buffer(c["nw"]), ctx.buffer(c["z"]), b, hv, dd,
+                                       1e-6)
+    return ob.download(), cp.download(), sp.download()
+
+
+@pytest.mark.parametrize("shape,prepare", [
+    ((7, 16, 16, 128, 4), True), ((7, 16, 16, 128, 4), False),  # one kernel
+    ((5, 2, 4, 64, 3), True), ((3, 4, 4, 96, 4), False),         # three-kernel chain
+])
+def test_ragged_gdn_layer_matches_chain_and_oracle(hip_ctx, shape, prepare):
+    """kraken_hip_qwen35_gdn_layer_ragged_decode_f32 against the three ragged ops
+    it replaces (equal bit for bit for the one-kernel shape; the chain shapes
+    are that chain) and against the oracle's conv, prepare, recurrence and
+    norm-gated steps per sequence (1e-4 absolute)."""
+    b, hk, hv, dd, kk = shape
+    print(f"gdn layer {shape} prepare={prepare}", flush=True)
+    rng = np.random.default_rng(50 + b + hk)
+    c = _gdn_layer_case(rng, b, hk, hv, dd, kk, prepare)
+    out, cpool, spool = _run_gdn_layer(hip_ctx, c, b, hk, hv, dd, kk)
+    ref_out, ref_cpool, ref_spool = _run_gdn_chain(hip_ctx, c, b, hk, hv, dd, kk)
+    np.testing.assert_array_equal(out, ref_out)
+    np.testing.assert_array_equal(cpool, ref_cpool)
+    np.testing.assert_array_equal(spool, ref_spool)
+    ch = (2 * hk + hv) * dd
+    conv_elems, state_elems = ch * (kk - 1), hv * dd * dd
+    g, beta = c["gate"], c["beta"]
+    if prepare:
+        g, beta = oracle.prepare_gdn_gate_beta(g, beta, c["dtb"], c["ssa"], b, hv)
+    for i in range(b):
+        co, so = int(c["coffs"][i]), int(c["soffs"][i])
+        ci, new_conv = oracle.build_ssm_conv_state(c["conv_pool"][co:co + conv_elems],
+                                                   c["qkv"][i * ch:(i + 1) * ch], kk, ch, 1)
+        y = oracle.silu(oracle.ssm_conv(ci, c["w"], kk, ch, 1, 1))
+        q, k, v = oracle.split_qkv_l2_norm(y, 1, hk, hv, dd, 1e-6)
+        gl = slice(i * hv, (i + 1) * hv)
+        yo, st = oracle.gated_delta_net(q, k, v, g[gl], beta[gl],
+                                        c["state_pool"][so:so + state_elems], 1, hk, hv, dd)
+        yo = oracle.norm_gated(yo, c["nw"], c["z"][i * hv * dd:(i + 1) * hv * dd], 1, hv, dd,
+                               1e-6)
+        np.testing.assert_allclose(out[i * hv * dd:(i + 1) * hv * dd], yo, rtol=0, atol=1e-4)
+        np.testing.assert_array_equal(cpool[co:co + conv_elems], new_conv)
+        np.testing.assert_allclose(spool[so:so + state_elems], st, rtol=0, atol=1e-4)
+
+
+def test_ragged_gdn_layer_skips_out_of_pool_sequence(hip_ctx):
+    """A sequence whose state offset is outside its pool is skipped by the one
+    kernel: its output, conv state and state are untouched; the others match."""
+    b, hk, hv, dd, kk = 4, 16, 16, 128, 4
+    rng = np.random.default_rng(61)
+    c = _gdn_layer_case(rng, b, hk, hv, dd, kk, True)
+    good = dict(c)
+    c["soffs"] = c["soffs"].copy()
+    c["soffs"][2] = np.uint64(len(c["state_pool"]) + 5)
+    out, cpool, spool = _run_gdn_layer(hip_ctx, c, b, hk, hv, dd, kk)
+    ref_out, _, ref_spool = _run_gdn_layer(hip_ctx, good, b, hk, hv, dd, kk)
+    d = hv * dd
+    np.testing.assert_array_equal(out[2 * d:3 * d], 7.0)
+    co = int(c["coffs"][2])
+    conv_elems = (2 * hk + hv) * dd * (kk - 1)
+    np.testing.assert_array_equal(cpool[co:co + conv_elems], c["conv_pool"][co:co + conv_elems])
+    for i in (0, 1, 3):
+        np.testing.assert_array_equal(out[i * d:(i + 1) * d], ref_out[i * d:(i + 1) * d])
