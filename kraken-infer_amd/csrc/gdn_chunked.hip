@@ -92,8 +92,14 @@ __device__ __forceinline__ float4_v mfma4(float a, float b, float4_v c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Eight waves: the prep phases are latency-bound at one workgroup per CU (its
+// LDS), so twice the waves hide more of each phase's latency and shorten the
+// MFMA critical paths of the Gram and U/W phases.
+constexpr int kPrepThreads = 512;
+constexpr int kPrepWaves = kPrepThreads / 64;
+
 template <bool kPrepare>
-__global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
+__global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParams p) {
   __shared__ __attribute__((aligned(16))) float Ks[kC][kRowPad];
   __shared__ __attribute__((aligned(16))) float Qs[kC][kRowPad];
   __shared__ __attribute__((aligned(16))) float Vs[kC][kRowPad];
@@ -119,8 +125,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
   // Unconditional loads from a valid row (the chunk's first token stands in for
   // rows past its end), zeroed afterwards, so all of them are in flight at once.
 #pragma unroll
-  for (int it = 0; it < kC * (kDim / 4) / 256; ++it) {
-    const int idx = tid + 256 * it;
+  for (int it = 0; it < kC * (kDim / 4) / kPrepThreads; ++it) {
+    const int idx = tid + kPrepThreads * it;
     const int t = idx >> 5;
     const int c4 = (idx & 31) * 4;
     const bool ok = (uint32_t)t < n;
@@ -136,7 +142,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
     *reinterpret_cast<float4*>(&Qs[t][c4]) = qq;
     *reinterpret_cast<float4*>(&Vs[t][c4]) = vv;
   }
-  for (int idx = tid; idx < kC * kCPad; idx += 256) {
+  for (int idx = tid; idx < kC * kCPad; idx += kPrepThreads) {
     (&As[0][0])[idx] = 0.0f;
     (&Ts[0][0])[idx] = 0.0f;
   }
@@ -168,9 +174,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
   const float g_last = Gs[kC - 1];  // padded tokens carry g = 0
 
   // ---- Gram matrices: tiles (I, J), J <= I, of K K^T (A) and Q K^T (M) ----
-  // Jobs 0..9: the ten lower tiles of K K^T, 10..19: of Q K^T.  A wave runs two
-  // jobs per pass with independent accumulators (LDS reads of one overlap the
-  // MFMAs of the other).
+  // Jobs 0..9: the ten lower tiles of K K^T, 10..19: of Q K^T.  Wave w runs
+  // jobs w and w + 8 in one pass with independent accumulators (LDS reads of
+  // one overlap the MFMAs of the other), then job w + 16 if it exists.
   auto gram_tile = [&](int job, int& I, int& J, bool& is_q) __attribute__((always_inline)) {
     is_q = job >= 10;
     int jj = is_q ? job - 10 : job;  // lower-triangular tile index
@@ -194,12 +200,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
       }
     }
   };
-  for (int job = wave; job < 20; job += 8) {
+  static_assert(kPrepWaves == 8, "job assignment");
+  for (int job = wave; job < 20; job += 16) {
     int I0, J0, I1, J1;
     bool q0, q1;
     gram_tile(job, I0, J0, q0);
-    const bool two = job + 4 < 20;
-    gram_tile(two ? job + 4 : job, I1, J1, q1);
+    const bool two = job + 8 < 20;
+    gram_tile(two ? job + 8 : job, I1, J1, q1);
     const float(*X0)[kRowPad] = q0 ? Qs : Ks;
     const float(*X1)[kRowPad] = q1 ? Qs : Ks;
     float4_v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
@@ -224,7 +231,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
     }
   }
   // Upper tiles of M are zero.
-  for (int idx = tid; idx < 6 * 256; idx += 256) {
+  for (int idx = tid; idx < 6 * 256; idx += kPrepThreads) {
     int u = idx >> 8;  // upper tile index: (I, J) with J > I
     const int e = idx & 255;
     int I = 0, J = 1;
@@ -240,7 +247,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
   __syncthreads();
 
   // ---- T = (I + A)^-1: diagonal 16 x 16 blocks by substitution ----
-  if (li == lane) {  // lanes 0..15 of each wave: column j of block `wave`
+  if (wave < 4 && li == lane) {  // lanes 0..15 of waves 0..3: column j of block `wave`
     const int b0 = 16 * wave;
     const int j = lane;
     float col[16];
@@ -261,7 +268,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
   __syncthreads();
   // Off-diagonal blocks by block rows: T_IJ = -T_II sum_{K=J}^{I-1} A_IK T_KJ.
   for (int I = 1; I < 4; ++I) {
-    for (int idx = tid; idx < I * 256; idx += 256) {
+    for (int idx = tid; idx < I * 256; idx += kPrepThreads) {
       const int J = idx >> 8;
       const int i = (idx >> 4) & 15;
       const int j = idx & 15;
@@ -275,7 +282,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
       Tmp[J][i][j] = acc;
     }
     __syncthreads();
-    for (int idx = tid; idx < I * 256; idx += 256) {
+    for (int idx = tid; idx < I * 256; idx += kPrepThreads) {
       const int J = idx >> 8;
       const int i = (idx >> 4) & 15;
       const int j = idx & 15;
@@ -290,7 +297,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
   }
 
   // ---- Qtil = diag(gamma) Q and Ktil^T = (diag(exp(G_C - G)) K)^T ----
-  for (int idx = tid; idx < kC * (kDim / 4); idx += 256) {
+  for (int idx = tid; idx < kC * (kDim / 4); idx += kPrepThreads) {
     const int t = idx >> 5;
     const int c4 = (idx & 31) * 4;
     const float gm = Gam[t];
@@ -301,7 +308,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
     qq.w *= gm;
     *reinterpret_cast<float4*>(blk + kOffQ + t * kDim + c4) = qq;
   }
-  for (int idx = tid; idx < kDim * (kC / 4); idx += 256) {
+  for (int idx = tid; idx < kDim * (kC / 4); idx += kPrepThreads) {
     const int d = idx >> 4;
     const int t4 = (idx & 15) * 4;
     float4 v;
@@ -316,7 +323,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
   }
   __syncthreads();
   // V <- diag(beta) V, K <- diag(beta gamma) K (in place; the Grams are done).
-  for (int idx = tid; idx < kC * (kDim / 4); idx += 256) {
+  for (int idx = tid; idx < kC * (kDim / 4); idx += kPrepThreads) {
     const int t = idx >> 5;
     const int c4 = (idx & 31) * 4;
     const float bv = Bs[t];
@@ -337,7 +344,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkParams p) {
   __syncthreads();
 
   // ---- U = T V', W = T K' (C x D): 2 x 32 output tiles, four per pass ----
-  for (int job0 = 4 * wave; job0 < 64; job0 += 16) {
+  for (int job0 = 4 * wave; job0 < 64; job0 += 4 * kPrepWaves) {
     float4_v acc[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -685,9 +692,9 @@ hipError_t launch_gdn_chunked(const GdnArgs& a, void* workspace, size_t workspac
     p.chunks = chunks - c0 < kSlabChunks ? chunks - c0 : kSlabChunks;
     const dim3 pgrid(p.chunks, a.value_heads);
     if (a.dt_bias != nullptr) {
-      gdn_chunk_prep_kernel<true><<<pgrid, 256, 0, stream>>>(p);
+      gdn_chunk_prep_kernel<true><<<pgrid, kPrepThreads, 0, stream>>>(p);
     } else {
-      gdn_chunk_prep_kernel<false><<<pgrid, 256, 0, stream>>>(p);
+      gdn_chunk_prep_kernel<false><<<pgrid, kPrepThreads, 0, stream>>>(p);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
