@@ -14,7 +14,9 @@ resident in HBM before the timed region starts.
 (C2: T=1024 chunk after P = 0/3072/7168 prefix tokens, causal FLOP/s vs the
 2.5 PFLOP/s dense fp16 MFMA peak), the GDN recurrence (C3: 1024-token chunk
 prefill tok/s; single-token decode tok/s and GB/s cold over rotating state
-sets) and the fused GDN layer core (conv prologue + gated recurrence).
+sets) and the fused GDN layer core (conv prologue + gated recurrence), the C4 ragged block,
+and the box's achievable rates (a 2 GiB copy and read, fp16 and fp32 GEMMs on the vendor BLAS)
+with the hot-path results as fractions of them.
 
 `cpu_baseline`: the CPU oracle's restatement of the same decode step
 (oracle/kraken_oracle.c, one core), timed on a bounded sample.
@@ -404,6 +406,60 @@ def decode_traffic():
     return None
 
 
+def bench_peaks(torch, ctx, run):
+    """Achievable rates on this box, next to the published peaks.  The library's probes
+    (include/kraken_hip_diag.h): a nontemporal streaming read of 2 GiB and an fp16 MFMA loop
+    (one wave per SIMD, four independent v_mfma_f32_32x32x16_f16 chains), both timed as graph
+    replays like the hot-path kernels.  For comparison, the same box through torch: a 2 GiB
+    copy and sum, and dense fp16 / fp32 GEMMs on the vendor BLAS.  The roofline fractions in the
+    JSON line stay against the published peaks."""
+    def timed(fn, reps=10, warm=3):
+        for _ in range(warm):
+            fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3  # seconds per call
+
+    n = 1 << 29  # floats: 2 GiB
+    src = torch.ones(n, device="cuda")
+    sink = torch.empty(1 << 20, device="cuda")
+    ms_probe_read, graph = run.time([lambda: ctx.diag_stream_read(src, 4 * n, sink)] * 10, 2)
+    del graph
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 4000
+    ms_probe_mfma, graph = run.time([lambda: ctx.diag_mfma_f16(cus, iters, sink)] * 5, 1)
+    del graph
+    mfma_flops = cus * 4 * iters * 8 * 32768
+    dst = torch.empty_like(src)
+    t_copy = timed(lambda: dst.copy_(src))
+    t_read = timed(lambda: src.sum())
+    del src, dst, sink
+    m = 8192
+    a = torch.randn(m, m, device="cuda", dtype=torch.float16)
+    b = torch.randn(m, m, device="cuda", dtype=torch.float16)
+    t_h = timed(lambda: torch.matmul(a, b))
+    del a, b
+    m32 = 4096
+    a = torch.randn(m32, m32, device="cuda")
+    b = torch.randn(m32, m32, device="cuda")
+    t_f = timed(lambda: torch.matmul(a, b))
+    del a, b
+    return {"probe_read_GB_s": 4 * n / (ms_probe_read * 1e-3) / 1e9,
+            "probe_mfma_f16_TFLOP_s": mfma_flops / (ms_probe_mfma * 1e-3) / 1e12,
+            "torch_copy_GB_s": 2 * 4 * n / t_copy / 1e9, "torch_read_GB_s": 4 * n / t_read / 1e9,
+            "fp16_gemm_TFLOP_s": 2 * m ** 3 / t_h / 1e12,
+            "fp32_gemm_TFLOP_s": 2 * m32 ** 3 / t_f / 1e12,
+            "note": "probes: kraken_hip_diag_stream_read over 2 GiB, kraken_hip_diag_mfma_f16 "
+                    f"({cus} workgroups x {iters} iterations); torch: 2 GiB copy_ (read + "
+                    "write bytes) and sum (read bytes), matmul 8192^3 fp16 and 4096^3 fp32"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -412,9 +468,9 @@ def main():
     ap.add_argument("--kv-len", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline only, no details")
-    ap.add_argument("--sections", default="decode,prefill,gdn,c4",
+    ap.add_argument("--sections", default="decode,prefill,gdn,c4,peaks",
                     help="comma-separated detail sections to run after the headline "
-                         "(decode, prefill, gdn, c4)")
+                         "(decode, prefill, gdn, c4, peaks)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run torch copies of MIB MiB (20 launches), the known-size "
@@ -470,6 +526,20 @@ def main():
             gen.manual_seed(4)
             details["ragged_c4"] = bench_c4(torch, ctx, run, gen)
             progress("ragged c4 done")
+        if "peaks" in sections:
+            peaks = bench_peaks(torch, ctx, run)
+            details["achievable_peaks"] = peaks
+            # The hot-path results as fractions of what this box reaches.
+            vs = {"decode_c1_vs_probe_read": head["GB_s"] / peaks["probe_read_GB_s"]}
+            if "ragged_c4" in details:
+                vs["c4_attention_vs_probe_read"] = (details["ragged_c4"]["attention"]["GB_s"] /
+                                                    peaks["probe_read_GB_s"])
+            if "prefill_c2" in details:
+                vs["prefill_c2_vs_probe_mfma"] = [x["TFLOP_s"] / peaks["probe_mfma_f16_TFLOP_s"]
+                                                  for x in details["prefill_c2"]]
+            details["vs_achievable"] = vs
+            progress(f"peaks: probe read {peaks['probe_read_GB_s']:.0f} GB/s, probe MFMA "
+                     f"{peaks['probe_mfma_f16_TFLOP_s']:.0f} TFLOP/s")
     run.close()
     ctx.close()
 

@@ -12,14 +12,6 @@
 
 using namespace kraken;
 
-#define KRAKEN_TRY(expr)            \
-  do {                              \
-    const int kraken_s_ = (expr);   \
-    if (kraken_s_ != KRAKEN_OK) {   \
-      return kraken_s_;             \
-    }                               \
-  } while (0)
-
 namespace {
 
 enum class FlashChoice { automatic, force_on, force_off };

@@ -26,6 +26,15 @@ struct kraken_hip_context {
   size_t workspace_bytes = 0;
 };
 
+// Returns from the calling entry point with the status of `expr` unless it is OK.
+#define KRAKEN_TRY(expr)            \
+  do {                              \
+    const int kraken_s_ = (expr);   \
+    if (kraken_s_ != KRAKEN_OK) {   \
+      return kraken_s_;             \
+    }                               \
+  } while (0)
+
 namespace kraken {
 
 // --------------------------------------------------------------- status ----

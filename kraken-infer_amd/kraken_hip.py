@@ -46,6 +46,9 @@ _ctx = ctypes.c_void_p
 
 # name -> argument types after the context pointer (all return int).
 SIGNATURES = {
+    # Measurement aids (include/kraken_hip_diag.h).
+    "kraken_hip_diag_stream_read": [_B, _sz, _B],
+    "kraken_hip_diag_mfma_f16": [ctypes.c_uint32, ctypes.c_uint32, _B],
     "kraken_hip_attention_f32_batched_f16_kv": [_B, _B, _B] + [_sz] * 7 + [_B],
     "kraken_hip_attention_f32_batched": [_B, _B, _B] + [_sz] * 7 + [_B],
     "kraken_hip_attention_f32_batched_f16_kv_gated": [_B, _B, _B, _B] + [_sz] * 7 + [_B],

@@ -8,6 +8,7 @@ mps_backend.mm:10625-10713 for attention.  The validation-only context runs
 every check and answers `unavailable` instead of launching.
 """
 import ctypes
+import glob
 import os
 import re
 
@@ -16,12 +17,13 @@ import pytest
 import kraken_hip as kh
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "kraken_hip.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 ACCEPTED = "validation-only context: arguments accepted"
 
 
 def declared_symbols():
-    text = open(HEADER).read()
+    """Entry points declared in every C header under include/."""
+    text = "".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"KRAKEN_API[^;]*?\b(kraken_hip_\w+)\s*\(", text, re.S)))
 
 
@@ -363,3 +365,21 @@ def test_gdn_layer_dt_bias_and_ssm_a_together(vctx):
     args[8] = kh.KrakenBuffer(None, 0)  # ssm_a missing, dt_bias given
     code, msg = status(vctx, "qwen35_gdn_layer_ragged_decode_f32", *args)
     assert code == kh.INVALID_ARGUMENT and "given together" in msg
+
+
+def test_diag_probe_argument_checks(vctx):
+    """The measurement aids (include/kraken_hip_diag.h) check sizes and alignment."""
+    sink = fake(256 * 256 * 4)
+    assert status(vctx, "diag_stream_read", fake(1 << 20), 1 << 20, sink) == (kh.UNAVAILABLE,
+                                                                             ACCEPTED)
+    code, _ = status(vctx, "diag_stream_read", fake(1 << 20), 1000, sink)  # not a multiple of 16
+    assert code == kh.INVALID_ARGUMENT
+    code, _ = status(vctx, "diag_stream_read", fake(1 << 10), 1 << 20, sink)  # source too small
+    assert code == kh.INVALID_ARGUMENT
+    code, _ = status(vctx, "diag_stream_read", fake(1 << 20), 1 << 20, fake(16))  # sink too small
+    assert code == kh.INVALID_ARGUMENT
+    assert status(vctx, "diag_mfma_f16", 256, 10, sink) == (kh.UNAVAILABLE, ACCEPTED)
+    code, _ = status(vctx, "diag_mfma_f16", 257, 10, sink)  # sink holds 256 workgroups
+    assert code == kh.INVALID_ARGUMENT
+    code, _ = status(vctx, "diag_mfma_f16", 256, 0, sink)
+    assert code == kh.INVALID_ARGUMENT
