@@ -22,6 +22,7 @@
 #include <string>
 #include <vector>
 
+#include "kraken/qwen35_bench.hpp"
 #include "kraken/qwen35_layers.hpp"
 
 using kraken::hip::HipBuffer;
@@ -364,10 +365,61 @@ int run_full(const std::string& dir, q35::OpOrder order) {
 
 }  // namespace
 
+// bench-gdn <tokens> <key_heads> <value_heads> <head_dim> <warmup> <timed>
+// bench-attention <tokens> <start> <capacity> <heads> <kv_heads> <head_dim> <warmup> <timed> <f16>
+// Prints the formatted result, or "error <code>: <message>" (exit 1).
+int run_bench(const std::string& mode, int argc, char** argv) {
+  auto arg = [&](int i) { return (std::size_t)std::strtoull(argv[i], nullptr, 10); };
+  auto fail = [](const kraken::hip::Status& s) {
+    std::printf("error %d: %s\n", (int)s.code(), s.message().c_str());
+    return 1;
+  };
+  if (mode == "bench-gdn" && argc >= 8) {
+    q35::GdnBenchConfig c;
+    c.tokens = arg(2);
+    c.key_heads = arg(3);
+    c.value_heads = arg(4);
+    c.head_dim = arg(5);
+    c.warmup_iterations = arg(6);
+    c.timed_iterations = arg(7);
+    auto r = q35::benchmark_gdn(c);
+    if (!r.is_ok()) {
+      return fail(r.status());
+    }
+    std::printf("%s", q35::format_gdn_bench_result(r.value()).c_str());
+    std::printf("checksum_exact %.17g\n", r.value().sample_checksum);
+    return 0;
+  }
+  if (mode == "bench-attention" && argc >= 11) {
+    q35::AttentionBenchConfig c;
+    c.tokens = arg(2);
+    c.start_position = arg(3);
+    c.capacity_tokens = arg(4);
+    c.heads = arg(5);
+    c.kv_heads = arg(6);
+    c.head_dim = arg(7);
+    c.warmup_iterations = arg(8);
+    c.timed_iterations = arg(9);
+    c.f16_kv = arg(10) != 0;
+    auto r = q35::benchmark_attention(c);
+    if (!r.is_ok()) {
+      return fail(r.status());
+    }
+    std::printf("%s", q35::format_attention_bench_result(r.value()).c_str());
+    std::printf("checksum_exact %.17g\n", r.value().sample_checksum);
+    return 0;
+  }
+  std::printf("usage: see run_bench\n");
+  return 2;
+}
+
 int main(int argc, char** argv) {
   const std::string mode = argc > 1 ? argv[1] : "plan";
   if (mode == "plan") {
     return run_plan();
+  }
+  if (mode.rfind("bench-", 0) == 0) {
+    return run_bench(mode, argc, argv);
   }
   if (argc < 4) {
     std::printf("usage: qwen35_driver_check plan | linear <dir> <order> | full <dir> <order>\n");
