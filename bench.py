@@ -392,6 +392,97 @@ def cpu_baseline(kv_len, budget_s):
             "host_threads_available": os.cpu_count()}
 
 
+def host_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "cpu_count": os.cpu_count(),
+            "affinity": len(os.sched_getaffinity(0))}
+
+
+def cpu_baselines(budget_s):
+    """The CPU oracle (oracle/kraken_oracle.c, -O3, one thread, called through ctypes) on a
+    bounded sample of each configuration, about `budget_s` seconds each.  Scaled figures say
+    so in their names."""
+    import numpy as np
+
+    import oracle
+
+    oracle.lib()
+    rng = np.random.default_rng(0)
+
+    def timed(fn):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn(n)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                return el / n, n
+
+    res = {"host": host_info(), "threads": 1}
+    # C0: legacy attention decode steps (16 Q / 8 KV heads, head_dim 128, F32 KV) at the
+    # positions of the 64 decode steps after a 512-token prefill.
+    cap = 576
+    kc0 = rng.standard_normal(cap * 8 * 128).astype(np.float32)
+    vc0 = rng.standard_normal(cap * 8 * 128).astype(np.float32)
+    q0 = rng.standard_normal(16 * 128).astype(np.float32)
+    sec, n = timed(lambda i: oracle.qwen3_attention(kc0, vc0, cap, 0, 512 + i % 64, q0, 16, 8,
+                                                    128))
+    res["c0_decode"] = {"ms_per_step": sec * 1e3, "steps_sampled": n,
+                        "sample": "oracle_qwen3_attention at positions 512..575"}
+    # C2: flash256 prefill at P=7168, sampled query tokens of the chunk.
+    p, t = 7168, 1024
+    cap2 = p + t
+    kc2 = rng.standard_normal(cap2 * HKV * D).astype(np.float16).view(np.uint16)
+    vc2 = rng.standard_normal(cap2 * HKV * D).astype(np.float16).view(np.uint16)
+    q2 = rng.standard_normal(HQ * D).astype(np.float32)
+    toks = [0, 255, 511, 767, 1023]
+    sec, n = timed(lambda i: oracle.attention_batched(q2, kc2, vc2, 0, p + toks[i % 5], 1, cap2,
+                                                      HQ, HKV, D, round_query_f16=True))
+    mean_keys = p + sum(toks) / len(toks) + 1
+    res["c2_prefill_p7168"] = {
+        "TFLOP_s": 8192 * mean_keys / sec / 1e12, "ms_per_token": sec * 1e3,
+        "ms_per_chunk_scaled": sec * 1e3 * t, "tokens_sampled": n,
+        "sample": "oracle_attention_batched, one query token at a time (tokens 0, 255, 511, "
+                  "767, 1023 of the chunk)"}
+    # C3: GDN recurrence, 16 heads, head_dim 128: a 64-token prefill and single-token decode.
+    hk = hv = 16
+    dk = 128
+    state = np.zeros(hv * dk * dk, np.float32)
+    qg = rng.standard_normal(64 * hk * dk).astype(np.float32)
+    gg = -np.log1p(np.exp(rng.standard_normal(64 * hv))).astype(np.float32)
+    bb = (1 / (1 + np.exp(-rng.standard_normal(64 * hv)))).astype(np.float32)
+    sec, n = timed(lambda i: oracle.gated_delta_net(qg, qg, qg, gg, bb, state, 64, hk, hv, dk))
+    res["c3_prefill"] = {"tok_s": 64 / sec, "ms_per_64_tokens": sec * 1e3, "calls": n}
+    sec1, n1 = timed(lambda i: oracle.gated_delta_net(qg, qg, qg, gg, bb, state, 1, hk, hv, dk))
+    res["c3_decode"] = {"tok_s": 1 / sec1, "ms_per_token": sec1 * 1e3, "calls": n1}
+    # C4: one sequence's block step (attention decode at the mean K/V length 16872, plus three
+    # GDN decode steps), scaled to 64 sequences on one thread.
+    l4 = 16872
+    kc4 = rng.standard_normal((l4 + 1) * HKV * D).astype(np.float16).view(np.uint16)
+    vc4 = rng.standard_normal((l4 + 1) * HKV * D).astype(np.float16).view(np.uint16)
+
+    def c4_step(i):
+        oracle.attention_batched(q2, kc4, vc4, 0, l4, 1, l4 + 1, HQ, HKV, D)
+        for _ in range(3):
+            oracle.gated_delta_net(qg, qg, qg, gg, bb, state, 1, hk, hv, dk)
+
+    sec4, n4 = timed(c4_step)
+    res["c4_block"] = {"ms_per_sequence_step": sec4 * 1e3,
+                       "tok_s_64_sequences_scaled": 1 / sec4,
+                       "sequence_steps_sampled": n4,
+                       "sample": "one sequence at the mean K/V length 16872: attention decode "
+                                 "+ 3 GDN decode steps; 64 sequences on one thread take 64x"}
+    return res
+
+
 def decode_traffic():
     """HBM bytes per C1 (L=4096) decode step from the committed rocprofv3 counter
     summary (FETCH_SIZE + WRITE_SIZE of both dispatches, scaled by the plain-copy
@@ -544,6 +635,8 @@ def main():
     ctx.close()
 
     cpu = None if args.no_cpu else cpu_baseline(args.kv_len, args.cpu_seconds)
+    if not args.no_cpu and not args.quick:
+        details["cpu_baselines"] = cpu_baselines(2.0)
     progress("cpu baseline done")
     traffic = decode_traffic() if args.kv_len == 4096 else None
     line = {
