@@ -221,6 +221,26 @@ def bench_gdn(torch, ctx, run, gen):
     ms, graph = run.time([lstep(i) for i in range(512)], 8)
     del graph
     res["decode_layer_core_fused"] = {"ms_per_token_layer": ms, "tok_s": 1 / (ms * 1e-3)}
+
+    # The same layer (conv prologue, gate/beta prepare, recurrence, norm-gated epilogue) in
+    # one kernel: the ragged GDN-layer entry with a single sequence, cold over the state sets.
+    conv_offs = [torch.tensor([i * channels * 3], device=dev, dtype=torch.int64)
+                 for i in range(sets)]
+    state_offs = [torch.tensor([i * hv * d * d], device=dev, dtype=torch.int64)
+                  for i in range(sets)]
+
+    def ostep(i):
+        def f():
+            ctx.qwen35_gdn_layer_ragged_decode_f32(qkv, conv_states, conv_offs[i % sets], w, 4,
+                                                   alpha, beta, dtb, ssa, z, nw, states,
+                                                   state_offs[i % sets], 1, hk, hv, d, 1e-6,
+                                                   out1)
+        return f
+
+    ms, graph = run.time([ostep(i) for i in range(512)], 8)
+    del graph
+    res["decode_layer_one_kernel"] = {"ms_per_token_layer": ms, "tok_s": 1 / (ms * 1e-3),
+                                      "GB_s": GDN_DECODE_BYTES / (ms * 1e-3) / 1e9}
     del states, conv_states
     torch.cuda.empty_cache()
     return res
