@@ -188,6 +188,19 @@ namespace detail {
   HipBuffer& vb = *v.value();
 
   Status s;
+  if (order == OpOrder::fused && tokens == 1 && cache.recurrent_offsets.valid()) {
+    // One decode token: conv prologue, gated delta rule and norm-gated epilogue
+    // in one launch, the slot's offsets read from the cache's offset table.
+    auto* table = static_cast<unsigned char*>(cache.recurrent_offsets.data());
+    const HipBuffer conv_offset =
+      HipBuffer::borrow(table + 2 * slot * sizeof(std::uint64_t), sizeof(std::uint64_t));
+    const HipBuffer state_offset =
+      HipBuffer::borrow(table + (2 * slot + 1) * sizeof(std::uint64_t), sizeof(std::uint64_t));
+    return ctx.qwen35_gdn_layer_ragged_decode_f32(
+      qkv_mixed, cache.recurrent_r_cache, conv_offset, *w.conv1d, kc, alpha, beta, *w.dt_bias,
+      *w.ssm_a, z, *w.ssm_norm, cache.recurrent_s_cache, state_offset, 1, hk, hv, dk, rms_eps,
+      output);
+  }
   if (order == OpOrder::fused) {
     s = ctx.qwen35_conv_split_l2_f32(qkv_mixed, cache.recurrent_r_cache, r_offset, *w.conv1d, kc,
                                      tokens, hk, hv, dk, rms_eps, qb, kb, vb);

@@ -339,6 +339,10 @@ struct DeviceCache {
   HipBuffer value_cache;
   HipBuffer recurrent_r_cache;
   HipBuffer recurrent_s_cache;
+  // Per recurrent slot (linear_layer * recurrent_rows + row) the pair of element
+  // offsets {R offset, S offset}, uint64, so one-sequence decode can address its
+  // slot through the ragged layer kernel without a per-token upload.
+  HipBuffer recurrent_offsets;
   bool kv_cache_f16{true};
   std::uint64_t key_cache_bytes{0};
   std::uint64_t value_cache_bytes{0};
@@ -386,6 +390,25 @@ struct DeviceCache {
     const Status z = context.zero_buffer(*part.buffer, static_cast<std::size_t>(part.bytes));
     if (!z.is_ok()) {
       return z;
+    }
+  }
+  const std::size_t slots = plan.cache.linear_attention_layers * plan.cache.recurrent_rows;
+  if (slots > 0) {
+    std::vector<std::uint64_t> offsets(2 * slots);
+    for (std::size_t i = 0; i < slots; ++i) {
+      offsets[2 * i] = static_cast<std::uint64_t>(i) * plan.cache.recurrent_r_elements_per_layer;
+      offsets[2 * i + 1] =
+        static_cast<std::uint64_t>(i) * plan.cache.recurrent_s_elements_per_layer;
+    }
+    const std::size_t bytes = offsets.size() * sizeof(std::uint64_t);
+    auto b = context.make_buffer(bytes);
+    if (!b.is_ok()) {
+      return b.status();
+    }
+    cache.recurrent_offsets = std::move(b.value());
+    const Status c = context.copy_to_buffer(cache.recurrent_offsets, offsets.data(), bytes);
+    if (!c.is_ok()) {
+      return c;
     }
   }
   return cache;
