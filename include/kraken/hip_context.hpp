@@ -239,6 +239,13 @@ class HipContext {
   [[nodiscard]] Status zero_buffer(HipBuffer& buffer, std::size_t byte_size) const {
     return Status::from_code(kraken_hip_zero_buffer(ctx_, buffer.raw(), byte_size));
   }
+  // Many ranges from `source` to `destination` in one launch (no counterpart in
+  // the reference; at most KRAKEN_COPY_REGIONS_MAX per call).
+  [[nodiscard]] Status copy_regions(const HipBuffer& source, HipBuffer& destination,
+                                    const kraken_copy_region* regions, std::size_t count) const {
+    return Status::from_code(
+      kraken_hip_copy_regions(ctx_, source.raw(), destination.raw(), regions, count));
+  }
 
   // Attention (mps_backend.hpp:404-420).
   [[nodiscard]] Status attention_f32_batched_f16_kv(

@@ -14,12 +14,14 @@
 //
 // Where the reference keeps payloads in host memory (unified memory on its
 // platform), this store keeps them in HBM: one device allocation per block,
-// filled and drained with stream-ordered device-to-device copies, so neither
-// commit nor restore crosses PCIe or waits for the host.  A block evicted by
+// filled and drained with device-to-device copies, so neither commit nor
+// restore crosses PCIe.  The rows of all layers move in one launch
+// (kraken_hip_copy_regions) rather than one copy per layer and cache.  A block evicted by
 // the index hands its allocation to the next commit.  Its size is fixed by the
 // layout, e.g. about 19 MiB a block for Qwen3.5-0.8B with 1024-token blocks.
 #pragma once
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 #include <limits>
@@ -126,7 +128,14 @@ class PrefixCacheStore {
     if (!hash.has_value() || payloads_.count(*hash) != 0) {
       return PrefixCommitResult{};
     }
-    auto payload = read_payload(ctx, cache, plan, chunk_hidden, token_start, chunk_tokens);
+    Result<Payload> payload = Status::ok();
+    const Status read = deferred(ctx, [&]() {
+      payload = read_payload(ctx, cache, plan, chunk_hidden, token_start, chunk_tokens);
+      return payload.status();
+    });
+    if (!read.is_ok()) {
+      return read;
+    }
     if (!payload.is_ok()) {
       return payload.status();
     }
@@ -157,6 +166,39 @@ class PrefixCacheStore {
     if (!layout_.has_value()) {
       return Status::ok();
     }
+    return deferred(ctx, [&]() { return restore_blocks(ctx, cache, plan, block_hashes); });
+  }
+
+  // qwen35_runtime.cpp:708-715: the stored last hidden row of a block, as a
+  // device view of hidden_size floats (copy it out with copy_buffer_region),
+  // or nullptr when the block is not stored.
+  [[nodiscard]] const HipBuffer* last_hidden(std::uint64_t hash) const {
+    const auto it = payloads_.find(hash);
+    return it == payloads_.end() ? nullptr : &it->second.last_hidden;
+  }
+
+  [[nodiscard]] PrefixCacheStats stats() const { return index_.stats(); }
+
+ private:
+  // Runs `body` with the context's per-launch host wait off, so the copies are
+  // waited for once at the end; inside a caller's open graph the caller's
+  // commit waits for them instead.
+  template <class Body>
+  [[nodiscard]] static Status deferred(const HipContext& ctx, Body&& body) {
+    if (!ctx.begin_graph().is_ok()) {
+      return body();
+    }
+    const Status s = body();
+    if (!s.is_ok()) {
+      ctx.abort_graph();
+      return s;
+    }
+    return ctx.commit_graph();
+  }
+
+  [[nodiscard]] Status restore_blocks(const HipContext& ctx, DeviceCache& cache,
+                                      const ExecutionPlan& plan,
+                                      const std::vector<std::uint64_t>& block_hashes) const {
     for (std::size_t i = 0; i < block_hashes.size(); ++i) {
       const auto it = payloads_.find(block_hashes[i]);
       if (it == payloads_.end()) {
@@ -177,17 +219,6 @@ class PrefixCacheStore {
     return Status::ok();
   }
 
-  // qwen35_runtime.cpp:708-715: the stored last hidden row of a block, as a
-  // device view of hidden_size floats (copy it out with copy_buffer_region),
-  // or nullptr when the block is not stored.
-  [[nodiscard]] const HipBuffer* last_hidden(std::uint64_t hash) const {
-    const auto it = payloads_.find(hash);
-    return it == payloads_.end() ? nullptr : &it->second.last_hidden;
-  }
-
-  [[nodiscard]] PrefixCacheStats stats() const { return index_.stats(); }
-
- private:
   struct Payload {
     HipBuffer storage;      // K | V | R | S | last hidden, one allocation
     HipBuffer last_hidden;  // view into storage
@@ -216,6 +247,39 @@ class PrefixCacheStore {
     }
     out = a + b;
     return true;
+  }
+
+  // Issues `regions` in launches of at most KRAKEN_COPY_REGIONS_MAX ranges.
+  [[nodiscard]] static Status copy_all(const HipContext& ctx, const HipBuffer& source,
+                                       HipBuffer& destination,
+                                       const std::vector<kraken_copy_region>& regions) {
+    for (std::size_t i = 0; i < regions.size(); i += KRAKEN_COPY_REGIONS_MAX) {
+      const std::size_t n = std::min<std::size_t>(KRAKEN_COPY_REGIONS_MAX, regions.size() - i);
+      const Status s = ctx.copy_regions(source, destination, regions.data() + i, n);
+      if (!s.is_ok()) {
+        return s;
+      }
+    }
+    return Status::ok();
+  }
+
+  // The block's rows of every full-attention layer: {cache offset, payload offset}.
+  [[nodiscard]] Result<std::vector<kraken_copy_region>> kv_regions(const ExecutionPlan& plan,
+                                                                   const Offsets& o,
+                                                                   std::size_t token_start,
+                                                                   bool to_payload) const {
+    std::vector<kraken_copy_region> regions;
+    regions.reserve(layout_->full_attention_layers);
+    for (std::size_t layer = 0; layer < layout_->full_attention_layers; ++layer) {
+      auto row = cache_row_offset(plan, layer, token_start);
+      if (!row.is_ok()) {
+        return row.status();
+      }
+      const std::size_t at = layer * o.kv_block_layer;
+      regions.push_back(to_payload ? kraken_copy_region{row.value(), at, o.kv_block_layer}
+                                   : kraken_copy_region{at, row.value(), o.kv_block_layer});
+    }
+    return regions;
   }
 
   // Payload sizes and sections (qwen35_runtime.cpp:725-750, 766-777, 811-857),
@@ -312,36 +376,29 @@ class PrefixCacheStore {
       }
       p.storage = std::move(b.value());
     }
-    for (std::size_t layer = 0; layer < layout_->full_attention_layers; ++layer) {
-      auto src = cache_row_offset(plan, layer, token_start);
-      if (!src.is_ok()) {
-        return src.status();
-      }
-      const std::size_t dst = layer * o.kv_block_layer;
-      Status s = ctx.copy_buffer_region(cache.key_cache, p.storage, src.value(), o.key + dst,
-                                        o.kv_block_layer);
-      if (s.is_ok()) {
-        s = ctx.copy_buffer_region(cache.value_cache, p.storage, src.value(), o.value + dst,
-                                   o.kv_block_layer);
-      }
-      if (!s.is_ok()) {
-        return s;
-      }
+    // K and V rows: the K section is the payload's start and the V section
+    // follows it, so the same ranges shifted by o.value serve V.
+    auto kv = kv_regions(plan, o, token_start, true);
+    if (!kv.is_ok()) {
+      return kv.status();
     }
-    if (o.r_bytes != 0) {
-      const Status s = ctx.copy_buffer_region(cache.recurrent_r_cache, p.storage, 0, o.r, o.r_bytes);
-      if (!s.is_ok()) {
-        return s;
-      }
+    std::vector<kraken_copy_region> v_regions = kv.value();
+    for (kraken_copy_region& g : v_regions) {
+      g.destination_offset += o.value;
     }
-    if (o.s_bytes != 0) {
-      const Status s = ctx.copy_buffer_region(cache.recurrent_s_cache, p.storage, 0, o.s, o.s_bytes);
-      if (!s.is_ok()) {
-        return s;
-      }
+    Status s = copy_all(ctx, cache.key_cache, p.storage, kv.value());
+    if (s.is_ok()) {
+      s = copy_all(ctx, cache.value_cache, p.storage, v_regions);
     }
-    const Status s = ctx.copy_buffer_region(chunk_hidden, p.storage, hidden_offset, o.hidden,
-                                            o.hidden_bytes);
+    if (s.is_ok() && o.r_bytes != 0) {
+      s = copy_all(ctx, cache.recurrent_r_cache, p.storage, {{0, o.r, o.r_bytes}});
+    }
+    if (s.is_ok() && o.s_bytes != 0) {
+      s = copy_all(ctx, cache.recurrent_s_cache, p.storage, {{0, o.s, o.s_bytes}});
+    }
+    if (s.is_ok()) {
+      s = copy_all(ctx, chunk_hidden, p.storage, {{hidden_offset, o.hidden, o.hidden_bytes}});
+    }
     if (!s.is_ok()) {
       return s;
     }
@@ -359,23 +416,16 @@ class PrefixCacheStore {
       return off.status();
     }
     const Offsets& o = off.value();
-    for (std::size_t layer = 0; layer < layout_->full_attention_layers; ++layer) {
-      auto dst = cache_row_offset(plan, layer, token_start);
-      if (!dst.is_ok()) {
-        return dst.status();
-      }
-      const std::size_t src = layer * o.kv_block_layer;
-      Status s = ctx.copy_buffer_region(p.storage, cache.key_cache, o.key + src, dst.value(),
-                                        o.kv_block_layer);
-      if (s.is_ok()) {
-        s = ctx.copy_buffer_region(p.storage, cache.value_cache, o.value + src, dst.value(),
-                                   o.kv_block_layer);
-      }
-      if (!s.is_ok()) {
-        return s;
-      }
+    auto kv = kv_regions(plan, o, token_start, false);
+    if (!kv.is_ok()) {
+      return kv.status();
     }
-    return Status::ok();
+    std::vector<kraken_copy_region> v_regions = kv.value();
+    for (kraken_copy_region& g : v_regions) {
+      g.source_offset += o.value;
+    }
+    const Status s = copy_all(ctx, p.storage, cache.key_cache, kv.value());
+    return s.is_ok() ? copy_all(ctx, p.storage, cache.value_cache, v_regions) : s;
   }
 
   // qwen35_runtime.cpp:895-921
@@ -387,13 +437,13 @@ class PrefixCacheStore {
     }
     const Offsets& o = off.value();
     if (o.r_bytes != 0) {
-      const Status s = ctx.copy_buffer_region(p.storage, cache.recurrent_r_cache, o.r, 0, o.r_bytes);
+      const Status s = copy_all(ctx, p.storage, cache.recurrent_r_cache, {{o.r, 0, o.r_bytes}});
       if (!s.is_ok()) {
         return s;
       }
     }
     if (o.s_bytes != 0) {
-      return ctx.copy_buffer_region(p.storage, cache.recurrent_s_cache, o.s, 0, o.s_bytes);
+      return copy_all(ctx, p.storage, cache.recurrent_s_cache, {{o.s, 0, o.s_bytes}});
     }
     return Status::ok();
   }

@@ -120,6 +120,23 @@ KRAKEN_API int kraken_hip_copy_buffer_region(kraken_hip_context* context, kraken
 KRAKEN_API int kraken_hip_zero_buffer(kraken_hip_context* context, kraken_buffer buffer,
                                       size_t byte_size);
 
+/* Many byte ranges from one buffer to another in one launch (no counterpart in
+ * the reference, which copies range by range; the prefix cache store uses it to
+ * move a block's rows of every layer at once).  `regions` is a host array of
+ * `count` triples {source_offset, destination_offset, byte_size}; count is at
+ * most KRAKEN_COPY_REGIONS_MAX and every range must lie inside its buffer.
+ * Ranges must not overlap each other's destinations or a source they read.
+ * Stream-ordered: no host wait, no allocation. */
+#define KRAKEN_COPY_REGIONS_MAX 64
+typedef struct kraken_copy_region {
+  size_t source_offset;
+  size_t destination_offset;
+  size_t byte_size;
+} kraken_copy_region;
+KRAKEN_API int kraken_hip_copy_regions(kraken_hip_context* context, kraken_buffer source,
+                                       kraken_buffer destination,
+                                       const kraken_copy_region* regions, size_t count);
+
 /* ------------------------------------------------------- attention ------ */
 
 /* MpsContext::attention_f32_batched_f16_kv (mps_backend.hpp:415-420;

@@ -93,6 +93,7 @@ SIGNATURES = {
     "kraken_hip_copy_from_buffer_at": [_B, _sz, ctypes.c_void_p, _sz],
     "kraken_hip_copy_buffer_region": [_B, _B, _sz, _sz, _sz],
     "kraken_hip_zero_buffer": [_B, _sz],
+    "kraken_hip_copy_regions": [_B, _B, ctypes.c_void_p, _sz],
     "kraken_hip_context_set_stream": [ctypes.c_void_p],
 }
 

@@ -383,3 +383,23 @@ def test_diag_probe_argument_checks(vctx):
     assert code == kh.INVALID_ARGUMENT
     code, _ = status(vctx, "diag_mfma_f16", 256, 0, sink)
     assert code == kh.INVALID_ARGUMENT
+
+
+class _Region(ctypes.Structure):
+    _fields_ = [("source_offset", ctypes.c_size_t), ("destination_offset", ctypes.c_size_t),
+                ("byte_size", ctypes.c_size_t)]
+
+
+def test_copy_regions_argument_checks(vctx):
+    """kraken_hip_copy_regions bounds every range by its buffers and caps the count."""
+    src, dst = fake(4096), fake(2048)
+    ok = (_Region * 2)((0, 0, 1024), (1024, 1024, 1024))
+    assert status(vctx, "copy_regions", src, dst, ctypes.addressof(ok), 2) == (kh.UNAVAILABLE,
+                                                                              ACCEPTED)
+    for bad in [(4000, 0, 200), (0, 1900, 200), (0, 0, 1 << 62)]:
+        r = (_Region * 1)(bad)
+        code, _ = status(vctx, "copy_regions", src, dst, ctypes.addressof(r), 1)
+        assert code == kh.INVALID_ARGUMENT, bad
+    many = (_Region * 65)()
+    code, _ = status(vctx, "copy_regions", src, dst, ctypes.addressof(many), 65)
+    assert code == kh.INVALID_ARGUMENT
