@@ -517,6 +517,25 @@ def decode_traffic():
     return None
 
 
+def bench_prefix():
+    """Prompt prefix cache store (include/kraken/qwen35_prefix_store.hpp): commit and
+    restore of 1024-token blocks of the Qwen3.5-0.8B cache, timed by
+    tests/cpp/prefix_cache_check.cpp in its own process."""
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "kraken-infer_amd", "build",
+                       "prefix_cache_check")
+    if not os.path.exists(exe):
+        raise RuntimeError(f"{exe} is not built (run __graft_entry__.build())")
+    out = subprocess.run([exe, "store-bench"], capture_output=True, text=True, timeout=120,
+                         check=True).stdout.split()
+    vals = {k: float(v) for k, v in zip(out[0::2], out[1::2])}
+    vals["note"] = ("8 blocks of 1024 tokens: K/V rows of 6 layers, R/S of 18 layers, last "
+                    "hidden row; restore = all 8 blocks' K/V rows + R/S once; commit includes "
+                    "the first allocation of each payload")
+    return vals
+
+
 def bench_peaks(torch, ctx, run):
     """Achievable rates on this box, next to the published peaks.  The library's probes
     (include/kraken_hip_diag.h): a nontemporal streaming read of 2 GiB and an fp16 MFMA loop
@@ -579,9 +598,9 @@ def main():
     ap.add_argument("--kv-len", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline only, no details")
-    ap.add_argument("--sections", default="decode,prefill,gdn,c4,peaks",
+    ap.add_argument("--sections", default="decode,prefill,gdn,c4,peaks,prefix",
                     help="comma-separated detail sections to run after the headline "
-                         "(decode, prefill, gdn, c4, peaks)")
+                         "(decode, prefill, gdn, c4, peaks, prefix)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run torch copies of MIB MiB (20 launches), the known-size "
@@ -653,6 +672,9 @@ def main():
                      f"{peaks['probe_mfma_f16_TFLOP_s']:.0f} TFLOP/s")
     run.close()
     ctx.close()
+    if "prefix" in sections:
+        details["prefix_store"] = bench_prefix()
+        progress(f"prefix store: restore {details['prefix_store']['restore_GB_s']:.0f} GB/s")
 
     cpu = None if args.no_cpu else cpu_baseline(args.kv_len, args.cpu_seconds)
     if not args.no_cpu and not args.quick:
