@@ -531,8 +531,8 @@ def bench_prefix():
                          check=True).stdout.split()
     vals = {k: float(v) for k, v in zip(out[0::2], out[1::2])}
     vals["note"] = ("8 blocks of 1024 tokens: K/V rows of 6 layers, R/S of 18 layers, last "
-                    "hidden row; restore = all 8 blocks' K/V rows + R/S once; commit includes "
-                    "the first allocation of each payload")
+                    "hidden row; restore = all 8 blocks' K/V rows + R/S once; payloads live in one "
+                    "HBM arena allocated at the first (untimed) commit")
     return vals
 
 

@@ -335,6 +335,11 @@ namespace detail {
 // Qwen35MetalCache (qwen35_runtime.cpp:35-45): the caller-owned caches the
 // layer drivers read and write, one device allocation each.
 struct DeviceCache {
+  // One device allocation holding the four caches below, each 256-byte aligned;
+  // key_cache .. recurrent_s_cache are views into it (a cache of zero bytes is
+  // an empty view).  One allocation lets a single region-copy launch move rows
+  // of several caches at once.
+  HipBuffer storage;
   HipBuffer key_cache;
   HipBuffer value_cache;
   HipBuffer recurrent_r_cache;
@@ -351,8 +356,8 @@ struct DeviceCache {
 };
 
 // allocate_qwen35_metal_cache (qwen35_runtime.cpp:1252-1330): K and V halves
-// of kv_cache_bytes, R and S caches, each zeroed.  A cache of zero bytes (no
-// layer of that kind) gets no allocation.
+// of kv_cache_bytes, R and S caches, all zeroed, as views into one allocation.
+// A cache of zero bytes (no layer of that kind) is an empty view.
 [[nodiscard]] inline Result<DeviceCache> allocate_device_cache(const HipContext& context,
                                                                const ExecutionPlan& plan) {
   if (plan.cache.kv_cache_bytes % 2 != 0) {
@@ -375,21 +380,35 @@ struct DeviceCache {
     {&cache.recurrent_r_cache, cache.recurrent_r_cache_bytes, "Qwen3.5 recurrent R cache"},
     {&cache.recurrent_s_cache, cache.recurrent_s_cache_bytes, "Qwen3.5 recurrent S cache"},
   };
-  for (const Part& part : parts) {
-    if (part.bytes == 0) {
-      continue;
+  constexpr std::uint64_t kMax = std::numeric_limits<std::size_t>::max();
+  std::uint64_t part_offsets[4] = {0, 0, 0, 0};
+  std::uint64_t total = 0;
+  for (int i = 0; i < 4; ++i) {
+    if (parts[i].bytes > kMax) {
+      return Status::invalid_argument(std::string{parts[i].name} + " exceeds size_t range");
     }
-    if (part.bytes > static_cast<std::uint64_t>(std::numeric_limits<std::size_t>::max())) {
-      return Status::invalid_argument(std::string{part.name} + " exceeds size_t range");
+    part_offsets[i] = total;
+    if (parts[i].bytes > kMax - 255 - total) {
+      return Status::invalid_argument("Qwen3.5 total cache exceeds size_t range");
     }
-    auto b = context.make_buffer(static_cast<std::size_t>(part.bytes));
+    total = (total + parts[i].bytes + 255) / 256 * 256;
+  }
+  if (total > 0) {
+    auto b = context.make_buffer(static_cast<std::size_t>(total));
     if (!b.is_ok()) {
       return b.status();
     }
-    *part.buffer = std::move(b.value());
-    const Status z = context.zero_buffer(*part.buffer, static_cast<std::size_t>(part.bytes));
+    cache.storage = std::move(b.value());
+    const Status z = context.zero_buffer(cache.storage, static_cast<std::size_t>(total));
     if (!z.is_ok()) {
       return z;
+    }
+    auto* base = static_cast<unsigned char*>(cache.storage.data());
+    for (int i = 0; i < 4; ++i) {
+      if (parts[i].bytes != 0) {
+        *parts[i].buffer = HipBuffer::borrow(base + part_offsets[i],
+                                             static_cast<std::size_t>(parts[i].bytes));
+      }
     }
   }
   const std::size_t slots = plan.cache.linear_attention_layers * plan.cache.recurrent_rows;

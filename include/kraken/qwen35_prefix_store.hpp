@@ -13,12 +13,15 @@
 // and S caches of the last block (:885-921).
 //
 // Where the reference keeps payloads in host memory (unified memory on its
-// platform), this store keeps them in HBM: one device allocation per block,
-// filled and drained with device-to-device copies, so neither commit nor
-// restore crosses PCIe.  The rows of all layers move in one launch
-// (kraken_hip_copy_regions) rather than one copy per layer and cache.  A block evicted by
-// the index hands its allocation to the next commit.  Its size is fixed by the
-// layout, e.g. about 19 MiB a block for Qwen3.5-0.8B with 1024-token blocks.
+// platform), this store keeps them in HBM: one arena of capacity_blocks + 1
+// payload slots, allocated at the first commit, filled and drained with
+// device-to-device region copies (kraken_hip_copy_regions), so neither commit
+// nor restore crosses PCIe.  With the device cache in one allocation
+// (allocate_device_cache), a commit is two launches (cache parts, hidden row)
+// and a restore of n blocks ceil((12 n + 2) / 64) launches for Qwen3.5-0.8B,
+// with one host wait each.  The spare slot takes a commit's payload before the
+// index decides, so a failed copy never touches a stored block.  A payload is
+// 32.8 MB for Qwen3.5-0.8B with 1024-token blocks.
 #pragma once
 
 #include <algorithm>
@@ -103,8 +106,9 @@ class PrefixCacheStore {
         config.min_reuse_tokens != c.min_reuse_tokens || config.enabled != c.enabled) {
       layout_ = layout;
       index_ = PrefixCacheIndex(config);
-      payloads_.clear();
-      spare_ = Payload{};
+      slot_of_.clear();
+      free_slots_.clear();
+      arena_ = HipBuffer{};
     }
   }
 
@@ -115,7 +119,7 @@ class PrefixCacheStore {
   // qwen35_runtime.cpp:639-675: after the prefill chunk [token_start,
   // token_start + chunk_tokens) of `tokens`, store its payload if it is one
   // whole block not yet stored.  `chunk_hidden` holds the chunk's hidden rows,
-  // [chunk_tokens][hidden_size] floats.
+  // [chunk_tokens][hidden_size] floats.  `cache` comes from allocate_device_cache.
   [[nodiscard]] Result<PrefixCommitResult> commit_block(
     const HipContext& ctx, const DeviceCache& cache, const ExecutionPlan& plan,
     const HipBuffer& chunk_hidden, const std::vector<std::int64_t>& tokens,
@@ -125,35 +129,40 @@ class PrefixCacheStore {
       return PrefixCommitResult{};
     }
     const std::optional<std::uint64_t> hash = index_.hash_for_block(tokens, token_start);
-    if (!hash.has_value() || payloads_.count(*hash) != 0) {
+    if (!hash.has_value() || slot_of_.count(*hash) != 0) {
       return PrefixCommitResult{};
     }
-    Result<Payload> payload = Status::ok();
+    auto off = offsets();
+    if (!off.is_ok()) {
+      return off.status();
+    }
+    const Status ready = ensure_arena(ctx, off.value());
+    if (!ready.is_ok()) {
+      return ready;
+    }
+    const std::size_t slot = free_slots_.back();
     const Status read = deferred(ctx, [&]() {
-      payload = read_payload(ctx, cache, plan, chunk_hidden, token_start, chunk_tokens);
-      return payload.status();
+      return read_payload(ctx, cache, plan, chunk_hidden, off.value(), slot, token_start,
+                          chunk_tokens);
     });
     if (!read.is_ok()) {
       return read;
     }
-    if (!payload.is_ok()) {
-      return payload.status();
-    }
     const PrefixCacheCommit commit = index_.commit_block(tokens, token_start);
     PrefixCommitResult result;
     if (!commit.inserted) {
-      spare_ = std::move(payload.value());
       return result;
     }
+    free_slots_.pop_back();
     if (commit.evicted) {
-      const auto it = payloads_.find(commit.evicted_hash);
-      if (it != payloads_.end()) {
-        spare_ = std::move(it->second);
-        payloads_.erase(it);
+      const auto it = slot_of_.find(commit.evicted_hash);
+      if (it != slot_of_.end()) {
+        free_slots_.push_back(it->second);
+        slot_of_.erase(it);
       }
       result.evicted = true;
     }
-    payloads_[commit.hash] = std::move(payload.value());
+    slot_of_[commit.hash] = slot;
     result.committed = true;
     return result;
   }
@@ -163,66 +172,54 @@ class PrefixCacheStore {
   [[nodiscard]] Status restore(const HipContext& ctx, DeviceCache& cache,
                                const ExecutionPlan& plan,
                                const std::vector<std::uint64_t>& block_hashes) const {
-    if (!layout_.has_value()) {
+    if (!layout_.has_value() || block_hashes.empty()) {
       return Status::ok();
     }
-    return deferred(ctx, [&]() { return restore_blocks(ctx, cache, plan, block_hashes); });
+    std::vector<std::size_t> slots;
+    slots.reserve(block_hashes.size());
+    for (const std::uint64_t h : block_hashes) {
+      const auto it = slot_of_.find(h);
+      if (it == slot_of_.end()) {
+        return Status::invalid_argument("Qwen3.5 prefix cache payload is missing");
+      }
+      slots.push_back(it->second);
+    }
+    auto off = offsets();
+    if (!off.is_ok()) {
+      return off.status();
+    }
+    const Offsets& o = off.value();
+    std::vector<kraken_copy_region> regions;
+    for (std::size_t i = 0; i < slots.size(); ++i) {
+      const Status s = add_kv_regions(cache, plan, o, slots[i], i * layout_->block_tokens,
+                                      false, regions);
+      if (!s.is_ok()) {
+        return s;
+      }
+    }
+    const std::size_t last = slots.back() * o.total;
+    add_region(regions, last + o.r, part_offset(cache, cache.recurrent_r_cache), o.r_bytes);
+    add_region(regions, last + o.s, part_offset(cache, cache.recurrent_s_cache), o.s_bytes);
+    return deferred(ctx, [&]() { return copy_all(ctx, arena_, cache.storage, regions); });
   }
 
   // qwen35_runtime.cpp:708-715: the stored last hidden row of a block, as a
   // device view of hidden_size floats (copy it out with copy_buffer_region),
-  // or nullptr when the block is not stored.
-  [[nodiscard]] const HipBuffer* last_hidden(std::uint64_t hash) const {
-    const auto it = payloads_.find(hash);
-    return it == payloads_.end() ? nullptr : &it->second.last_hidden;
+  // or an empty view (valid() false) when the block is not stored.
+  [[nodiscard]] HipBuffer last_hidden(std::uint64_t hash) const {
+    const auto it = slot_of_.find(hash);
+    auto off = offsets();
+    if (it == slot_of_.end() || !off.is_ok() || !arena_.valid()) {
+      return HipBuffer{};
+    }
+    return HipBuffer::borrow(static_cast<unsigned char*>(arena_.data()) +
+                               it->second * off.value().total + off.value().hidden,
+                             off.value().hidden_bytes);
   }
 
   [[nodiscard]] PrefixCacheStats stats() const { return index_.stats(); }
 
  private:
-  // Runs `body` with the context's per-launch host wait off, so the copies are
-  // waited for once at the end; inside a caller's open graph the caller's
-  // commit waits for them instead.
-  template <class Body>
-  [[nodiscard]] static Status deferred(const HipContext& ctx, Body&& body) {
-    if (!ctx.begin_graph().is_ok()) {
-      return body();
-    }
-    const Status s = body();
-    if (!s.is_ok()) {
-      ctx.abort_graph();
-      return s;
-    }
-    return ctx.commit_graph();
-  }
-
-  [[nodiscard]] Status restore_blocks(const HipContext& ctx, DeviceCache& cache,
-                                      const ExecutionPlan& plan,
-                                      const std::vector<std::uint64_t>& block_hashes) const {
-    for (std::size_t i = 0; i < block_hashes.size(); ++i) {
-      const auto it = payloads_.find(block_hashes[i]);
-      if (it == payloads_.end()) {
-        return Status::invalid_argument("Qwen3.5 prefix cache payload is missing");
-      }
-      const Status s = restore_kv_block(ctx, cache, plan, it->second, i * layout_->block_tokens);
-      if (!s.is_ok()) {
-        return s;
-      }
-    }
-    if (!block_hashes.empty()) {
-      const auto it = payloads_.find(block_hashes.back());
-      if (it == payloads_.end()) {
-        return Status::invalid_argument("Qwen3.5 prefix cache payload is missing");
-      }
-      return restore_recurrent(ctx, cache, it->second);
-    }
-    return Status::ok();
-  }
-
-  struct Payload {
-    HipBuffer storage;      // K | V | R | S | last hidden, one allocation
-    HipBuffer last_hidden;  // view into storage
-  };
   struct Offsets {
     std::size_t kv_block_layer;  // bytes of one layer's block rows
     std::size_t key, value, r, s, hidden, total;
@@ -231,8 +228,9 @@ class PrefixCacheStore {
 
   PrefixCacheIndex index_{PrefixCacheConfig{}};
   std::optional<PrefixCacheLayout> layout_;
-  std::unordered_map<std::uint64_t, Payload> payloads_;
-  Payload spare_;
+  HipBuffer arena_;                                      // (capacity + 1) payload slots
+  std::unordered_map<std::uint64_t, std::size_t> slot_of_;  // stored block -> arena slot
+  std::vector<std::size_t> free_slots_;
 
   [[nodiscard]] static bool mul(std::size_t a, std::size_t b, std::size_t& out) {
     if (a != 0 && b > std::numeric_limits<std::size_t>::max() / a) {
@@ -249,6 +247,22 @@ class PrefixCacheStore {
     return true;
   }
 
+  // Runs `body` with the context's per-launch host wait off, so the copies are
+  // waited for once at the end; inside a caller's open graph the caller's
+  // commit waits for them instead.
+  template <class Body>
+  [[nodiscard]] static Status deferred(const HipContext& ctx, Body&& body) {
+    if (!ctx.begin_graph().is_ok()) {
+      return body();
+    }
+    const Status s = body();
+    if (!s.is_ok()) {
+      ctx.abort_graph();
+      return s;
+    }
+    return ctx.commit_graph();
+  }
+
   // Issues `regions` in launches of at most KRAKEN_COPY_REGIONS_MAX ranges.
   [[nodiscard]] static Status copy_all(const HipContext& ctx, const HipBuffer& source,
                                        HipBuffer& destination,
@@ -263,23 +277,42 @@ class PrefixCacheStore {
     return Status::ok();
   }
 
-  // The block's rows of every full-attention layer: {cache offset, payload offset}.
-  [[nodiscard]] Result<std::vector<kraken_copy_region>> kv_regions(const ExecutionPlan& plan,
-                                                                   const Offsets& o,
-                                                                   std::size_t token_start,
-                                                                   bool to_payload) const {
-    std::vector<kraken_copy_region> regions;
-    regions.reserve(layout_->full_attention_layers);
-    for (std::size_t layer = 0; layer < layout_->full_attention_layers; ++layer) {
-      auto row = cache_row_offset(plan, layer, token_start);
-      if (!row.is_ok()) {
-        return row.status();
-      }
-      const std::size_t at = layer * o.kv_block_layer;
-      regions.push_back(to_payload ? kraken_copy_region{row.value(), at, o.kv_block_layer}
-                                   : kraken_copy_region{at, row.value(), o.kv_block_layer});
+  static void add_region(std::vector<kraken_copy_region>& regions, std::size_t source,
+                         std::size_t destination, std::size_t bytes) {
+    if (bytes != 0) {
+      regions.push_back(kraken_copy_region{source, destination, bytes});
     }
-    return regions;
+  }
+
+  // Byte offset of one of the cache's parts within its one allocation.
+  [[nodiscard]] static std::size_t part_offset(const DeviceCache& cache, const HipBuffer& part) {
+    if (!part.valid()) {
+      return 0;
+    }
+    return static_cast<std::size_t>(static_cast<const unsigned char*>(part.data()) -
+                                    static_cast<const unsigned char*>(cache.storage.data()));
+  }
+
+  // Allocates the arena at the first commit: capacity + 1 slots, all free.
+  [[nodiscard]] Status ensure_arena(const HipContext& ctx, const Offsets& o) {
+    if (arena_.valid()) {
+      return Status::ok();
+    }
+    std::size_t bytes = 0;
+    const std::size_t slots = index_.config().capacity_blocks + 1;
+    if (slots == 0 || !mul(slots, o.total, bytes)) {
+      return Status::invalid_argument("Qwen3.5 prefix cache arena size overflow");
+    }
+    auto b = ctx.make_buffer(bytes);
+    if (!b.is_ok()) {
+      return b.status();
+    }
+    arena_ = std::move(b.value());
+    free_slots_.clear();
+    for (std::size_t i = slots; i-- > 0;) {
+      free_slots_.push_back(i);
+    }
+    return Status::ok();
   }
 
   // Payload sizes and sections (qwen35_runtime.cpp:725-750, 766-777, 811-857),
@@ -328,7 +361,7 @@ class PrefixCacheStore {
   }
 
   // qwen35_runtime.cpp:752-774: byte offset of cache row `token_start` of
-  // full-attention layer `layer`.
+  // full-attention layer `layer`, within the K (or V) cache.
   [[nodiscard]] static Result<std::size_t> cache_row_offset(const ExecutionPlan& plan,
                                                             std::size_t layer,
                                                             std::size_t token_start) {
@@ -350,102 +383,65 @@ class PrefixCacheStore {
     return bytes;
   }
 
-  // qwen35_runtime.cpp:776-859
-  [[nodiscard]] Result<Payload> read_payload(const HipContext& ctx, const DeviceCache& cache,
-                                             const ExecutionPlan& plan,
-                                             const HipBuffer& chunk_hidden,
-                                             std::size_t token_start,
-                                             std::size_t chunk_tokens) {
-    auto off = offsets();
-    if (!off.is_ok()) {
-      return off.status();
+  // The block's K and V rows of every full-attention layer, between arena slot
+  // `slot` and the cache's allocation (to_arena: cache -> arena).
+  [[nodiscard]] Status add_kv_regions(const DeviceCache& cache, const ExecutionPlan& plan,
+                                      const Offsets& o, std::size_t slot,
+                                      std::size_t token_start, bool to_arena,
+                                      std::vector<kraken_copy_region>& regions) const {
+    const std::size_t base = slot * o.total;
+    const std::size_t k_part = part_offset(cache, cache.key_cache);
+    const std::size_t v_part = part_offset(cache, cache.value_cache);
+    for (std::size_t layer = 0; layer < layout_->full_attention_layers; ++layer) {
+      auto row = cache_row_offset(plan, layer, token_start);
+      if (!row.is_ok()) {
+        return row.status();
+      }
+      const std::size_t at = layer * o.kv_block_layer;
+      const std::size_t pk = base + o.key + at, ck = k_part + row.value();
+      const std::size_t pv = base + o.value + at, cv = v_part + row.value();
+      if (to_arena) {
+        add_region(regions, ck, pk, o.kv_block_layer);
+        add_region(regions, cv, pv, o.kv_block_layer);
+      } else {
+        add_region(regions, pk, ck, o.kv_block_layer);
+        add_region(regions, pv, cv, o.kv_block_layer);
+      }
     }
-    const Offsets& o = off.value();
+    return Status::ok();
+  }
+
+  // qwen35_runtime.cpp:776-859: K/V rows, R and S from the cache's allocation in
+  // one launch, then the chunk's last hidden row.
+  [[nodiscard]] Status read_payload(const HipContext& ctx, const DeviceCache& cache,
+                                    const ExecutionPlan& plan, const HipBuffer& chunk_hidden,
+                                    const Offsets& o, std::size_t slot, std::size_t token_start,
+                                    std::size_t chunk_tokens) {
     std::size_t hidden_row = 0;
     std::size_t hidden_offset = 0;
     if (chunk_tokens == 0 || !mul(chunk_tokens - 1, layout_->hidden_size, hidden_row) ||
         !mul(hidden_row, sizeof(float), hidden_offset)) {
       return Status::invalid_argument("Qwen3.5 prefix last hidden offset overflow");
     }
-    Payload p = std::move(spare_);
-    spare_ = Payload{};
-    if (!p.storage.valid() || p.storage.byte_size() != o.total) {
-      auto b = ctx.make_buffer(o.total);
-      if (!b.is_ok()) {
-        return b.status();
-      }
-      p.storage = std::move(b.value());
+    if (!cache.storage.valid() && (o.r_bytes != 0 || o.s_bytes != 0 ||
+                                   layout_->full_attention_layers != 0)) {
+      return Status::invalid_argument(
+        "Qwen3.5 prefix cache needs a device cache from allocate_device_cache");
     }
-    // K and V rows: the K section is the payload's start and the V section
-    // follows it, so the same ranges shifted by o.value serve V.
-    auto kv = kv_regions(plan, o, token_start, true);
-    if (!kv.is_ok()) {
-      return kv.status();
+    std::vector<kraken_copy_region> regions;
+    const Status k = add_kv_regions(cache, plan, o, slot, token_start, true, regions);
+    if (!k.is_ok()) {
+      return k;
     }
-    std::vector<kraken_copy_region> v_regions = kv.value();
-    for (kraken_copy_region& g : v_regions) {
-      g.destination_offset += o.value;
-    }
-    Status s = copy_all(ctx, cache.key_cache, p.storage, kv.value());
+    const std::size_t base = slot * o.total;
+    add_region(regions, part_offset(cache, cache.recurrent_r_cache), base + o.r, o.r_bytes);
+    add_region(regions, part_offset(cache, cache.recurrent_s_cache), base + o.s, o.s_bytes);
+    HipBuffer& arena = arena_;
+    Status s = copy_all(ctx, cache.storage, arena, regions);
     if (s.is_ok()) {
-      s = copy_all(ctx, cache.value_cache, p.storage, v_regions);
+      s = copy_all(ctx, chunk_hidden, arena, {{hidden_offset, base + o.hidden, o.hidden_bytes}});
     }
-    if (s.is_ok() && o.r_bytes != 0) {
-      s = copy_all(ctx, cache.recurrent_r_cache, p.storage, {{0, o.r, o.r_bytes}});
-    }
-    if (s.is_ok() && o.s_bytes != 0) {
-      s = copy_all(ctx, cache.recurrent_s_cache, p.storage, {{0, o.s, o.s_bytes}});
-    }
-    if (s.is_ok()) {
-      s = copy_all(ctx, chunk_hidden, p.storage, {{hidden_offset, o.hidden, o.hidden_bytes}});
-    }
-    if (!s.is_ok()) {
-      return s;
-    }
-    p.last_hidden = HipBuffer::borrow(static_cast<unsigned char*>(p.storage.data()) + o.hidden,
-                                      o.hidden_bytes);
-    return p;
-  }
-
-  // qwen35_runtime.cpp:861-893
-  [[nodiscard]] Status restore_kv_block(const HipContext& ctx, DeviceCache& cache,
-                                        const ExecutionPlan& plan, const Payload& p,
-                                        std::size_t token_start) const {
-    auto off = offsets();
-    if (!off.is_ok()) {
-      return off.status();
-    }
-    const Offsets& o = off.value();
-    auto kv = kv_regions(plan, o, token_start, false);
-    if (!kv.is_ok()) {
-      return kv.status();
-    }
-    std::vector<kraken_copy_region> v_regions = kv.value();
-    for (kraken_copy_region& g : v_regions) {
-      g.source_offset += o.value;
-    }
-    const Status s = copy_all(ctx, p.storage, cache.key_cache, kv.value());
-    return s.is_ok() ? copy_all(ctx, p.storage, cache.value_cache, v_regions) : s;
-  }
-
-  // qwen35_runtime.cpp:895-921
-  [[nodiscard]] Status restore_recurrent(const HipContext& ctx, DeviceCache& cache,
-                                         const Payload& p) const {
-    auto off = offsets();
-    if (!off.is_ok()) {
-      return off.status();
-    }
-    const Offsets& o = off.value();
-    if (o.r_bytes != 0) {
-      const Status s = copy_all(ctx, p.storage, cache.recurrent_r_cache, {{o.r, 0, o.r_bytes}});
-      if (!s.is_ok()) {
-        return s;
-      }
-    }
-    if (o.s_bytes != 0) {
-      return copy_all(ctx, p.storage, cache.recurrent_s_cache, {{o.s, 0, o.s_bytes}});
-    }
-    return Status::ok();
+    return s;
   }
 };
 

@@ -261,9 +261,9 @@ int run_store() {
     std::printf("FAIL recurrent caches are not the last block's\n");
     ok = false;
   }
-  const HipBuffer* last = store.last_hidden(hit.block_hashes.back());
-  if (ok && (last == nullptr ||
-             !check(ctx.copy_from_buffer(*last, h.data(), h.size()), "last hidden") ||
+  const HipBuffer last = store.last_hidden(hit.block_hashes.back());
+  if (ok && (!last.valid() ||
+             !check(ctx.copy_from_buffer(last, h.data(), h.size()), "last hidden") ||
              std::memcmp(h.data(), hidden_bytes_b.data() + (kBlock - 1) * h.size(), h.size()) !=
                0)) {
     std::printf("FAIL last hidden row\n");
@@ -281,8 +281,9 @@ int run_store() {
   }
   const auto after = store.lookup(tokens);
   const Status missing = store.restore(ctx, dc, plan, {hit.block_hashes.front()});
-  std::printf("evict %d%d lookup %zu missing '%s'\n", c2.value().committed, c2.value().evicted,
-              after.hit_tokens, missing.message().c_str());
+  std::printf("evict %d%d lookup %zu missing '%s' evicted-hidden %d\n", c2.value().committed,
+              c2.value().evicted, after.hit_tokens, missing.message().c_str(),
+              store.last_hidden(hit.block_hashes.front()).valid() ? 1 : 0);
   auto st = store.stats();
   std::printf("stats %zu %zu %zu %zu %zu\n", st.stored_blocks, st.hit_tokens, st.miss_tokens,
               st.committed_tokens, st.evicted_blocks);

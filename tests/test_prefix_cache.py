@@ -172,7 +172,8 @@ def test_store_round_trip_on_device():
     assert lines["lookup"] == "8 2"
     # Block 2 evicts block 0 (least recently used), so the chain misses at once
     # and block 0's payload is gone.
-    assert lines["evict"] == "11 lookup 0 missing 'Qwen3.5 prefix cache payload is missing'"
+    assert lines["evict"] == ("11 lookup 0 missing 'Qwen3.5 prefix cache payload is missing' "
+                              "evicted-hidden 0")
     # stored, hit, miss, committed tokens, evicted: lookups of 12 tokens hit 8 then 0.
     assert lines["stats"] == "2 8 16 12 1"
     assert lines["same-config"] == "stored 2"
