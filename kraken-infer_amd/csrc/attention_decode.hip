@@ -34,48 +34,22 @@
 //    which needs no atomics or cross-workgroup fences.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
 
 #include "context_internal.hpp"
+#include "attention_decode_internal.hpp"
 #include "device_common.hpp"
 
 namespace kraken {
 namespace {
 
+using namespace decode;
+
 constexpr int kMaxSplits = 256;  // merge pass: 64 subsets x 4 loads per thread
-
-struct DecodeParams {
-  const float* query;
-  const void* key_cache;
-  const void* value_cache;
-  const float* gate;
-  float* output;
-  float* part_o;   // [tokens][kv_heads][splits][G][D]
-  float* part_ml;  // [tokens][kv_heads][splits][G][2]
-  uint32_t layer, start_position, tokens, capacity_tokens, heads, kv_heads;
-  uint32_t keys_per_split, splits;
-  float scale_log2;
-  // Ragged multi-sequence mode (see AttentionArgs): per-token K/V element
-  // offsets and positions, and the pools' element count.
-  const uint64_t* seq_kv_offsets;
-  const uint32_t* seq_positions;
-  uint64_t pool_elems;
-  // Ragged mode: dense work list, one item per workgroup (blockIdx.x):
-  // {token, kv_head << 16 | split}, token 0xffffffff past the last item.
-  const uint2* work_items;
-};
-
-// Keys of token t (positions table in ragged mode); at least 1 (a position of
-// 2^32 - 1 saturates instead of wrapping to 0).
-__device__ __forceinline__ uint32_t token_keys(const uint32_t* positions, uint32_t start,
-                                               uint32_t token) {
-  const uint64_t keys = positions != nullptr ? (uint64_t)positions[token] + 1u
-                                             : (uint64_t)start + token + 1u;
-  return (uint32_t)min(keys, (uint64_t)0xffffffffu);
-}
 
 template <typename KV>
 struct KvTraits;
@@ -101,8 +75,6 @@ struct KvTraits<float> {
     out[3] = __uint_as_float(raw.w);
   }
 };
-
-__device__ __forceinline__ float sigmoidf_acc(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // Lane geometry of a key row: a lane holds one 16-byte chunk of E elements
 // (EL = E), R = D/E lanes span a row, a wave takes KW = 64/R keys per round, a
@@ -166,25 +138,6 @@ __device__ __forceinline__ float slots_sum(float x) {
   }
   return x;
 }
-
-template <int D, int G>
-__device__ __forceinline__ void write_final(const DecodeParams& p, uint32_t token, uint32_t kvh,
-                                            int idx, float den, float acc) {
-  const int g = idx / D;
-  const int d = idx % D;
-  const size_t out_index = ((size_t)token * p.heads + kvh * G + g) * D + d;
-  float r = den == 0.0f ? 0.0f : acc / den;
-  if (p.gate != nullptr) {
-    r *= sigmoidf_acc(p.gate[out_index]);
-  }
-  p.output[out_index] = r;
-}
-
-// Lazy rescale slack (log2 domain): a wave exponentiates against a reference
-// max that moves only when a score exceeds it by more than this, so p <= 2^8
-// (far from f32 overflow) and most rounds skip the rescale of o and l.  The
-// result is exact either way: o and l always share the same reference.
-constexpr float kRescaleSlack = 8.0f;
 
 __device__ __forceinline__ float uniform_f(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, x)));
@@ -521,14 +474,9 @@ __global__ __launch_bounds__((64 * RowShape<D, KV>::W)) void attention_decode_ke
 // LDS rows are XOR-swizzled in 16-byte chunks (K: chunk ^ (row & 7); V: chunk ^
 // 2 (row & 3)) so that both fragment reads are free of bank conflicts.
 // ---------------------------------------------------------------------------
-constexpr int kMD = 256;
-constexpr int kMTile = 16;                        // keys per tile
 constexpr int kMWaves = 4;
 constexpr int kMStages = 2;                       // tiles in flight per wave
-constexpr int kMTileHalfs = kMTile * kMD;         // 8 KB per K or V tile
 constexpr int kMCopiesPerTile = kMTile;           // 1 KB copies per tile: 8 for K, 8 for V
-
-typedef float float4v_t __attribute__((ext_vector_type(4)));
 
 template <int G>
 __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(DecodeParams p) {
@@ -818,6 +766,27 @@ __device__ __forceinline__ float merge_lanes_sum(float x) {
   return xor32_sum(xor16_sum(x));
 }
 
+// Gate values of four output dims, loaded before the partials so that the
+// two loads overlap; (1, 1, 1, 1) when ungated or not needed.
+__device__ __forceinline__ float4 load_gate4(const float* gate, size_t out_index, bool needed) {
+  if (gate == nullptr || !needed) {
+    return make_float4(1.f, 1.f, 1.f, 1.f);
+  }
+  return *reinterpret_cast<const float4*>(gate + out_index);
+}
+
+__device__ __forceinline__ void store_gated4(const CombineArgs& p, size_t out_index, float4 r,
+                                             float inv, float4 gv) {
+  float out[4] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
+  if (p.gate != nullptr) {
+    out[0] *= sigmoidf_acc(gv.x);
+    out[1] *= sigmoidf_acc(gv.y);
+    out[2] *= sigmoidf_acc(gv.z);
+    out[3] *= sigmoidf_acc(gv.w);
+  }
+  *reinterpret_cast<float4*>(p.output + out_index) = make_float4(out[0], out[1], out[2], out[3]);
+}
+
 __global__ __launch_bounds__(256) void attention_merge(CombineArgs p) {
   __shared__ float s_mx[4];
   __shared__ float s_den[4][kMergeChunks];
@@ -835,6 +804,8 @@ __global__ __launch_bounds__(256) void attention_merge(CombineArgs p) {
   const int subset = tid / kMergeChunks;
   const size_t base = (size_t)token * p.kv_heads + kvh;
   const uint32_t nsp = token_splits(p, token);
+  const size_t out_index = ((size_t)token * p.heads + head) * p.head_dim + d0 + chunk * 4;
+  const float4 gv = load_gate4(p.gate, out_index, tid < kMergeChunks);
 
   float mv[kMergePerThread], lv[kMergePerThread];
   float4 ov[kMergePerThread];
@@ -898,15 +869,7 @@ __global__ __launch_bounds__(256) void attention_merge(CombineArgs p) {
   }
 
   const float inv = tden == 0.0f ? 0.0f : 1.0f / tden;
-  const size_t out_index = ((size_t)token * p.heads + head) * p.head_dim + d0 + chunk * 4;
-  float out[4] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
-  if (p.gate != nullptr) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      out[e] *= sigmoidf_acc(p.gate[out_index + e]);
-    }
-  }
-  *reinterpret_cast<float4*>(p.output + out_index) = make_float4(out[0], out[1], out[2], out[3]);
+  store_gated4(p, out_index, r, inv, gv);
 }
 
 // Ragged work list.  The dispatcher hands workgroup i to XCD i mod 8, so empty
@@ -1087,23 +1050,31 @@ size_t data_bytes(const AttentionArgs& a, const SplitPlan& plan) {
   return (partial_bytes(a, plan) + 255u) / 256u * 256u + work_item_count(a, plan) * 8u;
 }
 
-// The MFMA kernel serves head_dim 256 with an f16 cache and up to 4 query heads
-// per KV head, for splits of at least kMfmaMinKeys keys (8 tiles per wave).
-// On shorter splits (batch-1 decode, where a split is a few dozen keys) the
-// vector kernel's single 1024-thread pass is faster: the MFMA kernel's copy,
-// wait and merge chain is then its whole run time (measured: 11.0 vs 12.5 us
-// per C1 step at 4096 keys).  KRAKEN_DECODE_KERNEL=mfma or =vector forces one.
+// Kernel choice for head_dim 256 with an f16 cache and up to 4 query heads per
+// KV head.  Splits of at least kMfmaMinKeys keys (the ragged batched decode)
+// take the MFMA kernel with its direct-to-LDS copy pipeline; shorter splits of
+// one sequence (batch-1 decode) take the short-split MFMA kernel, whose loads
+// are all issued up front.  Other shapes take the vector kernel.
+// KRAKEN_DECODE_KERNEL=vector, =mfma or =short forces one.
 constexpr uint32_t kMfmaMinKeys = 512;
 
-bool mfma_decode_enabled(uint32_t keys_per_split) {
+enum class DecodeKernel { vector, mfma, short_split };
+
+DecodeKernel decode_kernel_choice(uint32_t keys_per_split, bool ragged) {
   const char* v = std::getenv("KRAKEN_DECODE_KERNEL");
   if (v != nullptr && std::strcmp(v, "vector") == 0) {
-    return false;
+    return DecodeKernel::vector;
   }
   if (v != nullptr && std::strcmp(v, "mfma") == 0) {
-    return true;
+    return DecodeKernel::mfma;
   }
-  return keys_per_split >= kMfmaMinKeys;
+  if (v != nullptr && std::strcmp(v, "short") == 0 && !ragged) {
+    return DecodeKernel::short_split;
+  }
+  if (keys_per_split >= kMfmaMinKeys) {
+    return DecodeKernel::mfma;
+  }
+  return ragged ? DecodeKernel::vector : DecodeKernel::short_split;
 }
 
 template <int D, int G, typename KV>
@@ -1111,14 +1082,19 @@ hipError_t launch_tuned(const DecodeParams& p, hipStream_t stream) {
   // Ragged: one workgroup per work-list entry (see ragged_plan_kernel).
   const dim3 grid = p.work_items != nullptr ? dim3(p.splits * p.kv_heads * p.tokens)
                                             : dim3(p.splits, p.kv_heads, p.tokens);
-  bool mfma = false;
+  DecodeKernel kind = DecodeKernel::vector;
   if constexpr (D == kMD && std::is_same_v<KV, half_t> && (G == 1 || G == 2 || G == 4)) {
-    mfma = mfma_decode_enabled(p.keys_per_split);
-    if (mfma) {
+    kind = decode_kernel_choice(p.keys_per_split, p.work_items != nullptr);
+    if (kind == DecodeKernel::mfma) {
       attention_decode_mfma_kernel<G><<<grid, 64 * kMWaves, 0, stream>>>(p);
+    } else if (kind == DecodeKernel::short_split) {
+      const hipError_t es = launch_decode_short(p, G, grid, stream);
+      if (es != hipSuccess) {
+        return es;
+      }
     }
   }
-  if (!mfma) {
+  if (kind == DecodeKernel::vector) {
     attention_decode_kernel<D, G, KV><<<grid, 64 * RowShape<D, KV>::W, 0, stream>>>(p);
   }
   hipError_t e = hipGetLastError();
@@ -1190,6 +1166,8 @@ __global__ __launch_bounds__(256) void attention_merge_narrow(CombineArgs p) {
   const uint32_t g = head % group;
   const size_t base = (size_t)token * p.kv_heads + kvh;
   const uint32_t nsp = token_splits(p, token);
+  const size_t out_index = th * p.head_dim + chunk * 4;
+  const float4 gv = load_gate4(p.gate, out_index, true);
   float mv[S], lv[S];
   float4 ov[S];
 #pragma unroll
@@ -1220,15 +1198,7 @@ __global__ __launch_bounds__(256) void attention_merge_narrow(CombineArgs p) {
     r.w = fmaf(w, ov[j].w, r.w);
   }
   const float inv = den == 0.0f ? 0.0f : 1.0f / den;
-  const size_t out_index = th * p.head_dim + chunk * 4;
-  float out[4] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
-  if (p.gate != nullptr) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      out[e] *= sigmoidf_acc(p.gate[out_index + e]);
-    }
-  }
-  *reinterpret_cast<float4*>(p.output + out_index) = make_float4(out[0], out[1], out[2], out[3]);
+  store_gated4(p, out_index, r, inv, gv);
 }
 
 // Many tokens with more than 16 splits (ragged batched decode): the same
@@ -1252,6 +1222,8 @@ __global__ __launch_bounds__(256) void attention_merge_tokens(CombineArgs p) {
   const uint32_t g = head % group;
   const size_t base = (size_t)token * p.kv_heads + kvh;
   const uint32_t nsp = token_splits(p, token);
+  const size_t out_index = th * p.head_dim + chunk * 4;
+  const float4 gv = load_gate4(p.gate, out_index, true);
   float mx = -INFINITY;
   float den = 0.0f;
   float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1292,15 +1264,7 @@ __global__ __launch_bounds__(256) void attention_merge_tokens(CombineArgs p) {
     }
   }
   const float inv = den == 0.0f ? 0.0f : 1.0f / den;
-  const size_t out_index = th * p.head_dim + chunk * 4;
-  float out[4] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
-  if (p.gate != nullptr) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      out[e] *= sigmoidf_acc(p.gate[out_index + e]);
-    }
-  }
-  *reinterpret_cast<float4*>(p.output + out_index) = make_float4(out[0], out[1], out[2], out[3]);
+  store_gated4(p, out_index, r, inv, gv);
 }
 
 hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream) {

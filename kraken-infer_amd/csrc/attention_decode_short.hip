@@ -1,0 +1,314 @@
+// Short-split MFMA decode kernel (head_dim 256, f16 cache), in its own
+// translation unit: it keeps its MFMA accumulators in architectural VGPRs
+// (built with -mllvm -amdgpu-mfma-vgpr-form), so the softmax rescale and the
+// epilogue read them without AGPR copies.
+//
+// Semantics: reference MSL attention_f32_batched_f16_kv (mps_backend.mm:
+// 2943-3008) with the output gate of qwen35_runtime.cpp:3347-3355, as in
+// attention_decode.hip, whose merge pass combines the split partials.
+#include <hip/hip_runtime.h>
+
+#include "attention_decode_internal.hpp"
+#include "device_common.hpp"
+
+namespace kraken {
+namespace decode {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Short-split MFMA kernel: head_dim 256, f16 cache, G <= 4, one sequence, for
+// splits of a few dozen keys (batch-1 decode, where a split is what one CU
+// reads).  There the step is bounded by latency, not by bandwidth, so every
+// load of the split is issued before anything else: a wave's K tile goes
+// straight into the MFMA A-fragment registers (lane (key r16, kq) loads dims
+// 32 s + 8 kq .. + 7 of step s) and its V tile into registers that are then
+// written to the wave's LDS region for the transposing V^T reads; the query
+// is loaded after them.  The math is the MFMA kernel's (hi + lo query and
+// probabilities, lazy rescale, same partial format); a wave with more than one
+// tile loads its next tile while it computes the current one.
+// ---------------------------------------------------------------------------
+constexpr int kSWaves = 4;
+
+template <int G>
+__global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(DecodeParams p) {
+  static_assert(G == 1 || G == 2 || G == 4, "query heads per KV head (rows 0..3 of a tile)");
+  __shared__ __attribute__((aligned(16))) half_t s_v[kSWaves][kMTileHalfs];
+  // Query fragments (hi, lo) per MFMA step, converted cooperatively.
+  __shared__ __attribute__((aligned(16))) half8_t s_q[8][2][64];
+  __shared__ float s_m[kSWaves][G];
+  __shared__ float s_l[kSWaves][G];
+  static_assert(sizeof(float) * kSWaves * G * kMD <= sizeof(s_v), "merge area");
+  float(*s_o)[G * kMD] = reinterpret_cast<float(*)[G * kMD]>(&s_v[0][0]);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const uint32_t split = blockIdx.x;
+  const uint32_t kvh = blockIdx.y;
+  const uint32_t token = blockIdx.z;
+  const uint32_t n_keys = token_keys(nullptr, p.start_position, token);
+  const uint32_t key_begin = split * p.keys_per_split;
+  if (key_begin >= n_keys) {
+    return;  // empty split (whole workgroup)
+  }
+  const uint32_t count = min(n_keys, key_begin + p.keys_per_split) - key_begin;
+  const size_t row_stride = (size_t)p.kv_heads * kMD;
+  const uint32_t row_bytes = (uint32_t)(row_stride * sizeof(half_t));
+  const size_t first = ((size_t)p.layer * p.capacity_tokens + key_begin) * row_stride +
+                       (size_t)kvh * kMD;
+  // Rows at or past the split's end read as zeros (resource range check).
+  const __amdgpu_buffer_rsrc_t krs =
+    make_buffer_rsrc(static_cast<const half_t*>(p.key_cache) + first, count * row_bytes);
+  const __amdgpu_buffer_rsrc_t vrs =
+    make_buffer_rsrc(static_cast<const half_t*>(p.value_cache) + first, count * row_bytes);
+  const uint32_t ntiles = (count + kMTile - 1) / kMTile;
+
+  // The query first: loads retire in issue order, so its conversion below
+  // waits only for the query while the K/V tile is still in flight.  Wave w
+  // converts steps 2 w and 2 w + 1: lane (head r16, kq) holds dims
+  // 32 s + 8 kq .. + 7 of step s, scaled into the log2 domain.
+  float4 qraw[2][2];
+  const int qg = r16 < G ? r16 : 0;
+  const float qscale = r16 < G ? p.scale_log2 : 0.0f;
+  {
+    const float* qh = p.query + ((size_t)token * p.heads + kvh * G + qg) * kMD + 8 * kq;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int s = 2 * wave + i;
+      qraw[i][0] = *reinterpret_cast<const float4*>(qh + 32 * s);
+      qraw[i][1] = *reinterpret_cast<const float4*>(qh + 32 * s + 4);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  half8_t kf[8];
+  u32x4_t vr[8];
+  const uint32_t k_off = (uint32_t)r16 * row_bytes + 16u * (uint32_t)kq;
+  const uint32_t v_off = (uint32_t)(lane >> 5) * row_bytes + 16u * (uint32_t)(lane & 31);
+  auto load_k = [&](uint32_t t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      kf[s] = __builtin_bit_cast(half8_t,
+                                 buffer_load_nt_b128(krs, t * kMTile * row_bytes + k_off + 64u * s));
+    }
+  };
+  auto load_v = [&](uint32_t t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      vr[c] = buffer_load_nt_b128(vrs, (t * kMTile + 2u * c) * row_bytes + v_off);
+    }
+  };
+  uint32_t t = (uint32_t)wave;
+  if (t < ntiles) {
+    load_k(t);
+    load_v(t);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Query fragments (B operand of S^T) as f16 hi + lo (lo = x - hi, rounded
+  // again), so that K (exact in f16) times hi + lo reproduces the f32 product.
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float v[8] = {qraw[i][0].x, qraw[i][0].y, qraw[i][0].z, qraw[i][0].w,
+                        qraw[i][1].x, qraw[i][1].y, qraw[i][1].z, qraw[i][1].w};
+    half8_t hi8, lo8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = v[j] * qscale;
+      const half_t hi = static_cast<half_t>(x);
+      hi8[j] = hi;
+      lo8[j] = static_cast<half_t>(x - static_cast<float>(hi));
+    }
+    s_q[2 * wave + i][0][lane] = hi8;
+    s_q[2 * wave + i][1][lane] = lo8;
+  }
+  __syncthreads();
+  half8_t qhi[8], qlo[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    qhi[s] = s_q[s][0][lane];
+    qlo[s] = s_q[s][1][lane];
+  }
+
+  float m[G];  // wave-uniform reference max per head (log2 domain)
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+  }
+  float lpart = 0.0f;  // this lane's share of head r16's denominator
+  float4v_t o[16];     // O tile n: lane l holds dim 16 n + l % 16 of heads 4 (l / 16) + r
+#pragma unroll
+  for (int n = 0; n < 16; ++n) {
+    o[n] = float4v_t{0.f, 0.f, 0.f, 0.f};
+  }
+  half_t* vs = &s_v[wave][0];
+  for (; t < ntiles; t += kSWaves) {
+    // V rows of tile t into the wave's LDS region, 16-byte chunks XOR-swizzled
+    // by 2 (row & 3) so that the transposing reads are free of bank conflicts.
+    // The region's previous reads were consumed by last tile's MFMAs.
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t row = 2u * c + (uint32_t)(lane >> 5);
+      const uint32_t chunk = (uint32_t)(lane & 31);
+      *reinterpret_cast<u32x4_t*>(vs + row * kMD + 8 * (chunk ^ (2u * (row & 3u)))) = vr[c];
+    }
+    asm volatile("" ::: "memory");
+    const bool more = t + kSWaves < ntiles;
+    if (more) {
+      load_v(t + kSWaves);
+    }
+
+    // S^T = K Q^T (keys x heads).
+    float4v_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[s], qhi[s], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[s], qlo[s], sacc, 0, 0, 0);
+    }
+    if (more) {
+      load_k(t + kSWaves);
+    }
+
+    // Softmax: lane holds keys 16 t + 4 kq + r of head r16.
+    float sc[4];
+    bool valid[4];
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      valid[r] = r16 < G && kMTile * t + 4u * kq + r < count;
+      sc[r] = valid[r] ? sacc[r] : -INFINITY;
+      cmax = fmaxf(cmax, sc[r]);
+    }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+    float corr_lane = 1.0f;
+    float m_lane = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float bm = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                   __builtin_bit_cast(int, cmax), g));
+      if (bm > m[g] + kRescaleSlack) {  // wave-uniform
+        // Before the head's first valid tile o and l are zero: no rescale.
+        if (m[g] != -INFINITY) {
+          const float corr = fast_exp2(m[g] - bm);
+#pragma unroll
+          for (int n = 0; n < 16; ++n) {
+            o[n][g] *= corr;  // head g is row g: register g of lanes 0..15
+          }
+          corr_lane = r16 == g ? corr : corr_lane;
+        }
+        m[g] = bm;
+      }
+      m_lane = r16 == g ? m[g] : m_lane;
+    }
+    lpart *= corr_lane;
+    half4_t phi, plo;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pr = valid[r] ? fast_exp2(sc[r] - m_lane) : 0.0f;
+      lpart += pr;
+      const half_t h = static_cast<half_t>(pr);
+      phi[r] = h;
+      plo[r] = static_cast<half_t>(pr - static_cast<float>(h));
+    }
+
+    // O += P V: lane 4 e + q of group kq points at row 4 kq + e, columns
+    // 16 n + 4 q .. + 3; the transposing read returns column 16 n + l % 16
+    // of rows 4 kq .. 4 kq + 3.
+    const int vrow = 4 * kq + (r16 >> 2);
+    const int q = r16 & 3;
+    const half_t* vrow_p = vs + vrow * kMD + 4 * (q & 1);
+    const int vswz = 2 * (vrow & 3);
+#pragma unroll
+    for (int n = 0; n < 16; ++n) {
+      const half4_t vf = read_tr16(vrow_p + 8 * ((2 * n + (q >> 1)) ^ vswz));
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, vf, o[n], 0, 0, 0);
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, vf, o[n], 0, 0, 0);
+    }
+  }
+
+  // Wave partial: head r16's denominator over the four lane groups.
+  float lw = lpart;
+  lw += __shfl_xor(lw, 16, 64);
+  lw += __shfl_xor(lw, 32, 64);
+  __syncthreads();  // every wave is done with its V region
+  if (lane < G) {
+    s_l[wave][lane] = lw;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      s_m[wave][g] = m[g];
+    }
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int n = 0; n < 16; ++n) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        s_o[wave][g * kMD + 16 * n + lane] = o[n][g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Workgroup merge of the wave partials (waves without a tile hold m = -inf).
+  constexpr int kThreads = 64 * kSWaves;
+  constexpr int kOutPerThread = G * kMD / kThreads;
+  const size_t tk = (size_t)token * p.kv_heads + kvh;
+  float* po = p.part_o + (tk * p.splits + split) * (size_t)(G * kMD);
+  float* pml = p.part_ml + (tk * p.splits + split) * (size_t)(G * 2);
+#pragma unroll
+  for (int k = 0; k < kOutPerThread; ++k) {
+    const int idx = tid + k * kThreads;
+    const int g = idx / kMD;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kSWaves; ++w) {
+      mx = fmaxf(mx, s_m[w][g]);
+    }
+    float acc = 0.0f;
+    float den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kSWaves; ++w) {
+      const float wt = s_m[w][g] == -INFINITY ? 0.0f : fast_exp2(s_m[w][g] - mx);
+      acc = fmaf(wt, s_o[w][idx], acc);
+      den = fmaf(wt, s_l[w][g], den);
+    }
+    if (p.splits == 1) {
+      write_final<kMD, G>(p, token, kvh, idx, den, acc);
+    } else {
+      po[idx] = acc;
+      if (idx % kMD == 0) {
+        pml[g * 2 + 0] = mx;
+        pml[g * 2 + 1] = den;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_decode_short(const DecodeParams& p, uint32_t group, dim3 grid,
+                               hipStream_t stream) {
+  switch (group) {
+    case 1:
+      attention_decode_short_kernel<1><<<grid, 64 * kSWaves, 0, stream>>>(p);
+      break;
+    case 2:
+      attention_decode_short_kernel<2><<<grid, 64 * kSWaves, 0, stream>>>(p);
+      break;
+    case 4:
+      attention_decode_short_kernel<4><<<grid, 64 * kSWaves, 0, stream>>>(p);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace decode
+}  // namespace kraken

@@ -112,6 +112,32 @@ def test_decode_mfma_matches_vector_kernel_and_oracle(hip_ctx, monkeypatch, shap
     vec = run_hip(hip_ctx, q, kc, vc, 1, start, tokens, cap, heads, kv_heads, d)
     close(vec, ref, msg=f"vector {shape}")
     close(got, vec, rtol=1e-3, atol=5e-4, msg=f"mfma vs vector {shape}")
+    monkeypatch.setenv("KRAKEN_DECODE_KERNEL", "short")
+    short = run_hip(hip_ctx, q, kc, vc, 1, start, tokens, cap, heads, kv_heads, d)
+    close(short, ref, msg=f"short {shape}")
+    close(short, vec, rtol=1e-3, atol=5e-4, msg=f"short vs vector {shape}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("keys_per_split", ["16", "33", "100", "300"])
+@pytest.mark.parametrize("shape", [(1, 4096, 8, 2), (1, 30000, 8, 2), (7, 100, 8, 2),
+                                   (3, 2000, 2, 1), (1, 5000, 4, 2)])
+def test_decode_short_kernel_split_sizes(hip_ctx, monkeypatch, keys_per_split, shape):
+    """The short-split decode kernel (the batch-1 default) with splits of one
+    tile, of several tiles per wave (its next-tile loads overlap the current
+    tile's math) and with a partial last tile, GQA groups 1/2/4, sharp softmax
+    (q scaled by 8), against the oracle."""
+    tokens, start, heads, kv_heads = shape
+    d = 256
+    cap = start + tokens + 1
+    print(f"decode short {shape} kps={keys_per_split}", flush=True)
+    q, kc, vc = make_case(13, tokens, start, cap, heads, kv_heads, d)
+    q = (q * 8.0).astype(np.float32)
+    ref = oracle.attention_batched(q, kc, vc, 0, start, tokens, cap, heads, kv_heads, d)
+    monkeypatch.setenv("KRAKEN_DECODE_KERNEL", "short")
+    monkeypatch.setenv("KRAKEN_DECODE_KEYS_PER_SPLIT", keys_per_split)
+    got = run_hip(hip_ctx, q, kc, vc, 0, start, tokens, cap, heads, kv_heads, d)
+    close(got, ref, msg=f"short {shape} kps={keys_per_split}")
 
 
 @pytest.mark.gpu
