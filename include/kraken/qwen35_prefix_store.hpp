@@ -136,7 +136,7 @@ class PrefixCacheStore {
     if (!off.is_ok()) {
       return off.status();
     }
-    const Status ready = ensure_arena(ctx, off.value());
+    const Status ready = ensure_arena(off.value());
     if (!ready.is_ok()) {
       return ready;
     }
@@ -228,6 +228,12 @@ class PrefixCacheStore {
 
   PrefixCacheIndex index_{PrefixCacheConfig{}};
   std::optional<PrefixCacheLayout> layout_;
+  // The arena belongs to the store, not to the request context that first
+  // commits: requests create and destroy their contexts (qwen35_runtime.cpp:
+  // 5583-5589) while the store lives on, so the arena is allocated through a
+  // context of the store's own, created at the first commit on the device that
+  // is current then.  Declared before arena_, so it outlives the allocation.
+  std::optional<HipContext> own_context_;
   HipBuffer arena_;                                      // (capacity + 1) payload slots
   std::unordered_map<std::uint64_t, std::size_t> slot_of_;  // stored block -> arena slot
   std::vector<std::size_t> free_slots_;
@@ -294,7 +300,7 @@ class PrefixCacheStore {
   }
 
   // Allocates the arena at the first commit: capacity + 1 slots, all free.
-  [[nodiscard]] Status ensure_arena(const HipContext& ctx, const Offsets& o) {
+  [[nodiscard]] Status ensure_arena(const Offsets& o) {
     if (arena_.valid()) {
       return Status::ok();
     }
@@ -303,7 +309,14 @@ class PrefixCacheStore {
     if (slots == 0 || !mul(slots, o.total, bytes)) {
       return Status::invalid_argument("Qwen3.5 prefix cache arena size overflow");
     }
-    auto b = ctx.make_buffer(bytes);
+    if (!own_context_.has_value()) {
+      auto c = HipContext::create();
+      if (!c.is_ok()) {
+        return c.status();
+      }
+      own_context_.emplace(std::move(c.value()));
+    }
+    auto b = own_context_->make_buffer(bytes);
     if (!b.is_ok()) {
       return b.status();
     }
@@ -392,10 +405,20 @@ class PrefixCacheStore {
     const std::size_t base = slot * o.total;
     const std::size_t k_part = part_offset(cache, cache.key_cache);
     const std::size_t v_part = part_offset(cache, cache.value_cache);
+    // Each layer's rows must lie inside the K and V caches themselves, as the
+    // reference's per-buffer copies check (mps_backend.mm:5768-5830): a block
+    // past the capacity would otherwise run into the next part of the one
+    // allocation.
+    const std::size_t part_bytes =
+      std::min(cache.key_cache.byte_size(), cache.value_cache.byte_size());
     for (std::size_t layer = 0; layer < layout_->full_attention_layers; ++layer) {
       auto row = cache_row_offset(plan, layer, token_start);
       if (!row.is_ok()) {
         return row.status();
+      }
+      if (row.value() > part_bytes || o.kv_block_layer > part_bytes - row.value()) {
+        return Status::invalid_argument(to_arena ? "HIP copy size exceeds source buffer size"
+                                                 : "HIP copy size exceeds destination buffer size");
       }
       const std::size_t at = layer * o.kv_block_layer;
       const std::size_t pk = base + o.key + at, ck = k_part + row.value();

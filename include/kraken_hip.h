@@ -103,7 +103,10 @@ KRAKEN_API int kraken_hip_free_buffer(kraken_hip_context* context, kraken_buffer
 
 /* MpsContext::copy_to_buffer[_at] / copy_from_buffer[_at] / copy_buffer_region /
  * zero_buffer (mps_backend.hpp:97-114; mps_backend.mm:5763-5874).  Host copies
- * first finish pending work, as the reference commits the open graph. */
+ * first finish pending work, as the reference commits the open graph.
+ * copy_buffer_region also commits first, then enqueues the device copy on the
+ * context's stream and waits for it; overlapping ranges copy as memmove, staged
+ * through the context's workspace (which grows once, then is reused). */
 KRAKEN_API int kraken_hip_copy_to_buffer(kraken_hip_context* context, kraken_buffer buffer,
                                          const void* data, size_t byte_size);
 KRAKEN_API int kraken_hip_copy_to_buffer_at(kraken_hip_context* context, kraken_buffer buffer,
@@ -126,7 +129,8 @@ KRAKEN_API int kraken_hip_zero_buffer(kraken_hip_context* context, kraken_buffer
  * `count` triples {source_offset, destination_offset, byte_size}; count is at
  * most KRAKEN_COPY_REGIONS_MAX and every range must lie inside its buffer.
  * Ranges must not overlap each other's destinations or a source they read.
- * Stream-ordered: no host wait, no allocation. */
+ * Enqueued on the context's stream with no allocation; like the other ops it
+ * waits for completion unless a begin_graph / commit_graph batch is open. */
 #define KRAKEN_COPY_REGIONS_MAX 64
 typedef struct kraken_copy_region {
   size_t source_offset;

@@ -1313,7 +1313,7 @@ size_t attention_decode_workspace_bytes(const AttentionArgs& a, int cu_count) {
   if (!use_tuned(a, plan)) {
     return 0;
   }
-  return kCounterRegionBytes + data_bytes(a, plan);
+  return data_bytes(a, plan);
 }
 
 hipError_t launch_attention_decode(const AttentionArgs& a, int cu_count, void* workspace,
@@ -1345,20 +1345,18 @@ hipError_t launch_attention_decode(const AttentionArgs& a, int cu_count, void* w
     p.keys_per_split = plan.keys_per_split;
     p.splits = plan.splits;
     if (plan.splits > 1) {
-      if (workspace == nullptr || workspace_bytes < kCounterRegionBytes + data_bytes(a, plan)) {
+      if (workspace == nullptr || workspace_bytes < data_bytes(a, plan)) {
         return hipErrorInvalidValue;
       }
       const size_t units = (size_t)a.tokens * a.kv_heads;
-      // Partials follow the counter region, which they must never overlap.
-      p.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterRegionBytes);
+      p.part_o = static_cast<float*>(workspace);
       p.part_ml = p.part_o + units * plan.splits * g * a.head_dim;
     }
     if (a.seq_positions != nullptr) {
-      if (workspace == nullptr || workspace_bytes < kCounterRegionBytes + data_bytes(a, plan)) {
+      if (workspace == nullptr || workspace_bytes < data_bytes(a, plan)) {
         return hipErrorInvalidValue;
       }
       uint2* items = reinterpret_cast<uint2*>(static_cast<char*>(workspace) +
-                                              kCounterRegionBytes +
                                               (partial_bytes(a, plan) + 255u) / 256u * 256u);
       p.work_items = items;
       ragged_plan_kernel<<<1, 256, 0, stream>>>(a.seq_positions, a.tokens, a.kv_heads,

@@ -518,7 +518,7 @@ size_t attention_flash_workspace_bytes(const AttentionArgs& a, int cu_count) {
     return 0;
   }
   const size_t units = (size_t)a.tokens * a.heads * plan.splits;
-  return kCounterRegionBytes + units * (kD + 2) * sizeof(float);
+  return units * (kD + 2) * sizeof(float);
 }
 
 hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* workspace,
@@ -545,11 +545,11 @@ hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* wo
   if (plan.splits > 1) {
     const size_t units = (size_t)a.tokens * a.heads * plan.splits;
     if (workspace == nullptr ||
-        workspace_bytes < kCounterRegionBytes + units * (kD + 2) * sizeof(float)) {
+        workspace_bytes < units * (kD + 2) * sizeof(float)) {
       return hipErrorInvalidValue;
     }
     // Partials follow the counter region, which they must never overlap.
-    p.partial_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterRegionBytes);
+    p.partial_o = static_cast<float*>(workspace);
     p.partial_ml = p.partial_o + units * kD;
   }
   const uint32_t g = a.heads / a.kv_heads;

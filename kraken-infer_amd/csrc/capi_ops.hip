@@ -1256,15 +1256,14 @@ KRAKEN_API int kraken_hip_qwen35_gdn_layer_ragged_decode_f32(
     return finish_launch(ctx, (w + " command failed: ").c_str());
   }
 
-  // Three-kernel chain: q/k/v in the context workspace, after its counter region.
+  // Three-kernel chain: q/k/v in the context workspace.
   size_t tmp_bytes = 0;
-  if (!checked_mul(2u * key_values + value_values, sizeof(float), tmp_bytes) ||
-      !checked_add(tmp_bytes, kCounterRegionBytes, tmp_bytes)) {
+  if (!checked_mul(2u * key_values + value_values, sizeof(float), tmp_bytes)) {
     return invalid(w + " value count overflow");
   }
   KRAKEN_TRY(ensure_workspace(ctx, tmp_bytes));
   KRAKEN_TRY(begin_launch(ctx));
-  float* qb = reinterpret_cast<float*>(static_cast<char*>(ctx->workspace) + kCounterRegionBytes);
+  float* qb = static_cast<float*>(ctx->workspace);
   float* kb = qb + key_values;
   float* vb = kb + key_values;
   hipError_t e = launch_conv_split_l2_ragged(

@@ -103,11 +103,6 @@ int ensure_workspace(kraken_hip_context* ctx, size_t bytes) {
     ctx->workspace = nullptr;
     return internal("HIP workspace allocation failed: " + hip_message(e));
   }
-  // Counters in the workspace must start at zero; kernels leave them at zero.
-  e = hipMemset(ctx->workspace, 0, rounded);
-  if (e != hipSuccess) {
-    return internal("HIP workspace clear failed: " + hip_message(e));
-  }
   ctx->workspace_bytes = rounded;
   return KRAKEN_OK;
 }
@@ -471,26 +466,25 @@ KRAKEN_API int kraken_hip_copy_buffer_region(kraken_hip_context* ctx, kraken_buf
   }
   const uint8_t* src = static_cast<const uint8_t*>(source.data) + source_offset;
   uint8_t* dst = static_cast<uint8_t*>(destination.data) + destination_offset;
-  hipError_t e;
+  // Enqueued on the context's stream.  Overlapping ranges get memmove
+  // semantics (mps_backend.mm:5855-5856) through the context workspace.
   const bool overlap = src < dst + byte_size && dst < src + byte_size;
+  hipError_t e;
   if (overlap) {
-    // memmove semantics (mps_backend.mm:5855-5856) through a staging allocation.
-    void* staging = nullptr;
-    e = hipMalloc(&staging, byte_size);
+    if ((s = ensure_workspace(ctx, byte_size)) != KRAKEN_OK) {
+      return s;
+    }
+    e = hipMemcpyAsync(ctx->workspace, src, byte_size, hipMemcpyDeviceToDevice, ctx->stream);
     if (e == hipSuccess) {
-      e = hipMemcpy(staging, src, byte_size, hipMemcpyDeviceToDevice);
-      if (e == hipSuccess) {
-        e = hipMemcpy(dst, staging, byte_size, hipMemcpyDeviceToDevice);
-      }
-      (void)hipFree(staging);
+      e = hipMemcpyAsync(dst, ctx->workspace, byte_size, hipMemcpyDeviceToDevice, ctx->stream);
     }
   } else {
-    e = hipMemcpy(dst, src, byte_size, hipMemcpyDeviceToDevice);
+    e = hipMemcpyAsync(dst, src, byte_size, hipMemcpyDeviceToDevice, ctx->stream);
   }
   if (e != hipSuccess) {
     return internal("HIP buffer region copy failed: " + hip_message(e));
   }
-  return KRAKEN_OK;
+  return finish_launch(ctx, "HIP buffer region copy failed: ");
 }
 
 KRAKEN_API int kraken_hip_zero_buffer(kraken_hip_context* ctx, kraken_buffer buffer,

@@ -19,8 +19,8 @@ struct kraken_hip_context {
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;  // where work is enqueued (own or caller's)
   bool graph_active = false;
-  // Device workspace owned by the context (split-K partials, counters).  Grown on
-  // demand outside of any kernel; the reference likewise owns only its flash-tail
+  // Device workspace owned by the context (split-K partials, chunk operands,
+  // staging).  Grown on demand outside of any kernel; the reference likewise owns only its flash-tail
   // scratch (mps_backend.mm:4402-4407).
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
@@ -107,12 +107,6 @@ int strided_region_end(size_t offset, size_t rows, size_t stride, size_t row_siz
 // -------------------------------------------------------------- launches ----
 // Implemented by the kernel translation units; all enqueue on `stream` and
 // return hipSuccess or the launch error.
-
-// The context workspace starts with a fixed region of uint32 counters used by
-// in-kernel last-arriver reductions.  Counters start at zero and every kernel
-// that uses one returns it to zero, so the region is never cleared per call and
-// no partial-result buffer may overlap it.
-constexpr size_t kCounterRegionBytes = size_t(1) << 20;
 
 struct AttentionArgs {
   const float* query;

@@ -662,7 +662,7 @@ bool gdn_chunked_supported(const GdnArgs& a) {
 size_t gdn_chunked_workspace_bytes(const GdnArgs& a) {
   const uint32_t chunks = (a.tokens + kC - 1) / kC;
   const uint32_t slab = chunks < kSlabChunks ? chunks : kSlabChunks;
-  return kCounterRegionBytes + (size_t)slab * a.value_heads * kBlockFloats * sizeof(float);
+  return (size_t)slab * a.value_heads * kBlockFloats * sizeof(float);
 }
 
 hipError_t launch_gdn_chunked(const GdnArgs& a, void* workspace, size_t workspace_bytes,
@@ -681,7 +681,7 @@ hipError_t launch_gdn_chunked(const GdnArgs& a, void* workspace, size_t workspac
   p.state = a.state;
   p.output = a.output;
   // Blocks follow the counter region, which they must never overlap.
-  p.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterRegionBytes);
+  p.ws = static_cast<float*>(workspace);
   p.tokens = a.tokens;
   p.key_heads = a.key_heads;
   p.value_heads = a.value_heads;

@@ -370,6 +370,120 @@ int run_store_bench() {
   return 0;
 }
 
+// The store outlives the request contexts that use it: a block committed
+// through one context, which is then destroyed with its cache, is restored
+// through a second context; reconfiguring then frees the arena (through the
+// store's own context) and a commit allocates it again.  A block whose rows
+// would run past the attention capacity is rejected, not copied.
+int run_lifetime() {
+  constexpr std::size_t kBlock = 4;
+  q35::RuntimeOptions options;
+  options.context_tokens = 32;
+  auto plan_r = q35::build_execution_plan(q35::qwen35_0_8b_shape(), 12, options);
+  if (!check(plan_r.status(), "plan")) {
+    return 1;
+  }
+  const q35::ExecutionPlan& plan = plan_r.value();
+  const std::size_t layers = plan.cache.full_attention_layers;
+  const std::size_t cap = plan.cache.attention_capacity_tokens;
+  const std::size_t row = plan.cache.kv_dim * plan.cache.kv_cache_element_bytes;
+  const std::size_t hidden = plan.hidden_size;
+  std::vector<std::int64_t> tokens(cap + 2 * kBlock);
+  for (std::size_t i = 0; i < tokens.size(); ++i) {
+    tokens[i] = 500 + static_cast<std::int64_t>(i * 13 % 17);
+  }
+  q35::PrefixCacheStore store;
+  const q35::PrefixCacheConfig config{true, kBlock, 4, 0};
+  store.configure(q35::prefix_layout_from_plan(plan, kBlock), config);
+  HostCache a;
+  const std::vector<std::uint8_t> hidden_a = pattern(kBlock * hidden * sizeof(float), 70);
+  {
+    auto first_r = HipContext::create();
+    if (!check(first_r.status(), "create first")) {
+      return 1;
+    }
+    const HipContext& first = first_r.value();
+    auto cache_r = q35::allocate_device_cache(first, plan);
+    auto hidden_r = first.make_buffer(kBlock * hidden * sizeof(float));
+    if (!check(cache_r.status(), "cache first") || !check(hidden_r.status(), "hidden first") ||
+        !fill(first, cache_r.value(), 21, a) ||
+        !check(first.copy_to_buffer(hidden_r.value(), hidden_a.data(), hidden_a.size()), "h")) {
+      return 1;
+    }
+    auto c0 = store.commit_block(first, cache_r.value(), plan, hidden_r.value(), tokens, 0,
+                                 kBlock);
+    if (!check(c0.status(), "commit first") || !c0.value().committed) {
+      std::printf("FAIL first commit not stored\n");
+      return 1;
+    }
+  }  // the first context, its cache and its hidden buffer are gone
+  auto second_r = HipContext::create();
+  if (!check(second_r.status(), "create second")) {
+    return 1;
+  }
+  const HipContext& second = second_r.value();
+  auto cache_r = q35::allocate_device_cache(second, plan);
+  if (!check(cache_r.status(), "cache second")) {
+    return 1;
+  }
+  q35::DeviceCache& dc = cache_r.value();
+  for (HipBuffer* buf : {&dc.key_cache, &dc.value_cache, &dc.recurrent_r_cache,
+                         &dc.recurrent_s_cache}) {
+    if (!check(second.zero_buffer(*buf, buf->byte_size()), "zero")) {
+      return 1;
+    }
+  }
+  const auto hit = store.lookup(tokens);
+  if (hit.block_hashes.size() != 1 ||
+      !check(store.restore(second, dc, plan, hit.block_hashes), "restore second")) {
+    std::printf("FAIL lookup after the first context: %zu blocks\n", hit.block_hashes.size());
+    return 1;
+  }
+  std::vector<std::uint8_t> k, v, r, st, h(hidden * sizeof(float));
+  if (!read(second, dc.key_cache, k) || !read(second, dc.value_cache, v) ||
+      !read(second, dc.recurrent_r_cache, r) || !read(second, dc.recurrent_s_cache, st)) {
+    return 1;
+  }
+  if (!rows_equal(k, a.k, layers, cap, row, 0, kBlock, "K") ||
+      !rows_equal(v, a.v, layers, cap, row, 0, kBlock, "V") || r != a.r || st != a.s) {
+    return 1;
+  }
+  const HipBuffer last = store.last_hidden(hit.block_hashes.back());
+  if (!last.valid() || !check(second.copy_from_buffer(last, h.data(), h.size()), "hidden") ||
+      std::memcmp(h.data(), hidden_a.data() + (kBlock - 1) * h.size(), h.size()) != 0) {
+    std::printf("FAIL last hidden row after the first context\n");
+    return 1;
+  }
+  std::printf("restored-after-destroy ok\n");
+
+  // A new layout drops the arena; a commit through the second context
+  // allocates a new one.
+  auto other = q35::prefix_layout_from_plan(plan, kBlock);
+  other.tokenizer_fingerprint = 3;
+  store.configure(other, config);
+  auto hidden_r = second.make_buffer(kBlock * hidden * sizeof(float));
+  if (!check(hidden_r.status(), "hidden second")) {
+    return 1;
+  }
+  auto c1 = store.commit_block(second, dc, plan, hidden_r.value(), tokens, 0, kBlock);
+  if (!check(c1.status(), "commit after reconfigure") || !c1.value().committed) {
+    return 1;
+  }
+  std::printf("reconfigured stored %zu\n", store.stats().stored_blocks);
+
+  // The block at rows [cap, cap + kBlock) is past the K/V caches' capacity.
+  if (cap % kBlock != 0) {
+    std::printf("FAIL capacity %zu is not whole blocks\n", cap);
+    return 1;
+  }
+  auto past = store.commit_block(second, dc, plan, hidden_r.value(), tokens, cap, kBlock);
+  std::printf("past-capacity '%s' stored %zu\n",
+              past.is_ok() ? "accepted" : past.status().message().c_str(),
+              store.stats().stored_blocks);
+  std::printf("ok\n");
+  return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -383,6 +497,9 @@ int main(int argc, char** argv) {
   if (mode == "store-bench") {
     return run_store_bench();
   }
-  std::printf("usage: prefix_cache_check index | store | store-bench\n");
+  if (mode == "lifetime") {
+    return run_lifetime();
+  }
+  std::printf("usage: prefix_cache_check index | store | store-bench | lifetime\n");
   return 2;
 }

@@ -182,6 +182,23 @@ def test_store_round_trip_on_device():
 
 
 @pytest.mark.gpu
+def test_store_outlives_request_contexts():
+    """The store keeps its payload arena through its own context: a block
+    committed through a context that is then destroyed restores through a
+    second context byte for byte; reconfiguring frees and a commit reallocates
+    the arena; a block running past the attention capacity is rejected with the
+    reference's region error (mps_backend.mm:5768-5830)."""
+    print("prefix store lifetime", flush=True)
+    code, out = _run("lifetime")
+    assert code == 0, out
+    lines = dict(line.split(" ", 1) for line in out.splitlines() if " " in line)
+    assert lines["restored-after-destroy"] == "ok"
+    assert lines["reconfigured"] == "stored 1"
+    assert lines["past-capacity"] == "'HIP copy size exceeds source buffer size' stored 1"
+    assert out.strip().endswith("ok")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_copy_regions_matches_numpy(hip_ctx, seed):
     """kraken_hip_copy_regions: aligned tiles, partial tiles, unaligned starts and byte
