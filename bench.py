@@ -4,8 +4,9 @@ Headline (`value`): C1 decode attention -- one query token, 8 Q / 2 KV heads,
 head_dim 256, F16 KV cache holding 4096 prior tokens plus the new one, output
 gated by sigmoid(G) -- as algorithmic HBM GB/s:
     bytes/step = 2048 * (L + 1)  (K and V rows)  +  24 KiB (q, G, out) + 1 KiB
-with the KV sets rotating over > 512 MB so every step reads from HBM, not the
-256 MB Infinity Cache ("cold").  A step is one call of
+with the KV sets rotating over > 512 MB and 1 GiB of other data read between the
+untimed and the timed replay, so every step reads from HBM, not the 256 MB
+Infinity Cache ("cold"), whatever --steps is.  A step is one call of
 kraken_hip_attention_f32_batched_f16_kv_gated.  The timed steps are captured in
 one HIP graph on torch's stream and replayed between HIP events; inputs are
 resident in HBM before the timed region starts.
@@ -61,13 +62,18 @@ class Runner:
     def __init__(self, torch, ctx):
         self.torch = torch
         self.ctx = ctx
+        self.flush_buf = None
+        self.flush_sink = None
         self.stream = torch.cuda.Stream()
         ctx.set_stream(self.stream.cuda_stream)
         ctx.begin_graph()
 
-    def time(self, steps, warmup):
+    def time(self, steps, warmup, cold=False):
         """steps: list of zero-arg callables, each enqueueing one step.  Returns
-        ms per step over one replay of the captured list."""
+        ms per step over one replay of the captured list.  cold: between the
+        untimed and the timed replay, read 4x the Infinity Cache of other data,
+        so the timed replay finds none of its inputs in any cache, whatever the
+        number of steps."""
         torch = self.torch
         with torch.cuda.stream(self.stream):
             for i in range(warmup):
@@ -78,6 +84,10 @@ class Runner:
                 for s in steps:
                     s()
             graph.replay()  # untimed replay
+            if cold:
+                if self.flush_buf is None:
+                    self.flush_buf = torch.ones(4 * MALL_BYTES // 4, device="cuda")
+                self.flush_sink = self.flush_buf.sum()
             self.stream.synchronize()
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
@@ -110,7 +120,7 @@ def bench_decode(torch, ctx, run, kv_len, steps, warmup, cold, gen):
         return lambda: ctx.attention_f32_batched_f16_kv_gated(
             q, ks[i % n_sets], vs[i % n_sets], g, 0, kv_len, 1, cap, HQ, HKV, D, out)
 
-    ms, graph = run.time([step(i) for i in range(steps)], warmup)
+    ms, graph = run.time([step(i) for i in range(steps)], warmup, cold=cold)
     del graph
     gbs = decode_bytes(kv_len) / (ms * 1e-3) / 1e9
     res = {"kv_len": kv_len, "cold": cold, "kv_sets": n_sets, "ms_per_step": ms, "GB_s": gbs,
@@ -187,7 +197,7 @@ def bench_gdn(torch, ctx, run, gen):
         return lambda: ctx.gated_delta_net_f32_batched_in_place_at(
             q1, k1, v1, g1, b1, states[i % sets], 0, 1, hk, hv, d, out1)
 
-    ms, graph = run.time([dstep(i) for i in range(1024)], 16)
+    ms, graph = run.time([dstep(i) for i in range(1024)], 16, cold=True)
     del graph
     gbs = GDN_DECODE_BYTES / (ms * 1e-3) / 1e9
     res["decode"] = {"ms_per_token_layer": ms, "tok_s": 1 / (ms * 1e-3), "GB_s": gbs,
@@ -218,7 +228,7 @@ def bench_gdn(torch, ctx, run, gen):
                                      0, 1, hk, hv, d, 1e-6, out1)
         return f
 
-    ms, graph = run.time([lstep(i) for i in range(512)], 8)
+    ms, graph = run.time([lstep(i) for i in range(512)], 8, cold=True)
     del graph
     res["decode_layer_core_fused"] = {"ms_per_token_layer": ms, "tok_s": 1 / (ms * 1e-3)}
 
@@ -237,7 +247,7 @@ def bench_gdn(torch, ctx, run, gen):
                                                    out1)
         return f
 
-    ms, graph = run.time([ostep(i) for i in range(512)], 8)
+    ms, graph = run.time([ostep(i) for i in range(512)], 8, cold=True)
     del graph
     res["decode_layer_one_kernel"] = {"ms_per_token_layer": ms, "tok_s": 1 / (ms * 1e-3),
                                       "GB_s": GDN_DECODE_BYTES / (ms * 1e-3) / 1e9}
@@ -702,7 +712,7 @@ def main():
                    "bytes_per_step": decode_bytes(args.kv_len)},
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": head["GB_s"] / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernels": "attention_decode_kernel<256,4,f16> + attention_merge "
+                     "kernels": "attention_decode_short_kernel<4> + attention_merge "
                                 "(the two dispatches of one decode step, timed together)"},
         "cpu_baseline": cpu,
         "details": details,

@@ -1,7 +1,9 @@
 /*
- * kraken_hip_diag.h -- measurement aids of the MI355X backend.  Not part of the
- * drop-in boundary: no counterpart in the reference.  They give the benchmark
- * the rates this GPU reaches, next to the published peaks:
+ * kraken_hip_diag.h -- measurement aids of the MI355X backend, in their own
+ * library (kraken-infer_amd/build/libkraken_hip_diag.so, linked against
+ * libkraken_hip.so).  Not part of the drop-in boundary: no counterpart in the
+ * reference.  They give the benchmark the rates this GPU reaches, next to the
+ * published peaks:
  *
  *  - kraken_hip_diag_stream_read reads `bytes` (a positive multiple of 16; source
  *    16-byte aligned) with nontemporal 16-byte loads from 256 x 256 threads and
@@ -10,7 +12,10 @@
  *    issuing `iterations` x 8 v_mfma_f32_32x32x16_f16 (32,768 flops each), and writes
  *    `workgroups` x 256 floats to `sink`.
  *
- * Status codes, argument checks and synchronisation follow kraken_hip.h.
+ * Status codes and argument checks follow kraken_hip.h; the message of the last
+ * non-OK call on this thread is kraken_hip_diag_last_error().  Both probes only
+ * enqueue on the context's stream (they never wait; a host copy or
+ * commit_graph on the context waits for them).
  */
 #ifndef KRAKEN_HIP_DIAG_H
 #define KRAKEN_HIP_DIAG_H
@@ -25,6 +30,7 @@ KRAKEN_API int kraken_hip_diag_stream_read(kraken_hip_context* context, kraken_b
                                            size_t bytes, kraken_buffer sink);
 KRAKEN_API int kraken_hip_diag_mfma_f16(kraken_hip_context* context, uint32_t workgroups,
                                         uint32_t iterations, kraken_buffer sink);
+KRAKEN_API const char* kraken_hip_diag_last_error(void);
 
 #ifdef __cplusplus
 }

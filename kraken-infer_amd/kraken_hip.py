@@ -46,9 +46,6 @@ _ctx = ctypes.c_void_p
 
 # name -> argument types after the context pointer (all return int).
 SIGNATURES = {
-    # Measurement aids (include/kraken_hip_diag.h).
-    "kraken_hip_diag_stream_read": [_B, _sz, _B],
-    "kraken_hip_diag_mfma_f16": [ctypes.c_uint32, ctypes.c_uint32, _B],
     "kraken_hip_attention_f32_batched_f16_kv": [_B, _B, _B] + [_sz] * 7 + [_B],
     "kraken_hip_attention_f32_batched": [_B, _B, _B] + [_sz] * 7 + [_B],
     "kraken_hip_attention_f32_batched_f16_kv_gated": [_B, _B, _B, _B] + [_sz] * 7 + [_B],
@@ -97,7 +94,15 @@ SIGNATURES = {
     "kraken_hip_context_set_stream": [ctypes.c_void_p],
 }
 
+# Measurement aids (include/kraken_hip_diag.h), in libkraken_hip_diag.so.
+DIAG_SIGNATURES = {
+    "kraken_hip_diag_stream_read": [_B, _sz, _B],
+    "kraken_hip_diag_mfma_f16": [ctypes.c_uint32, ctypes.c_uint32, _B],
+}
+DIAG_LIB_PATH = os.path.join(os.path.dirname(LIB_PATH), "libkraken_hip_diag.so")
+
 _lib = None
+_diag = None
 
 
 def lib():
@@ -127,6 +132,24 @@ def lib():
         l.kraken_hip_last_error.argtypes = []
         _lib = l
     return _lib
+
+
+def diag_lib():
+    """Loads the measurement-probe library (bench.py and its tests only)."""
+    global _diag
+    if _diag is None:
+        lib()
+        if not os.path.exists(DIAG_LIB_PATH):
+            raise RuntimeError(f"{DIAG_LIB_PATH} is missing: build it with `make -C kraken-infer_amd`")
+        d = ctypes.CDLL(DIAG_LIB_PATH)
+        for name, args in DIAG_SIGNATURES.items():
+            fn = getattr(d, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [_ctx] + args
+        d.kraken_hip_diag_last_error.restype = ctypes.c_char_p
+        d.kraken_hip_diag_last_error.argtypes = []
+        _diag = d
+    return _diag
 
 
 def last_error() -> str:
@@ -217,16 +240,21 @@ class Context:
 
     def status(self, name: str, *args) -> int:
         """Calls kraken_hip_<name> and returns its status code."""
-        fn = getattr(lib(), "kraken_hip_" + name)
-        types = SIGNATURES["kraken_hip_" + name]
+        full = "kraken_hip_" + name
+        diag = full in DIAG_SIGNATURES
+        fn = getattr(diag_lib() if diag else lib(), full)
+        types = DIAG_SIGNATURES[full] if diag else SIGNATURES[full]
         conv = [as_buffer(a) if t is KrakenBuffer else a for a, t in zip(args, types)]
         return fn(self.handle, *conv)
 
     def call(self, name: str, *args):
-        self._check(name, self.status(name, *args))
+        code = self.status(name, *args)
+        if code != OK and "kraken_hip_" + name in DIAG_SIGNATURES:
+            raise KrakenError(code, diag_lib().kraken_hip_diag_last_error().decode(), name)
+        self._check(name, code)
 
     def __getattr__(self, name):
-        if "kraken_hip_" + name in SIGNATURES:
+        if "kraken_hip_" + name in SIGNATURES or "kraken_hip_" + name in DIAG_SIGNATURES:
             return lambda *args: self.call(name, *args)
         raise AttributeError(name)
 

@@ -18,13 +18,23 @@ import kraken_hip as kh
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
+BOUNDARY_HEADERS = [h for h in HEADERS if not h.endswith("kraken_hip_diag.h")]
+DIAG_HEADERS = [h for h in HEADERS if h.endswith("kraken_hip_diag.h")]
 ACCEPTED = "validation-only context: arguments accepted"
 
 
-def declared_symbols():
-    """Entry points declared in every C header under include/."""
-    text = "".join(open(h).read() for h in HEADERS)
+def declared_symbols(headers=None):
+    """Entry points declared in the boundary's C headers under include/ (or in
+    `headers`)."""
+    text = "".join(open(h).read() for h in (BOUNDARY_HEADERS if headers is None else headers))
     return sorted(set(re.findall(r"KRAKEN_API[^;]*?\b(kraken_hip_\w+)\s*\(", text, re.S)))
+
+
+def exported(path):
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    return set(re.findall(r"\b(kraken_hip_\w+)\b", out))
 
 
 def test_library_exports_every_declared_symbol():
@@ -36,12 +46,15 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_no_undeclared_exports():
-    """Every exported kraken_hip_* symbol is declared in the header."""
-    import subprocess
-    out = subprocess.run(["nm", "-D", "--defined-only", kh.LIB_PATH], capture_output=True,
-                         text=True, check=True).stdout
-    exported = set(re.findall(r"\b(kraken_hip_\w+)\b", out))
-    assert exported == set(declared_symbols())
+    """The boundary library exports exactly what its headers declare: the
+    measurement probes live in their own library."""
+    assert exported(kh.LIB_PATH) == set(declared_symbols())
+
+
+def test_diag_library_exports_its_header():
+    assert exported(kh.DIAG_LIB_PATH) == set(declared_symbols(DIAG_HEADERS))
+    assert set(kh.DIAG_SIGNATURES) | {"kraken_hip_diag_last_error"} == set(
+        declared_symbols(DIAG_HEADERS))
 
 
 def test_python_signatures_cover_header():
@@ -66,6 +79,8 @@ def fake(nbytes):
 
 def status(ctx, name, *args):
     code = ctx.status(name, *args)
+    if "kraken_hip_" + name in kh.DIAG_SIGNATURES:
+        return code, kh.diag_lib().kraken_hip_diag_last_error().decode()
     return code, kh.last_error()
 
 
@@ -368,7 +383,8 @@ def test_gdn_layer_dt_bias_and_ssm_a_together(vctx):
 
 
 def test_diag_probe_argument_checks(vctx):
-    """The measurement aids (include/kraken_hip_diag.h) check sizes and alignment."""
+    """The measurement aids (include/kraken_hip_diag.h, their own library) check
+    sizes and alignment, and answer a validation-only context like the boundary."""
     sink = fake(256 * 256 * 4)
     assert status(vctx, "diag_stream_read", fake(1 << 20), 1 << 20, sink) == (kh.UNAVAILABLE,
                                                                              ACCEPTED)
