@@ -136,6 +136,24 @@ int oracle_qwen3_attention_sequence(const float* q_raw, const float* k_raw,
                                     float* key_cache, float* value_cache, float* q_out,
                                     float* output);
 
+/* K-quant projections and argmax (oracle/kquant_oracle.c).  Formats: */
+enum { ORACLE_Q4_K = 0, ORACLE_Q5_K = 1, ORACLE_Q6_K = 2 };
+/* Bytes per 256-value block: 144, 176, 210 (0 for an unknown format). */
+size_t oracle_kquant_block_bytes(int format);
+/* q4_k/q5_k/q6_k_get_row, mps_backend.mm:1448-1540: `blocks` consecutive blocks
+ * into 256 * blocks floats, in the reference's float arithmetic. */
+void oracle_kquant_dequantize(int format, const uint8_t* data, size_t blocks, float* out);
+/* matvec / matmul (mps_backend.mm:295-460, 1268-1440): out[t][r] =
+ * sum_c w[r][c] x[t][c], accumulated in double; weight rows of cols/256 blocks.
+ * weight_f16 / input_f16 round each dequantized weight / input to binary16
+ * first (the reference's many-token mul_mm path, mps_backend.mm:1082-1230). */
+void oracle_kquant_matmul(int format, const uint8_t* weight, size_t rows, size_t cols,
+                          const float* input, size_t tokens, int weight_f16, int input_f16,
+                          float* out);
+/* argmax_f32_i32 / argmax_prob_f32_i32, mps_backend.mm:2681-2779 (probability
+ * may be NULL). */
+int32_t oracle_argmax(const float* values, size_t size, float* probability);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,13 @@ def _declare(l):
     l.oracle_qwen3_attention_sequence.restype = ctypes.c_int
     l.oracle_qwen3_attention_sequence.argtypes = ([_f32p] * 3 + [_sz] * 4 + [_f32p, _f32p] +
                                                   [ctypes.c_double] * 2 + [_f32p] * 4)
+    l.oracle_kquant_block_bytes.restype = _sz
+    l.oracle_kquant_block_bytes.argtypes = [ctypes.c_int]
+    l.oracle_kquant_dequantize.argtypes = [ctypes.c_int, ctypes.c_void_p, _sz, _f32p]
+    l.oracle_kquant_matmul.argtypes = [ctypes.c_int, ctypes.c_void_p, _sz, _sz, _f32p, _sz,
+                                       ctypes.c_int, ctypes.c_int, _f32p]
+    l.oracle_argmax.restype = ctypes.c_int32
+    l.oracle_argmax.argtypes = [_f32p, _sz, _f32p]
 
 
 def _f32(a) -> np.ndarray:
@@ -292,3 +299,42 @@ def mul(target, rhs):
     t, r = _f32(target), _f32(rhs)
     lib().oracle_mul_f32(_p(t), _p(r), t.size)
     return t
+
+
+# ------------------------------------------------------------ K-quants -----
+# Formats (oracle/kquant_oracle.c): GGUF Q4_K, Q5_K, Q6_K, 256 values per block.
+KQUANT_FORMATS = {"q4_k": 0, "q5_k": 1, "q6_k": 2}
+KQUANT_BLOCK_BYTES = {"q4_k": 144, "q5_k": 176, "q6_k": 210}
+
+
+def _bytes(data) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(data, dtype=np.uint8)).copy()
+
+
+def kquant_dequantize(fmt, data, blocks):
+    """`blocks` consecutive blocks of format `fmt` -> 256 * blocks floats."""
+    d = _bytes(data)
+    assert d.size >= blocks * KQUANT_BLOCK_BYTES[fmt]
+    out = np.empty(256 * blocks, np.float32)
+    lib().oracle_kquant_dequantize(KQUANT_FORMATS[fmt], d.ctypes.data, blocks, _p(out))
+    return out
+
+
+def kquant_matmul(fmt, weight, rows, cols, x, tokens, weight_f16=False, input_f16=False):
+    """out [tokens][rows] = W [rows][cols] (quantized rows) times x [tokens][cols]."""
+    w = _bytes(weight)
+    xx = _f32(x)
+    assert cols % 256 == 0 and w.size >= rows * (cols // 256) * KQUANT_BLOCK_BYTES[fmt]
+    assert xx.size >= tokens * cols
+    out = np.empty(tokens * rows, np.float32)
+    lib().oracle_kquant_matmul(KQUANT_FORMATS[fmt], w.ctypes.data, rows, cols, _p(xx), tokens,
+                               int(weight_f16), int(input_f16), _p(out))
+    return out
+
+
+def argmax(values, probability=False):
+    """argmax_f32_i32 (index) or argmax_prob_f32_i32 ((index, probability))."""
+    v = _f32(values)
+    p = np.zeros(1, np.float32)
+    idx = int(lib().oracle_argmax(_p(v), v.size, _p(p) if probability else None))
+    return (idx, float(p[0])) if probability else idx
