@@ -546,6 +546,58 @@ def bench_prefix():
     return vals
 
 
+KQUANT_SHAPES = [("q5_k", 6144, 1024), ("q4_k", 3584, 1024), ("q6_k", 1024, 3584),
+                 ("q4_k", 1024, 2048)]
+KQUANT_BLOCK = {"q4_k": 144, "q5_k": 176, "q6_k": 210}
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def kquant_weight(torch, fmt, rows, cols, gen):
+    """Random K-quant blocks with small positive f16 scales (every other byte
+    pattern is a valid block), as a uint8 device tensor."""
+    nb = KQUANT_BLOCK[fmt]
+    blocks = rows * cols // 256
+    w = torch.randint(0, 256, (blocks, nb), generator=gen, device="cuda", dtype=torch.uint8)
+    d = (torch.rand(blocks, generator=gen, device="cuda") * 0.02 + 0.001).half()
+    at = 208 if fmt == "q6_k" else 0
+    w[:, at:at + 2] = d.view(torch.uint8).view(blocks, 2)
+    if fmt != "q6_k":
+        w[:, 2:4] = d.view(torch.uint8).view(blocks, 2)
+    return w.reshape(-1)
+
+
+def bench_kquant(torch, ctx, run, gen):
+    """The Qwen3.5-0.8B K-quant projections: one-token GEMV (weights read
+    once; sets rotated over 2x the Infinity Cache so every replay reads HBM)
+    and 1024-token GEMM (dequantize to fp16 + MFMA GEMM), as graph replays.
+    GEMV bytes = quantized weight + f32 input + f32 output; GEMM flops =
+    2 * rows * cols * tokens over the whole call (its three launches)."""
+    out = []
+    for fmt, rows, cols in KQUANT_SHAPES:
+        wbytes = rows * cols // 256 * KQUANT_BLOCK[fmt]
+        sets = max(1, -(-2 * MALL_BYTES // wbytes))
+        ws = [kquant_weight(torch, fmt, rows, cols, gen) for _ in range(sets)]
+        x = torch.randn(1024 * cols, generator=gen, device="cuda")
+        y = torch.empty(1024 * rows, device="cuda")
+        mv = getattr(ctx, f"matvec_{fmt}_f32_device")
+        mm = getattr(ctx, f"matmul_{fmt}_f32_device")
+        gemv_steps = [lambda i=i: mv(ws[i % sets], rows, cols, x, y) for i in range(2 * sets)]
+        ms_gemv, graph = run.time(gemv_steps, 4, cold=True)
+        del graph
+        gemv_bytes = wbytes + 4 * cols + 4 * rows
+        gemv_gbs = gemv_bytes / (ms_gemv * 1e-3) / 1e9
+        ms_gemm, graph = run.time([lambda: mm(ws[0], rows, cols, 1024, x, y)] * 10, 2)
+        del graph
+        tflops = 2.0 * rows * cols * 1024 / (ms_gemm * 1e-3) / 1e12
+        out.append({"format": fmt, "rows": rows, "cols": cols,
+                    "gemv_us": ms_gemv * 1e3, "gemv_bytes": gemv_bytes, "gemv_GB_s": gemv_gbs,
+                    "gemv_frac_hbm": gemv_gbs / HBM_PEAK_GBS, "gemv_weight_sets": sets,
+                    "gemm_tokens": 1024, "gemm_us": ms_gemm * 1e3, "gemm_TFLOP_s": tflops,
+                    "gemm_frac_mfma_f16": tflops / MFMA_F16_PEAK_TFLOPS})
+        del ws
+    return out
+
+
 def bench_peaks(torch, ctx, run):
     """Achievable rates on this box, next to the published peaks.  The library's probes
     (include/kraken_hip_diag.h): a nontemporal streaming read of 2 GiB and an fp16 MFMA loop
@@ -608,9 +660,9 @@ def main():
     ap.add_argument("--kv-len", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline only, no details")
-    ap.add_argument("--sections", default="decode,prefill,gdn,c4,peaks,prefix",
+    ap.add_argument("--sections", default="decode,prefill,gdn,c4,kquant,peaks,prefix",
                     help="comma-separated detail sections to run after the headline "
-                         "(decode, prefill, gdn, c4, peaks, prefix)")
+                         "(decode, prefill, gdn, c4, kquant, peaks, prefix)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run torch copies of MIB MiB (20 launches), the known-size "
@@ -666,6 +718,12 @@ def main():
             gen.manual_seed(4)
             details["ragged_c4"] = bench_c4(torch, ctx, run, gen)
             progress("ragged c4 done")
+        if "kquant" in sections:
+            gen.manual_seed(5)
+            details["kquant"] = bench_kquant(torch, ctx, run, gen)
+            progress("kquant: " + ", ".join(
+                f"{k['format']} {k['rows']}x{k['cols']} GEMV {k['gemv_GB_s']:.0f} GB/s "
+                f"GEMM {k['gemm_TFLOP_s']:.0f} TFLOP/s" for k in details["kquant"]))
         if "peaks" in sections:
             peaks = bench_peaks(torch, ctx, run)
             details["achievable_peaks"] = peaks

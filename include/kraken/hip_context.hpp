@@ -20,7 +20,9 @@
 #pragma once
 
 #include <cstddef>
+#include <cstdint>
 #include <string>
+#include <vector>
 #include <utility>
 
 #include "kraken_hip.h"
@@ -541,8 +543,188 @@ class HipContext {
       kraken_hip_mul_f32_row_in_place(ctx_, target.raw(), row.raw(), rows, row_size));
   }
 
+  // K-quant projections (mps_backend.hpp:134-226).  matvec_*_f32 takes and
+  // returns host vectors through temporary device buffers, as the reference's
+  // overload does (mps_backend.mm:6456-6492).
+  [[nodiscard]] Result<std::vector<float>> matvec_q4_k_f32(const HipBuffer& weight,
+                                                        std::size_t rows, std::size_t cols,
+                                                        const std::vector<float>& input) const {
+    return host_matvec(&kraken_hip_matvec_q4_k_f32_device, "HIP Q4_K", weight, rows, cols, input);
+  }
+  [[nodiscard]] Status matvec_q4_k_f32_device(const HipBuffer& weight, std::size_t rows,
+                                          std::size_t cols, const HipBuffer& input,
+                                          HipBuffer& output) const {
+    return Status::from_code(kraken_hip_matvec_q4_k_f32_device(ctx_, weight.raw(), rows, cols,
+                                                              input.raw(), output.raw()));
+  }
+  [[nodiscard]] Status matvec_q4_k_f32_top1(const HipBuffer& weight, std::size_t rows,
+                                        std::size_t cols, const HipBuffer& input,
+                                        HipBuffer& token_output,
+                                        HipBuffer& probability_output) const {
+    return Status::from_code(kraken_hip_matvec_q4_k_f32_top1(
+      ctx_, weight.raw(), rows, cols, input.raw(), token_output.raw(), probability_output.raw()));
+  }
+  [[nodiscard]] Status matvec_q4_k_f32_argmax(const HipBuffer& weight, std::size_t rows,
+                                          std::size_t cols, const HipBuffer& input,
+                                          HipBuffer& token_output) const {
+    return Status::from_code(kraken_hip_matvec_q4_k_f32_argmax(ctx_, weight.raw(), rows, cols,
+                                                              input.raw(), token_output.raw()));
+  }
+  [[nodiscard]] Status matmul_q4_k_f32_device(const HipBuffer& weight, std::size_t rows,
+                                          std::size_t cols, std::size_t tokens,
+                                          const HipBuffer& input, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_matmul_q4_k_f32_device(ctx_, weight.raw(), rows, cols,
+                                                              tokens, input.raw(), output.raw()));
+  }
+  [[nodiscard]] Status dequantize_row_q4_k_f32(const HipBuffer& weight, std::size_t row,
+                                           std::size_t cols, HipBuffer& output) const {
+    return Status::from_code(
+      kraken_hip_dequantize_row_q4_k_f32(ctx_, weight.raw(), row, cols, output.raw()));
+  }
+  [[nodiscard]] Status dequantize_rows_q4_k_f32(const HipBuffer& weight, std::size_t rows,
+                                            const HipBuffer& row_ids, std::size_t tokens,
+                                            std::size_t cols, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_dequantize_rows_q4_k_f32(
+      ctx_, weight.raw(), rows, row_ids.raw(), tokens, cols, output.raw()));
+  }
+  [[nodiscard]] Result<std::vector<float>> matvec_q5_k_f32(const HipBuffer& weight,
+                                                        std::size_t rows, std::size_t cols,
+                                                        const std::vector<float>& input) const {
+    return host_matvec(&kraken_hip_matvec_q5_k_f32_device, "HIP Q5_K", weight, rows, cols, input);
+  }
+  [[nodiscard]] Status matvec_q5_k_f32_device(const HipBuffer& weight, std::size_t rows,
+                                          std::size_t cols, const HipBuffer& input,
+                                          HipBuffer& output) const {
+    return Status::from_code(kraken_hip_matvec_q5_k_f32_device(ctx_, weight.raw(), rows, cols,
+                                                              input.raw(), output.raw()));
+  }
+  [[nodiscard]] Status matvec_q5_k_f32_top1(const HipBuffer& weight, std::size_t rows,
+                                        std::size_t cols, const HipBuffer& input,
+                                        HipBuffer& token_output,
+                                        HipBuffer& probability_output) const {
+    return Status::from_code(kraken_hip_matvec_q5_k_f32_top1(
+      ctx_, weight.raw(), rows, cols, input.raw(), token_output.raw(), probability_output.raw()));
+  }
+  [[nodiscard]] Status matvec_q5_k_f32_argmax(const HipBuffer& weight, std::size_t rows,
+                                          std::size_t cols, const HipBuffer& input,
+                                          HipBuffer& token_output) const {
+    return Status::from_code(kraken_hip_matvec_q5_k_f32_argmax(ctx_, weight.raw(), rows, cols,
+                                                              input.raw(), token_output.raw()));
+  }
+  [[nodiscard]] Status matmul_q5_k_f32_device(const HipBuffer& weight, std::size_t rows,
+                                          std::size_t cols, std::size_t tokens,
+                                          const HipBuffer& input, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_matmul_q5_k_f32_device(ctx_, weight.raw(), rows, cols,
+                                                              tokens, input.raw(), output.raw()));
+  }
+  [[nodiscard]] Status dequantize_row_q5_k_f32(const HipBuffer& weight, std::size_t row,
+                                           std::size_t cols, HipBuffer& output) const {
+    return Status::from_code(
+      kraken_hip_dequantize_row_q5_k_f32(ctx_, weight.raw(), row, cols, output.raw()));
+  }
+  [[nodiscard]] Status dequantize_rows_q5_k_f32(const HipBuffer& weight, std::size_t rows,
+                                            const HipBuffer& row_ids, std::size_t tokens,
+                                            std::size_t cols, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_dequantize_rows_q5_k_f32(
+      ctx_, weight.raw(), rows, row_ids.raw(), tokens, cols, output.raw()));
+  }
+  [[nodiscard]] Result<std::vector<float>> matvec_q6_k_f32(const HipBuffer& weight,
+                                                        std::size_t rows, std::size_t cols,
+                                                        const std::vector<float>& input) const {
+    return host_matvec(&kraken_hip_matvec_q6_k_f32_device, "HIP Q6_K", weight, rows, cols, input);
+  }
+  [[nodiscard]] Status matvec_q6_k_f32_device(const HipBuffer& weight, std::size_t rows,
+                                          std::size_t cols, const HipBuffer& input,
+                                          HipBuffer& output) const {
+    return Status::from_code(kraken_hip_matvec_q6_k_f32_device(ctx_, weight.raw(), rows, cols,
+                                                              input.raw(), output.raw()));
+  }
+  [[nodiscard]] Status matvec_q6_k_f32_top1(const HipBuffer& weight, std::size_t rows,
+                                        std::size_t cols, const HipBuffer& input,
+                                        HipBuffer& token_output,
+                                        HipBuffer& probability_output) const {
+    return Status::from_code(kraken_hip_matvec_q6_k_f32_top1(
+      ctx_, weight.raw(), rows, cols, input.raw(), token_output.raw(), probability_output.raw()));
+  }
+  [[nodiscard]] Status matvec_q6_k_f32_argmax(const HipBuffer& weight, std::size_t rows,
+                                          std::size_t cols, const HipBuffer& input,
+                                          HipBuffer& token_output) const {
+    return Status::from_code(kraken_hip_matvec_q6_k_f32_argmax(ctx_, weight.raw(), rows, cols,
+                                                              input.raw(), token_output.raw()));
+  }
+  [[nodiscard]] Status matmul_q6_k_f32_device(const HipBuffer& weight, std::size_t rows,
+                                          std::size_t cols, std::size_t tokens,
+                                          const HipBuffer& input, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_matmul_q6_k_f32_device(ctx_, weight.raw(), rows, cols,
+                                                              tokens, input.raw(), output.raw()));
+  }
+  [[nodiscard]] Status dequantize_row_q6_k_f32(const HipBuffer& weight, std::size_t row,
+                                           std::size_t cols, HipBuffer& output) const {
+    return Status::from_code(
+      kraken_hip_dequantize_row_q6_k_f32(ctx_, weight.raw(), row, cols, output.raw()));
+  }
+  [[nodiscard]] Status dequantize_rows_q6_k_f32(const HipBuffer& weight, std::size_t rows,
+                                            const HipBuffer& row_ids, std::size_t tokens,
+                                            std::size_t cols, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_dequantize_rows_q6_k_f32(
+      ctx_, weight.raw(), rows, row_ids.raw(), tokens, cols, output.raw()));
+  }
+
+  // Device argmax (mps_backend.hpp:384-390).
+  [[nodiscard]] Status argmax_f32_i32(const HipBuffer& values, std::size_t size,
+                                      HipBuffer& output) const {
+    return Status::from_code(kraken_hip_argmax_f32_i32(ctx_, values.raw(), size, output.raw()));
+  }
+  [[nodiscard]] Status argmax_prob_f32_i32(const HipBuffer& values, std::size_t size,
+                                           HipBuffer& token_output,
+                                           HipBuffer& probability_output) const {
+    return Status::from_code(kraken_hip_argmax_prob_f32_i32(
+      ctx_, values.raw(), size, token_output.raw(), probability_output.raw()));
+  }
+
  private:
   explicit HipContext(kraken_hip_context* raw) : ctx_(raw) {}
+
+  using MatvecEntry = int (*)(kraken_hip_context*, kraken_buffer, std::size_t, std::size_t,
+                              kraken_buffer, kraken_buffer);
+
+  // The host-vector matvec: input size check, buffers, copy in, run, copy out.
+  [[nodiscard]] Result<std::vector<float>> host_matvec(MatvecEntry entry, const char* name,
+                                                       const HipBuffer& weight,
+                                                       std::size_t rows, std::size_t cols,
+                                                       const std::vector<float>& input) const {
+    if (input.size() != cols) {
+      return Status::invalid_argument(std::string(name) +
+                                      " matvec input size does not match cols");
+    }
+    if (rows == 0 || cols == 0 || rows > SIZE_MAX / sizeof(float)) {
+      return Status::invalid_argument(std::string(name) +
+                                      " matvec rows and cols must be greater than zero");
+    }
+    auto in = make_buffer(cols * sizeof(float));
+    if (!in.is_ok()) {
+      return in.status();
+    }
+    auto out = make_buffer(rows * sizeof(float));
+    if (!out.is_ok()) {
+      return out.status();
+    }
+    Status s = copy_to_buffer(in.value(), input.data(), cols * sizeof(float));
+    if (!s.is_ok()) {
+      return s;
+    }
+    s = Status::from_code(entry(ctx_, weight.raw(), rows, cols, in.value().raw(),
+                                out.value().raw()));
+    if (!s.is_ok()) {
+      return s;
+    }
+    std::vector<float> output(rows);
+    s = copy_from_buffer(out.value(), output.data(), rows * sizeof(float));
+    if (!s.is_ok()) {
+      return s;
+    }
+    return output;
+  }
 
   kraken_hip_context* ctx_{nullptr};
 };

@@ -428,6 +428,108 @@ KRAKEN_API int kraken_hip_qwen35_gdn_layer_ragged_decode_f32(
   kraken_buffer seq_state_offsets, size_t sequences, size_t key_heads, size_t value_heads,
   size_t head_dim, float eps, kraken_buffer output);
 
+/* ---- K-quant projections (GGUF Q4_K / Q5_K / Q6_K weights) and argmax ----
+ *
+ * Weights are rows of GGUF super-blocks of 256 values (Q4_K 144 bytes, Q5_K
+ * 176, Q6_K 210 per block), row-major [rows][cols / 256]; cols must be a
+ * multiple of 256.  Outputs are f32.  Validation follows the reference's
+ * order and messages ("HIP" for "MPS").  Beyond the reference, the weight must
+ * be 4-byte aligned (Q6_K: 2-byte) and inputs and dequantized outputs 16-byte
+ * aligned, as every allocation of this library is.
+ *
+ * matvec_*_device: output[rows] = W @ input[cols], fp32 arithmetic
+ *   (mps_backend.hpp:137-140, 158-161, 179-182).
+ * matvec_*_top1: token_output[0] = argmax_r (W @ input)[r] and
+ *   probability_output[0] = its softmax probability over all rows; _argmax
+ *   only the token (mps_backend.hpp:141-149, 162-170, 183-191).  Limited to
+ *   cols <= 4096 (16 blocks per row), as the reference's kernels are.
+ * matmul_*_device: output[tokens][rows] = input[tokens][cols] @ W^T
+ *   (mps_backend.hpp:150-154, 171-175, 192-196).  Up to 8 tokens the weights
+ *   are dequantized to f32 and multiplied in fp32; above 8, as in the
+ *   reference's tiled kernel, weights and inputs are rounded to f16 and
+ *   multiplied with f32 accumulation (MFMA), using context workspace of
+ *   2 * (rows + tokens) * cols bytes.
+ * dequantize_row_*: output[cols] = row `row` of W (mps_backend.hpp:197-200,
+ *   207-210, 217-220).  dequantize_rows_*: output[tokens][cols], row
+ *   row_ids[t] (i32) for token t; an id outside [0, rows) gives a zero row
+ *   (mps_backend.hpp:201-206, 211-216, 221-226). */
+KRAKEN_API int kraken_hip_matvec_q4_k_f32_device(kraken_hip_context* context,
+                                              kraken_buffer weight, size_t rows, size_t cols,
+                                              kraken_buffer input, kraken_buffer output);
+KRAKEN_API int kraken_hip_matvec_q4_k_f32_top1(kraken_hip_context* context, kraken_buffer weight,
+                                            size_t rows, size_t cols, kraken_buffer input,
+                                            kraken_buffer token_output,
+                                            kraken_buffer probability_output);
+KRAKEN_API int kraken_hip_matvec_q4_k_f32_argmax(kraken_hip_context* context,
+                                              kraken_buffer weight, size_t rows, size_t cols,
+                                              kraken_buffer input, kraken_buffer token_output);
+KRAKEN_API int kraken_hip_matmul_q4_k_f32_device(kraken_hip_context* context,
+                                              kraken_buffer weight, size_t rows, size_t cols,
+                                              size_t tokens, kraken_buffer input,
+                                              kraken_buffer output);
+KRAKEN_API int kraken_hip_dequantize_row_q4_k_f32(kraken_hip_context* context,
+                                               kraken_buffer weight, size_t row, size_t cols,
+                                               kraken_buffer output);
+KRAKEN_API int kraken_hip_dequantize_rows_q4_k_f32(kraken_hip_context* context,
+                                                kraken_buffer weight, size_t rows,
+                                                kraken_buffer row_ids, size_t tokens,
+                                                size_t cols, kraken_buffer output);
+
+KRAKEN_API int kraken_hip_matvec_q5_k_f32_device(kraken_hip_context* context,
+                                              kraken_buffer weight, size_t rows, size_t cols,
+                                              kraken_buffer input, kraken_buffer output);
+KRAKEN_API int kraken_hip_matvec_q5_k_f32_top1(kraken_hip_context* context, kraken_buffer weight,
+                                            size_t rows, size_t cols, kraken_buffer input,
+                                            kraken_buffer token_output,
+                                            kraken_buffer probability_output);
+KRAKEN_API int kraken_hip_matvec_q5_k_f32_argmax(kraken_hip_context* context,
+                                              kraken_buffer weight, size_t rows, size_t cols,
+                                              kraken_buffer input, kraken_buffer token_output);
+KRAKEN_API int kraken_hip_matmul_q5_k_f32_device(kraken_hip_context* context,
+                                              kraken_buffer weight, size_t rows, size_t cols,
+                                              size_t tokens, kraken_buffer input,
+                                              kraken_buffer output);
+KRAKEN_API int kraken_hip_dequantize_row_q5_k_f32(kraken_hip_context* context,
+                                               kraken_buffer weight, size_t row, size_t cols,
+                                               kraken_buffer output);
+KRAKEN_API int kraken_hip_dequantize_rows_q5_k_f32(kraken_hip_context* context,
+                                                kraken_buffer weight, size_t rows,
+                                                kraken_buffer row_ids, size_t tokens,
+                                                size_t cols, kraken_buffer output);
+
+KRAKEN_API int kraken_hip_matvec_q6_k_f32_device(kraken_hip_context* context,
+                                              kraken_buffer weight, size_t rows, size_t cols,
+                                              kraken_buffer input, kraken_buffer output);
+KRAKEN_API int kraken_hip_matvec_q6_k_f32_top1(kraken_hip_context* context, kraken_buffer weight,
+                                            size_t rows, size_t cols, kraken_buffer input,
+                                            kraken_buffer token_output,
+                                            kraken_buffer probability_output);
+KRAKEN_API int kraken_hip_matvec_q6_k_f32_argmax(kraken_hip_context* context,
+                                              kraken_buffer weight, size_t rows, size_t cols,
+                                              kraken_buffer input, kraken_buffer token_output);
+KRAKEN_API int kraken_hip_matmul_q6_k_f32_device(kraken_hip_context* context,
+                                              kraken_buffer weight, size_t rows, size_t cols,
+                                              size_t tokens, kraken_buffer input,
+                                              kraken_buffer output);
+KRAKEN_API int kraken_hip_dequantize_row_q6_k_f32(kraken_hip_context* context,
+                                               kraken_buffer weight, size_t row, size_t cols,
+                                               kraken_buffer output);
+KRAKEN_API int kraken_hip_dequantize_rows_q6_k_f32(kraken_hip_context* context,
+                                                kraken_buffer weight, size_t rows,
+                                                kraken_buffer row_ids, size_t tokens,
+                                                size_t cols, kraken_buffer output);
+
+/* argmax_f32_i32 (mps_backend.hpp:384-386): output[0] = the first index of
+ * the largest of values[size]; NaN never wins, -inf can; all-NaN gives size.
+ * argmax_prob_f32_i32 (mps_backend.hpp:387-390): also probability_output[0]
+ * = 1 / sum_i exp(values[i] - max), or 0 when that sum is not positive.
+ * Inputs above 16384 values use context workspace (12 bytes per 4096). */
+KRAKEN_API int kraken_hip_argmax_f32_i32(kraken_hip_context* context, kraken_buffer values,
+                                         size_t size, kraken_buffer output);
+KRAKEN_API int kraken_hip_argmax_prob_f32_i32(kraken_hip_context* context, kraken_buffer values,
+                                              size_t size, kraken_buffer token_output,
+                                              kraken_buffer probability_output);
+
 #ifdef __cplusplus
 }
 #endif

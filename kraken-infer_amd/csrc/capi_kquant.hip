@@ -1,0 +1,369 @@
+// C-ABI entry points of the K-quant projections and the device argmax:
+// argument validation in the reference's order and wording ("HIP" in place of
+// "MPS"), then dispatch to kquant.hip.  Host dispatchers followed:
+// make_q*_k_matvec_layout / make_k_quant_matmul_layout (mps_backend.mm:
+// 4036-4189), matvec_q*_k_f32_device (:6134-6197), matvec_q*_k_f32_top1
+// (:6199-6271), matvec_q*_k_f32_argmax (:6273-6334), matmul_q*_k_f32_device
+// (:6336-6450), dequantize_row(s)_q*_k_f32 (:7217-7756), argmax_f32_i32 /
+// argmax_prob_f32_i32 (:10004-10120).  The Q5_K and Q6_K methods repeat the
+// Q4_K ones with their names and block sizes.
+//
+// Beyond the reference, the device kernels read weights as 32-bit words and
+// the input as 16-byte vectors, so the weight must be 4-byte aligned (Q6_K:
+// 2-byte, its blocks are 210 bytes) and the input 16-byte aligned; any
+// allocation of this library or of torch is.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "context_internal.hpp"
+
+using namespace kraken;
+
+namespace {
+
+constexpr size_t kTop1MaxBlocksPerRow = 16;  // kKQuantTop1MaxBlocksPerRow, mps_backend.mm:3798
+
+const char* fmt_name(int format) {
+  return format == 0 ? "Q4_K" : (format == 1 ? "Q5_K" : "Q6_K");
+}
+
+struct Layout {
+  size_t blocks_per_row = 0;
+  size_t weight_bytes = 0;
+};
+
+// make_q*_k_matvec_layout (mps_backend.mm:4036-4141).
+int matvec_layout(int format, size_t rows, size_t cols, Layout& out) {
+  const std::string p = std::string("HIP ") + fmt_name(format) + " matvec ";
+  if (rows == 0 || cols == 0) {
+    return invalid(p + "rows and cols must be greater than zero");
+  }
+  if (cols % 256u != 0) {
+    return invalid(p + "cols must be divisible by 256");
+  }
+  if (!fits_u32(cols)) {
+    return invalid(p + "cols exceeds uint32 range");
+  }
+  out.blocks_per_row = cols / 256u;
+  size_t total_blocks = 0;
+  if (!checked_mul(rows, out.blocks_per_row, total_blocks)) {
+    return invalid(p + "block count overflow");
+  }
+  if (!checked_mul(total_blocks, kquant_block_bytes(format), out.weight_bytes)) {
+    return invalid(p + "weight byte count overflow");
+  }
+  size_t bytes = 0;
+  if (!checked_mul(cols, sizeof(float), bytes) || !checked_mul(rows, sizeof(float), bytes)) {
+    return invalid(p + "buffer byte count overflow");
+  }
+  return KRAKEN_OK;
+}
+
+int check_alignment(int format, const kraken_buffer& weight, const kraken_buffer& input,
+                    const char* what) {
+  const uintptr_t need = format == 2 ? 2u : 4u;
+  if (((uintptr_t)weight.data & (need - 1u)) != 0) {
+    return invalid(std::string("HIP ") + fmt_name(format) + " " + what +
+                   " weight buffer must be " + (format == 2 ? "2" : "4") + "-byte aligned");
+  }
+  if (((uintptr_t)input.data & 15u) != 0) {
+    return invalid(std::string("HIP ") + fmt_name(format) + " " + what +
+                   " input buffer must be 16-byte aligned");
+  }
+  return KRAKEN_OK;
+}
+
+// matvec_q*_k_f32_device (mps_backend.mm:6134-6197).
+int matvec_entry(kraken_hip_context* ctx, int format, const kraken_buffer& weight, size_t rows,
+                 size_t cols, const kraken_buffer& input, const kraken_buffer& output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string f = fmt_name(format);
+  if (weight.data == nullptr) {
+    return invalid("HIP " + f + " weight buffer is not initialized");
+  }
+  Layout l;
+  KRAKEN_TRY(matvec_layout(format, rows, cols, l));
+  if (weight.byte_size < l.weight_bytes) {
+    return invalid("HIP " + f + " weight buffer is too small");
+  }
+  KRAKEN_TRY(validate_f32(input, cols, (f + " matvec input").c_str()));
+  KRAKEN_TRY(validate_f32(output, rows, (f + " matvec output").c_str()));
+  KRAKEN_TRY(check_alignment(format, weight, input, "matvec"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e =
+    launch_kquant_matmul(format, weight.data, rows, cols, 1, static_cast<const float*>(input.data),
+                         static_cast<float*>(output.data), nullptr, 0, ctx->stream);
+  if (e != hipSuccess) {
+    return internal("HIP " + f + " matvec launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, ("HIP " + f + " matvec command failed: ").c_str());
+}
+
+// matvec_q*_k_f32_top1 / _argmax (mps_backend.mm:6199-6334): the logits of
+// one token, then their argmax (and the top probability for top1).
+int top1_entry(kraken_hip_context* ctx, int format, bool with_probability,
+               const kraken_buffer& weight, size_t rows, size_t cols, const kraken_buffer& input,
+               const kraken_buffer& token_output, const kraken_buffer* probability_output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string f = fmt_name(format);
+  const std::string w = with_probability ? " top1" : " argmax";
+  if (weight.data == nullptr) {
+    return invalid("HIP " + f + w + " weight buffer is not initialized");
+  }
+  Layout l;
+  KRAKEN_TRY(matvec_layout(format, rows, cols, l));
+  if (l.blocks_per_row > kTop1MaxBlocksPerRow) {
+    return invalid("HIP " + f + w + " block count exceeds kernel limit");
+  }
+  if (weight.byte_size < l.weight_bytes) {
+    return invalid("HIP " + f + w + " weight buffer is too small");
+  }
+  KRAKEN_TRY(validate_f32(input, cols, (f + w + " input").c_str()));
+  KRAKEN_TRY(validate_i32(token_output, 1, (f + w + " token output").c_str()));
+  if (with_probability) {
+    KRAKEN_TRY(validate_f32(*probability_output, 1, (f + w + " probability output").c_str()));
+  }
+  KRAKEN_TRY(check_alignment(format, weight, input, w.c_str() + 1));
+  KRAKEN_TRY(ensure_workspace(ctx, kquant_argmax_workspace_bytes(rows)));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_kquant_argmax(
+    format, weight.data, rows, cols, static_cast<const float*>(input.data),
+    static_cast<int32_t*>(token_output.data),
+    with_probability ? static_cast<float*>(probability_output->data) : nullptr, ctx->workspace,
+    ctx->workspace_bytes, ctx->stream);
+  if (e != hipSuccess) {
+    return internal("HIP " + f + w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, ("HIP " + f + w + " command failed: ").c_str());
+}
+
+// matmul_q*_k_f32_device with make_k_quant_matmul_layout (mps_backend.mm:
+// 4143-4189, 6336-6450).
+int matmul_entry(kraken_hip_context* ctx, int format, const kraken_buffer& weight, size_t rows,
+                 size_t cols, size_t tokens, const kraken_buffer& input,
+                 const kraken_buffer& output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string f = fmt_name(format);
+  const std::string p = "HIP " + f + " matmul ";
+  if (weight.data == nullptr) {
+    return invalid("HIP " + f + " weight buffer is not initialized");
+  }
+  if (rows == 0 || cols == 0 || tokens == 0) {
+    return invalid(p + "rows, cols and tokens must be greater than zero");
+  }
+  if (cols % 256u != 0) {
+    return invalid(p + "cols must be divisible by 256");
+  }
+  if (!fits_u32(cols) || !fits_u32(rows) || !fits_u32(tokens)) {
+    return invalid(p + "dimensions exceed uint32 range");
+  }
+  const size_t blocks_per_row = cols / 256u;
+  size_t total_blocks = 0;
+  size_t weight_bytes = 0;
+  if (!checked_mul(rows, blocks_per_row, total_blocks)) {
+    return invalid(p + "block count overflow");
+  }
+  if (!checked_mul(total_blocks, kquant_block_bytes(format), weight_bytes)) {
+    return invalid(p + "weight byte count overflow");
+  }
+  size_t input_values = 0;
+  size_t output_values = 0;
+  size_t bytes = 0;
+  if (!checked_mul(tokens, cols, input_values) || !checked_mul(tokens, rows, output_values) ||
+      !checked_mul(input_values, sizeof(float), bytes) ||
+      !checked_mul(output_values, sizeof(float), bytes)) {
+    return invalid(p + "buffer byte count overflow");
+  }
+  if (weight.byte_size < weight_bytes) {
+    return invalid(p + "weight buffer is too small");
+  }
+  KRAKEN_TRY(validate_f32(input, input_values, (f + " matmul input").c_str()));
+  KRAKEN_TRY(validate_f32(output, output_values, (f + " matmul output").c_str()));
+  KRAKEN_TRY(check_alignment(format, weight, input, "matmul"));
+  KRAKEN_TRY(ensure_workspace(ctx, kquant_matmul_workspace_bytes(format, rows, cols, tokens)));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_kquant_matmul(
+    format, weight.data, rows, cols, tokens, static_cast<const float*>(input.data),
+    static_cast<float*>(output.data), ctx->workspace, ctx->workspace_bytes, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(p + "launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (p + "command failed: ").c_str());
+}
+
+// dequantize_row_q*_k_f32 (mps_backend.mm:7217-7283).
+int get_row_entry(kraken_hip_context* ctx, int format, const kraken_buffer& weight, size_t row,
+                  size_t cols, const kraken_buffer& output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string f = fmt_name(format);
+  const std::string p = "HIP " + f + " get-row ";
+  if (weight.data == nullptr) {
+    return invalid(p + "weight buffer is not initialized");
+  }
+  if (cols == 0 || cols % 256u != 0) {
+    return invalid(p + "cols must be positive and divisible by 256");
+  }
+  const size_t blocks_per_row = cols / 256u;
+  size_t row_bytes = 0;
+  size_t required = 0;
+  if (row == SIZE_MAX || !checked_mul(blocks_per_row, kquant_block_bytes(format), row_bytes) ||
+      !checked_mul(row + 1u, row_bytes, required)) {
+    return invalid(p + "weight byte count overflow");
+  }
+  if (weight.byte_size < required) {
+    return invalid(p + "weight buffer is too small");
+  }
+  KRAKEN_TRY(validate_f32(output, cols, (f + " get-row output").c_str()));
+  KRAKEN_TRY(check_u32(row, (f + " get-row row").c_str()));
+  KRAKEN_TRY(check_u32(cols, (f + " get-row cols").c_str()));
+  KRAKEN_TRY(check_u32(blocks_per_row, (f + " get-row blocks").c_str()));
+  if (((uintptr_t)weight.data & (format == 2 ? 1u : 3u)) != 0 ||
+      ((uintptr_t)output.data & 15u) != 0) {
+    return invalid(p + "weight or output buffer is not aligned");
+  }
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_kquant_dequantize_rows(format, weight.data, row + 1u, nullptr, row,
+                                                     1, cols, static_cast<float*>(output.data),
+                                                     ctx->stream);
+  if (e != hipSuccess) {
+    return internal(p + "launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (p + "command failed: ").c_str());
+}
+
+// dequantize_rows_q*_k_f32 (mps_backend.mm:7285-7380): row_ids i32 [tokens].
+int get_rows_entry(kraken_hip_context* ctx, int format, const kraken_buffer& weight, size_t rows,
+                   const kraken_buffer& row_ids, size_t tokens, size_t cols,
+                   const kraken_buffer& output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string f = fmt_name(format);
+  const std::string p = "HIP " + f + " get-rows ";
+  if (weight.data == nullptr) {
+    return invalid(p + "weight buffer is not initialized");
+  }
+  if (rows == 0 || tokens == 0 || cols == 0 || cols % 256u != 0) {
+    return invalid(p + "rows, tokens and cols must be positive and cols divisible by 256");
+  }
+  const size_t blocks_per_row = cols / 256u;
+  size_t row_bytes = 0;
+  size_t required = 0;
+  if (!checked_mul(blocks_per_row, kquant_block_bytes(format), row_bytes) ||
+      !checked_mul(rows, row_bytes, required)) {
+    return invalid(p + "weight byte count overflow");
+  }
+  if (weight.byte_size < required) {
+    return invalid(p + "weight buffer is too small");
+  }
+  KRAKEN_TRY(validate_i32(row_ids, tokens, (f + " get-rows row ids").c_str()));
+  size_t total = 0;
+  if (!checked_mul(cols, tokens, total)) {
+    return invalid(p + "value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(output, total, (f + " get-rows output").c_str()));
+  KRAKEN_TRY(check_u32(rows, (f + " get-rows rows").c_str()));
+  KRAKEN_TRY(check_u32(tokens, (f + " get-rows tokens").c_str()));
+  KRAKEN_TRY(check_u32(cols, (f + " get-rows cols").c_str()));
+  if (((uintptr_t)weight.data & (format == 2 ? 1u : 3u)) != 0 ||
+      ((uintptr_t)output.data & 15u) != 0) {
+    return invalid(p + "weight or output buffer is not aligned");
+  }
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_kquant_dequantize_rows(
+    format, weight.data, rows, static_cast<const int32_t*>(row_ids.data), 0, tokens, cols,
+    static_cast<float*>(output.data), ctx->stream);
+  if (e != hipSuccess) {
+    return internal(p + "launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (p + "command failed: ").c_str());
+}
+
+// argmax_f32_i32 / argmax_prob_f32_i32 (mps_backend.mm:10004-10120).
+int argmax_entry(kraken_hip_context* ctx, bool with_probability, const kraken_buffer& values,
+                 size_t size, const kraken_buffer& token_output,
+                 const kraken_buffer* probability_output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string w = with_probability ? "argmax probability" : "argmax";
+  if (size == 0) {
+    return invalid("HIP " + w + " size must be positive");
+  }
+  KRAKEN_TRY(check_u32(size, (w + " size").c_str()));
+  KRAKEN_TRY(validate_f32(values, size, (w + " values").c_str()));
+  const std::string out = with_probability ? " token output" : " output";
+  if (token_output.data == nullptr) {
+    return invalid("HIP " + w + out + " buffer is not initialized");
+  }
+  if (token_output.byte_size < sizeof(int32_t)) {
+    return invalid("HIP " + w + out + " buffer is too small");
+  }
+  if (with_probability) {
+    KRAKEN_TRY(validate_f32(*probability_output, 1, (w + " output").c_str()));
+  }
+  KRAKEN_TRY(ensure_workspace(ctx, argmax_workspace_bytes(size)));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_argmax(
+    static_cast<const float*>(values.data), size, static_cast<int32_t*>(token_output.data),
+    with_probability ? static_cast<float*>(probability_output->data) : nullptr, ctx->workspace,
+    ctx->workspace_bytes, ctx->stream);
+  if (e != hipSuccess) {
+    return internal("HIP " + w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, ("HIP " + w + " command failed: ").c_str());
+}
+
+}  // namespace
+
+extern "C" {
+
+#define KRAKEN_KQUANT_ENTRIES(FMT, ID)                                                          \
+  KRAKEN_API int kraken_hip_matvec_##FMT##_f32_device(kraken_hip_context* ctx,                 \
+                                                      kraken_buffer weight, size_t rows,        \
+                                                      size_t cols, kraken_buffer input,         \
+                                                      kraken_buffer output) {                   \
+    return matvec_entry(ctx, ID, weight, rows, cols, input, output);                           \
+  }                                                                                            \
+  KRAKEN_API int kraken_hip_matvec_##FMT##_f32_top1(                                           \
+    kraken_hip_context* ctx, kraken_buffer weight, size_t rows, size_t cols,                   \
+    kraken_buffer input, kraken_buffer token_output, kraken_buffer probability_output) {       \
+    return top1_entry(ctx, ID, true, weight, rows, cols, input, token_output,                  \
+                      &probability_output);                                                    \
+  }                                                                                            \
+  KRAKEN_API int kraken_hip_matvec_##FMT##_f32_argmax(kraken_hip_context* ctx,                 \
+                                                      kraken_buffer weight, size_t rows,        \
+                                                      size_t cols, kraken_buffer input,         \
+                                                      kraken_buffer token_output) {             \
+    return top1_entry(ctx, ID, false, weight, rows, cols, input, token_output, nullptr);       \
+  }                                                                                            \
+  KRAKEN_API int kraken_hip_matmul_##FMT##_f32_device(                                         \
+    kraken_hip_context* ctx, kraken_buffer weight, size_t rows, size_t cols, size_t tokens,    \
+    kraken_buffer input, kraken_buffer output) {                                               \
+    return matmul_entry(ctx, ID, weight, rows, cols, tokens, input, output);                   \
+  }                                                                                            \
+  KRAKEN_API int kraken_hip_dequantize_row_##FMT##_f32(kraken_hip_context* ctx,                \
+                                                       kraken_buffer weight, size_t row,        \
+                                                       size_t cols, kraken_buffer output) {     \
+    return get_row_entry(ctx, ID, weight, row, cols, output);                                  \
+  }                                                                                            \
+  KRAKEN_API int kraken_hip_dequantize_rows_##FMT##_f32(                                       \
+    kraken_hip_context* ctx, kraken_buffer weight, size_t rows, kraken_buffer row_ids,         \
+    size_t tokens, size_t cols, kraken_buffer output) {                                        \
+    return get_rows_entry(ctx, ID, weight, rows, row_ids, tokens, cols, output);               \
+  }
+
+KRAKEN_KQUANT_ENTRIES(q4_k, 0)
+KRAKEN_KQUANT_ENTRIES(q5_k, 1)
+KRAKEN_KQUANT_ENTRIES(q6_k, 2)
+#undef KRAKEN_KQUANT_ENTRIES
+
+KRAKEN_API int kraken_hip_argmax_f32_i32(kraken_hip_context* ctx, kraken_buffer values,
+                                         size_t size, kraken_buffer output) {
+  return argmax_entry(ctx, false, values, size, output, nullptr);
+}
+
+KRAKEN_API int kraken_hip_argmax_prob_f32_i32(kraken_hip_context* ctx, kraken_buffer values,
+                                              size_t size, kraken_buffer token_output,
+                                              kraken_buffer probability_output) {
+  return argmax_entry(ctx, true, values, size, token_output, &probability_output);
+}
+
+}  // extern "C"

@@ -268,6 +268,33 @@ struct PrologueArgs {
 };
 hipError_t launch_attention_prologue(const PrologueArgs& a, hipStream_t stream);
 
+// K-quant projections (kquant.hip).  format: 0 = Q4_K, 1 = Q5_K, 2 = Q6_K;
+// weights are row-major blocks (cols / 256 per row).  Up to
+// kKquantGemvMaxTokens tokens take the fp32 GEMV; more take the fp16 MFMA
+// GEMM, which stages fp16 weights and inputs in the workspace.
+constexpr size_t kKquantGemvMaxTokens = 8;
+uint32_t kquant_block_bytes(int format);
+size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens);
+hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, size_t cols,
+                                size_t tokens, const float* input, float* output,
+                                void* workspace, size_t workspace_bytes, hipStream_t stream);
+// Rows row_ids[t] (or fixed_row when row_ids is null, tokens = 1) dequantized
+// into output [tokens][cols]; ids outside [0, rows) give zero rows.
+hipError_t launch_kquant_dequantize_rows(int format, const void* weight, size_t rows,
+                                         const int32_t* row_ids, size_t fixed_row,
+                                         size_t tokens, size_t cols, float* output,
+                                         hipStream_t stream);
+// argmax (probability_out null) or argmax with probability over `size` values.
+size_t argmax_workspace_bytes(size_t size);
+hipError_t launch_argmax(const float* values, size_t size, int32_t* token_out,
+                         float* probability_out, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
+// GEMV of one token into workspace logits, then argmax (and probability).
+size_t kquant_argmax_workspace_bytes(size_t rows);
+hipError_t launch_kquant_argmax(int format, const void* weight, size_t rows, size_t cols,
+                                const float* input, int32_t* token_out, float* probability_out,
+                                void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 hipError_t launch_rms_norm_heads(float* values, const float* weight, const float* gate,
                                  uint32_t tokens, uint32_t heads, uint32_t head_dim,
                                  float eps, hipStream_t stream);

@@ -1,0 +1,858 @@
+// K-quant (GGUF Q4_K / Q5_K / Q6_K) projections, dequantization and device
+// argmax for gfx950.
+//
+// Semantics (reference Metal kernels, mps_backend.mm):
+//  * matvec / few-token matmul (q*_k_matvec :295-460, q*_k_matmul
+//    :1268-1440): out[t][r] = sum_c w[r][c] x[t][c] in fp32, with w
+//    dequantized in fp32 ((d*sc)*q - dmin*m for Q4_K/Q5_K, (d*sc)*(q-32) for
+//    Q6_K);
+//  * many-token matmul (q*_k_mul_mm_simd :1082-1266): weights and inputs
+//    rounded to fp16, fp32 accumulation;
+//  * get_row / get_rows (:1448-1540, 1693-1825): dequantized rows, zeros for
+//    row ids outside the matrix;
+//  * argmax_f32_i32 / argmax_prob_f32_i32 (:2681-2779) and the top1/argmax
+//    matvecs (:466-740, 1546-1690): first index of the maximum (NaN never
+//    wins), probability 1 / sum exp(v - max).
+// Block layouts are spelled out in oracle/kquant_oracle.c's header.
+//
+// Design (wave64):
+//  * Every kernel decodes weights in units of one 16-byte quant chunk per lane:
+//    8 lanes cover a 256-value block, a lane's chunk holds 32 quants, 16 of
+//    each of two sub-blocks (Q4_K/Q5_K) or quarter-halves (Q6_K).  Nibbles are
+//    split four at a time with masks on 32-bit words and converted with the
+//    byte-to-float conversions; the Q5_K and Q6_K high bits are merged into the
+//    same words before conversion.
+//  * GEMV (1..8 tokens): a row is spread over 8 * BC lanes (BC blocks at a
+//    time), a 64-lane wave holds 64 / (8 BC) rows, so every lane issues one
+//    16-byte load per block for the quants; the fp32 input stays in the CU's
+//    L1.  Partial sums reduce over the row's lanes with DPP and lane swaps.
+//  * Many tokens: the weights are dequantized to fp16 and the inputs rounded to
+//    fp16 in two streaming passes, then an fp16 MFMA GEMM (v_mfma_f32_32x32x16_f16,
+//    128 x 128 output tile per 4-wave workgroup, 64-deep K steps double-
+//    buffered through LDS with XOR-swizzled 16-byte chunks) writes
+//    [tokens][rows] in fp32.
+//  * argmax: per-workgroup (max, first index, sum of exp) candidates, merged by
+//    one workgroup; sizes that fit one workgroup take a single launch.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "context_internal.hpp"
+#include "device_common.hpp"
+
+namespace kraken {
+namespace {
+
+template <int F>
+struct KqFormat;
+template <>
+struct KqFormat<0> {  // Q4_K
+  static constexpr uint32_t kBytes = 144;
+};
+template <>
+struct KqFormat<1> {  // Q5_K
+  static constexpr uint32_t kBytes = 176;
+};
+template <>
+struct KqFormat<2> {  // Q6_K
+  static constexpr uint32_t kBytes = 210;
+};
+
+// A value the compiler must treat as opaque: no instruction is emitted, but an
+// expression cannot be fused across it (a multiply into an FMA, or an
+// arithmetic result and its fp16 conversion into one v_fma_mix rounding).
+__device__ __forceinline__ float rounded(float v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+  return static_cast<float>(__builtin_bit_cast(half_t, (uint16_t)(bits & 0xFFFFu)));
+}
+
+__device__ __forceinline__ uint32_t byte_of(const u32x4_t& w, uint32_t k) {
+  const uint32_t word = k < 4 ? w.x : (k < 8 ? w.y : (k < 12 ? w.z : w.w));
+  return (word >> (8u * (k & 3u))) & 0xFFu;
+}
+
+// The 6-bit scale and min of sub-block j from the 12 scale bytes held in
+// header bytes 4..15 (mps_backend.mm:284-293).
+__device__ __forceinline__ void scale_min(const u32x4_t& hdr, uint32_t j, uint32_t& sc,
+                                          uint32_t& m) {
+  if (j < 4) {
+    sc = byte_of(hdr, 4 + j) & 63u;
+    m = byte_of(hdr, 8 + j) & 63u;
+  } else {
+    sc = (byte_of(hdr, 12 + j - 4) & 0xFu) | ((byte_of(hdr, 4 + j - 4) >> 6) << 4);
+    m = (byte_of(hdr, 12 + j - 4) >> 4) | ((byte_of(hdr, 4 + j) >> 6) << 4);
+  }
+}
+
+// Four bytes of a word as floats (the compiler selects v_cvt_f32_ubyte0..3).
+__device__ __forceinline__ void bytes_to_float(uint32_t w, float* out) {
+  out[0] = (float)(w & 0xFFu);
+  out[1] = (float)((w >> 8) & 0xFFu);
+  out[2] = (float)((w >> 16) & 0xFFu);
+  out[3] = (float)(w >> 24);
+}
+
+// The 16 bytes at `offset` (even) from the 4-byte-aligned `base`, read as
+// aligned dwords and shifted by the misalignment (0 or 2 bytes), so Q6_K's
+// 210-byte blocks need no unaligned access.  An aligned chunk re-reads its
+// last dword instead of the one after it, so no byte past the chunk is read.
+__device__ __forceinline__ u32x4_t load16_even(const uint8_t* base, uint64_t offset) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(base + (offset & ~(uint64_t)3));
+  const uint32_t shift = (uint32_t)(offset & 3u);
+  const uint32_t w0 = __builtin_nontemporal_load(p);
+  const uint32_t w1 = __builtin_nontemporal_load(p + 1);
+  const uint32_t w2 = __builtin_nontemporal_load(p + 2);
+  const uint32_t w3 = __builtin_nontemporal_load(p + 3);
+  const uint32_t w4 = __builtin_nontemporal_load(p + (shift != 0u ? 4 : 3));
+  u32x4_t r;
+  r.x = __builtin_amdgcn_alignbyte(w1, w0, shift);
+  r.y = __builtin_amdgcn_alignbyte(w2, w1, shift);
+  r.z = __builtin_amdgcn_alignbyte(w3, w2, shift);
+  r.w = __builtin_amdgcn_alignbyte(w4, w3, shift);
+  return r;
+}
+
+// One lane's share of a block: chunk c (0..7) holds 32 quants, dequantized
+// into v0 (block positions p0 .. p0 + 15) and v1 (p1 .. p1 + 15).  With
+// kExact the arithmetic is the reference's, operation for operation (no
+// contraction), so dequantized rows are bit-identical to the oracle.
+template <int F, bool kExact>
+struct ChunkDecoder {
+  float v0[16], v1[16];
+  uint32_t p0, p1;
+
+  __device__ __forceinline__ void decode(const uint8_t* block, uint32_t c) {
+    if constexpr (F == 2) {
+      decode_q6(block, c);
+    } else {
+      decode_q45(block, c);
+    }
+  }
+
+  __device__ __forceinline__ static float axpy(float a, float x, float b) {
+    if constexpr (kExact) {
+      // a * x - b with two roundings, as the reference writes it, and the
+      // f32 result kept as such before any later fp16 conversion.
+      return rounded(rounded(a * x) - b);
+    } else {
+      return fmaf(a, x, -b);
+    }
+  }
+
+  __device__ __forceinline__ void decode_q45(const uint8_t* block, uint32_t c) {
+    const u32x4_t hdr = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(block));
+    const uint32_t qs_at = F == 1 ? 48u : 16u;
+    const u32x4_t qs =
+      __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(block + qs_at + 16u * c));
+    u32x4_t qh = {0u, 0u, 0u, 0u};
+    if constexpr (F == 1) {
+      qh = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t*>(block + 16u + 16u * (c & 1u)));
+    }
+    const uint32_t s = c >> 1;
+    p0 = 64u * s + 16u * (c & 1u);
+    p1 = p0 + 32u;
+    uint32_t sc0, m0, sc1, m1;
+    scale_min(hdr, 2u * s, sc0, m0);
+    scale_min(hdr, 2u * s + 1u, sc1, m1);
+    const float d = half_bits_to_float(hdr.x);
+    const float dmin = half_bits_to_float(hdr.x >> 16);
+    float ds0, ms0, ds1, ms1;
+    if constexpr (kExact) {
+      ds0 = rounded(d * (float)sc0);
+      ms0 = rounded(dmin * (float)m0);
+      ds1 = rounded(d * (float)sc1);
+      ms1 = rounded(dmin * (float)m1);
+    } else {
+      ds0 = d * (float)sc0;
+      ms0 = dmin * (float)m0;
+      ds1 = d * (float)sc1;
+      ms1 = dmin * (float)m1;
+    }
+    const uint32_t words[4] = {qs.x, qs.y, qs.z, qs.w};
+    const uint32_t hwords[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t lo = words[k] & 0x0F0F0F0Fu;
+      uint32_t hi = (words[k] >> 4) & 0x0F0F0F0Fu;
+      if constexpr (F == 1) {
+        lo |= ((hwords[k] >> (2u * s)) & 0x01010101u) << 4;
+        hi |= ((hwords[k] >> (2u * s + 1u)) & 0x01010101u) << 4;
+      }
+      float ql[4], qhf[4];
+      bytes_to_float(lo, ql);
+      bytes_to_float(hi, qhf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v0[4 * k + e] = axpy(ds0, ql[e], ms0);
+        v1[4 * k + e] = axpy(ds1, qhf[e], ms1);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void decode_q6(const uint8_t* block, uint32_t c) {
+    const uint64_t base = (uint64_t)(uintptr_t)block;
+    const uint8_t* b0 = reinterpret_cast<const uint8_t*>(base & ~(uint64_t)3);
+    const uint64_t mis = base & 3u;
+    const uint32_t h = c >> 2;
+    const uint32_t c4 = c & 3u;
+    const uint32_t g = c4 >> 1;
+    const uint32_t half = c4 & 1u;
+    const u32x4_t ql = load16_even(b0, mis + 16u * c);
+    const u32x4_t qh = load16_even(b0, mis + 128u + 32u * h + 16u * half);
+    const u32x4_t sc = load16_even(b0, mis + 192u);
+    const float d = half_bits_to_float(
+      __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(block + 208u)));
+    const int s_lo = (int8_t)byte_of(sc, 8u * h + 2u * g + half);
+    const int s_hi = (int8_t)byte_of(sc, 8u * h + 4u + 2u * g + half);
+    float dl, dh;
+    if constexpr (kExact) {
+      dl = rounded(d * (float)s_lo);
+      dh = rounded(d * (float)s_hi);
+    } else {
+      dl = d * (float)s_lo;
+      dh = d * (float)s_hi;
+    }
+    p0 = 128u * h + 32u * g + 16u * half;
+    p1 = p0 + 64u;
+    const uint32_t words[4] = {ql.x, ql.y, ql.z, ql.w};
+    const uint32_t hwords[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = (words[k] & 0x0F0F0F0Fu) | (((hwords[k] >> (2u * g)) & 0x03030303u) << 4);
+      const uint32_t hi =
+        ((words[k] >> 4) & 0x0F0F0F0Fu) | (((hwords[k] >> (2u * g + 4u)) & 0x03030303u) << 4);
+      float ql4[4], qh4[4];
+      bytes_to_float(lo, ql4);
+      bytes_to_float(hi, qh4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // (d * sc) * (q - 32); q - 32 is exact.
+        if constexpr (kExact) {
+          v0[4 * k + e] = rounded(dl * (ql4[e] - 32.0f));
+          v1[4 * k + e] = rounded(dh * (qh4[e] - 32.0f));
+        } else {
+          v0[4 * k + e] = dl * (ql4[e] - 32.0f);
+          v1[4 * k + e] = dh * (qh4[e] - 32.0f);
+        }
+      }
+    }
+  }
+};
+
+// Sum over an aligned group of R lanes (R = 8, 16, 32 or 64); result in all.
+template <int R>
+__device__ __forceinline__ float group_sum(float x) {
+  x = reduce8_sum(x);
+  if constexpr (R >= 16) {
+    x += dpp<kDppRowMirror>(x);
+  }
+  if constexpr (R >= 32) {
+    x = xor16_sum(x);
+  }
+  if constexpr (R >= 64) {
+    x = xor32_sum(x);
+  }
+  return x;
+}
+
+struct GemvArgs {
+  const uint8_t* weight;
+  const float* input;  // [tokens][cols]
+  float* output;       // [tokens][rows]
+  uint32_t rows, cols, blocks_per_row, tokens;
+  uint32_t token_base;  // first token of this launch's group
+  uint32_t round_f16;   // weights rounded to fp16 before the products
+};
+
+// GEMV over a group of TG tokens (tokens past `tokens` are computed on token
+// 0's input and not stored).  One wave per workgroup: rows spread over
+// 64 / (8 BC) row slots.
+template <int F, int BC, int TG>
+__global__ __launch_bounds__(64) void kq_gemv_kernel(GemvArgs a) {
+  constexpr int LR = 8 * BC;
+  constexpr int RW = 64 / LR;
+  const int lane = threadIdx.x;
+  const uint32_t row_slot = (uint32_t)(lane / LR);
+  const uint32_t row = blockIdx.x * RW + row_slot;
+  const bool row_ok = row < a.rows;
+  const uint32_t r = row_ok ? row : a.rows - 1u;
+  const uint32_t bl = (uint32_t)((lane % LR) / 8);
+  const uint32_t c = (uint32_t)(lane & 7);
+  const uint8_t* row_ptr = a.weight + (uint64_t)r * a.blocks_per_row * KqFormat<F>::kBytes;
+  const float* xin[TG];
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+    const uint32_t tok = a.token_base + t;
+    xin[t] = a.input + (uint64_t)(tok < a.tokens ? tok : 0u) * a.cols;
+  }
+  float acc[TG];
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+    acc[t] = 0.0f;
+  }
+  for (uint32_t b = bl; b < a.blocks_per_row; b += BC) {
+    ChunkDecoder<F, false> dec;
+    dec.decode(row_ptr + (uint64_t)b * KqFormat<F>::kBytes, c);
+    if (a.round_f16 != 0u) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        dec.v0[i] = static_cast<float>(static_cast<half_t>(rounded(dec.v0[i])));
+        dec.v1[i] = static_cast<float>(static_cast<half_t>(rounded(dec.v1[i])));
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TG; ++t) {
+      const float4* x0 = reinterpret_cast<const float4*>(xin[t] + 256u * b + dec.p0);
+      const float4* x1 = reinterpret_cast<const float4*>(xin[t] + 256u * b + dec.p1);
+      float s = acc[t];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 u = x0[q];
+        const float4 v = x1[q];
+        s = fmaf(dec.v0[4 * q + 0], u.x, s);
+        s = fmaf(dec.v0[4 * q + 1], u.y, s);
+        s = fmaf(dec.v0[4 * q + 2], u.z, s);
+        s = fmaf(dec.v0[4 * q + 3], u.w, s);
+        s = fmaf(dec.v1[4 * q + 0], v.x, s);
+        s = fmaf(dec.v1[4 * q + 1], v.y, s);
+        s = fmaf(dec.v1[4 * q + 2], v.z, s);
+        s = fmaf(dec.v1[4 * q + 3], v.w, s);
+      }
+      acc[t] = s;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+    const float total = group_sum<LR>(acc[t]);
+    const uint32_t tok = a.token_base + t;
+    if (row_ok && (lane % LR) == 0 && tok < a.tokens) {
+      a.output[(uint64_t)tok * a.rows + row] = total;
+    }
+  }
+}
+
+// Dequantized rows (get_row / get_rows): one lane per 16-byte chunk, exact
+// reference arithmetic.  Row ids outside [0, rows) give zeros.
+template <int F>
+__global__ __launch_bounds__(256) void kq_dequant_rows_kernel(const uint8_t* weight,
+                                                              const int32_t* row_ids,
+                                                              uint32_t fixed_row, uint32_t rows,
+                                                              uint32_t tokens,
+                                                              uint32_t blocks_per_row,
+                                                              float* output) {
+  const uint64_t id = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  const uint64_t per_token = (uint64_t)blocks_per_row * 8u;
+  if (id >= per_token * tokens) {
+    return;
+  }
+  const uint32_t token = (uint32_t)(id / per_token);
+  const uint32_t within = (uint32_t)(id % per_token);
+  const uint32_t b = within / 8u;
+  const uint32_t c = within % 8u;
+  float* out = output + (uint64_t)token * blocks_per_row * 256u + 256u * b;
+  const int64_t row = row_ids != nullptr ? (int64_t)row_ids[token] : (int64_t)fixed_row;
+  ChunkDecoder<F, true> dec;
+  if (row < 0 || row >= (int64_t)rows) {
+    // Positions of this chunk's values, without touching the weights.
+    dec.p0 = F == 2 ? 128u * (c >> 2) + 32u * ((c & 3u) >> 1) + 16u * (c & 1u)
+                    : 64u * (c >> 1) + 16u * (c & 1u);
+    dec.p1 = dec.p0 + (F == 2 ? 64u : 32u);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      dec.v0[j] = 0.0f;
+      dec.v1[j] = 0.0f;
+    }
+  } else {
+    dec.decode(weight + ((uint64_t)row * blocks_per_row + b) * KqFormat<F>::kBytes, c);
+  }
+  float4* o0 = reinterpret_cast<float4*>(out + dec.p0);
+  float4* o1 = reinterpret_cast<float4*>(out + dec.p1);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    o0[q] = make_float4(dec.v0[4 * q], dec.v0[4 * q + 1], dec.v0[4 * q + 2], dec.v0[4 * q + 3]);
+    o1[q] = make_float4(dec.v1[4 * q], dec.v1[4 * q + 1], dec.v1[4 * q + 2], dec.v1[4 * q + 3]);
+  }
+}
+
+// Weights dequantized and rounded to fp16 (RNE) for the MFMA GEMM, [rows][cols].
+template <int F>
+__global__ __launch_bounds__(256) void kq_dequant_f16_kernel(const uint8_t* weight, uint32_t rows,
+                                                             uint32_t blocks_per_row,
+                                                             half_t* out) {
+  const uint64_t id = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  const uint64_t chunks = (uint64_t)rows * blocks_per_row * 8u;
+  if (id >= chunks) {
+    return;
+  }
+  const uint64_t blk = id / 8u;
+  const uint32_t c = (uint32_t)(id % 8u);
+  ChunkDecoder<F, true> dec;
+  dec.decode(weight + blk * KqFormat<F>::kBytes, c);
+  half_t* o = out + blk * 256u;
+  half8_t h0, h1;
+#pragma unroll
+  for (int half_i = 0; half_i < 2; ++half_i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      h0[j] = static_cast<half_t>(dec.v0[8 * half_i + j]);
+      h1[j] = static_cast<half_t>(dec.v1[8 * half_i + j]);
+    }
+    *reinterpret_cast<half8_t*>(o + dec.p0 + 8 * half_i) = h0;
+    *reinterpret_cast<half8_t*>(o + dec.p1 + 8 * half_i) = h1;
+  }
+}
+
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* in, half_t* out,
+                                                         uint64_t n8) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i >= n8) {
+    return;
+  }
+  const float4 a = reinterpret_cast<const float4*>(in)[2 * i];
+  const float4 b = reinterpret_cast<const float4*>(in)[2 * i + 1];
+  const half8_t h = {static_cast<half_t>(a.x), static_cast<half_t>(a.y), static_cast<half_t>(a.z),
+                     static_cast<half_t>(a.w), static_cast<half_t>(b.x), static_cast<half_t>(b.y),
+                     static_cast<half_t>(b.z), static_cast<half_t>(b.w)};
+  reinterpret_cast<half8_t*>(out)[i] = h;
+}
+
+// ------------------------------------------------------------------ GEMM ----
+// C[t][r] = sum_k X[t][k] W[r][k] with X [M = tokens][K], W [N = rows][K] fp16
+// (both K-contiguous), C fp32 [M][N].  128 x 128 tile per workgroup of four
+// waves; wave w owns tokens 64 (w / 2) .. + 63 and rows 64 (w % 2) .. + 63 as
+// 2 x 2 tiles of v_mfma_f32_32x32x16_f16.  K steps of 64 through two LDS
+// stages; a 16-byte chunk j of tile row i lives at chunk j ^ (i & 7), so the
+// fragment reads (32 rows, one chunk each) hit distinct banks.
+constexpr int kGM = 128, kGN = 128, kGK = 64;
+typedef float float16v_t __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const half_t* w,
+                                                          float* c, uint32_t m, uint32_t n,
+                                                          uint32_t k) {
+  __shared__ __attribute__((aligned(16))) half_t s_a[2][kGM * kGK];
+  __shared__ __attribute__((aligned(16))) half_t s_b[2][kGN * kGK];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint32_t m0 = blockIdx.y * kGM;
+  const uint32_t n0 = blockIdx.x * kGN;
+  // Range-checked operands: rows past the matrix read as zeros.
+  const __amdgpu_buffer_rsrc_t xr =
+    make_buffer_rsrc(x + (uint64_t)m0 * k, (uint32_t)min((uint64_t)kGM, (uint64_t)(m - m0)) * k * 2u);
+  const __amdgpu_buffer_rsrc_t wr =
+    make_buffer_rsrc(w + (uint64_t)n0 * k, (uint32_t)min((uint64_t)kGN, (uint64_t)(n - n0)) * k * 2u);
+  // Global -> register staging: thread t moves chunks t + 256 i (i < 4) of
+  // each 128 x 64 tile (row = idx / 8, chunk = idx % 8).
+  u32x4_t ra[4], rb[4];
+  auto load_step = [&](uint32_t kk) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      const uint32_t row = (uint32_t)(idx >> 3);
+      const uint32_t off = (row * k + kk + 8u * (uint32_t)(idx & 7)) * 2u;
+      ra[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
+      rb[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)off, 0, 0));
+    }
+  };
+  auto store_step = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      const int row = idx >> 3;
+      const int chunk = (idx & 7) ^ (row & 7);
+      *reinterpret_cast<u32x4_t*>(&s_a[st][row * kGK + 8 * chunk]) = ra[i];
+      *reinterpret_cast<u32x4_t*>(&s_b[st][row * kGK + 8 * chunk]) = rb[i];
+    }
+  };
+  float16v_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        acc[i][j][e] = 0.0f;
+      }
+    }
+  }
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int frow = lane & 31;
+  const int fk = lane >> 5;
+  load_step(0);
+  store_step(0);
+  __syncthreads();
+  const uint32_t steps = k / kGK;
+  for (uint32_t s = 0; s < steps; ++s) {
+    const int st = (int)(s & 1u);
+    if (s + 1 < steps) {
+      load_step((s + 1) * kGK);
+    }
+#pragma unroll
+    for (int ks = 0; ks < kGK / 16; ++ks) {
+      half8_t fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = 64 * wm + 32 * i + frow;
+        const int chunk = (2 * ks + fk) ^ (row & 7);
+        fa[i] = *reinterpret_cast<const half8_t*>(&s_a[st][row * kGK + 8 * chunk]);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int row = 64 * wn + 32 * j + frow;
+        const int chunk = (2 * ks + fk) ^ (row & 7);
+        fb[j] = *reinterpret_cast<const half8_t*>(&s_b[st][row * kGK + 8 * chunk]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    if (s + 1 < steps) {
+      store_step(st ^ 1);
+    }
+    __syncthreads();
+  }
+  // D layout: lane l holds column (row of W) l % 32 and tokens
+  // 8 (e / 4) + 4 (l / 32) + e % 4 of its 32 x 32 tile.
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t col = n0 + 64u * wn + 32u * j + (uint32_t)frow;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t row = m0 + 64u * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
+        if (row < m && col < n) {
+          c[(uint64_t)row * n + col] = acc[i][j][e];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- argmax ----
+struct ArgCand {
+  float value;
+  uint32_t index;
+  float sum;  // sum of exp(v - value) over the candidate's range
+};
+
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// Candidate of [begin, end) of `values`, reduced over a 256-thread workgroup.
+// `with_sum` adds the range's sum of exp(v - max).
+__device__ ArgCand block_candidate(const float* values, uint64_t begin, uint64_t end,
+                                   uint32_t size_marker, bool with_sum) {
+  __shared__ float s_v[256];
+  __shared__ uint32_t s_i[256];
+  __shared__ float s_s[256];
+  const int tid = threadIdx.x;
+  float bv = -INFINITY;
+  uint32_t bi = size_marker;
+  for (uint64_t i = begin + tid; i < end; i += 256) {
+    const float v = values[i];
+    if (better(v, (uint32_t)i, bv, bi)) {
+      bv = v;
+      bi = (uint32_t)i;
+    }
+  }
+  s_v[tid] = bv;
+  s_i[tid] = bi;
+  __syncthreads();
+  for (int stride = 128; stride > 0; stride >>= 1) {
+    if (tid < stride && better(s_v[tid + stride], s_i[tid + stride], s_v[tid], s_i[tid])) {
+      s_v[tid] = s_v[tid + stride];
+      s_i[tid] = s_i[tid + stride];
+    }
+    __syncthreads();
+  }
+  ArgCand r{s_v[0], s_i[0], 0.0f};
+  if (with_sum) {
+    // A range whose values are all -inf or NaN has r.value == -inf; its -inf
+    // entries count 0 (they add exp(-inf) to any finite overall maximum) and
+    // its NaNs stay NaN, so the merged sum is what one pass would give.
+    float sum = 0.0f;
+    for (uint64_t i = begin + tid; i < end; i += 256) {
+      const float v = values[i];
+      sum += (v == -INFINITY && r.value == -INFINITY) ? 0.0f : expf(v - r.value);
+    }
+    s_s[tid] = sum;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+      if (tid < stride) {
+        s_s[tid] += s_s[tid + stride];
+      }
+      __syncthreads();
+    }
+    r.sum = s_s[0];
+  }
+  __syncthreads();
+  return r;
+}
+
+// Phase 1: workgroup g takes [g * span, (g + 1) * span).
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* values, uint64_t size,
+                                                             uint64_t span, bool with_sum,
+                                                             ArgCand* cands) {
+  const uint64_t begin = (uint64_t)blockIdx.x * span;
+  const uint64_t end = min(size, begin + span);
+  const ArgCand r = block_candidate(values, begin, end, (uint32_t)size, with_sum);
+  if (threadIdx.x == 0) {
+    cands[blockIdx.x] = r;
+  }
+}
+
+// Phase 2 (or the whole job when cands == nullptr): merges candidates.
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float* values, uint64_t size,
+                                                           const ArgCand* cands, uint32_t count,
+                                                           bool with_sum, int32_t* token_out,
+                                                           float* probability_out) {
+  __shared__ float s_v[256];
+  __shared__ uint32_t s_i[256];
+  __shared__ float s_s[256];
+  const int tid = threadIdx.x;
+  if (cands == nullptr) {
+    const ArgCand r = block_candidate(values, 0, size, (uint32_t)size, with_sum);
+    if (tid == 0) {
+      token_out[0] = (int32_t)r.index;
+      if (probability_out != nullptr) {
+        probability_out[0] = r.sum > 0.0f ? 1.0f / r.sum : 0.0f;
+      }
+    }
+    return;
+  }
+  float bv = -INFINITY;
+  uint32_t bi = (uint32_t)size;
+  for (uint32_t g = tid; g < count; g += 256) {
+    if (better(cands[g].value, cands[g].index, bv, bi)) {
+      bv = cands[g].value;
+      bi = cands[g].index;
+    }
+  }
+  s_v[tid] = bv;
+  s_i[tid] = bi;
+  __syncthreads();
+  for (int stride = 128; stride > 0; stride >>= 1) {
+    if (tid < stride && better(s_v[tid + stride], s_i[tid + stride], s_v[tid], s_i[tid])) {
+      s_v[tid] = s_v[tid + stride];
+      s_i[tid] = s_i[tid + stride];
+    }
+    __syncthreads();
+  }
+  const float gmax = s_v[0];
+  const uint32_t gidx = s_i[0];
+  if (with_sum) {
+    float sum = 0.0f;
+    for (uint32_t g = tid; g < count; g += 256) {
+      sum += cands[g].sum * expf(cands[g].value - gmax);
+    }
+    s_s[tid] = sum;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+      if (tid < stride) {
+        s_s[tid] += s_s[tid + stride];
+      }
+      __syncthreads();
+    }
+  }
+  if (tid == 0) {
+    token_out[0] = (int32_t)gidx;
+    if (probability_out != nullptr) {
+      probability_out[0] = s_s[0] > 0.0f ? 1.0f / s_s[0] : 0.0f;
+    }
+  }
+}
+
+constexpr uint64_t kArgmaxSingleMax = 16384;  // one workgroup up to this size
+constexpr uint64_t kArgmaxSpan = 4096;        // values per phase-1 workgroup
+
+template <int F>
+hipError_t launch_gemv_f(const GemvArgs& base, hipStream_t stream) {
+  const uint32_t bpr = base.blocks_per_row;
+  const int bc = bpr >= 5 ? 8 : (bpr >= 3 ? 4 : (bpr == 2 ? 2 : 1));
+  const uint32_t rows_per_wg = 64u / (8u * (uint32_t)bc);
+  const dim3 grid((base.rows + rows_per_wg - 1) / rows_per_wg);
+  for (uint32_t t0 = 0; t0 < base.tokens;) {
+    GemvArgs a = base;
+    a.token_base = t0;
+    const uint32_t left = base.tokens - t0;
+    const int tg = left >= 8 ? 8 : (left >= 4 ? 4 : (left >= 2 ? 2 : 1));
+#define KQ_GEMV_CASE(BC, TG) \
+  if (bc == BC && tg == TG) kq_gemv_kernel<F, BC, TG><<<grid, 64, 0, stream>>>(a);
+#define KQ_GEMV_BC(BC) KQ_GEMV_CASE(BC, 1) KQ_GEMV_CASE(BC, 2) KQ_GEMV_CASE(BC, 4) KQ_GEMV_CASE(BC, 8)
+    KQ_GEMV_BC(1) KQ_GEMV_BC(2) KQ_GEMV_BC(4) KQ_GEMV_BC(8)
+#undef KQ_GEMV_BC
+#undef KQ_GEMV_CASE
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      return e;
+    }
+    t0 += (uint32_t)tg;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_gemv(int format, const GemvArgs& a, hipStream_t stream) {
+  switch (format) {
+    case 0:
+      return launch_gemv_f<0>(a, stream);
+    case 1:
+      return launch_gemv_f<1>(a, stream);
+    case 2:
+      return launch_gemv_f<2>(a, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+size_t align256(size_t v) { return (v + 255u) & ~static_cast<size_t>(255u); }
+
+}  // namespace
+
+uint32_t kquant_block_bytes(int format) {
+  return format == 0 ? 144u : (format == 1 ? 176u : (format == 2 ? 210u : 0u));
+}
+
+size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens) {
+  (void)format;
+  if (tokens <= kKquantGemvMaxTokens) {
+    return 0;
+  }
+  return align256(rows * cols * 2u) + align256(tokens * cols * 2u);
+}
+
+hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, size_t cols,
+                                size_t tokens, const float* input, float* output,
+                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const uint32_t bpr = (uint32_t)(cols / 256u);
+  if (tokens <= kKquantGemvMaxTokens) {
+    // The reference's batched matvec (4 to 8 tokens) multiplies fp16-rounded
+    // weights with fp32 inputs; 1 to 3 tokens stay fp32 throughout.
+    GemvArgs a{static_cast<const uint8_t*>(weight), input, output, (uint32_t)rows,
+               (uint32_t)cols, bpr, (uint32_t)tokens, 0u, tokens >= 4u ? 1u : 0u};
+    return launch_gemv(format, a, stream);
+  }
+  if (workspace == nullptr ||
+      workspace_bytes < kquant_matmul_workspace_bytes(format, rows, cols, tokens)) {
+    return hipErrorInvalidValue;
+  }
+  half_t* w16 = static_cast<half_t*>(workspace);
+  half_t* x16 = reinterpret_cast<half_t*>(static_cast<char*>(workspace) +
+                                          align256(rows * cols * 2u));
+  const uint64_t chunks = (uint64_t)rows * bpr * 8u;
+  const dim3 dq((uint32_t)((chunks + 255) / 256));
+  const uint8_t* wq = static_cast<const uint8_t*>(weight);
+  if (format == 0) {
+    kq_dequant_f16_kernel<0><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
+  } else if (format == 1) {
+    kq_dequant_f16_kernel<1><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
+  } else {
+    kq_dequant_f16_kernel<2><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    return e;
+  }
+  const uint64_t n8 = (uint64_t)tokens * cols / 8u;
+  f32_to_f16_kernel<<<dim3((uint32_t)((n8 + 255) / 256)), 256, 0, stream>>>(input, x16, n8);
+  if ((e = hipGetLastError()) != hipSuccess) {
+    return e;
+  }
+  const dim3 grid((uint32_t)((rows + kGN - 1) / kGN), (uint32_t)((tokens + kGM - 1) / kGM));
+  gemm_f16_nt_kernel<<<grid, 256, 0, stream>>>(x16, w16, output, (uint32_t)tokens,
+                                               (uint32_t)rows, (uint32_t)cols);
+  return hipGetLastError();
+}
+
+hipError_t launch_kquant_dequantize_rows(int format, const void* weight, size_t rows,
+                                         const int32_t* row_ids, size_t fixed_row,
+                                         size_t tokens, size_t cols, float* output,
+                                         hipStream_t stream) {
+  const uint32_t bpr = (uint32_t)(cols / 256u);
+  const uint64_t threads = (uint64_t)tokens * bpr * 8u;
+  const dim3 grid((uint32_t)((threads + 255) / 256));
+  const uint8_t* w = static_cast<const uint8_t*>(weight);
+  if (format == 0) {
+    kq_dequant_rows_kernel<0><<<grid, 256, 0, stream>>>(w, row_ids, (uint32_t)fixed_row,
+                                                        (uint32_t)rows, (uint32_t)tokens, bpr,
+                                                        output);
+  } else if (format == 1) {
+    kq_dequant_rows_kernel<1><<<grid, 256, 0, stream>>>(w, row_ids, (uint32_t)fixed_row,
+                                                        (uint32_t)rows, (uint32_t)tokens, bpr,
+                                                        output);
+  } else {
+    kq_dequant_rows_kernel<2><<<grid, 256, 0, stream>>>(w, row_ids, (uint32_t)fixed_row,
+                                                        (uint32_t)rows, (uint32_t)tokens, bpr,
+                                                        output);
+  }
+  return hipGetLastError();
+}
+
+size_t argmax_workspace_bytes(size_t size) {
+  if (size <= kArgmaxSingleMax) {
+    return 0;
+  }
+  const size_t groups = (size + kArgmaxSpan - 1) / kArgmaxSpan;
+  return groups * sizeof(ArgCand);
+}
+
+hipError_t launch_argmax(const float* values, size_t size, int32_t* token_out,
+                         float* probability_out, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
+  const bool with_sum = probability_out != nullptr;
+  if (size <= kArgmaxSingleMax) {
+    argmax_final_kernel<<<1, 256, 0, stream>>>(values, size, nullptr, 0, with_sum, token_out,
+                                               probability_out);
+    return hipGetLastError();
+  }
+  const size_t groups = (size + kArgmaxSpan - 1) / kArgmaxSpan;
+  if (workspace == nullptr || workspace_bytes < groups * sizeof(ArgCand)) {
+    return hipErrorInvalidValue;
+  }
+  ArgCand* cands = static_cast<ArgCand*>(workspace);
+  argmax_partial_kernel<<<dim3((uint32_t)groups), 256, 0, stream>>>(values, size, kArgmaxSpan,
+                                                                    with_sum, cands);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    return e;
+  }
+  argmax_final_kernel<<<1, 256, 0, stream>>>(values, size, cands, (uint32_t)groups, with_sum,
+                                             token_out, probability_out);
+  return hipGetLastError();
+}
+
+size_t kquant_argmax_workspace_bytes(size_t rows) {
+  return align256(rows * sizeof(float)) + argmax_workspace_bytes(rows);
+}
+
+hipError_t launch_kquant_argmax(int format, const void* weight, size_t rows, size_t cols,
+                                const float* input, int32_t* token_out, float* probability_out,
+                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (workspace == nullptr || workspace_bytes < kquant_argmax_workspace_bytes(rows)) {
+    return hipErrorInvalidValue;
+  }
+  float* logits = static_cast<float*>(workspace);
+  GemvArgs a{static_cast<const uint8_t*>(weight), input, logits, (uint32_t)rows, (uint32_t)cols,
+             (uint32_t)(cols / 256u), 1u, 0u, 0u};
+  hipError_t e = launch_gemv(format, a, stream);
+  if (e != hipSuccess) {
+    return e;
+  }
+  void* rest = static_cast<char*>(workspace) + align256(rows * sizeof(float));
+  return launch_argmax(logits, rows, token_out, probability_out, rest,
+                       workspace_bytes - align256(rows * sizeof(float)), stream);
+}
+
+}  // namespace kraken

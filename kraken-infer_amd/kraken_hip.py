@@ -80,6 +80,26 @@ SIGNATURES = {
     "kraken_hip_mul_f32_in_place": [_B, _B, _sz],
     "kraken_hip_add_f32_row_in_place": [_B, _B, _sz, _sz],
     "kraken_hip_mul_f32_row_in_place": [_B, _B, _sz, _sz],
+    "kraken_hip_matvec_q4_k_f32_device": [_B, _sz, _sz, _B, _B],
+    "kraken_hip_matvec_q4_k_f32_top1": [_B, _sz, _sz, _B, _B, _B],
+    "kraken_hip_matvec_q4_k_f32_argmax": [_B, _sz, _sz, _B, _B],
+    "kraken_hip_matmul_q4_k_f32_device": [_B, _sz, _sz, _sz, _B, _B],
+    "kraken_hip_dequantize_row_q4_k_f32": [_B, _sz, _sz, _B],
+    "kraken_hip_dequantize_rows_q4_k_f32": [_B, _sz, _B, _sz, _sz, _B],
+    "kraken_hip_matvec_q5_k_f32_device": [_B, _sz, _sz, _B, _B],
+    "kraken_hip_matvec_q5_k_f32_top1": [_B, _sz, _sz, _B, _B, _B],
+    "kraken_hip_matvec_q5_k_f32_argmax": [_B, _sz, _sz, _B, _B],
+    "kraken_hip_matmul_q5_k_f32_device": [_B, _sz, _sz, _sz, _B, _B],
+    "kraken_hip_dequantize_row_q5_k_f32": [_B, _sz, _sz, _B],
+    "kraken_hip_dequantize_rows_q5_k_f32": [_B, _sz, _B, _sz, _sz, _B],
+    "kraken_hip_matvec_q6_k_f32_device": [_B, _sz, _sz, _B, _B],
+    "kraken_hip_matvec_q6_k_f32_top1": [_B, _sz, _sz, _B, _B, _B],
+    "kraken_hip_matvec_q6_k_f32_argmax": [_B, _sz, _sz, _B, _B],
+    "kraken_hip_matmul_q6_k_f32_device": [_B, _sz, _sz, _sz, _B, _B],
+    "kraken_hip_dequantize_row_q6_k_f32": [_B, _sz, _sz, _B],
+    "kraken_hip_dequantize_rows_q6_k_f32": [_B, _sz, _B, _sz, _sz, _B],
+    "kraken_hip_argmax_f32_i32": [_B, _sz, _B],
+    "kraken_hip_argmax_prob_f32_i32": [_B, _sz, _B, _B],
     "kraken_hip_begin_graph": [],
     "kraken_hip_commit_graph": [],
     "kraken_hip_make_buffer": [_sz, ctypes.POINTER(_B)],
@@ -417,3 +437,56 @@ class NumpyOps:
             self.ctx.attention_f32_batched(q, kb, vb, layer, start_position, tokens,
                                            capacity_tokens, heads, kv_heads, head_dim, out)
         return out.download()
+
+    # ---- K-quant projections and argmax (oracle.kquant_* / oracle.argmax) ----
+
+    def kquant_dequantize(self, fmt, data, blocks):
+        """blocks super-blocks -> 256 * blocks f32 values (dequantize_rows_*
+        with one 256-value row per block, rows in order)."""
+        w = self.ctx.buffer(np.ascontiguousarray(data, np.uint8))
+        ids = self._buf(np.arange(blocks), np.int32)
+        out = self.ctx.buffer(byte_size=4 * 256 * blocks)
+        getattr(self.ctx, f"dequantize_rows_{fmt}_f32")(w, blocks, ids, blocks, 256, out)
+        return out.download(256 * blocks)
+
+    def kquant_dequantize_row(self, fmt, data, row, cols):
+        w = self.ctx.buffer(np.ascontiguousarray(data, np.uint8))
+        out = self.ctx.buffer(byte_size=4 * cols)
+        getattr(self.ctx, f"dequantize_row_{fmt}_f32")(w, row, cols, out)
+        return out.download(cols)
+
+    def kquant_matmul(self, fmt, weight, rows, cols, x, tokens, weight_f16=False,
+                      input_f16=False):
+        """output [tokens][rows].  The device picks the arithmetic by token
+        count (fp32 up to 8 tokens, f16 operands above); the flags exist for
+        signature parity with the oracle and are not consulted."""
+        w = self.ctx.buffer(np.ascontiguousarray(weight, np.uint8))
+        xb = self._buf(np.asarray(x, np.float32).reshape(-1))
+        out = self.ctx.buffer(byte_size=4 * rows * tokens)
+        if tokens == 1:
+            getattr(self.ctx, f"matvec_{fmt}_f32_device")(w, rows, cols, xb, out)
+        else:
+            getattr(self.ctx, f"matmul_{fmt}_f32_device")(w, rows, cols, tokens, xb, out)
+        return out.download(rows * tokens)
+
+    def kquant_top1(self, fmt, weight, rows, cols, x, probability=False):
+        w = self.ctx.buffer(np.ascontiguousarray(weight, np.uint8))
+        xb = self._buf(np.asarray(x, np.float32).reshape(-1))
+        tok = self.ctx.buffer(np.array([-7], np.int32))
+        if probability:
+            prob = self._buf(np.array([-1.0], np.float32))
+            getattr(self.ctx, f"matvec_{fmt}_f32_top1")(w, rows, cols, xb, tok, prob)
+            return int(tok.download(1)[0]), float(prob.download(1)[0])
+        getattr(self.ctx, f"matvec_{fmt}_f32_argmax")(w, rows, cols, xb, tok)
+        return int(tok.download(1)[0])
+
+    def argmax(self, values, probability=False):
+        v = _f32(values).reshape(-1)
+        vb = self._buf(v)
+        tok = self.ctx.buffer(np.array([-7], np.int32))
+        if probability:
+            prob = self._buf(np.array([-1.0], np.float32))
+            self.ctx.argmax_prob_f32_i32(vb, v.size, tok, prob)
+            return int(tok.download(1)[0]), float(prob.download(1)[0])
+        self.ctx.argmax_f32_i32(vb, v.size, tok)
+        return int(tok.download(1)[0])

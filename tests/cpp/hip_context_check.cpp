@@ -114,6 +114,24 @@ int run_cpu() {
   s = ctx.gated_delta_net_f32_batched_in_place_at(gq, gk, gv, gg, gb, st, 1, t, hk, hv, dd, go);
   expect(s.code() == StatusCode::invalid_argument, "GDN state offset past the buffer rejected",
          s);
+
+  // K-quant projections (Q5_K 6144 x 1024, the Qwen3.5 shape) and argmax.
+  HipBuffer qw = view(6144 * 4 * 176), qx = view(4 * 1024 * 9), qy = view(4 * 6144 * 9);
+  s = ctx.matmul_q5_k_f32_device(qw, 6144, 1024, 9, qx, qy);
+  expect(s.code() == StatusCode::unavailable, "valid Q5_K matmul arguments accepted", s);
+  s = ctx.matmul_q5_k_f32_device(qw, 6144, 1000, 9, qx, qy);
+  expect(s.code() == StatusCode::invalid_argument &&
+           s.message() == "HIP Q5_K matmul cols must be divisible by 256",
+         "Q5_K matmul cols % 256 rejected", s);
+  auto host = ctx.matvec_q4_k_f32(qw, 16, 1024, std::vector<float>(1000, 1.0f));
+  expect(!host.is_ok() &&
+           host.status().message() == "HIP Q4_K matvec input size does not match cols",
+         "host-vector Q4_K matvec input size checked first", host.status());
+  HipBuffer tok = view(4), prob = view(4);
+  s = ctx.argmax_prob_f32_i32(qy, 0, tok, prob);
+  expect(s.code() == StatusCode::invalid_argument &&
+           s.message() == "HIP argmax probability size must be positive",
+         "argmax_prob size 0 rejected", s);
   return failures == 0 ? 0 : 1;
 }
 
@@ -188,6 +206,28 @@ int run_gpu() {
   expect(s.is_ok(), "copy_buffer_region", s);
   s = ctx.copy_from_buffer(ob, back.data(), 4 * back.size());
   expect(s.is_ok() && back == gate, "buffer round trip through copy_buffer_region", s);
+
+  // The reference smoke test's Q4_K block (smoke_test.cpp:875-894): d = 1,
+  // dmin = 0, all 6-bit scales 1, quants 0x21, so W x = 128 * 1 + 128 * 2 for
+  // x = 1; then argmax_prob over {-1, 5, 2} (smoke_test.cpp:1622-1638).
+  std::vector<uint8_t> block(144, 0);
+  block[1] = 0x3C;
+  for (int i = 4; i < 16; ++i) block[i] = 1;
+  for (int i = 16; i < 144; ++i) block[i] = 0x21;
+  HipBuffer wq = make(block.size(), block.data());
+  auto mv = ctx.matvec_q4_k_f32(wq, 1, 256, std::vector<float>(256, 1.0f));
+  expect(mv.is_ok() && mv.value().size() == 1 && std::fabs(mv.value()[0] - 384.0f) < 1e-5f,
+         "host-vector Q4_K matvec known answer 384", mv.status());
+  const float logits[3] = {-1.0f, 5.0f, 2.0f};
+  HipBuffer lb = make(sizeof(logits), logits);
+  HipBuffer tb = make(4, nullptr), pb = make(4, nullptr);
+  s = ctx.argmax_prob_f32_i32(lb, 3, tb, pb);
+  int32_t token = -1;
+  float probability = 0.0f;
+  expect(s.is_ok() && ctx.copy_from_buffer(tb, &token, 4).is_ok() &&
+           ctx.copy_from_buffer(pb, &probability, 4).is_ok() && token == 1 &&
+           std::fabs(probability - 0.950330f) < 1e-4f,
+         "argmax_prob known answer (1, 0.950330)", s);
   return failures == 0 ? 0 : 1;
 }
 

@@ -157,3 +157,32 @@ def random_weight_fast(fmt, rows, cols, seed):
         dm = rng.uniform(0.0, 0.02, size=blocks).astype(np.float16).view(np.uint8).reshape(-1, 2)
         w[:, 2:4] = dm
     return w.reshape(-1)
+
+
+def run_case(impl, case, gold):
+    """Runs one known-answer case through `impl` (the oracle module or a device
+    front end with the same function names) and checks it."""
+    a = case.get("args", {})
+    op = case["op"]
+    if op in ("argmax", "argmax_prob"):
+        if op == "argmax":
+            assert impl.argmax(case["values"]) == case["expected_index"]
+        else:
+            idx, p = impl.argmax(case["values"], probability=True)
+            assert idx == case["expected_index"]
+            assert abs(p - case["expected_probability"]) < case["probability_atol"]
+        return
+    fmt = case["format"]
+    w = case_weight(case)
+    if op == "dequantize_row":
+        got = impl.kquant_dequantize(fmt, w, a["cols"] // 256)
+    elif op == "dequantize_rows":
+        row_bytes = (a["cols"] // 256) * BLOCK_BYTES[fmt]
+        got = np.concatenate([impl.kquant_dequantize(fmt, w[r * row_bytes:(r + 1) * row_bytes],
+                                                     a["cols"] // 256) for r in a["row_ids"]])
+    else:
+        got = impl.kquant_matmul(fmt, w, a["rows"], a["cols"], case_input(case), a["tokens"])
+    if "expected" in case:
+        np.testing.assert_allclose(got, case["expected"], rtol=0, atol=gold["atol"])
+    for index, value in case["expected_at"].items() if "expected_at" in case else []:
+        assert abs(got[int(index)] - value) <= gold["atol"], (case["name"], index)

@@ -1,0 +1,221 @@
+"""CPU tests of the K-quant and argmax entry points' argument checks, in the
+reference's order and wording ("HIP" for "MPS"): make_q*_k_matvec_layout and
+make_k_quant_matmul_layout (mps_backend.mm:4038-4189), the matvec / top1 /
+argmax / matmul methods (:6134-6450 for Q4_K; Q5_K and Q6_K repeat them),
+dequantize_row(s) (:7217-7380) and argmax_f32_i32 / argmax_prob_f32_i32
+(:10004-10090).  The validation-only context runs every check and answers
+`unavailable` instead of launching.
+"""
+import pytest
+
+import kraken_hip as kh
+
+ACCEPTED = "validation-only context: arguments accepted"
+BLOCK = {"q4_k": 144, "q5_k": 176, "q6_k": 210}
+NAME = {"q4_k": "Q4_K", "q5_k": "Q5_K", "q6_k": "Q6_K"}
+FORMATS = tuple(BLOCK)
+
+
+@pytest.fixture()
+def vctx():
+    ctx = kh.Context(validation_only=True)
+    yield ctx
+    ctx.close()
+
+
+def fake(nbytes, address=0x1000):
+    return kh.KrakenBuffer(address, nbytes)
+
+
+def null(nbytes=0):
+    return kh.KrakenBuffer(0, nbytes)
+
+
+def status(ctx, name, *args):
+    return ctx.status(name, *args), kh.last_error()
+
+
+def wbytes(fmt, rows, cols):
+    return rows * (cols // 256) * BLOCK[fmt]
+
+
+def invalid(msg):
+    return (kh.INVALID_ARGUMENT, msg)
+
+
+# The Qwen3.5-0.8B projection shapes named for this row (rows x cols).
+QWEN_SHAPES = [("q5_k", 6144, 1024), ("q4_k", 3584, 1024), ("q6_k", 1024, 3584),
+               ("q4_k", 1024, 2048)]
+
+
+@pytest.mark.parametrize("fmt,rows,cols", QWEN_SHAPES)
+@pytest.mark.parametrize("tokens", [1, 4, 8, 9, 1024])
+def test_matmul_accepts_qwen_shapes(vctx, fmt, rows, cols, tokens):
+    args = (fake(wbytes(fmt, rows, cols)), rows, cols, tokens, fake(4 * tokens * cols),
+            fake(4 * tokens * rows))
+    assert status(vctx, f"matmul_{fmt}_f32_device", *args) == (kh.UNAVAILABLE, ACCEPTED)
+    if tokens == 1:
+        args = (fake(wbytes(fmt, rows, cols)), rows, cols, fake(4 * cols), fake(4 * rows))
+        assert status(vctx, f"matvec_{fmt}_f32_device", *args) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_matvec_check_order(vctx, fmt):
+    n = NAME[fmt]
+    op = f"matvec_{fmt}_f32_device"
+    rows, cols = 32, 512
+    w, x, y = fake(wbytes(fmt, rows, cols)), fake(4 * cols), fake(4 * rows)
+    assert status(vctx, op, null(), rows, cols, x, y) == invalid(
+        f"HIP {n} weight buffer is not initialized")
+    assert status(vctx, op, w, 0, cols, x, y) == invalid(
+        f"HIP {n} matvec rows and cols must be greater than zero")
+    assert status(vctx, op, w, rows, 300, x, y) == invalid(
+        f"HIP {n} matvec cols must be divisible by 256")
+    assert status(vctx, op, w, rows, 256 << 32, x, y) == invalid(
+        f"HIP {n} matvec cols exceeds uint32 range")
+    assert status(vctx, op, w, 1 << 63, cols, x, y) == invalid(
+        f"HIP {n} matvec block count overflow")
+    assert status(vctx, op, fake(wbytes(fmt, rows, cols) - 1), rows, cols, x, y) == invalid(
+        f"HIP {n} weight buffer is too small")
+    code, msg = status(vctx, op, w, rows, cols, fake(4 * cols - 4), y)
+    assert code == kh.INVALID_ARGUMENT and f"{n} matvec input" in msg
+    code, msg = status(vctx, op, w, rows, cols, x, fake(4 * rows - 4))
+    assert code == kh.INVALID_ARGUMENT and f"{n} matvec output" in msg
+    # Beyond the reference: the device loads need aligned weights and inputs.
+    code, msg = status(vctx, op, fake(wbytes(fmt, rows, cols) + 8, 0x1001), rows, cols, x, y)
+    assert code == kh.INVALID_ARGUMENT and "aligned" in msg
+    code, msg = status(vctx, op, w, rows, cols, fake(4 * cols, 0x1004), y)
+    assert code == kh.INVALID_ARGUMENT and "16-byte aligned" in msg
+    assert status(vctx, op, w, rows, cols, x, y) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+def test_q6_k_weight_needs_only_two_byte_alignment(vctx):
+    rows, cols = 3, 256
+    args = (fake(wbytes("q6_k", rows, cols), 0x1002), rows, cols, fake(4 * cols),
+            fake(4 * rows))
+    assert status(vctx, "matvec_q6_k_f32_device", *args) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("kind", ["top1", "argmax"])
+def test_top1_and_argmax_check_order(vctx, fmt, kind):
+    n = NAME[fmt]
+    op = f"matvec_{fmt}_f32_{kind}"
+    rows, cols = 248320, 1024
+    w, x, tok, prob = fake(wbytes(fmt, rows, cols)), fake(4 * cols), fake(4), fake(4)
+    outs = (tok, prob) if kind == "top1" else (tok,)
+    assert status(vctx, op, null(), rows, cols, x, *outs) == invalid(
+        f"HIP {n} {kind} weight buffer is not initialized")
+    assert status(vctx, op, w, rows, 100, x, *outs) == invalid(
+        f"HIP {n} matvec cols must be divisible by 256")
+    big = fake(wbytes(fmt, rows, 4352))
+    assert status(vctx, op, big, rows, 4352, fake(4 * 4352), *outs) == invalid(
+        f"HIP {n} {kind} block count exceeds kernel limit")
+    assert status(vctx, op, fake(10), rows, cols, x, *outs) == invalid(
+        f"HIP {n} {kind} weight buffer is too small")
+    code, msg = status(vctx, op, w, rows, cols, fake(8), *outs)
+    assert code == kh.INVALID_ARGUMENT and f"{n} {kind} input" in msg
+    bad_tok = (null(), prob) if kind == "top1" else (null(),)
+    code, msg = status(vctx, op, w, rows, cols, x, *bad_tok)
+    assert code == kh.INVALID_ARGUMENT and f"{n} {kind} token output" in msg
+    if kind == "top1":
+        code, msg = status(vctx, op, w, rows, cols, x, tok, fake(2))
+        assert code == kh.INVALID_ARGUMENT and f"{n} top1 probability output" in msg
+    assert status(vctx, op, w, rows, cols, x, *outs) == (kh.UNAVAILABLE, ACCEPTED)
+    # 4096 columns (16 blocks) is the largest row the top1 kernels take.
+    assert status(vctx, op, fake(wbytes(fmt, 8, 4096)), 8, 4096, fake(4 * 4096),
+                  *outs) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_matmul_check_order(vctx, fmt):
+    n = NAME[fmt]
+    op = f"matmul_{fmt}_f32_device"
+    rows, cols, tokens = 64, 512, 33
+    w, x, y = fake(wbytes(fmt, rows, cols)), fake(4 * tokens * cols), fake(4 * tokens * rows)
+    assert status(vctx, op, null(), rows, cols, tokens, x, y) == invalid(
+        f"HIP {n} weight buffer is not initialized")
+    assert status(vctx, op, w, rows, cols, 0, x, y) == invalid(
+        f"HIP {n} matmul rows, cols and tokens must be greater than zero")
+    assert status(vctx, op, w, rows, 257, tokens, x, y) == invalid(
+        f"HIP {n} matmul cols must be divisible by 256")
+    assert status(vctx, op, w, 1 << 33, cols, tokens, x, y) == invalid(
+        f"HIP {n} matmul dimensions exceed uint32 range")
+    assert status(vctx, op, w, rows, cols, 1 << 60, x, y) == invalid(
+        f"HIP {n} matmul dimensions exceed uint32 range")
+    assert status(vctx, op, fake(100), rows, cols, tokens, x, y) == invalid(
+        f"HIP {n} matmul weight buffer is too small")
+    code, msg = status(vctx, op, w, rows, cols, tokens, fake(4 * cols), y)
+    assert code == kh.INVALID_ARGUMENT and f"{n} matmul input" in msg
+    code, msg = status(vctx, op, w, rows, cols, tokens, x, fake(4 * rows))
+    assert code == kh.INVALID_ARGUMENT and f"{n} matmul output" in msg
+    assert status(vctx, op, w, rows, cols, tokens, x, y) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_get_row_check_order(vctx, fmt):
+    n = NAME[fmt]
+    op = f"dequantize_row_{fmt}_f32"
+    cols = 1024
+    w, y = fake(wbytes(fmt, 10, cols)), fake(4 * cols)
+    assert status(vctx, op, null(), 3, cols, y) == invalid(
+        f"HIP {n} get-row weight buffer is not initialized")
+    assert status(vctx, op, w, 3, 0, y) == invalid(
+        f"HIP {n} get-row cols must be positive and divisible by 256")
+    assert status(vctx, op, w, 2**64 - 1, cols, y) == invalid(
+        f"HIP {n} get-row weight byte count overflow")
+    assert status(vctx, op, w, 10, cols, y) == invalid(
+        f"HIP {n} get-row weight buffer is too small")
+    code, msg = status(vctx, op, w, 9, cols, fake(4))
+    assert code == kh.INVALID_ARGUMENT and f"{n} get-row output" in msg
+    assert status(vctx, op, w, 9, cols, y) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_get_rows_check_order(vctx, fmt):
+    n = NAME[fmt]
+    op = f"dequantize_rows_{fmt}_f32"
+    rows, tokens, cols = 10, 5, 512
+    w, ids, y = fake(wbytes(fmt, rows, cols)), fake(4 * tokens), fake(4 * tokens * cols)
+    assert status(vctx, op, null(), rows, ids, tokens, cols, y) == invalid(
+        f"HIP {n} get-rows weight buffer is not initialized")
+    assert status(vctx, op, w, rows, ids, 0, cols, y) == invalid(
+        f"HIP {n} get-rows rows, tokens and cols must be positive and cols divisible by 256")
+    assert status(vctx, op, w, 2**62, ids, tokens, cols, y) == invalid(
+        f"HIP {n} get-rows weight byte count overflow")
+    assert status(vctx, op, fake(20), rows, ids, tokens, cols, y) == invalid(
+        f"HIP {n} get-rows weight buffer is too small")
+    code, msg = status(vctx, op, w, rows, fake(4), tokens, cols, y)
+    assert code == kh.INVALID_ARGUMENT and f"{n} get-rows row ids" in msg
+    code, msg = status(vctx, op, w, rows, ids, tokens, cols, fake(16))
+    assert code == kh.INVALID_ARGUMENT and f"{n} get-rows output" in msg
+    assert status(vctx, op, w, rows, ids, tokens, cols, y) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+def test_argmax_check_order(vctx):
+    v, tok, prob = fake(4 * 100), fake(4), fake(4)
+    assert status(vctx, "argmax_f32_i32", v, 0, tok) == invalid("HIP argmax size must be positive")
+    code, msg = status(vctx, "argmax_f32_i32", v, 1 << 33, tok)
+    assert code == kh.INVALID_ARGUMENT and "argmax size" in msg
+    code, msg = status(vctx, "argmax_f32_i32", fake(8), 100, tok)
+    assert code == kh.INVALID_ARGUMENT and "argmax values" in msg
+    assert status(vctx, "argmax_f32_i32", v, 100, null()) == invalid(
+        "HIP argmax output buffer is not initialized")
+    assert status(vctx, "argmax_f32_i32", v, 100, fake(2)) == invalid(
+        "HIP argmax output buffer is too small")
+    assert status(vctx, "argmax_f32_i32", v, 100, tok) == (kh.UNAVAILABLE, ACCEPTED)
+
+    op = "argmax_prob_f32_i32"
+    assert status(vctx, op, v, 0, tok, prob) == invalid(
+        "HIP argmax probability size must be positive")
+    code, msg = status(vctx, op, fake(8), 100, tok, prob)
+    assert code == kh.INVALID_ARGUMENT and "argmax probability values" in msg
+    assert status(vctx, op, v, 100, null(), prob) == invalid(
+        "HIP argmax probability token output buffer is not initialized")
+    assert status(vctx, op, v, 100, fake(3), prob) == invalid(
+        "HIP argmax probability token output buffer is too small")
+    code, msg = status(vctx, op, v, 100, tok, null())
+    assert code == kh.INVALID_ARGUMENT and "argmax probability output" in msg
+    assert status(vctx, op, v, 100, tok, prob) == (kh.UNAVAILABLE, ACCEPTED)
+    # Vocabulary-sized inputs take the two-pass path (context workspace).
+    assert status(vctx, op, fake(4 * 248320), 248320, tok, prob) == (kh.UNAVAILABLE, ACCEPTED)

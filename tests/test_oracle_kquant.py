@@ -25,36 +25,9 @@ GOLD = kc.load()
 FORMATS = ("q4_k", "q5_k", "q6_k")
 
 
-def run_case(impl, case):
-    a = case.get("args", {})
-    op = case["op"]
-    if op in ("argmax", "argmax_prob"):
-        if op == "argmax":
-            assert impl.argmax(case["values"]) == case["expected_index"]
-        else:
-            idx, p = impl.argmax(case["values"], probability=True)
-            assert idx == case["expected_index"]
-            assert abs(p - case["expected_probability"]) < case["probability_atol"]
-        return
-    fmt = case["format"]
-    w = kc.case_weight(case)
-    if op == "dequantize_row":
-        got = impl.kquant_dequantize(fmt, w, a["cols"] // 256)
-    elif op == "dequantize_rows":
-        row_bytes = (a["cols"] // 256) * kc.BLOCK_BYTES[fmt]
-        got = np.concatenate([impl.kquant_dequantize(fmt, w[r * row_bytes:(r + 1) * row_bytes],
-                                                     a["cols"] // 256) for r in a["row_ids"]])
-    else:
-        got = impl.kquant_matmul(fmt, w, a["rows"], a["cols"], kc.case_input(case), a["tokens"])
-    if "expected" in case:
-        np.testing.assert_allclose(got, case["expected"], rtol=0, atol=GOLD["atol"])
-    for index, value in case["expected_at"].items() if "expected_at" in case else []:
-        assert abs(got[int(index)] - value) <= GOLD["atol"], (case["name"], index)
-
-
 @pytest.mark.parametrize("case", GOLD["cases"], ids=[c["name"] for c in GOLD["cases"]])
 def test_oracle_matches_smoke_known_answer(case):
-    run_case(oracle, case)
+    kc.run_case(oracle, case, GOLD)
 
 
 def test_planted_nibble_swap_is_caught():
@@ -68,7 +41,7 @@ def test_planted_nibble_swap_is_caught():
 
     case = next(c for c in GOLD["cases"] if c["name"] == "q4_k_dequantize_row")
     with pytest.raises(AssertionError):
-        run_case(Broken, case)
+        kc.run_case(Broken, case, GOLD)
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
