@@ -176,6 +176,23 @@ KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv_gated(
   size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim,
   kraken_buffer output);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): kraken_hip_attention_f32_batched_f16_kv_gated with the
+ * same arguments, kernels and results, but its split partials live in a static
+ * 8 MiB device array that the library holds on each GPU until the process
+ * ends, so the call allocates nothing.  Shapes whose partials need more
+ * (e.g. long prefills split over the KV) are rejected with
+ * KRAKEN_INVALID_ARGUMENT; single-token decode at any supported KV length
+ * fits.  All calls on one GPU share the array: calls that overlap in time on
+ * one GPU (other contexts or streams) race and must be serialised by the
+ * caller.  Nothing in the array needs to start at zero. */
+KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv_gated_no_alloc(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key_cache,
+  kraken_buffer value_cache, kraken_buffer gate, size_t layer, size_t start_position,
+  size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+  kraken_buffer output);
+
 /* The full-attention prologue of run_qwen35_full_attention_layer_chunk
  * (qwen35_runtime.cpp:3229-3326) fused into one launch; no single MpsContext
  * method corresponds.  It replaces, with the same arithmetic:

@@ -37,7 +37,8 @@ int attention_entry(kraken_hip_context* ctx, const char* what, bool kv_f16,
                     const kraken_buffer& query, const kraken_buffer& key_cache,
                     const kraken_buffer& value_cache, const kraken_buffer* gate, size_t layer,
                     size_t start_position, size_t tokens, size_t capacity_tokens, size_t heads,
-                    size_t kv_heads, size_t head_dim, const kraken_buffer& output) {
+                    size_t kv_heads, size_t head_dim, const kraken_buffer& output,
+                    bool no_alloc = false) {
   KRAKEN_TRY(check_context(ctx));
   const std::string w = std::string("HIP ") + what;
   if (tokens == 0 || heads == 0 || kv_heads == 0 || head_dim == 0 || capacity_tokens == 0) {
@@ -112,14 +113,29 @@ int attention_entry(kraken_hip_context* ctx, const char* what, bool kv_f16,
   const bool use_flash = flash_ok && choice != FlashChoice::force_off &&
                          (choice == FlashChoice::force_on || tokens >= 64u);
 
-  KRAKEN_TRY(begin_launch(ctx));
   const size_t need = use_flash ? attention_flash_workspace_bytes(a, ctx->cu_count)
                                 : attention_decode_workspace_bytes(a, ctx->cu_count);
-  KRAKEN_TRY(ensure_workspace(ctx, need));
+  if (no_alloc && need > kNoAllocScratchBytes) {
+    return invalid(w + " needs " + std::to_string(need) +
+                   " bytes of split partials; the allocation-free entry point has " +
+                   std::to_string(kNoAllocScratchBytes));
+  }
+  KRAKEN_TRY(begin_launch(ctx));
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+  if (no_alloc) {
+    // Every split partial the kernels read is written earlier in the same
+    // call, so the array needs no clearing between calls.
+    workspace = ctx->no_alloc_scratch;
+    workspace_bytes = kNoAllocScratchBytes;
+  } else {
+    KRAKEN_TRY(ensure_workspace(ctx, need));
+    workspace = ctx->workspace;
+    workspace_bytes = ctx->workspace_bytes;
+  }
   const hipError_t e =
-    use_flash ? launch_attention_flash(a, ctx->cu_count, ctx->workspace, ctx->workspace_bytes,
-                                       ctx->stream)
-              : launch_attention_decode(a, ctx->cu_count, ctx->workspace, ctx->workspace_bytes,
+    use_flash ? launch_attention_flash(a, ctx->cu_count, workspace, workspace_bytes, ctx->stream)
+              : launch_attention_decode(a, ctx->cu_count, workspace, workspace_bytes,
                                         ctx->stream);
   if (e != hipSuccess) {
     return internal(w + " launch failed: " + hipGetErrorString(e));
@@ -359,6 +375,19 @@ KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv_gated(
   return attention_entry(ctx, "gated F16 KV batched attention", true, query, key_cache,
                          value_cache, &gate, layer, start_position, tokens, capacity_tokens,
                          heads, kv_heads, head_dim, output);
+}
+
+// No counterpart in the reference: the gated F16-KV attention above with its
+// split partials in the library's static per-device scratch array instead of
+// context workspace, so it never allocates device memory.
+KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv_gated_no_alloc(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key_cache,
+  kraken_buffer value_cache, kraken_buffer gate, size_t layer, size_t start_position,
+  size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+  kraken_buffer output) {
+  return attention_entry(ctx, "gated F16 KV batched attention", true, query, key_cache,
+                         value_cache, &gate, layer, start_position, tokens, capacity_tokens,
+                         heads, kv_heads, head_dim, output, /*no_alloc=*/true);
 }
 
 KRAKEN_API int kraken_hip_gated_delta_net_f32_batched_in_place_at(

@@ -226,6 +226,12 @@ KRAKEN_API int kraken_hip_context_create(kraken_hip_context** out_context) {
     return unavailable("HIP backend: stream creation failed: " + hip_message(e));
   }
   ctx->stream = ctx->own_stream;
+  const int scratch_status = resolve_no_alloc_scratch(device, &ctx->no_alloc_scratch);
+  if (scratch_status != KRAKEN_OK) {
+    (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return scratch_status;
+  }
   *out_context = ctx;
   return KRAKEN_OK;
 }

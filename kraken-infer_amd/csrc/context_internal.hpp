@@ -24,6 +24,9 @@ struct kraken_hip_context {
   // scratch (mps_backend.mm:4402-4407).
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
+  // This device's copy of the static scratch array used by the allocation-free
+  // entry point (device address, resolved at context creation).
+  void* no_alloc_scratch = nullptr;
 };
 
 // Returns from the calling entry point with the status of `expr` unless it is OK.
@@ -58,6 +61,12 @@ int finish_launch(kraken_hip_context* ctx, const char* error_prefix);
 // Ensures ctx->workspace holds at least `bytes`; waits for pending work before
 // reallocating.  Returns KRAKEN_OK or an error status.
 int ensure_workspace(kraken_hip_context* ctx, size_t bytes);
+
+// Size of the static per-device scratch array of the allocation-free entry
+// point, and the lookup of its device address on `device` (which must be the
+// current device); the address is resolved once per device and cached.
+constexpr size_t kNoAllocScratchBytes = size_t{8} << 20;
+int resolve_no_alloc_scratch(int device, void** out);
 
 // ------------------------------------------------------------ validation ----
 // Restatements of the reference's helpers, mps_backend.mm:4196-4308.

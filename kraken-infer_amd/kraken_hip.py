@@ -49,6 +49,8 @@ SIGNATURES = {
     "kraken_hip_attention_f32_batched_f16_kv": [_B, _B, _B] + [_sz] * 7 + [_B],
     "kraken_hip_attention_f32_batched": [_B, _B, _B] + [_sz] * 7 + [_B],
     "kraken_hip_attention_f32_batched_f16_kv_gated": [_B, _B, _B, _B] + [_sz] * 7 + [_B],
+    "kraken_hip_attention_f32_batched_f16_kv_gated_no_alloc": [_B, _B, _B, _B] + [_sz] * 7
+                                                              + [_B],
     "kraken_hip_gated_delta_net_f32_batched_in_place_at": [_B] * 6 + [_sz] * 5 + [_B],
     "kraken_hip_gated_delta_net_f32_batched_in_place": [_B] * 6 + [_sz] * 4 + [_B],
     "kraken_hip_gated_delta_net_f32_in_place_at": [_B] * 6 + [_sz] * 4 + [_B],

@@ -419,3 +419,21 @@ def test_copy_regions_argument_checks(vctx):
     many = (_Region * 65)()
     code, _ = status(vctx, "copy_regions", src, dst, ctypes.addressof(many), 65)
     assert code == kh.INVALID_ARGUMENT
+
+
+def test_no_alloc_attention_limits_its_scratch(vctx):
+    """The allocation-free attention accepts what fits its static 8 MiB array
+    (decode at long KV) and rejects, before launching, a prefill whose split
+    partials would not fit."""
+    h, kvh, d = 8, 2, 256
+    for tokens, start, ok in ((1, 262143, True), (64, 0, True), (1024, 7168, False)):
+        cap = start + tokens
+        q, kv = fake(4 * tokens * h * d), fake(2 * cap * kvh * d)
+        code, msg = status(vctx, "attention_f32_batched_f16_kv_gated_no_alloc", q, kv, kv, q,
+                           0, start, tokens, cap, h, kvh, d, q)
+        if ok:
+            assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED)
+        else:
+            assert code == kh.INVALID_ARGUMENT
+            assert msg == ("HIP gated F16 KV batched attention needs 33816576 bytes of split "
+                           "partials; the allocation-free entry point has 8388608")
