@@ -528,7 +528,6 @@ __global__ void conv1_stateful_kernel(float* state, const float* input, const fl
 // tile of tokens; lane owns CPL channels.  Each wave walks TPW consecutive tokens
 // with a register sliding window of the last K rows.
 constexpr int kConvTokensPerWave = 4;
-constexpr int kConvMaxKernel = 8;
 
 template <int CPL, int K>
 __global__ __launch_bounds__(256) void conv_split_l2_kernel(
@@ -633,14 +632,13 @@ __global__ void conv_state_update_kernel(float* conv_state, const float* qkv,
     return;
   }
   const uint32_t width = conv_kernel - 1u;
-  float old[kConvMaxKernel];
+  float* state = conv_state + (size_t)c * width;
+  // New entry j is row tokens - width + j of [old state | chunk]: a chunk row,
+  // or old entry j + tokens.  Ascending j reads each old entry before it is
+  // overwritten (j + tokens > j), so the shift needs no private copy.
   for (uint32_t j = 0; j < width; ++j) {
-    old[j] = conv_state[(size_t)c * width + j];
-  }
-  for (uint32_t j = 0; j < width; ++j) {
-    const int64_t r = (int64_t)tokens - (int64_t)width + j;  // row in [old | chunk] - width
-    conv_state[(size_t)c * width + j] =
-      r >= 0 ? qkv[(size_t)r * channels + c] : old[width + r];
+    const int64_t r = (int64_t)tokens - (int64_t)width + j;
+    state[j] = r >= 0 ? qkv[(size_t)r * channels + c] : state[j + tokens];
   }
 }
 

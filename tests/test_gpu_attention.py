@@ -263,7 +263,7 @@ def test_flash_c2_full_shape_sampled_tokens(hip_ctx, prefix):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("prefix", [0, 3072])
+@pytest.mark.parametrize("prefix", [0, 3072, 7168])
 def test_flash_agrees_with_split_decode_unnormalised(hip_ctx, prefix, monkeypatch):
     """Two independent kernels (MFMA flash and VALU split-K) agree on every
     output at C2's shape with un-normalised N(0,1) q/k (a sharper softmax than

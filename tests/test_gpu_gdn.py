@@ -144,11 +144,12 @@ def test_gdn_chunked_decay_and_beta_extremes(hip_ctx):
 
 @pytest.mark.gpu
 def test_gdn_c3_prefill_4096_in_chunks_then_decode(hip_ctx):
-    """C3: 4096-token prefill in 1024-token chunks, then decode steps, state carried
-    on the device; oracle runs the same sequence.  Checks state after every chunk."""
+    """C3: 4096-token prefill in 1024-token chunks, then its 256 decode steps, state
+    carried on the device; oracle runs the same sequence.  Checks the output and the
+    state after every chunk and every decode step."""
     hk = hv = 16
     d = 128
-    total, chunk, decode = 4096, 1024, 16
+    total, chunk, decode = 4096, 1024, 256
     q, k, v, g, b, _ = gdn_inputs(3, total + decode, hk, hv, d)
     ctx = hip_ctx
     s_dev = ctx.buffer(np.zeros(hv * d * d, np.float32))

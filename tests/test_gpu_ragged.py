@@ -353,3 +353,124 @@ def test_ragged_gdn_layer_skips_out_of_pool_sequence(hip_ctx):
     np.testing.assert_array_equal(cpool[co:co + conv_elems], c["conv_pool"][co:co + conv_elems])
     for i in (0, 1, 3):
         np.testing.assert_array_equal(out[i * d:(i + 1) * d], ref_out[i * d:(i + 1) * d])
+
+
+def test_c4_block_two_steps_sampled_against_oracle(hip_ctx):
+    """The C4 hybrid block as bench.py runs it: 64 sequences with the bench's KV
+    lengths (512 + mt19937_64(4) mod 32257), each step three GDN layers (one
+    launch each: conv prologue, prepared gate/beta, recurrence, norm-gated
+    epilogue with a non-unit weight) and one full-attention layer (ragged K/V
+    append, gated attention).  Two steps, so the second reads the conv and
+    recurrent states and the K/V rows the first wrote.  Eight sequences
+    (shortest, longest, six others) are replayed through the oracle chain and
+    compared after every step: GDN outputs and states 1e-4, conv states and
+    appended K/V rows exactly, attention 2e-3 rel / 1e-3 abs."""
+    import bench
+
+    rng = np.random.default_rng(44)
+    b, layers, steps = 64, 3, 2
+    hk = hv = 16
+    dd, kk = 128, 4
+    heads, kv_heads, d = 8, 2, 256
+    ch = (2 * hk + hv) * dd
+    kv_dim = kv_heads * d
+    conv_elems, state_elems = ch * (kk - 1), hv * dd * dd
+    lengths = np.array(bench.c4_lengths(), np.int64)
+    kv_offsets, kv_total = scattered_offsets(rng, lengths + steps, kv_dim)
+    block = 1 << 20
+    kpool = np.resize(rng.standard_normal(block).astype(np.float16), kv_total)
+    vpool = np.resize(rng.standard_normal(block + 8).astype(np.float16), kv_total)
+    ctx = hip_ctx
+    kb, vb = ctx.buffer(kpool.view(np.uint16)), ctx.buffer(vpool.view(np.uint16))
+    kvo = ctx.buffer(kv_offsets)
+    lay = []
+    for l in range(layers):
+        coffs, ctotal = scattered_offsets(rng, [1] * b, conv_elems, align=64)
+        soffs, stotal = scattered_offsets(rng, [1] * b, state_elems, align=dd)
+        c = dict(conv=rng.standard_normal(ctotal).astype(np.float32),
+                 state=(0.1 * rng.standard_normal(stotal)).astype(np.float32),
+                 w=(0.5 * rng.standard_normal(ch * kk)).astype(np.float32),
+                 nw=(1 + 0.1 * rng.standard_normal(dd)).astype(np.float32),
+                 dtb=rng.standard_normal(hv).astype(np.float32),
+                 ssa=(-rng.random(hv)).astype(np.float32), coffs=coffs, soffs=soffs)
+        c["dev"] = {k: ctx.buffer(c[k]) for k in ("conv", "state", "w", "nw", "dtb", "ssa",
+                                                   "coffs", "soffs")}
+        lay.append(c)
+    pick = sorted({int(np.argmin(lengths)), int(np.argmax(lengths)), 5, 19, 33, 42, 57, 62})
+    # Host copies the oracle advances for the sampled sequences.
+    conv_ref = {(l, i): lay[l]["conv"][int(lay[l]["coffs"][i]):][:conv_elems].copy()
+                for l in range(layers) for i in pick}
+    state_ref = {(l, i): lay[l]["state"][int(lay[l]["soffs"][i]):][:state_elems].copy()
+                 for l in range(layers) for i in pick}
+    kv_rows = {i: (kpool[int(kv_offsets[i]):][:(int(lengths[i]) + steps) * kv_dim].copy(),
+                   vpool[int(kv_offsets[i]):][:(int(lengths[i]) + steps) * kv_dim].copy())
+               for i in pick}
+    for s in range(steps):
+        print(f"c4 block step {s}", flush=True)
+        pos = (lengths + s).astype(np.uint32)
+        inp = [dict(qkv=rng.standard_normal(b * ch).astype(np.float32),
+                    gate=rng.standard_normal(b * hv).astype(np.float32),
+                    beta=rng.standard_normal(b * hv).astype(np.float32),
+                    z=rng.standard_normal(b * hv * dd).astype(np.float32))
+               for _ in range(layers)]
+        knew = rng.standard_normal(b * kv_dim).astype(np.float32)
+        vnew = rng.standard_normal(b * kv_dim).astype(np.float32)
+        aq = rng.standard_normal(b * heads * d).astype(np.float32)
+        agate = rng.standard_normal(b * heads * d).astype(np.float32)
+        outs = [ctx.buffer(byte_size=4 * b * hv * dd) for _ in range(layers)]
+        aout = ctx.buffer(byte_size=4 * b * heads * d)
+        posb = ctx.buffer(pos)
+        dev_in = [{k: ctx.buffer(v) for k, v in x.items()} for x in inp]
+        knb, vnb, aqb, agb = (ctx.buffer(x) for x in (knew, vnew, aq, agate))
+        ctx.begin_graph()  # the block as one batch: one host wait per step
+        for l in range(layers):
+            dv, di = lay[l]["dev"], dev_in[l]
+            ctx.qwen35_gdn_layer_ragged_decode_f32(
+                di["qkv"], dv["conv"], dv["coffs"], dv["w"], kk, di["gate"], di["beta"],
+                dv["dtb"], dv["ssa"], di["z"], dv["nw"], dv["state"], dv["soffs"], b, hk, hv, dd,
+                1e-6, outs[l])
+        ctx.append_kv_ragged_f16(knb, vnb, kb, vb, kvo, posb, b, kv_dim)
+        ctx.attention_f32_ragged_f16_kv(aqb, kb, vb, agb, kvo, posb, b, int(pos.max()), heads,
+                                        kv_heads, d, aout)
+        ctx.commit_graph()
+        got_out = [o.download() for o in outs]
+        got_conv = [lay[l]["dev"]["conv"].download() for l in range(layers)]
+        got_state = [lay[l]["dev"]["state"].download() for l in range(layers)]
+        got_att = aout.download()
+        for i in pick:
+            for l in range(layers):
+                g, be = oracle.prepare_gdn_gate_beta(inp[l]["gate"][i * hv:(i + 1) * hv],
+                                                     inp[l]["beta"][i * hv:(i + 1) * hv],
+                                                     lay[l]["dtb"], lay[l]["ssa"], 1, hv)
+                ci, conv_ref[(l, i)] = oracle.build_ssm_conv_state(
+                    conv_ref[(l, i)], inp[l]["qkv"][i * ch:(i + 1) * ch], kk, ch, 1)
+                y = oracle.silu(oracle.ssm_conv(ci, lay[l]["w"], kk, ch, 1, 1))
+                q, k, v = oracle.split_qkv_l2_norm(y, 1, hk, hv, dd, 1e-6)
+                yo, state_ref[(l, i)] = oracle.gated_delta_net(q, k, v, g, be, state_ref[(l, i)],
+                                                               1, hk, hv, dd)
+                yo = oracle.norm_gated(yo, lay[l]["nw"], inp[l]["z"][i * hv * dd:][:hv * dd],
+                                       1, hv, dd, 1e-6)
+                msg = f"step {s} layer {l} sequence {i}"
+                np.testing.assert_allclose(got_out[l][i * hv * dd:][:hv * dd], yo, rtol=0,
+                                           atol=1e-4, err_msg=msg)
+                co, so = int(lay[l]["coffs"][i]), int(lay[l]["soffs"][i])
+                np.testing.assert_array_equal(got_conv[l][co:co + conv_elems], conv_ref[(l, i)],
+                                              err_msg=msg)
+                np.testing.assert_allclose(got_state[l][so:so + state_elems], state_ref[(l, i)],
+                                           rtol=0, atol=1e-4, err_msg=msg)
+            kc, vc = kv_rows[i]
+            row = int(pos[i])
+            kc[row * kv_dim:(row + 1) * kv_dim] = knew[i * kv_dim:(i + 1) * kv_dim]
+            vc[row * kv_dim:(row + 1) * kv_dim] = vnew[i * kv_dim:(i + 1) * kv_dim]
+            off = 2 * (int(kv_offsets[i]) + row * kv_dim)
+            np.testing.assert_array_equal(kb.download(kv_dim, np.uint16, off), kc[
+                row * kv_dim:(row + 1) * kv_dim].view(np.uint16))
+            np.testing.assert_array_equal(vb.download(kv_dim, np.uint16, off), vc[
+                row * kv_dim:(row + 1) * kv_dim].view(np.uint16))
+            sl = slice(i * heads * d, (i + 1) * heads * d)
+            ref = oracle.attention_batched(aq[sl], kc[:(row + 1) * kv_dim].view(np.uint16),
+                                           vc[:(row + 1) * kv_dim].view(np.uint16), 0, row, 1,
+                                           row + 1, heads, kv_heads, d)
+            ref = oracle.sigmoid_gate_mul(ref, agate[sl])
+            np.testing.assert_allclose(got_att[sl], ref, rtol=2e-3, atol=1e-3,
+                                       err_msg=f"step {s} attention sequence {i}")

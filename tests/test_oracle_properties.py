@@ -265,3 +265,36 @@ def test_legacy_qwen3_attention_agrees_with_generic_attention():
     q0 = oracle.qwen3_qk_norm(q[:heads * d], heads, d, ones, 1e-6)
     np.testing.assert_array_equal(oracle.qwen3_rope(q0, heads, d, 0, 1e6), q0)
     np.testing.assert_allclose(qo[:heads * d], q0, rtol=0, atol=0)
+
+
+def test_qwen3_rope_is_complex_rotation_at_nonzero_positions():
+    """Pair (i, i + d/2) of each head turns by position * theta^(-2i/d): the
+    closed form as a complex rotation, at positions far from 0, and the
+    rotations compose (rope(rope(x, a), b) = rope(x, a + b))."""
+    rng = np.random.default_rng(11)
+    heads, d, theta = 3, 128, 1e6
+    half = d // 2
+    x = rng.standard_normal(heads * d).astype(np.float32)
+    xr = x.reshape(heads, d).astype(np.float64)
+    for p in (1, 7, 511, 4096, 100003):
+        got = oracle.qwen3_rope(x, heads, d, p, theta).reshape(heads, d)
+        ang = p * theta ** (-2.0 * np.arange(half) / d)
+        z = (xr[:, :half] + 1j * xr[:, half:]) * np.exp(1j * ang)
+        np.testing.assert_allclose(got[:, :half], z.real, rtol=1e-5, atol=2e-6)
+        np.testing.assert_allclose(got[:, half:], z.imag, rtol=1e-5, atol=2e-6)
+    twice = oracle.qwen3_rope(oracle.qwen3_rope(x, heads, d, 300, theta), heads, d, 211, theta)
+    np.testing.assert_allclose(twice, oracle.qwen3_rope(x, heads, d, 511, theta), rtol=0,
+                               atol=1e-5)
+
+
+def test_qwen3_qk_norm_applies_weight_after_normalising():
+    """RMSNorm with weight w equals the unit-weight result times w, element by
+    element, and the unit-weight result has unit RMS per head."""
+    rng = np.random.default_rng(12)
+    heads, d = 4, 128
+    x = (3 * rng.standard_normal(heads * d)).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(d)).astype(np.float32)
+    unit = oracle.qwen3_qk_norm(x, heads, d, np.ones(d, np.float32), 1e-6).reshape(heads, d)
+    got = oracle.qwen3_qk_norm(x, heads, d, w, 1e-6).reshape(heads, d)
+    np.testing.assert_allclose(got, unit * w, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(np.sqrt((unit.astype(np.float64) ** 2).mean(1)), 1.0, rtol=1e-5)
