@@ -566,14 +566,14 @@ def kquant_weight(torch, fmt, rows, cols, gen):
     return w.reshape(-1)
 
 
-def bench_kquant(torch, ctx, run, gen):
+def bench_kquant(torch, ctx, run, gen, shapes=(0, 1, 2, 3)):
     """The Qwen3.5-0.8B K-quant projections: one-token GEMV (weights read
     once; sets rotated over 2x the Infinity Cache so every replay reads HBM)
     and 1024-token GEMM (dequantize to fp16 + MFMA GEMM), as graph replays.
     GEMV bytes = quantized weight + f32 input + f32 output; GEMM flops =
     2 * rows * cols * tokens over the whole call (its three launches)."""
     out = []
-    for fmt, rows, cols in KQUANT_SHAPES:
+    for fmt, rows, cols in (KQUANT_SHAPES[i] for i in shapes):
         wbytes = rows * cols // 256 * KQUANT_BLOCK[fmt]
         sets = max(1, -(-2 * MALL_BYTES // wbytes))
         ws = [kquant_weight(torch, fmt, rows, cols, gen) for _ in range(sets)]
@@ -663,6 +663,10 @@ def main():
     ap.add_argument("--sections", default="decode,prefill,gdn,c4,kquant,peaks,prefix",
                     help="comma-separated detail sections to run after the headline "
                          "(decode, prefill, gdn, c4, kquant, peaks, prefix)")
+    ap.add_argument("--prefill-prefixes", default="0,3072,7168",
+                    help="comma-separated KV prefixes of the prefill section")
+    ap.add_argument("--kquant-shapes", default="0,1,2,3",
+                    help="comma-separated indices into KQUANT_SHAPES for the kquant section")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run torch copies of MIB MiB (20 launches), the known-size "
@@ -707,8 +711,8 @@ def main():
             progress("decode details done")
         if "prefill" in sections:
             gen.manual_seed(2)
-            details["prefill_c2"] = [bench_prefill(torch, ctx, run, p, 10, 2, gen)
-                                     for p in (0, 3072, 7168)]
+            details["prefill_c2"] = [bench_prefill(torch, ctx, run, int(p), 10, 2, gen)
+                                     for p in args.prefill_prefixes.split(",")]
             progress("prefill done")
         if "gdn" in sections:
             gen.manual_seed(3)
@@ -720,7 +724,8 @@ def main():
             progress("ragged c4 done")
         if "kquant" in sections:
             gen.manual_seed(5)
-            details["kquant"] = bench_kquant(torch, ctx, run, gen)
+            details["kquant"] = bench_kquant(torch, ctx, run, gen,
+                                             [int(i) for i in args.kquant_shapes.split(",")])
             progress("kquant: " + ", ".join(
                 f"{k['format']} {k['rows']}x{k['cols']} GEMV {k['gemv_GB_s']:.0f} GB/s "
                 f"GEMM {k['gemm_TFLOP_s']:.0f} TFLOP/s" for k in details["kquant"]))
