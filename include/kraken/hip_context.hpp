@@ -542,6 +542,20 @@ class HipContext {
     return Status::from_code(
       kraken_hip_mul_f32_row_in_place(ctx_, target.raw(), row.raw(), rows, row_size));
   }
+  [[nodiscard]] Status add_f32_in_place(HipBuffer& target, const HipBuffer& delta,
+                                        std::size_t size) const {
+    return Status::from_code(kraken_hip_add_f32_in_place(ctx_, target.raw(), delta.raw(), size));
+  }
+  [[nodiscard]] Status silu_mul_f32_in_place(HipBuffer& gate, const HipBuffer& up,
+                                             std::size_t size) const {
+    return Status::from_code(kraken_hip_silu_mul_f32_in_place(ctx_, gate.raw(), up.raw(), size));
+  }
+  [[nodiscard]] Status rms_norm_f32_f32_batched(const HipBuffer& input, const HipBuffer& weight,
+                                                std::size_t tokens, std::size_t size, float eps,
+                                                HipBuffer& output) const {
+    return Status::from_code(kraken_hip_rms_norm_f32_f32_batched(
+      ctx_, input.raw(), weight.raw(), tokens, size, eps, output.raw()));
+  }
 
   // K-quant projections (mps_backend.hpp:134-226).  matvec_*_f32 takes and
   // returns host vectors through temporary device buffers, as the reference's

@@ -1,0 +1,295 @@
+// The Qwen3.5 decode step on the device: token embedding, the main-layer loop
+// of run_qwen35_decode_tokens (src/runtime/qwen35_runtime.cpp:3860-3936) with
+// each layer's norm, projections, attention core, residuals and SwiGLU FFN
+// (run_qwen35_linear_layer_chunk :2634-3144, run_qwen35_full_attention_layer_chunk
+// :3146-3423), the output norm (:3461-3503) and the greedy LM head
+// (run_qwen35_lm_head_logits :3505-3647, its rows == 1 top-1 path), and the
+// generation loop around it (:6212-6263: one graph per token, committed once).
+//
+// The next token never leaves the device inside the loop: the LM-head argmax
+// writes it into a device token array, and the next step's embedding reads
+// its row id from there.  Each step is one begin_graph / commit_graph batch,
+// so the host waits once per token; the tokens are read back at the end.
+#pragma once
+
+#include <array>
+#include <cstddef>
+#include <cstdint>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "kraken/qwen35_layers.hpp"
+
+namespace kraken::qwen35 {
+
+// GGUF tensor type ids of the weights the decode step reads (gguf_reader.hpp).
+enum class TensorType : std::uint32_t { f32 = 0, q4_k = 12, q5_k = 13, q6_k = 14 };
+
+// A weight in device memory.  For a projection, rows = output values and
+// cols = input values (GGUF shape {cols, rows}).
+struct Tensor {
+  const HipBuffer* buffer{nullptr};
+  TensorType type{TensorType::f32};
+  std::size_t rows{0};
+  std::size_t cols{0};
+};
+
+// The weights of one main layer.  Layers of either kind have the norms and the
+// FFN; the projections and core weights of the other kind stay empty.
+struct DecoderLayerWeights {
+  const HipBuffer* attn_norm{nullptr};            // [hidden]
+  const HipBuffer* post_attention_norm{nullptr};  // [hidden]
+  Tensor ffn_gate, ffn_up, ffn_down;
+  // Linear attention: attn_qkv [conv_channels], attn_gate (z) [inner],
+  // ssm_beta and ssm_alpha [value_heads], ssm_out [hidden] from [inner].
+  Tensor qkv, gate, beta, alpha, ssm_out;
+  LinearAttentionWeights linear;
+  // Full attention: attn_q [heads * 2 * head_dim] (query and gate per head),
+  // attn_k and attn_v [kv_heads * head_dim], attn_output [hidden] from
+  // [heads * head_dim].
+  Tensor q, k, v, output;
+  FullAttentionWeights full;
+};
+
+struct ModelWeights {
+  Tensor token_embd;                      // [vocab][hidden], a K-quant type
+  const HipBuffer* output_norm{nullptr};  // [hidden]
+  Tensor output;                          // LM head [vocab][hidden]; token_embd when tied
+  std::vector<DecoderLayerWeights> layers;  // plan.main_layers entries
+  std::array<std::size_t, 4> mrope_sections{11, 11, 10, 0};
+  float rope_theta{1.0e7f};
+  float rms_eps{1.0e-6f};
+};
+
+// run_qwen35_quant_matmul (qwen35_runtime.cpp:1972-2048): output[tokens][rows]
+// = input[tokens][cols] times the K-quant weight.
+[[nodiscard]] inline Status project(const HipContext& ctx, const Tensor& w,
+                                    const HipBuffer& input, std::size_t tokens,
+                                    HipBuffer& output) {
+  if (tokens == 0) {
+    return Status::invalid_argument("Qwen3.5 matmul requires tokens");
+  }
+  if (w.buffer == nullptr || w.rows == 0 || w.cols == 0) {
+    return Status::invalid_argument("Qwen3.5 matmul weight is missing");
+  }
+  switch (w.type) {
+    case TensorType::q4_k:
+      return ctx.matmul_q4_k_f32_device(*w.buffer, w.rows, w.cols, tokens, input, output);
+    case TensorType::q5_k:
+      return ctx.matmul_q5_k_f32_device(*w.buffer, w.rows, w.cols, tokens, input, output);
+    case TensorType::q6_k:
+      return ctx.matmul_q6_k_f32_device(*w.buffer, w.rows, w.cols, tokens, input, output);
+    default:
+      return Status::invalid_argument("Qwen3.5 matmul weight type is not a K-quant type");
+  }
+}
+
+// Device buffers one decode step reuses; sized for the plan on first use.
+class DecodeScratch {
+ public:
+  HipBuffer hidden, normed, a, b, c, d, attn, ffn_gate, ffn_up;
+  LayerWorkspace layer_ws;
+
+  [[nodiscard]] Status prepare(const HipContext& ctx, const ExecutionPlan& plan,
+                               const ModelWeights& w) {
+    std::size_t widest = plan.hidden_size;
+    for (const auto& l : w.layers) {
+      for (const Tensor* t : {&l.ffn_gate, &l.ffn_up, &l.qkv, &l.gate, &l.q, &l.k, &l.v}) {
+        widest = t->rows > widest ? t->rows : widest;
+      }
+    }
+    widest = plan.linear_inner_size > widest ? plan.linear_inner_size : widest;
+    widest = plan.attention_heads * plan.head_dim > widest ? plan.attention_heads * plan.head_dim
+                                                           : widest;
+    for (HipBuffer* buf : {&hidden, &normed, &a, &b, &c, &d, &attn, &ffn_gate, &ffn_up}) {
+      if (!buf->valid() || buf->byte_size() < widest * sizeof(float)) {
+        auto made = ctx.make_buffer(widest * sizeof(float));
+        if (!made.is_ok()) {
+          return made.status();
+        }
+        *buf = std::move(made.value());
+      }
+    }
+    return Status::ok();
+  }
+};
+
+namespace detail {
+
+[[nodiscard]] inline Status embed_token(const HipContext& ctx, const Tensor& e,
+                                        const HipBuffer& token_id, std::size_t hidden,
+                                        HipBuffer& out) {
+  if (e.buffer == nullptr || e.cols != hidden) {
+    return Status::invalid_argument("Qwen3.5 token embedding shape mismatch");
+  }
+  switch (e.type) {
+    case TensorType::q4_k:
+      return ctx.dequantize_rows_q4_k_f32(*e.buffer, e.rows, token_id, 1, hidden, out);
+    case TensorType::q5_k:
+      return ctx.dequantize_rows_q5_k_f32(*e.buffer, e.rows, token_id, 1, hidden, out);
+    case TensorType::q6_k:
+      return ctx.dequantize_rows_q6_k_f32(*e.buffer, e.rows, token_id, 1, hidden, out);
+    default:
+      return Status::invalid_argument(
+        "Qwen3.5 device token embedding needs a K-quant token_embd");
+  }
+}
+
+[[nodiscard]] inline Status lm_head_argmax(const HipContext& ctx, const Tensor& w,
+                                           const HipBuffer& normed, HipBuffer& token_out) {
+  switch (w.type) {
+    case TensorType::q4_k:
+      return ctx.matvec_q4_k_f32_argmax(*w.buffer, w.rows, w.cols, normed, token_out);
+    case TensorType::q5_k:
+      return ctx.matvec_q5_k_f32_argmax(*w.buffer, w.rows, w.cols, normed, token_out);
+    case TensorType::q6_k:
+      return ctx.matvec_q6_k_f32_argmax(*w.buffer, w.rows, w.cols, normed, token_out);
+    default:
+      return Status::invalid_argument("Qwen3.5 greedy LM head needs a K-quant output weight");
+  }
+}
+
+// The FFN half of a layer (qwen35_runtime.cpp:3024-3144): hidden += down(silu(gate(n)) *
+// up(n)) with n = RMSNorm(hidden) * post_attention_norm.
+[[nodiscard]] inline Status ffn_block(const HipContext& ctx, const ExecutionPlan& plan,
+                                      const DecoderLayerWeights& l, float eps, DecodeScratch& s) {
+  const std::size_t h = plan.hidden_size;
+  Status st = ctx.rms_norm_f32_f32_batched(s.hidden, *l.post_attention_norm, 1, h, eps, s.normed);
+  if (st.is_ok()) st = project(ctx, l.ffn_up, s.normed, 1, s.ffn_up);
+  if (st.is_ok()) st = project(ctx, l.ffn_gate, s.normed, 1, s.ffn_gate);
+  if (st.is_ok()) st = ctx.silu_mul_f32_in_place(s.ffn_gate, s.ffn_up, l.ffn_gate.rows);
+  if (st.is_ok()) st = project(ctx, l.ffn_down, s.ffn_gate, 1, s.a);
+  if (st.is_ok()) st = ctx.add_f32_in_place(s.hidden, s.a, h);
+  return st;
+}
+
+}  // namespace detail
+
+// Enqueues one decode step for the token whose id (int32) is at
+// token_in[0], at sequence position `position`: embedding, every main layer,
+// output norm and the greedy LM head, whose argmax lands in token_out[0].
+// Recurrent row 0 and the F16 KV cache of `cache` are read and advanced.
+// `after_layer`, when given, is called with each main layer's index once its
+// output is in s.hidden (for inspection; it may wait for the device).
+using LayerHook = std::function<Status(std::size_t layer, const HipBuffer& hidden)>;
+
+[[nodiscard]] inline Status enqueue_decode_step(const HipContext& ctx, const ExecutionPlan& plan,
+                                                DeviceCache& cache, const ModelWeights& w,
+                                                DecodeScratch& s, const HipBuffer& token_in,
+                                                HipBuffer& token_out, std::size_t position,
+                                                const LayerHook* after_layer = nullptr) {
+  if (w.layers.size() != plan.main_layers || w.output_norm == nullptr) {
+    return Status::invalid_argument("Qwen3.5 decode weights do not match the plan");
+  }
+  if (position >= plan.cache.attention_capacity_tokens) {
+    return Status::invalid_argument("Qwen3.5 decode position exceeds cache capacity");
+  }
+  const std::size_t h = plan.hidden_size;
+  const float eps = w.rms_eps;
+  Status st = detail::embed_token(ctx, w.token_embd, token_in, h, s.hidden);
+  if (!st.is_ok()) {
+    return st;
+  }
+  st = for_each_main_layer(plan, [&](std::size_t index, LayerKind kind, std::size_t kind_index) {
+    const DecoderLayerWeights& l = w.layers[index];
+    if (l.attn_norm == nullptr || l.post_attention_norm == nullptr) {
+      return Status::invalid_argument("Qwen3.5 decode layer is missing its norms");
+    }
+    Status r = ctx.rms_norm_f32_f32_batched(s.hidden, *l.attn_norm, 1, h, eps, s.normed);
+    if (kind == LayerKind::linear_attention) {
+      // qwen35_runtime.cpp:2720-3034: qkv, z, beta, alpha projections; the
+      // attention core; ssm_out; residual.
+      if (r.is_ok()) r = project(ctx, l.qkv, s.normed, 1, s.a);
+      if (r.is_ok()) r = project(ctx, l.gate, s.normed, 1, s.b);
+      if (r.is_ok()) r = project(ctx, l.beta, s.normed, 1, s.c);
+      if (r.is_ok()) r = project(ctx, l.alpha, s.normed, 1, s.d);
+      if (r.is_ok()) {
+        r = run_linear_attention_chunk(ctx, plan, cache, l.linear, kind_index, 0, s.a, s.b, s.c,
+                                       s.d, 1, eps, OpOrder::fused, s.layer_ws, s.attn);
+      }
+      if (r.is_ok()) r = project(ctx, l.ssm_out, s.attn, 1, s.a);
+    } else {
+      // qwen35_runtime.cpp:3200-3400: joint Q/gate, K and V projections; the
+      // attention core with the F16 KV append at `position`; attn_output;
+      // residual.
+      if (r.is_ok()) r = project(ctx, l.q, s.normed, 1, s.a);
+      if (r.is_ok()) r = project(ctx, l.k, s.normed, 1, s.b);
+      if (r.is_ok()) r = project(ctx, l.v, s.normed, 1, s.c);
+      if (r.is_ok()) {
+        r = run_full_attention_chunk(ctx, plan, cache, l.full, kind_index, s.a, s.b, s.c, 1,
+                                     position, position, w.mrope_sections, w.rope_theta, eps,
+                                     nullptr, OpOrder::fused, s.layer_ws, s.attn);
+      }
+      if (r.is_ok()) r = project(ctx, l.output, s.attn, 1, s.a);
+    }
+    if (r.is_ok()) r = ctx.add_f32_in_place(s.hidden, s.a, h);
+    if (r.is_ok()) r = detail::ffn_block(ctx, plan, l, eps, s);
+    if (r.is_ok() && after_layer != nullptr) r = (*after_layer)(index, s.hidden);
+    return r;
+  });
+  if (!st.is_ok()) {
+    return st;
+  }
+  st = ctx.rms_norm_f32_f32_batched(s.hidden, *w.output_norm, 1, h, eps, s.normed);
+  if (!st.is_ok()) {
+    return st;
+  }
+  return detail::lm_head_argmax(ctx, w.output, s.normed, token_out);
+}
+
+// Greedy generation of `steps` tokens after `first_token` at `start_position`
+// (the decode loop of qwen35_runtime.cpp:6212-6263 with sampling off): step i
+// feeds the token of step i - 1 (first_token for i = 0) at position
+// start_position + i.  Each step is one graph batch committed once, so the host
+// waits once per token; the device keeps the tokens and they are read back
+// after the last step.  Returns the generated token ids.
+[[nodiscard]] inline Result<std::vector<std::int32_t>> greedy_decode(
+  const HipContext& ctx, const ExecutionPlan& plan, DeviceCache& cache, const ModelWeights& w,
+  DecodeScratch& s, std::int32_t first_token, std::size_t start_position, std::size_t steps,
+  const LayerHook* after_layer = nullptr) {
+  if (steps == 0) {
+    return std::vector<std::int32_t>{};
+  }
+  if (start_position + steps > plan.cache.attention_capacity_tokens) {
+    return Status::invalid_argument("Qwen3.5 decode position exceeds cache capacity");
+  }
+  Status st = s.prepare(ctx, plan, w);
+  if (!st.is_ok()) {
+    return st;
+  }
+  auto tokens = ctx.make_buffer((steps + 1) * sizeof(std::int32_t));
+  if (!tokens.is_ok()) {
+    return tokens.status();
+  }
+  st = ctx.copy_to_buffer(tokens.value(), &first_token, sizeof(first_token));
+  if (!st.is_ok()) {
+    return st;
+  }
+  auto* base = static_cast<unsigned char*>(tokens.value().data());
+  for (std::size_t i = 0; i < steps; ++i) {
+    const HipBuffer in = HipBuffer::borrow(base + i * sizeof(std::int32_t), sizeof(std::int32_t));
+    HipBuffer out =
+      HipBuffer::borrow(base + (i + 1) * sizeof(std::int32_t), sizeof(std::int32_t));
+    st = ctx.begin_graph();
+    if (st.is_ok()) {
+      st = enqueue_decode_step(ctx, plan, cache, w, s, in, out, start_position + i, after_layer);
+    }
+    if (!st.is_ok()) {
+      ctx.abort_graph();
+      return st;
+    }
+    st = ctx.commit_graph();
+    if (!st.is_ok()) {
+      return st;
+    }
+  }
+  std::vector<std::int32_t> all(steps + 1);
+  st = ctx.copy_from_buffer(tokens.value(), all.data(), all.size() * sizeof(std::int32_t));
+  if (!st.is_ok()) {
+    return st;
+  }
+  return std::vector<std::int32_t>(all.begin() + 1, all.end());
+}
+
+}  // namespace kraken::qwen35

@@ -368,6 +368,21 @@ KRAKEN_API int kraken_hip_mul_f32_row_in_place(kraken_hip_context* context,
                                                kraken_buffer target, kraken_buffer row,
                                                size_t rows, size_t row_size);
 
+/* The residual and FFN ops of a decoder layer around the hot path:
+ * add_f32_in_place (mps_backend.hpp:342-343; target += delta),
+ * silu_mul_f32_in_place (mps_backend.hpp:360-361; gate = silu(gate) * up) and
+ * rms_norm_f32_f32_batched (mps_backend.hpp:238-243; output[t] = input[t] *
+ * rsqrt(mean(input[t]^2) + eps) * weight for `tokens` rows of `size`; output
+ * may be input). */
+KRAKEN_API int kraken_hip_add_f32_in_place(kraken_hip_context* context, kraken_buffer target,
+                                           kraken_buffer delta, size_t size);
+KRAKEN_API int kraken_hip_silu_mul_f32_in_place(kraken_hip_context* context, kraken_buffer gate,
+                                                kraken_buffer up, size_t size);
+KRAKEN_API int kraken_hip_rms_norm_f32_f32_batched(kraken_hip_context* context,
+                                                   kraken_buffer input, kraken_buffer weight,
+                                                   size_t tokens, size_t size, float eps,
+                                                   kraken_buffer output);
+
 /* ---- Ragged multi-sequence decode ------------------------------------------
  * No counterpart in the reference, which serves one sequence per context
  * (README.md:540); for callers that batch the decode step of many sequences

@@ -316,7 +316,8 @@ int unary_entry(kraken_hip_context* ctx, UnaryKind kind, const char* what,
 
 int binary_entry(kraken_hip_context* ctx, BinaryKind kind, const char* what,
                  const kraken_buffer& target, const kraken_buffer& rhs, size_t rows,
-                 size_t row_size, bool rowwise) {
+                 size_t row_size, bool rowwise, const char* target_name = nullptr,
+                 const char* rhs_name = nullptr) {
   KRAKEN_TRY(check_context(ctx));
   const std::string base(what);
   size_t total = rows;
@@ -330,8 +331,10 @@ int binary_entry(kraken_hip_context* ctx, BinaryKind kind, const char* what,
     KRAKEN_TRY(check_u32(row_size, (base + " row size").c_str()));
   }
   KRAKEN_TRY(check_u32(total, (base + " size").c_str()));
-  KRAKEN_TRY(validate_f32(target, total, (base + " target").c_str()));
-  KRAKEN_TRY(validate_f32(rhs, rowwise ? row_size : total, (base + " rhs").c_str()));
+  const std::string tn = target_name != nullptr ? target_name : base + " target";
+  const std::string rn = rhs_name != nullptr ? rhs_name : base + " rhs";
+  KRAKEN_TRY(validate_f32(target, total, tn.c_str()));
+  KRAKEN_TRY(validate_f32(rhs, rowwise ? row_size : total, rn.c_str()));
   KRAKEN_TRY(begin_launch(ctx));
   if (total == 0) {
     return KRAKEN_OK;
@@ -901,6 +904,47 @@ KRAKEN_API int kraken_hip_silu_f32_in_place(kraken_hip_context* ctx, kraken_buff
 KRAKEN_API int kraken_hip_mul_f32_in_place(kraken_hip_context* ctx, kraken_buffer target,
                                            kraken_buffer rhs, size_t size) {
   return binary_entry(ctx, BinaryKind::mul, "mul", target, rhs, size, 0, false);
+}
+
+KRAKEN_API int kraken_hip_add_f32_in_place(kraken_hip_context* ctx, kraken_buffer target,
+                                           kraken_buffer delta, size_t size) {
+  return binary_entry(ctx, BinaryKind::add, "add", target, delta, size, 0, false, "add target",
+                      "add delta");
+}
+
+KRAKEN_API int kraken_hip_silu_mul_f32_in_place(kraken_hip_context* ctx, kraken_buffer gate,
+                                                kraken_buffer up, size_t size) {
+  return binary_entry(ctx, BinaryKind::silu_mul, "silu mul", gate, up, size, 0, false,
+                      "silu gate", "silu up");
+}
+
+// rms_norm_f32_f32_batched host side (mps_backend.mm:7865-7935): output[t] =
+// input[t] * rsqrt(mean(input[t]^2) + eps) * weight, one row of `size` per token.
+KRAKEN_API int kraken_hip_rms_norm_f32_f32_batched(kraken_hip_context* ctx, kraken_buffer input,
+                                                   kraken_buffer weight, size_t tokens,
+                                                   size_t size, float eps,
+                                                   kraken_buffer output) {
+  KRAKEN_TRY(check_context(ctx));
+  if (tokens == 0 || size == 0) {
+    return invalid("HIP batched rms norm dimensions must be positive");
+  }
+  KRAKEN_TRY(check_u32(tokens, "batched rms norm tokens"));
+  KRAKEN_TRY(check_u32(size, "batched rms norm size"));
+  size_t values = 0;
+  if (!checked_mul(tokens, size, values)) {
+    return invalid("HIP batched rms norm value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(input, values, "batched rms norm input"));
+  KRAKEN_TRY(validate_f32(output, values, "batched rms norm output"));
+  KRAKEN_TRY(validate_f32(weight, size, "batched rms norm weight"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_rms_norm_rows(
+    static_cast<const float*>(input.data), static_cast<const float*>(weight.data),
+    static_cast<float*>(output.data), (uint32_t)tokens, (uint32_t)size, eps, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP batched rms norm launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP batched rms norm command failed: ");
 }
 
 KRAKEN_API int kraken_hip_add_f32_row_in_place(kraken_hip_context* ctx, kraken_buffer target,

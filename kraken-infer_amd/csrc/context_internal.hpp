@@ -304,6 +304,9 @@ hipError_t launch_kquant_argmax(int format, const void* weight, size_t rows, siz
                                 const float* input, int32_t* token_out, float* probability_out,
                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+// RMSNorm of `rows` rows of `size` values, input -> output (may alias).
+hipError_t launch_rms_norm_rows(const float* input, const float* weight, float* output,
+                                uint32_t rows, uint32_t size, float eps, hipStream_t stream);
 hipError_t launch_rms_norm_heads(float* values, const float* weight, const float* gate,
                                  uint32_t tokens, uint32_t heads, uint32_t head_dim,
                                  float eps, hipStream_t stream);
@@ -321,7 +324,7 @@ hipError_t launch_copy_rows(CopyKind kind, const void* source, void* destination
                             size_t destination_offset, hipStream_t stream);
 enum class UnaryKind { sigmoid, softplus, silu };
 hipError_t launch_unary(UnaryKind kind, float* values, size_t size, hipStream_t stream);
-enum class BinaryKind { mul, add_row, mul_row };
+enum class BinaryKind { mul, add_row, mul_row, add, silu_mul };
 hipError_t launch_binary(BinaryKind kind, float* target, const float* rhs, size_t size,
                          size_t row_size, hipStream_t stream);
 

@@ -226,6 +226,32 @@ __global__ void unary_kernel(float* values, size_t size) {
 }
 
 // mul_f32_in_place / add_f32_row_in_place / mul_f32_row_in_place (mps_backend.mm:2539-2567).
+// One workgroup per row of `size` values: output = input * rsqrt(mean(input^2)
+// + eps) * weight (rms_norm_f32_f32_batched, mps_backend.mm:1890-1920).  Input and
+// output may be the same buffer: every value is read before the row is written.
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* input,
+                                                            const float* weight, float* output,
+                                                            uint32_t size, float eps) {
+  __shared__ float s_part[4];
+  const float* x = input + (size_t)blockIdx.x * size;
+  float* y = output + (size_t)blockIdx.x * size;
+  float sum = 0.0f;
+  for (uint32_t i = threadIdx.x; i < size; i += 256u) {
+    const float v = x[i];
+    sum = fmaf(v, v, sum);
+  }
+  sum = wave_sum(sum);
+  if ((threadIdx.x & 63) == 0) {
+    s_part[threadIdx.x >> 6] = sum;
+  }
+  __syncthreads();
+  const float total = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+  const float scale = 1.0f / sqrtf(total / (float)size + eps);
+  for (uint32_t i = threadIdx.x; i < size; i += 256u) {
+    y[i] = x[i] * scale * weight[i];
+  }
+}
+
 template <BinaryKind K>
 __global__ void binary_kernel(float* target, const float* rhs, size_t size, size_t row_size) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < size;
@@ -234,8 +260,14 @@ __global__ void binary_kernel(float* target, const float* rhs, size_t size, size
       target[i] *= rhs[i];
     } else if (K == BinaryKind::add_row) {
       target[i] += rhs[i % row_size];
-    } else {
+    } else if (K == BinaryKind::mul_row) {
       target[i] *= rhs[i % row_size];
+    } else if (K == BinaryKind::add) {
+      target[i] += rhs[i];
+    } else {
+      // silu(gate) * up, as silu_mul_f32_in_place writes it (mps_backend.mm:2620-2629).
+      const float g = target[i];
+      target[i] = (g / (1.0f + expf(-g))) * rhs[i];
     }
   }
 }
@@ -252,6 +284,12 @@ unsigned grid_for(size_t total, unsigned block = 256) {
 }
 
 }  // namespace
+
+hipError_t launch_rms_norm_rows(const float* input, const float* weight, float* output,
+                                uint32_t rows, uint32_t size, float eps, hipStream_t stream) {
+  rms_norm_rows_kernel<<<rows, 256, 0, stream>>>(input, weight, output, size, eps);
+  return hipGetLastError();
+}
 
 hipError_t launch_rms_norm_heads(float* values, const float* weight, const float* gate,
                                  uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps,
@@ -367,6 +405,12 @@ hipError_t launch_binary(BinaryKind kind, float* target, const float* rhs, size_
       break;
     case BinaryKind::mul_row:
       binary_kernel<BinaryKind::mul_row><<<grid, 256, 0, stream>>>(target, rhs, size, row_size);
+      break;
+    case BinaryKind::add:
+      binary_kernel<BinaryKind::add><<<grid, 256, 0, stream>>>(target, rhs, size, row_size);
+      break;
+    case BinaryKind::silu_mul:
+      binary_kernel<BinaryKind::silu_mul><<<grid, 256, 0, stream>>>(target, rhs, size, row_size);
       break;
   }
   return hipGetLastError();

@@ -82,6 +82,9 @@ SIGNATURES = {
     "kraken_hip_mul_f32_in_place": [_B, _B, _sz],
     "kraken_hip_add_f32_row_in_place": [_B, _B, _sz, _sz],
     "kraken_hip_mul_f32_row_in_place": [_B, _B, _sz, _sz],
+    "kraken_hip_add_f32_in_place": [_B, _B, _sz],
+    "kraken_hip_silu_mul_f32_in_place": [_B, _B, _sz],
+    "kraken_hip_rms_norm_f32_f32_batched": [_B, _B, _sz, _sz, _f, _B],
     "kraken_hip_matvec_q4_k_f32_device": [_B, _sz, _sz, _B, _B],
     "kraken_hip_matvec_q4_k_f32_top1": [_B, _sz, _sz, _B, _B, _B],
     "kraken_hip_matvec_q4_k_f32_argmax": [_B, _sz, _sz, _B, _B],

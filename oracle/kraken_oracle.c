@@ -354,6 +354,19 @@ void oracle_mul_f32(float* target, const float* rhs, size_t size) {
   }
 }
 
+void oracle_add_f32(float* target, const float* delta, size_t size) {
+  for (size_t i = 0; i < size; ++i) {
+    target[i] = target[i] + delta[i];
+  }
+}
+
+void oracle_silu_mul_f32(float* gate, const float* up, size_t size) {
+  for (size_t i = 0; i < size; ++i) {
+    const double g = gate[i];
+    gate[i] = (float)(g * sigmoid_d(g) * (double)up[i]);
+  }
+}
+
 void oracle_prepare_gdn_gate_beta(float* gate, float* beta, const float* gate_bias,
                                   const float* gate_scale, size_t rows, size_t row_size) {
   for (size_t r = 0; r < rows; ++r) {

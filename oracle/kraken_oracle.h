@@ -86,6 +86,10 @@ void oracle_sigmoid_f32(float* values, size_t size);
 void oracle_softplus_f32(float* values, size_t size);
 void oracle_silu_f32(float* values, size_t size);
 void oracle_mul_f32(float* target, const float* rhs, size_t size);
+/* add_f32_in_place (mps_backend.mm:2529-2537): target += delta. */
+void oracle_add_f32(float* target, const float* delta, size_t size);
+/* silu_mul_f32_in_place (mps_backend.mm:2620-2629): gate = silu(gate) * up. */
+void oracle_silu_mul_f32(float* gate, const float* up, size_t size);
 void oracle_prepare_gdn_gate_beta(float* gate, float* beta, const float* gate_bias,
                                   const float* gate_scale, size_t rows, size_t row_size);
 

@@ -63,6 +63,8 @@ def _declare(l):
     for name in ("oracle_sigmoid_f32", "oracle_softplus_f32", "oracle_silu_f32"):
         getattr(l, name).argtypes = [_f32p, _sz]
     l.oracle_mul_f32.argtypes = [_f32p, _f32p, _sz]
+    l.oracle_add_f32.argtypes = [_f32p, _f32p, _sz]
+    l.oracle_silu_mul_f32.argtypes = [_f32p, _f32p, _sz]
     l.oracle_prepare_gdn_gate_beta.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz]
     l.oracle_copy_f32_rows.argtypes = [_f32p, _f32p] + [_sz] * 6
     l.oracle_copy_f32_rows_to_f16.argtypes = [_f32p, _u16p] + [_sz] * 6
@@ -299,6 +301,24 @@ def mul(target, rhs):
     t, r = _f32(target), _f32(rhs)
     lib().oracle_mul_f32(_p(t), _p(r), t.size)
     return t
+
+
+def add(target, delta):
+    t, d = _f32(target), _f32(delta)
+    lib().oracle_add_f32(_p(t), _p(d), t.size)
+    return t
+
+
+def silu_mul(gate, up):
+    g, u = _f32(gate), _f32(up)
+    lib().oracle_silu_mul_f32(_p(g), _p(u), g.size)
+    return g
+
+
+def rms_norm_batched(values, weight, tokens, size, eps):
+    """rms_norm_f32_f32_batched (mps_backend.mm:1890-1920): the per-row RMSNorm
+    with weight, which is qk_norm_f32_batched with one head of `size`."""
+    return qk_norm_f32_batched(values, weight, tokens, 1, size, eps)
 
 
 # ------------------------------------------------------------ K-quants -----

@@ -12,17 +12,30 @@
 //       caches from raw files in <dir> (written by the test), runs one layer
 //       driver on the 0.8B plan and writes the output and the final caches
 //       back to <dir>.
+//   qwen35_driver_check gguf-info <file.gguf>
+//       No GPU needed.  Parses a GGUF file and prints its header, tensor table
+//       and metadata as lines, or "error <message>".
+//   qwen35_driver_check decode <model.gguf> <outdir> <first_token> <steps>
+//       On a GPU.  Loads a Qwen3.5-0.8B-shaped GGUF (include/kraken/gguf.hpp),
+//       uploads its tensors, runs the greedy decode loop
+//       (include/kraken/qwen35_decode.hpp) from position 0 and writes the
+//       generated tokens (tokens.i32) and the last step's LM-head input
+//       (normed.f32) to <outdir>.
 // Exits non-zero on the first failure.
+#include <algorithm>
 #include <array>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
 #include <iterator>
+#include <memory>
 #include <string>
 #include <vector>
 
+#include "kraken/gguf.hpp"
 #include "kraken/qwen35_bench.hpp"
+#include "kraken/qwen35_decode.hpp"
 #include "kraken/qwen35_layers.hpp"
 
 using kraken::hip::HipBuffer;
@@ -413,6 +426,219 @@ int run_bench(const std::string& mode, int argc, char** argv) {
   return 2;
 }
 
+// Device copies of a GGUF's tensors, by name.
+class DeviceTensors {
+ public:
+  DeviceTensors(const HipContext& ctx, const kraken::gguf::File& f,
+                const kraken::gguf::MappedData& m)
+      : ctx_(ctx), file_(f), map_(m) {}
+
+  // The tensor `name` as a projection / embedding (2-D, GGUF shape {cols, rows}),
+  // or a vector (1-D, rows = 1); missing or failing loads print and return false.
+  bool get(const std::string& name, q35::Tensor& out) {
+    const kraken::gguf::TensorInfo* t = kraken::gguf::find_tensor(file_, name);
+    if (t == nullptr) {
+      std::printf("FAIL missing tensor %s\n", name.c_str());
+      return false;
+    }
+    auto bytes = map_.tensor_bytes(*t);
+    if (!check(bytes.status(), name.c_str())) {
+      return false;
+    }
+    auto b = ctx_.make_buffer(bytes.value().second);
+    if (!check(b.status(), name.c_str()) ||
+        !check(ctx_.copy_to_buffer(b.value(), bytes.value().first, bytes.value().second),
+               name.c_str())) {
+      return false;
+    }
+    owned_.push_back(std::make_unique<HipBuffer>(std::move(b.value())));
+    out.buffer = owned_.back().get();
+    out.type = static_cast<q35::TensorType>(t->type);
+    out.cols = (std::size_t)t->shape[0];
+    out.rows = t->shape.size() > 1 ? (std::size_t)t->shape[1] : 1;
+    return true;
+  }
+  bool vec(const std::string& name, const HipBuffer*& out) {
+    q35::Tensor t;
+    if (!get(name, t)) {
+      return false;
+    }
+    out = t.buffer;
+    return true;
+  }
+
+ private:
+  const HipContext& ctx_;
+  const kraken::gguf::File& file_;
+  const kraken::gguf::MappedData& map_;
+  std::vector<std::unique_ptr<HipBuffer>> owned_;
+};
+
+int run_decode(const std::string& path, const std::string& out_dir, std::int32_t first_token,
+               std::size_t steps, bool trace) {
+  auto file = kraken::gguf::read_file(path);
+  if (!check(file.status(), "read GGUF")) {
+    return 1;
+  }
+  auto map = kraken::gguf::MappedData::open(file.value());
+  if (!check(map.status(), "map GGUF")) {
+    return 1;
+  }
+  const q35::ModelShape shape = q35::qwen35_0_8b_shape();
+  auto blocks = kraken::gguf::get_i64(file.value(), "qwen35.block_count");
+  auto width = kraken::gguf::get_i64(file.value(), "qwen35.embedding_length");
+  if (!check(blocks.status(), "block_count") || !check(width.status(), "embedding_length") ||
+      blocks.value() != shape.total_layer_count || width.value() != shape.hidden_size) {
+    std::printf("FAIL GGUF is not Qwen3.5-0.8B shaped\n");
+    return 1;
+  }
+  auto ctx_r = HipContext::create();
+  if (!check(ctx_r.status(), "create")) {
+    return 1;
+  }
+  const HipContext& ctx = ctx_r.value();
+  q35::RuntimeOptions options;
+  options.context_tokens = steps + 1;
+  auto plan = q35::build_execution_plan(shape, steps, options);
+  if (!check(plan.status(), "plan")) {
+    return 1;
+  }
+  auto cache = q35::allocate_device_cache(ctx, plan.value());
+  if (!check(cache.status(), "allocate_device_cache")) {
+    return 1;
+  }
+  DeviceTensors dt(ctx, file.value(), map.value());
+  q35::ModelWeights w;
+  if (!dt.get("token_embd.weight", w.token_embd) ||
+      !dt.vec("output_norm.weight", w.output_norm)) {
+    return 1;
+  }
+  // output.weight absent: the LM head is tied to token_embd (qwen35.cpp:45-52
+  // of llama.cpp, as the reference's loader does).
+  if (kraken::gguf::find_tensor(file.value(), "output.weight") != nullptr) {
+    if (!dt.get("output.weight", w.output)) {
+      return 1;
+    }
+  } else {
+    w.output = w.token_embd;
+  }
+  w.layers.resize(plan.value().main_layers);
+  for (std::size_t i = 0; i < plan.value().main_layers; ++i) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    q35::DecoderLayerWeights& l = w.layers[i];
+    bool ok = dt.vec(p + "attn_norm.weight", l.attn_norm) &&
+              dt.vec(p + "post_attention_norm.weight", l.post_attention_norm) &&
+              dt.get(p + "ffn_gate.weight", l.ffn_gate) && dt.get(p + "ffn_up.weight", l.ffn_up) &&
+              dt.get(p + "ffn_down.weight", l.ffn_down);
+    if (ok && plan.value().layer_kinds[i] == q35::LayerKind::linear_attention) {
+      ok = dt.get(p + "attn_qkv.weight", l.qkv) && dt.get(p + "attn_gate.weight", l.gate) &&
+           dt.get(p + "ssm_beta.weight", l.beta) && dt.get(p + "ssm_alpha.weight", l.alpha) &&
+           dt.get(p + "ssm_out.weight", l.ssm_out) &&
+           dt.vec(p + "ssm_conv1d.weight", l.linear.conv1d) &&
+           dt.vec(p + "ssm_dt.bias", l.linear.dt_bias) && dt.vec(p + "ssm_a", l.linear.ssm_a) &&
+           dt.vec(p + "ssm_norm.weight", l.linear.ssm_norm);
+    } else if (ok) {
+      ok = dt.get(p + "attn_q.weight", l.q) && dt.get(p + "attn_k.weight", l.k) &&
+           dt.get(p + "attn_v.weight", l.v) && dt.get(p + "attn_output.weight", l.output) &&
+           dt.vec(p + "attn_q_norm.weight", l.full.q_norm) &&
+           dt.vec(p + "attn_k_norm.weight", l.full.k_norm);
+    }
+    if (!ok) {
+      return 1;
+    }
+  }
+  q35::DecodeScratch scratch;
+  // With `trace`, every layer's output hidden state of every step is appended
+  // to hidden_trace.f32 (steps x layers x hidden).
+  std::vector<float> trace_rows;
+  const q35::LayerHook hook = [&](std::size_t, const HipBuffer& hidden) {
+    std::vector<float> row(plan.value().hidden_size);
+    const Status st = ctx.copy_from_buffer(hidden, row.data(), row.size() * sizeof(float));
+    trace_rows.insert(trace_rows.end(), row.begin(), row.end());
+    return st;
+  };
+  auto tokens = q35::greedy_decode(ctx, plan.value(), cache.value(), w, scratch, first_token, 0,
+                                   steps, trace ? &hook : nullptr);
+  if (trace && !write_file(out_dir + "/hidden_trace.f32", trace_rows)) {
+    std::printf("FAIL write trace\n");
+    return 1;
+  }
+  if (!check(tokens.status(), "greedy_decode")) {
+    return 1;
+  }
+  std::vector<float> normed(plan.value().hidden_size);
+  if (!check(ctx.copy_from_buffer(scratch.normed, normed.data(), normed.size() * 4), "normed")) {
+    return 1;
+  }
+  if (!write_file(out_dir + "/tokens.i32", tokens.value()) ||
+      !write_file(out_dir + "/normed.f32", normed)) {
+    std::printf("FAIL write outputs\n");
+    return 1;
+  }
+  std::printf("decode done:");
+  for (const std::int32_t t : tokens.value()) {
+    std::printf(" %d", t);
+  }
+  std::printf("\n");
+  return 0;
+}
+
+int run_gguf_info(const std::string& path) {
+  auto f = kraken::gguf::read_file(path);
+  if (!f.is_ok()) {
+    std::printf("error %s\n", f.status().message().c_str());
+    return 1;
+  }
+  const kraken::gguf::File& g = f.value();
+  std::printf("version=%u tensors=%llu metadata=%llu alignment=%llu data_offset=%llu\n",
+              g.version, (unsigned long long)g.tensor_count,
+              (unsigned long long)g.metadata_count, (unsigned long long)g.alignment,
+              (unsigned long long)g.data_offset);
+  auto map = kraken::gguf::MappedData::open(g);
+  for (const auto& t : g.tensors) {
+    std::string shape;
+    for (const auto d : t.shape) {
+      shape += (shape.empty() ? "" : ",") + std::to_string(d);
+    }
+    unsigned long long sum = 0;  // byte sum of the tensor's data, read through the mapping
+    if (map.is_ok()) {
+      auto bytes = map.value().tensor_bytes(t);
+      if (bytes.is_ok()) {
+        for (std::size_t i = 0; i < bytes.value().second; ++i) {
+          sum += bytes.value().first[i];
+        }
+      }
+    }
+    std::printf("tensor %s type=%u shape=%s offset=%llu abs=%llu bytes=%llu sum=%llu\n",
+                t.name.c_str(), t.type, shape.c_str(), (unsigned long long)t.offset,
+                (unsigned long long)t.absolute_offset, (unsigned long long)t.byte_size, sum);
+  }
+  std::vector<std::string> keys;
+  for (const auto& kv : g.metadata) {
+    keys.push_back(kv.first);
+  }
+  std::sort(keys.begin(), keys.end());
+  for (const auto& k : keys) {
+    const auto& v = g.metadata.at(k);
+    std::string val;
+    if (v.kind == kraken::gguf::ValueKind::array) {
+      val = "array[" + std::to_string(v.count) + "]";
+      if (!v.sa.empty()) val += " first=" + v.sa.front();
+      if (!v.ia.empty()) val += " first=" + std::to_string(v.ia.front());
+      if (!v.ua.empty()) val += " first=" + std::to_string(v.ua.front());
+    } else if (v.kind == kraken::gguf::ValueKind::string) {
+      val = v.s;
+    } else {
+      auto i = kraken::gguf::get_i64(g, k);
+      auto d = kraken::gguf::get_f64(g, k);
+      val = i.is_ok() ? std::to_string(i.value())
+                      : (d.is_ok() ? std::to_string(d.value()) : (v.b ? "true" : "false"));
+    }
+    std::printf("meta %s kind=%u %s\n", k.c_str(), (unsigned)v.kind, val.c_str());
+  }
+  return 0;
+}
+
 int main(int argc, char** argv) {
   const std::string mode = argc > 1 ? argv[1] : "plan";
   if (mode == "plan") {
@@ -421,8 +647,16 @@ int main(int argc, char** argv) {
   if (mode.rfind("bench-", 0) == 0) {
     return run_bench(mode, argc, argv);
   }
+  if (mode == "gguf-info" && argc >= 3) {
+    return run_gguf_info(argv[2]);
+  }
+  if (mode == "decode" && argc >= 6) {
+    return run_decode(argv[2], argv[3], (std::int32_t)std::stol(argv[4]),
+                      (std::size_t)std::stoul(argv[5]), argc > 6 && std::string(argv[6]) == "trace");
+  }
   if (argc < 4) {
-    std::printf("usage: qwen35_driver_check plan | linear <dir> <order> | full <dir> <order>\n");
+    std::printf("usage: qwen35_driver_check plan | linear <dir> <order> | full <dir> <order> | "
+                "decode <model.gguf> <outdir> <first_token> <steps>\n");
     return 2;
   }
   const q35::OpOrder order =

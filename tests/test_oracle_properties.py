@@ -298,3 +298,24 @@ def test_qwen3_qk_norm_applies_weight_after_normalising():
     got = oracle.qwen3_qk_norm(x, heads, d, w, 1e-6).reshape(heads, d)
     np.testing.assert_allclose(got, unit * w, rtol=1e-6, atol=1e-7)
     np.testing.assert_allclose(np.sqrt((unit.astype(np.float64) ** 2).mean(1)), 1.0, rtol=1e-5)
+
+
+def test_add_silu_mul_and_batched_rms_norm_closed_forms():
+    """add is the float32 sum; silu_mul is g * sigmoid(g) * up (0 at g = 0, up * g
+    for large g, -> 0 for very negative g); the batched RMSNorm is the per-row
+    RMSNorm with weight."""
+    rng = np.random.default_rng(13)
+    a = rng.standard_normal(1000).astype(np.float32)
+    b = rng.standard_normal(1000).astype(np.float32)
+    np.testing.assert_array_equal(oracle.add(a, b), a + b)
+    g = np.array([0.0, 30.0, -30.0, 1.0, -2.0], np.float32)
+    up = np.array([5.0, 2.0, 3.0, 4.0, -1.5], np.float32)
+    want = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * up
+    np.testing.assert_allclose(oracle.silu_mul(g, up), want, rtol=1e-6, atol=1e-30)
+    assert oracle.silu_mul(g, up)[0] == 0.0
+    x = (3 * rng.standard_normal(3 * 1024)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(1024)).astype(np.float32)
+    got = oracle.rms_norm_batched(x, w, 3, 1024, 1e-6).reshape(3, 1024)
+    xr = x.reshape(3, 1024).astype(np.float64)
+    ref = xr / np.sqrt((xr ** 2).mean(1, keepdims=True) + 1e-6) * w
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
