@@ -28,6 +28,7 @@ import argparse
 import json
 import os
 import sys
+import subprocess
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -598,6 +599,27 @@ def bench_kquant(torch, ctx, run, gen, shapes=(0, 1, 2, 3)):
     return out
 
 
+def bench_decode_loop(warmup=8, steps=64):
+    """Greedy decode of the whole 0.8B model (synthetic K-quant weights: every
+    layer's norms, projections, attention core and FFN, the tied Q6_K LM head
+    with device argmax), one graph batch and one host wait per token, through
+    the C++ driver (include/kraken/qwen35_decode.hpp) as
+    `qwen35_driver_check bench-decode`.  weight_GB_s counts every weight byte
+    read once per token."""
+    exe = os.path.join(ROOT, "kraken-infer_amd", "build", "qwen35_driver_check")
+    out = subprocess.run([exe, "bench-decode", str(warmup), str(steps)], capture_output=True,
+                         text=True, timeout=300)
+    if out.returncode != 0:
+        raise RuntimeError("bench-decode failed: " + out.stdout + out.stderr)
+    line = [l for l in out.stdout.splitlines() if l.startswith("bench-decode ")][-1]
+    fields = dict(kv.split("=") for kv in line.split()[1:])
+    res = {k: float(v) for k, v in fields.items()}
+    res["frac_hbm_peak"] = res["weight_GB_s"] / HBM_PEAK_GBS
+    res["note"] = ("synthetic Qwen3.5-0.8B shapes: Q6_K token_embd/LM head 248320x1024, per layer "
+                   "Q4_K/Q5_K/Q6_K projections and FFN 3584; tokens fed back greedily")
+    return res
+
+
 def bench_peaks(torch, ctx, run):
     """Achievable rates on this box, next to the published peaks.  The library's probes
     (include/kraken_hip_diag.h): a nontemporal streaming read of 2 GiB and an fp16 MFMA loop
@@ -660,9 +682,9 @@ def main():
     ap.add_argument("--kv-len", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline only, no details")
-    ap.add_argument("--sections", default="decode,prefill,gdn,c4,kquant,peaks,prefix",
+    ap.add_argument("--sections", default="decode,prefill,gdn,c4,kquant,peaks,prefix,loop",
                     help="comma-separated detail sections to run after the headline "
-                         "(decode, prefill, gdn, c4, kquant, peaks, prefix)")
+                         "(decode, prefill, gdn, c4, kquant, peaks, prefix, loop)")
     ap.add_argument("--prefill-prefixes", default="0,3072,7168",
                     help="comma-separated KV prefixes of the prefill section")
     ap.add_argument("--kquant-shapes", default="0,1,2,3",
@@ -745,6 +767,9 @@ def main():
                      f"{peaks['probe_mfma_f16_TFLOP_s']:.0f} TFLOP/s")
     run.close()
     ctx.close()
+    if "loop" in sections:
+        details["decode_loop"] = bench_decode_loop()
+        progress(f"decode loop: {details['decode_loop']['ms_per_token']:.3f} ms/token")
     if "prefix" in sections:
         details["prefix_store"] = bench_prefix()
         progress(f"prefix store: restore {details['prefix_store']['restore_GB_s']:.0f} GB/s")

@@ -24,6 +24,7 @@
 // Exits non-zero on the first failure.
 #include <algorithm>
 #include <array>
+#include <chrono>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -583,6 +584,146 @@ int run_decode(const std::string& path, const std::string& out_dir, std::int32_t
   return 0;
 }
 
+// Synthetic Qwen3.5-0.8B weights on the device for timing: random K-quant
+// blocks with f16 scales chosen so weights are a few hundredths (the decode
+// tests' recipe), f32 norms near 1.
+class SyntheticModel {
+ public:
+  explicit SyntheticModel(const HipContext& ctx) : ctx_(ctx) {}
+  std::uint64_t bytes() const { return bytes_; }
+
+  bool quant(q35::TensorType type, std::size_t rows, std::size_t cols, q35::Tensor& out) {
+    const std::size_t nb = type == q35::TensorType::q4_k ? 144 : (type == q35::TensorType::q5_k ? 176 : 210);
+    const std::size_t blocks = rows * cols / 256;
+    std::vector<std::uint8_t> data(blocks * nb);
+    for (auto& b : data) {
+      b = (std::uint8_t)(next() >> 56);
+    }
+    const float d = type == q35::TensorType::q4_k ? 1.5e-4f : (type == q35::TensorType::q5_k ? 8e-5f : 4e-5f);
+    for (std::size_t i = 0; i < blocks; ++i) {
+      std::uint8_t* blk = data.data() + i * nb;
+      const std::uint16_t dh = half_bits(d * (0.5f + unit()));
+      if (type == q35::TensorType::q6_k) {
+        std::memcpy(blk + 208, &dh, 2);
+      } else {
+        const std::uint16_t mh = half_bits(1e-3f * unit());
+        std::memcpy(blk, &dh, 2);
+        std::memcpy(blk + 2, &mh, 2);
+      }
+    }
+    if (!upload(data, out.buffer)) {
+      return false;
+    }
+    out.type = type;
+    out.rows = rows;
+    out.cols = cols;
+    return true;
+  }
+  bool vec(std::size_t n, float base, float spread, const HipBuffer*& out) {
+    std::vector<float> v(n);
+    for (auto& x : v) {
+      x = base + spread * (2.0f * unit() - 1.0f);
+    }
+    return upload(v, out);
+  }
+
+ private:
+  template <typename T>
+  bool upload(const std::vector<T>& host, const HipBuffer*& out) {
+    HipBuffer b;
+    if (!::upload(ctx_, host, b)) {
+      return false;
+    }
+    bytes_ += host.size() * sizeof(T);
+    owned_.push_back(std::make_unique<HipBuffer>(std::move(b)));
+    out = owned_.back().get();
+    return true;
+  }
+  std::uint64_t next() {  // xorshift64*
+    state_ ^= state_ >> 12;
+    state_ ^= state_ << 25;
+    state_ ^= state_ >> 27;
+    return state_ * 0x2545F4914F6CDD1DULL;
+  }
+  float unit() { return (float)(next() >> 40) / (float)(1 << 24); }
+  static std::uint16_t half_bits(float f) {  // small positive normal values only
+    std::uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const int e = (int)((x >> 23) & 0xFF) - 127 + 15;
+    return (std::uint16_t)((e << 10) | ((x >> 13) & 0x3FF));
+  }
+
+  const HipContext& ctx_;
+  std::vector<std::unique_ptr<HipBuffer>> owned_;
+  std::uint64_t bytes_{0};
+  std::uint64_t state_{0x9E3779B97F4A7C15ULL};
+};
+
+// bench-decode <warmup> <steps>: greedy decode of `steps` tokens on synthetic
+// 0.8B weights after `warmup` tokens; one graph batch and one wait per token.
+int run_bench_decode(std::size_t warmup, std::size_t steps) {
+  auto ctx_r = HipContext::create();
+  if (!check(ctx_r.status(), "create")) {
+    return 1;
+  }
+  const HipContext& ctx = ctx_r.value();
+  q35::RuntimeOptions options;
+  options.context_tokens = warmup + steps + 1;
+  auto plan = q35::build_execution_plan(q35::qwen35_0_8b_shape(), warmup + steps, options);
+  if (!check(plan.status(), "plan")) {
+    return 1;
+  }
+  auto cache = q35::allocate_device_cache(ctx, plan.value());
+  if (!check(cache.status(), "allocate_device_cache")) {
+    return 1;
+  }
+  using TT = q35::TensorType;
+  SyntheticModel sm(ctx);
+  q35::ModelWeights w;
+  const std::size_t h = 1024, ffn = 3584;
+  bool ok = sm.quant(TT::q6_k, 248320, h, w.token_embd) && sm.vec(h, 1.0f, 0.1f, w.output_norm);
+  w.output = w.token_embd;
+  w.layers.resize(plan.value().main_layers);
+  for (std::size_t i = 0; ok && i < w.layers.size(); ++i) {
+    q35::DecoderLayerWeights& l = w.layers[i];
+    ok = sm.vec(h, 1.0f, 0.1f, l.attn_norm) && sm.vec(h, 1.0f, 0.1f, l.post_attention_norm) &&
+         sm.quant(TT::q4_k, ffn, h, l.ffn_gate) && sm.quant(TT::q4_k, ffn, h, l.ffn_up) &&
+         sm.quant(TT::q6_k, h, ffn, l.ffn_down);
+    if (ok && plan.value().layer_kinds[i] == q35::LayerKind::linear_attention) {
+      ok = sm.quant(TT::q5_k, 6144, h, l.qkv) && sm.quant(TT::q4_k, 2048, h, l.gate) &&
+           sm.quant(TT::q4_k, 16, h, l.beta) && sm.quant(TT::q4_k, 16, h, l.alpha) &&
+           sm.quant(TT::q4_k, h, 2048, l.ssm_out) && sm.vec(6144 * 4, 0.0f, 0.5f, l.linear.conv1d) &&
+           sm.vec(16, 0.0f, 0.5f, l.linear.dt_bias) && sm.vec(16, -0.7f, 0.5f, l.linear.ssm_a) &&
+           sm.vec(128, 1.0f, 0.1f, l.linear.ssm_norm);
+    } else if (ok) {
+      ok = sm.quant(TT::q4_k, 4096, h, l.q) && sm.quant(TT::q4_k, 512, h, l.k) &&
+           sm.quant(TT::q6_k, 512, h, l.v) && sm.quant(TT::q4_k, h, 2048, l.output) &&
+           sm.vec(256, 1.0f, 0.1f, l.full.q_norm) && sm.vec(256, 1.0f, 0.1f, l.full.k_norm);
+    }
+  }
+  if (!ok) {
+    return 1;
+  }
+  q35::DecodeScratch scratch;
+  auto first = q35::greedy_decode(ctx, plan.value(), cache.value(), w, scratch, 11, 0, warmup);
+  if (!check(first.status(), "warmup decode")) {
+    return 1;
+  }
+  const std::int32_t next = warmup > 0 ? first.value().back() : 11;
+  const auto t0 = std::chrono::steady_clock::now();
+  auto timed = q35::greedy_decode(ctx, plan.value(), cache.value(), w, scratch, next, warmup, steps);
+  const auto t1 = std::chrono::steady_clock::now();
+  if (!check(timed.status(), "timed decode")) {
+    return 1;
+  }
+  const double sec = std::chrono::duration<double>(t1 - t0).count();
+  std::printf("bench-decode tokens=%zu warmup=%zu ms_per_token=%.4f tok_s=%.1f weight_bytes=%llu "
+              "weight_GB_s=%.1f\n",
+              steps, warmup, 1e3 * sec / (double)steps, (double)steps / sec,
+              (unsigned long long)sm.bytes(), (double)sm.bytes() * (double)steps / sec / 1e9);
+  return 0;
+}
+
 int run_gguf_info(const std::string& path) {
   auto f = kraken::gguf::read_file(path);
   if (!f.is_ok()) {
@@ -643,6 +784,9 @@ int main(int argc, char** argv) {
   const std::string mode = argc > 1 ? argv[1] : "plan";
   if (mode == "plan") {
     return run_plan();
+  }
+  if (mode == "bench-decode" && argc >= 4) {
+    return run_bench_decode((std::size_t)std::stoul(argv[2]), (std::size_t)std::stoul(argv[3]));
   }
   if (mode.rfind("bench-", 0) == 0) {
     return run_bench(mode, argc, argv);
