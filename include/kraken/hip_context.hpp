@@ -684,6 +684,49 @@ class HipContext {
       ctx_, weight.raw(), rows, row_ids.raw(), tokens, cols, output.raw()));
   }
 
+  // No counterpart in the reference: the one-token K-quant GEMV with RMSNorm or
+  // SwiGLU on its input and a residual add on its output (empty buffers when
+  // unused), and the top-1 LM head with the output norm folded in.
+  [[nodiscard]] Status kquant_matvec_fused_f32(std::uint32_t ggml_type, const HipBuffer& weight,
+                                               std::size_t rows, std::size_t cols,
+                                               const HipBuffer& input,
+                                               const HipBuffer& norm_weight, float eps,
+                                               const HipBuffer& up, const HipBuffer& residual,
+                                               HipBuffer& output) const {
+    return Status::from_code(kraken_hip_kquant_matvec_fused_f32(
+      ctx_, ggml_type, weight.raw(), rows, cols, input.raw(), norm_weight.raw(), eps, up.raw(),
+      residual.raw(), output.raw()));
+  }
+  // Up to four fused GEMVs over one input in one launch; entries of `weights`,
+  // `outputs` and `residuals` (nullptr for none) per matrix.
+  [[nodiscard]] Status kquant_matvec_multi_f32(std::size_t count, const std::uint32_t* ggml_types,
+                                               const HipBuffer* const* weights,
+                                               const std::size_t* rows, std::size_t cols,
+                                               const HipBuffer& input,
+                                               const HipBuffer& norm_weight, float eps,
+                                               const HipBuffer& up,
+                                               const HipBuffer* const* residuals,
+                                               HipBuffer* const* outputs) const {
+    kraken_buffer w[4], res[4], out[4];
+    for (std::size_t i = 0; i < count && i < 4; ++i) {
+      w[i] = weights[i]->raw();
+      res[i] = residuals[i] != nullptr ? residuals[i]->raw() : kraken_buffer{nullptr, 0};
+      out[i] = outputs[i]->raw();
+    }
+    return Status::from_code(kraken_hip_kquant_matvec_multi_f32(
+      ctx_, count, ggml_types, w, rows, cols, input.raw(), norm_weight.raw(), eps, up.raw(), res,
+      out));
+  }
+  [[nodiscard]] Status kquant_top1_fused_f32(std::uint32_t ggml_type, const HipBuffer& weight,
+                                             std::size_t rows, std::size_t cols,
+                                             const HipBuffer& input, const HipBuffer& norm_weight,
+                                             float eps, HipBuffer& token_output,
+                                             HipBuffer& probability_output) const {
+    return Status::from_code(kraken_hip_kquant_top1_fused_f32(
+      ctx_, ggml_type, weight.raw(), rows, cols, input.raw(), norm_weight.raw(), eps,
+      token_output.raw(), probability_output.raw()));
+  }
+
   // Device argmax (mps_backend.hpp:384-390).
   [[nodiscard]] Status argmax_f32_i32(const HipBuffer& values, std::size_t size,
                                       HipBuffer& output) const {

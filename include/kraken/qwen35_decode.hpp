@@ -150,11 +150,79 @@ namespace detail {
   }
 }
 
+// One-token projection with the fused GEMV: RMSNorm(input) * norm first when
+// `norm` is given, silu(input) * up when `up` is given, and the result added to
+// `residual` when given (which may be `out`).
+[[nodiscard]] inline Status project_fused(const HipContext& ctx, const Tensor& w,
+                                          const HipBuffer& input, const HipBuffer* norm,
+                                          float eps, const HipBuffer* up,
+                                          const HipBuffer* residual, HipBuffer& out) {
+  if (w.buffer == nullptr) {
+    return Status::invalid_argument("Qwen3.5 matmul weight is missing");
+  }
+  const HipBuffer none;
+  return ctx.kquant_matvec_fused_f32(static_cast<std::uint32_t>(w.type), *w.buffer, w.rows,
+                                     w.cols, input, norm != nullptr ? *norm : none, eps,
+                                     up != nullptr ? *up : none,
+                                     residual != nullptr ? *residual : none, out);
+}
+
+// Up to four one-token projections of the same input, RMSNorm(input) * norm
+// first, in one launch (separate fused GEMVs where the input is wider than one
+// launch takes).
+[[nodiscard]] inline Status project_multi(const HipContext& ctx, std::size_t count,
+                                          const Tensor* const* w, HipBuffer* const* out,
+                                          const HipBuffer& input, const HipBuffer& norm,
+                                          float eps) {
+  if (count == 0 || count > 4) {
+    return Status::invalid_argument("Qwen3.5 joint projection takes 1 to 4 weights");
+  }
+  std::uint32_t types[4];
+  std::size_t rows[4];
+  const HipBuffer* weights[4];
+  const HipBuffer* residuals[4] = {nullptr, nullptr, nullptr, nullptr};
+  for (std::size_t i = 0; i < count; ++i) {
+    if (w[i]->buffer == nullptr) {
+      return Status::invalid_argument("Qwen3.5 matmul weight is missing");
+    }
+    if (w[i]->cols != w[0]->cols) {
+      return Status::invalid_argument("Qwen3.5 joint projection weights differ in width");
+    }
+    types[i] = static_cast<std::uint32_t>(w[i]->type);
+    rows[i] = w[i]->rows;
+    weights[i] = w[i]->buffer;
+  }
+  if (w[0]->cols > 4096) {
+    for (std::size_t i = 0; i < count; ++i) {
+      Status st = project_fused(ctx, *w[i], input, &norm, eps, nullptr, nullptr, *out[i]);
+      if (!st.is_ok()) {
+        return st;
+      }
+    }
+    return Status::ok();
+  }
+  const HipBuffer none;
+  return ctx.kquant_matvec_multi_f32(count, types, weights, rows, w[0]->cols, input, norm, eps,
+                                     none, residuals, out);
+}
+
 // The FFN half of a layer (qwen35_runtime.cpp:3024-3144): hidden += down(silu(gate(n)) *
-// up(n)) with n = RMSNorm(hidden) * post_attention_norm.
+// up(n)) with n = RMSNorm(hidden) * post_attention_norm.  OpOrder::reference issues
+// the reference's six ops; OpOrder::fused three fused GEMVs.
 [[nodiscard]] inline Status ffn_block(const HipContext& ctx, const ExecutionPlan& plan,
-                                      const DecoderLayerWeights& l, float eps, DecodeScratch& s) {
+                                      const DecoderLayerWeights& l, float eps, OpOrder order,
+                                      DecodeScratch& s) {
   const std::size_t h = plan.hidden_size;
+  if (order == OpOrder::fused) {
+    const Tensor* w[2] = {&l.ffn_up, &l.ffn_gate};
+    HipBuffer* out[2] = {&s.ffn_up, &s.ffn_gate};
+    Status st = project_multi(ctx, 2, w, out, s.hidden, *l.post_attention_norm, eps);
+    if (st.is_ok()) {
+      st = project_fused(ctx, l.ffn_down, s.ffn_gate, nullptr, eps, &s.ffn_up, &s.hidden,
+                         s.hidden);
+    }
+    return st;
+  }
   Status st = ctx.rms_norm_f32_f32_batched(s.hidden, *l.post_attention_norm, 1, h, eps, s.normed);
   if (st.is_ok()) st = project(ctx, l.ffn_up, s.normed, 1, s.ffn_up);
   if (st.is_ok()) st = project(ctx, l.ffn_gate, s.normed, 1, s.ffn_gate);
@@ -170,6 +238,10 @@ namespace detail {
 // token_in[0], at sequence position `position`: embedding, every main layer,
 // output norm and the greedy LM head, whose argmax lands in token_out[0].
 // Recurrent row 0 and the F16 KV cache of `cache` are read and advanced.
+// OpOrder::reference issues the reference's op sequence (separate RMSNorm,
+// projections, residual adds and SwiGLU); OpOrder::fused folds each RMSNorm into
+// the projections that read it, SwiGLU and the residual add into the down and
+// output projections, and the output norm into the LM head.
 // `after_layer`, when given, is called with each main layer's index once its
 // output is in s.hidden (for inspection; it may wait for the device).
 using LayerHook = std::function<Status(std::size_t layer, const HipBuffer& hidden)>;
@@ -178,7 +250,8 @@ using LayerHook = std::function<Status(std::size_t layer, const HipBuffer& hidde
                                                 DeviceCache& cache, const ModelWeights& w,
                                                 DecodeScratch& s, const HipBuffer& token_in,
                                                 HipBuffer& token_out, std::size_t position,
-                                                const LayerHook* after_layer = nullptr) {
+                                                const LayerHook* after_layer = nullptr,
+                                                OpOrder order = OpOrder::fused) {
   if (w.layers.size() != plan.main_layers || w.output_norm == nullptr) {
     return Status::invalid_argument("Qwen3.5 decode weights do not match the plan");
   }
@@ -187,49 +260,80 @@ using LayerHook = std::function<Status(std::size_t layer, const HipBuffer& hidde
   }
   const std::size_t h = plan.hidden_size;
   const float eps = w.rms_eps;
+  const bool fused = order == OpOrder::fused;
   Status st = detail::embed_token(ctx, w.token_embd, token_in, h, s.hidden);
   if (!st.is_ok()) {
     return st;
   }
+  // The projections of the layer's normed input: fused, one launch normalises
+  // s.hidden and runs them all; otherwise one RMSNorm into s.normed feeds one
+  // projection each.
+  auto proj_in = [&](const Tensor& t, HipBuffer& out) { return project(ctx, t, s.normed, 1, out); };
+  // The output projection with the residual add.
+  auto proj_out = [&](const Tensor& t, const HipBuffer& in) {
+    if (fused) {
+      return detail::project_fused(ctx, t, in, nullptr, eps, nullptr, &s.hidden, s.hidden);
+    }
+    Status r = project(ctx, t, in, 1, s.a);
+    return r.is_ok() ? ctx.add_f32_in_place(s.hidden, s.a, h) : r;
+  };
   st = for_each_main_layer(plan, [&](std::size_t index, LayerKind kind, std::size_t kind_index) {
     const DecoderLayerWeights& l = w.layers[index];
     if (l.attn_norm == nullptr || l.post_attention_norm == nullptr) {
       return Status::invalid_argument("Qwen3.5 decode layer is missing its norms");
     }
-    Status r = ctx.rms_norm_f32_f32_batched(s.hidden, *l.attn_norm, 1, h, eps, s.normed);
+    Status r = fused ? Status::ok()
+                     : ctx.rms_norm_f32_f32_batched(s.hidden, *l.attn_norm, 1, h, eps, s.normed);
     if (kind == LayerKind::linear_attention) {
       // qwen35_runtime.cpp:2720-3034: qkv, z, beta, alpha projections; the
       // attention core; ssm_out; residual.
-      if (r.is_ok()) r = project(ctx, l.qkv, s.normed, 1, s.a);
-      if (r.is_ok()) r = project(ctx, l.gate, s.normed, 1, s.b);
-      if (r.is_ok()) r = project(ctx, l.beta, s.normed, 1, s.c);
-      if (r.is_ok()) r = project(ctx, l.alpha, s.normed, 1, s.d);
+      if (fused) {
+        const Tensor* t[4] = {&l.qkv, &l.gate, &l.beta, &l.alpha};
+        HipBuffer* out[4] = {&s.a, &s.b, &s.c, &s.d};
+        if (r.is_ok()) r = detail::project_multi(ctx, 4, t, out, s.hidden, *l.attn_norm, eps);
+      } else {
+        if (r.is_ok()) r = proj_in(l.qkv, s.a);
+        if (r.is_ok()) r = proj_in(l.gate, s.b);
+        if (r.is_ok()) r = proj_in(l.beta, s.c);
+        if (r.is_ok()) r = proj_in(l.alpha, s.d);
+      }
       if (r.is_ok()) {
         r = run_linear_attention_chunk(ctx, plan, cache, l.linear, kind_index, 0, s.a, s.b, s.c,
-                                       s.d, 1, eps, OpOrder::fused, s.layer_ws, s.attn);
+                                       s.d, 1, eps, order, s.layer_ws, s.attn);
       }
-      if (r.is_ok()) r = project(ctx, l.ssm_out, s.attn, 1, s.a);
+      if (r.is_ok()) r = proj_out(l.ssm_out, s.attn);
     } else {
       // qwen35_runtime.cpp:3200-3400: joint Q/gate, K and V projections; the
       // attention core with the F16 KV append at `position`; attn_output;
       // residual.
-      if (r.is_ok()) r = project(ctx, l.q, s.normed, 1, s.a);
-      if (r.is_ok()) r = project(ctx, l.k, s.normed, 1, s.b);
-      if (r.is_ok()) r = project(ctx, l.v, s.normed, 1, s.c);
+      if (fused) {
+        const Tensor* t[3] = {&l.q, &l.k, &l.v};
+        HipBuffer* out[3] = {&s.a, &s.b, &s.c};
+        if (r.is_ok()) r = detail::project_multi(ctx, 3, t, out, s.hidden, *l.attn_norm, eps);
+      } else {
+        if (r.is_ok()) r = proj_in(l.q, s.a);
+        if (r.is_ok()) r = proj_in(l.k, s.b);
+        if (r.is_ok()) r = proj_in(l.v, s.c);
+      }
       if (r.is_ok()) {
         r = run_full_attention_chunk(ctx, plan, cache, l.full, kind_index, s.a, s.b, s.c, 1,
                                      position, position, w.mrope_sections, w.rope_theta, eps,
-                                     nullptr, OpOrder::fused, s.layer_ws, s.attn);
+                                     nullptr, order, s.layer_ws, s.attn);
       }
-      if (r.is_ok()) r = project(ctx, l.output, s.attn, 1, s.a);
+      if (r.is_ok()) r = proj_out(l.output, s.attn);
     }
-    if (r.is_ok()) r = ctx.add_f32_in_place(s.hidden, s.a, h);
-    if (r.is_ok()) r = detail::ffn_block(ctx, plan, l, eps, s);
+    if (r.is_ok()) r = detail::ffn_block(ctx, plan, l, eps, order, s);
     if (r.is_ok() && after_layer != nullptr) r = (*after_layer)(index, s.hidden);
     return r;
   });
   if (!st.is_ok()) {
     return st;
+  }
+  if (fused) {
+    HipBuffer no_probability;
+    return ctx.kquant_top1_fused_f32(static_cast<std::uint32_t>(w.output.type), *w.output.buffer,
+                                     w.output.rows, w.output.cols, s.hidden, *w.output_norm, eps,
+                                     token_out, no_probability);
   }
   st = ctx.rms_norm_f32_f32_batched(s.hidden, *w.output_norm, 1, h, eps, s.normed);
   if (!st.is_ok()) {
@@ -247,7 +351,7 @@ using LayerHook = std::function<Status(std::size_t layer, const HipBuffer& hidde
 [[nodiscard]] inline Result<std::vector<std::int32_t>> greedy_decode(
   const HipContext& ctx, const ExecutionPlan& plan, DeviceCache& cache, const ModelWeights& w,
   DecodeScratch& s, std::int32_t first_token, std::size_t start_position, std::size_t steps,
-  const LayerHook* after_layer = nullptr) {
+  const LayerHook* after_layer = nullptr, OpOrder order = OpOrder::fused) {
   if (steps == 0) {
     return std::vector<std::int32_t>{};
   }
@@ -273,7 +377,8 @@ using LayerHook = std::function<Status(std::size_t layer, const HipBuffer& hidde
       HipBuffer::borrow(base + (i + 1) * sizeof(std::int32_t), sizeof(std::int32_t));
     st = ctx.begin_graph();
     if (st.is_ok()) {
-      st = enqueue_decode_step(ctx, plan, cache, w, s, in, out, start_position + i, after_layer);
+      st = enqueue_decode_step(ctx, plan, cache, w, s, in, out, start_position + i, after_layer,
+                               order);
     }
     if (!st.is_ok()) {
       ctx.abort_graph();

@@ -551,6 +551,39 @@ KRAKEN_API int kraken_hip_dequantize_rows_q6_k_f32(kraken_hip_context* context,
                                                 kraken_buffer row_ids, size_t tokens,
                                                 size_t cols, kraken_buffer output);
 
+/* No counterpart in the reference: the one-token K-quant GEMV with a decoder
+ * layer's neighbouring ops folded in, for the device decode loop.  ggml_type is
+ * the GGUF type id (12 Q4_K, 13 Q5_K, 14 Q6_K); weight, rows and cols as for
+ * matvec_*_f32_device.  output[r] = residual[r] + sum_k W[r][k] x_k, where x =
+ * input * rsqrt(mean(input^2) + eps) * norm_weight when norm_weight is given
+ * (rms_norm_f32_f32_batched), silu(input) * up when up is given
+ * (silu_mul_f32_in_place), else input; residual may be empty (then 0) or the
+ * output buffer itself (add_f32_in_place).  norm_weight and up are exclusive;
+ * they and input must be 16-byte aligned. */
+KRAKEN_API int kraken_hip_kquant_matvec_fused_f32(kraken_hip_context* context, uint32_t ggml_type,
+                                                  kraken_buffer weight, size_t rows, size_t cols,
+                                                  kraken_buffer input, kraken_buffer norm_weight,
+                                                  float eps, kraken_buffer up,
+                                                  kraken_buffer residual, kraken_buffer output);
+/* No counterpart in the reference: up to four kraken_hip_kquant_matvec_fused_f32
+ * calls that share input, norm_weight / up and eps, in one launch (the
+ * projections of one normed hidden state).  Arrays of `count` (1..4) entries
+ * give each matrix's type, weight, rows, residual (data may be NULL) and
+ * output; cols <= 4096. */
+KRAKEN_API int kraken_hip_kquant_matvec_multi_f32(
+  kraken_hip_context* context, size_t count, const uint32_t* ggml_types,
+  const kraken_buffer* weights, const size_t* rows, size_t cols, kraken_buffer input,
+  kraken_buffer norm_weight, float eps, kraken_buffer up, const kraken_buffer* residuals,
+  const kraken_buffer* outputs);
+/* No counterpart in the reference: matvec_q*_k_f32_top1 (probability_output
+ * given) or matvec_q*_k_f32_argmax (probability_output empty) with the output
+ * RMSNorm folded into the logits GEMV when norm_weight is given. */
+KRAKEN_API int kraken_hip_kquant_top1_fused_f32(kraken_hip_context* context, uint32_t ggml_type,
+                                                kraken_buffer weight, size_t rows, size_t cols,
+                                                kraken_buffer input, kraken_buffer norm_weight,
+                                                float eps, kraken_buffer token_output,
+                                                kraken_buffer probability_output);
+
 /* argmax_f32_i32 (mps_backend.hpp:384-386): output[0] = the first index of
  * the largest of values[size]; NaN never wins, -inf can; all-NaN gives size.
  * argmax_prob_f32_i32 (mps_backend.hpp:387-390): also probability_output[0]

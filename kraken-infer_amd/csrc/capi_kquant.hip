@@ -311,6 +311,40 @@ int argmax_entry(kraken_hip_context* ctx, bool with_probability, const kraken_bu
   return finish_launch(ctx, ("HIP " + w + " command failed: ").c_str());
 }
 
+// GGUF type id (12, 13, 14) -> this file's format index, or -1.
+int format_of_ggml_type(uint32_t ggml_type) {
+  return ggml_type >= 12u && ggml_type <= 14u ? (int)(ggml_type - 12u) : -1;
+}
+
+// Checks shared by the fused entries: type, weight, dimensions, input; returns
+// the format index through `format`.
+int fused_common(kraken_hip_context* ctx, const char* what, uint32_t ggml_type,
+                 const kraken_buffer& weight, size_t rows, size_t cols,
+                 const kraken_buffer& input, const kraken_buffer& norm_weight, int& format) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string p = std::string("HIP ") + what + " ";
+  format = format_of_ggml_type(ggml_type);
+  if (format < 0) {
+    return invalid(p + "weight type must be Q4_K (12), Q5_K (13) or Q6_K (14)");
+  }
+  if (weight.data == nullptr) {
+    return invalid(p + "weight buffer is not initialized");
+  }
+  Layout l;
+  KRAKEN_TRY(matvec_layout(format, rows, cols, l));
+  if (weight.byte_size < l.weight_bytes) {
+    return invalid(p + "weight buffer is too small");
+  }
+  KRAKEN_TRY(validate_f32(input, cols, (std::string(what) + " input").c_str()));
+  if (norm_weight.data != nullptr) {
+    KRAKEN_TRY(validate_f32(norm_weight, cols, (std::string(what) + " norm weight").c_str()));
+    if (((uintptr_t)norm_weight.data & 15u) != 0) {
+      return invalid(p + "norm weight buffer must be 16-byte aligned");
+    }
+  }
+  return check_alignment(format, weight, input, what);
+}
+
 }  // namespace
 
 extern "C" {
@@ -364,6 +398,127 @@ KRAKEN_API int kraken_hip_argmax_prob_f32_i32(kraken_hip_context* ctx, kraken_bu
                                               size_t size, kraken_buffer token_output,
                                               kraken_buffer probability_output) {
   return argmax_entry(ctx, true, values, size, token_output, &probability_output);
+}
+
+// No counterpart in the reference: the one-token K-quant GEMV with the
+// decoder layer's RMSNorm (or SwiGLU) on its input and residual add on its
+// output folded in (see include/kraken_hip.h).
+KRAKEN_API int kraken_hip_kquant_matvec_fused_f32(kraken_hip_context* ctx, uint32_t ggml_type,
+                                                  kraken_buffer weight, size_t rows, size_t cols,
+                                                  kraken_buffer input, kraken_buffer norm_weight,
+                                                  float eps, kraken_buffer up,
+                                                  kraken_buffer residual, kraken_buffer output) {
+  const char* what = "K-quant fused matvec";
+  int format = -1;
+  KRAKEN_TRY(fused_common(ctx, what, ggml_type, weight, rows, cols, input, norm_weight, format));
+  if (norm_weight.data != nullptr && up.data != nullptr) {
+    return invalid("HIP K-quant fused matvec takes a norm weight or an up input, not both");
+  }
+  if (up.data != nullptr) {
+    KRAKEN_TRY(validate_f32(up, cols, "K-quant fused matvec up"));
+    if (((uintptr_t)up.data & 15u) != 0) {
+      return invalid("HIP K-quant fused matvec up buffer must be 16-byte aligned");
+    }
+  }
+  if (residual.data != nullptr) {
+    KRAKEN_TRY(validate_f32(residual, rows, "K-quant fused matvec residual"));
+  }
+  KRAKEN_TRY(validate_f32(output, rows, "K-quant fused matvec output"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_kquant_matvec_fused(
+    format, weight.data, rows, cols, static_cast<const float*>(input.data),
+    static_cast<const float*>(norm_weight.data), eps, static_cast<const float*>(up.data),
+    static_cast<const float*>(residual.data), static_cast<float*>(output.data), ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP K-quant fused matvec launch failed: ") +
+                    hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP K-quant fused matvec command failed: ");
+}
+
+// No counterpart in the reference: matvec_q*_k_f32_top1 / _argmax with the
+// output norm folded into the logits GEMV (norm_weight may be empty);
+// probability_output may be empty for the argmax alone.
+KRAKEN_API int kraken_hip_kquant_top1_fused_f32(kraken_hip_context* ctx, uint32_t ggml_type,
+                                                kraken_buffer weight, size_t rows, size_t cols,
+                                                kraken_buffer input, kraken_buffer norm_weight,
+                                                float eps, kraken_buffer token_output,
+                                                kraken_buffer probability_output) {
+  const char* what = "K-quant fused top1";
+  int format = -1;
+  KRAKEN_TRY(fused_common(ctx, what, ggml_type, weight, rows, cols, input, norm_weight, format));
+  if (cols / 256u > kTop1MaxBlocksPerRow) {
+    return invalid("HIP K-quant fused top1 block count exceeds kernel limit");
+  }
+  KRAKEN_TRY(validate_i32(token_output, 1, "K-quant fused top1 token output"));
+  if (probability_output.data != nullptr) {
+    KRAKEN_TRY(validate_f32(probability_output, 1, "K-quant fused top1 probability output"));
+  }
+  KRAKEN_TRY(ensure_workspace(ctx, kquant_argmax_workspace_bytes(rows)));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_kquant_argmax(
+    format, weight.data, rows, cols, static_cast<const float*>(input.data),
+    static_cast<int32_t*>(token_output.data), static_cast<float*>(probability_output.data),
+    ctx->workspace, ctx->workspace_bytes, ctx->stream,
+    static_cast<const float*>(norm_weight.data), eps);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP K-quant fused top1 launch failed: ") + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP K-quant fused top1 command failed: ");
+}
+
+// No counterpart in the reference: up to four fused one-token GEMVs that read
+// the same input (the projections of one normed hidden state) in one launch.
+KRAKEN_API int kraken_hip_kquant_matvec_multi_f32(
+  kraken_hip_context* ctx, size_t count, const uint32_t* ggml_types, const kraken_buffer* weights,
+  const size_t* rows, size_t cols, kraken_buffer input, kraken_buffer norm_weight, float eps,
+  kraken_buffer up, const kraken_buffer* residuals, const kraken_buffer* outputs) {
+  const char* what = "K-quant multi matvec";
+  KRAKEN_TRY(check_context(ctx));
+  if (count == 0 || count > kKquantMultiMaxMatrices) {
+    return invalid("HIP K-quant multi matvec takes 1 to 4 matrices");
+  }
+  if (ggml_types == nullptr || weights == nullptr || rows == nullptr || residuals == nullptr ||
+      outputs == nullptr) {
+    return invalid("HIP K-quant multi matvec array argument is null");
+  }
+  if (cols > kKquantMultiMaxCols) {
+    return invalid("HIP K-quant multi matvec cols exceeds 4096");
+  }
+  if (norm_weight.data != nullptr && up.data != nullptr) {
+    return invalid("HIP K-quant multi matvec takes a norm weight or an up input, not both");
+  }
+  int formats[kKquantMultiMaxMatrices];
+  const void* w[kKquantMultiMaxMatrices];
+  const float* res[kKquantMultiMaxMatrices];
+  float* out[kKquantMultiMaxMatrices];
+  for (size_t i = 0; i < count; ++i) {
+    KRAKEN_TRY(fused_common(ctx, what, ggml_types[i], weights[i], rows[i], cols, input,
+                            norm_weight, formats[i]));
+    if (residuals[i].data != nullptr) {
+      KRAKEN_TRY(validate_f32(residuals[i], rows[i], "K-quant multi matvec residual"));
+    }
+    KRAKEN_TRY(validate_f32(outputs[i], rows[i], "K-quant multi matvec output"));
+    w[i] = weights[i].data;
+    res[i] = static_cast<const float*>(residuals[i].data);
+    out[i] = static_cast<float*>(outputs[i].data);
+  }
+  if (up.data != nullptr) {
+    KRAKEN_TRY(validate_f32(up, cols, "K-quant multi matvec up"));
+    if (((uintptr_t)up.data & 15u) != 0) {
+      return invalid("HIP K-quant multi matvec up buffer must be 16-byte aligned");
+    }
+  }
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_kquant_matvec_multi(
+    (uint32_t)count, formats, w, rows, cols, static_cast<const float*>(input.data),
+    static_cast<const float*>(norm_weight.data), eps, static_cast<const float*>(up.data), res,
+    out, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP K-quant multi matvec launch failed: ") +
+                    hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP K-quant multi matvec command failed: ");
 }
 
 }  // extern "C"

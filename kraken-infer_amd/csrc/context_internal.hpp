@@ -300,9 +300,28 @@ hipError_t launch_argmax(const float* values, size_t size, int32_t* token_out,
                          hipStream_t stream);
 // GEMV of one token into workspace logits, then argmax (and probability).
 size_t kquant_argmax_workspace_bytes(size_t rows);
+// input = RMSNorm(input) * norm_weight when norm_weight is given (eps as for
+// rms_norm_f32_f32_batched) before the products.
 hipError_t launch_kquant_argmax(int format, const void* weight, size_t rows, size_t cols,
                                 const float* input, int32_t* token_out, float* probability_out,
-                                void* workspace, size_t workspace_bytes, hipStream_t stream);
+                                void* workspace, size_t workspace_bytes, hipStream_t stream,
+                                const float* norm_weight = nullptr, float eps = 0.0f);
+// Up to four one-token GEMVs over the same transformed input in one launch
+// (cols / 256 <= 16), each with its own format, rows, residual and output.
+constexpr uint32_t kKquantMultiMaxMatrices = 4;
+constexpr size_t kKquantMultiMaxCols = 4096;
+hipError_t launch_kquant_matvec_multi(uint32_t count, const int* formats,
+                                      const void* const* weights, const size_t* rows,
+                                      size_t cols, const float* input, const float* norm_weight,
+                                      float eps, const float* up,
+                                      const float* const* residuals, float* const* outputs,
+                                      hipStream_t stream);
+// One-token GEMV output[r] = residual[r] (if given) + sum_k W[r][k] x_k, with x =
+// RMSNorm(input) * norm_weight (if norm_weight), silu(input) * up (if up), or input.
+hipError_t launch_kquant_matvec_fused(int format, const void* weight, size_t rows, size_t cols,
+                                      const float* input, const float* norm_weight, float eps,
+                                      const float* up, const float* residual, float* output,
+                                      hipStream_t stream);
 
 // RMSNorm of `rows` rows of `size` values, input -> output (may alias).
 hipError_t launch_rms_norm_rows(const float* input, const float* weight, float* output,

@@ -337,6 +337,390 @@ __global__ __launch_bounds__(64) void kq_gemv_kernel(GemvArgs a) {
   }
 }
 
+// One-token GEMV with the decoder layer's neighbouring ops folded in (no
+// counterpart kernel in the reference, which runs them as separate ops):
+//   XF = 1: the input is RMSNorm(input) * norm_weight (rms_norm_f32_f32_batched,
+//           mps_backend.mm:1890-1920), the scale computed by every workgroup
+//           from the whole input row;
+//   XF = 2: the input is silu(input) * up (silu_mul_f32_in_place, :2620-2629);
+//   residual != nullptr: output = residual + W x (add_f32_in_place, :2529-2537);
+//           output may be the residual buffer itself (each row's value is read
+//           and written by the same lane).
+struct FusedGemvArgs {
+  const uint8_t* weight;
+  const float* input;
+  const float* norm_weight;
+  const float* up;
+  const float* residual;
+  float* output;
+  uint32_t rows, cols, blocks_per_row;
+  float eps;
+};
+
+template <int F, int BC, int XF>
+__global__ __launch_bounds__(64) void kq_gemv_fused_kernel(FusedGemvArgs a) {
+  constexpr int LR = 8 * BC;
+  constexpr int RW = 64 / LR;
+  const int lane = threadIdx.x;
+  const uint32_t row = blockIdx.x * RW + (uint32_t)(lane / LR);
+  const bool row_ok = row < a.rows;
+  const uint32_t r = row_ok ? row : a.rows - 1u;
+  const uint32_t bl = (uint32_t)((lane % LR) / 8);
+  const uint32_t c = (uint32_t)(lane & 7);
+  const uint8_t* row_ptr = a.weight + (uint64_t)r * a.blocks_per_row * KqFormat<F>::kBytes;
+  float scale = 1.0f;
+  if constexpr (XF == 1) {
+    // cols is a multiple of 256: every lane takes cols / 256 float4s.
+    float ss = 0.0f;
+    for (uint32_t i = 4u * (uint32_t)lane; i < a.cols; i += 256u) {
+      const float4 v = *reinterpret_cast<const float4*>(a.input + i);
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+    ss = wave_sum(ss);
+    scale = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+  }
+  // The transformed input at k .. k + 3.
+  auto xin = [&](uint32_t k) __attribute__((always_inline)) {
+    float4 x = *reinterpret_cast<const float4*>(a.input + k);
+    if constexpr (XF == 1) {
+      const float4 w = *reinterpret_cast<const float4*>(a.norm_weight + k);
+      x = make_float4(x.x * scale * w.x, x.y * scale * w.y, x.z * scale * w.z, x.w * scale * w.w);
+    } else if constexpr (XF == 2) {
+      const float4 u = *reinterpret_cast<const float4*>(a.up + k);
+      x = make_float4((x.x / (1.0f + expf(-x.x))) * u.x, (x.y / (1.0f + expf(-x.y))) * u.y,
+                      (x.z / (1.0f + expf(-x.z))) * u.z, (x.w / (1.0f + expf(-x.w))) * u.w);
+    }
+    return x;
+  };
+  float s = 0.0f;
+  for (uint32_t b = bl; b < a.blocks_per_row; b += BC) {
+    ChunkDecoder<F, false> dec;
+    dec.decode(row_ptr + (uint64_t)b * KqFormat<F>::kBytes, c);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 u = xin(256u * b + dec.p0 + 4u * q);
+      const float4 v = xin(256u * b + dec.p1 + 4u * q);
+      s = fmaf(dec.v0[4 * q + 0], u.x, s);
+      s = fmaf(dec.v0[4 * q + 1], u.y, s);
+      s = fmaf(dec.v0[4 * q + 2], u.z, s);
+      s = fmaf(dec.v0[4 * q + 3], u.w, s);
+      s = fmaf(dec.v1[4 * q + 0], v.x, s);
+      s = fmaf(dec.v1[4 * q + 1], v.y, s);
+      s = fmaf(dec.v1[4 * q + 2], v.z, s);
+      s = fmaf(dec.v1[4 * q + 3], v.w, s);
+    }
+  }
+  const float total = group_sum<LR>(s);
+  if (row_ok && (lane % LR) == 0) {
+    a.output[row] = a.residual != nullptr ? a.residual[row] + total : total;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Input-stationary one-token GEMV (the decode path's matvecs, plain or with
+// the fused RMSNorm / SwiGLU / residual of kq_gemv_fused_kernel).  A row's
+// P = 8 * blocks_per_row quant chunks are spread over LR lanes (PPL chunks per
+// lane), so each lane needs the same 32 * PPL input values for every row: the
+// workgroup computes the (transformed) input once into registers and then
+// streams rows, U of them per lane in flight, each contributing one 16-byte
+// chunk load per lane.  Grid-stride over rows, so a few workgroups per CU serve
+// any row count and the input transform is paid once per workgroup.
+// ---------------------------------------------------------------------------
+
+// Block positions of chunk c's two 16-value halves (the decoders' p0 and p1).
+template <int F>
+__device__ __forceinline__ void chunk_positions(uint32_t c, uint32_t& p0, uint32_t& p1) {
+  if constexpr (F == 2) {
+    p0 = 128u * (c >> 2) + 32u * ((c & 3u) >> 1) + 16u * (c & 1u);
+    p1 = p0 + 64u;
+  } else {
+    p0 = 64u * (c >> 1) + 16u * (c & 1u);
+    p1 = p0 + 32u;
+  }
+}
+
+// The bytes one lane needs of a block's chunk c, loaded before any math.
+struct RawChunk {
+  u32x4_t a, b, c;
+  uint32_t d;
+};
+
+template <int F>
+__device__ __forceinline__ RawChunk load_chunk(const uint8_t* block, uint32_t c) {
+  RawChunk r;
+  if constexpr (F == 2) {
+    const uint64_t base = (uint64_t)(uintptr_t)block;
+    const uint8_t* b0 = reinterpret_cast<const uint8_t*>(base & ~(uint64_t)3);
+    const uint64_t mis = base & 3u;
+    const uint32_t h = c >> 2;
+    const uint32_t half = c & 1u;
+    r.a = load16_even(b0, mis + 16u * c);                           // ql
+    r.b = load16_even(b0, mis + 128u + 32u * h + 16u * half);       // qh
+    r.c = load16_even(b0, mis + 192u);                              // scales
+    r.d = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(block + 208u));
+  } else {
+    const uint32_t qs_at = F == 1 ? 48u : 16u;
+    r.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(block));  // header
+    r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(block + qs_at + 16u * c));
+    r.c = {0u, 0u, 0u, 0u};
+    if constexpr (F == 1) {
+      r.c = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t*>(block + 16u + 16u * (c & 1u)));
+    }
+    r.d = 0u;
+  }
+  return r;
+}
+
+// sum over the chunk's 32 values of w * x, x[0..15] at p0 and x[16..31] at p1;
+// the weights as the GEMV computes them (fma(d * sc, q, -dmin * m), (d * sc) * (q - 32)).
+template <int F>
+__device__ __forceinline__ float chunk_dot(const RawChunk& r, uint32_t c, const float* x,
+                                           float acc) {
+  const uint32_t words[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+  if constexpr (F == 2) {
+    const uint32_t g = (c & 3u) >> 1;
+    const uint32_t h = c >> 2;
+    const uint32_t half = c & 1u;
+    const int s_lo = (int8_t)byte_of(r.c, 8u * h + 2u * g + half);
+    const int s_hi = (int8_t)byte_of(r.c, 8u * h + 4u + 2u * g + half);
+    const float d = half_bits_to_float(r.d);
+    const float dl = d * (float)s_lo;
+    const float dh = d * (float)s_hi;
+    const uint32_t lw[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = (lw[k] & 0x0F0F0F0Fu) | (((words[k] >> (2u * g)) & 0x03030303u) << 4);
+      const uint32_t hi =
+        ((lw[k] >> 4) & 0x0F0F0F0Fu) | (((words[k] >> (2u * g + 4u)) & 0x03030303u) << 4);
+      float ql[4], qh[4];
+      bytes_to_float(lo, ql);
+      bytes_to_float(hi, qh);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc = fmaf(dl * (ql[e] - 32.0f), x[4 * k + e], acc);
+        acc = fmaf(dh * (qh[e] - 32.0f), x[16 + 4 * k + e], acc);
+      }
+    }
+  } else {
+    const uint32_t sb = c >> 1;
+    uint32_t sc0, m0, sc1, m1;
+    scale_min(r.a, 2u * sb, sc0, m0);
+    scale_min(r.a, 2u * sb + 1u, sc1, m1);
+    const float d = half_bits_to_float(r.a.x);
+    const float dmin = half_bits_to_float(r.a.x >> 16);
+    const float ds0 = d * (float)sc0, ms0 = dmin * (float)m0;
+    const float ds1 = d * (float)sc1, ms1 = dmin * (float)m1;
+    const uint32_t hw[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t lo = words[k] & 0x0F0F0F0Fu;
+      uint32_t hi = (words[k] >> 4) & 0x0F0F0F0Fu;
+      if constexpr (F == 1) {
+        lo |= ((hw[k] >> (2u * sb)) & 0x01010101u) << 4;
+        hi |= ((hw[k] >> (2u * sb + 1u)) & 0x01010101u) << 4;
+      }
+      float ql[4], qh[4];
+      bytes_to_float(lo, ql);
+      bytes_to_float(hi, qh);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc = fmaf(fmaf(ds0, ql[e], -ms0), x[4 * k + e], acc);
+        acc = fmaf(fmaf(ds1, qh[e], -ms1), x[16 + 4 * k + e], acc);
+      }
+    }
+  }
+  return acc;
+}
+
+constexpr int kXsWaves = 4;
+constexpr int kXsMaxMatrices = 4;
+
+// Up to four weight matrices that read the same input (the projections of one
+// normed hidden state): each has its format, rows, output and optional
+// residual; the workgroups of matrix m are [wg_begin[m], wg_begin[m + 1]).
+struct MultiGemvArgs {
+  const uint8_t* weight[kXsMaxMatrices];
+  float* output[kXsMaxMatrices];
+  const float* residual[kXsMaxMatrices];
+  uint32_t rows[kXsMaxMatrices];
+  int32_t format[kXsMaxMatrices];
+  uint32_t wg_begin[kXsMaxMatrices + 1];
+  uint32_t count;
+  const float* input;
+  const float* norm_weight;  // input = RMSNorm(input) * norm_weight
+  const float* up;           // input = silu(input) * up
+  uint32_t cols, blocks_per_row;
+  float eps;
+};
+
+// silu(x) * u with the hardware exp2 and reciprocal (about 2 ulp).
+__device__ __forceinline__ float silu_mul_fast(float x, float u) {
+  const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+  return x * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
+// The rows of one matrix for one workgroup (local index wl of nwg).
+template <int F, int LR, int PPL, int XF, int U>
+__device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_t wl,
+                                          uint32_t nwg) {
+  constexpr int RW = 64 / LR;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const uint32_t li = (uint32_t)(lane % LR);
+  const uint32_t slot = (uint32_t)(lane / LR);
+  const uint32_t positions = 8u * a.blocks_per_row;
+  const uint32_t rows = a.rows[m];
+  const uint8_t* weight = a.weight[m];
+  uint32_t pb[PPL], pc[PPL];
+  bool pv[PPL];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    const uint32_t pos = li + (uint32_t)LR * (uint32_t)i;
+    pv[i] = pos < positions;
+    const uint32_t pq = pv[i] ? pos : 0u;
+    pb[i] = pq >> 3;
+    pc[i] = pq & 7u;
+  }
+  const uint32_t row_bytes = a.blocks_per_row * KqFormat<F>::kBytes;
+  const uint32_t stride = nwg * (uint32_t)(kXsWaves * RW);
+  auto load_rows = [&](uint32_t r0, RawChunk (&raw)[U][PPL]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t row = r0 + (uint32_t)u * stride + slot;
+      const uint32_t rr = row < rows ? row : rows - 1u;
+      const uint8_t* rp = weight + (uint64_t)rr * row_bytes;
+#pragma unroll
+      for (int i = 0; i < PPL; ++i) {
+        raw[u][i] = load_chunk<F>(rp + pb[i] * KqFormat<F>::kBytes, pc[i]);
+      }
+    }
+  };
+  uint32_t r0 = (wl * kXsWaves + (uint32_t)wave) * RW;
+  // The first rows' weight loads go out before the input is read.
+  RawChunk cur[U][PPL];
+  load_rows(r0 < rows ? r0 : 0u, cur);
+
+  // The lane's input values (zeros at absent positions); the row's LR lanes
+  // hold the whole input once, so its sum of squares is a group sum.
+  float x[PPL][32];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    uint32_t p0, p1;
+    chunk_positions<F>(pc[i], p0, p1);
+#pragma unroll
+    for (int half_i = 0; half_i < 2; ++half_i) {
+      const uint32_t k0 = 256u * pb[i] + (half_i == 0 ? p0 : p1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float4 v = *reinterpret_cast<const float4*>(a.input + k0 + 4u * q);
+        if constexpr (XF == 2) {
+          const float4 u = *reinterpret_cast<const float4*>(a.up + k0 + 4u * q);
+          v = make_float4(silu_mul_fast(v.x, u.x), silu_mul_fast(v.y, u.y),
+                          silu_mul_fast(v.z, u.z), silu_mul_fast(v.w, u.w));
+        }
+        const bool ok = pv[i];
+        x[i][16 * half_i + 4 * q + 0] = ok ? v.x : 0.0f;
+        x[i][16 * half_i + 4 * q + 1] = ok ? v.y : 0.0f;
+        x[i][16 * half_i + 4 * q + 2] = ok ? v.z : 0.0f;
+        x[i][16 * half_i + 4 * q + 3] = ok ? v.w : 0.0f;
+      }
+    }
+  }
+  if constexpr (XF == 1) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+#pragma unroll
+      for (int e = 0; e < 32; ++e) {
+        ss = fmaf(x[i][e], x[i][e], ss);
+      }
+    }
+    ss = group_sum<LR>(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+      uint32_t p0, p1;
+      chunk_positions<F>(pc[i], p0, p1);
+#pragma unroll
+      for (int half_i = 0; half_i < 2; ++half_i) {
+        const uint32_t k0 = 256u * pb[i] + (half_i == 0 ? p0 : p1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 w = *reinterpret_cast<const float4*>(a.norm_weight + k0 + 4u * q);
+          float* xe = &x[i][16 * half_i + 4 * q];
+          xe[0] = xe[0] * scale * w.x;
+          xe[1] = xe[1] * scale * w.y;
+          xe[2] = xe[2] * scale * w.z;
+          xe[3] = xe[3] * scale * w.w;
+        }
+      }
+    }
+  }
+  const float* residual = a.residual[m];
+  float* output = a.output[m];
+  // Every lane of the wave runs the same trips, so the row reductions see all
+  // lanes; the next trip's loads are issued before this trip's math.
+  for (; r0 < rows; r0 += (uint32_t)U * stride) {
+    const uint32_t nr0 = r0 + (uint32_t)U * stride;
+    RawChunk nxt[U][PPL];
+    if (U > 1 && nr0 < rows) {
+      load_rows(nr0, nxt);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t row = r0 + (uint32_t)u * stride + slot;
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < PPL; ++i) {
+        if (pv[i]) {
+          acc = chunk_dot<F>(cur[u][i], pc[i], x[i], acc);
+        }
+      }
+      const float total = group_sum<LR>(acc);
+      if (li == 0 && row < rows) {
+        output[row] = residual != nullptr ? residual[row] + total : total;
+      }
+    }
+    if (U > 1) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) {
+          cur[u][i] = nxt[u][i];
+        }
+      }
+    } else if (nr0 < rows) {
+      load_rows(nr0, cur);
+    }
+  }
+}
+
+template <int LR, int PPL, int XF, int U>
+__global__ __launch_bounds__(64 * kXsWaves) void kq_gemv_xs_kernel(MultiGemvArgs a) {
+  int m = 0;
+#pragma unroll
+  for (int k = 1; k < kXsMaxMatrices; ++k) {
+    m += (k < (int)a.count && blockIdx.x >= a.wg_begin[k]) ? 1 : 0;
+  }
+  const uint32_t wl = blockIdx.x - a.wg_begin[m];
+  const uint32_t nwg = a.wg_begin[m + 1] - a.wg_begin[m];
+  switch (a.format[m]) {
+    case 0:
+      xs_matrix<0, LR, PPL, XF, U>(a, m, wl, nwg);
+      break;
+    case 1:
+      xs_matrix<1, LR, PPL, XF, U>(a, m, wl, nwg);
+      break;
+    default:
+      xs_matrix<2, LR, PPL, XF, U>(a, m, wl, nwg);
+      break;
+  }
+}
+
 // Dequantized rows (get_row / get_rows): one lane per 16-byte chunk, exact
 // reference arithmetic.  Row ids outside [0, rows) give zeros.
 template <int F>
@@ -704,6 +1088,124 @@ hipError_t launch_gemv_f(const GemvArgs& base, hipStream_t stream) {
   return hipSuccess;
 }
 
+template <int F, int XF>
+hipError_t launch_gemv_fused_fx(const FusedGemvArgs& a, hipStream_t stream) {
+  const uint32_t bpr = a.blocks_per_row;
+  const int bc = bpr >= 5 ? 8 : (bpr >= 3 ? 4 : (bpr == 2 ? 2 : 1));
+  const uint32_t rows_per_wg = 64u / (8u * (uint32_t)bc);
+  const dim3 grid((a.rows + rows_per_wg - 1) / rows_per_wg);
+  switch (bc) {
+    case 8:
+      kq_gemv_fused_kernel<F, 8, XF><<<grid, 64, 0, stream>>>(a);
+      break;
+    case 4:
+      kq_gemv_fused_kernel<F, 4, XF><<<grid, 64, 0, stream>>>(a);
+      break;
+    case 2:
+      kq_gemv_fused_kernel<F, 2, XF><<<grid, 64, 0, stream>>>(a);
+      break;
+    default:
+      kq_gemv_fused_kernel<F, 1, XF><<<grid, 64, 0, stream>>>(a);
+      break;
+  }
+  return hipGetLastError();
+}
+
+constexpr uint32_t kXsMaxWorkgroups = 1024;  // four per CU, over all matrices
+constexpr uint32_t kXsMaxBlocksPerRow = 16;   // two chunks per lane
+
+template <int LR, int PPL, int XF>
+hipError_t launch_xs(MultiGemvArgs a, hipStream_t stream) {
+  // Workgroups per matrix: enough to cover its rows in one trip, scaled down
+  // together when that exceeds kXsMaxWorkgroups (then every workgroup takes
+  // two rows per lane per trip, the next two prefetched).
+  constexpr uint32_t rows_per_wg = kXsWaves * (64 / LR);
+  uint32_t need[kXsMaxMatrices] = {0, 0, 0, 0};
+  uint32_t total = 0;
+  for (uint32_t m = 0; m < a.count; ++m) {
+    need[m] = (a.rows[m] + rows_per_wg - 1) / rows_per_wg;
+    total += need[m];
+  }
+  const bool one_trip = total <= kXsMaxWorkgroups;
+  a.wg_begin[0] = 0;
+  for (uint32_t m = 0; m < kXsMaxMatrices; ++m) {
+    uint32_t n = 0;
+    if (m < a.count) {
+      n = one_trip ? need[m]
+                   : (uint32_t)(((uint64_t)need[m] * kXsMaxWorkgroups + total - 1) / total);
+      n = n == 0 ? 1 : n;
+    }
+    a.wg_begin[m + 1] = a.wg_begin[m] + n;
+  }
+  const dim3 grid(a.wg_begin[a.count]);
+  if (one_trip) {
+    kq_gemv_xs_kernel<LR, PPL, XF, 1><<<grid, 64 * kXsWaves, 0, stream>>>(a);
+  } else {
+    kq_gemv_xs_kernel<LR, PPL, XF, 2><<<grid, 64 * kXsWaves, 0, stream>>>(a);
+  }
+  return hipGetLastError();
+}
+
+template <int XF>
+hipError_t launch_xs_x(const MultiGemvArgs& a, hipStream_t stream) {
+  const uint32_t chunks = 8u * a.blocks_per_row;
+  if (chunks <= 8u) return launch_xs<8, 1, XF>(a, stream);
+  if (chunks <= 16u) return launch_xs<16, 1, XF>(a, stream);
+  if (chunks <= 32u) return launch_xs<32, 1, XF>(a, stream);
+  if (chunks <= 64u) return launch_xs<64, 1, XF>(a, stream);
+  return launch_xs<64, 2, XF>(a, stream);
+}
+
+hipError_t launch_multi(const MultiGemvArgs& a, hipStream_t stream) {
+  if (a.norm_weight != nullptr) {
+    return launch_xs_x<1>(a, stream);
+  }
+  if (a.up != nullptr) {
+    return launch_xs_x<2>(a, stream);
+  }
+  return launch_xs_x<0>(a, stream);
+}
+
+template <int F>
+hipError_t launch_gemv_fused_f(const FusedGemvArgs& a, hipStream_t stream) {
+  if (a.blocks_per_row <= kXsMaxBlocksPerRow) {
+    MultiGemvArgs m{};
+    m.weight[0] = a.weight;
+    m.output[0] = a.output;
+    m.residual[0] = a.residual;
+    m.rows[0] = a.rows;
+    m.format[0] = F;
+    m.count = 1;
+    m.input = a.input;
+    m.norm_weight = a.norm_weight;
+    m.up = a.up;
+    m.cols = a.cols;
+    m.blocks_per_row = a.blocks_per_row;
+    m.eps = a.eps;
+    return launch_multi(m, stream);
+  }
+  if (a.norm_weight != nullptr) {
+    return launch_gemv_fused_fx<F, 1>(a, stream);
+  }
+  if (a.up != nullptr) {
+    return launch_gemv_fused_fx<F, 2>(a, stream);
+  }
+  return launch_gemv_fused_fx<F, 0>(a, stream);
+}
+
+hipError_t launch_gemv_fused(int format, const FusedGemvArgs& a, hipStream_t stream) {
+  switch (format) {
+    case 0:
+      return launch_gemv_fused_f<0>(a, stream);
+    case 1:
+      return launch_gemv_fused_f<1>(a, stream);
+    case 2:
+      return launch_gemv_fused_f<2>(a, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_gemv(int format, const GemvArgs& a, hipStream_t stream) {
   switch (format) {
     case 0:
@@ -737,6 +1239,11 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
                                 size_t tokens, const float* input, float* output,
                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const uint32_t bpr = (uint32_t)(cols / 256u);
+  if (tokens == 1 && bpr <= kXsMaxBlocksPerRow) {
+    FusedGemvArgs f{static_cast<const uint8_t*>(weight), input, nullptr, nullptr, nullptr, output,
+                    (uint32_t)rows, (uint32_t)cols, bpr, 0.0f};
+    return launch_gemv_fused(format, f, stream);
+  }
   if (tokens <= kKquantGemvMaxTokens) {
     // The reference's batched matvec (4 to 8 tokens) multiplies fp16-rounded
     // weights with fp32 inputs; 1 to 3 tokens stay fp32 throughout.
@@ -837,16 +1344,59 @@ size_t kquant_argmax_workspace_bytes(size_t rows) {
   return align256(rows * sizeof(float)) + argmax_workspace_bytes(rows);
 }
 
+hipError_t launch_kquant_matvec_fused(int format, const void* weight, size_t rows, size_t cols,
+                                      const float* input, const float* norm_weight, float eps,
+                                      const float* up, const float* residual, float* output,
+                                      hipStream_t stream) {
+  FusedGemvArgs a{static_cast<const uint8_t*>(weight), input, norm_weight, up, residual, output,
+                  (uint32_t)rows, (uint32_t)cols, (uint32_t)(cols / 256u), eps};
+  return launch_gemv_fused(format, a, stream);
+}
+
+hipError_t launch_kquant_matvec_multi(uint32_t count, const int* formats,
+                                      const void* const* weights, const size_t* rows,
+                                      size_t cols, const float* input, const float* norm_weight,
+                                      float eps, const float* up,
+                                      const float* const* residuals, float* const* outputs,
+                                      hipStream_t stream) {
+  if (count == 0 || count > (uint32_t)kXsMaxMatrices || cols / 256u > kXsMaxBlocksPerRow) {
+    return hipErrorInvalidValue;
+  }
+  MultiGemvArgs m{};
+  for (uint32_t i = 0; i < count; ++i) {
+    m.weight[i] = static_cast<const uint8_t*>(weights[i]);
+    m.output[i] = outputs[i];
+    m.residual[i] = residuals[i];
+    m.rows[i] = (uint32_t)rows[i];
+    m.format[i] = formats[i];
+  }
+  m.count = count;
+  m.input = input;
+  m.norm_weight = norm_weight;
+  m.up = up;
+  m.cols = (uint32_t)cols;
+  m.blocks_per_row = (uint32_t)(cols / 256u);
+  m.eps = eps;
+  return launch_multi(m, stream);
+}
+
 hipError_t launch_kquant_argmax(int format, const void* weight, size_t rows, size_t cols,
                                 const float* input, int32_t* token_out, float* probability_out,
-                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                                void* workspace, size_t workspace_bytes, hipStream_t stream,
+                                const float* norm_weight, float eps) {
   if (workspace == nullptr || workspace_bytes < kquant_argmax_workspace_bytes(rows)) {
     return hipErrorInvalidValue;
   }
   float* logits = static_cast<float*>(workspace);
-  GemvArgs a{static_cast<const uint8_t*>(weight), input, logits, (uint32_t)rows, (uint32_t)cols,
-             (uint32_t)(cols / 256u), 1u, 0u, 0u};
-  hipError_t e = launch_gemv(format, a, stream);
+  hipError_t e;
+  if (norm_weight != nullptr || cols / 256u <= kXsMaxBlocksPerRow) {
+    e = launch_kquant_matvec_fused(format, weight, rows, cols, input, norm_weight, eps, nullptr,
+                                   nullptr, logits, stream);
+  } else {
+    GemvArgs a{static_cast<const uint8_t*>(weight), input, logits, (uint32_t)rows,
+               (uint32_t)cols, (uint32_t)(cols / 256u), 1u, 0u, 0u};
+    e = launch_gemv(format, a, stream);
+  }
   if (e != hipSuccess) {
     return e;
   }

@@ -103,6 +103,11 @@ SIGNATURES = {
     "kraken_hip_matmul_q6_k_f32_device": [_B, _sz, _sz, _sz, _B, _B],
     "kraken_hip_dequantize_row_q6_k_f32": [_B, _sz, _sz, _B],
     "kraken_hip_dequantize_rows_q6_k_f32": [_B, _sz, _B, _sz, _sz, _B],
+    "kraken_hip_kquant_matvec_fused_f32": [ctypes.c_uint32, _B, _sz, _sz, _B, _B, _f, _B, _B, _B],
+    "kraken_hip_kquant_top1_fused_f32": [ctypes.c_uint32, _B, _sz, _sz, _B, _B, _f, _B, _B],
+    "kraken_hip_kquant_matvec_multi_f32": [_sz, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                           _sz, _B, _B, _f, _B, ctypes.c_void_p,
+                                           ctypes.c_void_p],
     "kraken_hip_argmax_f32_i32": [_B, _sz, _B],
     "kraken_hip_argmax_prob_f32_i32": [_B, _sz, _B, _B],
     "kraken_hip_begin_graph": [],
@@ -282,6 +287,19 @@ class Context:
         if "kraken_hip_" + name in SIGNATURES or "kraken_hip_" + name in DIAG_SIGNATURES:
             return lambda *args: self.call(name, *args)
         raise AttributeError(name)
+
+    def kquant_matvec_multi(self, ggml_types, weights, rows, cols, input, norm_weight, eps,
+                            up, residuals, outputs):
+        """kraken_hip_kquant_matvec_multi_f32 with Python sequences for the
+        per-matrix arrays (residual entries may be None)."""
+        n = len(weights)
+        types = (ctypes.c_uint32 * n)(*ggml_types)
+        ws = (KrakenBuffer * n)(*[as_buffer(w) for w in weights])
+        rs = (ctypes.c_size_t * n)(*rows)
+        res = (KrakenBuffer * n)(*[as_buffer(r) for r in residuals])
+        outs = (KrakenBuffer * n)(*[as_buffer(o) for o in outputs])
+        self.call("kquant_matvec_multi_f32", n, types, ws, rs, cols, input, norm_weight, eps, up,
+                  res, outs)
 
     def buffer(self, array=None, *, byte_size: int | None = None, dtype=np.float32):
         """Device buffer holding `array` (or `byte_size` uninitialised bytes)."""

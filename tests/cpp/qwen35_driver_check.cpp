@@ -15,12 +15,14 @@
 //   qwen35_driver_check gguf-info <file.gguf>
 //       No GPU needed.  Parses a GGUF file and prints its header, tensor table
 //       and metadata as lines, or "error <message>".
-//   qwen35_driver_check decode <model.gguf> <outdir> <first_token> <steps>
+//   qwen35_driver_check decode <model.gguf> <outdir> <first_token> <steps> [trace] [reference]
 //       On a GPU.  Loads a Qwen3.5-0.8B-shaped GGUF (include/kraken/gguf.hpp),
 //       uploads its tensors, runs the greedy decode loop
 //       (include/kraken/qwen35_decode.hpp) from position 0 and writes the
-//       generated tokens (tokens.i32) and the last step's LM-head input
-//       (normed.f32) to <outdir>.
+//       generated tokens (tokens.i32) to <outdir>; with `reference`, the
+//       reference's separate ops instead of the fused GEMVs, and also the last
+//       step's LM-head input (normed.f32); with `trace`, every layer's output
+//       hidden state (hidden_trace.f32).
 // Exits non-zero on the first failure.
 #include <algorithm>
 #include <array>
@@ -476,7 +478,7 @@ class DeviceTensors {
 };
 
 int run_decode(const std::string& path, const std::string& out_dir, std::int32_t first_token,
-               std::size_t steps, bool trace) {
+               std::size_t steps, bool trace, q35::OpOrder order) {
   auto file = kraken::gguf::read_file(path);
   if (!check(file.status(), "read GGUF")) {
     return 1;
@@ -559,7 +561,7 @@ int run_decode(const std::string& path, const std::string& out_dir, std::int32_t
     return st;
   };
   auto tokens = q35::greedy_decode(ctx, plan.value(), cache.value(), w, scratch, first_token, 0,
-                                   steps, trace ? &hook : nullptr);
+                                   steps, trace ? &hook : nullptr, order);
   if (trace && !write_file(out_dir + "/hidden_trace.f32", trace_rows)) {
     std::printf("FAIL write trace\n");
     return 1;
@@ -567,14 +569,17 @@ int run_decode(const std::string& path, const std::string& out_dir, std::int32_t
   if (!check(tokens.status(), "greedy_decode")) {
     return 1;
   }
-  std::vector<float> normed(plan.value().hidden_size);
-  if (!check(ctx.copy_from_buffer(scratch.normed, normed.data(), normed.size() * 4), "normed")) {
-    return 1;
-  }
-  if (!write_file(out_dir + "/tokens.i32", tokens.value()) ||
-      !write_file(out_dir + "/normed.f32", normed)) {
+  if (!write_file(out_dir + "/tokens.i32", tokens.value())) {
     std::printf("FAIL write outputs\n");
     return 1;
+  }
+  if (order == q35::OpOrder::reference) {
+    std::vector<float> normed(plan.value().hidden_size);
+    if (!check(ctx.copy_from_buffer(scratch.normed, normed.data(), normed.size() * 4),
+               "normed") ||
+        !write_file(out_dir + "/normed.f32", normed)) {
+      return 1;
+    }
   }
   std::printf("decode done:");
   for (const std::int32_t t : tokens.value()) {
@@ -659,9 +664,10 @@ class SyntheticModel {
   std::uint64_t state_{0x9E3779B97F4A7C15ULL};
 };
 
-// bench-decode <warmup> <steps>: greedy decode of `steps` tokens on synthetic
-// 0.8B weights after `warmup` tokens; one graph batch and one wait per token.
-int run_bench_decode(std::size_t warmup, std::size_t steps) {
+// bench-decode <warmup> <steps> [reference]: greedy decode of `steps` tokens on
+// synthetic 0.8B weights after `warmup` tokens; one graph batch and one wait per
+// token; the fused op order unless `reference`.
+int run_bench_decode(std::size_t warmup, std::size_t steps, q35::OpOrder order) {
   auto ctx_r = HipContext::create();
   if (!check(ctx_r.status(), "create")) {
     return 1;
@@ -705,13 +711,15 @@ int run_bench_decode(std::size_t warmup, std::size_t steps) {
     return 1;
   }
   q35::DecodeScratch scratch;
-  auto first = q35::greedy_decode(ctx, plan.value(), cache.value(), w, scratch, 11, 0, warmup);
+  auto first =
+    q35::greedy_decode(ctx, plan.value(), cache.value(), w, scratch, 11, 0, warmup, nullptr, order);
   if (!check(first.status(), "warmup decode")) {
     return 1;
   }
   const std::int32_t next = warmup > 0 ? first.value().back() : 11;
   const auto t0 = std::chrono::steady_clock::now();
-  auto timed = q35::greedy_decode(ctx, plan.value(), cache.value(), w, scratch, next, warmup, steps);
+  auto timed = q35::greedy_decode(ctx, plan.value(), cache.value(), w, scratch, next, warmup,
+                                  steps, nullptr, order);
   const auto t1 = std::chrono::steady_clock::now();
   if (!check(timed.status(), "timed decode")) {
     return 1;
@@ -786,7 +794,9 @@ int main(int argc, char** argv) {
     return run_plan();
   }
   if (mode == "bench-decode" && argc >= 4) {
-    return run_bench_decode((std::size_t)std::stoul(argv[2]), (std::size_t)std::stoul(argv[3]));
+    return run_bench_decode((std::size_t)std::stoul(argv[2]), (std::size_t)std::stoul(argv[3]),
+                            argc > 4 && std::string(argv[4]) == "reference" ? q35::OpOrder::reference
+                                                                            : q35::OpOrder::fused);
   }
   if (mode.rfind("bench-", 0) == 0) {
     return run_bench(mode, argc, argv);
@@ -795,8 +805,14 @@ int main(int argc, char** argv) {
     return run_gguf_info(argv[2]);
   }
   if (mode == "decode" && argc >= 6) {
+    bool trace = false;
+    q35::OpOrder order = q35::OpOrder::fused;
+    for (int i = 6; i < argc; ++i) {
+      trace = trace || std::string(argv[i]) == "trace";
+      order = std::string(argv[i]) == "reference" ? q35::OpOrder::reference : order;
+    }
     return run_decode(argv[2], argv[3], (std::int32_t)std::stol(argv[4]),
-                      (std::size_t)std::stoul(argv[5]), argc > 6 && std::string(argv[6]) == "trace");
+                      (std::size_t)std::stoul(argv[5]), trace, order);
   }
   if (argc < 4) {
     std::printf("usage: qwen35_driver_check plan | linear <dir> <order> | full <dir> <order> | "

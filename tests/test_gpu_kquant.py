@@ -275,3 +275,106 @@ def test_argmax_ties_nan_and_inf(ops, size):
         o_idx, o_p = oracle.argmax(values, probability=True)
         assert idx == o_idx, name
         assert abs(p - o_p) <= 1e-5 * abs(o_p) + 1e-12, (name, p, o_p)
+
+
+# ------------------------------------------------------------ fused GEMV ----
+
+GGML = {"q4_k": 12, "q5_k": 13, "q6_k": 14}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt,rows,cols", QWEN + [("q4_k", 16, 1024), ("q6_k", 77, 256)])
+@pytest.mark.parametrize("mode", ["norm", "swiglu", "plain"])
+@pytest.mark.parametrize("residual", [False, True])
+def test_fused_matvec_against_oracle_chain(hip_ctx, fmt, rows, cols, mode, residual):
+    """kraken_hip_kquant_matvec_fused_f32 against the oracle's separate ops: the
+    batched RMSNorm (or SwiGLU) of the input, the fp32 projection, the residual
+    add; the bound is the projection's, on the transformed input."""
+    rng = np.random.default_rng(rows + cols + len(mode) + residual)
+    w = kc.random_weight_fast(fmt, rows, cols, seed=rows)
+    x = (2 * rng.standard_normal(cols)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    up = rng.standard_normal(cols).astype(np.float32)
+    res = rng.standard_normal(rows).astype(np.float32)
+    xt = {"norm": lambda: oracle.rms_norm_batched(x, nw, 1, cols, 1e-6),
+          "swiglu": lambda: oracle.silu_mul(x, up), "plain": lambda: x}[mode]()
+    want, scale = oracle_projection(fmt, w, rows, cols, xt, 1)
+    if residual:
+        want = want + res
+    none = kh.KrakenBuffer(None, 0)
+    out = hip_ctx.buffer(res) if residual else hip_ctx.buffer(byte_size=4 * rows)
+    hip_ctx.kquant_matvec_fused_f32(
+        GGML[fmt], hip_ctx.buffer(w), rows, cols, hip_ctx.buffer(x),
+        hip_ctx.buffer(nw) if mode == "norm" else none, 1e-6,
+        hip_ctx.buffer(up) if mode == "swiglu" else none, out if residual else none, out)
+    # The norm's scale is a float32 sum in another order: allow 1e-6 relative on it.
+    check_projection(out.download(rows), want, scale * (1 + 2e-6 / TOL), f"{fmt} {mode}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_fused_top1_with_output_norm(hip_ctx, fmt):
+    rows, cols = 32768, 1024
+    rng = np.random.default_rng(9)
+    w = kc.random_weight_fast(fmt, rows, cols, seed=rows + 2)
+    x = (3 * rng.standard_normal(cols)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    xt = oracle.rms_norm_batched(x, nw, 1, cols, 1e-6)
+    want, scale = oracle_projection(fmt, w, rows, cols, xt, 1)
+    bound = TOL * scale + 1e-6
+    tok = hip_ctx.buffer(np.array([-1], np.int32))
+    prob = hip_ctx.buffer(np.array([-1], np.float32))
+    hip_ctx.kquant_top1_fused_f32(GGML[fmt], hip_ctx.buffer(w), rows, cols, hip_ctx.buffer(x),
+                                  hip_ctx.buffer(nw), 1e-6, tok, prob)
+    idx = int(tok.download(1)[0])
+    o_idx, o_p = oracle.argmax(want.astype(np.float32), probability=True)
+    assert want[idx] >= want[o_idx] - bound[idx] - bound[o_idx]
+    assert abs(float(prob.download(1)[0]) - o_p) <= (np.expm1(2 * bound.max()) + 1e-5) * o_p
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shapes", [
+    [("q5_k", 6144), ("q4_k", 2048), ("q4_k", 16), ("q4_k", 16)],   # qkv, z, beta, alpha
+    [("q4_k", 4096), ("q4_k", 512), ("q6_k", 512)],                 # q+gate, k, v
+    [("q4_k", 3584), ("q4_k", 3584)],                               # ffn up, gate
+    [("q6_k", 77)]])
+@pytest.mark.parametrize("mode", ["norm", "swiglu"])
+def test_multi_matvec_against_oracle_chain(hip_ctx, shapes, mode):
+    """kraken_hip_kquant_matvec_multi_f32: each matrix of one launch against the
+    oracle's transform and fp32 projection; the first matrix also adds a
+    residual.  A bad count or width is rejected before launch."""
+    cols = 1024
+    rng = np.random.default_rng(len(shapes) + len(mode))
+    x = (2 * rng.standard_normal(cols)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    up = rng.standard_normal(cols).astype(np.float32)
+    xt = (oracle.rms_norm_batched(x, nw, 1, cols, 1e-6) if mode == "norm"
+          else oracle.silu_mul(x, up))
+    ws = [kc.random_weight_fast(f, r, cols, seed=r + i) for i, (f, r) in enumerate(shapes)]
+    res = rng.standard_normal(shapes[0][1]).astype(np.float32)
+    outs = [hip_ctx.buffer(res)] + [hip_ctx.buffer(byte_size=4 * r) for _, r in shapes[1:]]
+    residuals = [outs[0]] + [None] * (len(shapes) - 1)
+    none = kh.KrakenBuffer(None, 0)
+    print(f"multi matvec {shapes} {mode}", flush=True)
+    hip_ctx.kquant_matvec_multi(
+        [GGML[f] for f, _ in shapes], [hip_ctx.buffer(w) for w in ws], [r for _, r in shapes],
+        cols, hip_ctx.buffer(x), hip_ctx.buffer(nw) if mode == "norm" else none, 1e-6,
+        hip_ctx.buffer(up) if mode == "swiglu" else none, residuals, outs)
+    for i, ((f, r), w) in enumerate(zip(shapes, ws)):
+        want, scale = oracle_projection(f, w, r, cols, xt, 1)
+        if i == 0:
+            want = want + res
+        check_projection(outs[i].download(r), want, scale * (1 + 2e-6 / TOL), f"{f} {r} #{i}")
+
+
+@pytest.mark.gpu
+def test_multi_matvec_rejections(hip_ctx):
+    w = hip_ctx.buffer(kc.random_weight_fast("q4_k", 16, 8192, seed=1))
+    x = hip_ctx.buffer(np.ones(8192, np.float32))
+    out = hip_ctx.buffer(byte_size=64)
+    none = kh.KrakenBuffer(None, 0)
+    with pytest.raises(kh.KrakenError, match="cols exceeds 4096"):
+        hip_ctx.kquant_matvec_multi([12], [w], [16], 8192, x, none, 1e-6, none, [None], [out])
+    with pytest.raises(kh.KrakenError, match="1 to 4 matrices"):
+        hip_ctx.kquant_matvec_multi([12] * 5, [w] * 5, [16] * 5, 1024, x, none, 1e-6, none,
+                                    [None] * 5, [out] * 5)

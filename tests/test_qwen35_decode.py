@@ -11,10 +11,11 @@ GPU: `qwen35_driver_check decode` loads a synthetic Qwen3.5-0.8B GGUF
 and one host wait per token, the next token kept on the device) and must
 produce the oracle chain's tokens step by step.  A step may pick a different
 token only where the oracle's two logits are within 5e-3 of each other (then
-the oracle continues from the device's token); the last step's LM-head input
-must match the oracle's within 5e-3, and a second run that reads the hidden
-state back after every layer must match the oracle layer by layer, step by
-step (1e-3 of the state's magnitude).
+the oracle continues from the device's token).  The run with the reference's
+separate ops must give the same tokens and a last-step LM-head input within
+5e-3 of the oracle's; runs of both op orders that read the hidden state back
+after every layer must match the oracle layer by layer, step by step (1e-3 of
+the state's magnitude).
 """
 import os
 import struct
@@ -124,14 +125,14 @@ def test_greedy_decode_matches_oracle_chain(tmp_path):
     path = tmp_path / "qwen35-0.8b-synthetic.gguf"
     qc.write_gguf(path, model)
     print(f"decode: GGUF written ({os.path.getsize(path) >> 20} MiB)", flush=True)
+    # The fused op order (the default), plain: one batch and one wait per token.
     r = run("decode", path, tmp_path, first, steps, timeout=300)
     print(r.stdout[-2000:], flush=True)
     assert r.returncode == 0, r.stdout + r.stderr
     got = np.fromfile(tmp_path / "tokens.i32", np.int32)
-    normed = np.fromfile(tmp_path / "normed.f32", np.float32)
     assert got.size == steps
     dec = qc.OracleDecoder(model, steps + 1)
-    token, switched = first, 0
+    token, switched, ref_normed = first, 0, None
     for i in range(steps):
         want, logits, ref_normed = dec.step(token, i)
         if got[i] != want:
@@ -141,22 +142,32 @@ def test_greedy_decode_matches_oracle_chain(tmp_path):
         print(f"step {i}: device {got[i]} oracle {want}", flush=True)
         token = int(got[i])
     assert switched <= 1
-    np.testing.assert_allclose(normed, ref_normed, rtol=5e-3, atol=5e-3)
-    # The same decode with the hidden state read back after every layer: each
-    # of the 6 x 24 layer outputs against the oracle's (the oracle fed the
-    # device's tokens), within 1e-3 of the state's largest magnitude.
-    r = run("decode", path, tmp_path, first, steps, "trace", timeout=300)
+    # The reference's separate ops: the same tokens, and the last step's LM-head
+    # input against the oracle's.
+    r = run("decode", path, tmp_path, first, steps, "reference", timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert np.array_equal(np.fromfile(tmp_path / "tokens.i32", np.int32), got)
-    trace = np.fromfile(tmp_path / "hidden_trace.f32", np.float32).reshape(steps, qc.LAYERS, -1)
-    dec = qc.OracleDecoder(model, steps + 1)
-    token, worst = first, 0.0
-    for i in range(steps):
-        ref = []
-        dec.step(token, i, ref)
-        for layer, want in enumerate(ref):
-            err = float(np.abs(trace[i, layer] - want).max()) / max(1.0, float(np.abs(want).max()))
-            worst = max(worst, err)
-            assert err <= 1e-3, (i, layer, err)
-        token = int(got[i])
-    print(f"worst per-layer relative error {worst:.2e}", flush=True)
+    normed = np.fromfile(tmp_path / "normed.f32", np.float32)
+    np.testing.assert_allclose(normed, ref_normed, rtol=5e-3, atol=5e-3)
+    # Both orders with the hidden state read back after every layer: each of the
+    # 6 x 24 layer outputs against the oracle's (fed the device's tokens), within
+    # 1e-3 of the state's largest magnitude.
+    for order in ("fused", "reference"):
+        args = ["trace"] + (["reference"] if order == "reference" else [])
+        r = run("decode", path, tmp_path, first, steps, *args, timeout=300)
+        assert r.returncode == 0, r.stdout + r.stderr
+        assert np.array_equal(np.fromfile(tmp_path / "tokens.i32", np.int32), got)
+        trace = np.fromfile(tmp_path / "hidden_trace.f32", np.float32).reshape(steps, qc.LAYERS,
+                                                                                 -1)
+        dec = qc.OracleDecoder(model, steps + 1)
+        token, worst = first, 0.0
+        for i in range(steps):
+            ref = []
+            dec.step(token, i, ref)
+            for layer, want in enumerate(ref):
+                err = float(np.abs(trace[i, layer] - want).max()) / max(
+                    1.0, float(np.abs(want).max()))
+                worst = max(worst, err)
+                assert err <= 1e-3, (order, i, layer, err)
+            token = int(got[i])
+        print(f"{order}: worst per-layer relative error {worst:.2e}", flush=True)
