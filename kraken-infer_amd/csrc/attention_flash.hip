@@ -16,15 +16,24 @@
 //    and its 512 registers (Q 64, O 128, two score tiles 64, P 16, fragment read
 //    pipelines).
 //  * K and V tiles (64 keys) are copied global -> LDS by the gfx950
-//    direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds), double buffered:
-//    at the top of iteration t the copies of tile t+1 are issued, so every copy
-//    has a whole iteration to land and no register holds staging data.  Rows stay row-major (512 bytes per key); the 16-byte chunks
-//    of each row are XOR-swizzled (K by row % 16, V by 4 * (row % 4)) by choosing
-//    which global chunk each lane fetches, which keeps the fragment reads below
-//    free of bank conflicts.  One barrier per tile publishes the copies.
-//  * Per tile a wave computes S^T = K Q^T, the softmax, then PV; the LDS
-//    fragment reads of both products run several MFMAs ahead through explicit
-//    register rings so that LDS latency stays off the MFMA issue.  S^T per 32 keys
+//    direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds), double buffered,
+//    so no register holds staging data.  Rows stay row-major (512 bytes per
+//    key); the 16-byte chunks of each row are XOR-swizzled (K by row % 16, V by
+//    4 * (row % 4)) by choosing which global chunk each lane fetches, which
+//    keeps the fragment reads below free of bank conflicts.  One barrier per
+//    tile publishes the copies.
+//  * Software pipeline, one step per tile t: S^T of tile t+1 runs on the MFMA
+//    pipe while the VALU does tile t's mask, max and exponentials (pinned
+//    between the MFMAs; the compiler would otherwise sink them to their use),
+//    and the copies of V(t+1) and K(t+2) are spread over the same MFMAs; then
+//    O += V^T P^T for tile t.  With one wave per SIMD every instruction costs an
+//    issue slot, so the loop keeps its non-MFMA instructions few: one buffer
+//    resource per workgroup for K and one for V, M0 walked from copy to copy
+//    (nothing else in the kernel touches M0; tests/test_isa_m0.py checks the
+//    ISA), Q held in AGPRs (the MFMA reads its B operand there), which leaves
+//    the architectural VGPRs to scores, P and the fragment rings without spills.
+//  * The LDS fragment reads of both products run several MFMAs ahead through
+//    explicit register rings so that LDS latency stays off the MFMA issue.  S^T per 32 keys
 //    (keys x queries, one 32x32 MFMA tile over 16 k-steps of 16 dims; lane l
 //    owns query column l%32).  The accumulator's registers are already the B
 //    operand of O^T = V^T P^T (dims x queries, 8 tiles of 32 dims, 4 k-steps of
@@ -59,6 +68,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
+#include <type_traits>
 
 #include "context_internal.hpp"
 #include "device_common.hpp"
@@ -71,6 +81,7 @@ constexpr int kQTile = 32;             // query tokens per workgroup
 constexpr int kKTile = 64;             // keys per LDS tile (two 32-key halves)
 constexpr int kRowHalfs = kD;          // an LDS row is a whole 512-byte key row
 constexpr int kTileHalfs = kKTile * kRowHalfs;  // 32 KB per K or V tile
+constexpr uint32_t kStageBytes = 2u * kTileHalfs;
 constexpr float kRescaleSlack = 8.0f;  // log2 headroom before O is rescaled
 
 struct FlashParams {
@@ -146,21 +157,79 @@ __device__ __forceinline__ CopyOffsets<W> copy_offsets(uint32_t row_bytes, uint3
   return c;
 }
 
-// Copies one 64-key tile (keys kt..kt+63) of K (kV false) or V into an LDS
-// stage.  Copy i reads through a resource based at row kt + 2 i W whose byte
-// count ends at key_end, so rows at or past key_end read as zeros; all of the
-// per-copy arithmetic is scalar.
+// The K or V rows of one workgroup: a buffer resource over the layer's first
+// key_end rows (rows at or past key_end read as zeros without a memory access;
+// the host keeps every byte offset below 2^31), the row size and the LDS byte
+// address of this wave's first copy slot in stage 0.
+struct TileSource {
+  i32x4_t rsrc;
+  uint32_t row_bytes;
+  uint32_t lds;
+};
+
+// One direct-to-LDS copy of 16 bytes per lane (as copy16_to_lds) with M0 given
+// as a scalar byte address.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void copy16_to_lds_m0(i32x4_t rsrc, uint32_t voffset, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Copy i of the 64-key tile starting at key row `row` into the stage whose LDS
+// byte address (plus this wave's slot) is `stage_lds`: two key rows per wave,
+// rows row + 2 (i W + wave) + lane / 32.  Scalar arithmetic plus one vector add.
 template <int W, bool kV>
-__device__ __forceinline__ void issue_tile_copy(const half_t* layer_base, half_t* stage,
-                                                uint32_t kt, uint32_t key_end, uint32_t row_bytes,
-                                                const CopyOffsets<W>& off, int wave) {
+__device__ __forceinline__ void issue_copy(const TileSource& src, const CopyOffsets<W>& off,
+                                           uint32_t row, uint32_t stage_lds, int i) {
+  const uint32_t row_off = (row + 2u * i * W) * src.row_bytes;
+  const uint32_t voff =
+    (kV ? off.v[i % CopyOffsets<W>::kV] : off.k[i % CopyOffsets<W>::kK]) + row_off;
+  copy16_to_lds_m0(src.rsrc, voff, stage_lds + (uint32_t)(i * W * 2 * kRowHalfs * 2));
+}
+
+// Copy i of a tile with M0 already holding its LDS address: the copy, then M0
+// moved on by kStep bytes (the next copy of the tile) or set to `next` (the
+// first copy of the other tile).  Whatever the caller issues between two copies
+// covers the one wait state an M0 write needs before an LDS-DMA load.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <int W, bool kV, int kStep>
+__device__ __forceinline__ void issue_copy_seq(const TileSource& src, const CopyOffsets<W>& off,
+                                               uint32_t row, int i, bool last, uint32_t next) {
+  const uint32_t voff = (kV ? off.v[i % CopyOffsets<W>::kV] : off.k[i % CopyOffsets<W>::kK]) +
+                        (row + 2u * i * W) * src.row_bytes;
+  if (last) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds\n\ts_mov_b32 m0, %2"
+                 :
+                 : "v"(voff), "s"(src.rsrc), "s"(next)
+                 : "memory", "m0");
+  } else {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds\n\ts_add_u32 m0, m0, %2"
+                 :
+                 : "v"(voff), "s"(src.rsrc), "n"(kStep)
+                 : "memory", "m0");
+  }
+}
+
+__device__ __forceinline__ void set_m0(uint32_t v) {
+  asm volatile("s_mov_b32 m0, %0" : : "s"(v) : "m0");
+}
+#pragma clang diagnostic pop
+
+// Copies per wave of one K or V tile.
+template <int W>
+constexpr int kCopiesPerTile = (kKTile / 2) / W;
+
+template <int W, bool kV>
+__device__ __forceinline__ void issue_tile_copy(const TileSource& src, const CopyOffsets<W>& off,
+                                                uint32_t row, uint32_t stage_lds) {
 #pragma unroll
-  for (int i = 0; i < (kKTile / 2) / W; ++i) {
-    const uint32_t row0 = kt + 2u * i * W;
-    const uint32_t bytes = key_end > row0 ? (key_end - row0) * row_bytes : 0u;
-    const i32x4_t rsrc = rsrc_words(layer_base + (size_t)row0 * (row_bytes / 2u), bytes);
-    const uint32_t voff = kV ? off.v[i % CopyOffsets<W>::kV] : off.k[i % CopyOffsets<W>::kK];
-    copy16_to_lds(rsrc, voff, stage + (i * W + wave) * 2 * kRowHalfs);
+  for (int i = 0; i < kCopiesPerTile<W>; ++i) {
+    issue_copy<W, kV>(src, off, row, stage_lds, i);
   }
 }
 
@@ -178,7 +247,9 @@ void flash256_kernel(FlashParams p) {
   constexpr int W = GW;  // waves
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;     // head slot
+  // Head slot; readfirstlane makes it a scalar, so the copies' resources and
+  // LDS destinations are scalar arithmetic.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5;       // lane half
   const int n = lane & 31;       // query column owned by this lane
   const uint32_t G = p.heads / p.kv_heads;
@@ -230,10 +301,15 @@ void flash256_kernel(FlashParams p) {
   const half_t* k_layer = p.key_cache + layer_elems;
   const half_t* v_layer = p.value_cache + layer_elems;
   const CopyOffsets<W> coff = copy_offsets<W>(row_bytes, kvh * kD * 2u, wave, lane);
+  const uint32_t slot_bytes = (uint32_t)wave * 2u * kRowHalfs * 2u;
+  const TileSource ksrc{rsrc_words(k_layer, key_end * row_bytes), row_bytes,
+                        (uint32_t)(uintptr_t)(lds_void_t*)s_k + slot_bytes};
+  const TileSource vsrc{rsrc_words(v_layer, key_end * row_bytes), row_bytes,
+                        (uint32_t)(uintptr_t)(lds_void_t*)s_v + slot_bytes};
 
   // Tile 0's copies go out before the query is loaded.
-  issue_tile_copy<W, false>(k_layer, s_k, key_begin, key_end, row_bytes, coff, wave);
-  issue_tile_copy<W, true>(v_layer, s_v, key_begin, key_end, row_bytes, coff, wave);
+  issue_tile_copy<W, false>(ksrc, coff, key_begin, ksrc.lds);
+  issue_tile_copy<W, true>(vsrc, coff, key_begin, vsrc.lds);
 
   // Q^T as the B operand of S^T = K Q^T: lane holds query n, dims 16*step + 8*h + j.
   half8_t qf[kD / 16];
@@ -251,6 +327,12 @@ void flash256_kernel(FlashParams p) {
                          (half_t)(a.w * qmask), (half_t)(b.x * qmask), (half_t)(b.y * qmask),
                          (half_t)(b.z * qmask), (half_t)(b.w * qmask)};
     }
+    // Q stays in AGPRs (an MFMA reads its B operand from either file), which
+    // leaves the architectural VGPRs to the scores, P and the fragment rings.
+#pragma unroll
+    for (int step = 0; step < kD / 16; ++step) {
+      asm volatile("" : "+a"(qf[step]));
+    }
   }
 
   float16_t o[kD / 32];  // O^T tiles: dims 32*dt + c_row(r, h), query n
@@ -263,9 +345,18 @@ void flash256_kernel(FlashParams p) {
   const float c = p.scale_log2;
 
   // K fragment reads: row 32*half + n, logical chunk 2*step + h at physical
-  // chunk (2*step + h) ^ (row % 16) = 2*step ^ u.
+  // chunk (2*step + h) ^ (row % 16) = 2*step ^ u.  For step s + 8 that is chunk
+  // 16 + (2s ^ u), 256 bytes past step s's, so 8 byte offsets cover the 16
+  // steps; they stay in registers (the empty asm hides their origin, so they
+  // are not recomputed at each read) and stage, key half and the step's high
+  // bit enter as immediates.
   const int u = h ^ (n & 15);
-  const int k_lane = n * kRowHalfs;
+  uint32_t k_byte[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    k_byte[s] = 2u * (uint32_t)(n * kRowHalfs + 8 * ((2 * s) ^ u));
+    asm volatile("" : "+v"(k_byte[s]));
+  }
   // V^T fragment reads (ds_read_b64_tr_b16): lane L = 16 g + 4 e + q of group g
   // (h = g / 2, 16-dim group gd = g % 2) supplies row 16 ks + 4h + e (+8 for the
   // high four keys), dims 32 dt + 16 gd + 4q, i.e. physical chunk
@@ -273,41 +364,48 @@ void flash256_kernel(FlashParams p) {
   // dt >= 4).
   const int e = (lane >> 2) & 3;
   const int v_lane = (4 * h + e) * kRowHalfs + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  int v_addr[4];
+  uint32_t v_byte[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    v_addr[b] = v_lane + 32 * (b ^ e);
+    v_byte[b] = 2u * (uint32_t)(v_lane + 32 * (b ^ e)) + kStageBytes;  // toggled at step 0
+    asm volatile("" : "+v"(v_byte[b]));
   }
+  // The offsets also carry the LDS stage (bit 15: stages are 32 KB apart and
+  // s_k, s_v start stage 0), toggled once per step.
+  auto kfrag = [&](int i) {  // read i: step i / 2, key half i % 2
+    const int s = i >> 1;
+    const char* p =
+      reinterpret_cast<const char*>(s_k + (i & 1) * 32 * kRowHalfs + 128 * (s >> 3));
+    return *reinterpret_cast<const half8_t*>(p + k_byte[s & 7]);
+  };
+  auto vfrag = [&](int i) {  // read i: k-step i / 8, dim tile i % 8
+    const int ks = i >> 3;
+    const int dt = i & 7;
+    const char* p =
+      reinterpret_cast<const char*>(s_v + 128 * (dt >> 2) + 16 * ks * kRowHalfs) + v_byte[dt & 3];
+    const half_t* vp = reinterpret_cast<const half_t*>(p);
+    const half4_t lo = read_tr16(vp);
+    const half4_t hi = read_tr16(vp + 8 * kRowHalfs);
+    return half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
 
-  // S^T of one 64-key tile: s0 = keys 0..31, s1 = keys 32..63.  The 32 fragment
-  // reads run kRing MFMAs ahead through an explicit register ring, which keeps
-  // the LDS latency off the MFMA issue.
-  constexpr int kRing = 6;   // K fragment reads in flight
+  constexpr int kRing = 4;   // K fragment reads in flight
   constexpr int kVRing = 4;  // V fragment read pairs in flight
-  auto scores = [&](const half_t* kst, float16_t& s0, float16_t& s1) {
+  // S^T of tile 0 (no softmax to overlap yet).
+  auto first_scores = [&](float16_t& s0, float16_t& s1) {
     s0 = float16_t{};
     s1 = float16_t{};
-    // The swizzled offsets are recomputed here (two VALU ops per read) rather
-    // than hoisted out of the tile loop, where 16 of them would pin registers.
-    int uu = u;
-    asm volatile("" : "+v"(uu));
-    auto frag = [&](int i) {  // read i: step i / 2, key half i % 2
-      const int off = 8 * ((2 * (i >> 1)) ^ uu) + (i & 1) * 32 * kRowHalfs;
-      return *reinterpret_cast<const half8_t*>(&kst[k_lane + off]);
-    };
-    // Scheduling barriers keep this block in source order: the machine
-    // scheduler would otherwise sink every read to just before its MFMA.
     half8_t ring[kRing];
 #pragma unroll
     for (int i = 0; i < kRing; ++i) {
-      ring[i] = frag(i);
+      ring[i] = kfrag(i);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < kD / 8; ++i) {
       const half8_t a = ring[i % kRing];
       if (i + kRing < kD / 8) {
-        ring[i % kRing] = frag(i + kRing);
+        ring[i % kRing] = kfrag(i + kRing);
       }
       if (i & 1) {
         s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[i >> 1], s1, 0, 0, 0);
@@ -318,22 +416,66 @@ void flash256_kernel(FlashParams p) {
     }
   };
 
-  // Iteration t: publish tile t's K/V copies, start the copies of tile t+1, then
-  // S^T of tile t, its softmax, and its PV.
-  auto iteration = [&](uint32_t t) __attribute__((always_inline)) {
+  // Step t (software pipelined): S^T of tile t is in (c0, c1).  After the
+  // barrier that publishes K of tile t+1 and V of tile t, the copies of K(t+2)
+  // and V(t+1) go out; then S^T of tile t+1 runs on the MFMA pipe into (n0, n1)
+  // while the VALU does tile t's mask, max and exponentials; then O += V^T P^T
+  // for tile t, which also covers the last exponentials.  Stage parity
+  // par = t % 2: K(t+1) sits in stage par ^ 1, V(t) in stage par.
+  auto step = [&](auto has_next, uint32_t t, float16_t& c0, float16_t& c1, float16_t& n0,
+                  float16_t& n1) __attribute__((always_inline)) {
+    constexpr bool kNext = decltype(has_next)::value;
+    const uint32_t par = t & 1u;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      k_byte[s] ^= kStageBytes;
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      v_byte[b] ^= kStageBytes;
+    }
     wait_tile_copies();
     __syncthreads();
     const uint32_t kt = key_begin + t * kKTile;
-    if (t + 1 < ntiles) {
-      issue_tile_copy<W, false>(k_layer, s_k + ((t + 1) & 1) * kTileHalfs, kt + kKTile, key_end,
-                                row_bytes, coff, wave);
-      issue_tile_copy<W, true>(v_layer, s_v + ((t + 1) & 1) * kTileHalfs, kt + kKTile, key_end,
-                               row_bytes, coff, wave);
+    half8_t ring[kRing];
+    // The copies of V(t+1) and K(t+2) are spread over the S^T region (in-order
+    // issue would otherwise hold the wave while the address unit takes them).
+    // K(t+2) past the last tile has key rows at or past key_end only: it writes
+    // zeros to a stage nothing reads again.
+    const uint32_t k_lds = ksrc.lds + par * kStageBytes;
+    const uint32_t v_lds = vsrc.lds + (par ^ 1u) * kStageBytes;
+    constexpr int kCopies = 2 * kCopiesPerTile<W>;
+    // M0 walks the copies' LDS addresses: V(t+1)'s, then K(t+2)'s.
+    constexpr int kStep = W * 2 * kRowHalfs * 2;
+    auto copy_piece = [&](int i) {
+      // Copies j with j * 32 / kCopies == i (V first, then K).
+#pragma unroll
+      for (int j = 0; j < kCopies; ++j) {
+        if (j * (kD / 8) / kCopies == i) {
+          constexpr int kc = kCopiesPerTile<W>;
+          if (j < kc) {
+            issue_copy_seq<W, true, kStep>(vsrc, coff, kt + kKTile, j, j == kc - 1, k_lds);
+          } else {
+            issue_copy_seq<W, false, kStep>(ksrc, coff, kt + 2 * kKTile, j - kc, false, 0u);
+          }
+        }
+      }
+    };
+    if (kNext) {
+      if (W == 1) {
+        // 64 copies per step: issued together (spread, their scalar
+        // resources would not fit beside the S^T region's registers).
+        issue_tile_copy<W, true>(vsrc, coff, kt + kKTile, v_lds);
+        issue_tile_copy<W, false>(ksrc, coff, kt + 2 * kKTile, k_lds);
+      } else {
+        set_m0(v_lds);
+      }
+#pragma unroll
+      for (int i = 0; i < kRing; ++i) {
+        ring[i] = kfrag(i);
+      }
     }
-    float16_t c0, c1;
-    scores(s_k + (t & 1) * kTileHalfs, c0, c1);
-
-    // ---- mask and max of tile t ----
+    // ---- mask of tile t (only tiles that reach past a query's window) ----
     const bool full = kt + kKTile <= key_end && kt + kKTile - 1u <= first_position;
     if (!full) {
 #pragma unroll
@@ -344,49 +486,95 @@ void flash256_kernel(FlashParams p) {
         c1[r] = (k1 < key_end && k1 <= position) ? c1[r] : -INFINITY;
       }
     }
-    float mx = fmaxf(c0[0], c1[0]);
-#pragma unroll
-    for (int r = 1; r < 16; ++r) {
-      mx = fmaxf(mx, fmaxf(c0[r], c1[r]));
+    if (kNext) {
+      n0 = float16_t{};
+      n1 = float16_t{};
     }
-    mx = xor32_max(mx) * c;  // tile max for query n (both lane halves)
-    const bool need = mx > m + kRescaleSlack;
-    if (__builtin_amdgcn_ballot_w64(need) != 0) {
-      const float m_new = need ? mx : m;
-      const float corr = need ? fast_exp2(m - m_new) : 1.0f;  // m = -inf -> 0
-      l *= corr;
-#pragma unroll
-      for (int dt = 0; dt < kD / 32; ++dt) {
-        o[dt] *= corr;
-      }
-      m = m_new;
-    }
-    // A query with no valid key yet keeps m = -inf; its scores are all -inf.
-    const float neg_m = m == -INFINITY ? 0.0f : -m;
-    half8_t pb[4];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p0 = fast_exp2(fmaf(c0[r], c, neg_m));
-      const float p1 = fast_exp2(fmaf(c1[r], c, neg_m));
-      l += p0 + p1;
-      pb[r >> 3][r & 7] = (half_t)p0;
-      pb[2 + (r >> 3)][r & 7] = (half_t)p1;
-    }
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- O^T += V^T P^T over the tile's 64 keys (4 k-steps of 16) ----
-    const half_t* vst = s_v + (t & 1) * kTileHalfs;
-    auto vfrag = [&](int i) {  // read i: k-step i / 8, dim tile i % 8
-      const int ks = i >> 3;
-      const int dt = i & 7;
-      const half_t* vp = vst + v_addr[dt & 3] + 128 * (dt >> 2) + 16 * ks * kRowHalfs;
-      const half4_t lo = read_tr16(vp);
-      const half4_t hi = read_tr16(vp + 8 * kRowHalfs);
-      return half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    // Softmax pieces of tile t, placed after MFMA i of the S^T region.
+    float mx = -INFINITY;
+    float corr = 1.0f;
+    float neg_m = 0.0f;
+    bool need = false;
+    half8_t pb[4];
+    // Each piece ends in an empty asm on its results: without it the compiler
+    // sinks the work next to its first use (the PV region) and nothing overlaps.
+    // Exponentials j (< 16): the two scores of pb[j / 4] at 2 (j % 4), +1.
+    auto exp_piece = [&](int j) {
+      const int b = j >> 2;
+      const int k = 2 * (j & 3);
+      const int r = 8 * (b & 1) + k;
+      const float s0 = b < 2 ? c0[r] : c1[r];
+      const float s1 = b < 2 ? c0[r + 1] : c1[r + 1];
+      const float p0 = fast_exp2(fmaf(s0, c, neg_m));
+      const float p1 = fast_exp2(fmaf(s1, c, neg_m));
+      // The denominator sums the f16 weights that PV multiplies (v_dot2_f32_f16).
+      half2_t hp = half2_t{(half_t)p0, (half_t)p1};
+      l = __builtin_amdgcn_fdot2(hp, half2_t{(half_t)1.0f, (half_t)1.0f}, l, false);
+      asm volatile("" : "+v"(hp), "+v"(l));
+      pb[b][k] = hp[0];
+      pb[b][k + 1] = hp[1];
     };
+    auto soft_piece = [&](int i) {
+      if (i < 4) {
+        // IEEE maximum (v_maximum3_f32): fmaxf would first quiet each MFMA
+        // result; a NaN score (non-finite inputs) propagates either way.
+#pragma unroll
+        for (int r = 4 * i; r < 4 * i + 4; ++r) {
+          mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(c0[r], c1[r]));
+        }
+        asm volatile("" : "+v"(mx));
+      } else if (i == 4) {
+        {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                           false, false);
+          mx = __builtin_elementwise_maximum(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        mx *= c;  // tile max for query n (both lane halves)
+        // The reference max moves only when the tile's exceeds it by the slack.
+        need = mx > m + kRescaleSlack;
+        const float m_new = need ? mx : m;
+        corr = need ? fast_exp2(m - m_new) : 1.0f;  // m = -inf -> 0
+        m = m_new;
+        l *= corr;
+        // A query with no valid key yet keeps m = -inf; its scores are all -inf.
+        neg_m = m == -INFINITY ? 0.0f : -m;
+        asm volatile("" : "+v"(neg_m), "+v"(corr), "+v"(l), "+v"(m));
+      } else if (i >= 6 && i < 30 && (i & 1) == 0) {
+        exp_piece((i - 6) >> 1);
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < kD / 8; ++i) {
+      if (kNext) {
+        const half8_t a = ring[i % kRing];
+        if (i + kRing < kD / 8) {
+          ring[i % kRing] = kfrag(i + kRing);
+        }
+        if (i & 1) {
+          n1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[i >> 1], n1, 0, 0, 0);
+        } else {
+          n0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[i >> 1], n0, 0, 0, 0);
+        }
+        if (W > 1) {
+          copy_piece(i);
+        }
+      }
+      soft_piece(i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // ---- O^T += V^T P^T over the tile's 64 keys (4 k-steps of 16) ----
     half8_t vring[kVRing];
 #pragma unroll
     for (int i = 0; i < kVRing; ++i) {
       vring[i] = vfrag(i);
+    }
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+#pragma unroll
+      for (int dt = 0; dt < kD / 32; ++dt) {
+        o[dt] *= corr;
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -396,14 +584,30 @@ void flash256_kernel(FlashParams p) {
         vring[i % kVRing] = vfrag(i + kVRing);
       }
       o[i & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[i >> 3], o[i & 7], 0, 0, 0);
+      if ((i & 3) == 0 && i < 16) {
+        exp_piece(12 + (i >> 2));  // pb[3], first read by MFMA 24
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // Prologue: tile 0's copies were issued above.
-  for (uint32_t t = 0; t < ntiles; ++t) {
-    iteration(t);
+  // Prologue: tiles 0's copies were issued above; publish them, start K(1),
+  // and compute S^T of tile 0.
+  float16_t ca, cb, na, nb;
+  wait_tile_copies();
+  __syncthreads();
+  if (ntiles > 1) {
+    issue_tile_copy<W, false>(ksrc, coff, key_begin + kKTile, ksrc.lds + kStageBytes);
   }
+  first_scores(ca, cb);
+  using Next = std::integral_constant<bool, true>;
+  using Last = std::integral_constant<bool, false>;
+  for (uint32_t t = 0; t + 1 < ntiles; ++t) {
+    step(Next{}, t, ca, cb, na, nb);
+    ca = na;
+    cb = nb;
+  }
+  step(Last{}, ntiles - 1, ca, cb, na, nb);
 
   l = xor32_sum(l);  // both lane halves hold keys of query n
   if (!token_ok) {

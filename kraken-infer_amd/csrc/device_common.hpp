@@ -179,7 +179,7 @@ __device__ __forceinline__ i32x4_t rsrc_words(const void* base, uint32_t bytes) 
 // wait for it (it cannot tell the copy's target from the LDS being read); the
 // caller awaits completion with an explicit s_waitcnt vmcnt.  M0 is set in the
 // same statement, with the one wait state the M0 -> LDS-DMA hazard needs.  A
-// kernel using this must have no other M0 user (its ISA is checked for one), so
+// kernel using this must have no other M0 user (tests/test_isa_m0.py checks the ISA), so
 // declaring the reserved register clobbered is safe there.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
