@@ -23,14 +23,14 @@
 //    in parallel: stages K, Q, V of the chunk in LDS, forms G, the Gram
 //    matrices K K^T and Q K^T (MFMA), A and M, inverts I + A (diagonal 16 x 16
 //    blocks by substitution, off-diagonal blocks by block substitution), then
-//    U, W (MFMA), Qtil = diag(gamma) Q and Ktil^T into a workspace block.
+//    U, W (MFMA), gamma and Ktil^T into a workspace block.
 //  * gdn_chunk_scan_kernel, one workgroup per (16 state rows, value head),
 //    sequential over the chunks, holds only the recurrence: the 16 x 128 state
 //    slice lives in LDS; per chunk it stores S_0 and forms delta = U - W S_0^T
-//    (stored too) and S_C = gamma_C S_0 + Ktil^T delta (MFMA).  The next
-//    chunk's operands are loaded between the MFMAs of the current one.
+//    (stored too) and S_C = gamma_C S_0 + Ktil^T delta (MFMA).  Loader waves
+//    stream the next chunk's W and Ktil^T into LDS meanwhile.
 //  * gdn_chunk_out_kernel, one workgroup per (chunk, value head, 64 state
-//    rows), all in parallel: Y = scale (Qtil S_0^T + M delta).
+//    rows), all in parallel: Y = scale (diag(gamma) Q S_0^T + M delta).
 // Taking Y out of the sequential kernel matters because each of its
 // workgroups reads the chunk's operands through one CU's load path (about
 // 30 bytes per clock measured), which then bounds the chunk's latency.
@@ -56,8 +56,8 @@ constexpr int kCPad = kC + 4;
 constexpr int kScanRows = 16;  // state rows per scan workgroup
 // Workspace block per (chunk, value head), in floats.
 constexpr size_t kOffW = 0;                     // W     [C][D]
-constexpr size_t kOffQ = kOffW + kC * kDim;     // Qtil  [C][D]
-constexpr size_t kOffU = kOffQ + kC * kDim;     // U^T   [D][C]
+constexpr size_t kOffGam = kOffW + kC * kDim;   // gamma [C] (exp of the inclusive sum of g)
+constexpr size_t kOffU = kOffGam + kC;          // U^T   [D][C]
 constexpr size_t kOffKT = kOffU + kC * kDim;    // Ktil^T [D][C]
 constexpr size_t kOffM = kOffKT + kDim * kC;    // M     [C][C]
 constexpr size_t kOffS0 = kOffM + kC * kC;     // S_0   [D][D] (state before the chunk)
@@ -101,12 +101,16 @@ constexpr int kPrepWaves = kPrepThreads / 64;
 template <bool kPrepare>
 __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParams p) {
   __shared__ __attribute__((aligned(16))) float Ks[kC][kRowPad];
-  __shared__ __attribute__((aligned(16))) float Qs[kC][kRowPad];
-  __shared__ __attribute__((aligned(16))) float Vs[kC][kRowPad];
+  // Q (rows) for the Gram matrices, then K^T (rows = key dims) for W: the
+  // products U and W read their B operand four tokens at a time from the
+  // transposed V and K.
+  __shared__ __attribute__((aligned(16))) float QK[kDim * kCPad];
+  __shared__ __attribute__((aligned(16))) float VsT[kDim][kCPad];
   __shared__ __attribute__((aligned(16))) float As[kC][kCPad];
   __shared__ __attribute__((aligned(16))) float Ts[kC][kCPad];
-  __shared__ __attribute__((aligned(16))) float Tmp[3][16][16];
   __shared__ float Gs[kC], Bs[kC], Gam[kC];
+  __shared__ __attribute__((aligned(16))) float Dec[kC];  // exp(G_C - G_t)
+  __shared__ __attribute__((aligned(16))) float Red[4][64][4];  // Gram partial sums
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -120,8 +124,11 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
   const uint32_t t0 = c * kC;
   const uint32_t n = min((uint32_t)kC, p.tokens - t0);
   float* blk = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats;
+  float(*Qs)[kRowPad] = reinterpret_cast<float(*)[kRowPad]>(QK);
+  float(*KsT)[kCPad] = reinterpret_cast<float(*)[kCPad]>(QK);
+  static_assert(kC * kRowPad <= kDim * kCPad, "Q fits the shared Q / K^T array");
 
-  // ---- stage K, Q, V (rows past the chunk's tokens are zero) ----
+  // ---- stage K, Q, V^T (rows past the chunk's tokens are zero) ----
   // Unconditional loads from a valid row (the chunk's first token stands in for
   // rows past its end), zeroed afterwards, so all of them are in flight at once.
 #pragma unroll
@@ -134,13 +141,29 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
     const size_t ko = ((size_t)tr * p.key_heads + kh) * kDim + c4;
     float4 kk = *reinterpret_cast<const float4*>(p.key + ko);
     float4 qq = *reinterpret_cast<const float4*>(p.query + ko);
-    float4 vv = *reinterpret_cast<const float4*>(p.value + ((size_t)tr * p.value_heads + h) * kDim + c4);
     if (!ok) {
-      kk = qq = vv = make_float4(0.f, 0.f, 0.f, 0.f);
+      kk = qq = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     *reinterpret_cast<float4*>(&Ks[t][c4]) = kk;
     *reinterpret_cast<float4*>(&Qs[t][c4]) = qq;
-    *reinterpret_cast<float4*>(&Vs[t][c4]) = vv;
+  }
+  // V transposed: four lanes read 64 contiguous bytes of a row, sixteen rows per
+  // 64 lanes, so the transposed writes of a row go to 16 consecutive tokens.
+#pragma unroll
+  for (int it = 0; it < kC * (kDim / 4) / kPrepThreads; ++it) {
+    const int idx = tid + kPrepThreads * it;
+    const int t = (idx >> 2) & (kC - 1);
+    const int c4 = 16 * (idx >> 8) + 4 * (idx & 3);
+    const bool ok = (uint32_t)t < n;
+    const uint32_t tr = t0 + (ok ? t : 0);
+    float4 vv = *reinterpret_cast<const float4*>(p.value + ((size_t)tr * p.value_heads + h) * kDim + c4);
+    if (!ok) {
+      vv = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    VsT[c4 + 0][t] = vv.x;
+    VsT[c4 + 1][t] = vv.y;
+    VsT[c4 + 2][t] = vv.z;
+    VsT[c4 + 3][t] = vv.w;
   }
   for (int idx = tid; idx < kC * kCPad; idx += kPrepThreads) {
     (&As[0][0])[idx] = 0.0f;
@@ -172,11 +195,14 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
   }
   __syncthreads();
   const float g_last = Gs[kC - 1];  // padded tokens carry g = 0
+  if (tid < kC) {
+    Dec[tid] = expf(g_last - Gs[tid]);
+  }
 
   // ---- Gram matrices: tiles (I, J), J <= I, of K K^T (A) and Q K^T (M) ----
   // Jobs 0..9: the ten lower tiles of K K^T, 10..19: of Q K^T.  Wave w runs
   // jobs w and w + 8 in one pass with independent accumulators (LDS reads of
-  // one overlap the MFMAs of the other), then job w + 16 if it exists.
+  // one overlap the MFMAs of the other), then half of job 16 + w % 4.
   auto gram_tile = [&](int job, int& I, int& J, bool& is_q) __attribute__((always_inline)) {
     is_q = job >= 10;
     int jj = is_q ? job - 10 : job;  // lower-triangular tile index
@@ -201,12 +227,13 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
     }
   };
   static_assert(kPrepWaves == 8, "job assignment");
-  for (int job = wave; job < 20; job += 16) {
+  {
+    // Jobs w and w + 8 (0..15) in one pass with independent accumulators.
+    const int job = wave;
     int I0, J0, I1, J1;
     bool q0, q1;
     gram_tile(job, I0, J0, q0);
-    const bool two = job + 8 < 20;
-    gram_tile(two ? job + 8 : job, I1, J1, q1);
+    gram_tile(job + 8, I1, J1, q1);
     const float(*X0)[kRowPad] = q0 ? Qs : Ks;
     const float(*X1)[kRowPad] = q1 ? Qs : Ks;
     float4_v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
@@ -226,8 +253,37 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
       acc1 = mfma4(a1.w, b1.w, acc1);
     }
     gram_store(I0, J0, q0, acc0);
-    if (two) {
-      gram_store(I1, J1, q1, acc1);
+    gram_store(I1, J1, q1, acc1);
+  }
+  {
+    // Jobs 16..19: wave w takes job 16 + w % 4 over half the key dims
+    // (w / 4); the second half's partial sums meet the first's in LDS.
+    int I, J;
+    bool q;
+    gram_tile(16 + (wave & 3), I, J, q);
+    const float(*X)[kRowPad] = q ? Qs : Ks;
+    const int s0 = 4 * (wave >> 2);
+    float4_v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = s0; s4 < s0 + 4; ++s4) {
+      const float4 a = *reinterpret_cast<const float4*>(&X[16 * I + li][16 * s4 + 4 * kq]);
+      const float4 b = *reinterpret_cast<const float4*>(&Ks[16 * J + li][16 * s4 + 4 * kq]);
+      acc = mfma4(a.x, b.x, acc);
+      acc = mfma4(a.y, b.y, acc);
+      acc = mfma4(a.z, b.z, acc);
+      acc = mfma4(a.w, b.w, acc);
+    }
+    if (wave >= 4) {
+      *reinterpret_cast<float4*>(&Red[wave & 3][lane][0]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
+    __syncthreads();
+    if (wave < 4) {
+      const float4 o = *reinterpret_cast<const float4*>(&Red[wave][lane][0]);
+      acc[0] += o.x;
+      acc[1] += o.y;
+      acc[2] += o.z;
+      acc[3] += o.w;
+      gram_store(I, J, q, acc);
     }
   }
   // Upper tiles of M are zero.
@@ -246,7 +302,26 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
   }
   __syncthreads();
 
-  // ---- T = (I + A)^-1: diagonal 16 x 16 blocks by substitution ----
+  // ---- T = (I + A)^-1: diagonal 16 x 16 blocks by substitution; waves 4..7
+  // meanwhile transpose K into K^T (Q is done with) and store
+  // Ktil^T = (diag(exp(G_C - G)) K)^T ----
+  // The transpose runs in four parts, one beside each inversion phase (the
+  // diagonal blocks and the three off-diagonal block rows keep waves 4..7
+  // idle); part `part` takes key dims 32 part .. 32 part + 31.
+  auto transpose_part = [&](int part) __attribute__((always_inline)) {
+    if (wave >= 4) {
+      for (int idx = tid - 256; idx < 32 * (kC / 4); idx += 256) {
+        const int d = 32 * part + (idx >> 4);
+        const int t4 = (idx & 15) * 4;
+        const float4 kv = make_float4(Ks[t4 + 0][d], Ks[t4 + 1][d], Ks[t4 + 2][d], Ks[t4 + 3][d]);
+        *reinterpret_cast<float4*>(&KsT[d][t4]) = kv;
+        const float4 e = *reinterpret_cast<const float4*>(&Dec[t4]);
+        *reinterpret_cast<float4*>(blk + kOffKT + d * kC + t4) =
+          make_float4(e.x * kv.x, e.y * kv.y, e.z * kv.z, e.w * kv.w);
+      }
+    }
+  };
+  transpose_part(0);
   if (wave < 4 && li == lane) {  // lanes 0..15 of waves 0..3: column j of block `wave`
     const int b0 = 16 * wave;
     const int j = lane;
@@ -266,84 +341,55 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
     }
   }
   __syncthreads();
-  // Off-diagonal blocks by block rows: T_IJ = -T_II sum_{K=J}^{I-1} A_IK T_KJ.
+  // Off-diagonal blocks by block rows: T_IJ = -T_II sum_{K=J}^{I-1} A_IK T_KJ,
+  // wave J computing T_IJ on MFMA.  The first product leaves lane (j, q) with
+  // rows 4q .. 4q + 3 of column j; the second relabels k = 4 kq + s for
+  // instruction s, so that accumulator register s is its B operand as is.
   for (int I = 1; I < 4; ++I) {
-    for (int idx = tid; idx < I * 256; idx += kPrepThreads) {
-      const int J = idx >> 8;
-      const int i = (idx >> 4) & 15;
-      const int j = idx & 15;
-      float acc = 0.0f;
+    transpose_part(I);
+    if (wave < I) {
+      const int J = wave;
+      float4_v acc = {0.f, 0.f, 0.f, 0.f};
       for (int K = J; K < I; ++K) {
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          acc = fmaf(As[16 * I + i][16 * K + k], Ts[16 * K + k][16 * J + j], acc);
+        for (int s4 = 0; s4 < 4; ++s4) {
+          acc = mfma4(As[16 * I + li][16 * K + 4 * s4 + kq], Ts[16 * K + 4 * s4 + kq][16 * J + li],
+                      acc);
         }
       }
-      Tmp[J][i][j] = acc;
-    }
-    __syncthreads();
-    for (int idx = tid; idx < I * 256; idx += kPrepThreads) {
-      const int J = idx >> 8;
-      const int i = (idx >> 4) & 15;
-      const int j = idx & 15;
-      float acc = 0.0f;
+      float4_v t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        acc = fmaf(Ts[16 * I + i][16 * I + k], Tmp[J][k][j], acc);
+      for (int s4 = 0; s4 < 4; ++s4) {
+        t = mfma4(Ts[16 * I + li][16 * I + 4 * kq + s4], acc[s4], t);
       }
-      Ts[16 * I + i][16 * J + j] = -acc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        Ts[16 * I + 4 * kq + r][16 * J + li] = -t[r];
+      }
     }
     __syncthreads();
   }
 
-  // ---- Qtil = diag(gamma) Q and Ktil^T = (diag(exp(G_C - G)) K)^T ----
-  for (int idx = tid; idx < kC * (kDim / 4); idx += kPrepThreads) {
-    const int t = idx >> 5;
-    const int c4 = (idx & 31) * 4;
-    const float gm = Gam[t];
-    float4 qq = *reinterpret_cast<const float4*>(&Qs[t][c4]);
-    qq.x *= gm;
-    qq.y *= gm;
-    qq.z *= gm;
-    qq.w *= gm;
-    *reinterpret_cast<float4*>(blk + kOffQ + t * kDim + c4) = qq;
-  }
-  for (int idx = tid; idx < kDim * (kC / 4); idx += kPrepThreads) {
-    const int d = idx >> 4;
-    const int t4 = (idx & 15) * 4;
-    float4 v;
-    v.x = expf(g_last - Gs[t4 + 0]) * Ks[t4 + 0][d];
-    v.y = expf(g_last - Gs[t4 + 1]) * Ks[t4 + 1][d];
-    v.z = expf(g_last - Gs[t4 + 2]) * Ks[t4 + 2][d];
-    v.w = expf(g_last - Gs[t4 + 3]) * Ks[t4 + 3][d];
-    *reinterpret_cast<float4*>(blk + kOffKT + d * kC + t4) = v;
+  // ---- gamma (the output kernel forms diag(gamma) Q S_0^T) ----
+  if (tid < kC) {
+    blk[kOffGam + tid] = Gam[tid];
   }
   if (tid == 0) {
     blk[kOffGammaC] = expf(g_last);
   }
-  __syncthreads();
-  // V <- diag(beta) V, K <- diag(beta gamma) K (in place; the Grams are done).
-  for (int idx = tid; idx < kC * (kDim / 4); idx += kPrepThreads) {
-    const int t = idx >> 5;
-    const int c4 = (idx & 31) * 4;
-    const float bv = Bs[t];
-    const float bk = Bs[t] * Gam[t];
-    float4 vv = *reinterpret_cast<const float4*>(&Vs[t][c4]);
-    float4 kk = *reinterpret_cast<const float4*>(&Ks[t][c4]);
-    vv.x *= bv;
-    vv.y *= bv;
-    vv.z *= bv;
-    vv.w *= bv;
-    kk.x *= bk;
-    kk.y *= bk;
-    kk.z *= bk;
-    kk.w *= bk;
-    *reinterpret_cast<float4*>(&Vs[t][c4]) = vv;
-    *reinterpret_cast<float4*>(&Ks[t][c4]) = kk;
+  // ---- U = T diag(beta) V, W = T diag(beta gamma) K (C x D): 2 x 32 output
+  // tiles, four per pass; the diagonal scales T's columns as the A operand is
+  // read (k = 16 s + 4 kq + c). ----
+  float fb[16], fbg[16];
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = 16 * s4 + 4 * kq + c;
+      fb[4 * s4 + c] = Bs[k];
+      fbg[4 * s4 + c] = Bs[k] * Gam[k];
+    }
   }
-  __syncthreads();
-
-  // ---- U = T V', W = T K' (C x D): 2 x 32 output tiles, four per pass ----
   for (int job0 = 4 * wave; job0 < 64; job0 += 4 * kPrepWaves) {
     float4_v acc[4];
 #pragma unroll
@@ -360,12 +406,14 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
         const int tile = job & 31;
         const int R = tile >> 3;   // token row block
         const int Cb = tile & 7;   // dim column block
-        const float(*X)[kRowPad] = is_w ? Ks : Vs;
+        const float(*XT)[kCPad] = is_w ? KsT : VsT;
+        const float* f = is_w ? &fbg[4 * s4] : &fb[4 * s4];
         const float4 a = *reinterpret_cast<const float4*>(&Ts[16 * R + li][k0]);
-        acc[u] = mfma4(a.x, X[k0 + 0][16 * Cb + li], acc[u]);
-        acc[u] = mfma4(a.y, X[k0 + 1][16 * Cb + li], acc[u]);
-        acc[u] = mfma4(a.z, X[k0 + 2][16 * Cb + li], acc[u]);
-        acc[u] = mfma4(a.w, X[k0 + 3][16 * Cb + li], acc[u]);
+        const float4 b = *reinterpret_cast<const float4*>(&XT[16 * Cb + li][k0]);
+        acc[u] = mfma4(a.x * f[0], b.x, acc[u]);
+        acc[u] = mfma4(a.y * f[1], b.y, acc[u]);
+        acc[u] = mfma4(a.z * f[2], b.z, acc[u]);
+        acc[u] = mfma4(a.w * f[3], b.w, acc[u]);
       }
     }
 #pragma unroll
@@ -386,23 +434,28 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
   }
 }
 
-// Global operands of one scan chunk for one lane (see gdn_chunk_scan_kernel).
-struct ScanOps {
-  // Lane (i, kq) holds, of row i, the values 16 s + 4 kq .. 16 s + 4 kq + 3 in
-  // entry s: one load instruction reads 64 contiguous bytes of each of 16 rows.
-  float4 x[8];      // W rows of the wave's 16 tokens (32 values)
-  float4 kt[2][4];  // Ktil^T rows of the wave's two state tiles (16 tokens)
-  float4 u;         // U entries of the lane's four delta values
-  float gamma_c;
-};
+// The scan's workgroup: four compute waves run the recurrence; four loader
+// waves stream the next chunk's W and Ktil^T into the other LDS buffer with
+// direct-to-LDS copies and store S_0 and delta.  The chunk is bound about
+// equally by one CU's MFMA rate and by its load path (about 30 bytes per clock
+// for the 64 KB of W and Ktil^T); with the loads issued by the compute waves,
+// an in-order wave stalled on a load issues no MFMAs and the two add up.
+constexpr int kScanThreads = 512;
+constexpr int kScanCompute = 4;  // waves 0..3; 4..7 load
 
-__global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ChunkParams p) {
+__global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkParams p) {
+  // W and Ktil^T of the current and the next chunk.  Each row's 16-byte chunks
+  // are XOR-swizzled by row % 16 (the copies pick which global chunk a lane
+  // fetches), so the compute waves' reads of 16 rows at one column are free of
+  // bank conflicts.
+  __shared__ __attribute__((aligned(16))) float Wb[2][kC * kDim];
+  __shared__ __attribute__((aligned(16))) float KTb[2][kDim * kC];
   __shared__ __attribute__((aligned(16))) float Sl[kScanRows][kRowPad];
   __shared__ __attribute__((aligned(16))) float dT[kScanRows][kCPad];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15;
   const int kq = lane >> 4;
   // Workgroup i runs on XCD i % 8.  The (head, row block) pairs are numbered
@@ -414,45 +467,92 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ChunkParams p) {
   const uint32_t row0 = (q % (kDim / kScanRows)) * kScanRows;
   const uint32_t h = q / (kDim / kScanRows);
   float* shead = p.state + ((size_t)h * kDim + row0) * kDim;
+  auto block = [&](uint32_t cl) { return p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats; };
 
-  for (int idx = tid; idx < kScanRows * (kDim / 4); idx += 256) {
+  // ---- loader side: chunk cl's W and Ktil^T into buffer b ----
+  // Copy i of W fills LDS rows 2i, 2i + 1 (lane / 32) at physical chunk
+  // lane % 32; copy i of Ktil^T fills rows 4i .. 4i + 3 (lane / 16) at
+  // physical chunk lane % 16.  Loader wave lw issues copies 8 lw .. 8 lw + 7
+  // of each.
+  auto load_chunk = [&](uint32_t cl, int b) {
+    const int lw = wave - kScanCompute;
+    const i32x4_t rs = rsrc_words(block(cl), (uint32_t)(kBlockFloats * 4));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = 8 * lw + j;
+      const int row = 2 * i + (lane >> 5);
+      const int g = (lane & 31) ^ (row & 15);
+      copy16_to_lds(rs, (uint32_t)(kOffW * 4 + row * 512 + g * 16),
+                    reinterpret_cast<const half_t*>(&Wb[b][0]) + i * 512);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = 8 * lw + j;
+      const int row = 4 * i + (lane >> 4);
+      const int g = (lane & 15) ^ (row & 15);
+      copy16_to_lds(rs, (uint32_t)(kOffKT * 4 + row * 256 + g * 16),
+                    reinterpret_cast<const half_t*>(&KTb[b][0]) + i * 512);
+    }
+  };
+
+  for (int idx = tid; idx < kScanRows * (kDim / 4); idx += kScanThreads) {
     const int r = idx >> 5;
     const int c4 = (idx & 31) * 4;
     *reinterpret_cast<float4*>(&Sl[r][c4]) =
       *reinterpret_cast<const float4*>(shead + (size_t)r * kDim + c4);
   }
+  if (wave >= kScanCompute) {
+    load_chunk(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  __syncthreads();  // state slice and chunk 0's operands staged
 
-  // Global operands of chunk cl that this lane uses, in two parts (W rows,
-  // then U, gamma_C, Ktil^T), issued for the next chunk between the MFMAs of
-  // the current one: the per-CU load path moves about as many cycles' worth of
-  // bytes per chunk as the MFMAs take, and an in-order wave stalled on a burst
-  // of loads issues no MFMAs.
-  auto load_x = [&](uint32_t cl, ScanOps& o) __attribute__((always_inline)) {
-    const float* xr = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats + kOffW +
-                      (size_t)(16 * wave + li) * kDim + 4 * kq;
+  if (wave >= kScanCompute) {
+    // Per chunk: S_0 out, the next chunk's copies, [barrier], delta out, the
+    // copies awaited, [barrier].
+    const int lt = tid - kScanCompute * 64;
+    for (uint32_t cl = 0; cl < p.chunks; ++cl) {
+      float* blk = block(cl);
 #pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4) {
-      o.x[s4] = *reinterpret_cast<const float4*>(xr + 16 * s4);
-    }
-  };
-  auto load_rest = [&](uint32_t cl, ScanOps& o) __attribute__((always_inline)) {
-    const float* blk = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats;
-    o.u = *reinterpret_cast<const float4*>(blk + kOffU + (size_t)(row0 + li) * kC + 16 * wave + 4 * kq);
-    o.gamma_c = blk[kOffGammaC];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const float* kr = blk + kOffKT + (size_t)(32 * wave + 16 * tt + li) * kC + 4 * kq;
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        o.kt[tt][s4] = *reinterpret_cast<const float4*>(kr + 16 * s4);
+      for (int it = 0; it < 2; ++it) {
+        const int idx = lt + 256 * it;
+        const int r = idx >> 5;
+        const int c4 = (idx & 31) * 4;
+        *reinterpret_cast<float4*>(blk + kOffS0 + (size_t)(row0 + r) * kDim + c4) =
+          *reinterpret_cast<const float4*>(&Sl[r][c4]);
       }
+      if (cl + 1 < p.chunks) {
+        load_chunk(cl + 1, (int)((cl + 1) & 1u));
+      }
+      __syncthreads();  // B1: delta^T is in dT
+      {
+        const int r = lt >> 4;
+        const int t4 = (lt & 15) * 4;
+        *reinterpret_cast<float4*>(blk + kOffDT + (size_t)(row0 + r) * kC + t4) =
+          *reinterpret_cast<const float4*>(&dT[r][t4]);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();  // B2: S_C in Sl, the next chunk's operands landed
     }
-  };
+    return;
+  }
 
-  // Chunk cl with operands o; loads chunk ncl's operands into nx meanwhile.
-  auto chunk = [&](uint32_t cl, const ScanOps& o, uint32_t ncl, ScanOps& nx)
-                 __attribute__((always_inline)) {
-    float* blk = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats;
+  // ---- compute side ----
+  // U entries of the lane's four delta values and gamma_C, one chunk ahead.
+  auto load_u = [&](uint32_t cl, float4& u, float& gamma_c) {
+    const float* blk = block(cl);
+    u = *reinterpret_cast<const float4*>(blk + kOffU + (size_t)(row0 + li) * kC + 16 * wave +
+                                          4 * kq);
+    gamma_c = blk[kOffGammaC];
+  };
+  float4 u, nu;
+  float gamma_c, ngamma_c;
+  load_u(0, u, gamma_c);
+  for (uint32_t cl = 0; cl < p.chunks; ++cl) {
+    const int b = (int)(cl & 1u);
+    const char* wb = reinterpret_cast<const char*>(&Wb[b][0]);
+    const char* kb = reinterpret_cast<const char*>(&KTb[b][0]);
+    load_u(min(cl + 1, p.chunks - 1), nu, ngamma_c);
     // State slice as the B operand: lane (j, kq) holds S[j][16 s + 4 kq + c],
     // s < 8, c < 4 (k = 16 s + 4 kq + c in MFMA 4 s + c, for A and B alike).
     float sb[32];
@@ -464,85 +564,49 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ChunkParams p) {
       sb[4 * s4 + 2] = v.z;
       sb[4 * s4 + 3] = v.w;
     }
-    // S_0 of this chunk, for the output kernel.
-#pragma unroll
-    for (int it = 0; it < kScanRows * (kDim / 4) / 256; ++it) {
-      const int idx = tid + 256 * it;
-      const int r = idx >> 5;
-      const int c4 = (idx & 31) * 4;
-      *reinterpret_cast<float4*>(blk + kOffS0 + (size_t)(row0 + r) * kDim + c4) =
-        *reinterpret_cast<const float4*>(&Sl[r][c4]);
-    }
-    load_x(ncl, nx);
-    // W S_0^T for tokens 16 w .. 16 w + 15.
+    // W S_0^T for tokens 16 w .. 16 w + 15 (W row 16 w + li, logical chunk
+    // 4 s + kq at physical chunk (4 s + kq) ^ li).
+    const int wrow = 16 * wave + li;
     float4_v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s4 = 0; s4 < 8; ++s4) {
-      const float4 a = o.x[s4];
+      const float4 a =
+        *reinterpret_cast<const float4*>(wb + wrow * 512 + 16 * ((4 * s4 + kq) ^ li));
       acc = mfma4(a.x, sb[4 * s4 + 0], acc);
       acc = mfma4(a.y, sb[4 * s4 + 1], acc);
       acc = mfma4(a.z, sb[4 * s4 + 2], acc);
       acc = mfma4(a.w, sb[4 * s4 + 3], acc);
     }
-    // Schedule: the state reads, then one load per four MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    }
-    // delta = U - W S_0^T, kept transposed (rows j, tokens t) in LDS and in
-    // the block.
-    const float4 d = make_float4(o.u.x - acc[0], o.u.y - acc[1], o.u.z - acc[2], o.u.w - acc[3]);
-    *reinterpret_cast<float4*>(&dT[li][16 * wave + 4 * kq]) = d;
-    *reinterpret_cast<float4*>(blk + kOffDT + (size_t)(row0 + li) * kC + 16 * wave + 4 * kq) = d;
-    __syncthreads();
-    load_rest(ncl, nx);
-    // S_C^T rows (key dims) 32 w .. 32 w + 31 = gamma_C S_0^T + Ktil^T delta.
+    // delta = U - W S_0^T, kept transposed (rows j, tokens t) in LDS; the
+    // loader waves store it.
+    *reinterpret_cast<float4*>(&dT[li][16 * wave + 4 * kq]) =
+      make_float4(u.x - acc[0], u.y - acc[1], u.z - acc[2], u.w - acc[3]);
+    __syncthreads();  // B1
+    // S_C^T rows (key dims) 32 w .. 32 w + 31 = gamma_C S_0^T + Ktil^T delta
+    // (Ktil^T row 32 w + 16 tt + li, logical chunk 4 s + kq at (4 s + kq) ^ li).
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const int kb = 32 * wave + 16 * tt;
-      const float4 s0 = *reinterpret_cast<const float4*>(&Sl[li][kb + 4 * kq]);
-      float4_v s = {o.gamma_c * s0.x, o.gamma_c * s0.y, o.gamma_c * s0.z, o.gamma_c * s0.w};
+      const int kbase = 32 * wave + 16 * tt;
+      const float4 s0 = *reinterpret_cast<const float4*>(&Sl[li][kbase + 4 * kq]);
+      float4_v s = {gamma_c * s0.x, gamma_c * s0.y, gamma_c * s0.z, gamma_c * s0.w};
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        const float4 a = o.kt[tt][s4];
-        const float4 b = *reinterpret_cast<const float4*>(&dT[li][16 * s4 + 4 * kq]);
-        s = mfma4(a.x, b.x, s);
-        s = mfma4(a.y, b.y, s);
-        s = mfma4(a.z, b.z, s);
-        s = mfma4(a.w, b.w, s);
+        const float4 a = *reinterpret_cast<const float4*>(kb + (kbase + li) * 256 +
+                                                          16 * ((4 * s4 + kq) ^ li));
+        const float4 d = *reinterpret_cast<const float4*>(&dT[li][16 * s4 + 4 * kq]);
+        s = mfma4(a.x, d.x, s);
+        s = mfma4(a.y, d.y, s);
+        s = mfma4(a.z, d.z, s);
+        s = mfma4(a.w, d.w, s);
       }
-      *reinterpret_cast<float4*>(&Sl[li][kb + 4 * kq]) = make_float4(s[0], s[1], s[2], s[3]);
+      *reinterpret_cast<float4*>(&Sl[li][kbase + 4 * kq]) = make_float4(s[0], s[1], s[2], s[3]);
     }
-    // Schedule: the delta and state reads, then one load per three MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
-#pragma unroll
-    for (int i = 0; i < 10; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-    }
-    __syncthreads();
-  };
-
-  // Two chunks per iteration with the operand sets swapped: the next chunk's
-  // loads (clamped to the last chunk, so always in range) are in flight during
-  // the current chunk.
-  ScanOps ops_a, ops_b;
-  load_x(0, ops_a);
-  load_rest(0, ops_a);
-  __syncthreads();  // state slice staged
-  const uint32_t last = p.chunks - 1;
-  uint32_t cl = 0;
-  for (; cl + 1 < p.chunks; cl += 2) {
-    chunk(cl, ops_a, cl + 1, ops_b);
-    chunk(cl + 1, ops_b, min(cl + 2, last), ops_a);
-  }
-  if (cl < p.chunks) {
-    chunk(cl, ops_a, last, ops_b);
+    __syncthreads();  // B2
+    u = nu;
+    gamma_c = ngamma_c;
   }
 
-  for (int idx = tid; idx < kScanRows * (kDim / 4); idx += 256) {
+  for (int idx = tid; idx < kScanRows * (kDim / 4); idx += kScanCompute * 64) {
     const int r = idx >> 5;
     const int c4 = (idx & 31) * 4;
     *reinterpret_cast<float4*>(shead + (size_t)r * kDim + c4) =
@@ -579,9 +643,21 @@ __global__ __launch_bounds__(256) void gdn_chunk_out_kernel(ChunkParams p) {
   const uint32_t r0 = half * kOutRows;
   const float* blk = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats;
 
-  // A operands first (global, in flight while S_0 and delta are staged).
-  const float* qr = blk + kOffQ + (size_t)(16 * wave + li) * kDim + 4 * kq;
+  const uint32_t t0 = (p.chunk0 + cl) * kC;
+  const uint32_t n = min((uint32_t)kC, p.tokens - t0);
+  // A operands first (global, in flight while S_0 and delta are staged): the
+  // query rows of the wave's tokens (a token past the chunk's end reads the
+  // first row; its outputs are dropped) and M.
+  const uint32_t qt = 16 * wave + li;
+  const float* qr = p.query +
+                    ((size_t)(t0 + (qt < n ? qt : 0u)) * p.key_heads + h % p.key_heads) * kDim +
+                    4 * kq;
   const float* mr = blk + kOffM + (size_t)(16 * wave + li) * kC + 4 * kq;
+  float gam[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    gam[r] = blk[kOffGam + 16 * wave + 4 * kq + r];
+  }
   float4 qa[8], ma[4];
 #pragma unroll
   for (int s4 = 0; s4 < 8; ++s4) {
@@ -609,8 +685,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_out_kernel(ChunkParams p) {
   }
   __syncthreads();
 
-  const uint32_t t0 = (p.chunk0 + cl) * kC;
-  const uint32_t n = min((uint32_t)kC, p.tokens - t0);
   const size_t row_floats = (size_t)p.value_heads * kDim;
   // Rows at or past the chunk's last token fall outside the resource and are
   // dropped.
@@ -627,6 +701,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_out_kernel(ChunkParams p) {
       y = mfma4(qa[s4].y, b.y, y);
       y = mfma4(qa[s4].z, b.z, y);
       y = mfma4(qa[s4].w, b.w, y);
+    }
+    // Row t of Q S_0^T times gamma_t (lane (j, kq) holds rows 4 kq + r).
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      y[r] *= gam[r];
     }
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
@@ -680,7 +759,6 @@ hipError_t launch_gdn_chunked(const GdnArgs& a, void* workspace, size_t workspac
   p.ssm_a = a.ssm_a;
   p.state = a.state;
   p.output = a.output;
-  // Blocks follow the counter region, which they must never overlap.
   p.ws = static_cast<float*>(workspace);
   p.tokens = a.tokens;
   p.key_heads = a.key_heads;
@@ -702,7 +780,7 @@ hipError_t launch_gdn_chunked(const GdnArgs& a, void* workspace, size_t workspac
     }
     // One workgroup per (head, 16-row block); the kernel maps the linear index
     // (value_heads * 8 of them, a multiple of the XCD count) to the pair.
-    gdn_chunk_scan_kernel<<<a.value_heads * (kDim / kScanRows), 256, 0, stream>>>(p);
+    gdn_chunk_scan_kernel<<<a.value_heads * (kDim / kScanRows), kScanThreads, 0, stream>>>(p);
     e = hipGetLastError();
     if (e != hipSuccess) {
       return e;

@@ -1,6 +1,6 @@
 """The direct-to-LDS copies own M0.
 
-attention_flash.hip and attention_decode.hip issue their global -> LDS copies
+attention_flash.hip, attention_decode.hip and gdn_chunked.hip issue their global -> LDS copies
 (buffer_load_dwordx4 ... lds) from inline asm that sets M0 itself, and the
 flash kernel walks M0 from one copy to the next across the instructions in
 between.  That is only sound while nothing else in those kernels reads or
@@ -21,7 +21,8 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
          "-packed-fp32-ops", f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}",
          "--cuda-device-only", "-S"]
-EXTRA = {"attention_flash.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "attention_decode.hip": []}
+EXTRA = {"attention_flash.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "attention_decode.hip": [],
+         "gdn_chunked.hip": []}
 # Instructions that read M0 without naming it.
 IMPLICIT = re.compile(r"^(s_movrel|v_movrel|ds_append|ds_consume|ds_gws|s_sendmsg|v_interp|"
                       r"ds_param|lds_direct|s_ttracedata)")
