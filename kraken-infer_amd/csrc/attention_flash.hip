@@ -20,13 +20,14 @@
 //    so no register holds staging data.  Rows stay row-major (512 bytes per
 //    key); the 16-byte chunks of each row are XOR-swizzled (K by row % 16, V by
 //    4 * (row % 4)) by choosing which global chunk each lane fetches, which
-//    keeps the fragment reads below free of bank conflicts.  One barrier per
-//    tile publishes the copies.
+//    keeps the fragment reads below free of bank conflicts.  Two barriers per
+//    tile publish the copies (K before the S^T region, V before PV).
 //  * Software pipeline, one step per tile t: S^T of tile t+1 runs on the MFMA
 //    pipe while the VALU does tile t's mask, max and exponentials (pinned
 //    between the MFMAs; the compiler would otherwise sink them to their use),
-//    and the copies of V(t+1) and K(t+2) are spread over the same MFMAs; then
-//    O += V^T P^T for tile t.  With one wave per SIMD every instruction costs an
+//    and the copies of K(t+2) are spread over the same MFMAs; then
+//    O += V^T P^T for tile t, with the copies of V(t+1) spread over its MFMAs.
+//    With one wave per SIMD every instruction costs an
 //    issue slot, so the loop keeps its non-MFMA instructions few: one buffer
 //    resource per workgroup for K and one for V, M0 walked from copy to copy
 //    (nothing else in the kernel touches M0; tests/test_isa_m0.py checks the
@@ -237,12 +238,24 @@ __device__ __forceinline__ void wait_tile_copies() {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// Wait until at most N of this wave's vector-memory loads are outstanding.  The
+// loop issues no other vector-memory loads than the tile copies, and loads
+// complete in issue order, so this waits for all but the newest N copies.
+template <int N>
+__device__ __forceinline__ void wait_copies_but() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
 template <int GW>
 __global__ __launch_bounds__(64 * GW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flash256_kernel(FlashParams p) {
   // K and V tiles, two stages each (128 KB).
   __shared__ __attribute__((aligned(16))) half_t s_k[2 * kTileHalfs];
   __shared__ __attribute__((aligned(16))) half_t s_v[2 * kTileHalfs];
+  // Staging for the query rows of waves 0 and 1 (waves 2 and 3 stage theirs in
+  // V's second stage, which no copy writes before the loop): 160 KB in all.
+  __shared__ __attribute__((aligned(16))) half_t s_q[2 * kQTile * kRowHalfs];
 
   constexpr int W = GW;  // waves
   const int tid = threadIdx.x;
@@ -307,25 +320,44 @@ void flash256_kernel(FlashParams p) {
   const TileSource vsrc{rsrc_words(v_layer, key_end * row_bytes), row_bytes,
                         (uint32_t)(uintptr_t)(lds_void_t*)s_v + slot_bytes};
 
-  // Tile 0's copies go out before the query is loaded.
+  // The first tiles' copies go out before the query is loaded (K(1) past
+  // key_end reads as zeros).
   issue_tile_copy<W, false>(ksrc, coff, key_begin, ksrc.lds);
+  issue_tile_copy<W, false>(ksrc, coff, key_begin + kKTile, ksrc.lds + kStageBytes);
   issue_tile_copy<W, true>(vsrc, coff, key_begin, vsrc.lds);
 
   // Q^T as the B operand of S^T = K Q^T: lane holds query n, dims 16*step + 8*h + j.
+  // A lane's fragment takes 32 bytes from each of 16 places in its query row,
+  // so loading it straight from global memory would touch 32 rows per load
+  // instruction.  Instead each load reads one whole 1 KB row (16 bytes per
+  // lane), and the rows are turned around in LDS as f16, with their 16-byte
+  // chunks XOR-swizzled by row % 16 like the K tiles so that the fragment
+  // reads are free of bank conflicts.
   half8_t qf[kD / 16];
   {
+    half_t* stage = wave < 2 ? s_q + wave * (kQTile * kRowHalfs)
+                             : s_v + kTileHalfs + (wave - 2) * (kQTile * kRowHalfs);
     // Unconditional loads from a valid row (token 0 stands in for tokens past the
     // end), zeroed afterwards, so all 32 loads are in flight together.
-    const float* qrow = p.query + ((size_t)(token_ok ? token : 0) * p.heads + head) * kD;
-    const float qmask = token_ok ? 1.0f : 0.0f;
+    float4 rows[kQTile];
+#pragma unroll
+    for (int r = 0; r < kQTile; ++r) {
+      const uint32_t tok = t0 + (uint32_t)r < p.tokens ? t0 + (uint32_t)r : 0u;
+      const float* qrow = p.query + ((size_t)tok * p.heads + head) * kD;
+      rows[r] = *reinterpret_cast<const float4*>(qrow + 4 * lane);
+    }
+#pragma unroll
+    for (int r = 0; r < kQTile; ++r) {
+      const float qmask = t0 + (uint32_t)r < p.tokens ? 1.0f : 0.0f;
+      const half4_t hv = {(half_t)(rows[r].x * qmask), (half_t)(rows[r].y * qmask),
+                          (half_t)(rows[r].z * qmask), (half_t)(rows[r].w * qmask)};
+      const int chunk = (lane >> 1) ^ (r & 15);
+      *reinterpret_cast<half4_t*>(stage + r * kRowHalfs + chunk * 8 + (lane & 1) * 4) = hv;
+    }
 #pragma unroll
     for (int step = 0; step < kD / 16; ++step) {
-      const int d0 = step * 16 + h * 8;
-      const float4 a = *reinterpret_cast<const float4*>(qrow + d0);
-      const float4 b = *reinterpret_cast<const float4*>(qrow + d0 + 4);
-      qf[step] = half8_t{(half_t)(a.x * qmask), (half_t)(a.y * qmask), (half_t)(a.z * qmask),
-                         (half_t)(a.w * qmask), (half_t)(b.x * qmask), (half_t)(b.y * qmask),
-                         (half_t)(b.z * qmask), (half_t)(b.w * qmask)};
+      const int chunk = (2 * step + h) ^ (n & 15);
+      qf[step] = *reinterpret_cast<const half8_t*>(stage + n * kRowHalfs + chunk * 8);
     }
     // Q stays in AGPRs (an MFMA reads its B operand from either file), which
     // leaves the architectural VGPRs to the scores, P and the fragment rings.
@@ -417,11 +449,15 @@ void flash256_kernel(FlashParams p) {
   };
 
   // Step t (software pipelined): S^T of tile t is in (c0, c1).  After the
-  // barrier that publishes K of tile t+1 and V of tile t, the copies of K(t+2)
-  // and V(t+1) go out; then S^T of tile t+1 runs on the MFMA pipe into (n0, n1)
-  // while the VALU does tile t's mask, max and exponentials; then O += V^T P^T
-  // for tile t, which also covers the last exponentials.  Stage parity
-  // par = t % 2: K(t+1) sits in stage par ^ 1, V(t) in stage par.
+  // barrier that publishes K of tile t+1, S^T of tile t+1 runs on the MFMA pipe
+  // into (n0, n1) while the VALU does tile t's mask, max and exponentials and
+  // the copies of K(t+2) go out; after a second barrier, which publishes V of
+  // tile t, O += V^T P^T for tile t runs while the copies of V(t+1) go out and
+  // the last exponentials finish.  Each copy burst thus has a whole region to
+  // land, and a region's copies are spread over its 32 MFMAs (a CU's
+  // vector-memory path takes a tile's 64 KB only at a few tens of bytes per
+  // clock).  Stage parity par = t % 2: K(t+1) sits in stage par ^ 1, V(t) in
+  // stage par.
   auto step = [&](auto has_next, uint32_t t, float16_t& c0, float16_t& c1, float16_t& n0,
                   float16_t& n1) __attribute__((always_inline)) {
     constexpr bool kNext = decltype(has_next)::value;
@@ -434,41 +470,43 @@ void flash256_kernel(FlashParams p) {
     for (int b = 0; b < 4; ++b) {
       v_byte[b] ^= kStageBytes;
     }
-    wait_tile_copies();
+    // Outstanding here: K(t+1)'s copies, then V(t)'s (none at t = 0: the
+    // prologue waited for everything it issued).
+    constexpr int kc = kCopiesPerTile<W>;
+    wait_copies_but<kc>();
     __syncthreads();
     const uint32_t kt = key_begin + t * kKTile;
     half8_t ring[kRing];
-    // The copies of V(t+1) and K(t+2) are spread over the S^T region (in-order
-    // issue would otherwise hold the wave while the address unit takes them).
     // K(t+2) past the last tile has key rows at or past key_end only: it writes
     // zeros to a stage nothing reads again.
     const uint32_t k_lds = ksrc.lds + par * kStageBytes;
     const uint32_t v_lds = vsrc.lds + (par ^ 1u) * kStageBytes;
-    constexpr int kCopies = 2 * kCopiesPerTile<W>;
-    // M0 walks the copies' LDS addresses: V(t+1)'s, then K(t+2)'s.
+    // M0 walks the copies' LDS addresses: K(t+2)'s in the S^T region, whose
+    // last copy points M0 at V(t+1)'s, walked in the PV region.
     constexpr int kStep = W * 2 * kRowHalfs * 2;
-    auto copy_piece = [&](int i) {
-      // Copies j with j * 32 / kCopies == i (V first, then K).
+    // Copy j of a region goes after MFMA j * 32 / kc + offset (offset < 32 / kc).
+    auto copy_piece = [&](int i, auto is_v, int offset) {
+      constexpr bool kIsV = decltype(is_v)::value;
 #pragma unroll
-      for (int j = 0; j < kCopies; ++j) {
-        if (j * (kD / 8) / kCopies == i) {
-          constexpr int kc = kCopiesPerTile<W>;
-          if (j < kc) {
-            issue_copy_seq<W, true, kStep>(vsrc, coff, kt + kKTile, j, j == kc - 1, k_lds);
+      for (int j = 0; j < kc; ++j) {
+        if (j * (kD / 8) / kc + offset == i) {
+          if (kIsV) {
+            issue_copy_seq<W, true, kStep>(vsrc, coff, kt + kKTile, j, false, 0u);
           } else {
-            issue_copy_seq<W, false, kStep>(ksrc, coff, kt + 2 * kKTile, j - kc, false, 0u);
+            issue_copy_seq<W, false, kStep>(ksrc, coff, kt + 2 * kKTile, j, j == kc - 1, v_lds);
           }
         }
       }
     };
+    using IsV = std::integral_constant<bool, true>;
+    using IsK = std::integral_constant<bool, false>;
     if (kNext) {
       if (W == 1) {
-        // 64 copies per step: issued together (spread, their scalar
+        // 32 copies per region: issued together (spread, their scalar
         // resources would not fit beside the S^T region's registers).
-        issue_tile_copy<W, true>(vsrc, coff, kt + kKTile, v_lds);
         issue_tile_copy<W, false>(ksrc, coff, kt + 2 * kKTile, k_lds);
       } else {
-        set_m0(v_lds);
+        set_m0(k_lds);
       }
 #pragma unroll
       for (int i = 0; i < kRing; ++i) {
@@ -558,13 +596,19 @@ void flash256_kernel(FlashParams p) {
           n0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[i >> 1], n0, 0, 0, 0);
         }
         if (W > 1) {
-          copy_piece(i);
+          copy_piece(i, IsK{}, 0);
         }
       }
       soft_piece(i);
       __builtin_amdgcn_sched_barrier(0);
     }
     // ---- O^T += V^T P^T over the tile's 64 keys (4 k-steps of 16) ----
+    // Outstanding: V(t)'s copies, then K(t+2)'s (none in the last step).
+    wait_copies_but<kNext ? kc : 0>();
+    __syncthreads();
+    if (kNext && W == 1) {
+      issue_tile_copy<W, true>(vsrc, coff, kt + kKTile, v_lds);
+    }
     half8_t vring[kVRing];
 #pragma unroll
     for (int i = 0; i < kVRing; ++i) {
@@ -587,18 +631,18 @@ void flash256_kernel(FlashParams p) {
       if ((i & 3) == 0 && i < 16) {
         exp_piece(12 + (i >> 2));  // pb[3], first read by MFMA 24
       }
+      if (kNext && W > 1) {
+        copy_piece(i, IsV{}, (kD / 8) / kc / 2);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // Prologue: tiles 0's copies were issued above; publish them, start K(1),
-  // and compute S^T of tile 0.
+  // Prologue: the copies of K(0), K(1) and V(0) were issued above; publish
+  // them and compute S^T of tile 0.
   float16_t ca, cb, na, nb;
   wait_tile_copies();
   __syncthreads();
-  if (ntiles > 1) {
-    issue_tile_copy<W, false>(ksrc, coff, key_begin + kKTile, ksrc.lds + kStageBytes);
-  }
   first_scores(ca, cb);
   using Next = std::integral_constant<bool, true>;
   using Last = std::integral_constant<bool, false>;
