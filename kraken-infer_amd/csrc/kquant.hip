@@ -72,8 +72,10 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
 }
 
 __device__ __forceinline__ uint32_t byte_of(const u32x4_t& w, uint32_t k) {
-  const uint32_t word = k < 4 ? w.x : (k < 8 ? w.y : (k < 12 ? w.z : w.w));
-  return (word >> (8u * (k & 3u))) & 0xFFu;
+  // A 64-bit half and a shift (a select chain over the four words can be
+  // turned into an indexed stack copy of the vector).
+  const uint64_t half = k < 8 ? (((uint64_t)w.y << 32) | w.x) : (((uint64_t)w.w << 32) | w.z);
+  return (uint32_t)(half >> (8u * (k & 7u))) & 0xFFu;
 }
 
 // The 6-bit scale and min of sub-block j from the 12 scale bytes held in
@@ -536,8 +538,84 @@ __device__ __forceinline__ float chunk_dot(const RawChunk& r, uint32_t c, const 
   return acc;
 }
 
+// chunk_dot with each sub-block's affine part taken out of the sum: a
+// sub-block of 16 weights w = a * q + b (a = d * scale; b = -dmin * min, or
+// -32 * a for Q6_K) against inputs x gives a * sum(q x) + b * sum(x), and the
+// input sums xs_lo (x[0..15]) and xs_hi (x[16..31]) are fixed for a lane
+// across rows.  A weight then costs a byte conversion and one FMA; the
+// rounding is that of two fp32 sums of 16 terms, well inside the GEMV's
+// accumulation bound.
+template <int F>
+__device__ __forceinline__ float chunk_dot_split(const RawChunk& r, uint32_t c, const float* x,
+                                                 float xs_lo, float xs_hi, float acc) {
+  const uint32_t words[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+  float s_lo = 0.0f, s_hi = 0.0f;
+  float a_lo, a_hi, b_lo, b_hi;
+  if constexpr (F == 2) {
+    const uint32_t g = (c & 3u) >> 1;
+    const uint32_t h = c >> 2;
+    const uint32_t half = c & 1u;
+    const int sc_lo = (int8_t)byte_of(r.c, 8u * h + 2u * g + half);
+    const int sc_hi = (int8_t)byte_of(r.c, 8u * h + 4u + 2u * g + half);
+    const float d = half_bits_to_float(r.d);
+    a_lo = d * (float)sc_lo;
+    a_hi = d * (float)sc_hi;
+    b_lo = -32.0f * a_lo;
+    b_hi = -32.0f * a_hi;
+    const uint32_t lw[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = (lw[k] & 0x0F0F0F0Fu) | (((words[k] >> (2u * g)) & 0x03030303u) << 4);
+      const uint32_t hi =
+        ((lw[k] >> 4) & 0x0F0F0F0Fu) | (((words[k] >> (2u * g + 4u)) & 0x03030303u) << 4);
+      float ql[4], qh[4];
+      bytes_to_float(lo, ql);
+      bytes_to_float(hi, qh);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s_lo = fmaf(ql[e], x[4 * k + e], s_lo);
+        s_hi = fmaf(qh[e], x[16 + 4 * k + e], s_hi);
+      }
+    }
+  } else {
+    const uint32_t sb = c >> 1;
+    uint32_t sc0, m0, sc1, m1;
+    scale_min(r.a, 2u * sb, sc0, m0);
+    scale_min(r.a, 2u * sb + 1u, sc1, m1);
+    const float d = half_bits_to_float(r.a.x);
+    const float dmin = half_bits_to_float(r.a.x >> 16);
+    a_lo = d * (float)sc0;
+    a_hi = d * (float)sc1;
+    b_lo = -(dmin * (float)m0);
+    b_hi = -(dmin * (float)m1);
+    const uint32_t hw[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t lo = words[k] & 0x0F0F0F0Fu;
+      uint32_t hi = (words[k] >> 4) & 0x0F0F0F0Fu;
+      if constexpr (F == 1) {
+        lo |= ((hw[k] >> (2u * sb)) & 0x01010101u) << 4;
+        hi |= ((hw[k] >> (2u * sb + 1u)) & 0x01010101u) << 4;
+      }
+      float ql[4], qh[4];
+      bytes_to_float(lo, ql);
+      bytes_to_float(hi, qh);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s_lo = fmaf(ql[e], x[4 * k + e], s_lo);
+        s_hi = fmaf(qh[e], x[16 + 4 * k + e], s_hi);
+      }
+    }
+  }
+  acc = fmaf(a_lo, s_lo, acc);
+  acc = fmaf(b_lo, xs_lo, acc);
+  acc = fmaf(a_hi, s_hi, acc);
+  return fmaf(b_hi, xs_hi, acc);
+}
+
 constexpr int kXsWaves = 4;
 constexpr int kXsMaxMatrices = 4;
+constexpr int kXsMaxCols = 4096;  // 16 blocks per row
 
 // Up to four weight matrices that read the same input (the projections of one
 // normed hidden state): each has its format, rows, output and optional
@@ -557,6 +635,39 @@ struct MultiGemvArgs {
   float eps;
 };
 
+// The raw weight bytes one lane holds for its rows of one trip slot.  Q4_K and
+// Q5_K (16-byte aligned blocks): the lane's own chunk loads.  Q6_K with
+// staging (internal format 3): the wave's rows are one contiguous byte span,
+// read as 16-byte aligned pieces (piece k = lane + 64 j) and taken apart in
+// LDS, since the 210-byte blocks put a lane's fields at 2-byte alignment and
+// loading them per lane takes sixteen dword loads over a few dozen cache lines.
+constexpr int kSpanPieces = 4;  // 16 * 64 * 4 bytes per wave >= 16 blocks + 15
+template <int F, int PPL>
+struct LaneRaw {
+  RawChunk c[PPL];
+};
+template <int PPL>
+struct LaneRaw<3, PPL> {
+  u32x4_t v[kSpanPieces];
+};
+
+// The 16 bytes at byte offset o (even) of an LDS word array (as load16_even).
+__device__ __forceinline__ u32x4_t lds_load16_even(const uint32_t* words, uint32_t o) {
+  const uint32_t w = o >> 2;
+  const uint32_t shift = o & 3u;
+  const uint32_t w0 = words[w];
+  const uint32_t w1 = words[w + 1];
+  const uint32_t w2 = words[w + 2];
+  const uint32_t w3 = words[w + 3];
+  const uint32_t w4 = words[w + (shift != 0u ? 4 : 3)];
+  u32x4_t r;
+  r.x = __builtin_amdgcn_alignbyte(w1, w0, shift);
+  r.y = __builtin_amdgcn_alignbyte(w2, w1, shift);
+  r.z = __builtin_amdgcn_alignbyte(w3, w2, shift);
+  r.w = __builtin_amdgcn_alignbyte(w4, w3, shift);
+  return r;
+}
+
 // silu(x) * u with the hardware exp2 and reciprocal (about 2 ulp).
 __device__ __forceinline__ float silu_mul_fast(float x, float u) {
   const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
@@ -566,7 +677,10 @@ __device__ __forceinline__ float silu_mul_fast(float x, float u) {
 // The rows of one matrix for one workgroup (local index wl of nwg).
 template <int F, int LR, int PPL, int XF, int U>
 __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_t wl,
-                                          uint32_t nwg) {
+                                          uint32_t nwg, float* s_x, float* s_red,
+                                          u32x4_t* s_span) {
+  constexpr int FB = F == 3 ? 2 : F;  // block format (3: Q6_K read as spans)
+  constexpr bool kSpan = F == 3;
   constexpr int RW = 64 / LR;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -585,43 +699,145 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
     pb[i] = pq >> 3;
     pc[i] = pq & 7u;
   }
-  const uint32_t row_bytes = a.blocks_per_row * KqFormat<F>::kBytes;
+  const uint32_t row_bytes = a.blocks_per_row * KqFormat<FB>::kBytes;
   const uint32_t stride = nwg * (uint32_t)(kXsWaves * RW);
-  auto load_rows = [&](uint32_t r0, RawChunk (&raw)[U][PPL]) __attribute__((always_inline)) {
+  // Span layout: the wave's RW rows from row `first` start `shift` bytes into
+  // the 16-byte piece at span_base(first); pieces at or past the matrix end
+  // (rows * row_bytes, a multiple of 16 for format 3) read as zeros.
+  const uint64_t matrix_bytes = (uint64_t)rows * row_bytes;
+  const uint32_t span_pieces = (15u + (uint32_t)RW * row_bytes + 15u) >> 4;
+  auto load_rows = [&](uint32_t r0, LaneRaw<F, PPL> (&raw)[U]) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t row = r0 + (uint32_t)u * stride + slot;
-      const uint32_t rr = row < rows ? row : rows - 1u;
-      const uint8_t* rp = weight + (uint64_t)rr * row_bytes;
+      if constexpr (kSpan) {
+        const uint64_t start = (uint64_t)(r0 + (uint32_t)u * stride) * row_bytes;
+        const uint64_t base = start & ~(uint64_t)15;
 #pragma unroll
-      for (int i = 0; i < PPL; ++i) {
-        raw[u][i] = load_chunk<F>(rp + pb[i] * KqFormat<F>::kBytes, pc[i]);
+        for (int j = 0; j < kSpanPieces; ++j) {
+          const uint32_t k = (uint32_t)lane + 64u * (uint32_t)j;
+          const uint64_t at = base + 16u * k;
+          raw[u].v[j] = u32x4_t{0u, 0u, 0u, 0u};
+          if (k < span_pieces && at < matrix_bytes) {
+            raw[u].v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(weight + at));
+          }
+        }
+      } else {
+        const uint32_t row = r0 + (uint32_t)u * stride + slot;
+        const uint32_t rr = row < rows ? row : rows - 1u;
+        const uint8_t* rp = weight + (uint64_t)rr * row_bytes;
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) {
+          raw[u].c[i] = load_chunk<FB>(rp + pb[i] * KqFormat<FB>::kBytes, pc[i]);
+        }
       }
+    }
+  };
+  // This lane's chunk i of its row in trip slot (r0, u), from the lane's raw
+  // bytes (format 3: through this wave's LDS span buffer).
+  u32x4_t* span_lds = s_span + wave * (kSpanPieces * 64);
+  auto stage_span = [&](const LaneRaw<F, PPL>& raw) __attribute__((always_inline)) {
+    if constexpr (kSpan) {
+      // Every lane writes its pieces (another lane's chunk may lie in them).
+#pragma unroll
+      for (int j = 0; j < kSpanPieces; ++j) {
+        span_lds[lane + 64 * j] = raw.v[j];
+      }
+    }
+  };
+  auto chunk_of = [&](const LaneRaw<F, PPL>& raw, uint32_t r0, int u, int i)
+      __attribute__((always_inline)) -> RawChunk {
+    if constexpr (kSpan) {
+      const uint32_t shift = (uint32_t)(((uint64_t)(r0 + (uint32_t)u * stride) * row_bytes) & 15u);
+      const uint32_t o = shift + slot * row_bytes + pb[i] * KqFormat<2>::kBytes;
+      const uint32_t c = pc[i];
+      const uint32_t* words = reinterpret_cast<const uint32_t*>(span_lds);
+      RawChunk r;
+      r.a = lds_load16_even(words, o + 16u * c);                                  // ql
+      r.b = lds_load16_even(words, o + 128u + 32u * (c >> 2) + 16u * (c & 1u));   // qh
+      r.c = lds_load16_even(words, o + 192u);                                     // scales
+      r.d = reinterpret_cast<const uint16_t*>(span_lds)[(o + 208u) >> 1];
+      return r;
+    } else {
+      return raw.c[i];
     }
   };
   uint32_t r0 = (wl * kXsWaves + (uint32_t)wave) * RW;
   // The first rows' weight loads go out before the input is read.
-  RawChunk cur[U][PPL];
+  LaneRaw<F, PPL> cur[U];
   load_rows(r0 < rows ? r0 : 0u, cur);
 
-  // The lane's input values (zeros at absent positions); the row's LR lanes
-  // hold the whole input once, so its sum of squares is a group sum.
+  // The transformed input is computed once per workgroup into LDS (each
+  // thread takes up to four float4s of it; the RMSNorm's sum of squares is a
+  // workgroup sum), then each lane reads the 32 * PPL values its chunks need
+  // (zeros at absent positions).  Reading it per row group from global memory
+  // instead would move several times the weight bytes through the caches.
+  {
+    constexpr int kVecPerThread = kXsMaxCols / 4 / (64 * kXsWaves);
+    const uint32_t nvec = a.cols / 4u;
+    float4 xv[kVecPerThread];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const uint32_t vi = threadIdx.x + (uint32_t)(64 * kXsWaves * k);
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (vi < nvec) {
+        v = reinterpret_cast<const float4*>(a.input)[vi];
+        if constexpr (XF == 2) {
+          const float4 u = reinterpret_cast<const float4*>(a.up)[vi];
+          v = make_float4(silu_mul_fast(v.x, u.x), silu_mul_fast(v.y, u.y),
+                          silu_mul_fast(v.z, u.z), silu_mul_fast(v.w, u.w));
+        }
+      }
+      if constexpr (XF == 1) {
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+      }
+      xv[k] = v;
+    }
+    if constexpr (XF == 1) {
+      ss = group_sum<64>(ss);
+      if (lane == 0) {
+        s_red[wave] = ss;
+      }
+      __syncthreads();
+      ss = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kXsWaves; ++w) {
+        ss += s_red[w];
+      }
+      const float scale = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+#pragma unroll
+      for (int k = 0; k < kVecPerThread; ++k) {
+        const uint32_t vi = threadIdx.x + (uint32_t)(64 * kXsWaves * k);
+        if (vi < nvec) {
+          const float4 w = reinterpret_cast<const float4*>(a.norm_weight)[vi];
+          xv[k] = make_float4(xv[k].x * scale * w.x, xv[k].y * scale * w.y,
+                              xv[k].z * scale * w.z, xv[k].w * scale * w.w);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const uint32_t vi = threadIdx.x + (uint32_t)(64 * kXsWaves * k);
+      if (vi < nvec) {
+        reinterpret_cast<float4*>(s_x)[vi] = xv[k];
+      }
+    }
+    __syncthreads();
+  }
   float x[PPL][32];
 #pragma unroll
   for (int i = 0; i < PPL; ++i) {
     uint32_t p0, p1;
-    chunk_positions<F>(pc[i], p0, p1);
+    chunk_positions<FB>(pc[i], p0, p1);
 #pragma unroll
     for (int half_i = 0; half_i < 2; ++half_i) {
       const uint32_t k0 = 256u * pb[i] + (half_i == 0 ? p0 : p1);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        float4 v = *reinterpret_cast<const float4*>(a.input + k0 + 4u * q);
-        if constexpr (XF == 2) {
-          const float4 u = *reinterpret_cast<const float4*>(a.up + k0 + 4u * q);
-          v = make_float4(silu_mul_fast(v.x, u.x), silu_mul_fast(v.y, u.y),
-                          silu_mul_fast(v.z, u.z), silu_mul_fast(v.w, u.w));
-        }
+        const float4 v = *reinterpret_cast<const float4*>(s_x + k0 + 4u * q);
         const bool ok = pv[i];
         x[i][16 * half_i + 4 * q + 0] = ok ? v.x : 0.0f;
         x[i][16 * half_i + 4 * q + 1] = ok ? v.y : 0.0f;
@@ -630,34 +846,15 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
       }
     }
   }
-  if constexpr (XF == 1) {
-    float ss = 0.0f;
+  float xs_lo[PPL], xs_hi[PPL];
 #pragma unroll
-    for (int i = 0; i < PPL; ++i) {
+  for (int i = 0; i < PPL; ++i) {
+    xs_lo[i] = 0.0f;
+    xs_hi[i] = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 32; ++e) {
-        ss = fmaf(x[i][e], x[i][e], ss);
-      }
-    }
-    ss = group_sum<LR>(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
-#pragma unroll
-    for (int i = 0; i < PPL; ++i) {
-      uint32_t p0, p1;
-      chunk_positions<F>(pc[i], p0, p1);
-#pragma unroll
-      for (int half_i = 0; half_i < 2; ++half_i) {
-        const uint32_t k0 = 256u * pb[i] + (half_i == 0 ? p0 : p1);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 w = *reinterpret_cast<const float4*>(a.norm_weight + k0 + 4u * q);
-          float* xe = &x[i][16 * half_i + 4 * q];
-          xe[0] = xe[0] * scale * w.x;
-          xe[1] = xe[1] * scale * w.y;
-          xe[2] = xe[2] * scale * w.z;
-          xe[3] = xe[3] * scale * w.w;
-        }
-      }
+    for (int e = 0; e < 16; ++e) {
+      xs_lo[i] += x[i][e];
+      xs_hi[i] += x[i][16 + e];
     }
   }
   const float* residual = a.residual[m];
@@ -666,18 +863,20 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
   // lanes; the next trip's loads are issued before this trip's math.
   for (; r0 < rows; r0 += (uint32_t)U * stride) {
     const uint32_t nr0 = r0 + (uint32_t)U * stride;
-    RawChunk nxt[U][PPL];
+    LaneRaw<F, PPL> nxt[U];
     if (U > 1 && nr0 < rows) {
       load_rows(nr0, nxt);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t row = r0 + (uint32_t)u * stride + slot;
+      stage_span(cur[u]);
       float acc = 0.0f;
 #pragma unroll
       for (int i = 0; i < PPL; ++i) {
         if (pv[i]) {
-          acc = chunk_dot<F>(cur[u][i], pc[i], x[i], acc);
+          acc = chunk_dot_split<FB>(chunk_of(cur[u], r0, u, i), pc[i], x[i], xs_lo[i], xs_hi[i],
+                                    acc);
         }
       }
       const float total = group_sum<LR>(acc);
@@ -688,10 +887,7 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
     if (U > 1) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int i = 0; i < PPL; ++i) {
-          cur[u][i] = nxt[u][i];
-        }
+        cur[u] = nxt[u];
       }
     } else if (nr0 < rows) {
       load_rows(nr0, cur);
@@ -701,6 +897,9 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
 
 template <int LR, int PPL, int XF, int U>
 __global__ __launch_bounds__(64 * kXsWaves) void kq_gemv_xs_kernel(MultiGemvArgs a) {
+  __shared__ __attribute__((aligned(16))) float s_x[kXsMaxCols];
+  __shared__ float s_red[kXsWaves];
+  __shared__ u32x4_t s_span[kXsWaves * kSpanPieces * 64];
   int m = 0;
 #pragma unroll
   for (int k = 1; k < kXsMaxMatrices; ++k) {
@@ -710,13 +909,16 @@ __global__ __launch_bounds__(64 * kXsWaves) void kq_gemv_xs_kernel(MultiGemvArgs
   const uint32_t nwg = a.wg_begin[m + 1] - a.wg_begin[m];
   switch (a.format[m]) {
     case 0:
-      xs_matrix<0, LR, PPL, XF, U>(a, m, wl, nwg);
+      xs_matrix<0, LR, PPL, XF, U>(a, m, wl, nwg, s_x, s_red, s_span);
       break;
     case 1:
-      xs_matrix<1, LR, PPL, XF, U>(a, m, wl, nwg);
+      xs_matrix<1, LR, PPL, XF, U>(a, m, wl, nwg, s_x, s_red, s_span);
+      break;
+    case 2:
+      xs_matrix<2, LR, PPL, XF, U>(a, m, wl, nwg, s_x, s_red, s_span);
       break;
     default:
-      xs_matrix<2, LR, PPL, XF, U>(a, m, wl, nwg);
+      xs_matrix<3, LR, PPL, XF, U>(a, m, wl, nwg, s_x, s_red, s_span);
       break;
   }
 }
@@ -1112,13 +1314,17 @@ hipError_t launch_gemv_fused_fx(const FusedGemvArgs& a, hipStream_t stream) {
 }
 
 constexpr uint32_t kXsMaxWorkgroups = 1024;  // four per CU, over all matrices
+// Up to this many workgroups the launch covers every row in one trip (the
+// workgroups beyond those resident start as others finish).
+constexpr uint32_t kXsOneTripWorkgroups = 2 * kXsMaxWorkgroups;
 constexpr uint32_t kXsMaxBlocksPerRow = 16;   // two chunks per lane
 
 template <int LR, int PPL, int XF>
 hipError_t launch_xs(MultiGemvArgs a, hipStream_t stream) {
-  // Workgroups per matrix: enough to cover its rows in one trip, scaled down
-  // together when that exceeds kXsMaxWorkgroups (then every workgroup takes
-  // two rows per lane per trip, the next two prefetched).
+  // Workgroups per matrix: enough to cover its rows in one trip, or, past
+  // kXsOneTripWorkgroups, kXsMaxWorkgroups shared in proportion (then every
+  // workgroup takes two rows per lane per trip, the next two prefetched, and
+  // computes the transformed input once for all its trips).
   constexpr uint32_t rows_per_wg = kXsWaves * (64 / LR);
   uint32_t need[kXsMaxMatrices] = {0, 0, 0, 0};
   uint32_t total = 0;
@@ -1126,7 +1332,7 @@ hipError_t launch_xs(MultiGemvArgs a, hipStream_t stream) {
     need[m] = (a.rows[m] + rows_per_wg - 1) / rows_per_wg;
     total += need[m];
   }
-  const bool one_trip = total <= kXsMaxWorkgroups;
+  const bool one_trip = total <= kXsOneTripWorkgroups;
   a.wg_begin[0] = 0;
   for (uint32_t m = 0; m < kXsMaxMatrices; ++m) {
     uint32_t n = 0;
@@ -1156,7 +1362,16 @@ hipError_t launch_xs_x(const MultiGemvArgs& a, hipStream_t stream) {
   return launch_xs<64, 2, XF>(a, stream);
 }
 
-hipError_t launch_multi(const MultiGemvArgs& a, hipStream_t stream) {
+hipError_t launch_multi(MultiGemvArgs a, hipStream_t stream) {
+  // Q6_K matrices read as whole-wave spans (format 3) when every 16-byte piece
+  // of a span lies wholly inside or wholly outside the matrix: a 16-byte
+  // aligned base and rows * blocks_per_row * 210 a multiple of 16.
+  for (uint32_t m = 0; m < a.count; ++m) {
+    if (a.format[m] == 2 && ((uintptr_t)a.weight[m] & 15u) == 0 &&
+        ((uint64_t)a.rows[m] * a.blocks_per_row) % 8u == 0) {
+      a.format[m] = 3;
+    }
+  }
   if (a.norm_weight != nullptr) {
     return launch_xs_x<1>(a, stream);
   }
