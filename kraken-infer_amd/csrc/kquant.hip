@@ -641,14 +641,19 @@ struct MultiGemvArgs {
 // read as 16-byte aligned pieces (piece k = lane + 64 j) and taken apart in
 // LDS, since the 210-byte blocks put a lane's fields at 2-byte alignment and
 // loading them per lane takes sixteen dword loads over a few dozen cache lines.
-constexpr int kSpanPieces = 4;  // 16 * 64 * 4 bytes per wave >= 16 blocks + 15
+// A wave's span holds RW * blocks_per_row <= 8 * PPL blocks (LR lanes per row,
+// 8 chunks per block), so 2 * PPL pieces per lane cover it with the 15-byte
+// lead: 16 * 64 * 2 * PPL bytes >= 8 * PPL * 210 + 15.
+constexpr int kSpanPiecesMax = 4;
+template <int PPL>
+constexpr int kSpanPieces = 2 * PPL;
 template <int F, int PPL>
 struct LaneRaw {
   RawChunk c[PPL];
 };
 template <int PPL>
 struct LaneRaw<3, PPL> {
-  u32x4_t v[kSpanPieces];
+  u32x4_t v[kSpanPieces<PPL>];
 };
 
 // The 16 bytes at byte offset o (even) of an LDS word array (as load16_even).
@@ -713,7 +718,7 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
         const uint64_t start = (uint64_t)(r0 + (uint32_t)u * stride) * row_bytes;
         const uint64_t base = start & ~(uint64_t)15;
 #pragma unroll
-        for (int j = 0; j < kSpanPieces; ++j) {
+        for (int j = 0; j < kSpanPieces<PPL>; ++j) {
           const uint32_t k = (uint32_t)lane + 64u * (uint32_t)j;
           const uint64_t at = base + 16u * k;
           raw[u].v[j] = u32x4_t{0u, 0u, 0u, 0u};
@@ -734,12 +739,12 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
   };
   // This lane's chunk i of its row in trip slot (r0, u), from the lane's raw
   // bytes (format 3: through this wave's LDS span buffer).
-  u32x4_t* span_lds = s_span + wave * (kSpanPieces * 64);
+  u32x4_t* span_lds = s_span + wave * (kSpanPiecesMax * 64);
   auto stage_span = [&](const LaneRaw<F, PPL>& raw) __attribute__((always_inline)) {
     if constexpr (kSpan) {
       // Every lane writes its pieces (another lane's chunk may lie in them).
 #pragma unroll
-      for (int j = 0; j < kSpanPieces; ++j) {
+      for (int j = 0; j < kSpanPieces<PPL>; ++j) {
         span_lds[lane + 64 * j] = raw.v[j];
       }
     }
@@ -762,31 +767,45 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
     }
   };
   uint32_t r0 = (wl * kXsWaves + (uint32_t)wave) * RW;
-  // The first rows' weight loads go out before the input is read.
-  LaneRaw<F, PPL> cur[U];
-  load_rows(r0 < rows ? r0 : 0u, cur);
 
   // The transformed input is computed once per workgroup into LDS (each
   // thread takes up to four float4s of it; the RMSNorm's sum of squares is a
   // workgroup sum), then each lane reads the 32 * PPL values its chunks need
   // (zeros at absent positions).  Reading it per row group from global memory
   // instead would move several times the weight bytes through the caches.
+  // The input loads (and the norm weights or the up half) go out first and
+  // the first rows' weight loads right behind them: loads complete in issue
+  // order, so the transform then waits only for the input while the weights
+  // stream in.
+  constexpr int kVecPerThread = kXsMaxCols / 4 / (64 * kXsWaves);
+  const uint32_t nvec = a.cols / 4u;
+  float4 xv[kVecPerThread], yv[kVecPerThread];
+#pragma unroll
+  for (int k = 0; k < kVecPerThread; ++k) {
+    const uint32_t vi = threadIdx.x + (uint32_t)(64 * kXsWaves * k);
+    xv[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    yv[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (vi < nvec) {
+      xv[k] = reinterpret_cast<const float4*>(a.input)[vi];
+      if constexpr (XF == 1) {
+        yv[k] = reinterpret_cast<const float4*>(a.norm_weight)[vi];
+      } else if constexpr (XF == 2) {
+        yv[k] = reinterpret_cast<const float4*>(a.up)[vi];
+      }
+    }
+  }
+  asm volatile("" ::: "memory");
+  LaneRaw<F, PPL> cur[U];
+  load_rows(r0 < rows ? r0 : 0u, cur);
   {
-    constexpr int kVecPerThread = kXsMaxCols / 4 / (64 * kXsWaves);
-    const uint32_t nvec = a.cols / 4u;
-    float4 xv[kVecPerThread];
     float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < kVecPerThread; ++k) {
-      const uint32_t vi = threadIdx.x + (uint32_t)(64 * kXsWaves * k);
-      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (vi < nvec) {
-        v = reinterpret_cast<const float4*>(a.input)[vi];
-        if constexpr (XF == 2) {
-          const float4 u = reinterpret_cast<const float4*>(a.up)[vi];
-          v = make_float4(silu_mul_fast(v.x, u.x), silu_mul_fast(v.y, u.y),
-                          silu_mul_fast(v.z, u.z), silu_mul_fast(v.w, u.w));
-        }
+      float4 v = xv[k];
+      if constexpr (XF == 2) {
+        const float4 u = yv[k];
+        v = make_float4(silu_mul_fast(v.x, u.x), silu_mul_fast(v.y, u.y),
+                        silu_mul_fast(v.z, u.z), silu_mul_fast(v.w, u.w));
       }
       if constexpr (XF == 1) {
         ss = fmaf(v.x, v.x, ss);
@@ -810,12 +829,9 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
       const float scale = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
 #pragma unroll
       for (int k = 0; k < kVecPerThread; ++k) {
-        const uint32_t vi = threadIdx.x + (uint32_t)(64 * kXsWaves * k);
-        if (vi < nvec) {
-          const float4 w = reinterpret_cast<const float4*>(a.norm_weight)[vi];
-          xv[k] = make_float4(xv[k].x * scale * w.x, xv[k].y * scale * w.y,
-                              xv[k].z * scale * w.z, xv[k].w * scale * w.w);
-        }
+        const float4 w = yv[k];
+        xv[k] = make_float4(xv[k].x * scale * w.x, xv[k].y * scale * w.y,
+                            xv[k].z * scale * w.z, xv[k].w * scale * w.w);
       }
     }
 #pragma unroll
@@ -895,11 +911,15 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
   }
 }
 
+// Four workgroups per CU must be resident for the kXsMaxWorkgroups launches
+// (one chunk per lane: at most 128 VGPRs, four waves per SIMD).
 template <int LR, int PPL, int XF, int U>
-__global__ __launch_bounds__(64 * kXsWaves) void kq_gemv_xs_kernel(MultiGemvArgs a) {
+__global__ __launch_bounds__(64 * kXsWaves)
+__attribute__((amdgpu_waves_per_eu(PPL == 1 ? 4 : 1)))
+void kq_gemv_xs_kernel(MultiGemvArgs a) {
   __shared__ __attribute__((aligned(16))) float s_x[kXsMaxCols];
   __shared__ float s_red[kXsWaves];
-  __shared__ u32x4_t s_span[kXsWaves * kSpanPieces * 64];
+  __shared__ u32x4_t s_span[kXsWaves * kSpanPiecesMax * 64];
   int m = 0;
 #pragma unroll
   for (int k = 1; k < kXsMaxMatrices; ++k) {
@@ -1322,10 +1342,12 @@ constexpr uint32_t kXsMaxBlocksPerRow = 16;   // two chunks per lane
 template <int LR, int PPL, int XF>
 hipError_t launch_xs(MultiGemvArgs a, hipStream_t stream) {
   // Workgroups per matrix: enough to cover its rows in one trip, or, past
-  // kXsOneTripWorkgroups, kXsMaxWorkgroups shared in proportion (then every
+  // kXsOneTripWorkgroups, the resident count shared in proportion (then every
   // workgroup takes two rows per lane per trip, the next two prefetched, and
   // computes the transformed input once for all its trips).
   constexpr uint32_t rows_per_wg = kXsWaves * (64 / LR);
+  // Two chunks per lane take about twice the registers: two workgroups per CU.
+  constexpr uint32_t max_wgs = PPL == 1 ? kXsMaxWorkgroups : kXsMaxWorkgroups / 2;
   uint32_t need[kXsMaxMatrices] = {0, 0, 0, 0};
   uint32_t total = 0;
   for (uint32_t m = 0; m < a.count; ++m) {
@@ -1338,7 +1360,7 @@ hipError_t launch_xs(MultiGemvArgs a, hipStream_t stream) {
     uint32_t n = 0;
     if (m < a.count) {
       n = one_trip ? need[m]
-                   : (uint32_t)(((uint64_t)need[m] * kXsMaxWorkgroups + total - 1) / total);
+                   : (uint32_t)(((uint64_t)need[m] * max_wgs + total - 1) / total);
       n = n == 0 ? 1 : n;
     }
     a.wg_begin[m + 1] = a.wg_begin[m] + n;
