@@ -21,7 +21,18 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def hip_ctx():
-    """One HIP context for the whole GPU session (skips cleanly on CPU)."""
+    """One HIP context for the whole GPU session (skips cleanly on CPU).
+
+    torch (which carries its own HIP runtime) is initialised first when it sees
+    the GPU, as bench.py does, so that tests can hand torch streams and graph
+    captures to the library."""
+    try:
+        import torch
+
+        if torch.cuda.is_available():
+            torch.cuda.init()
+    except ImportError:
+        pass
     import kraken_hip
 
     ctx = kraken_hip.Context()

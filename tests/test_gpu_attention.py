@@ -141,6 +141,54 @@ def test_decode_short_kernel_split_sizes(hip_ctx, monkeypatch, keys_per_split, s
 
 
 @pytest.mark.gpu
+def test_decode_graph_replays(hip_ctx):
+    """Batch-1 decode as bench.py runs it: three steps (two KV sets, two
+    lengths) captured in one HIP graph on a torch stream and replayed three
+    times, with eager work between the replays (the query changes in place);
+    every replay matches the oracle."""
+    torch = pytest.importorskip("torch")
+    heads, kv_heads, d = 8, 2, 256
+    lens = [4096, 1000, 4096]
+    cap = 4097
+    rng = np.random.default_rng(24)
+    kcs = [f16_bits(rng.standard_normal(cap * kv_heads * d)) for _ in range(2)]
+    vcs = [f16_bits(rng.standard_normal(cap * kv_heads * d)) for _ in range(2)]
+    gate = rng.standard_normal(heads * d).astype(np.float32)
+    dev = "cuda"
+    kt = [torch.from_numpy(k.view(np.float16)).to(dev) for k in kcs]
+    vt = [torch.from_numpy(v.view(np.float16)).to(dev) for v in vcs]
+    gt = torch.from_numpy(gate).to(dev)
+    qt = torch.zeros(heads * d, device=dev, dtype=torch.float32)
+    outs = [torch.zeros(heads * d, device=dev, dtype=torch.float32) for _ in lens]
+    stream = torch.cuda.Stream()
+    hip_ctx.set_stream(stream.cuda_stream)
+    hip_ctx.begin_graph()
+    try:
+        with torch.cuda.stream(stream):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i, n in enumerate(lens):
+                    hip_ctx.attention_f32_batched_f16_kv_gated(
+                        qt, kt[i % 2], vt[i % 2], gt, 0, n, 1, cap, heads, kv_heads, d, outs[i])
+            for replay in range(3):
+                q = rng.standard_normal(heads * d).astype(np.float32) * (1.0 + 4.0 * replay)
+                qt.copy_(torch.from_numpy(q).to(dev))
+                torch.cuda.synchronize()
+                graph.replay()
+                stream.synchronize()
+                for i, n in enumerate(lens):
+                    ref = oracle.sigmoid_gate_mul(
+                        oracle.attention_batched(q, kcs[i % 2], vcs[i % 2], 0, n, 1, cap, heads,
+                                                 kv_heads, d), gate)
+                    close(outs[i].cpu().numpy(), ref, msg=f"replay {replay} step {i}")
+                    outs[i].zero_()
+            del graph
+    finally:
+        hip_ctx.commit_graph()
+        hip_ctx.set_stream(None)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("shape", [(1, 300, 16, 8, 128), (8, 64, 8, 2, 256), (3, 9, 4, 1, 64)])
 def test_f32_kv_twin(hip_ctx, shape):
     tokens, start, heads, kv_heads, d = shape
