@@ -1,5 +1,7 @@
 // Chunked (WY / UT-transform) form of the gated-delta-net prefill for head_dim
-// 128, on fp32 MFMA (v_mfma_f32_16x16x4f32).
+// 128, on fp32 MFMA (v_mfma_f32_16x16x4f32), with the sequential scan's two
+// products on fp16 MFMA in split (hi + lo) form, which keeps them to about
+// 2^-20 of fp32.
 //
 // It computes exactly the recurrence of the reference MSL kernel
 // gated_delta_net_f32_batched_qwen35 (mps_backend.mm:2307-2374), per value head
@@ -27,8 +29,8 @@
 //  * gdn_chunk_scan_kernel, one workgroup per (16 state rows, value head),
 //    sequential over the chunks, holds only the recurrence: the 16 x 128 state
 //    slice lives in LDS; per chunk it stores S_0 and forms delta = U - W S_0^T
-//    (stored too) and S_C = gamma_C S_0 + Ktil^T delta (MFMA).  Loader waves
-//    stream the next chunk's W and Ktil^T into LDS meanwhile.
+//    (stored too) and S_C = gamma_C S_0 + Ktil^T delta (split fp16 MFMA).
+//    Loader waves stream the next chunk's W and Ktil^T into LDS meanwhile.
 //  * gdn_chunk_out_kernel, one workgroup per (chunk, value head, 64 state
 //    rows), all in parallel: Y = scale (diag(gamma) Q S_0^T + M delta).
 // Taking Y out of the sequential kernel matters because each of its
@@ -55,10 +57,10 @@ constexpr int kRowPad = kDim + 4;
 constexpr int kCPad = kC + 4;
 constexpr int kScanRows = 16;  // state rows per scan workgroup
 // Workspace block per (chunk, value head), in floats.
-constexpr size_t kOffW = 0;                     // W     [C][D]
+constexpr size_t kOffW = 0;                     // W     [C][D] as f16 (hi | lo), see below
 constexpr size_t kOffGam = kOffW + kC * kDim;   // gamma [C] (exp of the inclusive sum of g)
 constexpr size_t kOffU = kOffGam + kC;          // U^T   [D][C]
-constexpr size_t kOffKT = kOffU + kC * kDim;    // Ktil^T [D][C]
+constexpr size_t kOffKT = kOffU + kC * kDim;    // Ktil^T [D][C] as f16 (hi | lo)
 constexpr size_t kOffM = kOffKT + kDim * kC;    // M     [C][C]
 constexpr size_t kOffS0 = kOffM + kC * kC;     // S_0   [D][D] (state before the chunk)
 constexpr size_t kOffDT = kOffS0 + kDim * kDim; // delta^T [D][C]
@@ -90,6 +92,43 @@ __device__ __forceinline__ float softplus_ref(float x) {
 
 __device__ __forceinline__ float4_v mfma4(float a, float b, float4_v c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Split fp32 products on fp16 MFMA (the scan's two per-chunk products).  A value
+// x is held as hi = f16(x) and lo = f16((x - hi) 2^11), so x = hi + 2^-11 lo to
+// about 2^-21 relative; a product sums hi hi + 2^-11 (hi lo + lo hi) in fp32
+// (the dropped lo lo term is below 2^-20 of the product).  Below the smallest
+// normal f16 (2^-14) hi is zero and the whole value goes into the scaled lo:
+// an f16 denormal hi can be flushed on its way through the matrix core, which
+// would drop up to 6e-5 of the value (measured: 3.5e-4 errors after the
+// norm-gated epilogue); a flushed denormal lo costs at most 2^-25.  W and
+// Ktil^T rows are stored by the prep kernel in this form: a row of n values is
+// n hi halves then n lo halves, the same bytes as the fp32 row.
+constexpr float kLoScale = 2048.0f;        // 2^11
+constexpr float kLoUnscale = 1.0f / 2048.0f;
+constexpr float kF16MinNormal = 6.103515625e-05f;  // 2^-14
+
+__device__ __forceinline__ void split_f16(float x, half_t& hi, half_t& lo) {
+  hi = static_cast<half_t>(fabsf(x) < kF16MinNormal ? 0.0f : x);
+  lo = static_cast<half_t>((x - static_cast<float>(hi)) * kLoScale);
+}
+
+__device__ __forceinline__ void split4_f16(const float x[4], half4_t& hi, half4_t& lo) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    half_t h, l;
+    split_f16(x[c], h, l);
+    hi[c] = h;
+    lo[c] = l;
+  }
+}
+
+// hi hi into acc_h, the cross terms into acc_x (v_mfma_f32_16x16x32_f16).
+__device__ __forceinline__ void mfma_split(half8_t a_hi, half8_t a_lo, half8_t b_hi, half8_t b_lo,
+                                           float4_v& acc_h, float4_v& acc_x) {
+  acc_h = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, b_hi, acc_h, 0, 0, 0);
+  acc_x = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, b_lo, acc_x, 0, 0, 0);
+  acc_x = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo, b_hi, acc_x, 0, 0, 0);
 }
 
 // Eight waves: the prep phases are latency-bound at one workgroup per CU (its
@@ -316,8 +355,12 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
         const float4 kv = make_float4(Ks[t4 + 0][d], Ks[t4 + 1][d], Ks[t4 + 2][d], Ks[t4 + 3][d]);
         *reinterpret_cast<float4*>(&KsT[d][t4]) = kv;
         const float4 e = *reinterpret_cast<const float4*>(&Dec[t4]);
-        *reinterpret_cast<float4*>(blk + kOffKT + d * kC + t4) =
-          make_float4(e.x * kv.x, e.y * kv.y, e.z * kv.z, e.w * kv.w);
+        const float kt[4] = {e.x * kv.x, e.y * kv.y, e.z * kv.z, e.w * kv.w};
+        half4_t hi, lo;
+split4_f16(kt, hi, lo);
+        half_t* row = reinterpret_cast<half_t*>(blk + kOffKT) + d * (2 * kC);
+        *reinterpret_cast<half4_t*>(row + t4) = hi;
+        *reinterpret_cast<half4_t*>(row + kC + t4) = lo;
       }
     }
   };
@@ -424,7 +467,11 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
       if (job >= 32) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          blk[kOffW + (16 * R + 4 * kq + r) * kDim + 16 * Cb + li] = acc[u][r];
+          half_t hi, lo;
+          split_f16(acc[u][r], hi, lo);
+          half_t* row = reinterpret_cast<half_t*>(blk + kOffW) + (16 * R + 4 * kq + r) * (2 * kDim);
+          row[16 * Cb + li] = hi;
+          row[kDim + 16 * Cb + li] = lo;
         }
       } else {  // U transposed: the four tokens of a lane are contiguous
         *reinterpret_cast<float4*>(blk + kOffU + (16 * Cb + li) * kC + 16 * R + 4 * kq) =
@@ -452,6 +499,13 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkParam
   __shared__ __attribute__((aligned(16))) float KTb[2][kDim * kC];
   __shared__ __attribute__((aligned(16))) float Sl[kScanRows][kRowPad];
   __shared__ __attribute__((aligned(16))) float dT[kScanRows][kCPad];
+  // The state slice and delta^T again in split form (hi, lo) for the MFMA B
+  // operands; rows padded by 8 halves so that 16 rows at one column start in
+  // distinct 4-bank groups.
+  __shared__ __attribute__((aligned(16))) half_t Sh[kScanRows][kDim + 8];
+  __shared__ __attribute__((aligned(16))) half_t Slo[kScanRows][kDim + 8];
+  __shared__ __attribute__((aligned(16))) half_t dTh[kScanRows][kC + 8];
+  __shared__ __attribute__((aligned(16))) half_t dTl[kScanRows][kC + 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -498,8 +552,13 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkParam
   for (int idx = tid; idx < kScanRows * (kDim / 4); idx += kScanThreads) {
     const int r = idx >> 5;
     const int c4 = (idx & 31) * 4;
-    *reinterpret_cast<float4*>(&Sl[r][c4]) =
-      *reinterpret_cast<const float4*>(shead + (size_t)r * kDim + c4);
+    const float4 v = *reinterpret_cast<const float4*>(shead + (size_t)r * kDim + c4);
+    *reinterpret_cast<float4*>(&Sl[r][c4]) = v;
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    half4_t hi, lo;
+split4_f16(x, hi, lo);
+    *reinterpret_cast<half4_t*>(&Sh[r][c4]) = hi;
+    *reinterpret_cast<half4_t*>(&Slo[r][c4]) = lo;
   }
   if (wave >= kScanCompute) {
     load_chunk(0, 0);
@@ -553,53 +612,67 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkParam
     const char* wb = reinterpret_cast<const char*>(&Wb[b][0]);
     const char* kb = reinterpret_cast<const char*>(&KTb[b][0]);
     load_u(min(cl + 1, p.chunks - 1), nu, ngamma_c);
-    // State slice as the B operand: lane (j, kq) holds S[j][16 s + 4 kq + c],
-    // s < 8, c < 4 (k = 16 s + 4 kq + c in MFMA 4 s + c, for A and B alike).
-    float sb[32];
-#pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4) {
-      const float4 v = *reinterpret_cast<const float4*>(&Sl[li][16 * s4 + 4 * kq]);
-      sb[4 * s4 + 0] = v.x;
-      sb[4 * s4 + 1] = v.y;
-      sb[4 * s4 + 2] = v.z;
-      sb[4 * s4 + 3] = v.w;
-    }
-    // W S_0^T for tokens 16 w .. 16 w + 15 (W row 16 w + li, logical chunk
-    // 4 s + kq at physical chunk (4 s + kq) ^ li).
+    // delta = U - W S_0^T for tokens 16 w .. 16 w + 15 on split fp16 MFMA
+    // (v_mfma_f32_16x16x32_f16, k steps of 32 key dims): lane (li, kq) holds
+    // A = W[16 w + li][32 s + 8 kq .. + 7] (hi at logical chunk 4 s + kq of the
+    // row, lo at 16 + 4 s + kq; physical chunk = logical ^ li) and
+    // B = S_0[li][32 s + 8 kq .. + 7].
     const int wrow = 16 * wave + li;
-    float4_v acc = {0.f, 0.f, 0.f, 0.f};
+    float4_v acc_h = {0.f, 0.f, 0.f, 0.f};
+    float4_v acc_x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4) {
-      const float4 a =
-        *reinterpret_cast<const float4*>(wb + wrow * 512 + 16 * ((4 * s4 + kq) ^ li));
-      acc = mfma4(a.x, sb[4 * s4 + 0], acc);
-      acc = mfma4(a.y, sb[4 * s4 + 1], acc);
-      acc = mfma4(a.z, sb[4 * s4 + 2], acc);
-      acc = mfma4(a.w, sb[4 * s4 + 3], acc);
+    for (int st = 0; st < kDim / 32; ++st) {
+      const half8_t a_hi =
+        *reinterpret_cast<const half8_t*>(wb + wrow * 512 + 16 * ((4 * st + kq) ^ li));
+      const half8_t a_lo =
+        *reinterpret_cast<const half8_t*>(wb + wrow * 512 + 16 * ((16 + 4 * st + kq) ^ li));
+      const half8_t b_hi = *reinterpret_cast<const half8_t*>(&Sh[li][32 * st + 8 * kq]);
+      const half8_t b_lo = *reinterpret_cast<const half8_t*>(&Slo[li][32 * st + 8 * kq]);
+      mfma_split(a_hi, a_lo, b_hi, b_lo, acc_h, acc_x);
     }
-    // delta = U - W S_0^T, kept transposed (rows j, tokens t) in LDS; the
-    // loader waves store it.
-    *reinterpret_cast<float4*>(&dT[li][16 * wave + 4 * kq]) =
-      make_float4(u.x - acc[0], u.y - acc[1], u.z - acc[2], u.w - acc[3]);
+    // delta^T (rows j, tokens t): lane holds tokens 16 w + 4 kq + r of row li.
+    // fp32 for the loader waves to store, split for the S_C product.
+    {
+      const float d[4] = {u.x - (acc_h[0] + kLoUnscale * acc_x[0]),
+                          u.y - (acc_h[1] + kLoUnscale * acc_x[1]),
+                          u.z - (acc_h[2] + kLoUnscale * acc_x[2]),
+                          u.w - (acc_h[3] + kLoUnscale * acc_x[3])};
+      *reinterpret_cast<float4*>(&dT[li][16 * wave + 4 * kq]) = make_float4(d[0], d[1], d[2], d[3]);
+      half4_t hi, lo;
+split4_f16(d, hi, lo);
+      *reinterpret_cast<half4_t*>(&dTh[li][16 * wave + 4 * kq]) = hi;
+      *reinterpret_cast<half4_t*>(&dTl[li][16 * wave + 4 * kq]) = lo;
+    }
     __syncthreads();  // B1
-    // S_C^T rows (key dims) 32 w .. 32 w + 31 = gamma_C S_0^T + Ktil^T delta
-    // (Ktil^T row 32 w + 16 tt + li, logical chunk 4 s + kq at (4 s + kq) ^ li).
+    // S_C^T rows (key dims) 32 w .. 32 w + 31 = gamma_C S_0^T + Ktil^T delta,
+    // k steps of 32 tokens: A = Ktil^T[32 w + 16 tt + li][32 s + 8 kq .. + 7]
+    // (hi at logical chunk 4 s + kq, lo at 8 + 4 s + kq; physical = logical ^ li),
+    // B = delta[32 s + 8 kq .. + 7][li].
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       const int kbase = 32 * wave + 16 * tt;
       const float4 s0 = *reinterpret_cast<const float4*>(&Sl[li][kbase + 4 * kq]);
-      float4_v s = {gamma_c * s0.x, gamma_c * s0.y, gamma_c * s0.z, gamma_c * s0.w};
+      float4_v sh = {0.f, 0.f, 0.f, 0.f};
+      float4_v sx = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const float4 a = *reinterpret_cast<const float4*>(kb + (kbase + li) * 256 +
-                                                          16 * ((4 * s4 + kq) ^ li));
-        const float4 d = *reinterpret_cast<const float4*>(&dT[li][16 * s4 + 4 * kq]);
-        s = mfma4(a.x, d.x, s);
-        s = mfma4(a.y, d.y, s);
-        s = mfma4(a.z, d.z, s);
-        s = mfma4(a.w, d.w, s);
+      for (int st = 0; st < kC / 32; ++st) {
+        const half8_t a_hi = *reinterpret_cast<const half8_t*>(kb + (kbase + li) * 256 +
+                                                               16 * ((4 * st + kq) ^ li));
+        const half8_t a_lo = *reinterpret_cast<const half8_t*>(kb + (kbase + li) * 256 +
+                                                               16 * ((8 + 4 * st + kq) ^ li));
+        const half8_t b_hi = *reinterpret_cast<const half8_t*>(&dTh[li][32 * st + 8 * kq]);
+        const half8_t b_lo = *reinterpret_cast<const half8_t*>(&dTl[li][32 * st + 8 * kq]);
+        mfma_split(a_hi, a_lo, b_hi, b_lo, sh, sx);
       }
-      *reinterpret_cast<float4*>(&Sl[li][kbase + 4 * kq]) = make_float4(s[0], s[1], s[2], s[3]);
+      const float sc[4] = {fmaf(gamma_c, s0.x, sh[0] + kLoUnscale * sx[0]),
+                           fmaf(gamma_c, s0.y, sh[1] + kLoUnscale * sx[1]),
+                           fmaf(gamma_c, s0.z, sh[2] + kLoUnscale * sx[2]),
+                           fmaf(gamma_c, s0.w, sh[3] + kLoUnscale * sx[3])};
+      *reinterpret_cast<float4*>(&Sl[li][kbase + 4 * kq]) = make_float4(sc[0], sc[1], sc[2], sc[3]);
+      half4_t hi, lo;
+split4_f16(sc, hi, lo);
+      *reinterpret_cast<half4_t*>(&Sh[li][kbase + 4 * kq]) = hi;
+      *reinterpret_cast<half4_t*>(&Slo[li][kbase + 4 * kq]) = lo;
     }
     __syncthreads();  // B2
     u = nu;

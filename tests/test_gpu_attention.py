@@ -163,13 +163,20 @@ def test_decode_graph_replays(hip_ctx):
     stream = torch.cuda.Stream()
     hip_ctx.set_stream(stream.cuda_stream)
     hip_ctx.begin_graph()
+    def steps():
+        for i, n in enumerate(lens):
+            hip_ctx.attention_f32_batched_f16_kv_gated(
+                qt, kt[i % 2], vt[i % 2], gt, 0, n, 1, cap, heads, kv_heads, d, outs[i])
+
     try:
         with torch.cuda.stream(stream):
+            # One eager pass first: the context sizes its workspace outside the
+            # capture (a capturing stream cannot wait for a resize).
+            steps()
+            stream.synchronize()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream):
-                for i, n in enumerate(lens):
-                    hip_ctx.attention_f32_batched_f16_kv_gated(
-                        qt, kt[i % 2], vt[i % 2], gt, 0, n, 1, cap, heads, kv_heads, d, outs[i])
+                steps()
             for replay in range(3):
                 q = rng.standard_normal(heads * d).astype(np.float32) * (1.0 + 4.0 * replay)
                 qt.copy_(torch.from_numpy(q).to(dev))
