@@ -30,7 +30,8 @@
 //    fp16 in two streaming passes, then an fp16 MFMA GEMM (v_mfma_f32_32x32x16_f16,
 //    128 x 128 output tile per 4-wave workgroup, 64-deep K steps double-
 //    buffered through LDS with XOR-swizzled 16-byte chunks) writes
-//    [tokens][rows] in fp32.
+//    [tokens][rows] in fp32; grids too small for the chip split K into fp32
+//    partial planes summed by one more pass.
 //  * argmax: per-workgroup (max, first index, sum of exp) candidates, merged by
 //    one workgroup; sizes that fit one workgroup take a single launch.
 #include <hip/hip_runtime.h>
@@ -1030,57 +1031,77 @@ __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* in, half_t
 
 // ------------------------------------------------------------------ GEMM ----
 // C[t][r] = sum_k X[t][k] W[r][k] with X [M = tokens][K], W [N = rows][K] fp16
-// (both K-contiguous), C fp32 [M][N].  128 x 128 tile per workgroup of four
-// waves; wave w owns tokens 64 (w / 2) .. + 63 and rows 64 (w % 2) .. + 63 as
-// 2 x 2 tiles of v_mfma_f32_32x32x16_f16.  K steps of 64 through two LDS
-// stages; a 16-byte chunk j of tile row i lives at chunk j ^ (i & 7), so the
-// fragment reads (32 rows, one chunk each) hit distinct banks.
-constexpr int kGM = 128, kGN = 128, kGK = 64;
+// (both K-contiguous), C fp32 [M][N].  TM x TN tile per workgroup of four
+// waves (128 x 128, or 64 x 64 when the large tiles would leave most CUs
+// idle); wave w owns tokens TM/2 (w / 2) .. + TM/2 - 1 and rows TN/2 (w % 2)
+// .. + TN/2 - 1 as (TM/64) x (TN/64) tiles of v_mfma_f32_32x32x16_f16.  K
+// steps of 64 through two LDS stages; a 16-byte chunk j of tile row i lives at
+// chunk j ^ (i & 7), so the fragment reads (32 rows, one chunk each) hit
+// distinct banks.
+constexpr int kGK = 64;
 typedef float float16v_t __attribute__((ext_vector_type(16)));
 
+template <int TM, int TN>
 __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const half_t* w,
                                                           float* c, uint32_t m, uint32_t n,
-                                                          uint32_t k) {
-  __shared__ __attribute__((aligned(16))) half_t s_a[2][kGM * kGK];
-  __shared__ __attribute__((aligned(16))) half_t s_b[2][kGN * kGK];
+                                                          uint32_t k, uint32_t split_steps) {
+  static_assert(TM % 64 == 0 && TN % 64 == 0, "whole 32 x 32 MFMA tiles per wave");
+  constexpr int IA = TM / 64;   // MFMA tiles per wave along tokens
+  constexpr int JB = TN / 64;   // along rows
+  constexpr int LA = TM / 32;   // 16-byte chunks per thread per A tile step
+  constexpr int LB = TN / 32;
+  __shared__ __attribute__((aligned(16))) half_t s_a[2][TM * kGK];
+  __shared__ __attribute__((aligned(16))) half_t s_b[2][TN * kGK];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const uint32_t m0 = blockIdx.y * kGM;
-  const uint32_t n0 = blockIdx.x * kGN;
+  const uint32_t m0 = blockIdx.y * TM;
+  const uint32_t n0 = blockIdx.x * TN;
   // Range-checked operands: rows past the matrix read as zeros.
   const __amdgpu_buffer_rsrc_t xr =
-    make_buffer_rsrc(x + (uint64_t)m0 * k, (uint32_t)min((uint64_t)kGM, (uint64_t)(m - m0)) * k * 2u);
+    make_buffer_rsrc(x + (uint64_t)m0 * k, (uint32_t)min((uint64_t)TM, (uint64_t)(m - m0)) * k * 2u);
   const __amdgpu_buffer_rsrc_t wr =
-    make_buffer_rsrc(w + (uint64_t)n0 * k, (uint32_t)min((uint64_t)kGN, (uint64_t)(n - n0)) * k * 2u);
-  // Global -> register staging: thread t moves chunks t + 256 i (i < 4) of
-  // each 128 x 64 tile (row = idx / 8, chunk = idx % 8).
-  u32x4_t ra[4], rb[4];
+    make_buffer_rsrc(w + (uint64_t)n0 * k, (uint32_t)min((uint64_t)TN, (uint64_t)(n - n0)) * k * 2u);
+  // Global -> register staging: thread t moves chunks t + 256 i of each
+  // T x 64 tile (row = idx / 8, chunk = idx % 8).
+  u32x4_t ra[LA], rb[LB];
   auto load_step = [&](uint32_t kk) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < LA; ++i) {
       const int idx = tid + 256 * i;
       const uint32_t row = (uint32_t)(idx >> 3);
       const uint32_t off = (row * k + kk + 8u * (uint32_t)(idx & 7)) * 2u;
       ra[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      const int idx = tid + 256 * i;
+      const uint32_t row = (uint32_t)(idx >> 3);
+      const uint32_t off = (row * k + kk + 8u * (uint32_t)(idx & 7)) * 2u;
       rb[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)off, 0, 0));
     }
   };
   auto store_step = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < LA; ++i) {
       const int idx = tid + 256 * i;
       const int row = idx >> 3;
       const int chunk = (idx & 7) ^ (row & 7);
       *reinterpret_cast<u32x4_t*>(&s_a[st][row * kGK + 8 * chunk]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      const int idx = tid + 256 * i;
+      const int row = idx >> 3;
+      const int chunk = (idx & 7) ^ (row & 7);
       *reinterpret_cast<u32x4_t*>(&s_b[st][row * kGK + 8 * chunk]) = rb[i];
     }
   };
-  float16v_t acc[2][2];
+  float16v_t acc[IA][JB];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < IA; ++i) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < JB; ++j) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         acc[i][j][e] = 0.0f;
@@ -1091,34 +1112,39 @@ __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const
   const int wn = wave & 1;
   const int frow = lane & 31;
   const int fk = lane >> 5;
-  load_step(0);
+  // K split z (blockIdx.z) takes K steps [z * split_steps, ...) and writes its
+  // partial sums to plane z of c (split_steps = all steps: one plane, C itself).
+  const uint32_t s_begin = blockIdx.z * split_steps;
+  const uint32_t total_steps = k / kGK;
+  const uint32_t steps = s_begin < total_steps ? min(total_steps - s_begin, split_steps) : 0u;
+  c += (uint64_t)blockIdx.z * m * n;
+  load_step(s_begin * kGK);
   store_step(0);
   __syncthreads();
-  const uint32_t steps = k / kGK;
   for (uint32_t s = 0; s < steps; ++s) {
     const int st = (int)(s & 1u);
     if (s + 1 < steps) {
-      load_step((s + 1) * kGK);
+      load_step((s_begin + s + 1) * kGK);
     }
 #pragma unroll
     for (int ks = 0; ks < kGK / 16; ++ks) {
-      half8_t fa[2], fb[2];
+      half8_t fa[IA], fb[JB];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int row = 64 * wm + 32 * i + frow;
+      for (int i = 0; i < IA; ++i) {
+        const int row = (TM / 2) * wm + 32 * i + frow;
         const int chunk = (2 * ks + fk) ^ (row & 7);
         fa[i] = *reinterpret_cast<const half8_t*>(&s_a[st][row * kGK + 8 * chunk]);
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int row = 64 * wn + 32 * j + frow;
+      for (int j = 0; j < JB; ++j) {
+        const int row = (TN / 2) * wn + 32 * j + frow;
         const int chunk = (2 * ks + fk) ^ (row & 7);
         fb[j] = *reinterpret_cast<const half8_t*>(&s_b[st][row * kGK + 8 * chunk]);
       }
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < IA; ++i) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < JB; ++j) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
       }
@@ -1131,19 +1157,57 @@ __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const
   // D layout: lane l holds column (row of W) l % 32 and tokens
   // 8 (e / 4) + 4 (l / 32) + e % 4 of its 32 x 32 tile.
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < IA; ++i) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t col = n0 + 64u * wn + 32u * j + (uint32_t)frow;
+    for (int j = 0; j < JB; ++j) {
+      const uint32_t col = n0 + (TN / 2) * wn + 32u * j + (uint32_t)frow;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const uint32_t row = m0 + 64u * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
+        const uint32_t row = m0 + (TM / 2) * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
         if (row < m && col < n) {
           c[(uint64_t)row * n + col] = acc[i][j][e];
         }
       }
     }
   }
+}
+
+// K splits: a 128 x 128 grid that would fill less than half of a 256-CU chip
+// (the 1024-row projections at 1024 tokens: 64 tiles) splits K into up to four
+// ranges of whole 64-deep steps, each writing an fp32 partial plane that one
+// more pass sums in a fixed order.  Smaller tiles instead (64 x 64: four times
+// the workgroups) were measured slower at K = 2048: each CU then loads twice
+// the operand bytes per MFMA, and a CU's load path is what bounds the kernel.
+constexpr uint64_t kGemmSmallGrid = 128;
+constexpr uint32_t kGemmMaxSplits = 4;
+
+uint32_t gemm_k_splits(size_t rows, size_t cols, size_t tokens) {
+  const uint64_t tiles = (uint64_t)((rows + 127) / 128) * ((tokens + 127) / 128);
+  const uint32_t steps = (uint32_t)(cols / kGK);
+  uint32_t splits = 1;
+  while (splits < kGemmMaxSplits && tiles * splits * 2 <= 2 * kGemmSmallGrid && steps >= 8 * splits * 2) {
+    splits *= 2;
+  }
+  // The plane sum moves float4s: the output must be a whole number of them.
+  return tiles >= kGemmSmallGrid || (tokens * rows) % 4u != 0 ? 1u : splits;
+}
+
+__global__ __launch_bounds__(256) void sum_planes_kernel(const float* planes, float* out,
+                                                         uint64_t n4, uint32_t count) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i >= n4) {
+    return;
+  }
+  const float4* p = reinterpret_cast<const float4*>(planes);
+  float4 acc = p[i];
+  for (uint32_t z = 1; z < count; ++z) {
+    const float4 v = p[z * n4 + i];
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  reinterpret_cast<float4*>(out)[i] = acc;
 }
 
 // ---------------------------------------------------------------- argmax ----
@@ -1469,7 +1533,9 @@ size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_
   if (tokens <= kKquantGemvMaxTokens) {
     return 0;
   }
-  return align256(rows * cols * 2u) + align256(tokens * cols * 2u);
+  const uint32_t splits = gemm_k_splits(rows, cols, tokens);
+  return align256(rows * cols * 2u) + align256(tokens * cols * 2u) +
+         (splits > 1 ? align256(splits * tokens * rows * 4u) : 0u);
 }
 
 hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, size_t cols,
@@ -1514,9 +1580,22 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
   if ((e = hipGetLastError()) != hipSuccess) {
     return e;
   }
-  const dim3 grid((uint32_t)((rows + kGN - 1) / kGN), (uint32_t)((tokens + kGM - 1) / kGM));
-  gemm_f16_nt_kernel<<<grid, 256, 0, stream>>>(x16, w16, output, (uint32_t)tokens,
-                                               (uint32_t)rows, (uint32_t)cols);
+  const uint32_t splits = gemm_k_splits(rows, cols, tokens);
+  const uint32_t steps = (uint32_t)(cols / kGK);
+  const uint32_t split_steps = (steps + splits - 1) / splits;
+  float* planes = splits > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(x16) +
+                                                        align256(tokens * cols * 2u))
+                             : output;
+  const dim3 grid((uint32_t)((rows + 127) / 128), (uint32_t)((tokens + 127) / 128), splits);
+  gemm_f16_nt_kernel<128, 128><<<grid, 256, 0, stream>>>(x16, w16, planes, (uint32_t)tokens,
+                                                         (uint32_t)rows, (uint32_t)cols,
+                                                         split_steps);
+  if ((e = hipGetLastError()) != hipSuccess || splits == 1) {
+    return e;
+  }
+  const uint64_t n4 = (uint64_t)tokens * rows / 4u;
+  sum_planes_kernel<<<dim3((uint32_t)((n4 + 255) / 256)), 256, 0, stream>>>(planes, output, n4,
+                                                                         splits);
   return hipGetLastError();
 }
 
