@@ -235,10 +235,6 @@ __device__ __forceinline__ void issue_tile_copy(const TileSource& src, const Cop
   }
 }
 
-__device__ __forceinline__ void wait_tile_copies() {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
-
 // Wait until at most N of this wave's vector-memory loads are outstanding.  The
 // loop issues no other vector-memory loads than the tile copies, and loads
 // complete in issue order, so this waits for all but the newest N copies.
@@ -331,11 +327,10 @@ void flash256_kernel(FlashParams p) {
   const TileSource vsrc{rsrc_words(v_layer, key_end * row_bytes), row_bytes,
                         (uint32_t)(uintptr_t)(lds_void_t*)s_v + slot_bytes};
 
-  // The first tiles' copies go out before the query is loaded (K(1) past
-  // key_end reads as zeros).
+  // K(0)'s copies go out before the query is loaded; K(1)'s and V(0)'s after
+  // the query is staged, so that the first S^T waits only for K(0) and the
+  // query (K(1) past key_end reads as zeros).
   issue_tile_copy<W, false>(ksrc, coff, key_begin, ksrc.lds);
-  issue_tile_copy<W, false>(ksrc, coff, key_begin + kKTile, ksrc.lds + kStageBytes);
-  issue_tile_copy<W, true>(vsrc, coff, key_begin, vsrc.lds);
 
   // Q^T as the B operand of S^T = K Q^T: lane holds query n, dims 16*step + 8*h + j.
   // A lane's fragment takes 32 bytes from each of 16 places in its query row,
@@ -377,6 +372,8 @@ void flash256_kernel(FlashParams p) {
       asm volatile("" : "+a"(qf[step]));
     }
   }
+  issue_tile_copy<W, false>(ksrc, coff, key_begin + kKTile, ksrc.lds + kStageBytes);
+  issue_tile_copy<W, true>(vsrc, coff, key_begin, vsrc.lds);
 
   float16_t o[kD / 32];  // O^T tiles: dims 32*dt + c_row(r, h), query n
 #pragma unroll
@@ -649,10 +646,12 @@ void flash256_kernel(FlashParams p) {
     }
   };
 
-  // Prologue: the copies of K(0), K(1) and V(0) were issued above; publish
-  // them and compute S^T of tile 0.
+  // Prologue: publish K(0) (its copies and the query loads were issued before
+  // K(1)'s and V(0)'s, and loads complete in issue order) and compute S^T of
+  // tile 0; step 0 waits for K(1) and V(0).
   float16_t ca, cb, na, nb;
-  wait_tile_copies();
+  constexpr int kAfterK0 = 2 * kCopiesPerTile<W> <= 63 ? 2 * kCopiesPerTile<W> : kCopiesPerTile<W>;
+  wait_copies_but<kAfterK0>();
   __syncthreads();
   first_scores(ca, cb);
   using Next = std::integral_constant<bool, true>;
