@@ -139,12 +139,18 @@ constexpr int kPrepWaves = kPrepThreads / 64;
 
 template <bool kPrepare>
 __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParams p) {
-  __shared__ __attribute__((aligned(16))) float Ks[kC][kRowPad];
-  // Q (rows) for the Gram matrices, then K^T (rows = key dims) for W: the
-  // products U and W read their B operand four tokens at a time from the
-  // transposed V and K.
-  __shared__ __attribute__((aligned(16))) float QK[kDim * kCPad];
-  __shared__ __attribute__((aligned(16))) float VsT[kDim][kCPad];
+  // Operands of the split fp16 products, staged once in split form (hi, lo):
+  // K rows; Q rows for the Gram matrices, then (same space) K^T rows (key
+  // dims) for W; V^T rows for U.  Rows are padded by 8 halves so that 16 rows
+  // at one column start in distinct 4-bank groups.
+  constexpr int kRowH = kDim + 8;  // halves per K / Q row
+  constexpr int kColH = kC + 8;    // halves per K^T / V^T row
+  __shared__ __attribute__((aligned(16))) half_t Kh[kC][kRowH];
+  __shared__ __attribute__((aligned(16))) half_t Kl[kC][kRowH];
+  __shared__ __attribute__((aligned(16))) half_t QKT[2 * kDim * kColH];
+  __shared__ __attribute__((aligned(16))) half_t VTh[kDim][kColH];
+  __shared__ __attribute__((aligned(16))) half_t VTl[kDim][kColH];
+  static_assert(2 * kC * kRowH <= 2 * kDim * kColH, "Q fits the shared Q / K^T array");
   __shared__ __attribute__((aligned(16))) float As[kC][kCPad];
   __shared__ __attribute__((aligned(16))) float Ts[kC][kCPad];
   __shared__ float Gs[kC], Bs[kC], Gam[kC];
@@ -163,9 +169,10 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
   const uint32_t t0 = c * kC;
   const uint32_t n = min((uint32_t)kC, p.tokens - t0);
   float* blk = p.ws + ((size_t)cl * p.value_heads + h) * kBlockFloats;
-  float(*Qs)[kRowPad] = reinterpret_cast<float(*)[kRowPad]>(QK);
-  float(*KsT)[kCPad] = reinterpret_cast<float(*)[kCPad]>(QK);
-  static_assert(kC * kRowPad <= kDim * kCPad, "Q fits the shared Q / K^T array");
+  half_t(*Qh)[kRowH] = reinterpret_cast<half_t(*)[kRowH]>(QKT);
+  half_t(*Ql)[kRowH] = reinterpret_cast<half_t(*)[kRowH]>(QKT + kC * kRowH);
+  half_t(*KTh)[kColH] = reinterpret_cast<half_t(*)[kColH]>(QKT);
+  half_t(*KTl)[kColH] = reinterpret_cast<half_t(*)[kColH]>(QKT + kDim * kColH);
 
   // ---- stage K, Q, V^T (rows past the chunk's tokens are zero) ----
   // Unconditional loads from a valid row (the chunk's first token stands in for
@@ -183,8 +190,15 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
     if (!ok) {
       kk = qq = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    *reinterpret_cast<float4*>(&Ks[t][c4]) = kk;
-    *reinterpret_cast<float4*>(&Qs[t][c4]) = qq;
+    const float kx[4] = {kk.x, kk.y, kk.z, kk.w};
+    const float qx[4] = {qq.x, qq.y, qq.z, qq.w};
+    half4_t hi, lo;
+    split4_f16(kx, hi, lo);
+    *reinterpret_cast<half4_t*>(&Kh[t][c4]) = hi;
+    *reinterpret_cast<half4_t*>(&Kl[t][c4]) = lo;
+    split4_f16(qx, hi, lo);
+    *reinterpret_cast<half4_t*>(&Qh[t][c4]) = hi;
+    *reinterpret_cast<half4_t*>(&Ql[t][c4]) = lo;
   }
   // V transposed: four lanes read 64 contiguous bytes of a row, sixteen rows per
   // 64 lanes, so the transposed writes of a row go to 16 consecutive tokens.
@@ -199,10 +213,14 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
     if (!ok) {
       vv = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    VsT[c4 + 0][t] = vv.x;
-    VsT[c4 + 1][t] = vv.y;
-    VsT[c4 + 2][t] = vv.z;
-    VsT[c4 + 3][t] = vv.w;
+    const float vx[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      half_t hi, lo;
+      split_f16(vx[e], hi, lo);
+      VTh[c4 + e][t] = hi;
+      VTl[c4 + e][t] = lo;
+    }
   }
   for (int idx = tid; idx < kC * kCPad; idx += kPrepThreads) {
     (&As[0][0])[idx] = 0.0f;
@@ -266,6 +284,25 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
     }
   };
   static_assert(kPrepWaves == 8, "job assignment");
+  // X rows 16 I .. + 15 times K rows 16 J .. + 15 over k steps [s0, s1) of 32
+  // key dims, split fp16 (lane (li, kq): dims 32 s + 8 kq .. + 7 of row li).
+  auto gram_acc = [&](bool is_q, int I, int J, int s0, int s1, float4_v& ah, float4_v& ax)
+                    __attribute__((always_inline)) {
+    const half_t(*Xh)[kRowH] = is_q ? Qh : Kh;
+    const half_t(*Xl)[kRowH] = is_q ? Ql : Kl;
+#pragma unroll
+    for (int st = s0; st < s1; ++st) {
+      const int c = 32 * st + 8 * kq;
+      mfma_split(*reinterpret_cast<const half8_t*>(&Xh[16 * I + li][c]),
+                 *reinterpret_cast<const half8_t*>(&Xl[16 * I + li][c]),
+                 *reinterpret_cast<const half8_t*>(&Kh[16 * J + li][c]),
+                 *reinterpret_cast<const half8_t*>(&Kl[16 * J + li][c]), ah, ax);
+    }
+  };
+  auto combine = [&](const float4_v& ah, const float4_v& ax) __attribute__((always_inline)) {
+    return float4_v{ah[0] + kLoUnscale * ax[0], ah[1] + kLoUnscale * ax[1],
+                    ah[2] + kLoUnscale * ax[2], ah[3] + kLoUnscale * ax[3]};
+  };
   {
     // Jobs w and w + 8 (0..15) in one pass with independent accumulators.
     const int job = wave;
@@ -273,26 +310,14 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
     bool q0, q1;
     gram_tile(job, I0, J0, q0);
     gram_tile(job + 8, I1, J1, q1);
-    const float(*X0)[kRowPad] = q0 ? Qs : Ks;
-    const float(*X1)[kRowPad] = q1 ? Qs : Ks;
-    float4_v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+    float4_v h0 = {0.f, 0.f, 0.f, 0.f}, x0 = h0, h1 = h0, x1 = h0;
 #pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4) {
-      const float4 a0 = *reinterpret_cast<const float4*>(&X0[16 * I0 + li][16 * s4 + 4 * kq]);
-      const float4 b0 = *reinterpret_cast<const float4*>(&Ks[16 * J0 + li][16 * s4 + 4 * kq]);
-      const float4 a1 = *reinterpret_cast<const float4*>(&X1[16 * I1 + li][16 * s4 + 4 * kq]);
-      const float4 b1 = *reinterpret_cast<const float4*>(&Ks[16 * J1 + li][16 * s4 + 4 * kq]);
-      acc0 = mfma4(a0.x, b0.x, acc0);
-      acc1 = mfma4(a1.x, b1.x, acc1);
-      acc0 = mfma4(a0.y, b0.y, acc0);
-      acc1 = mfma4(a1.y, b1.y, acc1);
-      acc0 = mfma4(a0.z, b0.z, acc0);
-      acc1 = mfma4(a1.z, b1.z, acc1);
-      acc0 = mfma4(a0.w, b0.w, acc0);
-      acc1 = mfma4(a1.w, b1.w, acc1);
+    for (int st = 0; st < kDim / 32; ++st) {
+      gram_acc(q0, I0, J0, st, st + 1, h0, x0);
+      gram_acc(q1, I1, J1, st, st + 1, h1, x1);
     }
-    gram_store(I0, J0, q0, acc0);
-    gram_store(I1, J1, q1, acc1);
+    gram_store(I0, J0, q0, combine(h0, x0));
+    gram_store(I1, J1, q1, combine(h1, x1));
   }
   {
     // Jobs 16..19: wave w takes job 16 + w % 4 over half the key dims
@@ -300,18 +325,10 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
     int I, J;
     bool q;
     gram_tile(16 + (wave & 3), I, J, q);
-    const float(*X)[kRowPad] = q ? Qs : Ks;
-    const int s0 = 4 * (wave >> 2);
-    float4_v acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = s0; s4 < s0 + 4; ++s4) {
-      const float4 a = *reinterpret_cast<const float4*>(&X[16 * I + li][16 * s4 + 4 * kq]);
-      const float4 b = *reinterpret_cast<const float4*>(&Ks[16 * J + li][16 * s4 + 4 * kq]);
-      acc = mfma4(a.x, b.x, acc);
-      acc = mfma4(a.y, b.y, acc);
-      acc = mfma4(a.z, b.z, acc);
-      acc = mfma4(a.w, b.w, acc);
-    }
+    const int s0 = 2 * (wave >> 2);
+    float4_v ah = {0.f, 0.f, 0.f, 0.f}, ax = ah;
+    gram_acc(q, I, J, s0, s0 + 2, ah, ax);
+    float4_v acc = combine(ah, ax);
     if (wave >= 4) {
       *reinterpret_cast<float4*>(&Red[wave & 3][lane][0]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     }
@@ -352,12 +369,20 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkParam
       for (int idx = tid - 256; idx < 32 * (kC / 4); idx += 256) {
         const int d = 32 * part + (idx >> 4);
         const int t4 = (idx & 15) * 4;
-        const float4 kv = make_float4(Ks[t4 + 0][d], Ks[t4 + 1][d], Ks[t4 + 2][d], Ks[t4 + 3][d]);
-        *reinterpret_cast<float4*>(&KsT[d][t4]) = kv;
+        half4_t kh, kl;
+        float kt[4];
         const float4 e = *reinterpret_cast<const float4*>(&Dec[t4]);
-        const float kt[4] = {e.x * kv.x, e.y * kv.y, e.z * kv.z, e.w * kv.w};
+        const float ev[4] = {e.x, e.y, e.z, e.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          kh[i] = Kh[t4 + i][d];
+          kl[i] = Kl[t4 + i][d];
+          kt[i] = ev[i] * (static_cast<float>(kh[i]) + kLoUnscale * static_cast<float>(kl[i]));
+        }
+        *reinterpret_cast<half4_t*>(&KTh[d][t4]) = kh;
+        *reinterpret_cast<half4_t*>(&KTl[d][t4]) = kl;
         half4_t hi, lo;
-split4_f16(kt, hi, lo);
+        split4_f16(kt, hi, lo);
         half_t* row = reinterpret_cast<half_t*>(blk + kOffKT) + d * (2 * kC);
         *reinterpret_cast<half4_t*>(row + t4) = hi;
         *reinterpret_cast<half4_t*>(row + kC + t4) = lo;
@@ -421,43 +446,40 @@ split4_f16(kt, hi, lo);
     blk[kOffGammaC] = expf(g_last);
   }
   // ---- U = T diag(beta) V, W = T diag(beta gamma) K (C x D): 2 x 32 output
-  // tiles, four per pass; the diagonal scales T's columns as the A operand is
-  // read (k = 16 s + 4 kq + c). ----
-  float fb[16], fbg[16];
-#pragma unroll
-  for (int s4 = 0; s4 < 4; ++s4) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int k = 16 * s4 + 4 * kq + c;
-      fb[4 * s4 + c] = Bs[k];
-      fbg[4 * s4 + c] = Bs[k] * Gam[k];
-    }
-  }
+  // tiles, four per pass (one token row block R, four dim column blocks), on
+  // split fp16 MFMA.  The A operand, T's rows 16 R + li with column k scaled by
+  // beta_k (or beta_k gamma_k), k = 32 s + 8 kq + e, is split once per pass;
+  // the B operands are the staged split V^T and K^T rows. ----
   for (int job0 = 4 * wave; job0 < 64; job0 += 4 * kPrepWaves) {
+    const bool is_w = job0 >= 32;
+    const int R = (job0 & 31) >> 3;
+    half8_t ah[kC / 32], al[kC / 32];
+#pragma unroll
+    for (int st = 0; st < kC / 32; ++st) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int k = 32 * st + 8 * kq + e;
+        const float f = is_w ? Bs[k] * Gam[k] : Bs[k];
+        half_t hi, lo;
+        split_f16(Ts[16 * R + li][k] * f, hi, lo);
+        ah[st][e] = hi;
+        al[st][e] = lo;
+      }
+    }
+    const half_t(*XTh)[kColH] = is_w ? KTh : VTh;
+    const half_t(*XTl)[kColH] = is_w ? KTl : VTl;
     float4_v acc[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      acc[u] = float4_v{0.f, 0.f, 0.f, 0.f};
-    }
+      const int Cb = (job0 + u) & 7;  // dim column block
+      float4_v h = {0.f, 0.f, 0.f, 0.f}, x = h;
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      const int k0 = 16 * s4 + 4 * kq;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int job = job0 + u;
-        const bool is_w = job >= 32;
-        const int tile = job & 31;
-        const int R = tile >> 3;   // token row block
-        const int Cb = tile & 7;   // dim column block
-        const float(*XT)[kCPad] = is_w ? KsT : VsT;
-        const float* f = is_w ? &fbg[4 * s4] : &fb[4 * s4];
-        const float4 a = *reinterpret_cast<const float4*>(&Ts[16 * R + li][k0]);
-        const float4 b = *reinterpret_cast<const float4*>(&XT[16 * Cb + li][k0]);
-        acc[u] = mfma4(a.x * f[0], b.x, acc[u]);
-        acc[u] = mfma4(a.y * f[1], b.y, acc[u]);
-        acc[u] = mfma4(a.z * f[2], b.z, acc[u]);
-        acc[u] = mfma4(a.w * f[3], b.w, acc[u]);
+      for (int st = 0; st < kC / 32; ++st) {
+        const int c = 32 * st + 8 * kq;
+        mfma_split(ah[st], al[st], *reinterpret_cast<const half8_t*>(&XTh[16 * Cb + li][c]),
+                   *reinterpret_cast<const half8_t*>(&XTl[16 * Cb + li][c]), h, x);
       }
+      acc[u] = combine(h, x);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
