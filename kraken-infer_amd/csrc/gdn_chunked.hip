@@ -98,10 +98,11 @@ __device__ __forceinline__ float4_v mfma4(float a, float b, float4_v c) {
 // x is held as hi = f16(x) and lo = f16((x - hi) 2^11), so x = hi + 2^-11 lo to
 // about 2^-21 relative; a product sums hi hi + 2^-11 (hi lo + lo hi) in fp32
 // (the dropped lo lo term is below 2^-20 of the product).  Below the smallest
-// normal f16 (2^-14) hi is zero and the whole value goes into the scaled lo:
-// an f16 denormal hi can be flushed on its way through the matrix core, which
-// would drop up to 6e-5 of the value (measured: 3.5e-4 errors after the
-// norm-gated epilogue); a flushed denormal lo costs at most 2^-25.  W and
+// normal f16 (2^-14) hi is zero and the whole value goes into the scaled lo, at
+// f16 precision (at most 2^-25 absolute): an f16 denormal hi can be flushed on
+// its way through the matrix core, which would drop up to 6e-5 of the value
+// (measured: 3.5e-4 errors after the norm-gated epilogue).  tests/
+// test_split_f16.py checks these bounds with every f16 denormal flushed.  W and
 // Ktil^T rows are stored by the prep kernel in this form: a row of n values is
 // n hi halves then n lo halves, the same bytes as the fp32 row.
 constexpr float kLoScale = 2048.0f;        // 2^11
