@@ -319,3 +319,62 @@ def test_add_silu_mul_and_batched_rms_norm_closed_forms():
     xr = x.reshape(3, 1024).astype(np.float64)
     ref = xr / np.sqrt((xr ** 2).mean(1, keepdims=True) + 1e-6) * w
     np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+
+
+# ------------------------------------------------- gate and KV append ----
+
+def test_sigmoid_gate_mul_equals_mul_of_sigmoid_and_closed_forms():
+    """The fused output gate (qwen35_runtime.cpp:3347-3355: sigmoid_f32_in_place on G,
+    then mul_f32_in_place into o) equals o * sigmoid(G) built from the smoke-pinned
+    sigmoid and mul ops, up to the one f32 rounding of sigmoid(G) those two round
+    separately; G = 0 halves o, large G keeps o, very negative G zeroes it, and
+    negating G must change the result (sigmoid(-g) = 1 - sigmoid(g))."""
+    rng = np.random.default_rng(21)
+    o = (3 * rng.standard_normal(4096)).astype(np.float32)
+    g = (2 * rng.standard_normal(4096)).astype(np.float32)
+    got = oracle.sigmoid_gate_mul(o, g)
+    chained = oracle.mul(o, oracle.sigmoid(g))
+    np.testing.assert_allclose(got, chained, rtol=2.5e-7, atol=0)
+    want = o.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))
+    np.testing.assert_allclose(got, want, rtol=1.2e-7, atol=0)
+    flipped = oracle.sigmoid_gate_mul(o, -g)
+    np.testing.assert_allclose(flipped, o.astype(np.float64) - want, rtol=2e-6, atol=2e-6)
+    big = np.abs(g) > 0.5
+    assert np.all(np.abs(flipped - got)[big] > 1e-3 * np.abs(o)[big])
+    edge_o = np.array([5.0, -3.0, 7.0, 2.0], np.float32)
+    edge_g = np.array([0.0, 0.0, 40.0, -120.0], np.float32)
+    np.testing.assert_array_equal(oracle.sigmoid_gate_mul(edge_o, edge_g),
+                                  np.array([2.5, -1.5, 7.0, 0.0], np.float32))
+    # The output buffer is the first operand: gate and output must not be swapped.
+    assert not np.allclose(oracle.sigmoid_gate_mul(g, o), got)
+
+
+def test_copy_f32_rows_to_f16_equals_rounded_row_copy_with_distinct_strides():
+    """The KV append (mps_backend.mm:2655-2666: cache[dst_off + r dst_stride + c] =
+    half(x[src_off + r src_stride + c])) equals the smoke-pinned f32 row copy followed by
+    the exhaustively pinned f32 -> f16 rounding, and an independent numpy scatter; four
+    distinct strides and offsets make any swap of source and destination geometry fail,
+    and bytes outside the copied rows keep their values."""
+    rng = np.random.default_rng(22)
+    rows, row_size = 5, 24
+    src_stride, src_off, dst_stride, dst_off = 37, 3, 29, 11
+    src = (4 * rng.standard_normal(src_off + rows * src_stride)).astype(np.float32)
+    # Long enough for both geometries, so the swapped call below stays in bounds.
+    dst_len = max(dst_off + rows * dst_stride, src_off + rows * src_stride) + 7
+    background = rng.integers(0, 2**16, dst_len, dtype=np.uint16)
+    got = oracle.copy_f32_rows_to_f16(src, background, rows, row_size, src_stride, src_off,
+                                      dst_stride, dst_off)
+    via_f32 = oracle.copy_f32_rows(src, np.zeros(dst_len, np.float32), rows, row_size,
+                                   src_stride, src_off, dst_stride, dst_off)
+    ref = background.copy()
+    idx_d = dst_off + np.arange(rows)[:, None] * dst_stride + np.arange(row_size)[None, :]
+    idx_s = src_off + np.arange(rows)[:, None] * src_stride + np.arange(row_size)[None, :]
+    ref[idx_d] = src[idx_s].astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(got, ref)
+    np.testing.assert_array_equal(got[idx_d], oracle.f32_to_f16_bits(via_f32[idx_d]))
+    untouched = np.ones(dst_len, bool)
+    untouched[idx_d.ravel()] = False
+    np.testing.assert_array_equal(got[untouched], background[untouched])
+    swapped = oracle.copy_f32_rows_to_f16(src, background, rows, row_size, dst_stride, dst_off,
+                                          src_stride, src_off)
+    assert not np.array_equal(swapped, got)
