@@ -461,13 +461,15 @@ __global__ __launch_bounds__((64 * RowShape<D, KV>::W)) void attention_decode_ke
 //    C4 block, whose GDN state then stays cached.
 //  * S^T = K Q^T on v_mfma_f32_16x16x32_f16.  A = the tile's 16 key rows (k =
 //    head dims, 16-byte LDS fragments), B = the G query heads as columns.  The
-//    query, pre-scaled into the log2 domain, is split into f16 hi + lo (lo =
-//    q - hi, rounded again), so K (exact in f16) times hi + lo reproduces the
-//    f32 dot product to about 2^-22 relative.
+//    query, pre-scaled into the log2 domain, is held in the split fp16 form of
+//    device_common.hpp (split_f16: hi, and lo scaled by 2^11, both normal f16
+//    where it matters), with the hi and lo products in separate accumulators,
+//    so K (exact in f16) times the query reproduces the f32 dot product to
+//    about 2^-21 relative even where the matrix core flushes f16 denormals.
 //  * The S^T accumulator (lane l: head l % 16, keys 4 (l / 16) + r) is already
 //    the A operand of O += P V on v_mfma_f32_16x16x16_f16 (k = keys), with P
-//    split into f16 hi + lo the same way.  V^T fragments come from LDS through
-//    the transposing read ds_read_b64_tr_b16.
+//    split the same way into a hi and a lo output accumulator.  V^T fragments
+//    come from LDS through the transposing read ds_read_b64_tr_b16.
 //  * Online softmax per head with the vector kernel's wave-uniform lazy
 //    rescale; wave partials merge through LDS and splits in the same second
 //    pass, in the same partial format.
@@ -552,10 +554,10 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
       const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float x = v[j] * qscale;
-        const half_t hi = static_cast<half_t>(x);
+        half_t hi, lo;
+        split_f16(v[j] * qscale, hi, lo);
         qhi[s][j] = hi;
-        qlo[s][j] = static_cast<half_t>(x - static_cast<float>(hi));
+        qlo[s][j] = lo;
       }
     }
   }
@@ -583,10 +585,13 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
     m[g] = -INFINITY;
   }
   float lpart = 0.0f;  // this lane's share of head r16's denominator
-  float4v_t o[16];     // O tile n: lane l holds dim 16 n + l % 16 of heads 4 (l / 16) + r
+  // O tile n: lane l holds dim 16 n + l % 16 of heads 4 (l / 16) + r; o from
+  // the hi probabilities, olo from the lo ones (scaled by 2^11).
+  float4v_t o[16], olo[16];
 #pragma unroll
   for (int n = 0; n < 16; ++n) {
     o[n] = float4v_t{0.f, 0.f, 0.f, 0.f};
+    olo[n] = float4v_t{0.f, 0.f, 0.f, 0.f};
   }
 
   const uint32_t ntiles = (count + kMTile - 1) / kMTile;
@@ -599,14 +604,20 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
     const half_t* ks = &s_kv[wave][st][0][0];
     const half_t* vs = &s_kv[wave][st][1][0];
 
-    // S^T = K Q^T (keys x heads).
-    float4v_t sacc = {0.f, 0.f, 0.f, 0.f};
+    // S^T = K Q^T (keys x heads): the hi and the lo chain, then combined.
+    float4v_t shi = {0.f, 0.f, 0.f, 0.f};
+    float4v_t slo = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const half8_t kf = *reinterpret_cast<const half8_t*>(
         ks + r16 * kMD + 8 * ((4 * s + kq) ^ (r16 & 7)));
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qhi[s], sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qlo[s], sacc, 0, 0, 0);
+      shi = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qhi[s], shi, 0, 0, 0);
+      slo = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qlo[s], slo, 0, 0, 0);
+    }
+    float4v_t sacc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sacc[r] = fmaf(slo[r], kLoUnscale, shi[r]);
     }
 
     // Softmax: lane holds keys 16 t + 4 kq + r of head r16.
@@ -633,6 +644,7 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
 #pragma unroll
         for (int n = 0; n < 16; ++n) {
           o[n][g] *= corr;  // head g is row g: register g of lanes 0..15
+          olo[n][g] *= corr;
         }
         corr_lane = r16 == g ? corr : corr_lane;
       }
@@ -644,9 +656,10 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
     for (int r = 0; r < 4; ++r) {
       const float pr = valid[r] ? fast_exp2(sc[r] - m_lane) : 0.0f;
       lpart += pr;
-      const half_t h = static_cast<half_t>(pr);
+      half_t h, l;
+      split_f16(pr, h, l);
       phi[r] = h;
-      plo[r] = static_cast<half_t>(pr - static_cast<float>(h));
+      plo[r] = l;
     }
 
     // O += P V: lane 4 e + q of group kq points at row 4 kq + e, columns
@@ -660,7 +673,7 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
     for (int n = 0; n < 16; ++n) {
       const half4_t vf = read_tr16(vrow_p + 8 * ((2 * n + (q >> 1)) ^ vswz));
       o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, vf, o[n], 0, 0, 0);
-      o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, vf, o[n], 0, 0, 0);
+      olo[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, vf, olo[n], 0, 0, 0);
     }
 
     // Refill this stage with tile t + 8 once its LDS reads have returned.
@@ -690,7 +703,7 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
     for (int n = 0; n < 16; ++n) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        s_o[wave][g * kMD + 16 * n + lane] = o[n][g];
+        s_o[wave][g * kMD + 16 * n + lane] = fmaf(olo[n][g], kLoUnscale, o[n][g]);
       }
     }
   }

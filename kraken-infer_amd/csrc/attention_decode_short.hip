@@ -23,9 +23,11 @@ namespace {
 // straight into the MFMA A-fragment registers (lane (key r16, kq) loads dims
 // 32 s + 8 kq .. + 7 of step s) and its V tile into registers that are then
 // written to the wave's LDS region for the transposing V^T reads; the query
-// is loaded after them.  The math is the MFMA kernel's (hi + lo query and
+// is loaded after them.  The math is the MFMA kernel's (split fp16 query and
 // probabilities, lazy rescale, same partial format); a wave with more than one
-// tile loads its next tile while it computes the current one.
+// tile loads its next tile while it computes the current one.  The query
+// fragments stay in LDS and are read per tile, which leaves the registers for
+// the second (lo) output accumulator.
 // ---------------------------------------------------------------------------
 constexpr int kSWaves = 4;
 
@@ -107,8 +109,9 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // Query fragments (B operand of S^T) as f16 hi + lo (lo = x - hi, rounded
-  // again), so that K (exact in f16) times hi + lo reproduces the f32 product.
+  // Query fragments (B operand of S^T) in the split fp16 form (split_f16:
+  // hi, and lo scaled by 2^11), so that K (exact in f16) times hi plus 2^-11
+  // times K lo reproduces the f32 product to about 2^-21 relative.
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const float v[8] = {qraw[i][0].x, qraw[i][0].y, qraw[i][0].z, qraw[i][0].w,
@@ -116,21 +119,15 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
     half8_t hi8, lo8;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float x = v[j] * qscale;
-      const half_t hi = static_cast<half_t>(x);
+      half_t hi, lo;
+      split_f16(v[j] * qscale, hi, lo);
       hi8[j] = hi;
-      lo8[j] = static_cast<half_t>(x - static_cast<float>(hi));
+      lo8[j] = lo;
     }
     s_q[2 * wave + i][0][lane] = hi8;
     s_q[2 * wave + i][1][lane] = lo8;
   }
   __syncthreads();
-  half8_t qhi[8], qlo[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    qhi[s] = s_q[s][0][lane];
-    qlo[s] = s_q[s][1][lane];
-  }
 
   float m[G];  // wave-uniform reference max per head (log2 domain)
 #pragma unroll
@@ -138,10 +135,13 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
     m[g] = -INFINITY;
   }
   float lpart = 0.0f;  // this lane's share of head r16's denominator
-  float4v_t o[16];     // O tile n: lane l holds dim 16 n + l % 16 of heads 4 (l / 16) + r
+  // O tile n: lane l holds dim 16 n + l % 16 of heads 4 (l / 16) + r; o from
+  // the hi probabilities, olo from the lo ones (scaled by 2^11).
+  float4v_t o[16], olo[16];
 #pragma unroll
   for (int n = 0; n < 16; ++n) {
     o[n] = float4v_t{0.f, 0.f, 0.f, 0.f};
+    olo[n] = float4v_t{0.f, 0.f, 0.f, 0.f};
   }
   half_t* vs = &s_v[wave][0];
   for (; t < ntiles; t += kSWaves) {
@@ -161,15 +161,21 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
       load_v(t + kSWaves);
     }
 
-    // S^T = K Q^T (keys x heads).
-    float4v_t sacc = {0.f, 0.f, 0.f, 0.f};
+    // S^T = K Q^T (keys x heads): the hi and the lo chain, then combined.
+    float4v_t shi = {0.f, 0.f, 0.f, 0.f};
+    float4v_t slo = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[s], qhi[s], sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[s], qlo[s], sacc, 0, 0, 0);
+      shi = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[s], s_q[s][0][lane], shi, 0, 0, 0);
+      slo = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[s], s_q[s][1][lane], slo, 0, 0, 0);
     }
     if (more) {
       load_k(t + kSWaves);
+    }
+    float4v_t sacc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sacc[r] = fmaf(slo[r], kLoUnscale, shi[r]);
     }
 
     // Softmax: lane holds keys 16 t + 4 kq + r of head r16.
@@ -197,6 +203,7 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
 #pragma unroll
           for (int n = 0; n < 16; ++n) {
             o[n][g] *= corr;  // head g is row g: register g of lanes 0..15
+            olo[n][g] *= corr;
           }
           corr_lane = r16 == g ? corr : corr_lane;
         }
@@ -210,9 +217,10 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
     for (int r = 0; r < 4; ++r) {
       const float pr = valid[r] ? fast_exp2(sc[r] - m_lane) : 0.0f;
       lpart += pr;
-      const half_t h = static_cast<half_t>(pr);
+      half_t h, l;
+      split_f16(pr, h, l);
       phi[r] = h;
-      plo[r] = static_cast<half_t>(pr - static_cast<float>(h));
+      plo[r] = l;
     }
 
     // O += P V: lane 4 e + q of group kq points at row 4 kq + e, columns
@@ -226,7 +234,7 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
     for (int n = 0; n < 16; ++n) {
       const half4_t vf = read_tr16(vrow_p + 8 * ((2 * n + (q >> 1)) ^ vswz));
       o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, vf, o[n], 0, 0, 0);
-      o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, vf, o[n], 0, 0, 0);
+      olo[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, vf, olo[n], 0, 0, 0);
     }
   }
 
@@ -249,7 +257,7 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
     for (int n = 0; n < 16; ++n) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        s_o[wave][g * kMD + 16 * n + lane] = o[n][g];
+        s_o[wave][g * kMD + 16 * n + lane] = fmaf(olo[n][g], kLoUnscale, o[n][g]);
       }
     }
   }

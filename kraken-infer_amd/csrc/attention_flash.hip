@@ -210,10 +210,11 @@ __device__ __forceinline__ void issue_copy_seq(const TileSource& src, const Copy
                  : "v"(voff), "s"(src.rsrc), "s"(next)
                  : "memory", "m0");
   } else {
+    // s_add_u32 also writes SCC.
     asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds\n\ts_add_u32 m0, m0, %2"
                  :
                  : "v"(voff), "s"(src.rsrc), "n"(kStep)
-                 : "memory", "m0");
+                 : "memory", "m0", "scc");
   }
 }
 

@@ -86,23 +86,23 @@ int ensure_workspace(kraken_hip_context* ctx, size_t bytes) {
   if (ctx->validation_only || bytes <= ctx->workspace_bytes) {
     return KRAKEN_OK;
   }
-  // Pending kernels may still read the old workspace.
-  hipError_t e = hipStreamSynchronize(ctx->stream);
-  if (e != hipSuccess) {
-    return internal("HIP workspace resize wait failed: " + hip_message(e));
+  // Round up to 1 MiB and at least double, so steady-state calls never
+  // reallocate and the retired workspaces stay smaller than the live one.
+  size_t rounded = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
+  if (ctx->workspace_bytes > 0 && rounded < 2 * ctx->workspace_bytes) {
+    rounded = 2 * ctx->workspace_bytes;
   }
-  if (ctx->workspace != nullptr) {
-    (void)hipFree(ctx->workspace);
-    ctx->workspace = nullptr;
-    ctx->workspace_bytes = 0;
-  }
-  // Round up to 1 MiB so steady-state calls never reallocate.
-  const size_t rounded = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
-  e = hipMalloc(&ctx->workspace, rounded);
+  void* fresh = nullptr;
+  const hipError_t e = hipMalloc(&fresh, rounded);
   if (e != hipSuccess) {
-    ctx->workspace = nullptr;
     return internal("HIP workspace allocation failed: " + hip_message(e));
   }
+  // Kernels already enqueued, and graphs captured earlier, may still use the
+  // old workspace: keep it until the context is destroyed.
+  if (ctx->workspace != nullptr) {
+    ctx->retired_workspaces.push_back(ctx->workspace);
+  }
+  ctx->workspace = fresh;
   ctx->workspace_bytes = rounded;
   return KRAKEN_OK;
 }
@@ -256,6 +256,9 @@ KRAKEN_API void kraken_hip_context_destroy(kraken_hip_context* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->workspace != nullptr) {
       (void)hipFree(ctx->workspace);
+    }
+    for (void* w : ctx->retired_workspaces) {
+      (void)hipFree(w);
     }
     if (ctx->own_stream != nullptr) {
       (void)hipStreamDestroy(ctx->own_stream);

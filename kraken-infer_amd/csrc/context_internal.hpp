@@ -9,6 +9,7 @@
 #include <cstdint>
 #include <limits>
 #include <string>
+#include <vector>
 
 #include "kraken_hip.h"
 
@@ -21,9 +22,13 @@ struct kraken_hip_context {
   bool graph_active = false;
   // Device workspace owned by the context (split-K partials, chunk operands,
   // staging).  Grown on demand outside of any kernel; the reference likewise owns only its flash-tail
-  // scratch (mps_backend.mm:4402-4407).
+  // scratch (mps_backend.mm:4402-4407).  A workspace that is outgrown is kept,
+  // not freed, until the context is destroyed: a HIP graph captured earlier may
+  // hold its address and replay into it.  Growth at least doubles, so the kept
+  // ones add up to less than the current one.
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
+  std::vector<void*> retired_workspaces;
   // This device's copy of the static scratch array used by the allocation-free
   // entry point (device address, resolved at context creation).
   void* no_alloc_scratch = nullptr;
@@ -58,8 +63,10 @@ int begin_launch(kraken_hip_context* ctx);
 // (finish_command_buffer, mps_backend.mm:4416-4428).
 int finish_launch(kraken_hip_context* ctx, const char* error_prefix);
 
-// Ensures ctx->workspace holds at least `bytes`; waits for pending work before
-// reallocating.  Returns KRAKEN_OK or an error status.
+// Ensures ctx->workspace holds at least `bytes`.  A larger workspace is a new
+// allocation; the old one stays valid (and allocated) until the context is
+// destroyed, so work already enqueued or captured into a graph keeps a valid
+// address and nothing waits.  Returns KRAKEN_OK or an error status.
 int ensure_workspace(kraken_hip_context* ctx, size_t bytes);
 
 // Size of the static per-device scratch array of the allocation-free entry
@@ -293,11 +300,15 @@ hipError_t launch_kquant_dequantize_rows(int format, const void* weight, size_t 
                                          const int32_t* row_ids, size_t fixed_row,
                                          size_t tokens, size_t cols, float* output,
                                          hipStream_t stream);
-// argmax (probability_out null) or argmax with probability over `size` values.
+// argmax (probability_out null) or argmax with probability over `size` values:
+// the first index of the maximum, NaN never wins.  With nothing above -inf the
+// token is `size` (every value NaN) or the first -inf index, or 0 under
+// `kquant_rule` (the K-quant top-1/argmax kernels' reduction, which starts from
+// index 0).
 size_t argmax_workspace_bytes(size_t size);
 hipError_t launch_argmax(const float* values, size_t size, int32_t* token_out,
                          float* probability_out, void* workspace, size_t workspace_bytes,
-                         hipStream_t stream);
+                         hipStream_t stream, bool kquant_rule = false);
 // GEMV of one token into workspace logits, then argmax (and probability).
 size_t kquant_argmax_workspace_bytes(size_t rows);
 // input = RMSNorm(input) * norm_weight when norm_weight is given (eps as for

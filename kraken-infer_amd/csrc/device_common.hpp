@@ -129,6 +129,27 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Split fp32 operands for fp16 MFMA.  A value x is held as hi = f16(x) and
+// lo = f16((x - hi) 2^11), so x = hi + 2^-11 lo to about 2^-21 relative; hi
+// products and lo products go to separate fp32 accumulators and the lo sum is
+// scaled by 2^-11 at the end.  Below the smallest normal f16 (2^-14) hi is zero
+// and the whole value goes into the scaled lo, at f16 precision (at most 2^-25
+// absolute).  The 2^11 scale keeps lo a normal f16: the matrix core can flush
+// f16 denormal operands, and an unscaled lo = f16(x - hi) is denormal for every
+// |x| < 2^-3 (and an f16 denormal hi lost that way dropped up to 6e-5 of a
+// value: 3.5e-4 errors after the GDN norm-gated epilogue).  Valid for |x| below
+// the f16 range (65504).  tests/test_split_f16.py and
+// tests/test_decode_split_emulation.py check these bounds with every f16
+// denormal flushed.
+constexpr float kLoScale = 2048.0f;        // 2^11
+constexpr float kLoUnscale = 1.0f / 2048.0f;
+constexpr float kF16MinNormal = 6.103515625e-05f;  // 2^-14
+
+__device__ __forceinline__ void split_f16(float x, half_t& hi, half_t& lo) {
+  hi = static_cast<half_t>(__builtin_fabsf(x) < kF16MinNormal ? 0.0f : x);
+  lo = static_cast<half_t>((x - static_cast<float>(hi)) * kLoScale);
+}
+
 // Raw (unswizzled, stride 0) buffer resource over `bytes` bytes from `base`;
 // word 3 = 0x00020000 is the gfx9-family data format for raw dword access.
 // A load whose offset is at or past `bytes` returns zeros without a memory

@@ -94,26 +94,12 @@ __device__ __forceinline__ float4_v mfma4(float a, float b, float4_v c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Split fp32 products on fp16 MFMA (the scan's two per-chunk products).  A value
-// x is held as hi = f16(x) and lo = f16((x - hi) 2^11), so x = hi + 2^-11 lo to
-// about 2^-21 relative; a product sums hi hi + 2^-11 (hi lo + lo hi) in fp32
-// (the dropped lo lo term is below 2^-20 of the product).  Below the smallest
-// normal f16 (2^-14) hi is zero and the whole value goes into the scaled lo, at
-// f16 precision (at most 2^-25 absolute): an f16 denormal hi can be flushed on
-// its way through the matrix core, which would drop up to 6e-5 of the value
-// (measured: 3.5e-4 errors after the norm-gated epilogue).  tests/
-// test_split_f16.py checks these bounds with every f16 denormal flushed.  W and
-// Ktil^T rows are stored by the prep kernel in this form: a row of n values is
-// n hi halves then n lo halves, the same bytes as the fp32 row.
-constexpr float kLoScale = 2048.0f;        // 2^11
-constexpr float kLoUnscale = 1.0f / 2048.0f;
-constexpr float kF16MinNormal = 6.103515625e-05f;  // 2^-14
-
-__device__ __forceinline__ void split_f16(float x, half_t& hi, half_t& lo) {
-  hi = static_cast<half_t>(fabsf(x) < kF16MinNormal ? 0.0f : x);
-  lo = static_cast<half_t>((x - static_cast<float>(hi)) * kLoScale);
-}
-
+// The scan's two per-chunk products run on fp16 MFMA in the split form of
+// device_common.hpp (split_f16: x = hi + 2^-11 lo, about 2^-21 relative; a
+// product sums hi hi + 2^-11 (hi lo + lo hi) in fp32, the dropped lo lo term is
+// below 2^-20 of the product).  W and Ktil^T rows are stored by the prep kernel
+// in this form: a row of n values is n hi halves then n lo halves, the same bytes
+// as the fp32 row.
 __device__ __forceinline__ void split4_f16(const float x[4], half4_t& hi, half4_t& lo) {
 #pragma unroll
   for (int c = 0; c < 4; ++c) {

@@ -1285,9 +1285,14 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* values
 }
 
 // Phase 2 (or the whole job when cands == nullptr): merges candidates.
+// `max_above_neg_inf`: the K-quant top-1/argmax rule (mps_backend.mm:692-750,
+// 1652-1690: the reduction starts from index 0 at -inf), where the token is 0
+// unless some value exceeds -inf; otherwise the generic argmax_f32_i32 rule (the
+// first index of the maximum, `size` when every value is NaN).
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float* values, uint64_t size,
                                                            const ArgCand* cands, uint32_t count,
-                                                           bool with_sum, int32_t* token_out,
+                                                           bool with_sum, bool max_above_neg_inf,
+                                                           int32_t* token_out,
                                                            float* probability_out) {
   __shared__ float s_v[256];
   __shared__ uint32_t s_i[256];
@@ -1296,7 +1301,7 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* values, 
   if (cands == nullptr) {
     const ArgCand r = block_candidate(values, 0, size, (uint32_t)size, with_sum);
     if (tid == 0) {
-      token_out[0] = (int32_t)r.index;
+      token_out[0] = max_above_neg_inf && !(r.value > -INFINITY) ? 0 : (int32_t)r.index;
       if (probability_out != nullptr) {
         probability_out[0] = r.sum > 0.0f ? 1.0f / r.sum : 0.0f;
       }
@@ -1338,7 +1343,7 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* values, 
     }
   }
   if (tid == 0) {
-    token_out[0] = (int32_t)gidx;
+    token_out[0] = max_above_neg_inf && !(gmax > -INFINITY) ? 0 : (int32_t)gidx;
     if (probability_out != nullptr) {
       probability_out[0] = s_s[0] > 0.0f ? 1.0f / s_s[0] : 0.0f;
     }
@@ -1633,11 +1638,11 @@ size_t argmax_workspace_bytes(size_t size) {
 
 hipError_t launch_argmax(const float* values, size_t size, int32_t* token_out,
                          float* probability_out, void* workspace, size_t workspace_bytes,
-                         hipStream_t stream) {
+                         hipStream_t stream, bool kquant_rule) {
   const bool with_sum = probability_out != nullptr;
   if (size <= kArgmaxSingleMax) {
-    argmax_final_kernel<<<1, 256, 0, stream>>>(values, size, nullptr, 0, with_sum, token_out,
-                                               probability_out);
+    argmax_final_kernel<<<1, 256, 0, stream>>>(values, size, nullptr, 0, with_sum, kquant_rule,
+                                               token_out, probability_out);
     return hipGetLastError();
   }
   const size_t groups = (size + kArgmaxSpan - 1) / kArgmaxSpan;
@@ -1652,7 +1657,7 @@ hipError_t launch_argmax(const float* values, size_t size, int32_t* token_out,
     return e;
   }
   argmax_final_kernel<<<1, 256, 0, stream>>>(values, size, cands, (uint32_t)groups, with_sum,
-                                             token_out, probability_out);
+                                             kquant_rule, token_out, probability_out);
   return hipGetLastError();
 }
 
@@ -1718,7 +1723,8 @@ hipError_t launch_kquant_argmax(int format, const void* weight, size_t rows, siz
   }
   void* rest = static_cast<char*>(workspace) + align256(rows * sizeof(float));
   return launch_argmax(logits, rows, token_out, probability_out, rest,
-                       workspace_bytes - align256(rows * sizeof(float)), stream);
+                       workspace_bytes - align256(rows * sizeof(float)), stream,
+                       /*kquant_rule=*/true);
 }
 
 }  // namespace kraken

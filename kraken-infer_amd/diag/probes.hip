@@ -108,6 +108,50 @@ void diag_mfma_f16_kernel(uint32_t iterations, float* sink) {
   sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+
+// What the f16 matrix cores do with an f16 denormal operand: one wave runs
+// v_mfma_f32_16x16x32_f16 and v_mfma_f32_16x16x16_f16 with a single nonzero
+// element x at (row 0, k 0) of A (B all ones), then at (k 0, col 0) of B (A all
+// ones), for x in {2^-15, 2^-24 (denormals), 2^-14 (smallest normal)}, and
+// writes C[0][0] (lane 0, register 0 in both output layouts), which is x if the
+// operand survives and 0 if it is flushed.  sink[4 v + 2 i + o]: value v,
+// instruction i (0: 16x16x32, 1: 16x16x16), operand o (0: A, 1: B).
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+constexpr int kDenormalCases = 12;
+
+__global__ __launch_bounds__(64) void diag_mfma_denormal_kernel(float* sink) {
+  const int lane = threadIdx.x;
+  const float values[3] = {0x1p-15f, 0x1p-24f, 0x1p-14f};
+#pragma unroll
+  for (int v = 0; v < 3; ++v) {
+    const half_t x = static_cast<half_t>(values[v]);
+    half8_t one8, pick8;
+    half4_t one4, pick4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      one8[j] = 1;
+      pick8[j] = (lane == 0 && j == 0) ? x : half_t(0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      one4[j] = 1;
+      pick4[j] = (lane == 0 && j == 0) ? x : half_t(0);
+    }
+    const float4_t zero = {0.f, 0.f, 0.f, 0.f};
+    const float4_t a32 = __builtin_amdgcn_mfma_f32_16x16x32_f16(pick8, one8, zero, 0, 0, 0);
+    const float4_t b32 = __builtin_amdgcn_mfma_f32_16x16x32_f16(one8, pick8, zero, 0, 0, 0);
+    const float4_t a16 = __builtin_amdgcn_mfma_f32_16x16x16f16(pick4, one4, zero, 0, 0, 0);
+    const float4_t b16 = __builtin_amdgcn_mfma_f32_16x16x16f16(one4, pick4, zero, 0, 0, 0);
+    if (lane == 0) {
+      sink[4 * v + 0] = a32[0];
+      sink[4 * v + 1] = b32[0];
+      sink[4 * v + 2] = a16[0];
+      sink[4 * v + 3] = b16[0];
+    }
+  }
+}
+
 }  // namespace
 }  // namespace kraken_diag
 
@@ -163,6 +207,22 @@ KRAKEN_API int kraken_hip_diag_mfma_f16(kraken_hip_context* ctx, uint32_t workgr
   diag_mfma_f16_kernel<<<workgroups, kMfmaThreads, 0, stream>>>(iterations,
                                                                static_cast<float*>(sink.data));
   return launched("HIP MFMA loop launch failed: ");
+}
+
+KRAKEN_API int kraken_hip_diag_mfma_f16_denormals(kraken_hip_context* ctx, kraken_buffer sink) {
+  if (ctx == nullptr) {
+    return fail(KRAKEN_UNAVAILABLE, "HIP context is not initialized");
+  }
+  int s = check_f32(sink, kDenormalCases, "MFMA denormal probe sink");
+  if (s != KRAKEN_OK) {
+    return s;
+  }
+  hipStream_t stream;
+  if ((s = stream_of(ctx, &stream)) != KRAKEN_OK) {
+    return s;
+  }
+  diag_mfma_denormal_kernel<<<1, 64, 0, stream>>>(static_cast<float*>(sink.data));
+  return launched("HIP MFMA denormal probe launch failed: ");
 }
 
 }  // extern "C"

@@ -128,6 +128,7 @@ SIGNATURES = {
 DIAG_SIGNATURES = {
     "kraken_hip_diag_stream_read": [_B, _sz, _B],
     "kraken_hip_diag_mfma_f16": [ctypes.c_uint32, ctypes.c_uint32, _B],
+    "kraken_hip_diag_mfma_f16_denormals": [_B],
 }
 DIAG_LIB_PATH = os.path.join(os.path.dirname(LIB_PATH), "libkraken_hip_diag.so")
 

@@ -399,6 +399,9 @@ def test_diag_probe_argument_checks(vctx):
     assert code == kh.INVALID_ARGUMENT
     code, _ = status(vctx, "diag_mfma_f16", 256, 0, sink)
     assert code == kh.INVALID_ARGUMENT
+    assert status(vctx, "diag_mfma_f16_denormals", fake(48)) == (kh.UNAVAILABLE, ACCEPTED)
+    code, _ = status(vctx, "diag_mfma_f16_denormals", fake(44))  # holds 11 of the 12 results
+    assert code == kh.INVALID_ARGUMENT
 
 
 class _Region(ctypes.Structure):

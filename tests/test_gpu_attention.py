@@ -57,6 +57,66 @@ def test_decode_c1_shape(hip_ctx, kv_len):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("kernel", ["short", "mfma"])
+@pytest.mark.parametrize("q_scale,atol", [(1.0, 4e-6), (8.0, 2e-5)])
+def test_decode_keeps_f32_query_precision(hip_ctx, monkeypatch, kernel, q_scale, atol):
+    """C1 at L=4096: the MFMA decode kernels hold the f32 query (and the f32
+    probabilities) in the split fp16 form with lo scaled by 2^11, so their result
+    stays within `atol` of the oracle's f32-query attention (mps_backend.mm:
+    2979-2983 multiplies an f32 query).  The same attention on an f16-rounded
+    query misses by more than twice `atol`, so this tolerance tells the two apart
+    where the default 2e-3 / 1e-3 does not."""
+    heads, kv_heads, d, kv_len = 8, 2, 256, 4096
+    cap = kv_len + 1
+    print(f"decode f32 query {kernel} q_scale={q_scale}", flush=True)
+    q, kc, vc = make_case(1, 1, kv_len, cap, heads, kv_heads, d)
+    q = (q * q_scale).astype(np.float32)
+    ref = oracle.attention_batched(q, kc, vc, 0, kv_len, 1, cap, heads, kv_heads, d)
+    ref_f16q = oracle.attention_batched(q, kc, vc, 0, kv_len, 1, cap, heads, kv_heads, d,
+                                        round_query_f16=True)
+    assert np.abs(ref_f16q - ref).max() > 2 * atol
+    monkeypatch.setenv("KRAKEN_DECODE_KERNEL", kernel)
+    got = run_hip(hip_ctx, q, kc, vc, 0, kv_len, 1, cap, heads, kv_heads, d)
+    err = np.abs(got - ref).max()
+    print(f"  max abs error {err:.3g} (f16 query: {np.abs(ref_f16q - ref).max():.3g})", flush=True)
+    assert err <= atol
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kernel", ["short", "mfma", "vector"])
+@pytest.mark.parametrize("keys_per_split", [None, 16384])
+def test_decode_sink_over_flat_tail(hip_ctx, monkeypatch, kernel, keys_per_split):
+    """L=16384: key 0 scores 10 nats above 16383 equal keys (zero K rows), for
+    every query head.  In the wave that holds the sink every other weight is
+    e^-10 = 4.5e-5, below the smallest normal f16, and the tail carries 43% of
+    the softmax mass; a kernel that lost those weights to a denormal flush would
+    miss by far more than the 2e-5 allowed here.  One split of all keys puts a
+    quarter of the tail in the sink's wave."""
+    heads, kv_heads, d, kv_len = 8, 2, 256, 16383
+    cap = kv_len + 1
+    print(f"decode sink {kernel} keys_per_split={keys_per_split}", flush=True)
+    rng = np.random.default_rng(7)
+    qg = rng.standard_normal((kv_heads, d)).astype(np.float32)
+    q = np.repeat(qg, heads // kv_heads, axis=0).reshape(-1)  # the heads of a group agree
+    k = np.zeros((cap, kv_heads, d), np.float32)
+    for h in range(kv_heads):
+        k[0, h] = qg[h] * (10.0 * np.sqrt(d) / float(qg[h].astype(np.float64) @ qg[h]))
+    kc = f16_bits(k.reshape(-1))
+    vc = f16_bits(rng.standard_normal(cap * kv_heads * d))
+    ref = oracle.attention_batched(q, kc, vc, 0, kv_len, 1, cap, heads, kv_heads, d)
+    v0 = np.repeat(vc.view(np.float16).astype(np.float32).reshape(cap, kv_heads, d)[0],
+                   heads // kv_heads, axis=0).reshape(-1)
+    assert np.abs(ref - v0).max() > 0.1  # the tail matters
+    monkeypatch.setenv("KRAKEN_DECODE_KERNEL", kernel)
+    if keys_per_split is not None:
+        monkeypatch.setenv("KRAKEN_DECODE_KEYS_PER_SPLIT", str(keys_per_split))
+    got = run_hip(hip_ctx, q, kc, vc, 0, kv_len, 1, cap, heads, kv_heads, d)
+    err = np.abs(got - ref).max()
+    print(f"  max abs error {err:.3g}", flush=True)
+    assert err <= 2e-5
+
+
+@pytest.mark.gpu
 def test_decode_gated_matches_separate_gate(hip_ctx):
     heads, kv_heads, d, kv_len = 8, 2, 256, 4096
     q, kc, vc = make_case(1, 1, kv_len, kv_len + 1, heads, kv_heads, d)
@@ -190,6 +250,80 @@ def test_decode_graph_replays(hip_ctx):
                     close(outs[i].cpu().numpy(), ref, msg=f"replay {replay} step {i}")
                     outs[i].zero_()
             del graph
+    finally:
+        hip_ctx.commit_graph()
+        hip_ctx.set_stream(None)
+
+
+@pytest.mark.gpu
+def test_workspace_growth_between_replays(hip_ctx):
+    """A graph captured while the context's workspace was small keeps replaying
+    correctly after an eager call has grown the workspace: the outgrown
+    workspace stays allocated (the graph holds its address) until the context
+    is destroyed.  Decode step at L=4096 captured; a C2-sized flash prefill
+    (T=1024 after 3072 cached tokens, 34 MB of split partials) grows the
+    workspace between replays, and the context is used again afterwards."""
+    torch = pytest.importorskip("torch")
+    heads, kv_heads, d, n = 8, 2, 256, 4096
+    cap = 4096 + 1024
+    rng = np.random.default_rng(31)
+    kc = f16_bits(rng.standard_normal(cap * kv_heads * d))
+    vc = f16_bits(rng.standard_normal(cap * kv_heads * d))
+    gate = rng.standard_normal(heads * d).astype(np.float32)
+    dev = "cuda"
+    kt = torch.from_numpy(kc.view(np.float16)).to(dev)
+    vt = torch.from_numpy(vc.view(np.float16)).to(dev)
+    gt = torch.from_numpy(gate).to(dev)
+    qt = torch.zeros(heads * d, device=dev, dtype=torch.float32)
+    out = torch.zeros(heads * d, device=dev, dtype=torch.float32)
+    stream = torch.cuda.Stream()
+    hip_ctx.set_stream(stream.cuda_stream)
+    hip_ctx.begin_graph()
+
+    def step():
+        hip_ctx.attention_f32_batched_f16_kv_gated(qt, kt, vt, gt, 0, n, 1, cap, heads,
+                                                   kv_heads, d, out)
+
+    def check(q, what):
+        ref = oracle.sigmoid_gate_mul(
+            oracle.attention_batched(q, kc, vc, 0, n, 1, cap, heads, kv_heads, d), gate)
+        close(out.cpu().numpy(), ref, msg=what)
+        out.zero_()
+
+    try:
+        with torch.cuda.stream(stream):
+            step()
+            stream.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                step()
+            for replay in range(3):
+                q = rng.standard_normal(heads * d).astype(np.float32)
+                qt.copy_(torch.from_numpy(q).to(dev))
+                torch.cuda.synchronize()
+                graph.replay()
+                stream.synchronize()
+                check(q, f"replay {replay}")
+                if replay == 0:
+                    # Eager prefill chunk that needs a larger workspace.
+                    t, start = 1024, 3072
+                    qp = rng.standard_normal(t * heads * d).astype(np.float32)
+                    qpt = torch.from_numpy(qp).to(dev)
+                    op = torch.zeros(t * heads * d, device=dev, dtype=torch.float32)
+                    hip_ctx.attention_f32_batched_f16_kv(qpt, kt, vt, 0, start, t, cap, heads,
+                                                         kv_heads, d, op)
+                    stream.synchronize()
+                    sample = [0, 511, 1023]
+                    got = op.cpu().numpy().reshape(t, heads * d)[sample]
+                    for i, tok in enumerate(sample):
+                        qs = qp.reshape(t, heads * d)[tok]
+                        ref = oracle.attention_batched(qs, kc, vc, 0, start + tok, 1, cap, heads,
+                                                       kv_heads, d, round_query_f16=True)
+                        close(got[i], ref, msg=f"prefill token {tok}")
+            del graph
+            step()  # eager again, on the grown workspace
+            stream.synchronize()
+            check(q, "eager after growth")
     finally:
         hip_ctx.commit_graph()
         hip_ctx.set_stream(None)

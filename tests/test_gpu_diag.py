@@ -27,3 +27,25 @@ def test_mfma_probe_runs(hip_ctx):
     sink = hip_ctx.buffer(byte_size=8 * 256 * 4)
     hip_ctx.diag_mfma_f16(8, 10, sink)
     assert np.isfinite(sink.download(8 * 256)).all()
+
+
+@pytest.mark.gpu
+def test_mfma_f16_denormal_operands_recorded(hip_ctx, record_property):
+    """Records whether v_mfma_f32_16x16x32_f16 and v_mfma_f32_16x16x16_f16 keep an
+    f16 denormal operand (2^-15, 2^-24) in A and in B; the smallest normal (2^-14)
+    must pass through exactly.  The decode and GDN kernels keep their split lo
+    halves normal (2^11 scale) so that their results do not depend on the answer."""
+    sink = hip_ctx.buffer(byte_size=12 * 4)
+    hip_ctx.diag_mfma_f16_denormals(sink)
+    got = sink.download(12).reshape(3, 2, 2)
+    values = (2.0 ** -15, 2.0 ** -24, 2.0 ** -14)
+    for v, x in enumerate(values):
+        for i, ins in enumerate(("16x16x32_f16", "16x16x16f16")):
+            for o, operand in enumerate("AB"):
+                r = float(got[v, i, o])
+                what = "kept" if r == x else "flushed" if r == 0.0 else f"{r!r}"
+                print(f"v_mfma_f32_{ins} operand {operand} x=2^{int(np.log2(x))}: {what}",
+                      flush=True)
+                record_property(f"{ins}_{operand}_2^{int(np.log2(x))}", what)
+                assert r == x or r == 0.0
+    assert np.all(got[2] == values[2])

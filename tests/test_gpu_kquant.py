@@ -232,6 +232,25 @@ def test_top1_random_logits(ops, fmt, rows, cols):
     assert abs(p - o_p) <= slack * o_p, (p, o_p)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("rows", [1000, 32768])
+def test_top1_without_a_finite_logit_returns_row_zero(ops, fmt, rows):
+    """When no logit exceeds -inf (an all-NaN input; or -inf in the input against
+    all-positive weights, which gives -inf or NaN logits) the K-quant top-1 and
+    argmax return token 0 with probability 0, as the reference's reduction does:
+    it starts from index 0 at -inf and only a larger value or a smaller index at
+    an equal value replaces it (mps_backend.mm:692-750, 1652-1690).  One pass
+    (1000 rows) and two passes (32768 rows)."""
+    cols = 256
+    print(f"top1 no finite logit {fmt} rows={rows}", flush=True)
+    w = np.concatenate([planted_logit_weight(fmt, 1, cols, 0, seed=rows)] * rows)
+    for name, x in (("nan", np.full(cols, np.nan, np.float32)),
+                    ("-inf", np.concatenate([[-np.inf], np.zeros(cols - 1)]).astype(np.float32))):
+        assert ops.kquant_top1(fmt, w, rows, cols, x) == 0, name
+        assert ops.kquant_top1(fmt, w, rows, cols, x, probability=True) == (0, 0.0), name
+
+
 # ------------------------------------------------------------------ argmax ----
 
 ARGMAX_SIZES = [3, 255, 16384, 16385, 248320]

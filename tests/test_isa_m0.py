@@ -34,17 +34,61 @@ ALLOWED = [
 ]
 
 
-@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
-@pytest.mark.parametrize("source", sorted(EXTRA))
-def test_m0_has_no_other_user(tmp_path, source):
+# SCC readers, and the scalar ALU instructions that write SCC (a conservative
+# superset: every SOP1/SOP2/SOPC opcode family that sets it).
+SCC_USE = re.compile(r"^(s_cbranch_scc[01]|s_cselect_b(32|64)|s_addc_u32|s_subb_u32|"
+                     r"s_cmov_b(32|64)|s_cmovk_i32)\b")
+SCC_DEF = re.compile(r"^s_(add|sub|addc|subb|min|max|and|or|xor|andn[12]|orn[12]|nand|nor|xnor|"
+                     r"lshl|lshr|ashr|bfe|bfm|not|cmp|bitcmp|abs|absdiff|lshl\d_add|bcnt|ff[01]|"
+                     r"flbit|quadmask|wqm|[a-z0-9]+_saveexec)[a-z0-9_]*\b")
+
+
+def instructions(path):
+    for line in path.read_text().splitlines():
+        text = line.split(";")[0].strip()
+        if text and not text.startswith(".") and not text.endswith(":"):
+            yield text
+
+
+def compile_isa(tmp_path, source):
     out = tmp_path / "k.s"
     subprocess.run([HIPCC, *FLAGS, *EXTRA[source], os.path.join(CSRC, source), "-o", str(out)],
                    check=True, capture_output=True)
+    return out
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+@pytest.mark.parametrize("source", sorted(EXTRA))
+def test_m0_write_never_directly_precedes_an_lds_dma_load(tmp_path, source):
+    """An M0 write needs one wait state before an LDS-DMA load reads it: the
+    copies put an s_nop or other work in between, which the compiled code keeps."""
+    prev = ""
+    for text in instructions(compile_isa(tmp_path, source)):
+        if " lds" in text and text.startswith(("buffer_", "global_")):
+            assert not re.match(r"^s_(mov|add)_[bu]32 m0\b", prev), f"{source}: {prev} ; {text}"
+        prev = text
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+@pytest.mark.parametrize("source", sorted(EXTRA))
+def test_no_scc_value_lives_across_the_m0_add(tmp_path, source):
+    """The copy asm's s_add_u32 on M0 writes SCC (declared clobbered): no SCC
+    reader may take its value from that add, i.e. the last SCC writer before
+    every reader is some other instruction."""
+    last_def = ""
+    for text in instructions(compile_isa(tmp_path, source)):
+        if SCC_USE.match(text):
+            assert not re.match(r"^s_add_u32 m0, m0\b", last_def), f"{source}: {last_def} ; {text}"
+        if SCC_DEF.match(text):
+            last_def = text
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+@pytest.mark.parametrize("source", sorted(EXTRA))
+def test_m0_has_no_other_user(tmp_path, source):
+    out = compile_isa(tmp_path, source)
     users = 0
-    for line in out.read_text().splitlines():
-        text = line.split(";")[0].strip()
-        if not text or text.startswith("."):
-            continue
+    for text in instructions(out):
         assert not IMPLICIT.match(text), f"{source}: implicit M0 user: {text}"
         if " lds" in text and text.startswith(("buffer_", "global_")):
             assert any(p.match(text) for p in ALLOWED), f"{source}: other LDS-DMA load: {text}"

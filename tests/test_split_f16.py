@@ -67,3 +67,16 @@ def test_hi_below_min_normal_goes_to_lo():
     bad = np.abs(split_dot(a, b, flush_hi=False) - exact) / scale
     assert good.max() < 2.0 ** -10
     assert bad.max() > 0.1
+
+
+def test_range_is_the_f16_range():
+    """The split is defined for |x| up to the largest f16 (65504), which the
+    kernels' operands stay within (L2-normalised q/k, bounded GDN state, and the
+    log2-scaled decode query for |q| below about 7e5 at head_dim 256); from
+    65520 on, hi rounds to inf and the products are not finite.  This pins that
+    documented edge rather than a fallback."""
+    x = np.array([65504.0, -65504.0, 65519.0, 65520.0, -1e5], np.float32)
+    with np.errstate(over="ignore"):
+        hi, lo = split(x)
+    assert np.all(np.isfinite(hi[:3])) and np.all(hi[:3] + lo[:3] / 2048.0 == x[:3])
+    assert np.all(np.isinf(hi[3:]))
