@@ -293,11 +293,13 @@ __global__ __launch_bounds__((64 * RowShape<D, KV>::W)) void attention_decode_ke
 
   float m[G];  // wave-uniform reference max (log2 domain)
   float l[G];
+  float lc[G];  // Kahan compensation of l (see kahan_add)
   float o[G][EL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
     l[g] = 0.0f;
+    lc[g] = 0.0f;
 #pragma unroll
     for (int e = 0; e < EL; ++e) {
       o[g][e] = 0.0f;
@@ -354,13 +356,14 @@ __global__ __launch_bounds__((64 * RowShape<D, KV>::W)) void attention_decode_ke
         const float corr = fast_exp2(m[g] - bmax);  // 0 on the first valid round
         m[g] = bmax;
         l[g] *= corr;
+        lc[g] *= corr;
 #pragma unroll
         for (int e = 0; e < EL; ++e) {
           o[g][e] *= corr;
         }
       }
       const float pr = valid ? fast_exp2(sc[g] - m[g]) : 0.0f;
-      l[g] += pr;
+      kahan_add(l[g], lc[g], pr);
 #pragma unroll
       for (int e = 0; e < EL; ++e) {
         o[g][e] = fmaf(pr, vf[e], o[g][e]);
@@ -387,7 +390,7 @@ __global__ __launch_bounds__((64 * RowShape<D, KV>::W)) void attention_decode_ke
   // accumulators add lane-wise.
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float lw = slots_sum<R>(l[g]);
+    const float lw = slots_sum<R>(l[g] - lc[g]);
 #pragma unroll
     for (int e = 0; e < EL; ++e) {
       o[g][e] = slots_sum<R>(o[g][e]);
@@ -584,7 +587,11 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
   }
-  float lpart = 0.0f;  // this lane's share of head r16's denominator
+  // This lane's share of head r16's denominator, summed with Kahan's
+  // compensation (lcomp): a long split adds thousands of small weights to a sum
+  // near 1, where plain fp32 addition would drop a systematic part of each.
+  float lpart = 0.0f;
+  float lcomp = 0.0f;
   // O tile n: lane l holds dim 16 n + l % 16 of heads 4 (l / 16) + r; o from
   // the hi probabilities, olo from the lo ones (scaled by 2^11).
   float4v_t o[16], olo[16];
@@ -651,11 +658,12 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
       m_lane = r16 == g ? m[g] : m_lane;
     }
     lpart *= corr_lane;
+    lcomp *= corr_lane;
     half4_t phi, plo;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float pr = valid[r] ? fast_exp2(sc[r] - m_lane) : 0.0f;
-      lpart += pr;
+      kahan_add(lpart, lcomp, pr);
       half_t h, l;
       split_f16(pr, h, l);
       phi[r] = h;
@@ -685,7 +693,7 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Wave partial: head r16's denominator over the four lane groups.
-  float lw = lpart;
+  float lw = lpart - lcomp;
   lw += __shfl_xor(lw, 16, 64);
   lw += __shfl_xor(lw, 32, 64);
   __syncthreads();  // every wave is done with its stages

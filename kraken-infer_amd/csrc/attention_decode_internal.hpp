@@ -65,6 +65,17 @@ __device__ __forceinline__ void write_final(const DecodeParams& p, uint32_t toke
 // result is exact either way: o and l always share the same reference.
 constexpr float kRescaleSlack = 8.0f;
 
+// Kahan-compensated running sum: sum + (-comp) carries what plain fp32
+// addition would drop when many small terms join a larger sum (the softmax
+// denominator of a long split).  The library is built without fast-math, so
+// the compiler keeps the compensation's operation order.
+__device__ __forceinline__ void kahan_add(float& sum, float& comp, float x) {
+  const float y = x - comp;
+  const float t = sum + y;
+  comp = (t - sum) - y;
+  sum = t;
+}
+
 constexpr int kMD = 256;
 constexpr int kMTile = 16;                        // keys per tile
 constexpr int kMTileHalfs = kMTile * kMD;         // 8 KB per K or V tile

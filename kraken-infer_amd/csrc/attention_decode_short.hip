@@ -134,7 +134,11 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
   }
-  float lpart = 0.0f;  // this lane's share of head r16's denominator
+  // This lane's share of head r16's denominator, summed with Kahan's
+  // compensation (lcomp): a long split adds thousands of small weights to a sum
+  // near 1, where plain fp32 addition would drop a systematic part of each.
+  float lpart = 0.0f;
+  float lcomp = 0.0f;
   // O tile n: lane l holds dim 16 n + l % 16 of heads 4 (l / 16) + r; o from
   // the hi probabilities, olo from the lo ones (scaled by 2^11).
   float4v_t o[16], olo[16];
@@ -212,11 +216,12 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
       m_lane = r16 == g ? m[g] : m_lane;
     }
     lpart *= corr_lane;
+    lcomp *= corr_lane;
     half4_t phi, plo;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float pr = valid[r] ? fast_exp2(sc[r] - m_lane) : 0.0f;
-      lpart += pr;
+      kahan_add(lpart, lcomp, pr);
       half_t h, l;
       split_f16(pr, h, l);
       phi[r] = h;
@@ -239,7 +244,7 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
   }
 
   // Wave partial: head r16's denominator over the four lane groups.
-  float lw = lpart;
+  float lw = lpart - lcomp;
   lw += __shfl_xor(lw, 16, 64);
   lw += __shfl_xor(lw, 32, 64);
   __syncthreads();  // every wave is done with its V region
