@@ -528,19 +528,26 @@ def decode_traffic():
     return None
 
 
+MODEL_BENCH = os.path.join(ROOT, "kraken-infer_amd", "build", "qwen35_model_bench")
+
+
+def model_bench(*args, timeout=300):
+    """Runs kraken-infer_amd/build/qwen35_model_bench (whole-model timings on synthetic
+    Qwen3.5-0.8B weights) in its own process and returns its key=value fields."""
+    if not os.path.exists(MODEL_BENCH):
+        raise RuntimeError(f"{MODEL_BENCH} is not built (run __graft_entry__.build())")
+    out = subprocess.run([MODEL_BENCH, *map(str, args)], capture_output=True, text=True,
+                         timeout=timeout)
+    if out.returncode != 0:
+        raise RuntimeError(f"qwen35_model_bench {args[0]} failed: " + out.stdout + out.stderr)
+    line = [l for l in out.stdout.splitlines() if l.startswith(str(args[0]) + " ")][-1]
+    return {k: float(v) for k, v in (kv.split("=") for kv in line.split()[1:])}
+
+
 def bench_prefix():
     """Prompt prefix cache store (include/kraken/qwen35_prefix_store.hpp): commit and
-    restore of 1024-token blocks of the Qwen3.5-0.8B cache, timed by
-    tests/cpp/prefix_cache_check.cpp in its own process."""
-    import subprocess
-
-    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "kraken-infer_amd", "build",
-                       "prefix_cache_check")
-    if not os.path.exists(exe):
-        raise RuntimeError(f"{exe} is not built (run __graft_entry__.build())")
-    out = subprocess.run([exe, "store-bench"], capture_output=True, text=True, timeout=120,
-                         check=True).stdout.split()
-    vals = {k: float(v) for k, v in zip(out[0::2], out[1::2])}
+    restore of 1024-token blocks of the Qwen3.5-0.8B cache."""
+    vals = model_bench("prefix-store", timeout=120)
     vals["note"] = ("8 blocks of 1024 tokens: K/V rows of 6 layers, R/S of 18 layers, last "
                     "hidden row; restore = all 8 blocks' K/V rows + R/S once; payloads live in one "
                     "HBM arena allocated at the first (untimed) commit")
@@ -602,21 +609,25 @@ def bench_kquant(torch, ctx, run, gen, shapes=(0, 1, 2, 3)):
 def bench_decode_loop(warmup=8, steps=64):
     """Greedy decode of the whole 0.8B model (synthetic K-quant weights: every
     layer's norms, projections, attention core and FFN, the tied Q6_K LM head
-    with device argmax), one graph batch and one host wait per token, through
-    the C++ driver (include/kraken/qwen35_decode.hpp) as
-    `qwen35_driver_check bench-decode`.  weight_GB_s counts every weight byte
+    with device argmax), one graph batch and one host wait per token
+    (include/kraken/qwen35_decode.hpp).  weight_GB_s counts every weight byte
     read once per token."""
-    exe = os.path.join(ROOT, "kraken-infer_amd", "build", "qwen35_driver_check")
-    out = subprocess.run([exe, "bench-decode", str(warmup), str(steps)], capture_output=True,
-                         text=True, timeout=300)
-    if out.returncode != 0:
-        raise RuntimeError("bench-decode failed: " + out.stdout + out.stderr)
-    line = [l for l in out.stdout.splitlines() if l.startswith("bench-decode ")][-1]
-    fields = dict(kv.split("=") for kv in line.split()[1:])
-    res = {k: float(v) for k, v in fields.items()}
+    res = model_bench("decode", warmup, steps)
     res["frac_hbm_peak"] = res["weight_GB_s"] / HBM_PEAK_GBS
     res["note"] = ("synthetic Qwen3.5-0.8B shapes: Q6_K token_embd/LM head 248320x1024, per layer "
                    "Q4_K/Q5_K/Q6_K projections and FFN 3584; tokens fed back greedily")
+    return res
+
+
+def bench_prefill_model(prompt=4096, chunk=1024):
+    """Chunked prefill of the whole 0.8B model (include/kraken/qwen35_prefill.hpp):
+    every layer over each 1024-token chunk (RMSNorm, K-quant GEMM projections,
+    flash256 or the chunked gated delta rule, output projection, SwiGLU FFN), one
+    graph batch and one host wait per chunk, then the greedy LM head of the last
+    row; host clock over the whole prompt."""
+    res = model_bench("prefill", prompt, chunk)
+    res["note"] = ("synthetic Qwen3.5-0.8B weights; prompt of %d tokens in chunks of %d, "
+                   "timed on the second pass" % (prompt, chunk))
     return res
 
 
@@ -682,9 +693,10 @@ def main():
     ap.add_argument("--kv-len", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline only, no details")
-    ap.add_argument("--sections", default="decode,prefill,gdn,c4,kquant,peaks,prefix,loop",
+    ap.add_argument("--sections",
+                    default="decode,prefill,gdn,c4,kquant,peaks,prefix,loop,model_prefill",
                     help="comma-separated detail sections to run after the headline "
-                         "(decode, prefill, gdn, c4, kquant, peaks, prefix, loop)")
+                         "(decode, prefill, gdn, c4, kquant, peaks, prefix, loop, model_prefill)")
     ap.add_argument("--prefill-prefixes", default="0,3072,7168",
                     help="comma-separated KV prefixes of the prefill section")
     ap.add_argument("--kquant-shapes", default="0,1,2,3",
@@ -770,6 +782,9 @@ def main():
     if "loop" in sections:
         details["decode_loop"] = bench_decode_loop()
         progress(f"decode loop: {details['decode_loop']['ms_per_token']:.3f} ms/token")
+    if "model_prefill" in sections:
+        details["model_prefill"] = bench_prefill_model()
+        progress(f"model prefill: {details['model_prefill']['tok_s']:.0f} tok/s")
     if "prefix" in sections:
         details["prefix_store"] = bench_prefix()
         progress(f"prefix store: restore {details['prefix_store']['restore_GB_s']:.0f} GB/s")

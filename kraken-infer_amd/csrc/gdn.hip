@@ -171,6 +171,7 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnParams p) {
 // outside the pool).
 template <bool kPrepare, int RPL>
 __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnParams p) {
+  static_assert(RPL == 1 || RPL == 2 || RPL == 4, "rows per group");
   constexpr uint32_t D = 128;
   constexpr int CPL = 4;
   const int lane = threadIdx.x & 63;
@@ -203,8 +204,23 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnParams p) {
                                                     col0);
   const float4 q = *reinterpret_cast<const float4*>(
     p.query + ((size_t)t * p.key_heads + kh) * D + col0);
-  const float4 v4 =
-    *reinterpret_cast<const float4*>(p.value + ((size_t)t * p.value_heads + h) * D + row0);
+  // The group's RPL values of v (rows row0 .. row0 + RPL - 1).
+  float v[RPL];
+  {
+    const float* vrow = p.value + ((size_t)t * p.value_heads + h) * D + row0;
+    if constexpr (RPL == 4) {
+      const float4 v4 = *reinterpret_cast<const float4*>(vrow);
+      v[0] = v4.x;
+      v[1] = v4.y;
+      v[2] = v4.z;
+      v[3] = v4.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < RPL; ++j) {
+        v[j] = vrow[j];
+      }
+    }
+  }
   const size_t gi = (size_t)t * p.value_heads + h;
   float g = p.gate[gi];
   float b = p.beta[gi];
@@ -213,7 +229,6 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnParams p) {
     b = 1.0f / (1.0f + expf(-b));
   }
   const float decay = expf(g);
-  const float v[4] = {v4.x, v4.y, v4.z, v4.w};
 
   float sk[RPL];
 #pragma unroll
@@ -246,10 +261,18 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnParams p) {
   for (int j = 0; j < RPL; ++j) {
     *reinterpret_cast<float4*>(shead + (size_t)(row0 + j) * D + col0) = s[j];
   }
-  // Lanes 0..RPL-1 of the group write the RPL outputs (one 16-byte store).
+  // Lane 0 of the group writes the RPL outputs (one 16-byte store for 4).
   if ((lane & 31) == 0) {
-    *reinterpret_cast<float4*>(p.output + ((size_t)t * p.value_heads + h) * D + row0) =
-      make_float4(y[0] * p.scale, y[1] * p.scale, y[2] * p.scale, y[3] * p.scale);
+    float* yrow = p.output + ((size_t)t * p.value_heads + h) * D + row0;
+    if constexpr (RPL == 4) {
+      *reinterpret_cast<float4*>(yrow) =
+        make_float4(y[0] * p.scale, y[1] * p.scale, y[2] * p.scale, y[3] * p.scale);
+    } else {
+#pragma unroll
+      for (int j = 0; j < RPL; ++j) {
+        yrow[j] = y[j] * p.scale;
+      }
+    }
   }
 }
 
@@ -423,10 +446,19 @@ hipError_t launch_gdn_cpl(const GdnParams& p, hipStream_t stream) {
     return hipGetLastError();
   }
   if (one_token && p.head_dim == 128 && aligned) {
-    constexpr int kRpl = 4;
-    const dim3 grid(128 / (8 * kRpl), p.value_heads,
-                    p.seq_state_offsets != nullptr ? p.tokens : 1u);
-    gdn_decode_kernel<kPrepare, kRpl><<<grid, 256, 0, stream>>>(p);
+    // Rows per 32-lane group: 4 when there are many states to stream (ragged
+    // decode), 1 for few, so that a single sequence's 16 heads still spread
+    // over 256 workgroups (8 rows each) instead of 64.
+    const uint32_t sequences = p.seq_state_offsets != nullptr ? p.tokens : 1u;
+    if ((uint64_t)sequences * p.value_heads * 4u >= 1024u) {
+      constexpr int kRpl = 4;
+      const dim3 grid(128 / (8 * kRpl), p.value_heads, sequences);
+      gdn_decode_kernel<kPrepare, kRpl><<<grid, 256, 0, stream>>>(p);
+    } else {
+      constexpr int kRpl = 1;
+      const dim3 grid(128 / (8 * kRpl), p.value_heads, sequences);
+      gdn_decode_kernel<kPrepare, kRpl><<<grid, 256, 0, stream>>>(p);
+    }
     return hipGetLastError();
   }
   const dim3 grid((p.head_dim + kGdnRowsPerBlock - 1) / kGdnRowsPerBlock, p.value_heads,
@@ -766,6 +798,24 @@ __global__ __launch_bounds__(256) void gdn_layer_ragged_kernel(GdnLayerArgs p) {
   for (int j = 0; j < RPL; ++j) {
     s[j] = *reinterpret_cast<const float4*>(shead + (size_t)(row0 + j) * D + col0);
   }
+  // The epilogue's and the gate's inputs are loaded now too, so that no stage
+  // after the conv waits on a global round trip.
+  const size_t gi = (size_t)seq * H + h;
+  float g = p.gate[gi];
+  float b = p.beta[gi];
+  float dtb = 0.0f, sa = 0.0f;
+  if (kPrepare) {
+    dtb = p.dt_bias[h];
+    sa = p.ssm_a[h];
+  }
+  float zz[2], nw[2];
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      zz[i] = p.z[gi * D + lane + 64 * i];
+      nw[i] = p.norm_weight[lane + 64 * i];
+    }
+  }
 
   if (wave < 3) {
     // Unit wave * H + h: the q, k or v channels of this head.
@@ -807,11 +857,8 @@ __global__ __launch_bounds__(256) void gdn_layer_ragged_kernel(GdnLayerArgs p) {
       dst[lane + 64 * i] = wave < 2 ? y[i] * inv : y[i];
     }
   }
-  const size_t gi = (size_t)seq * H + h;
-  float g = p.gate[gi];
-  float b = p.beta[gi];
   if (kPrepare) {
-    g = softplus_ref(g + p.dt_bias[h]) * p.ssm_a[h];
+    g = softplus_ref(g + dtb) * sa;
     b = 1.0f / (1.0f + expf(-b));
   }
   const float decay = expf(g);
@@ -861,26 +908,21 @@ __global__ __launch_bounds__(256) void gdn_layer_ragged_kernel(GdnLayerArgs p) {
 
   if (wave == 0) {
     // Norm-gated epilogue: y <- y * rsqrt(mean(y^2) + eps) * w * silu(z).
-    float v[4];
+    float v[2];
     float sum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t d = lane + 64u * i;
-      v[i] = d < D ? ys[d] : 0.0f;
+    for (int i = 0; i < 2; ++i) {
+      v[i] = ys[lane + 64 * i];
       sum = fmaf(v[i], v[i], sum);
     }
     sum = wave_sum(sum);
     const float nscale = 1.0f / sqrtf(sum / (float)D + p.eps);
     const size_t rowoff = gi * D;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t d = lane + 64u * i;
-      if (d < D) {
-        float r = v[i] * nscale * p.norm_weight[d];
-        const float zz = p.z[rowoff + d];
-        r *= zz * (1.0f / (1.0f + expf(-zz)));
-        p.output[rowoff + d] = r;
-      }
+    for (int i = 0; i < 2; ++i) {
+      float r = v[i] * nscale * nw[i];
+      r *= zz[i] * (1.0f / (1.0f + expf(-zz[i])));
+      p.output[rowoff + lane + 64 * i] = r;
     }
   }
 }

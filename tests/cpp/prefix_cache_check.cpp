@@ -5,9 +5,7 @@
 //                                   prints one result line per operation (the
 //                                   CPU oracle prints the same lines);
 //   prefix_cache_check store        commit / restore / evict round trip over a
-//                                   real device cache (needs a GPU);
-//   prefix_cache_check store-bench  timing of commit and restore of 1024-token
-//                                   blocks of the Qwen3.5-0.8B cache (GPU).
+//                                   real device cache (needs a GPU).
 #include <chrono>
 #include <cinttypes>
 #include <cstdio>
@@ -297,79 +295,6 @@ int run_store() {
   return 0;
 }
 
-int run_store_bench() {
-  auto ctx_r = HipContext::create();
-  if (!check(ctx_r.status(), "create")) {
-    return 1;
-  }
-  const HipContext& ctx = ctx_r.value();
-  constexpr std::size_t kBlock = 1024;
-  constexpr int kBlocks = 8;
-  q35::RuntimeOptions options;
-  auto plan_r = q35::build_execution_plan(q35::qwen35_0_8b_shape(), kBlock * kBlocks, options);
-  if (!check(plan_r.status(), "plan")) {
-    return 1;
-  }
-  const q35::ExecutionPlan& plan = plan_r.value();
-  auto cache_r = q35::allocate_device_cache(ctx, plan);
-  auto hidden_b = ctx.make_buffer(kBlock * plan.hidden_size * sizeof(float));
-  if (!check(cache_r.status(), "cache") || !check(hidden_b.status(), "hidden")) {
-    return 1;
-  }
-  q35::DeviceCache& dc = cache_r.value();
-  std::vector<std::int64_t> tokens(kBlock * kBlocks);
-  for (std::size_t i = 0; i < tokens.size(); ++i) {
-    tokens[i] = static_cast<std::int64_t>(i * 7919 % 151936);
-  }
-  q35::PrefixCacheStore store;
-  store.configure(q35::prefix_layout_from_plan(plan, kBlock),
-                  q35::PrefixCacheConfig{true, kBlock, kBlocks, 0});
-  float sink = 0;
-  auto sync = [&]() { return ctx.copy_from_buffer(hidden_b.value(), &sink, sizeof(sink)); };
-  using clock = std::chrono::steady_clock;
-  // The first commit allocates its payload; time the other blocks' commits.
-  auto first = store.commit_block(ctx, dc, plan, hidden_b.value(), tokens, 0, kBlock);
-  if (!check(first.status(), "commit") || !check(sync(), "sync")) {
-    return 1;
-  }
-  auto t0 = clock::now();
-  for (int i = 1; i < kBlocks; ++i) {
-    auto c = store.commit_block(ctx, dc, plan, hidden_b.value(), tokens, i * kBlock, kBlock);
-    if (!check(c.status(), "commit")) {
-      return 1;
-    }
-  }
-  if (!check(sync(), "sync")) {
-    return 1;
-  }
-  const double commit_us =
-    std::chrono::duration<double, std::micro>(clock::now() - t0).count() / (kBlocks - 1);
-  const auto hit = store.lookup(tokens);
-  constexpr int kRepeats = 20;
-  t0 = clock::now();
-  for (int i = 0; i < kRepeats; ++i) {
-    if (!check(store.restore(ctx, dc, plan, hit.block_hashes), "restore")) {
-      return 1;
-    }
-  }
-  if (!check(sync(), "sync")) {
-    return 1;
-  }
-  const double restore_us =
-    std::chrono::duration<double, std::micro>(clock::now() - t0).count() / kRepeats;
-  const double kv_block = 2.0 * plan.cache.full_attention_layers * kBlock * plan.cache.kv_dim *
-                          plan.cache.kv_cache_element_bytes;
-  const double recurrent =
-    double(plan.cache.recurrent_r_cache_bytes + plan.cache.recurrent_s_cache_bytes);
-  const double payload = kv_block + recurrent + plan.hidden_size * 4.0;
-  const double restored = kBlocks * kv_block + recurrent;
-  std::printf("payload_bytes %.0f hit_tokens %zu commit_us %.2f commit_GB_s %.1f restore_us %.2f "
-              "restore_bytes %.0f restore_GB_s %.1f\n",
-              payload, hit.hit_tokens, commit_us, payload / commit_us * 1e-3, restore_us,
-              restored, restored / restore_us * 1e-3);
-  return 0;
-}
-
 // The store outlives the request contexts that use it: a block committed
 // through one context, which is then destroyed with its cache, is restored
 // through a second context; reconfiguring then frees the arena (through the
@@ -494,12 +419,9 @@ int main(int argc, char** argv) {
   if (mode == "store") {
     return run_store();
   }
-  if (mode == "store-bench") {
-    return run_store_bench();
-  }
   if (mode == "lifetime") {
     return run_lifetime();
   }
-  std::printf("usage: prefix_cache_check index | store | store-bench | lifetime\n");
+  std::printf("usage: prefix_cache_check index | store | lifetime\n");
   return 2;
 }

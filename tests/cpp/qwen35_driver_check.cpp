@@ -23,6 +23,12 @@
 //       reference's separate ops instead of the fused GEMVs, and also the last
 //       step's LM-head input (normed.f32); with `trace`, every layer's output
 //       hidden state (hidden_trace.f32).
+//   qwen35_driver_check prefill <model.gguf> <outdir> <prompt_tokens> <chunk_tokens> <steps>
+//                               [trace] [reference]
+//       On a GPU.  The same model: chunked prefill of a deterministic prompt
+//       (include/kraken/qwen35_prefill.hpp), then greedy decode from the
+//       prompt's end; writes prompt.i32 and tokens.i32, and with `trace` the
+//       sampled hidden rows after every layer of every chunk and step.
 // Exits non-zero on the first failure.
 #include <algorithm>
 #include <array>
@@ -40,6 +46,7 @@
 #include "kraken/qwen35_bench.hpp"
 #include "kraken/qwen35_decode.hpp"
 #include "kraken/qwen35_layers.hpp"
+#include "kraken/qwen35_prefill.hpp"
 
 using kraken::hip::HipBuffer;
 using kraken::hip::HipContext;
@@ -477,63 +484,60 @@ class DeviceTensors {
   std::vector<std::unique_ptr<HipBuffer>> owned_;
 };
 
-int run_decode(const std::string& path, const std::string& out_dir, std::int32_t first_token,
-               std::size_t steps, bool trace, q35::OpOrder order) {
+// A Qwen3.5-0.8B-shaped GGUF on the device: the file, its mapping, the
+// uploaded tensors and the weights table of the plan.
+struct LoadedModel {
+  kraken::gguf::File file;
+  std::unique_ptr<kraken::gguf::MappedData> map;
+  std::unique_ptr<DeviceTensors> tensors;
+  q35::ModelWeights weights;
+};
+
+bool load_gguf_model(const HipContext& ctx, const std::string& path, const q35::ExecutionPlan& plan,
+                     LoadedModel& m) {
   auto file = kraken::gguf::read_file(path);
   if (!check(file.status(), "read GGUF")) {
-    return 1;
+    return false;
   }
-  auto map = kraken::gguf::MappedData::open(file.value());
+  m.file = std::move(file.value());
+  auto map = kraken::gguf::MappedData::open(m.file);
   if (!check(map.status(), "map GGUF")) {
-    return 1;
+    return false;
   }
+  m.map = std::make_unique<kraken::gguf::MappedData>(std::move(map.value()));
   const q35::ModelShape shape = q35::qwen35_0_8b_shape();
-  auto blocks = kraken::gguf::get_i64(file.value(), "qwen35.block_count");
-  auto width = kraken::gguf::get_i64(file.value(), "qwen35.embedding_length");
+  auto blocks = kraken::gguf::get_i64(m.file, "qwen35.block_count");
+  auto width = kraken::gguf::get_i64(m.file, "qwen35.embedding_length");
   if (!check(blocks.status(), "block_count") || !check(width.status(), "embedding_length") ||
       blocks.value() != shape.total_layer_count || width.value() != shape.hidden_size) {
     std::printf("FAIL GGUF is not Qwen3.5-0.8B shaped\n");
-    return 1;
+    return false;
   }
-  auto ctx_r = HipContext::create();
-  if (!check(ctx_r.status(), "create")) {
-    return 1;
-  }
-  const HipContext& ctx = ctx_r.value();
-  q35::RuntimeOptions options;
-  options.context_tokens = steps + 1;
-  auto plan = q35::build_execution_plan(shape, steps, options);
-  if (!check(plan.status(), "plan")) {
-    return 1;
-  }
-  auto cache = q35::allocate_device_cache(ctx, plan.value());
-  if (!check(cache.status(), "allocate_device_cache")) {
-    return 1;
-  }
-  DeviceTensors dt(ctx, file.value(), map.value());
-  q35::ModelWeights w;
+  m.tensors = std::make_unique<DeviceTensors>(ctx, m.file, *m.map);
+  DeviceTensors& dt = *m.tensors;
+  q35::ModelWeights& w = m.weights;
   if (!dt.get("token_embd.weight", w.token_embd) ||
       !dt.vec("output_norm.weight", w.output_norm)) {
-    return 1;
+    return false;
   }
   // output.weight absent: the LM head is tied to token_embd (qwen35.cpp:45-52
   // of llama.cpp, as the reference's loader does).
-  if (kraken::gguf::find_tensor(file.value(), "output.weight") != nullptr) {
+  if (kraken::gguf::find_tensor(m.file, "output.weight") != nullptr) {
     if (!dt.get("output.weight", w.output)) {
-      return 1;
+      return false;
     }
   } else {
     w.output = w.token_embd;
   }
-  w.layers.resize(plan.value().main_layers);
-  for (std::size_t i = 0; i < plan.value().main_layers; ++i) {
+  w.layers.resize(plan.main_layers);
+  for (std::size_t i = 0; i < plan.main_layers; ++i) {
     const std::string p = "blk." + std::to_string(i) + ".";
     q35::DecoderLayerWeights& l = w.layers[i];
     bool ok = dt.vec(p + "attn_norm.weight", l.attn_norm) &&
               dt.vec(p + "post_attention_norm.weight", l.post_attention_norm) &&
               dt.get(p + "ffn_gate.weight", l.ffn_gate) && dt.get(p + "ffn_up.weight", l.ffn_up) &&
               dt.get(p + "ffn_down.weight", l.ffn_down);
-    if (ok && plan.value().layer_kinds[i] == q35::LayerKind::linear_attention) {
+    if (ok && plan.layer_kinds[i] == q35::LayerKind::linear_attention) {
       ok = dt.get(p + "attn_qkv.weight", l.qkv) && dt.get(p + "attn_gate.weight", l.gate) &&
            dt.get(p + "ssm_beta.weight", l.beta) && dt.get(p + "ssm_alpha.weight", l.alpha) &&
            dt.get(p + "ssm_out.weight", l.ssm_out) &&
@@ -547,9 +551,34 @@ int run_decode(const std::string& path, const std::string& out_dir, std::int32_t
            dt.vec(p + "attn_k_norm.weight", l.full.k_norm);
     }
     if (!ok) {
-      return 1;
+      return false;
     }
   }
+  return true;
+}
+
+int run_decode(const std::string& path, const std::string& out_dir, std::int32_t first_token,
+               std::size_t steps, bool trace, q35::OpOrder order) {
+  auto ctx_r = HipContext::create();
+  if (!check(ctx_r.status(), "create")) {
+    return 1;
+  }
+  const HipContext& ctx = ctx_r.value();
+  q35::RuntimeOptions options;
+  options.context_tokens = steps + 1;
+  auto plan = q35::build_execution_plan(q35::qwen35_0_8b_shape(), steps, options);
+  if (!check(plan.status(), "plan")) {
+    return 1;
+  }
+  auto cache = q35::allocate_device_cache(ctx, plan.value());
+  if (!check(cache.status(), "allocate_device_cache")) {
+    return 1;
+  }
+  LoadedModel model;
+  if (!load_gguf_model(ctx, path, plan.value(), model)) {
+    return 1;
+  }
+  const q35::ModelWeights& w = model.weights;
   q35::DecodeScratch scratch;
   // With `trace`, every layer's output hidden state of every step is appended
   // to hidden_trace.f32 (steps x layers x hidden).
@@ -589,93 +618,24 @@ int run_decode(const std::string& path, const std::string& out_dir, std::int32_t
   return 0;
 }
 
-// Synthetic Qwen3.5-0.8B weights on the device for timing: random K-quant
-// blocks with f16 scales chosen so weights are a few hundredths (the decode
-// tests' recipe), f32 norms near 1.
-class SyntheticModel {
- public:
-  explicit SyntheticModel(const HipContext& ctx) : ctx_(ctx) {}
-  std::uint64_t bytes() const { return bytes_; }
-
-  bool quant(q35::TensorType type, std::size_t rows, std::size_t cols, q35::Tensor& out) {
-    const std::size_t nb = type == q35::TensorType::q4_k ? 144 : (type == q35::TensorType::q5_k ? 176 : 210);
-    const std::size_t blocks = rows * cols / 256;
-    std::vector<std::uint8_t> data(blocks * nb);
-    for (auto& b : data) {
-      b = (std::uint8_t)(next() >> 56);
-    }
-    const float d = type == q35::TensorType::q4_k ? 1.5e-4f : (type == q35::TensorType::q5_k ? 8e-5f : 4e-5f);
-    for (std::size_t i = 0; i < blocks; ++i) {
-      std::uint8_t* blk = data.data() + i * nb;
-      const std::uint16_t dh = half_bits(d * (0.5f + unit()));
-      if (type == q35::TensorType::q6_k) {
-        std::memcpy(blk + 208, &dh, 2);
-      } else {
-        const std::uint16_t mh = half_bits(1e-3f * unit());
-        std::memcpy(blk, &dh, 2);
-        std::memcpy(blk + 2, &mh, 2);
-      }
-    }
-    if (!upload(data, out.buffer)) {
-      return false;
-    }
-    out.type = type;
-    out.rows = rows;
-    out.cols = cols;
-    return true;
-  }
-  bool vec(std::size_t n, float base, float spread, const HipBuffer*& out) {
-    std::vector<float> v(n);
-    for (auto& x : v) {
-      x = base + spread * (2.0f * unit() - 1.0f);
-    }
-    return upload(v, out);
-  }
-
- private:
-  template <typename T>
-  bool upload(const std::vector<T>& host, const HipBuffer*& out) {
-    HipBuffer b;
-    if (!::upload(ctx_, host, b)) {
-      return false;
-    }
-    bytes_ += host.size() * sizeof(T);
-    owned_.push_back(std::make_unique<HipBuffer>(std::move(b)));
-    out = owned_.back().get();
-    return true;
-  }
-  std::uint64_t next() {  // xorshift64*
-    state_ ^= state_ >> 12;
-    state_ ^= state_ << 25;
-    state_ ^= state_ >> 27;
-    return state_ * 0x2545F4914F6CDD1DULL;
-  }
-  float unit() { return (float)(next() >> 40) / (float)(1 << 24); }
-  static std::uint16_t half_bits(float f) {  // small positive normal values only
-    std::uint32_t x;
-    std::memcpy(&x, &f, 4);
-    const int e = (int)((x >> 23) & 0xFF) - 127 + 15;
-    return (std::uint16_t)((e << 10) | ((x >> 13) & 0x3FF));
-  }
-
-  const HipContext& ctx_;
-  std::vector<std::unique_ptr<HipBuffer>> owned_;
-  std::uint64_t bytes_{0};
-  std::uint64_t state_{0x9E3779B97F4A7C15ULL};
-};
-
-// bench-decode <warmup> <steps> [reference]: greedy decode of `steps` tokens on
-// synthetic 0.8B weights after `warmup` tokens; one graph batch and one wait per
-// token; the fused op order unless `reference`.
-int run_bench_decode(std::size_t warmup, std::size_t steps, q35::OpOrder order) {
+// prefill <model.gguf> <outdir> <prompt_tokens> <chunk_tokens> <steps> [trace] [reference]:
+// chunked prefill of a deterministic prompt (token i = (7919 i + 11) mod vocab,
+// written to prompt.i32), then greedy decode; the generated tokens go to
+// tokens.i32 (the prefill's token first).  With `trace`, the hidden state after
+// every layer of every chunk is sampled at the chunk's rows 0, tokens / 2 and
+// tokens - 1 (prefill_trace.f32, [chunk][layer][3][hidden]) and after every
+// layer of every decode step (hidden_trace.f32, [step][layer][hidden]).
+int run_prefill(const std::string& path, const std::string& out_dir, std::size_t prompt_tokens,
+                std::size_t chunk_tokens, std::size_t steps, bool trace, q35::OpOrder order) {
   auto ctx_r = HipContext::create();
   if (!check(ctx_r.status(), "create")) {
     return 1;
   }
   const HipContext& ctx = ctx_r.value();
   q35::RuntimeOptions options;
-  options.context_tokens = warmup + steps + 1;
-  auto plan = q35::build_execution_plan(q35::qwen35_0_8b_shape(), warmup + steps, options);
+  options.prefill_chunk_tokens = chunk_tokens;
+  options.decode_tokens = steps;
+  auto plan = q35::build_execution_plan(q35::qwen35_0_8b_shape(), prompt_tokens, options);
   if (!check(plan.status(), "plan")) {
     return 1;
   }
@@ -683,52 +643,65 @@ int run_bench_decode(std::size_t warmup, std::size_t steps, q35::OpOrder order) 
   if (!check(cache.status(), "allocate_device_cache")) {
     return 1;
   }
-  using TT = q35::TensorType;
-  SyntheticModel sm(ctx);
-  q35::ModelWeights w;
-  const std::size_t h = 1024, ffn = 3584;
-  bool ok = sm.quant(TT::q6_k, 248320, h, w.token_embd) && sm.vec(h, 1.0f, 0.1f, w.output_norm);
-  w.output = w.token_embd;
-  w.layers.resize(plan.value().main_layers);
-  for (std::size_t i = 0; ok && i < w.layers.size(); ++i) {
-    q35::DecoderLayerWeights& l = w.layers[i];
-    ok = sm.vec(h, 1.0f, 0.1f, l.attn_norm) && sm.vec(h, 1.0f, 0.1f, l.post_attention_norm) &&
-         sm.quant(TT::q4_k, ffn, h, l.ffn_gate) && sm.quant(TT::q4_k, ffn, h, l.ffn_up) &&
-         sm.quant(TT::q6_k, h, ffn, l.ffn_down);
-    if (ok && plan.value().layer_kinds[i] == q35::LayerKind::linear_attention) {
-      ok = sm.quant(TT::q5_k, 6144, h, l.qkv) && sm.quant(TT::q4_k, 2048, h, l.gate) &&
-           sm.quant(TT::q4_k, 16, h, l.beta) && sm.quant(TT::q4_k, 16, h, l.alpha) &&
-           sm.quant(TT::q4_k, h, 2048, l.ssm_out) && sm.vec(6144 * 4, 0.0f, 0.5f, l.linear.conv1d) &&
-           sm.vec(16, 0.0f, 0.5f, l.linear.dt_bias) && sm.vec(16, -0.7f, 0.5f, l.linear.ssm_a) &&
-           sm.vec(128, 1.0f, 0.1f, l.linear.ssm_norm);
-    } else if (ok) {
-      ok = sm.quant(TT::q4_k, 4096, h, l.q) && sm.quant(TT::q4_k, 512, h, l.k) &&
-           sm.quant(TT::q6_k, 512, h, l.v) && sm.quant(TT::q4_k, h, 2048, l.output) &&
-           sm.vec(256, 1.0f, 0.1f, l.full.q_norm) && sm.vec(256, 1.0f, 0.1f, l.full.k_norm);
+  LoadedModel model;
+  if (!load_gguf_model(ctx, path, plan.value(), model)) {
+    return 1;
+  }
+  const q35::ModelWeights& w = model.weights;
+  const std::size_t h = plan.value().hidden_size;
+  std::vector<std::int32_t> prompt(prompt_tokens);
+  for (std::size_t i = 0; i < prompt_tokens; ++i) {
+    prompt[i] = (std::int32_t)((7919u * i + 11u) % w.token_embd.rows);
+  }
+  std::vector<float> prefill_rows;
+  const q35::ChunkLayerHook chunk_hook = [&](std::size_t, const HipBuffer& hidden,
+                                             std::size_t, std::size_t tokens) {
+    std::vector<float> all(tokens * h);
+    const Status st = ctx.copy_from_buffer(hidden, all.data(), all.size() * sizeof(float));
+    for (const std::size_t r : {std::size_t{0}, tokens / 2, tokens - 1}) {
+      prefill_rows.insert(prefill_rows.end(), all.begin() + r * h, all.begin() + (r + 1) * h);
     }
-  }
-  if (!ok) {
-    return 1;
-  }
-  q35::DecodeScratch scratch;
-  auto first =
-    q35::greedy_decode(ctx, plan.value(), cache.value(), w, scratch, 11, 0, warmup, nullptr, order);
-  if (!check(first.status(), "warmup decode")) {
-    return 1;
-  }
-  const std::int32_t next = warmup > 0 ? first.value().back() : 11;
+    return st;
+  };
+  std::vector<float> decode_rows;
+  const q35::LayerHook step_hook = [&](std::size_t, const HipBuffer& hidden) {
+    std::vector<float> row(h);
+    const Status st = ctx.copy_from_buffer(hidden, row.data(), row.size() * sizeof(float));
+    decode_rows.insert(decode_rows.end(), row.begin(), row.end());
+    return st;
+  };
+  q35::PrefillScratch ps;
+  q35::DecodeScratch ds;
   const auto t0 = std::chrono::steady_clock::now();
-  auto timed = q35::greedy_decode(ctx, plan.value(), cache.value(), w, scratch, next, warmup,
-                                  steps, nullptr, order);
-  const auto t1 = std::chrono::steady_clock::now();
-  if (!check(timed.status(), "timed decode")) {
+  auto first = q35::prefill_prompt(ctx, plan.value(), cache.value(), w, ps, prompt,
+                                   trace ? &chunk_hook : nullptr, order);
+  const double prefill_ms =
+    std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  if (!check(first.status(), "prefill_prompt")) {
     return 1;
   }
-  const double sec = std::chrono::duration<double>(t1 - t0).count();
-  std::printf("bench-decode tokens=%zu warmup=%zu ms_per_token=%.4f tok_s=%.1f weight_bytes=%llu "
-              "weight_GB_s=%.1f\n",
-              steps, warmup, 1e3 * sec / (double)steps, (double)steps / sec,
-              (unsigned long long)sm.bytes(), (double)sm.bytes() * (double)steps / sec / 1e9);
+  std::vector<std::int32_t> tokens{first.value()};
+  if (steps > 1) {
+    auto rest = q35::greedy_decode(ctx, plan.value(), cache.value(), w, ds, first.value(),
+                                   prompt_tokens, steps - 1, trace ? &step_hook : nullptr, order);
+    if (!check(rest.status(), "greedy_decode")) {
+      return 1;
+    }
+    tokens.insert(tokens.end(), rest.value().begin(), rest.value().end());
+  }
+  if (!write_file(out_dir + "/prompt.i32", prompt) ||
+      !write_file(out_dir + "/tokens.i32", tokens) ||
+      (trace && (!write_file(out_dir + "/prefill_trace.f32", prefill_rows) ||
+                 !write_file(out_dir + "/hidden_trace.f32", decode_rows)))) {
+    std::printf("FAIL write outputs\n");
+    return 1;
+  }
+  std::printf("prefill done: chunks=%zu prefill_ms=%.3f tokens:", plan.value().prefill.chunk_count,
+              prefill_ms);
+  for (const std::int32_t t : tokens) {
+    std::printf(" %d", t);
+  }
+  std::printf("\n");
   return 0;
 }
 
@@ -793,11 +766,6 @@ int main(int argc, char** argv) {
   if (mode == "plan") {
     return run_plan();
   }
-  if (mode == "bench-decode" && argc >= 4) {
-    return run_bench_decode((std::size_t)std::stoul(argv[2]), (std::size_t)std::stoul(argv[3]),
-                            argc > 4 && std::string(argv[4]) == "reference" ? q35::OpOrder::reference
-                                                                            : q35::OpOrder::fused);
-  }
   if (mode.rfind("bench-", 0) == 0) {
     return run_bench(mode, argc, argv);
   }
@@ -814,9 +782,21 @@ int main(int argc, char** argv) {
     return run_decode(argv[2], argv[3], (std::int32_t)std::stol(argv[4]),
                       (std::size_t)std::stoul(argv[5]), trace, order);
   }
+  if (mode == "prefill" && argc >= 7) {
+    bool trace = false;
+    q35::OpOrder order = q35::OpOrder::fused;
+    for (int i = 7; i < argc; ++i) {
+      trace = trace || std::string(argv[i]) == "trace";
+      order = std::string(argv[i]) == "reference" ? q35::OpOrder::reference : order;
+    }
+    return run_prefill(argv[2], argv[3], (std::size_t)std::stoul(argv[4]),
+                       (std::size_t)std::stoul(argv[5]), (std::size_t)std::stoul(argv[6]), trace,
+                       order);
+  }
   if (argc < 4) {
     std::printf("usage: qwen35_driver_check plan | linear <dir> <order> | full <dir> <order> | "
-                "decode <model.gguf> <outdir> <first_token> <steps>\n");
+                "decode <model.gguf> <outdir> <first_token> <steps> | "
+                "prefill <model.gguf> <outdir> <prompt> <chunk> <steps>\n");
     return 2;
   }
   const q35::OpOrder order =

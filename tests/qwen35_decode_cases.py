@@ -12,7 +12,16 @@ OracleDecoder replays run_qwen35_decode_tokens (qwen35_runtime.cpp:3860-3936)
 for one token per step through the oracle's functions: each layer's RMSNorm,
 K-quant projections (fp32, as the reference multiplies one token), the
 linear-attention or full-attention core, residual adds and the SwiGLU FFN;
-then the output norm and the LM head's argmax.
+then the output norm and the LM head's argmax.  Its prefill_chunk replays the
+prompt pass of generate_qwen35_metal (qwen35_runtime.cpp:5787-6004) for one
+chunk of many tokens: the same ops over the whole chunk, with the chunk's
+projections at the reference's GEMM precision (weights and inputs rounded to
+f16, run_qwen35_quant_matmul for more than 8 tokens) and its attention at the
+flash kernel's (query rounded to f16, mps_backend.mm:3458-3461).  Those two
+products go through numpy (float32 sums of f16 products, and float64 softmax
+attention) for speed; everything else is the C oracle's, and
+tests/test_qwen35_prefill_cases.py checks both numpy products against the
+oracle's own kquant_matmul and attention_batched on small cases.
 """
 import numpy as np
 
@@ -113,8 +122,42 @@ def write_gguf(path, model):
     return gw.write(path, meta, tensors)
 
 
+def f16_round(x):
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def gemm_f16(weight_f32, x, tokens):
+    """run_qwen35_quant_matmul for more than 8 tokens: out [tokens][rows] =
+    f16(x) [tokens][cols] times f16(W)^T, summed in float32 (f16 products are
+    exact in float32)."""
+    rows, cols = weight_f32.shape
+    xx = f16_round(np.asarray(x, np.float32).reshape(tokens, cols))
+    return (xx @ f16_round(weight_f32).T).astype(np.float32).reshape(-1)
+
+
+def causal_attention_f16q(q, kc_bits, vc_bits, start, tokens, cap, heads, kv_heads, d):
+    """attention_batched over cache positions 0 .. start + t for query token t,
+    with the query rounded to f16 (the flash path), K/V the cache's f16 values;
+    float64 softmax.  q [tokens][heads][d] -> out [tokens][heads][d]."""
+    n = start + tokens
+    k = kc_bits.view(np.float16).astype(np.float64).reshape(cap, kv_heads, d)[:n]
+    v = vc_bits.view(np.float16).astype(np.float64).reshape(cap, kv_heads, d)[:n]
+    qq = f16_round(q).astype(np.float64).reshape(tokens, heads, d)
+    group = heads // kv_heads
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    mask = np.arange(n)[None, :] > (start + np.arange(tokens))[:, None]
+    out = np.empty((tokens, heads, d))
+    for hh in range(heads):
+        s = qq[:, hh, :] @ k[:, hh // group, :].T * scale
+        s[mask] = -np.inf
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, hh, :] = (p @ v[:, hh // group, :]) / p.sum(axis=1, keepdims=True)
+    return out.astype(np.float32).reshape(-1)
+
+
 class OracleDecoder:
-    """The oracle's greedy decode over `model`, one token per step."""
+    """The oracle's greedy decode over `model`, one token per step (step), and
+    its chunked prompt pass (prefill_chunk) over the same caches."""
 
     def __init__(self, model, capacity):
         self.m = model
@@ -128,6 +171,86 @@ class OracleDecoder:
     def proj(self, name, x):
         (cols, rows), typ, data = self.m[name]
         return oracle.kquant_matmul(FMT[typ], data, rows, cols, x, 1)
+
+    def dequant(self, name):
+        (cols, rows), typ, data = self.m[name]
+        return oracle.kquant_dequantize(FMT[typ], data, rows * cols // 256).reshape(rows, cols)
+
+    def proj_chunk(self, name, x, tokens):
+        assert tokens > 8, "the chunk products follow the GEMM precision"
+        return gemm_f16(self.dequant(name), x, tokens)
+
+    def embed(self, token_ids):
+        (_, _), typ, emb = self.m["token_embd.weight"]
+        row = HIDDEN // 256 * BLOCK[typ]
+        return np.concatenate([
+            oracle.kquant_dequantize(FMT[typ], emb[t * row:(t + 1) * row], HIDDEN // 256)
+            for t in token_ids])
+
+    def linear_chunk(self, i, h, t):
+        p = f"blk.{i}."
+        n = oracle.rms_norm_batched(h, self.vec(p + "attn_norm.weight"), t, HIDDEN, EPS)
+        qkv, z = self.proj_chunk(p + "attn_qkv.weight", n, t), self.proj_chunk(
+            p + "attn_gate.weight", n, t)
+        beta = self.proj_chunk(p + "ssm_beta.weight", n, t)
+        alpha = self.proj_chunk(p + "ssm_alpha.weight", n, t)
+        ci, self.conv[i] = oracle.build_ssm_conv_state(self.conv[i], qkv, CONV_K, CONV_CH, t)
+        y = oracle.silu(oracle.ssm_conv(ci, self.vec(p + "ssm_conv1d.weight"), CONV_K, CONV_CH,
+                                        t, 1))
+        q, k, v = oracle.split_qkv_l2_norm(y, t, HK, HV, DK, EPS)
+        g, b = oracle.prepare_gdn_gate_beta(alpha, beta, self.vec(p + "ssm_dt.bias"),
+                                            self.vec(p + "ssm_a"), t, HV)
+        o, self.state[i] = oracle.gated_delta_net(q, k, v, g, b, self.state[i], t, HK, HV, DK)
+        o = oracle.norm_gated(o, self.vec(p + "ssm_norm.weight"), z, t, HV, DK, EPS)
+        return self.proj_chunk(p + "ssm_out.weight", o, t)
+
+    def full_chunk(self, i, h, start, t):
+        p = f"blk.{i}."
+        n = oracle.rms_norm_batched(h, self.vec(p + "attn_norm.weight"), t, HIDDEN, EPS)
+        qg = self.proj_chunk(p + "attn_q.weight", n, t).reshape(t, HEADS, 2, HEAD_DIM)
+        q, gate = qg[:, :, 0].ravel(), qg[:, :, 1].ravel()
+        k, v = self.proj_chunk(p + "attn_k.weight", n, t), self.proj_chunk(p + "attn_v.weight",
+                                                                           n, t)
+        q = oracle.qk_norm_f32_batched(q, self.vec(p + "attn_q_norm.weight"), t, HEADS,
+                                       HEAD_DIM, EPS)
+        k = oracle.qk_norm_f32_batched(k, self.vec(p + "attn_k_norm.weight"), t, KV_HEADS,
+                                       HEAD_DIM, EPS)
+        positions = oracle.make_mrope_positions(start, t)
+        q = oracle.mrope(q, positions, t, HEADS, HEAD_DIM, ROPE_DIMS, SECTIONS, THETA)
+        k = oracle.mrope(k, positions, t, KV_HEADS, HEAD_DIM, ROPE_DIMS, SECTIONS, THETA)
+        kv = KV_HEADS * HEAD_DIM
+        self.kc[i][start * kv:(start + t) * kv] = oracle.f32_to_f16_bits(k)
+        self.vc[i][start * kv:(start + t) * kv] = oracle.f32_to_f16_bits(v)
+        a = causal_attention_f16q(q, self.kc[i], self.vc[i], start, t, self.cap, HEADS,
+                                  KV_HEADS, HEAD_DIM)
+        a = oracle.sigmoid_gate_mul(a, gate)
+        return self.proj_chunk(p + "attn_output.weight", a, t)
+
+    def prefill_chunk(self, token_ids, start, trace=None, rows=None):
+        """Every layer over the chunk `token_ids` at positions start ..; returns
+        the chunk's last hidden state [tokens][HIDDEN].  Appends, per layer,
+        the hidden rows `rows` (default 0, tokens // 2, tokens - 1) to `trace`."""
+        t = len(token_ids)
+        rows = [0, t // 2, t - 1] if rows is None else rows
+        h = self.embed(token_ids)
+        for i in range(LAYERS):
+            a = self.full_chunk(i, h, start, t) if full_attention(i) else self.linear_chunk(i, h, t)
+            h = oracle.add(h, a)
+            p = f"blk.{i}."
+            n = oracle.rms_norm_batched(h, self.vec(p + "post_attention_norm.weight"), t, HIDDEN,
+                                        EPS)
+            up = self.proj_chunk(p + "ffn_up.weight", n, t)
+            gate = self.proj_chunk(p + "ffn_gate.weight", n, t)
+            h = oracle.add(h, self.proj_chunk(p + "ffn_down.weight", oracle.silu_mul(gate, up), t))
+            if trace is not None:
+                trace.append(h.reshape(t, HIDDEN)[rows].copy())
+        return h.reshape(t, HIDDEN)
+
+    def lm_head(self, last_row):
+        """Output norm and LM head of one hidden row (fp32 GEMV): (argmax, logits)."""
+        normed = self.norm(np.asarray(last_row, np.float32), "output_norm.weight")
+        logits = self.proj("token_embd.weight", normed)
+        return oracle.argmax(logits), logits
 
     def vec(self, name):
         return self.m[name][2]

@@ -171,3 +171,69 @@ def test_greedy_decode_matches_oracle_chain(tmp_path):
                 assert err <= 1e-3, (order, i, layer, err)
             token = int(got[i])
         print(f"{order}: worst per-layer relative error {worst:.2e}", flush=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(900)
+def test_chunked_prefill_then_decode_matches_oracle_chain(tmp_path):
+    """`qwen35_driver_check prefill`: a 1500-token prompt through the whole model in
+    chunks of 1024 (the second one ragged, 476 tokens) with the layer cores on
+    flash256 and the chunked gated delta rule and the projections on the K-quant
+    GEMM, one graph commit per chunk (qwen35_runtime.cpp:5787-6004); then 5 greedy
+    decode steps from position 1500 over the filled caches.  Against the oracle's
+    chunked prompt pass (tests/qwen35_decode_cases.py prefill_chunk): every
+    layer's hidden rows 0, T/2 and T-1 of both chunks, and every layer of every
+    decode step, within 1e-3 of the state's largest magnitude; the tokens under
+    the decode test's rule (a different token only where the oracle's two logits
+    are within 5e-3, and then the oracle continues from the device's token)."""
+    import qwen35_decode_cases as qc
+
+    prompt, chunk, steps = 1500, 1024, 6
+    model = qc.build_model()
+    path = tmp_path / "qwen35-0.8b-synthetic.gguf"
+    qc.write_gguf(path, model)
+    print("prefill: GGUF written", flush=True)
+    r = run("prefill", path, tmp_path, prompt, chunk, steps, "trace", timeout=600)
+    print(r.stdout[-1000:], flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    ids = np.fromfile(tmp_path / "prompt.i32", np.int32)
+    got = np.fromfile(tmp_path / "tokens.i32", np.int32)
+    assert ids.size == prompt and got.size == steps
+    assert np.array_equal(ids, (7919 * np.arange(prompt, dtype=np.int64) + 11) % qc.VOCAB)
+    chunks = [(0, chunk), (chunk, prompt - chunk)]
+    trace = np.fromfile(tmp_path / "prefill_trace.f32", np.float32).reshape(
+        len(chunks), qc.LAYERS, 3, qc.HIDDEN)
+    dec = qc.OracleDecoder(model, prompt + steps)
+    worst = 0.0
+    for c, (start, t) in enumerate(chunks):
+        ref = []
+        h = dec.prefill_chunk(ids[start:start + t].tolist(), start, ref)
+        for layer, want in enumerate(ref):
+            err = float(np.abs(trace[c, layer] - want).max()) / max(1.0, float(np.abs(want).max()))
+            worst = max(worst, err)
+            assert err <= 1e-3, ("prefill", c, layer, err)
+        print(f"prefill chunk {c} ({t} tokens) matches, worst so far {worst:.2e}", flush=True)
+
+    def agree(i, device, want, logits):
+        if device != want:
+            gap = abs(float(logits[device]) - float(logits[want]))
+            assert gap <= 5e-3 * max(1.0, abs(float(logits[want]))), (i, device, want, gap)
+            return 1
+        return 0
+
+    want, logits = dec.lm_head(h[-1])
+    switched = agree(0, int(got[0]), want, logits)
+    steps_trace = np.fromfile(tmp_path / "hidden_trace.f32", np.float32).reshape(
+        steps - 1, qc.LAYERS, qc.HIDDEN)
+    for i in range(steps - 1):
+        ref = []
+        want, logits, _ = dec.step(int(got[i]), prompt + i, ref)
+        for layer, row in enumerate(ref):
+            err = float(np.abs(steps_trace[i, layer] - row).max()) / max(1.0,
+                                                                         float(np.abs(row).max()))
+            worst = max(worst, err)
+            assert err <= 1e-3, ("decode", i, layer, err)
+        switched += agree(i + 1, int(got[i + 1]), want, logits)
+        print(f"decode step {i}: device {got[i + 1]} oracle {want}", flush=True)
+    assert switched <= 1
+    print(f"prefill + decode: worst per-layer relative error {worst:.2e}", flush=True)
