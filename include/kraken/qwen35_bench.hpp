@@ -5,8 +5,12 @@
 //   benchmark_attention / format_attention_bench_result mirror
 //     benchmark_qwen35_metal_attention / format_qwen35_attention_bench_result
 //     (qwen35_runtime.cpp:4997-5236);
-//   the config and result types mirror Qwen35{Gdn,Attention}Bench{Config,Result}
-//     (qwen35_runtime.hpp:107-175), with the same defaults.
+//   benchmark_matmul / format_matmul_bench_result mirror
+//     benchmark_qwen35_metal_matmul / format_qwen35_matmul_bench_result
+//     (qwen35_runtime.cpp:4558-4806): one K-quant tensor of a GGUF file times a
+//     tokens x cols input on matmul_q{4,5,6}_k_f32_device;
+//   the config and result types mirror Qwen35{Matmul,Gdn,Attention}Bench{Config,Result}
+//     (qwen35_runtime.hpp:75-175), with the same defaults.
 // Same argument checks and messages, same deterministic modular inputs, same
 // loop (warmup, then timed iterations of one graph each: begin, op, commit,
 // which waits), same derived rates and the same 16-value weighted checksum of
@@ -15,6 +19,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <filesystem>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -23,10 +28,38 @@
 #include <string>
 #include <vector>
 
+#include "kraken/gguf.hpp"
 #include "kraken/hip_context.hpp"
 
 namespace kraken {
 namespace qwen35 {
+
+struct MatmulBenchConfig {
+  std::string model_path;  // a .gguf file, or a directory holding one
+  std::string tensor_name;
+  std::size_t tokens{1024};
+  std::size_t warmup_iterations{2};
+  std::size_t timed_iterations{10};
+};
+
+struct MatmulBenchResult {
+  std::string gguf_path;
+  std::string tensor_name;
+  std::string type_name;
+  std::string dispatch;
+  std::uint32_t type{0};
+  std::size_t tokens{0};
+  std::size_t rows{0};
+  std::size_t cols{0};
+  std::size_t warmup_iterations{0};
+  std::size_t timed_iterations{0};
+  std::uint64_t output_values_per_iteration{0};
+  double total_seconds{0.0};
+  double average_milliseconds{0.0};
+  double token_iterations_per_second{0.0};
+  double output_megavalues_per_second{0.0};
+  double sample_checksum{0.0};
+};
 
 struct GdnBenchConfig {
   std::size_t tokens{1024};
@@ -195,6 +228,223 @@ inline std::string attention_dispatch_name(std::size_t tokens, std::size_t head_
     return "flash256_f16_kv";
   }
   return f16_kv ? "split_kv_decode_f16_kv" : "split_kv_decode_f32";
+}
+
+// resolve_gguf_model_path (gguf_reader.cpp:521-546): a .gguf file as given, or
+// the first .gguf (by name) in a directory.
+inline hip::Result<std::string> resolve_gguf_path(const std::string& path) {
+  namespace fs = std::filesystem;
+  std::error_code ec;
+  const fs::path p(path);
+  if (!fs::exists(p, ec)) {
+    return hip::Status::unavailable("model path does not exist: " + path);
+  }
+  if (fs::is_regular_file(p, ec)) {
+    if (p.extension() == ".gguf") {
+      return path;
+    }
+    return hip::Status::invalid_argument("model file is not a GGUF file: " + path);
+  }
+  if (!fs::is_directory(p, ec)) {
+    return hip::Status::invalid_argument("model path is not a file or directory: " + path);
+  }
+  std::vector<std::string> candidates;
+  for (const auto& entry : fs::directory_iterator(p, ec)) {
+    if (entry.is_regular_file() && entry.path().extension() == ".gguf") {
+      candidates.push_back(entry.path().string());
+    }
+  }
+  if (candidates.empty()) {
+    return hip::Status::unavailable("no GGUF file found in " + path);
+  }
+  std::sort(candidates.begin(), candidates.end());
+  return candidates.front();
+}
+
+// The name of a GGUF tensor type id (ggml's table).
+inline std::string ggml_type_name(std::uint32_t type) {
+  static const char* const kNames[] = {"F32",  "F16",  "Q4_0", "Q4_1", "", "",
+                                       "Q5_0", "Q5_1", "Q8_0", "Q8_1", "Q2_K", "Q3_K",
+                                       "Q4_K", "Q5_K", "Q6_K", "Q8_K"};
+  if (type < sizeof(kNames) / sizeof(kNames[0]) && kNames[type][0] != '\0') {
+    return kNames[type];
+  }
+  return "type_" + std::to_string(type);
+}
+
+// The K-quant projection kernel this backend runs for `tokens` rows of input
+// (capi_kquant: the fp32 GEMV up to 3 tokens, the GEMV on fp16-rounded weights
+// for 4 to 8, the fp16 MFMA GEMM above 8).
+inline std::string kquant_matmul_dispatch_name(std::uint32_t type, std::size_t tokens) {
+  if (type != 12U && type != 13U && type != 14U) {
+    return "unsupported";
+  }
+  if (tokens > 8U) {
+    return "kquant_gemm_f16_mfma";
+  }
+  return tokens >= 4U ? "kquant_gemv_f16_weights" : "kquant_gemv_f32";
+}
+
+// benchmark_qwen35_metal_matmul (qwen35_runtime.cpp:4558-4782).
+inline hip::Result<MatmulBenchResult> benchmark_matmul(const MatmulBenchConfig& config) {
+  using hip::Status;
+  if (config.model_path.empty()) {
+    return Status::invalid_argument("Qwen3.5 matmul bench requires --model");
+  }
+  if (config.tensor_name.empty()) {
+    return Status::invalid_argument("Qwen3.5 matmul bench requires --tensor");
+  }
+  if (config.tokens == 0) {
+    return Status::invalid_argument("Qwen3.5 matmul bench tokens must be positive");
+  }
+  if (config.timed_iterations == 0) {
+    return Status::invalid_argument("Qwen3.5 matmul bench timed iterations must be positive");
+  }
+  auto path = resolve_gguf_path(config.model_path);
+  if (!path.is_ok()) {
+    return path.status();
+  }
+  auto file = gguf::read_file(path.value());
+  if (!file.is_ok()) {
+    return file.status();
+  }
+  const gguf::TensorInfo* tensor = gguf::find_tensor(file.value(), config.tensor_name);
+  if (tensor == nullptr) {
+    return Status::invalid_argument("Qwen3.5 matmul bench tensor not found: " +
+                                    config.tensor_name);
+  }
+  if (tensor->shape.size() != 2U) {
+    return Status::invalid_argument("Qwen3.5 matmul bench tensor must be 2D: " + tensor->name);
+  }
+  if (tensor->type != 12U && tensor->type != 13U && tensor->type != 14U) {
+    return Status::invalid_argument(
+      "Qwen3.5 matmul bench currently supports only Q4_K/Q5_K/Q6_K tensors: " + tensor->name);
+  }
+  if (tensor->shape[0] > std::numeric_limits<std::size_t>::max() ||
+      tensor->shape[1] > std::numeric_limits<std::size_t>::max()) {
+    return Status::invalid_argument(tensor->name + " exceeds size_t");
+  }
+  const auto cols = static_cast<std::size_t>(tensor->shape[0]);
+  const auto rows = static_cast<std::size_t>(tensor->shape[1]);
+  if (cols == 0 || rows == 0) {
+    return Status::invalid_argument("Qwen3.5 matmul bench tensor shape is empty: " +
+                                    tensor->name);
+  }
+  if (cols % 256U != 0) {
+    return Status::invalid_argument("Qwen3.5 matmul bench K-quant cols must be divisible by 256: " +
+                                    tensor->name);
+  }
+  std::size_t input_values = 0;
+  std::size_t output_values = 0;
+  std::size_t bytes = 0;
+  if (!bench_detail::checked_mul_size(config.tokens, cols, input_values) ||
+      !bench_detail::checked_mul_size(config.tokens, rows, output_values) ||
+      !bench_detail::checked_mul_size(input_values, sizeof(float), bytes) ||
+      !bench_detail::checked_mul_size(output_values, sizeof(float), bytes)) {
+    return Status::invalid_argument("Qwen3.5 matmul bench value count overflow");
+  }
+  auto mapped = gguf::MappedData::open(file.value());
+  if (!mapped.is_ok()) {
+    return mapped.status();
+  }
+  auto weight_bytes = mapped.value().tensor_bytes(*tensor);
+  if (!weight_bytes.is_ok()) {
+    return weight_bytes.status();
+  }
+
+  auto context = hip::HipContext::create();
+  if (!context.is_ok()) {
+    return context.status();
+  }
+  const hip::HipContext& ctx = context.value();
+  auto weight = ctx.make_buffer(weight_bytes.value().second);
+  if (!weight.is_ok()) {
+    return weight.status();
+  }
+  Status status =
+    ctx.copy_to_buffer(weight.value(), weight_bytes.value().first, weight_bytes.value().second);
+  if (!status.is_ok()) {
+    return status;
+  }
+  // The reference's input pattern: (index mod 23 - 11) / 32.
+  std::vector<float> input(input_values);
+  for (std::size_t i = 0; i < input.size(); ++i) {
+    input[i] = static_cast<float>(static_cast<int>(i % 23U) - 11) * 0.03125F;
+  }
+  auto input_buffer = bench_detail::f32_buffer(ctx, input);
+  if (!input_buffer.is_ok()) {
+    return input_buffer.status();
+  }
+  auto output = ctx.make_buffer(output_values * sizeof(float));
+  if (!output.is_ok()) {
+    return output.status();
+  }
+  status = ctx.zero_buffer(output.value(), output_values * sizeof(float));
+  if (!status.is_ok()) {
+    return status;
+  }
+  const std::uint32_t type = tensor->type;
+  auto seconds = bench_detail::timed_graph_loop(
+    ctx, config.warmup_iterations, config.timed_iterations, [&]() -> Status {
+      switch (type) {
+        case 12:
+          return ctx.matmul_q4_k_f32_device(weight.value(), rows, cols, config.tokens,
+                                            input_buffer.value(), output.value());
+        case 13:
+          return ctx.matmul_q5_k_f32_device(weight.value(), rows, cols, config.tokens,
+                                            input_buffer.value(), output.value());
+        default:
+          return ctx.matmul_q6_k_f32_device(weight.value(), rows, cols, config.tokens,
+                                            input_buffer.value(), output.value());
+      }
+    });
+  if (!seconds.is_ok()) {
+    return seconds.status();
+  }
+  auto checksum = bench_detail::sample_checksum(ctx, output.value(), output_values);
+  if (!checksum.is_ok()) {
+    return checksum.status();
+  }
+  MatmulBenchResult r;
+  r.gguf_path = path.value();
+  r.tensor_name = tensor->name;
+  r.type_name = ggml_type_name(type);
+  r.dispatch = kquant_matmul_dispatch_name(type, config.tokens);
+  r.type = type;
+  r.tokens = config.tokens;
+  r.rows = rows;
+  r.cols = cols;
+  r.warmup_iterations = config.warmup_iterations;
+  r.timed_iterations = config.timed_iterations;
+  r.output_values_per_iteration = output_values;
+  r.total_seconds = seconds.value();
+  const double timed = static_cast<double>(config.timed_iterations);
+  r.average_milliseconds = r.total_seconds * 1000.0 / timed;
+  r.token_iterations_per_second = static_cast<double>(config.tokens) * timed / r.total_seconds;
+  r.output_megavalues_per_second =
+    static_cast<double>(output_values) * timed / (r.total_seconds * 1.0e6);
+  r.sample_checksum = checksum.value();
+  return r;
+}
+
+// format_qwen35_matmul_bench_result (qwen35_runtime.cpp:4784-4806); the first
+// line names this backend.
+inline std::string format_matmul_bench_result(const MatmulBenchResult& r) {
+  std::ostringstream o;
+  o << "Qwen3.5 HIP matmul bench: ok\n";
+  o << "GGUF: " << r.gguf_path << '\n';
+  o << "Tensor: " << r.tensor_name << '\n';
+  o << "Type: " << r.type_name << " (" << r.type << ")\n";
+  o << "Dispatch: " << r.dispatch << '\n';
+  o << "Shape: rows=" << r.rows << ", cols=" << r.cols << ", tokens=" << r.tokens << '\n';
+  o << "Iterations: warmup=" << r.warmup_iterations << ", timed=" << r.timed_iterations << '\n';
+  o << "Output values/iter: " << r.output_values_per_iteration << '\n';
+  o << "Total seconds: " << r.total_seconds << '\n';
+  o << "Average ms/iter: " << r.average_milliseconds << '\n';
+  o << "Token-iterations/s: " << r.token_iterations_per_second << '\n';
+  o << "Output Mvalues/s: " << r.output_megavalues_per_second << '\n';
+  o << "Sample checksum: " << r.sample_checksum << '\n';
+  return o.str();
 }
 
 // benchmark_qwen35_metal_gdn (qwen35_runtime.cpp:4808-4975).

@@ -388,6 +388,7 @@ int run_full(const std::string& dir, q35::OpOrder order) {
 
 }  // namespace
 
+// bench-matmul <model.gguf|dir> <tensor> <tokens> <warmup> <timed>
 // bench-gdn <tokens> <key_heads> <value_heads> <head_dim> <warmup> <timed>
 // bench-attention <tokens> <start> <capacity> <heads> <kv_heads> <head_dim> <warmup> <timed> <f16>
 // Prints the formatted result, or "error <code>: <message>" (exit 1).
@@ -397,6 +398,21 @@ int run_bench(const std::string& mode, int argc, char** argv) {
     std::printf("error %d: %s\n", (int)s.code(), s.message().c_str());
     return 1;
   };
+  if (mode == "bench-matmul" && argc >= 7) {
+    q35::MatmulBenchConfig c;
+    c.model_path = argv[2];
+    c.tensor_name = argv[3];
+    c.tokens = arg(4);
+    c.warmup_iterations = arg(5);
+    c.timed_iterations = arg(6);
+    auto r = q35::benchmark_matmul(c);
+    if (!r.is_ok()) {
+      return fail(r.status());
+    }
+    std::printf("%s", q35::format_matmul_bench_result(r.value()).c_str());
+    std::printf("checksum_exact %.17g\n", r.value().sample_checksum);
+    return 0;
+  }
   if (mode == "bench-gdn" && argc >= 8) {
     q35::GdnBenchConfig c;
     c.tokens = arg(2);

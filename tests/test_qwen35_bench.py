@@ -1,6 +1,6 @@
 """The reference's hot-path micro-benchmarks over the HIP backend
-(include/kraken/qwen35_bench.hpp, mirroring benchmark_qwen35_metal_{gdn,attention},
-qwen35_runtime.cpp:4808-5236), driven by tests/cpp/qwen35_driver_check.cpp.
+(include/kraken/qwen35_bench.hpp, mirroring benchmark_qwen35_metal_{matmul,gdn,attention},
+qwen35_runtime.cpp:4558-5236), driven by tests/cpp/qwen35_driver_check.cpp.
 
 * CPU: the argument checks, in the reference's order with its messages.
 * GPU: the sample checksum (weighted sum of the first 16 output values, weights 1..16)
@@ -8,7 +8,9 @@ qwen35_runtime.cpp:4808-5236), driven by tests/cpp/qwen35_driver_check.cpp.
   updates its state in place on every iteration, so the oracle replays warmup + timed
   iterations with the state carried.  Bounds: the weighted sum of the per-value
   tolerances, 1e-4 absolute per GDN value (fp32 state) and 1e-3 + 2e-3 |ref| per
-  attention value (fp16 KV).
+  attention value (fp16 KV).  The matmul bench's checksum against the oracle's
+  kquant_matmul at the precision of the token count (f16 weights and inputs above 8
+  tokens, f16 weights for 4 to 8, fp32 below), 1e-5 of sum |w x| per value.
 """
 import os
 import subprocess
@@ -129,3 +131,69 @@ def test_attention_bench_checksum_matches_oracle(shape):
     want = float(np.dot(ref, WEIGHTS[:ref.size]))
     bound = float(np.dot(1e-3 + 2e-3 * np.abs(ref), WEIGHTS[:ref.size]))
     assert abs(_checksum(out) - want) <= bound, (_checksum(out), want, bound)
+
+
+def _small_gguf(path):
+    """A GGUF with one Q4_K, one Q6_K and one F32 tensor (tests/gguf_writer.py)."""
+    import gguf_writer as gw
+    import qwen35_decode_cases as qc
+
+    rng = np.random.default_rng(9)
+    tensors = [("w4", (512, 40), gw.GGML_Q4_K, qc.quant(rng, gw.GGML_Q4_K, 40, 512)),
+               ("w6", (256, 24), gw.GGML_Q6_K, qc.quant(rng, gw.GGML_Q6_K, 24, 256)),
+               ("v", (8,), gw.GGML_F32, np.ones(8, np.float32)),
+               ("w3", (256, 2, 2), gw.GGML_Q4_K, qc.quant(rng, gw.GGML_Q4_K, 4, 256))]
+    gw.write(path, [("general.architecture", gw.STRING, "qwen35")], tensors)
+    return {name: (shape, typ, data) for name, shape, typ, data in tensors}
+
+
+def test_matmul_bench_argument_checks(tmp_path):
+    """benchmark_qwen35_metal_matmul's checks, in its order, with its messages
+    (qwen35_runtime.cpp:4560-4626); all of them fail before a context is made."""
+    path = tmp_path / "m.gguf"
+    _small_gguf(path)
+    (tmp_path / "notes.txt").write_text("x")
+    empty = tmp_path / "empty"
+    empty.mkdir()
+    cases = [
+        (("", "w4", 8, 1, 1), "error 1: Qwen3.5 matmul bench requires --model"),
+        ((path, "", 8, 1, 1), "error 1: Qwen3.5 matmul bench requires --tensor"),
+        ((path, "w4", 0, 1, 1), "error 1: Qwen3.5 matmul bench tokens must be positive"),
+        ((path, "w4", 8, 1, 0), "error 1: Qwen3.5 matmul bench timed iterations must be positive"),
+        ((tmp_path / "absent.gguf", "w4", 8, 1, 1),
+         f"error 2: model path does not exist: {tmp_path / 'absent.gguf'}"),
+        ((tmp_path / "notes.txt", "w4", 8, 1, 1),
+         f"error 1: model file is not a GGUF file: {tmp_path / 'notes.txt'}"),
+        ((empty, "w4", 8, 1, 1), f"error 2: no GGUF file found in {empty}"),
+        ((path, "nope", 8, 1, 1), "error 1: Qwen3.5 matmul bench tensor not found: nope"),
+        ((path, "v", 8, 1, 1), "error 1: Qwen3.5 matmul bench tensor must be 2D: v"),
+        ((path, "w3", 8, 1, 1), "error 1: Qwen3.5 matmul bench tensor must be 2D: w3"),
+        ((path, "w4", 1 << 62, 1, 1), "error 1: Qwen3.5 matmul bench value count overflow"),
+    ]
+    for args, message in cases:
+        code, out = _bench("bench-matmul", *args)
+        assert code == 1 and out.strip() == message, (args, out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tensor,tokens", [("w4", 1024), ("w6", 13), ("w4", 5), ("w6", 2)])
+def test_matmul_bench_checksum_matches_oracle(tmp_path, tensor, tokens):
+    """The sample checksum of the matmul bench (tensor of a GGUF directory, the
+    reference's (i mod 23 - 11) / 32 input) against the oracle's product at the
+    precision the reference uses for that token count."""
+    import qwen35_decode_cases as qc
+
+    model = _small_gguf(tmp_path / "m.gguf")
+    print(f"bench matmul {tensor} tokens={tokens}", flush=True)
+    code, out = _bench("bench-matmul", tmp_path, tensor, tokens, 1, 2)
+    assert code == 0, out
+    assert f"Dispatch: {'kquant_gemm_f16_mfma' if tokens > 8 else ''}" in out
+    (cols, rows), typ, data = model[tensor]
+    x = ((np.arange(tokens * cols) % 23) - 11).astype(np.float32) * np.float32(0.03125)
+    fmt = qc.FMT[typ]
+    want = oracle.kquant_matmul(fmt, data, rows, cols, x, tokens, weight_f16=tokens >= 4,
+                                input_f16=tokens > 8)[:16].astype(np.float64)
+    w = oracle.kquant_dequantize(fmt, data, rows * cols // 256).reshape(rows, cols)
+    scale = (np.abs(w) @ np.abs(x[:cols]))[:16]
+    bound = float(np.dot(1e-5 * scale + 1e-6, WEIGHTS[:want.size]))
+    assert abs(_checksum(out) - float(np.dot(want, WEIGHTS[:want.size]))) <= bound
