@@ -38,6 +38,8 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
+#include <cstring>
 
 #include "context_internal.hpp"
 #include "device_common.hpp"
@@ -100,18 +102,31 @@ __device__ __forceinline__ void bytes_to_float(uint32_t w, float* out) {
   out[3] = (float)(w >> 24);
 }
 
+// A 16-byte (or 4-byte, 2-byte) load, with the nontemporal hint when the data
+// is read once (the GEMVs stream each weight once; the GEMM re-reads a weight
+// tile for every token tile and keeps it cached).
+template <bool kNt, typename T>
+__device__ __forceinline__ T load_hint(const T* p) {
+  if constexpr (kNt) {
+    return __builtin_nontemporal_load(p);
+  } else {
+    return *p;
+  }
+}
+
 // The 16 bytes at `offset` (even) from the 4-byte-aligned `base`, read as
 // aligned dwords and shifted by the misalignment (0 or 2 bytes), so Q6_K's
 // 210-byte blocks need no unaligned access.  An aligned chunk re-reads its
 // last dword instead of the one after it, so no byte past the chunk is read.
+template <bool kNt = true>
 __device__ __forceinline__ u32x4_t load16_even(const uint8_t* base, uint64_t offset) {
   const uint32_t* p = reinterpret_cast<const uint32_t*>(base + (offset & ~(uint64_t)3));
   const uint32_t shift = (uint32_t)(offset & 3u);
-  const uint32_t w0 = __builtin_nontemporal_load(p);
-  const uint32_t w1 = __builtin_nontemporal_load(p + 1);
-  const uint32_t w2 = __builtin_nontemporal_load(p + 2);
-  const uint32_t w3 = __builtin_nontemporal_load(p + 3);
-  const uint32_t w4 = __builtin_nontemporal_load(p + (shift != 0u ? 4 : 3));
+  const uint32_t w0 = load_hint<kNt>(p);
+  const uint32_t w1 = load_hint<kNt>(p + 1);
+  const uint32_t w2 = load_hint<kNt>(p + 2);
+  const uint32_t w3 = load_hint<kNt>(p + 3);
+  const uint32_t w4 = load_hint<kNt>(p + (shift != 0u ? 4 : 3));
   u32x4_t r;
   r.x = __builtin_amdgcn_alignbyte(w1, w0, shift);
   r.y = __builtin_amdgcn_alignbyte(w2, w1, shift);
@@ -120,20 +135,61 @@ __device__ __forceinline__ u32x4_t load16_even(const uint8_t* base, uint64_t off
   return r;
 }
 
+// The bytes one lane needs of a block's chunk c, loaded before any math: for
+// Q4_K/Q5_K the 16-byte header (d, dmin, the 12 scale bytes), the chunk's 16
+// nibble bytes and (Q5_K) the 16 fifth-bit bytes of its half; for Q6_K the
+// chunk's 16 low-nibble bytes, its 16 high-bit-pair bytes, the 16 scales and d.
+struct RawChunk {
+  u32x4_t a, b, c;
+  uint32_t d;
+};
+
+template <int F, bool kNt>
+__device__ __forceinline__ RawChunk load_raw(const uint8_t* block, uint32_t c) {
+  RawChunk r;
+  if constexpr (F == 2) {
+    const uint64_t base = (uint64_t)(uintptr_t)block;
+    const uint8_t* b0 = reinterpret_cast<const uint8_t*>(base & ~(uint64_t)3);
+    const uint64_t mis = base & 3u;
+    const uint32_t h = c >> 2;
+    const uint32_t half = c & 1u;
+    r.a = load16_even<kNt>(b0, mis + 16u * c);                      // ql
+    r.b = load16_even<kNt>(b0, mis + 128u + 32u * h + 16u * half);  // qh
+    r.c = load16_even<kNt>(b0, mis + 192u);                         // scales
+    r.d = load_hint<kNt>(reinterpret_cast<const uint16_t*>(block + 208u));
+  } else {
+    const uint32_t qs_at = F == 1 ? 48u : 16u;
+    r.a = load_hint<kNt>(reinterpret_cast<const u32x4_t*>(block));  // header
+    r.b = load_hint<kNt>(reinterpret_cast<const u32x4_t*>(block + qs_at + 16u * c));
+    r.c = u32x4_t{0u, 0u, 0u, 0u};
+    if constexpr (F == 1) {
+      r.c = load_hint<kNt>(reinterpret_cast<const u32x4_t*>(block + 16u + 16u * (c & 1u)));
+    }
+    r.d = 0u;
+  }
+  return r;
+}
+
 // One lane's share of a block: chunk c (0..7) holds 32 quants, dequantized
 // into v0 (block positions p0 .. p0 + 15) and v1 (p1 .. p1 + 15).  With
 // kExact the arithmetic is the reference's, operation for operation (no
-// contraction), so dequantized rows are bit-identical to the oracle.
+// contraction), so dequantized rows are bit-identical to the oracle.  load()
+// and compute() split decode() so that a kernel can issue the loads of its next
+// chunks before it decodes the current ones.
 template <int F, bool kExact>
 struct ChunkDecoder {
   float v0[16], v1[16];
   uint32_t p0, p1;
 
   __device__ __forceinline__ void decode(const uint8_t* block, uint32_t c) {
+    compute(load_raw<F, true>(block, c), c);
+  }
+
+  __device__ __forceinline__ void compute(const RawChunk& r, uint32_t c) {
     if constexpr (F == 2) {
-      decode_q6(block, c);
+      compute_q6(r, c);
     } else {
-      decode_q45(block, c);
+      compute_q45(r, c);
     }
   }
 
@@ -147,16 +203,10 @@ struct ChunkDecoder {
     }
   }
 
-  __device__ __forceinline__ void decode_q45(const uint8_t* block, uint32_t c) {
-    const u32x4_t hdr = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(block));
-    const uint32_t qs_at = F == 1 ? 48u : 16u;
-    const u32x4_t qs =
-      __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(block + qs_at + 16u * c));
-    u32x4_t qh = {0u, 0u, 0u, 0u};
-    if constexpr (F == 1) {
-      qh = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4_t*>(block + 16u + 16u * (c & 1u)));
-    }
+  __device__ __forceinline__ void compute_q45(const RawChunk& r, uint32_t c) {
+    const u32x4_t& hdr = r.a;
+    const u32x4_t& qs = r.b;
+    const u32x4_t& qh = r.c;
     const uint32_t s = c >> 1;
     p0 = 64u * s + 16u * (c & 1u);
     p1 = p0 + 32u;
@@ -198,19 +248,15 @@ struct ChunkDecoder {
     }
   }
 
-  __device__ __forceinline__ void decode_q6(const uint8_t* block, uint32_t c) {
-    const uint64_t base = (uint64_t)(uintptr_t)block;
-    const uint8_t* b0 = reinterpret_cast<const uint8_t*>(base & ~(uint64_t)3);
-    const uint64_t mis = base & 3u;
+  __device__ __forceinline__ void compute_q6(const RawChunk& r, uint32_t c) {
+    const u32x4_t& ql = r.a;
+    const u32x4_t& qh = r.b;
+    const u32x4_t& sc = r.c;
     const uint32_t h = c >> 2;
     const uint32_t c4 = c & 3u;
     const uint32_t g = c4 >> 1;
     const uint32_t half = c4 & 1u;
-    const u32x4_t ql = load16_even(b0, mis + 16u * c);
-    const u32x4_t qh = load16_even(b0, mis + 128u + 32u * h + 16u * half);
-    const u32x4_t sc = load16_even(b0, mis + 192u);
-    const float d = half_bits_to_float(
-      __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(block + 208u)));
+    const float d = half_bits_to_float(r.d);
     const int s_lo = (int8_t)byte_of(sc, 8u * h + 2u * g + half);
     const int s_hi = (int8_t)byte_of(sc, 8u * h + 4u + 2u * g + half);
     float dl, dh;
@@ -445,37 +491,9 @@ __device__ __forceinline__ void chunk_positions(uint32_t c, uint32_t& p0, uint32
   }
 }
 
-// The bytes one lane needs of a block's chunk c, loaded before any math.
-struct RawChunk {
-  u32x4_t a, b, c;
-  uint32_t d;
-};
-
 template <int F>
 __device__ __forceinline__ RawChunk load_chunk(const uint8_t* block, uint32_t c) {
-  RawChunk r;
-  if constexpr (F == 2) {
-    const uint64_t base = (uint64_t)(uintptr_t)block;
-    const uint8_t* b0 = reinterpret_cast<const uint8_t*>(base & ~(uint64_t)3);
-    const uint64_t mis = base & 3u;
-    const uint32_t h = c >> 2;
-    const uint32_t half = c & 1u;
-    r.a = load16_even(b0, mis + 16u * c);                           // ql
-    r.b = load16_even(b0, mis + 128u + 32u * h + 16u * half);       // qh
-    r.c = load16_even(b0, mis + 192u);                              // scales
-    r.d = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(block + 208u));
-  } else {
-    const uint32_t qs_at = F == 1 ? 48u : 16u;
-    r.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(block));  // header
-    r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(block + qs_at + 16u * c));
-    r.c = {0u, 0u, 0u, 0u};
-    if constexpr (F == 1) {
-      r.c = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4_t*>(block + 16u + 16u * (c & 1u)));
-    }
-    r.d = 0u;
-  }
-  return r;
+  return load_raw<F, true>(block, c);
 }
 
 // sum over the chunk's 32 values of w * x, x[0..15] at p0 and x[16..31] at p1;
@@ -1172,6 +1190,164 @@ __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const
   }
 }
 
+// The same GEMM with the weights dequantized inside it: the B tile is decoded
+// from the K-quant blocks on its way into LDS, so the fp16 weight matrix is
+// never written and read back (the unfused path's dequantization pass wrote
+// 2 bytes per weight and the GEMM read them again, against 0.56-0.82 bytes per
+// weight of quant data here).  128 x 128 output tile, four waves as above, K
+// steps of 128 (half a 256-value super-block: every format's chunks 4 s' ..
+// 4 s' + 3 cover block positions 128 s' .. + 127), two LDS stages of 32 KB per
+// operand.  Thread t decodes chunks 2 (t & 1) and + 1 of its K step for tile
+// row t / 2 with the dequantization's exact arithmetic (ChunkDecoder<F, true>,
+// then RNE to fp16), so the B tile holds the values the unfused pass wrote,
+// and the MFMAs run over K in the same order: the result equals the unfused
+// path's.  Rows past the matrix decode its last row (never stored).  16-byte
+// chunk j of an LDS row lives at j ^ (row & 15).
+constexpr int kQK = 128;
+
+template <int F>
+__global__ __launch_bounds__(256) void gemm_kq_kernel(const half_t* x, const uint8_t* wq,
+                                                      float* c, uint32_t m, uint32_t n,
+                                                      uint32_t k, uint32_t split_steps) {
+  constexpr int TM = 128;
+  constexpr int TN = 128;
+  constexpr int IA = TM / 64;
+  constexpr int JB = TN / 64;
+  constexpr int LA = TM * kQK / 8 / 256;  // 16-byte chunks of the A tile per thread
+  __shared__ __attribute__((aligned(16))) half_t s_a[2][TM * kQK];
+  __shared__ __attribute__((aligned(16))) half_t s_b[2][TN * kQK];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint32_t m0 = blockIdx.y * TM;
+  const uint32_t n0 = blockIdx.x * TN;
+  const uint32_t bpr = k / 256u;
+  const __amdgpu_buffer_rsrc_t xr =
+    make_buffer_rsrc(x + (uint64_t)m0 * k, (uint32_t)min((uint64_t)TM, (uint64_t)(m - m0)) * k * 2u);
+  // This thread's B row (clamped to the matrix) and chunk pair.
+  const uint32_t brow = (uint32_t)tid >> 1;
+  const uint8_t* wrow =
+    wq + (uint64_t)min(n0 + brow, n - 1u) * bpr * KqFormat<F>::kBytes;
+  const uint32_t cpair = 2u * ((uint32_t)tid & 1u);
+  u32x4_t ra[LA];
+  RawChunk rb[2];
+  auto load_step = [&](uint32_t st) __attribute__((always_inline)) {
+    const uint32_t kk = st * kQK;
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+      const int idx = tid + 256 * i;
+      const uint32_t row = (uint32_t)(idx >> 4);
+      const uint32_t off = (row * k + kk + 8u * (uint32_t)(idx & 15)) * 2u;
+      ra[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
+    }
+    const uint8_t* block = wrow + (uint64_t)(st >> 1) * KqFormat<F>::kBytes;
+    const uint32_t c0 = 4u * (st & 1u) + cpair;
+    rb[0] = load_raw<F, false>(block, c0);
+    rb[1] = load_raw<F, false>(block, c0 + 1u);
+  };
+  auto store_step = [&](uint32_t st, int stage) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+      const int idx = tid + 256 * i;
+      const int row = idx >> 4;
+      const int chunk = (idx & 15) ^ (row & 15);
+      *reinterpret_cast<u32x4_t*>(&s_a[stage][row * kQK + 8 * chunk]) = ra[i];
+    }
+    const uint32_t c0 = 4u * (st & 1u) + cpair;
+    const uint32_t base = 128u * (st & 1u);
+    half_t* brow_lds = &s_b[stage][brow * kQK];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      ChunkDecoder<F, true> dec;
+      dec.compute(rb[q], c0 + (uint32_t)q);
+#pragma unroll
+      for (int half_i = 0; half_i < 2; ++half_i) {
+        half8_t h0, h1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          h0[j] = static_cast<half_t>(dec.v0[8 * half_i + j]);
+          h1[j] = static_cast<half_t>(dec.v1[8 * half_i + j]);
+        }
+        const uint32_t j0 = (dec.p0 - base) / 8u + (uint32_t)half_i;
+        const uint32_t j1 = (dec.p1 - base) / 8u + (uint32_t)half_i;
+        *reinterpret_cast<half8_t*>(brow_lds + 8u * (j0 ^ (brow & 15u))) = h0;
+        *reinterpret_cast<half8_t*>(brow_lds + 8u * (j1 ^ (brow & 15u))) = h1;
+      }
+    }
+  };
+  float16v_t acc[IA][JB];
+#pragma unroll
+  for (int i = 0; i < IA; ++i) {
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        acc[i][j][e] = 0.0f;
+      }
+    }
+  }
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int frow = lane & 31;
+  const int fk = lane >> 5;
+  const uint32_t s_begin = blockIdx.z * split_steps;
+  const uint32_t total_steps = k / kQK;
+  const uint32_t steps = s_begin < total_steps ? min(total_steps - s_begin, split_steps) : 0u;
+  c += (uint64_t)blockIdx.z * m * n;
+  if (steps > 0) {
+    load_step(s_begin);
+    store_step(s_begin, 0);
+  }
+  __syncthreads();
+  for (uint32_t s = 0; s < steps; ++s) {
+    const int stage = (int)(s & 1u);
+    if (s + 1 < steps) {
+      load_step(s_begin + s + 1);
+    }
+#pragma unroll
+    for (int ks = 0; ks < kQK / 16; ++ks) {
+      half8_t fa[IA], fb[JB];
+#pragma unroll
+      for (int i = 0; i < IA; ++i) {
+        const int row = (TM / 2) * wm + 32 * i + frow;
+        const int chunk = (2 * ks + fk) ^ (row & 15);
+        fa[i] = *reinterpret_cast<const half8_t*>(&s_a[stage][row * kQK + 8 * chunk]);
+      }
+#pragma unroll
+      for (int j = 0; j < JB; ++j) {
+        const int row = (TN / 2) * wn + 32 * j + frow;
+        const int chunk = (2 * ks + fk) ^ (row & 15);
+        fb[j] = *reinterpret_cast<const half8_t*>(&s_b[stage][row * kQK + 8 * chunk]);
+      }
+#pragma unroll
+      for (int i = 0; i < IA; ++i) {
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    if (s + 1 < steps) {
+      store_step(s_begin + s + 1, stage ^ 1);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < IA; ++i) {
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const uint32_t col = n0 + (TN / 2) * wn + 32u * j + (uint32_t)frow;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t row = m0 + (TM / 2) * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
+        if (row < m && col < n) {
+          c[(uint64_t)row * n + col] = acc[i][j][e];
+        }
+      }
+    }
+  }
+}
+
 // K splits: a 128 x 128 grid that would fill less than half of a 256-CU chip
 // (the 1024-row projections at 1024 tokens: 64 tiles) splits K into up to four
 // ranges of whole 64-deep steps, each writing an fp32 partial plane that one
@@ -1533,13 +1709,21 @@ uint32_t kquant_block_bytes(int format) {
   return format == 0 ? 144u : (format == 1 ? 176u : (format == 2 ? 210u : 0u));
 }
 
+// KRAKEN_KQUANT_GEMM=unfused selects the two-pass form (the weights
+// dequantized to an fp16 matrix in the workspace, then the fp16 GEMM) instead
+// of the fused one.
+bool kquant_gemm_unfused() {
+  const char* v = std::getenv("KRAKEN_KQUANT_GEMM");
+  return v != nullptr && std::strcmp(v, "unfused") == 0;
+}
+
 size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens) {
   (void)format;
   if (tokens <= kKquantGemvMaxTokens) {
     return 0;
   }
   const uint32_t splits = gemm_k_splits(rows, cols, tokens);
-  return align256(rows * cols * 2u) + align256(tokens * cols * 2u) +
+  return (kquant_gemm_unfused() ? align256(rows * cols * 2u) : 0u) + align256(tokens * cols * 2u) +
          (splits > 1 ? align256(splits * tokens * rows * 4u) : 0u);
 }
 
@@ -1563,22 +1747,26 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
       workspace_bytes < kquant_matmul_workspace_bytes(format, rows, cols, tokens)) {
     return hipErrorInvalidValue;
   }
+  // Workspace: [fp16 weights (unfused only)] [fp16 inputs] [K-split planes].
+  const bool unfused = kquant_gemm_unfused();
   half_t* w16 = static_cast<half_t*>(workspace);
   half_t* x16 = reinterpret_cast<half_t*>(static_cast<char*>(workspace) +
-                                          align256(rows * cols * 2u));
-  const uint64_t chunks = (uint64_t)rows * bpr * 8u;
-  const dim3 dq((uint32_t)((chunks + 255) / 256));
+                                          (unfused ? align256(rows * cols * 2u) : 0u));
   const uint8_t* wq = static_cast<const uint8_t*>(weight);
-  if (format == 0) {
-    kq_dequant_f16_kernel<0><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
-  } else if (format == 1) {
-    kq_dequant_f16_kernel<1><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
-  } else {
-    kq_dequant_f16_kernel<2><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    return e;
+  hipError_t e = hipSuccess;
+  if (unfused) {
+    const uint64_t chunks = (uint64_t)rows * bpr * 8u;
+    const dim3 dq((uint32_t)((chunks + 255) / 256));
+    if (format == 0) {
+      kq_dequant_f16_kernel<0><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
+    } else if (format == 1) {
+      kq_dequant_f16_kernel<1><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
+    } else {
+      kq_dequant_f16_kernel<2><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
+    }
+    if ((e = hipGetLastError()) != hipSuccess) {
+      return e;
+    }
   }
   const uint64_t n8 = (uint64_t)tokens * cols / 8u;
   f32_to_f16_kernel<<<dim3((uint32_t)((n8 + 255) / 256)), 256, 0, stream>>>(input, x16, n8);
@@ -1586,15 +1774,30 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
     return e;
   }
   const uint32_t splits = gemm_k_splits(rows, cols, tokens);
-  const uint32_t steps = (uint32_t)(cols / kGK);
-  const uint32_t split_steps = (steps + splits - 1) / splits;
   float* planes = splits > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(x16) +
                                                         align256(tokens * cols * 2u))
                              : output;
   const dim3 grid((uint32_t)((rows + 127) / 128), (uint32_t)((tokens + 127) / 128), splits);
-  gemm_f16_nt_kernel<128, 128><<<grid, 256, 0, stream>>>(x16, w16, planes, (uint32_t)tokens,
-                                                         (uint32_t)rows, (uint32_t)cols,
-                                                         split_steps);
+  if (unfused) {
+    const uint32_t steps = (uint32_t)(cols / kGK);
+    const uint32_t split_steps = (steps + splits - 1) / splits;
+    gemm_f16_nt_kernel<128, 128><<<grid, 256, 0, stream>>>(x16, w16, planes, (uint32_t)tokens,
+                                                           (uint32_t)rows, (uint32_t)cols,
+                                                           split_steps);
+  } else {
+    const uint32_t steps = (uint32_t)(cols / kQK);
+    const uint32_t split_steps = (steps + splits - 1) / splits;
+    if (format == 0) {
+      gemm_kq_kernel<0><<<grid, 256, 0, stream>>>(x16, wq, planes, (uint32_t)tokens,
+                                                  (uint32_t)rows, (uint32_t)cols, split_steps);
+    } else if (format == 1) {
+      gemm_kq_kernel<1><<<grid, 256, 0, stream>>>(x16, wq, planes, (uint32_t)tokens,
+                                                  (uint32_t)rows, (uint32_t)cols, split_steps);
+    } else {
+      gemm_kq_kernel<2><<<grid, 256, 0, stream>>>(x16, wq, planes, (uint32_t)tokens,
+                                                  (uint32_t)rows, (uint32_t)cols, split_steps);
+    }
+  }
   if ((e = hipGetLastError()) != hipSuccess || splits == 1) {
     return e;
   }
