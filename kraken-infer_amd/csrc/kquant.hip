@@ -1709,21 +1709,30 @@ uint32_t kquant_block_bytes(int format) {
   return format == 0 ? 144u : (format == 1 ? 176u : (format == 2 ? 210u : 0u));
 }
 
-// KRAKEN_KQUANT_GEMM=unfused selects the two-pass form (the weights
-// dequantized to an fp16 matrix in the workspace, then the fp16 GEMM) instead
-// of the fused one.
-bool kquant_gemm_unfused() {
+// The GEMM form per format: the fused one (weights decoded in the B tile) for
+// Q4_K, the two-pass one (the weights dequantized to an fp16 matrix in the
+// workspace, then the fp16 GEMM) for Q5_K and Q6_K, whose decode costs more
+// VALU work per weight than the fused tile hides under its MFMAs (measured on
+// the Qwen3.5-0.8B shapes at 1024 tokens: Q4_K 3584 x 1024 31.3 -> 28.0 us,
+// Q5_K 6144 x 1024 38.2 -> 48.3 us, Q6_K 1024 x 3584 32.5 -> 40.1 us).
+// KRAKEN_KQUANT_GEMM=fused or =unfused forces one form for every format.
+bool kquant_gemm_unfused(int format) {
   const char* v = std::getenv("KRAKEN_KQUANT_GEMM");
-  return v != nullptr && std::strcmp(v, "unfused") == 0;
+  if (v != nullptr && std::strcmp(v, "unfused") == 0) {
+    return true;
+  }
+  if (v != nullptr && std::strcmp(v, "fused") == 0) {
+    return false;
+  }
+  return format != 0;
 }
 
 size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens) {
-  (void)format;
   if (tokens <= kKquantGemvMaxTokens) {
     return 0;
   }
   const uint32_t splits = gemm_k_splits(rows, cols, tokens);
-  return (kquant_gemm_unfused() ? align256(rows * cols * 2u) : 0u) + align256(tokens * cols * 2u) +
+  return (kquant_gemm_unfused(format) ? align256(rows * cols * 2u) : 0u) + align256(tokens * cols * 2u) +
          (splits > 1 ? align256(splits * tokens * rows * 4u) : 0u);
 }
 
@@ -1748,7 +1757,7 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
     return hipErrorInvalidValue;
   }
   // Workspace: [fp16 weights (unfused only)] [fp16 inputs] [K-split planes].
-  const bool unfused = kquant_gemm_unfused();
+  const bool unfused = kquant_gemm_unfused(format);
   half_t* w16 = static_cast<half_t*>(workspace);
   half_t* x16 = reinterpret_cast<half_t*>(static_cast<char*>(workspace) +
                                           (unfused ? align256(rows * cols * 2u) : 0u));

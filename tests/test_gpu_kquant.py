@@ -178,14 +178,16 @@ def test_matvec_and_one_token_matmul_agree(hip_ctx, ops):
     ("q4_k", 77, 512, 130), ("q5_k", 200, 768, 9), ("q6_k", 130, 1280, 257),
     ("q6_k", 16, 1024, 1024)])
 def test_fused_gemm_equals_two_pass_gemm(ops, monkeypatch, fmt, rows, cols, tokens):
-    """The GEMM that decodes the weights into its B tile (the default) against the
-    two-pass form (KRAKEN_KQUANT_GEMM=unfused: an fp16 weight matrix written by
-    the exact dequantization, then the fp16 GEMM): the same fp16 weights and the
-    same MFMA order over K, so the outputs are bit-identical; partial row and
-    token tiles, odd block counts per row and 16-row tensors included."""
+    """The GEMM that decodes the weights into its B tile (KRAKEN_KQUANT_GEMM=fused;
+    the default for Q4_K) against the two-pass form (=unfused: an fp16 weight
+    matrix written by the exact dequantization, then the fp16 GEMM; the default
+    for Q5_K and Q6_K): the same fp16 weights and the same MFMA order over K, so
+    the outputs are bit-identical; partial row and token tiles, odd block counts
+    per row and 16-row tensors included."""
     print(f"fused gemm {fmt} {rows}x{cols} tokens={tokens}", flush=True)
     w = kc.random_weight_fast(fmt, rows, cols, seed=rows * 7 + cols)
     x = np.random.default_rng(tokens).standard_normal(tokens * cols).astype(np.float32)
+    monkeypatch.setenv("KRAKEN_KQUANT_GEMM", "fused")
     fused = ops.kquant_matmul(fmt, w, rows, cols, x, tokens)
     monkeypatch.setenv("KRAKEN_KQUANT_GEMM", "unfused")
     two_pass = ops.kquant_matmul(fmt, w, rows, cols, x, tokens)
