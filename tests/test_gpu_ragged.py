@@ -297,19 +297,26 @@ def _run_gdn_chain(ctx, c, b, hk, hv, dd, kk):
 
 
 @pytest.mark.parametrize("shape,prepare", [
-    ((7, 16, 16, 128, 4), True), ((7, 16, 16, 128, 4), False),  # one kernel
+    ((7, 16, 16, 128, 4), True), ((7, 16, 16, 128, 4), False),  # one workgroup per head
+    ((1, 16, 16, 128, 4), True), ((4, 16, 16, 128, 4), False),  # heads split 8 ways
     ((5, 2, 4, 64, 3), True), ((3, 4, 4, 96, 4), False),         # three-kernel chain
 ])
 def test_ragged_gdn_layer_matches_chain_and_oracle(hip_ctx, shape, prepare):
     """kraken_hip_qwen35_gdn_layer_ragged_decode_f32 against the three ragged ops
-    it replaces (equal bit for bit for the one-kernel shape; the chain shapes
-    are that chain) and against the oracle's conv, prepare, recurrence and
-    norm-gated steps per sequence (1e-4 absolute)."""
+    it replaces (equal bit for bit for the one-kernel shapes, in both the form
+    with one workgroup per (sequence, head) and the one that splits each head
+    over eight workgroups for up to four sequences; the chain shapes are that
+    chain) and against the oracle's conv, prepare, recurrence and norm-gated
+    steps per sequence (1e-4 absolute).  The split form runs twice, so its
+    arrival counters are shown to be back at zero after a call."""
     b, hk, hv, dd, kk = shape
     print(f"gdn layer {shape} prepare={prepare}", flush=True)
     rng = np.random.default_rng(50 + b + hk)
     c = _gdn_layer_case(rng, b, hk, hv, dd, kk, prepare)
     out, cpool, spool = _run_gdn_layer(hip_ctx, c, b, hk, hv, dd, kk)
+    again = _run_gdn_layer(hip_ctx, c, b, hk, hv, dd, kk)
+    for x, y in zip((out, cpool, spool), again):
+        np.testing.assert_array_equal(x, y)
     ref_out, ref_cpool, ref_spool = _run_gdn_chain(hip_ctx, c, b, hk, hv, dd, kk)
     np.testing.assert_array_equal(out, ref_out)
     np.testing.assert_array_equal(cpool, ref_cpool)
