@@ -1302,13 +1302,6 @@ KRAKEN_API int kraken_hip_qwen35_gdn_layer_ragged_decode_f32(
   const auto* ssa = static_cast<const float*>(ssm_a.data);
   if (gdn_layer_fused_supported((uint32_t)head_dim, (uint32_t)conv_kernel, (uint32_t)key_heads,
                                 (uint32_t)value_heads)) {
-    // Few sequences split each head over several workgroups; the y rows meet
-    // in workspace scratch and the context's arrival counters.
-    const size_t split_floats =
-      gdn_layer_split_scratch_floats((uint32_t)sequences, (uint32_t)value_heads);
-    if (split_floats > 0) {
-      KRAKEN_TRY(ensure_workspace(ctx, split_floats * sizeof(float)));
-    }
     KRAKEN_TRY(begin_launch(ctx));
     GdnLayerArgs a{};
     a.qkv = static_cast<const float*>(qkv.data);
@@ -1329,9 +1322,7 @@ KRAKEN_API int kraken_hip_qwen35_gdn_layer_ragged_decode_f32(
     a.sequences = (uint32_t)sequences;
     a.heads = (uint32_t)value_heads;
     a.eps = eps;
-    const hipError_t e = launch_gdn_layer_ragged(
-      a, split_floats > 0 ? static_cast<float*>(ctx->workspace) : nullptr,
-      split_floats > 0 ? ctx->arrival_counters : nullptr, ctx->stream);
+    const hipError_t e = launch_gdn_layer_ragged(a, ctx->stream);
     if (e != hipSuccess) {
       return internal(w + " launch failed: " + hipGetErrorString(e));
     }

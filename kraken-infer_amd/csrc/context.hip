@@ -232,18 +232,6 @@ KRAKEN_API int kraken_hip_context_create(kraken_hip_context** out_context) {
     delete ctx;
     return scratch_status;
   }
-  // Zeroed once here, outside any caller's graph capture.
-  e = hipMalloc(reinterpret_cast<void**>(&ctx->arrival_counters),
-                kArrivalCounters * sizeof(uint32_t));
-  if (e == hipSuccess) {
-    e = hipMemset(ctx->arrival_counters, 0, kArrivalCounters * sizeof(uint32_t));
-  }
-  if (e != hipSuccess) {
-    (void)hipFree(ctx->arrival_counters);
-    (void)hipStreamDestroy(ctx->own_stream);
-    delete ctx;
-    return unavailable("HIP backend: counter allocation failed: " + hip_message(e));
-  }
   *out_context = ctx;
   return KRAKEN_OK;
 }
@@ -271,9 +259,6 @@ KRAKEN_API void kraken_hip_context_destroy(kraken_hip_context* ctx) {
     }
     for (void* w : ctx->retired_workspaces) {
       (void)hipFree(w);
-    }
-    if (ctx->arrival_counters != nullptr) {
-      (void)hipFree(ctx->arrival_counters);
     }
     if (ctx->own_stream != nullptr) {
       (void)hipStreamDestroy(ctx->own_stream);

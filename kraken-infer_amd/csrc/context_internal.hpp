@@ -32,10 +32,6 @@ struct kraken_hip_context {
   // This device's copy of the static scratch array used by the allocation-free
   // entry point (device address, resolved at context creation).
   void* no_alloc_scratch = nullptr;
-  // Arrival counters of kernels whose last workgroup finishes a shared result
-  // (the split GDN layer), zeroed once at creation; each such kernel resets
-  // the counters it used before it ends, so they stay zero between calls.
-  uint32_t* arrival_counters = nullptr;
 };
 
 // Returns from the calling entry point with the status of `expr` unless it is OK.
@@ -72,9 +68,6 @@ int finish_launch(kraken_hip_context* ctx, const char* error_prefix);
 // destroyed, so work already enqueued or captured into a graph keeps a valid
 // address and nothing waits.  Returns KRAKEN_OK or an error status.
 int ensure_workspace(kraken_hip_context* ctx, size_t bytes);
-
-// Number of the context's arrival counters (kraken_hip_context::arrival_counters).
-constexpr size_t kArrivalCounters = 4096;
 
 // Size of the static per-device scratch array of the allocation-free entry
 // point, and the lookup of its device address on `device` (which must be the
@@ -235,14 +228,7 @@ struct GdnLayerArgs {
 // 4, key_heads == value_heads).
 bool gdn_layer_fused_supported(uint32_t head_dim, uint32_t conv_kernel, uint32_t key_heads,
                                uint32_t value_heads);
-// `partials` (sequences * heads * 128 floats of scratch) and `counters`
-// (sequences * heads zeroed arrival counters, left zeroed) serve the split form
-// that few sequences take; either may be null, which keeps one workgroup per
-// (sequence, head).
-hipError_t launch_gdn_layer_ragged(const GdnLayerArgs& a, float* partials, uint32_t* counters,
-                                   hipStream_t stream);
-// Scratch floats the split form needs for `sequences` x `heads` (0: not split).
-size_t gdn_layer_split_scratch_floats(uint32_t sequences, uint32_t heads);
+hipError_t launch_gdn_layer_ragged(const GdnLayerArgs& a, hipStream_t stream);
 
 hipError_t launch_ssm_conv(const float* input, const float* kernel, float* output,
                            uint32_t conv_kernel, uint32_t channels, uint32_t tokens,

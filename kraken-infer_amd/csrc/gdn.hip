@@ -927,226 +927,6 @@ __global__ __launch_bounds__(256) void gdn_layer_ragged_kernel(GdnLayerArgs p) {
   }
 }
 
-// The same layer for few sequences, each (sequence, head) split over P
-// workgroups of 128 / P state rows (P = 8: 16 rows, two per 32-lane group), so
-// a single sequence's 16 heads stream their state through 128 CUs instead of
-// 16.  Every part recomputes the head's q and k convolutions and L2 norms
-// (256 channels) and convolves only its own v channels; it updates its rows of
-// S and writes their y to `partials` with device-scope stores.  The norm-gated
-// epilogue needs all 128 y of the head, and the conv-state update of the q/k
-// channels must wait until every part has read them, so the last part to
-// arrive (a device-scope counter per (sequence, head), which it resets to zero)
-// does both: it reads the y rows back with device-scope loads (the other parts
-// waited for their stores to complete before counting themselves in).  Each
-// value is computed with gdn_layer_ragged_kernel's arithmetic and lane mapping,
-// so the two forms agree bit for bit.
-template <bool kPrepare, int P>
-__global__ __launch_bounds__(256) void gdn_layer_split_kernel(GdnLayerArgs p, float* partials,
-                                                              uint32_t* counters) {
-  constexpr uint32_t D = 128;
-  constexpr int K = 4;
-  constexpr int W = K - 1;
-  constexpr int ROWS = D / P;      // state rows of a part
-  constexpr int RPL = ROWS / 8;    // rows per 32-lane group
-  constexpr int CPL = 2;           // conv channels per lane of the q/k waves (D / 64)
-  static_assert(RPL >= 1 && ROWS <= 64, "one v channel per lane of wave 2");
-  __shared__ float qs[D], ks[D], vs[ROWS];
-  __shared__ uint32_t s_last;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int grp = tid >> 5;
-  const uint32_t part = blockIdx.x;
-  const uint32_t h = blockIdx.y;
-  const uint32_t seq = blockIdx.z;
-  const uint32_t H = p.heads;
-  const size_t channels = (size_t)3 * H * D;
-
-  const uint64_t soff = p.seq_state_offsets[seq];
-  const uint64_t coff = p.seq_conv_offsets[seq];
-  if ((soff & 3u) != 0 || soff > p.state_pool_elems ||
-      p.state_pool_elems - soff < (uint64_t)H * D * D || coff > p.conv_pool_elems ||
-      p.conv_pool_elems - coff < channels * W) {
-    return;  // the sequence's every part returns here: its counter is never touched
-  }
-  float* shead = p.state_pool + soff + (size_t)h * D * D;
-  const uint32_t prow0 = part * ROWS;
-  const uint32_t row0 = prow0 + (uint32_t)grp * RPL;
-  const uint32_t col0 = (uint32_t)(lane & 31) * 4;
-  float4 s[RPL];
-#pragma unroll
-  for (int j = 0; j < RPL; ++j) {
-    s[j] = *reinterpret_cast<const float4*>(shead + (size_t)(row0 + j) * D + col0);
-  }
-  const size_t gi = (size_t)seq * H + h;
-  float g = p.gate[gi];
-  float b = p.beta[gi];
-  float dtb = 0.0f, sa = 0.0f;
-  if (kPrepare) {
-    dtb = p.dt_bias[h];
-    sa = p.ssm_a[h];
-  }
-  float zz[2], nw[2];
-  if (wave == 0) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      zz[i] = p.z[gi * D + lane + 64 * i];
-      nw[i] = p.norm_weight[lane + 64 * i];
-    }
-  }
-
-  float* state = p.conv_pool + coff;
-  // The q/k waves keep their window and input for the deferred state update.
-  float win[CPL][W];
-  float xt[CPL];
-  if (wave < 2) {
-    const uint32_t cbase = ((uint32_t)wave * H + h) * D;
-    float y[CPL];
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const size_t c = cbase + lane + 64u * i;
-#pragma unroll
-      for (int j = 0; j < W; ++j) {
-        win[i][j] = state[c * W + j];
-      }
-      xt[i] = p.qkv[(size_t)seq * channels + c];
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < W; ++j) {
-        acc = fmaf(win[i][j], p.conv_weights[c * K + j], acc);
-      }
-      acc = fmaf(xt[i], p.conv_weights[c * K + W], acc);
-      y[i] = acc / (1.0f + expf(-acc));  // SiLU
-      ss = fmaf(y[i], y[i], ss);
-    }
-    ss = wave_sum(ss);
-    const float inv = 1.0f / fmaxf(sqrtf(ss), p.eps);
-    float* dst = wave == 0 ? qs : ks;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      dst[lane + 64 * i] = y[i] * inv;
-    }
-  } else if (wave == 2 && lane < ROWS) {
-    // This part's v channels (one per lane): convolve and update their state.
-    const size_t c = ((size_t)2 * H + h) * D + prow0 + lane;
-    float w3[W];
-#pragma unroll
-    for (int j = 0; j < W; ++j) {
-      w3[j] = state[c * W + j];
-    }
-    const float x = p.qkv[(size_t)seq * channels + c];
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < W; ++j) {
-      acc = fmaf(w3[j], p.conv_weights[c * K + j], acc);
-    }
-    acc = fmaf(x, p.conv_weights[c * K + W], acc);
-#pragma unroll
-    for (int j = 0; j + 1 < W; ++j) {
-      state[c * W + j] = w3[j + 1];
-    }
-    state[c * W + (W - 1)] = x;
-    vs[lane] = acc / (1.0f + expf(-acc));
-  }
-  if (kPrepare) {
-    g = softplus_ref(g + dtb) * sa;
-    b = 1.0f / (1.0f + expf(-b));
-  }
-  const float decay = expf(g);
-  __syncthreads();
-
-  const float4 k = *reinterpret_cast<const float4*>(&ks[col0]);
-  const float4 q = *reinterpret_cast<const float4*>(&qs[col0]);
-  const float scale = 1.0f / sqrtf((float)D);
-  float sk[RPL];
-#pragma unroll
-  for (int j = 0; j < RPL; ++j) {
-    s[j].x *= decay;
-    s[j].y *= decay;
-    s[j].z *= decay;
-    s[j].w *= decay;
-    sk[j] = fmaf(s[j].x, k.x, fmaf(s[j].y, k.y, fmaf(s[j].z, k.z, s[j].w * k.w)));
-  }
-#pragma unroll
-  for (int j = 0; j < RPL; ++j) {
-    sk[j] = reduce32_sum(sk[j]);
-  }
-  float yv[RPL];
-#pragma unroll
-  for (int j = 0; j < RPL; ++j) {
-    const float delta = (vs[row0 - prow0 + j] - sk[j]) * b;
-    s[j].x = fmaf(k.x, delta, s[j].x);
-    s[j].y = fmaf(k.y, delta, s[j].y);
-    s[j].z = fmaf(k.z, delta, s[j].z);
-    s[j].w = fmaf(k.w, delta, s[j].w);
-    yv[j] = fmaf(s[j].x, q.x, fmaf(s[j].y, q.y, fmaf(s[j].z, q.z, s[j].w * q.w)));
-  }
-#pragma unroll
-  for (int j = 0; j < RPL; ++j) {
-    yv[j] = reduce32_sum(yv[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < RPL; ++j) {
-    *reinterpret_cast<float4*>(shead + (size_t)(row0 + j) * D + col0) = s[j];
-  }
-  float* yrow = partials + gi * D;
-  if ((lane & 31) == 0) {
-#pragma unroll
-    for (int j = 0; j < RPL; ++j) {
-      __hip_atomic_store(yrow + row0 + j, yv[j] * scale, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  // This part's y rows have reached device scope before it counts itself in.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t before =
-      __hip_atomic_fetch_add(counters + gi, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = before == (uint32_t)(P - 1) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (s_last == 0u) {
-    return;
-  }
-  // Last part: every other part has read the q/k conv state and stored its y.
-  if (tid == 0) {
-    __hip_atomic_store(counters + gi, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (wave < 2) {
-    const uint32_t cbase = ((uint32_t)wave * H + h) * D;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const size_t c = cbase + lane + 64u * i;
-#pragma unroll
-      for (int j = 0; j + 1 < W; ++j) {
-        state[c * W + j] = win[i][j + 1];
-      }
-      state[c * W + (W - 1)] = xt[i];
-    }
-  }
-  if (wave == 0) {
-    // Norm-gated epilogue: y <- y * rsqrt(mean(y^2) + eps) * w * silu(z).
-    float v[2];
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      v[i] = __hip_atomic_load(yrow + lane + 64 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sum = fmaf(v[i], v[i], sum);
-    }
-    sum = wave_sum(sum);
-    const float nscale = 1.0f / sqrtf(sum / (float)D + p.eps);
-    const size_t rowoff = gi * D;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      float r = v[i] * nscale * nw[i];
-      r *= zz[i] * (1.0f / (1.0f + expf(-zz[i])));
-      p.output[rowoff + lane + 64 * i] = r;
-    }
-  }
-}
-
 unsigned grid_for(size_t total, unsigned block = 256) {
   size_t blocks = (total + block - 1) / block;
   if (blocks < 1) {
@@ -1293,29 +1073,7 @@ bool gdn_layer_fused_supported(uint32_t head_dim, uint32_t conv_kernel, uint32_t
   return head_dim == 128 && conv_kernel == 4 && key_heads == value_heads;
 }
 
-// Parts per (sequence, head) of the split form: while sequences x heads
-// workgroups would leave most of a 256-CU chip idle.
-constexpr uint32_t kGdnLayerParts = 8;
-
-size_t gdn_layer_split_scratch_floats(uint32_t sequences, uint32_t heads) {
-  const uint64_t units = (uint64_t)sequences * heads;
-  return units > 0 && units * 4u <= 256u && units <= kArrivalCounters ? (size_t)units * 128u : 0;
-}
-
-hipError_t launch_gdn_layer_ragged(const GdnLayerArgs& a, float* partials, uint32_t* counters,
-                                   hipStream_t stream) {
-  if (partials != nullptr && counters != nullptr &&
-      gdn_layer_split_scratch_floats(a.sequences, a.heads) > 0) {
-    const dim3 grid(kGdnLayerParts, a.heads, a.sequences);
-    if (a.dt_bias != nullptr) {
-      gdn_layer_split_kernel<true, kGdnLayerParts><<<grid, 256, 0, stream>>>(a, partials,
-                                                                            counters);
-    } else {
-      gdn_layer_split_kernel<false, kGdnLayerParts><<<grid, 256, 0, stream>>>(a, partials,
-                                                                             counters);
-    }
-    return hipGetLastError();
-  }
+hipError_t launch_gdn_layer_ragged(const GdnLayerArgs& a, hipStream_t stream) {
   const dim3 grid(a.heads, a.sequences);
   if (a.dt_bias != nullptr) {
     gdn_layer_ragged_kernel<true><<<grid, 256, 0, stream>>>(a);
