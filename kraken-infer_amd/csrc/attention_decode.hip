@@ -1170,8 +1170,10 @@ hipError_t dispatch_kv(const DecodeParams& p, uint32_t d, uint32_t g, bool tuned
 }  // namespace
 
 // Few splits (chunked prefill): one thread per (token, head, 4 dims) with all of
-// its <= S partial loads in flight (clamped indices, masked), no LDS.
-template <int S>
+// its <= S partial loads in flight (clamped indices, masked), no LDS.  With
+// kF16 the partials are each split's o / l in f16 (the flash kernel's), scaled
+// back by l before the same weighted sum.
+template <int S, bool kF16>
 __global__ __launch_bounds__(256) void attention_merge_narrow(CombineArgs p) {
   const uint32_t chunks = p.head_dim / 4;
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -1197,7 +1199,19 @@ __global__ __launch_bounds__(256) void attention_merge_narrow(CombineArgs p) {
     const size_t unit = (base * p.splits + s) * group + g;
     mv[j] = p.partial_ml[unit * 2];
     lv[j] = p.partial_ml[unit * 2 + 1];
-    ov[j] = *reinterpret_cast<const float4*>(p.partial_o + unit * p.head_dim + chunk * 4);
+    if constexpr (kF16) {
+      const half4_t h = *reinterpret_cast<const half4_t*>(
+        reinterpret_cast<const half_t*>(p.partial_o) + unit * p.head_dim + chunk * 4);
+      ov[j] = make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+    } else {
+      ov[j] = *reinterpret_cast<const float4*>(p.partial_o + unit * p.head_dim + chunk * 4);
+    }
+  }
+  if constexpr (kF16) {
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      ov[j] = make_float4(ov[j].x * lv[j], ov[j].y * lv[j], ov[j].z * lv[j], ov[j].w * lv[j]);
+    }
   }
   float mx = -INFINITY;
 #pragma unroll
@@ -1292,15 +1306,26 @@ hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream) {
   if (c.splits > kMaxSplits || c.head_dim % kMergeDims != 0) {
     return hipErrorInvalidValue;
   }
+  if (c.partial_f16 != 0 && c.splits > 16) {
+    return hipErrorInvalidValue;
+  }
   if (c.splits <= 16) {
     const size_t threads = (size_t)c.tokens * c.heads * (c.head_dim / 4);
     const dim3 grid((uint32_t)((threads + 255) / 256));
-    if (c.splits <= 4) {
-      attention_merge_narrow<4><<<grid, 256, 0, stream>>>(c);
+    if (c.partial_f16 != 0) {
+      if (c.splits <= 4) {
+        attention_merge_narrow<4, true><<<grid, 256, 0, stream>>>(c);
+      } else if (c.splits <= 8) {
+        attention_merge_narrow<8, true><<<grid, 256, 0, stream>>>(c);
+      } else {
+        attention_merge_narrow<16, true><<<grid, 256, 0, stream>>>(c);
+      }
+    } else if (c.splits <= 4) {
+      attention_merge_narrow<4, false><<<grid, 256, 0, stream>>>(c);
     } else if (c.splits <= 8) {
-      attention_merge_narrow<8><<<grid, 256, 0, stream>>>(c);
+      attention_merge_narrow<8, false><<<grid, 256, 0, stream>>>(c);
     } else {
-      attention_merge_narrow<16><<<grid, 256, 0, stream>>>(c);
+      attention_merge_narrow<16, false><<<grid, 256, 0, stream>>>(c);
     }
     return hipGetLastError();
   }

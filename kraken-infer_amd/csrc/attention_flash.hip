@@ -45,7 +45,7 @@
 //    folded into the exp2 argument; a query's reference max moves (and O, l are
 //    rescaled) only when a tile's max exceeds it by more than 8, so P <= 2^8.
 //  * Tiles wholly inside every query's causal window skip the masking.
-//  * Key splits (when the grid would not fill the chip) write (m, l, O) partials
+//  * Key splits (when the grid would not fill the chip) write (m, l, O / l) partials
 //    in the decode path's layout; the decode combine pass merges them.  The
 //    workgroup order is XCD-aware: the dispatcher deals workgroup i to XCD i % 8,
 //    so work items are renumbered to give each XCD a contiguous run of
@@ -91,7 +91,7 @@ struct FlashParams {
   const half_t* value_cache;
   const float* gate;
   float* output;
-  float* partial_o;   // [tokens][kv_heads][splits][G][D]
+  half_t* partial_o;  // [tokens][kv_heads][splits][G][D]: each split's o / l in f16
   float* partial_ml;  // [tokens][kv_heads][splits][G][2]
   uint32_t layer, start_position, tokens, capacity_tokens, heads, kv_heads;
   uint32_t key_count, keys_per_split, splits, q_tiles, head_groups;
@@ -691,15 +691,21 @@ void flash256_kernel(FlashParams p) {
       }
     }
   } else {
+    // The split's o / l in f16 (its values are a weighted average of V rows,
+    // so within V's range); the merge scales it back by l.
     const size_t base = (((size_t)token * p.kv_heads + kvh) * p.splits + split) * G + g_in_group;
-    float* po = p.partial_o + base * kD;
+    half_t* po = p.partial_o + base * kD;
+    const float inv = l == 0.0f ? 0.0f : 1.0f / l;
 #pragma unroll
     for (int dt = 0; dt < kD / 32; ++dt) {
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int d = dt * 32 + r4 * 8 + h * 4;
-        *reinterpret_cast<float4*>(po + d) =
-          make_float4(o[dt][r4 * 4 + 0], o[dt][r4 * 4 + 1], o[dt][r4 * 4 + 2], o[dt][r4 * 4 + 3]);
+        const half4_t v = {static_cast<half_t>(o[dt][r4 * 4 + 0] * inv),
+                           static_cast<half_t>(o[dt][r4 * 4 + 1] * inv),
+                           static_cast<half_t>(o[dt][r4 * 4 + 2] * inv),
+                           static_cast<half_t>(o[dt][r4 * 4 + 3] * inv)};
+        *reinterpret_cast<half4_t*>(po + d) = v;
       }
     }
     if (h == 0) {
@@ -739,6 +745,10 @@ FlashPlan plan_flash(const AttentionArgs& a, int cu_count) {
       splits = (uint64_t)v;
     }
   }
+  // The f16 partials' merge takes at most 16 splits.
+  if (splits > 16) {
+    splits = 16;
+  }
   if (splits < 1) {
     splits = 1;
   }
@@ -771,13 +781,16 @@ bool flash_prefill_supported(const AttentionArgs& a) {
          (a.gate == nullptr || ((uintptr_t)a.gate & 15u) == 0);
 }
 
+// Workspace: the f16 partial outputs, then (256-byte aligned) the f32 (m, l).
+size_t partial_ml_offset(size_t units) { return (units * kD * sizeof(half_t) + 255u) / 256u * 256u; }
+
 size_t attention_flash_workspace_bytes(const AttentionArgs& a, int cu_count) {
   const FlashPlan plan = plan_flash(a, cu_count);
   if (plan.splits <= 1) {
     return 0;
   }
   const size_t units = (size_t)a.tokens * a.heads * plan.splits;
-  return units * (kD + 2) * sizeof(float);
+  return partial_ml_offset(units) + units * 2 * sizeof(float);
 }
 
 hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* workspace,
@@ -807,13 +820,13 @@ hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* wo
   p.scale_log2 = (1.0f / sqrtf(256.0f)) * kLog2e;
   if (plan.splits > 1) {
     const size_t units = (size_t)a.tokens * a.heads * plan.splits;
-    if (workspace == nullptr ||
-        workspace_bytes < units * (kD + 2) * sizeof(float)) {
+    if (workspace == nullptr || plan.splits > 16 ||
+        workspace_bytes < partial_ml_offset(units) + units * 2 * sizeof(float)) {
       return hipErrorInvalidValue;
     }
-    // Partials follow the counter region, which they must never overlap.
-    p.partial_o = static_cast<float*>(workspace);
-    p.partial_ml = p.partial_o + units * kD;
+    p.partial_o = static_cast<half_t*>(workspace);
+    p.partial_ml =
+      reinterpret_cast<float*>(static_cast<char*>(workspace) + partial_ml_offset(units));
   }
   const uint32_t g = a.heads / a.kv_heads;
   hipError_t e;
@@ -828,8 +841,9 @@ hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* wo
     return e;
   }
   CombineArgs cmb{};
-  cmb.partial_o = p.partial_o;
+  cmb.partial_o = reinterpret_cast<const float*>(p.partial_o);
   cmb.partial_ml = p.partial_ml;
+  cmb.partial_f16 = 1u;
   cmb.gate = a.gate;
   cmb.output = a.output;
   cmb.tokens = a.tokens;

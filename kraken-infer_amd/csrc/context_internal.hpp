@@ -151,8 +151,11 @@ hipError_t launch_attention_decode(const AttentionArgs& a, int cu_count, void* w
 // applying the optional sigmoid gate.  Partials are laid out
 // [tokens][kv_heads][splits][group][head_dim] (ml: [...][group][2]).
 struct CombineArgs {
+  // Partial outputs: f32 sums (o, with its max and denominator in partial_ml),
+  // or, with partial_f16, each split's o / l rounded to f16 (at most 16 splits).
   const float* partial_o;
   const float* partial_ml;
+  uint32_t partial_f16;
   const float* gate;
   float* output;
   uint32_t tokens, heads, kv_heads, splits, head_dim;

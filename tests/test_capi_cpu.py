@@ -438,5 +438,5 @@ def test_no_alloc_attention_limits_its_scratch(vctx):
             assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED)
         else:
             assert code == kh.INVALID_ARGUMENT
-            assert msg == ("HIP gated F16 KV batched attention needs 33816576 bytes of split "
+            assert msg == ("HIP gated F16 KV batched attention needs 17039360 bytes of split "
                            "partials; the allocation-free entry point has 8388608")
