@@ -37,6 +37,7 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 (vector + MFMA)
 MALL_BYTES = 256 << 20
 HQ, HKV, D = 8, 2, 256
 METRIC = "decode attn HBM GB/s & prefill TFLOP/s (% roofline), GDN tok/s, 1 GPU"
@@ -148,18 +149,18 @@ def bench_prefill(torch, ctx, run, prefix, reps, warmup, gen):
     ctx.mrope_f32_in_place(k, pos_k, cap, HKV, D, 64, 11, 11, 10, 0, 1e7)
     ctx.l2_norm_f32_in_place(q, tokens * HQ, D, 1e-6)
     ctx.l2_norm_f32_in_place(k, cap * HKV, D, 1e-6)
-    q = q.half().float()
-    kc, vc = k.half(), v.half()
+    # C2's inputs are fp16: the f16-query entry reads them as they are.
+    q16, kc, vc = q.half(), k.half(), v.half()
     out = torch.empty(tokens * HQ * D, device=dev)
-    step = lambda: ctx.attention_f32_batched_f16_kv(q, kc, vc, 0, prefix, tokens, cap, HQ, HKV,
-                                                    D, out)
+    step = lambda: ctx.attention_f16q_batched_f16_kv(q16, kc, vc, 0, prefix, tokens, cap, HQ,
+                                                     HKV, D, out)
     ms, graph = run.time([step] * reps, warmup)
     del graph
     flops = prefill_flops(tokens, prefix)
     tflops = flops / (ms * 1e-3) / 1e12
     return {"prefix": prefix, "tokens": tokens, "ms_per_chunk": ms, "TFLOP_s": tflops,
             "frac_fp16_mfma_peak": tflops / FP16_PEAK_TFLOPS, "tok_s": tokens / (ms * 1e-3),
-            "gflop": flops / 1e9}
+            "gflop": flops / 1e9, "query": "f16 (kraken_hip_attention_f16q_batched_f16_kv)"}
 
 
 def bench_gdn(torch, ctx, run, gen):
@@ -185,8 +186,12 @@ def bench_gdn(torch, ctx, run, gen):
                                                                hv, d, out)
     ms, graph = run.time([step] * 4, 1)
     del graph
+    gflops = 1.835e6 * t / (ms * 1e-3) / 1e9
     res["prefill"] = {"tokens_per_chunk": t, "ms_per_chunk": ms, "tok_s": t / (ms * 1e-3),
-                      "gflop_s_recurrent_equiv": 1.835e6 * t / (ms * 1e-3) / 1e9}
+                      "gflop_s_recurrent_equiv": gflops,
+                      "frac_fp32_peak": gflops / (FP32_PEAK_TFLOPS * 1e3),
+                      "arithmetic": "split-fp16 MFMA: each f32 operand as an f16 hi/lo pair, "
+                                    "three f16 products accumulated in f32"}
 
     # Decode: one token per step, cold over rotating state sets (>512 MB).
     sets = 512

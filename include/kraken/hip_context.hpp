@@ -259,6 +259,16 @@ class HipContext {
       ctx_, query.raw(), key_cache.raw(), value_cache.raw(), layer, start_position, tokens,
       capacity_tokens, heads, kv_heads, head_dim, output.raw()));
   }
+  // attention_f32_batched_f16_kv with an f16 query (no reference counterpart).
+  [[nodiscard]] Status attention_f16q_batched_f16_kv(
+    const HipBuffer& query, const HipBuffer& key_cache, const HipBuffer& value_cache,
+    std::size_t layer, std::size_t start_position, std::size_t tokens,
+    std::size_t capacity_tokens, std::size_t heads, std::size_t kv_heads,
+    std::size_t head_dim, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_attention_f16q_batched_f16_kv(
+      ctx_, query.raw(), key_cache.raw(), value_cache.raw(), layer, start_position, tokens,
+      capacity_tokens, heads, kv_heads, head_dim, output.raw()));
+  }
   [[nodiscard]] Status attention_f32_batched(
     const HipBuffer& query, const HipBuffer& key_cache, const HipBuffer& value_cache,
     std::size_t layer, std::size_t start_position, std::size_t tokens,

@@ -158,6 +158,20 @@ KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv(
   size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim,
   kraken_buffer output);
 
+/* attention_f32_batched_f16_kv with an f16 query: query holds f16 values
+ * [tokens][heads][head_dim].  No single MpsContext method corresponds: the
+ * reference's flash path rounds its f32 query to f16 on load
+ * (mps_backend.mm:3458-3461), and this entry takes queries that are f16
+ * already (the C2 prefill inputs are fp16), so the flash kernel reads half the
+ * query bytes.  Same checks (the query sized in f16 values), dispatch and
+ * results as the f32 entry given the same values; the decode path converts the
+ * query to f32 first. */
+KRAKEN_API int kraken_hip_attention_f16q_batched_f16_kv(
+  kraken_hip_context* context, kraken_buffer query, kraken_buffer key_cache,
+  kraken_buffer value_cache, size_t layer, size_t start_position, size_t tokens,
+  size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+  kraken_buffer output);
+
 /* MpsContext::attention_f32_batched (mps_backend.hpp:404-414; F32 KV twin,
  * mps_backend.mm:2879-2941): same contract with an f32 cache. */
 KRAKEN_API int kraken_hip_attention_f32_batched(

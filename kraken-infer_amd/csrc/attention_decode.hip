@@ -1167,6 +1167,15 @@ hipError_t dispatch_kv(const DecodeParams& p, uint32_t d, uint32_t g, bool tuned
   return hipGetLastError();
 }
 
+// Widens an f16 query for the decode kernels (exact: every f16 is an f32).
+__global__ __launch_bounds__(256) void f16_to_f32_kernel(const half_t* in, float* out,
+                                                         uint64_t count) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i < count) {
+    out[i] = static_cast<float>(in[i]);
+  }
+}
+
 }  // namespace
 
 // Few splits (chunked prefill): one thread per (token, head, 4 dims) with all of
@@ -1416,6 +1425,15 @@ hipError_t launch_attention_decode(const AttentionArgs& a, int cu_count, void* w
   }
   return a.kv_f16 ? dispatch_kv<half_t>(p, a.head_dim, g, tuned, stream)
                   : dispatch_kv<float>(p, a.head_dim, g, tuned, stream);
+}
+
+hipError_t launch_f16_to_f32(const void* in, float* out, size_t count, hipStream_t stream) {
+  if (count == 0) {
+    return hipSuccess;
+  }
+  f16_to_f32_kernel<<<dim3((uint32_t)((count + 255u) / 256u)), 256, 0, stream>>>(
+    static_cast<const half_t*>(in), out, (uint64_t)count);
+  return hipGetLastError();
 }
 
 }  // namespace kraken

@@ -87,6 +87,7 @@ constexpr float kRescaleSlack = 8.0f;  // log2 headroom before O is rescaled
 
 struct FlashParams {
   const float* query;
+  const half_t* query_f16;  // set: the query is f16 (read instead of query)
   const half_t* key_cache;
   const half_t* value_cache;
   const float* gate;
@@ -245,7 +246,7 @@ __device__ __forceinline__ void wait_copies_but() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
-template <int GW>
+template <int GW, bool kQF16>
 __global__ __launch_bounds__(64 * GW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flash256_kernel(FlashParams p) {
   // K and V tiles, two stages each (128 KB).
@@ -345,21 +346,39 @@ void flash256_kernel(FlashParams p) {
     half_t* stage = wave < 2 ? s_q + wave * (kQTile * kRowHalfs)
                              : s_v + kTileHalfs + (wave - 2) * (kQTile * kRowHalfs);
     // Unconditional loads from a valid row (token 0 stands in for tokens past the
-    // end), zeroed afterwards, so all 32 loads are in flight together.
-    float4 rows[kQTile];
+    // end), zeroed afterwards, so all 32 loads are in flight together.  An f16
+    // query is read as it is (8 bytes per lane of a 512-byte row).
+    if constexpr (kQF16) {
+      half4_t rows[kQTile];
 #pragma unroll
-    for (int r = 0; r < kQTile; ++r) {
-      const uint32_t tok = t0 + (uint32_t)r < p.tokens ? t0 + (uint32_t)r : 0u;
-      const float* qrow = p.query + ((size_t)tok * p.heads + head) * kD;
-      rows[r] = *reinterpret_cast<const float4*>(qrow + 4 * lane);
-    }
+      for (int r = 0; r < kQTile; ++r) {
+        const uint32_t tok = t0 + (uint32_t)r < p.tokens ? t0 + (uint32_t)r : 0u;
+        const half_t* qrow = p.query_f16 + ((size_t)tok * p.heads + head) * kD;
+        rows[r] = *reinterpret_cast<const half4_t*>(qrow + 4 * lane);
+      }
 #pragma unroll
-    for (int r = 0; r < kQTile; ++r) {
-      const float qmask = t0 + (uint32_t)r < p.tokens ? 1.0f : 0.0f;
-      const half4_t hv = {(half_t)(rows[r].x * qmask), (half_t)(rows[r].y * qmask),
-                          (half_t)(rows[r].z * qmask), (half_t)(rows[r].w * qmask)};
-      const int chunk = (lane >> 1) ^ (r & 15);
-      *reinterpret_cast<half4_t*>(stage + r * kRowHalfs + chunk * 8 + (lane & 1) * 4) = hv;
+      for (int r = 0; r < kQTile; ++r) {
+        const half4_t zero = {0, 0, 0, 0};
+        const half4_t hv = t0 + (uint32_t)r < p.tokens ? rows[r] : zero;
+        const int chunk = (lane >> 1) ^ (r & 15);
+        *reinterpret_cast<half4_t*>(stage + r * kRowHalfs + chunk * 8 + (lane & 1) * 4) = hv;
+      }
+    } else {
+      float4 rows[kQTile];
+#pragma unroll
+      for (int r = 0; r < kQTile; ++r) {
+        const uint32_t tok = t0 + (uint32_t)r < p.tokens ? t0 + (uint32_t)r : 0u;
+        const float* qrow = p.query + ((size_t)tok * p.heads + head) * kD;
+        rows[r] = *reinterpret_cast<const float4*>(qrow + 4 * lane);
+      }
+#pragma unroll
+      for (int r = 0; r < kQTile; ++r) {
+        const float qmask = t0 + (uint32_t)r < p.tokens ? 1.0f : 0.0f;
+        const half4_t hv = {(half_t)(rows[r].x * qmask), (half_t)(rows[r].y * qmask),
+                            (half_t)(rows[r].z * qmask), (half_t)(rows[r].w * qmask)};
+        const int chunk = (lane >> 1) ^ (r & 15);
+        *reinterpret_cast<half4_t*>(stage + r * kRowHalfs + chunk * 8 + (lane & 1) * 4) = hv;
+      }
     }
 #pragma unroll
     for (int step = 0; step < kD / 16; ++step) {
@@ -762,7 +781,11 @@ FlashPlan plan_flash(const AttentionArgs& a, int cu_count) {
 template <int GW>
 hipError_t launch_g(const FlashParams& p, hipStream_t stream) {
   const dim3 grid(p.q_tiles * p.kv_heads * p.head_groups * p.splits);
-  flash256_kernel<GW><<<grid, 64 * GW, 0, stream>>>(p);
+  if (p.query_f16 != nullptr) {
+    flash256_kernel<GW, true><<<grid, 64 * GW, 0, stream>>>(p);
+  } else {
+    flash256_kernel<GW, false><<<grid, 64 * GW, 0, stream>>>(p);
+  }
   return hipGetLastError();
 }
 
@@ -798,6 +821,7 @@ hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* wo
   const FlashPlan plan = plan_flash(a, cu_count);
   FlashParams p{};
   p.query = a.query;
+  p.query_f16 = static_cast<const half_t*>(a.query_f16);
   p.key_cache = static_cast<const half_t*>(a.key_cache);
   p.value_cache = static_cast<const half_t*>(a.value_cache);
   p.gate = a.gate;

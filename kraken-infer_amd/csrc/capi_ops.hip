@@ -38,7 +38,7 @@ int attention_entry(kraken_hip_context* ctx, const char* what, bool kv_f16,
                     const kraken_buffer& value_cache, const kraken_buffer* gate, size_t layer,
                     size_t start_position, size_t tokens, size_t capacity_tokens, size_t heads,
                     size_t kv_heads, size_t head_dim, const kraken_buffer& output,
-                    bool no_alloc = false) {
+                    bool no_alloc = false, bool query_f16 = false) {
   KRAKEN_TRY(check_context(ctx));
   const std::string w = std::string("HIP ") + what;
   if (tokens == 0 || heads == 0 || kv_heads == 0 || head_dim == 0 || capacity_tokens == 0) {
@@ -66,7 +66,8 @@ int attention_entry(kraken_hip_context* ctx, const char* what, bool kv_f16,
   const std::string nv = std::string(what) + " value cache";
   const std::string ng = std::string(what) + " gate";
   const std::string no = std::string(what) + " output";
-  KRAKEN_TRY(validate_f32(query, query_values, nq.c_str()));
+  KRAKEN_TRY(validate_buffer(query, query_values, query_f16 ? sizeof(uint16_t) : sizeof(float),
+                             nq.c_str()));
   const size_t elem = kv_f16 ? sizeof(uint16_t) : sizeof(float);
   KRAKEN_TRY(validate_buffer(key_cache, cache_values, elem, nk.c_str()));
   KRAKEN_TRY(validate_buffer(value_cache, cache_values, elem, nv.c_str()));
@@ -113,8 +114,20 @@ int attention_entry(kraken_hip_context* ctx, const char* what, bool kv_f16,
   const bool use_flash = flash_ok && choice != FlashChoice::force_off &&
                          (choice == FlashChoice::force_on || tokens >= 64u);
 
-  const size_t need = use_flash ? attention_flash_workspace_bytes(a, ctx->cu_count)
-                                : attention_decode_workspace_bytes(a, ctx->cu_count);
+  // An f16 query feeds the flash kernel as it is; the decode kernels read f32,
+  // so that path widens it (exactly) into the workspace past the split partials.
+  size_t need = use_flash ? attention_flash_workspace_bytes(a, ctx->cu_count)
+                          : attention_decode_workspace_bytes(a, ctx->cu_count);
+  size_t query_offset = 0;
+  if (query_f16) {
+    if (use_flash) {
+      a.query = nullptr;
+      a.query_f16 = query.data;
+    } else {
+      query_offset = (need + 255u) & ~size_t{255};
+      need = query_offset + query_values * sizeof(float);
+    }
+  }
   if (no_alloc && need > kNoAllocScratchBytes) {
     return invalid(w + " needs " + std::to_string(need) +
                    " bytes of split partials; the allocation-free entry point has " +
@@ -132,6 +145,15 @@ int attention_entry(kraken_hip_context* ctx, const char* what, bool kv_f16,
     KRAKEN_TRY(ensure_workspace(ctx, need));
     workspace = ctx->workspace;
     workspace_bytes = ctx->workspace_bytes;
+  }
+  if (query_f16 && !use_flash) {
+    float* q32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + query_offset);
+    const hipError_t ec = launch_f16_to_f32(query.data, q32, query_values, ctx->stream);
+    if (ec != hipSuccess) {
+      return internal(w + " launch failed: " + hipGetErrorString(ec));
+    }
+    a.query = q32;
+    workspace_bytes = query_offset;
   }
   const hipError_t e =
     use_flash ? launch_attention_flash(a, ctx->cu_count, workspace, workspace_bytes, ctx->stream)
@@ -359,6 +381,18 @@ KRAKEN_API int kraken_hip_attention_f32_batched_f16_kv(
   return attention_entry(ctx, "F16 KV batched attention", true, query, key_cache, value_cache,
                          nullptr, layer, start_position, tokens, capacity_tokens, heads,
                          kv_heads, head_dim, output);
+}
+
+// No single counterpart in the reference: attention_f32_batched_f16_kv
+// (mps_backend.mm:10619-10869) given a query that is f16 already.
+KRAKEN_API int kraken_hip_attention_f16q_batched_f16_kv(
+  kraken_hip_context* ctx, kraken_buffer query, kraken_buffer key_cache,
+  kraken_buffer value_cache, size_t layer, size_t start_position, size_t tokens,
+  size_t capacity_tokens, size_t heads, size_t kv_heads, size_t head_dim, kraken_buffer output) {
+  return attention_entry(ctx, "F16 query F16 KV batched attention", true, query, key_cache,
+                         value_cache, nullptr, layer, start_position, tokens, capacity_tokens,
+                         heads, kv_heads, head_dim, output, /*no_alloc=*/false,
+                         /*query_f16=*/true);
 }
 
 KRAKEN_API int kraken_hip_attention_f32_batched(

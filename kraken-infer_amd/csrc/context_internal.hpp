@@ -126,6 +126,8 @@ int strided_region_end(size_t offset, size_t rows, size_t stride, size_t row_siz
 
 struct AttentionArgs {
   const float* query;
+  // f16 query [tokens][heads][head_dim] for the flash path (query unused then).
+  const void* query_f16 = nullptr;
   const void* key_cache;
   const void* value_cache;
   const float* gate;  // nullable: fused sigmoid output gate
@@ -167,6 +169,8 @@ struct CombineArgs {
   uint32_t start_position, keys_per_split;
 };
 hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream);
+// out[i] = (float)in[i] for i < count (f16 -> f32, exact).
+hipError_t launch_f16_to_f32(const void* in, float* out, size_t count, hipStream_t stream);
 // True when the flash MFMA prefill kernel supports these arguments.
 bool flash_prefill_supported(const AttentionArgs& a);
 size_t attention_flash_workspace_bytes(const AttentionArgs& a, int cu_count);

@@ -47,6 +47,7 @@ _ctx = ctypes.c_void_p
 # name -> argument types after the context pointer (all return int).
 SIGNATURES = {
     "kraken_hip_attention_f32_batched_f16_kv": [_B, _B, _B] + [_sz] * 7 + [_B],
+    "kraken_hip_attention_f16q_batched_f16_kv": [_B, _B, _B] + [_sz] * 7 + [_B],
     "kraken_hip_attention_f32_batched": [_B, _B, _B] + [_sz] * 7 + [_B],
     "kraken_hip_attention_f32_batched_f16_kv_gated": [_B, _B, _B, _B] + [_sz] * 7 + [_B],
     "kraken_hip_attention_f32_batched_f16_kv_gated_no_alloc": [_B, _B, _B, _B] + [_sz] * 7

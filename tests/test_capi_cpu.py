@@ -172,6 +172,18 @@ def test_f32_kv_twin_validates_f32_cache_sizes(vctx):
     assert code == kh.INVALID_ARGUMENT and "key cache buffer is too small" in msg
 
 
+def test_f16_query_entry_validates_the_query_in_f16_values(vctx):
+    # The query is sized in 2-byte values; every other check is the F16 KV entry's.
+    args = attn_args(tokens=1024, start=7168, cap=8192, q_bytes=2 * 1024 * 8 * 256)
+    code, msg = status(vctx, "attention_f16q_batched_f16_kv", *args)
+    assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED)
+    args = attn_args(tokens=1024, start=7168, cap=8192, q_bytes=2 * 1024 * 8 * 256 - 2)
+    code, msg = status(vctx, "attention_f16q_batched_f16_kv", *args)
+    assert code == kh.INVALID_ARGUMENT and "F16 query F16 KV batched attention query buffer is too small" in msg
+    code, msg = status(vctx, "attention_f16q_batched_f16_kv", *attn_args(start=4097, q_bytes=4096))
+    assert code == kh.INVALID_ARGUMENT and "exceeds KV cache capacity" in msg
+
+
 def test_gated_attention_validates_gate(vctx):
     q, k, v, *rest = attn_args()
     code, msg = status(vctx, "attention_f32_batched_f16_kv_gated", q, k, v, fake(8), *rest)

@@ -420,6 +420,34 @@ def test_flash_sharp_softmax_and_split_counts(hip_ctx, q_scale, splits, monkeypa
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("shape", [
+    # tokens, start, heads, kv_heads: flash at C2's P=3072 and unaligned, then
+    # the decode kernels (short chunk, single token)
+    (1024, 3072, 8, 2), (100, 37, 8, 2), (7, 300, 8, 2), (1, 4096, 8, 2),
+])
+def test_f16_query_entry_equals_f32_entry(hip_ctx, shape):
+    """kraken_hip_attention_f16q_batched_f16_kv on f16 query values gives the f32
+    entry's output bit for bit on the same (f16-representable) values: the flash
+    kernel reads the f16 row instead of rounding the f32 one, the decode kernels
+    read the exact widening."""
+    tokens, start, heads, kv_heads = shape
+    d = 256
+    cap = start + tokens
+    print(f"f16 query entry {shape}", flush=True)
+    q, kc, vc = make_case(31, tokens, start, cap, heads, kv_heads, d)
+    q16 = q.astype(np.float16)
+    want = run_hip(hip_ctx, q16.astype(np.float32), kc, vc, 0, start, tokens, cap, heads,
+                   kv_heads, d)
+    qb = hip_ctx.buffer(q16.view(np.uint16), dtype=np.uint16)
+    kb, vb = hip_ctx.buffer(kc, dtype=np.uint16), hip_ctx.buffer(vc, dtype=np.uint16)
+    out = hip_ctx.buffer(byte_size=4 * tokens * heads * d)
+    hip_ctx.attention_f16q_batched_f16_kv(qb, kb, vb, 0, start, tokens, cap, heads, kv_heads,
+                                          d, out)
+    got = out.download(tokens * heads * d)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), shape
+
+
+@pytest.mark.gpu
 def test_flash_gated(hip_ctx):
     tokens, start, heads, kv_heads, d = 128, 200, 8, 2, 256
     cap = start + tokens
