@@ -256,6 +256,59 @@ def test_decode_graph_replays(hip_ctx):
 
 
 @pytest.mark.gpu
+def test_flash_graph_replays(hip_ctx):
+    """Two split flash prefill calls (flash launch, then the merge launch) captured
+    in one HIP graph and replayed three times with a new query before each replay
+    and eager calls in between: every replay gives the eager call's bits."""
+    torch = pytest.importorskip("torch")
+    heads, kv_heads, d = 8, 2, 256
+    calls = [(128, 1000), (1024, 3072)]  # tokens, start
+    cap = 4096
+    rng = np.random.default_rng(52)
+    dev = "cuda"
+    kt = torch.from_numpy(f16_bits(rng.standard_normal(cap * kv_heads * d)).view(np.float16)).to(dev)
+    vt = torch.from_numpy(f16_bits(rng.standard_normal(cap * kv_heads * d)).view(np.float16)).to(dev)
+    qts = [torch.zeros(t * heads * d, device=dev) for t, _ in calls]
+    outs = [torch.zeros(t * heads * d, device=dev) for t, _ in calls]
+    eager = [torch.zeros(t * heads * d, device=dev) for t, _ in calls]
+    stream = torch.cuda.Stream()
+    hip_ctx.set_stream(stream.cuda_stream)
+
+    def steps(dst):
+        for i, (t, start) in enumerate(calls):
+            hip_ctx.attention_f32_batched_f16_kv(qts[i], kt, vt, 0, start, t, cap, heads,
+                                                 kv_heads, d, dst[i])
+
+    try:
+        with torch.cuda.stream(stream):
+            steps(eager)
+            stream.synchronize()
+            hip_ctx.begin_graph()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                steps(outs)
+            hip_ctx.commit_graph()
+            for replay in range(3):
+                for i, (t, _) in enumerate(calls):
+                    q = rng.standard_normal(t * heads * d).astype(np.float32) * (1.0 + replay)
+                    qts[i].copy_(torch.from_numpy(q).to(dev))
+                torch.cuda.synchronize()
+                graph.replay()
+                stream.synchronize()
+                steps(eager)
+                stream.synchronize()
+                for i in range(len(calls)):
+                    got, want = outs[i].cpu().numpy(), eager[i].cpu().numpy()
+                    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+                        f"replay {replay} call {i}"
+                    outs[i].zero_()
+            del graph
+    finally:
+        hip_ctx.commit_graph()
+        hip_ctx.set_stream(None)
+
+
+@pytest.mark.gpu
 def test_workspace_growth_between_replays(hip_ctx):
     """A graph captured while the context's workspace was small keeps replaying
     correctly after an eager call has grown the workspace: the outgrown
