@@ -213,6 +213,17 @@ __device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t voffset, co
                : "memory", "m0");
 }
 
+// The same copy to a wave-uniform LDS byte address (no generic-to-LDS pointer
+// conversion per copy).
+__device__ __forceinline__ void copy16_to_lds_addr(i32x4_t rsrc, uint32_t voffset,
+                                                   uint32_t lds_address) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_address);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+
 // The same copy with the nontemporal hint, for data read once (a KV stream).
 __device__ __forceinline__ void copy16_to_lds_nt(i32x4_t rsrc, uint32_t voffset,
                                                  const half_t* lds) {

@@ -1005,12 +1005,33 @@ __global__ __launch_bounds__(256) void kq_dequant_rows_kernel(const uint8_t* wei
   }
 }
 
-// Weights dequantized and rounded to fp16 (RNE) for the MFMA GEMM, [rows][cols].
+// Eight f32 values rounded to fp16 (RNE), group i of in -> out.
+__device__ __forceinline__ void f32_to_f16_8(const float* in, half_t* out, uint64_t i) {
+  const float4 a = reinterpret_cast<const float4*>(in)[2 * i];
+  const float4 b = reinterpret_cast<const float4*>(in)[2 * i + 1];
+  const half8_t h = {static_cast<half_t>(a.x), static_cast<half_t>(a.y), static_cast<half_t>(a.z),
+                     static_cast<half_t>(a.w), static_cast<half_t>(b.x), static_cast<half_t>(b.y),
+                     static_cast<half_t>(b.z), static_cast<half_t>(b.w)};
+  reinterpret_cast<half8_t*>(out)[i] = h;
+}
+
+// The two-pass GEMM's first pass, one launch: workgroups [0, convert_blocks)
+// round the f32 inputs to fp16 (n8 groups of eight), the rest dequantize the
+// weights and round them to fp16 (RNE), [rows][cols].
 template <int F>
 __global__ __launch_bounds__(256) void kq_dequant_f16_kernel(const uint8_t* weight, uint32_t rows,
                                                              uint32_t blocks_per_row,
-                                                             half_t* out) {
-  const uint64_t id = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+                                                             half_t* out, const float* xin,
+                                                             half_t* x16, uint64_t n8,
+                                                             uint32_t convert_blocks) {
+  if (blockIdx.x < convert_blocks) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i < n8) {
+      f32_to_f16_8(xin, x16, i);
+    }
+    return;
+  }
+  const uint64_t id = (uint64_t)(blockIdx.x - convert_blocks) * 256u + threadIdx.x;
   const uint64_t chunks = (uint64_t)rows * blocks_per_row * 8u;
   if (id >= chunks) {
     return;
@@ -1033,19 +1054,6 @@ __global__ __launch_bounds__(256) void kq_dequant_f16_kernel(const uint8_t* weig
   }
 }
 
-__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* in, half_t* out,
-                                                         uint64_t n8) {
-  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-  if (i >= n8) {
-    return;
-  }
-  const float4 a = reinterpret_cast<const float4*>(in)[2 * i];
-  const float4 b = reinterpret_cast<const float4*>(in)[2 * i + 1];
-  const half8_t h = {static_cast<half_t>(a.x), static_cast<half_t>(a.y), static_cast<half_t>(a.z),
-                     static_cast<half_t>(a.w), static_cast<half_t>(b.x), static_cast<half_t>(b.y),
-                     static_cast<half_t>(b.z), static_cast<half_t>(b.w)};
-  reinterpret_cast<half8_t*>(out)[i] = h;
-}
 
 // ------------------------------------------------------------------ GEMM ----
 // C[t][r] = sum_k X[t][k] W[r][k] with X [M = tokens][K], W [N = rows][K] fp16
@@ -1053,10 +1061,15 @@ __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* in, half_t
 // waves (128 x 128, or 64 x 64 when the large tiles would leave most CUs
 // idle); wave w owns tokens TM/2 (w / 2) .. + TM/2 - 1 and rows TN/2 (w % 2)
 // .. + TN/2 - 1 as (TM/64) x (TN/64) tiles of v_mfma_f32_32x32x16_f16.  K
-// steps of 64 through two LDS stages; a 16-byte chunk j of tile row i lives at
-// chunk j ^ (i & 7), so the fragment reads (32 rows, one chunk each) hit
-// distinct banks.
+// steps of 64 through two LDS stages; a 16-byte chunk j of tile row i (128
+// bytes) lives at chunk j ^ gemm_swizzle(i).  A ds_read_b128 is served 16
+// lanes at a time from 64 four-byte banks (256 bytes), so the 16 rows one
+// fragment read visits (consecutive i, one chunk each) must cover all 16
+// 16-byte bank groups: row i starts at group 8 (i & 1), and (i >> 1) & 7 gives
+// the even and the odd rows eight distinct chunks each.  (j ^ (i & 7) put rows
+// i and i + 8 on the same banks.)
 constexpr int kGK = 64;
+__device__ __forceinline__ int gemm_swizzle(int row) { return (row >> 1) & 7; }
 typedef float float16v_t __attribute__((ext_vector_type(16)));
 
 template <int TM, int TN>
@@ -1104,14 +1117,14 @@ __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const
     for (int i = 0; i < LA; ++i) {
       const int idx = tid + 256 * i;
       const int row = idx >> 3;
-      const int chunk = (idx & 7) ^ (row & 7);
+      const int chunk = (idx & 7) ^ gemm_swizzle(row);
       *reinterpret_cast<u32x4_t*>(&s_a[st][row * kGK + 8 * chunk]) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
       const int idx = tid + 256 * i;
       const int row = idx >> 3;
-      const int chunk = (idx & 7) ^ (row & 7);
+      const int chunk = (idx & 7) ^ gemm_swizzle(row);
       *reinterpret_cast<u32x4_t*>(&s_b[st][row * kGK + 8 * chunk]) = rb[i];
     }
   };
@@ -1150,13 +1163,13 @@ __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const
 #pragma unroll
       for (int i = 0; i < IA; ++i) {
         const int row = (TM / 2) * wm + 32 * i + frow;
-        const int chunk = (2 * ks + fk) ^ (row & 7);
+        const int chunk = (2 * ks + fk) ^ gemm_swizzle(row);
         fa[i] = *reinterpret_cast<const half8_t*>(&s_a[st][row * kGK + 8 * chunk]);
       }
 #pragma unroll
       for (int j = 0; j < JB; ++j) {
         const int row = (TN / 2) * wn + 32 * j + frow;
-        const int chunk = (2 * ks + fk) ^ (row & 7);
+        const int chunk = (2 * ks + fk) ^ gemm_swizzle(row);
         fb[j] = *reinterpret_cast<const half8_t*>(&s_b[st][row * kGK + 8 * chunk]);
       }
 #pragma unroll
@@ -1171,6 +1184,172 @@ __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const
       store_step(st ^ 1);
     }
     __syncthreads();
+  }
+  // D layout: lane l holds column (row of W) l % 32 and tokens
+  // 8 (e / 4) + 4 (l / 32) + e % 4 of its 32 x 32 tile.
+#pragma unroll
+  for (int i = 0; i < IA; ++i) {
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const uint32_t col = n0 + (TN / 2) * wn + 32u * j + (uint32_t)frow;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t row = m0 + (TM / 2) * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
+        if (row < m && col < n) {
+          c[(uint64_t)row * n + col] = acc[i][j][e];
+        }
+      }
+    }
+  }
+}
+
+// The same GEMM, pipelined: the operand tiles go global -> LDS with
+// direct-to-LDS copies (no staging registers) through NS stages, so the copies
+// of K step s + NS - 1 are issued while step s computes.  With one step of
+// prefetch the kernel above waits for each step's loads (a step of 16 MFMAs
+// per wave is shorter than a load's latency).  Tile 128 tokens x TN rows
+// (TN = 128: 4 stages of 32 KB; TN = 256: 3 stages of 48 KB, one workgroup per
+// CU either way); wave w owns tokens 64 (w / 2) .. + 63 and rows TN/2 (w % 2)
+// .. + TN/2 - 1.  The LDS layout (16-byte chunk j of tile row i at
+// j ^ gemm_swizzle(i)) and the MFMA order over K are those of gemm_f16_nt_kernel, so each output
+// gets the same bits; copy lane l of a wave fills LDS slot 64 c + l of its
+// share and so loads the logical chunk that slot holds.
+template <int TN>
+struct GemmPipe {
+  static constexpr int kTM = 128;
+  static constexpr int kStages = TN == 128 ? 4 : 3;
+  static constexpr int kStageHalfs = (kTM + TN) * kGK;
+  static constexpr int kCopiesA = kTM / 32;  // per wave per stage
+  static constexpr int kCopiesB = TN / 32;
+  static constexpr int kCopies = kCopiesA + kCopiesB;
+};
+
+template <int TN>
+__global__ __launch_bounds__(256) void gemm_f16_pipe_kernel(const half_t* x, const half_t* w,
+                                                            float* c, uint32_t m, uint32_t n,
+                                                            uint32_t k, uint32_t split_steps) {
+  using G = GemmPipe<TN>;
+  constexpr int TM = G::kTM;
+  constexpr int NS = G::kStages;
+  constexpr int IA = TM / 64;
+  constexpr int JB = TN / 64;
+  static_assert(NS * G::kStageHalfs * 2 <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) half_t s_ab[NS * G::kStageHalfs];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t m0 = blockIdx.y * TM;
+  const uint32_t n0 = blockIdx.x * TN;
+  // Range-checked operands: rows past the matrix read as zeros.
+  const i32x4_t xr = rsrc_words(x + (uint64_t)m0 * k,
+                                (uint32_t)min((uint64_t)TM, (uint64_t)(m - m0)) * k * 2u);
+  const i32x4_t wr = rsrc_words(w + (uint64_t)n0 * k,
+                                (uint32_t)min((uint64_t)TN, (uint64_t)(n - n0)) * k * 2u);
+  // Byte offset (at K step 0) of the chunk copy i of this lane moves: LDS slot
+  // P = 64 (kCopies_op * wave + i) + lane of the operand tile.
+  uint32_t voff_a[G::kCopiesA], voff_b[G::kCopiesB];
+#pragma unroll
+  for (int i = 0; i < G::kCopiesA; ++i) {
+    const uint32_t slot = 64u * (uint32_t)(G::kCopiesA * wave + i) + (uint32_t)lane;
+    const uint32_t row = slot >> 3;
+    voff_a[i] = (row * k + 8u * ((slot & 7u) ^ (uint32_t)gemm_swizzle((int)row))) * 2u;
+  }
+#pragma unroll
+  for (int i = 0; i < G::kCopiesB; ++i) {
+    const uint32_t slot = 64u * (uint32_t)(G::kCopiesB * wave + i) + (uint32_t)lane;
+    const uint32_t row = slot >> 3;
+    voff_b[i] = (row * k + 8u * ((slot & 7u) ^ (uint32_t)gemm_swizzle((int)row))) * 2u;
+  }
+  const uint32_t s_begin = blockIdx.z * split_steps;
+  const uint32_t total_steps = k / kGK;
+  const uint32_t steps = s_begin < total_steps ? min(total_steps - s_begin, split_steps) : 0u;
+  c += (uint64_t)blockIdx.z * m * n;
+  // LDS byte addresses of this wave's first A and B copy in stage 0.
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void_t*)s_ab;
+  const uint32_t lds_a = lds_base + (uint32_t)(G::kCopiesA * wave) * 1024u;
+  const uint32_t lds_b = lds_base + (uint32_t)(TM * kGK * 2) + (uint32_t)(G::kCopiesB * wave) * 1024u;
+  auto issue = [&](uint32_t step, int st) __attribute__((always_inline)) {
+    const uint32_t kb = (s_begin + step) * (uint32_t)kGK * 2u;
+    const uint32_t so = (uint32_t)st * (uint32_t)(G::kStageHalfs * 2);
+#pragma unroll
+    for (int i = 0; i < G::kCopiesA; ++i) {
+      copy16_to_lds_addr(xr, voff_a[i] + kb, lds_a + so + (uint32_t)i * 1024u);
+    }
+#pragma unroll
+    for (int i = 0; i < G::kCopiesB; ++i) {
+      copy16_to_lds_addr(wr, voff_b[i] + kb, lds_b + so + (uint32_t)i * 1024u);
+    }
+  };
+  float16v_t acc[IA][JB];
+#pragma unroll
+  for (int i = 0; i < IA; ++i) {
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        acc[i][j][e] = 0.0f;
+      }
+    }
+  }
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int frow = lane & 31;
+  const int fk = lane >> 5;
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st) {
+    if ((uint32_t)st < steps) {
+      issue((uint32_t)st, st);
+    }
+  }
+  for (uint32_t s = 0; s < steps; ++s) {
+    // Step s's copies are the oldest in flight; those of the NS - 2 steps after
+    // it may stay outstanding (loads complete in issue order).
+    if (s + (NS - 2) < steps) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * G::kCopies) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();  // step s is in LDS; every wave is done with step s - 1's stage
+    if (s + (NS - 1) < steps) {
+      issue(s + (NS - 1), (int)((s + (NS - 1)) % NS));
+    }
+    const half_t* sa = s_ab + (int)(s % NS) * G::kStageHalfs;
+    const half_t* sb = sa + TM * kGK;
+    // Fragments of substep ks + 1 are read while substep ks's MFMAs run.
+    half8_t fa[2][IA], fb[2][JB];
+    auto read_frags = [&](int ks, int slot) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < IA; ++i) {
+        const int row = (TM / 2) * wm + 32 * i + frow;
+        const int chunk = (2 * ks + fk) ^ gemm_swizzle(row);
+        fa[slot][i] = *reinterpret_cast<const half8_t*>(&sa[row * kGK + 8 * chunk]);
+      }
+#pragma unroll
+      for (int j = 0; j < JB; ++j) {
+        const int row = (TN / 2) * wn + 32 * j + frow;
+        const int chunk = (2 * ks + fk) ^ gemm_swizzle(row);
+        fb[slot][j] = *reinterpret_cast<const half8_t*>(&sb[row * kGK + 8 * chunk]);
+      }
+    };
+    read_frags(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < kGK / 16; ++ks) {
+      if (ks + 1 < kGK / 16) {
+        read_frags(ks + 1, (ks + 1) & 1);
+      }
+      // Keeps the reads ahead of the MFMAs (the scheduler would otherwise
+      // interleave them back to one set of fragment registers).
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < IA; ++i) {
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[ks & 1][i], fb[ks & 1][j],
+                                                            acc[i][j], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   // D layout: lane l holds column (row of W) l % 32 and tokens
   // 8 (e / 4) + 4 (l / 32) + e % 4 of its 32 x 32 tile.
@@ -1206,7 +1385,7 @@ __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const
 constexpr int kQK = 128;
 
 template <int F>
-__global__ __launch_bounds__(256) void gemm_kq_kernel(const half_t* x, const uint8_t* wq,
+__global__ __launch_bounds__(256) void gemm_kq_kernel(const float* x, const uint8_t* wq,
                                                       float* c, uint32_t m, uint32_t n,
                                                       uint32_t k, uint32_t split_steps) {
   constexpr int TM = 128;
@@ -1222,14 +1401,15 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(const half_t* x, const uin
   const uint32_t m0 = blockIdx.y * TM;
   const uint32_t n0 = blockIdx.x * TN;
   const uint32_t bpr = k / 256u;
+  // The f32 inputs, rounded to fp16 (RNE) on their way into LDS.
   const __amdgpu_buffer_rsrc_t xr =
-    make_buffer_rsrc(x + (uint64_t)m0 * k, (uint32_t)min((uint64_t)TM, (uint64_t)(m - m0)) * k * 2u);
+    make_buffer_rsrc(x + (uint64_t)m0 * k, (uint32_t)min((uint64_t)TM, (uint64_t)(m - m0)) * k * 4u);
   // This thread's B row (clamped to the matrix) and chunk pair.
   const uint32_t brow = (uint32_t)tid >> 1;
   const uint8_t* wrow =
     wq + (uint64_t)min(n0 + brow, n - 1u) * bpr * KqFormat<F>::kBytes;
   const uint32_t cpair = 2u * ((uint32_t)tid & 1u);
-  u32x4_t ra[LA];
+  float4 ra[LA][2];
   RawChunk rb[2];
   auto load_step = [&](uint32_t st) __attribute__((always_inline)) {
     const uint32_t kk = st * kQK;
@@ -1237,8 +1417,10 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(const half_t* x, const uin
     for (int i = 0; i < LA; ++i) {
       const int idx = tid + 256 * i;
       const uint32_t row = (uint32_t)(idx >> 4);
-      const uint32_t off = (row * k + kk + 8u * (uint32_t)(idx & 15)) * 2u;
-      ra[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
+      const uint32_t off = (row * k + kk + 8u * (uint32_t)(idx & 15)) * 4u;
+      ra[i][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
+      ra[i][1] = __builtin_bit_cast(float4,
+                                    __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off + 16, 0, 0));
     }
     const uint8_t* block = wrow + (uint64_t)(st >> 1) * KqFormat<F>::kBytes;
     const uint32_t c0 = 4u * (st & 1u) + cpair;
@@ -1251,7 +1433,13 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(const half_t* x, const uin
       const int idx = tid + 256 * i;
       const int row = idx >> 4;
       const int chunk = (idx & 15) ^ (row & 15);
-      *reinterpret_cast<u32x4_t*>(&s_a[stage][row * kQK + 8 * chunk]) = ra[i];
+      const float4 a = ra[i][0];
+      const float4 b = ra[i][1];
+      const half8_t h = {static_cast<half_t>(a.x), static_cast<half_t>(a.y),
+                         static_cast<half_t>(a.z), static_cast<half_t>(a.w),
+                         static_cast<half_t>(b.x), static_cast<half_t>(b.y),
+                         static_cast<half_t>(b.z), static_cast<half_t>(b.w)};
+      *reinterpret_cast<half8_t*>(&s_a[stage][row * kQK + 8 * chunk]) = h;
     }
     const uint32_t c0 = 4u * (st & 1u) + cpair;
     const uint32_t base = 128u * (st & 1u);
@@ -1727,12 +1915,27 @@ bool kquant_gemm_unfused(int format) {
   return format != 0;
 }
 
+// The fp16 GEMM of the two-pass form.  All three give the same bits (same
+// LDS layout, same MFMA order over K, same K split); KRAKEN_GEMM_F16=plain
+// selects the one-step-prefetch kernel.  128 x 256 tiles when they alone give
+// at least 160 workgroups (one per CU, no K split), else 128 x 128.
+enum class GemmKernel { plain, pipe128, pipe256 };
+GemmKernel gemm_f16_kernel_choice(size_t rows, size_t tokens, uint32_t splits) {
+  const char* env = std::getenv("KRAKEN_GEMM_F16");
+  if (env != nullptr && std::strcmp(env, "plain") == 0) {
+    return GemmKernel::plain;
+  }
+  const uint64_t tiles256 = (uint64_t)((rows + 255) / 256) * ((tokens + 127) / 128);
+  return splits == 1 && tiles256 >= 160 ? GemmKernel::pipe256 : GemmKernel::pipe128;
+}
+
 size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens) {
   if (tokens <= kKquantGemvMaxTokens) {
     return 0;
   }
   const uint32_t splits = gemm_k_splits(rows, cols, tokens);
-  return (kquant_gemm_unfused(format) ? align256(rows * cols * 2u) : 0u) + align256(tokens * cols * 2u) +
+  return (kquant_gemm_unfused(format) ? align256(rows * cols * 2u) + align256(tokens * cols * 2u)
+                                      : 0u) +
          (splits > 1 ? align256(splits * tokens * rows * 4u) : 0u);
 }
 
@@ -1752,11 +1955,11 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
                (uint32_t)cols, bpr, (uint32_t)tokens, 0u, tokens >= 4u ? 1u : 0u};
     return launch_gemv(format, a, stream);
   }
-  if (workspace == nullptr ||
-      workspace_bytes < kquant_matmul_workspace_bytes(format, rows, cols, tokens)) {
+  const size_t need = kquant_matmul_workspace_bytes(format, rows, cols, tokens);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     return hipErrorInvalidValue;
   }
-  // Workspace: [fp16 weights (unfused only)] [fp16 inputs] [K-split planes].
+  // Workspace: [fp16 weights] [fp16 inputs] (two-pass form only) [K-split planes].
   const bool unfused = kquant_gemm_unfused(format);
   half_t* w16 = static_cast<half_t*>(workspace);
   half_t* x16 = reinterpret_cast<half_t*>(static_cast<char*>(workspace) +
@@ -1765,45 +1968,59 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
   hipError_t e = hipSuccess;
   if (unfused) {
     const uint64_t chunks = (uint64_t)rows * bpr * 8u;
-    const dim3 dq((uint32_t)((chunks + 255) / 256));
+    const uint64_t n8 = (uint64_t)tokens * cols / 8u;
+    const uint32_t convert_blocks = (uint32_t)((n8 + 255) / 256);
+    const dim3 dq(convert_blocks + (uint32_t)((chunks + 255) / 256));
     if (format == 0) {
-      kq_dequant_f16_kernel<0><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
+      kq_dequant_f16_kernel<0><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16, input, x16,
+                                                       n8, convert_blocks);
     } else if (format == 1) {
-      kq_dequant_f16_kernel<1><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
+      kq_dequant_f16_kernel<1><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16, input, x16,
+                                                       n8, convert_blocks);
     } else {
-      kq_dequant_f16_kernel<2><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16);
+      kq_dequant_f16_kernel<2><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16, input, x16,
+                                                       n8, convert_blocks);
     }
     if ((e = hipGetLastError()) != hipSuccess) {
       return e;
     }
   }
-  const uint64_t n8 = (uint64_t)tokens * cols / 8u;
-  f32_to_f16_kernel<<<dim3((uint32_t)((n8 + 255) / 256)), 256, 0, stream>>>(input, x16, n8);
-  if ((e = hipGetLastError()) != hipSuccess) {
-    return e;
-  }
   const uint32_t splits = gemm_k_splits(rows, cols, tokens);
-  float* planes = splits > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(x16) +
-                                                        align256(tokens * cols * 2u))
+  float* planes = splits > 1 ? reinterpret_cast<float*>(
+                                 static_cast<char*>(workspace) +
+                                 (unfused ? align256(rows * cols * 2u) + align256(tokens * cols * 2u)
+                                          : 0u))
                              : output;
   const dim3 grid((uint32_t)((rows + 127) / 128), (uint32_t)((tokens + 127) / 128), splits);
   if (unfused) {
     const uint32_t steps = (uint32_t)(cols / kGK);
     const uint32_t split_steps = (steps + splits - 1) / splits;
-    gemm_f16_nt_kernel<128, 128><<<grid, 256, 0, stream>>>(x16, w16, planes, (uint32_t)tokens,
-                                                           (uint32_t)rows, (uint32_t)cols,
-                                                           split_steps);
+    const GemmKernel kernel = gemm_f16_kernel_choice(rows, tokens, splits);
+    if (kernel == GemmKernel::pipe256) {
+      const dim3 g256((uint32_t)((rows + 255) / 256), (uint32_t)((tokens + 127) / 128), splits);
+      gemm_f16_pipe_kernel<256><<<g256, 256, 0, stream>>>(x16, w16, planes, (uint32_t)tokens,
+                                                          (uint32_t)rows, (uint32_t)cols,
+                                                          split_steps);
+    } else if (kernel == GemmKernel::pipe128) {
+      gemm_f16_pipe_kernel<128><<<grid, 256, 0, stream>>>(x16, w16, planes, (uint32_t)tokens,
+                                                          (uint32_t)rows, (uint32_t)cols,
+                                                          split_steps);
+    } else {
+      gemm_f16_nt_kernel<128, 128><<<grid, 256, 0, stream>>>(x16, w16, planes, (uint32_t)tokens,
+                                                             (uint32_t)rows, (uint32_t)cols,
+                                                             split_steps);
+    }
   } else {
     const uint32_t steps = (uint32_t)(cols / kQK);
     const uint32_t split_steps = (steps + splits - 1) / splits;
     if (format == 0) {
-      gemm_kq_kernel<0><<<grid, 256, 0, stream>>>(x16, wq, planes, (uint32_t)tokens,
+      gemm_kq_kernel<0><<<grid, 256, 0, stream>>>(input, wq, planes, (uint32_t)tokens,
                                                   (uint32_t)rows, (uint32_t)cols, split_steps);
     } else if (format == 1) {
-      gemm_kq_kernel<1><<<grid, 256, 0, stream>>>(x16, wq, planes, (uint32_t)tokens,
+      gemm_kq_kernel<1><<<grid, 256, 0, stream>>>(input, wq, planes, (uint32_t)tokens,
                                                   (uint32_t)rows, (uint32_t)cols, split_steps);
     } else {
-      gemm_kq_kernel<2><<<grid, 256, 0, stream>>>(x16, wq, planes, (uint32_t)tokens,
+      gemm_kq_kernel<2><<<grid, 256, 0, stream>>>(input, wq, planes, (uint32_t)tokens,
                                                   (uint32_t)rows, (uint32_t)cols, split_steps);
     }
   }

@@ -194,6 +194,30 @@ def test_fused_gemm_equals_two_pass_gemm(ops, monkeypatch, fmt, rows, cols, toke
     np.testing.assert_array_equal(fused, two_pass)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt,rows,cols,tokens", [
+    ("q5_k", 6144, 1024, 1024),   # 128 x 256 tiles
+    ("q6_k", 6000, 1280, 1000),   # 128 x 256 tiles, partial row and token tiles
+    ("q6_k", 1024, 3584, 1024),   # 128 x 128 tiles, four K splits of 14 steps
+    ("q4_k", 1024, 2048, 1024),   # four K splits of 8 steps
+    ("q5_k", 300, 256, 300),      # four K steps, fewer than the stages
+    ("q4_k", 77, 512, 130), ("q5_k", 200, 768, 9)])
+def test_pipelined_gemm_equals_plain_gemm(ops, monkeypatch, fmt, rows, cols, tokens):
+    """The two-pass form's fp16 GEMM with direct-to-LDS copies through three or
+    four stages (the default) against the kernel that prefetches one step into
+    registers (KRAKEN_GEMM_F16=plain): same LDS layout and MFMA order over K,
+    so bit-identical outputs."""
+    print(f"pipelined gemm {fmt} {rows}x{cols} tokens={tokens}", flush=True)
+    w = kc.random_weight_fast(fmt, rows, cols, seed=rows * 5 + cols)
+    x = np.random.default_rng(tokens + 1).standard_normal(tokens * cols).astype(np.float32)
+    monkeypatch.setenv("KRAKEN_KQUANT_GEMM", "unfused")
+    piped = ops.kquant_matmul(fmt, w, rows, cols, x, tokens)
+    monkeypatch.setenv("KRAKEN_GEMM_F16", "plain")
+    plain = ops.kquant_matmul(fmt, w, rows, cols, x, tokens)
+    np.testing.assert_array_equal(piped, plain)
+    assert np.isfinite(piped).all()
+
+
 # ------------------------------------------------------------------ top1 ----
 
 def planted_logit_weight(fmt, rows, cols, winner, seed):

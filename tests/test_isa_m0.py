@@ -22,7 +22,7 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-featu
          "-packed-fp32-ops", f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}",
          "--cuda-device-only", "-S"]
 EXTRA = {"attention_flash.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "attention_decode.hip": [],
-         "gdn_chunked.hip": []}
+         "gdn_chunked.hip": [], "kquant.hip": []}
 # Instructions that read M0 without naming it.
 IMPLICIT = re.compile(r"^(s_movrel|v_movrel|ds_append|ds_consume|ds_gws|s_sendmsg|v_interp|"
                       r"ds_param|lds_direct|s_ttracedata)")
