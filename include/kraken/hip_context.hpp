@@ -454,6 +454,20 @@ class HipContext {
       eps, output.raw()));
   }
 
+  // The layer's gated delta rule alone, for a qkv already through the conv
+  // (no reference counterpart; see kraken_hip_qwen35_gdn_state_ragged_decode_f32).
+  [[nodiscard]] Status qwen35_gdn_state_ragged_decode_f32(
+    const HipBuffer& qkv, const HipBuffer& gate, const HipBuffer& beta, const HipBuffer& dt_bias,
+    const HipBuffer& ssm_a, const HipBuffer& z, const HipBuffer& norm_weight,
+    HipBuffer& state_pool, const HipBuffer& seq_state_offsets, std::size_t sequences,
+    std::size_t key_heads, std::size_t value_heads, std::size_t head_dim, float eps,
+    HipBuffer& output, HipBuffer& gate_output) const {
+    return Status::from_code(kraken_hip_qwen35_gdn_state_ragged_decode_f32(
+      ctx_, qkv.raw(), gate.raw(), beta.raw(), dt_bias.raw(), ssm_a.raw(), z.raw(),
+      norm_weight.raw(), state_pool.raw(), seq_state_offsets.raw(), sequences, key_heads,
+      value_heads, head_dim, eps, output.raw(), gate_output.raw()));
+  }
+
   [[nodiscard]] Status split_qkv_l2_norm_f32_qwen35(
     const HipBuffer& source, HipBuffer& query, HipBuffer& key, HipBuffer& value,
     std::size_t tokens, std::size_t key_heads, std::size_t value_heads, std::size_t head_dim,
@@ -726,6 +740,33 @@ class HipContext {
     return Status::from_code(kraken_hip_kquant_matvec_multi_f32(
       ctx_, count, ggml_types, w, rows, cols, input.raw(), norm_weight.raw(), eps, up.raw(), res,
       out));
+  }
+  // kquant_matvec_multi_f32 whose matrix 0 rows take the conv prologue (no
+  // reference counterpart; see kraken_hip_kquant_matvec_multi_conv_f32).
+  [[nodiscard]] Status kquant_matvec_multi_conv_f32(
+    std::size_t count, const std::uint32_t* ggml_types, const HipBuffer* const* weights,
+    const std::size_t* rows, std::size_t cols, const HipBuffer& input,
+    const HipBuffer& norm_weight, float eps, HipBuffer* const* outputs, HipBuffer& conv_pool,
+    const HipBuffer& conv_offset, const HipBuffer& conv_kernel_weights,
+    std::size_t conv_kernel) const {
+    kraken_buffer w[4], out[4];
+    for (std::size_t i = 0; i < count && i < 4; ++i) {
+      w[i] = weights[i]->raw();
+      out[i] = outputs[i]->raw();
+    }
+    return Status::from_code(kraken_hip_kquant_matvec_multi_conv_f32(
+      ctx_, count, ggml_types, w, rows, cols, input.raw(), norm_weight.raw(), eps, out,
+      conv_pool.raw(), conv_offset.raw(), conv_kernel_weights.raw(), conv_kernel));
+  }
+  // The output projection GEMV with the norm-gated epilogue finished on its
+  // input (no reference counterpart; see kraken_hip_kquant_matvec_head_norm_f32).
+  [[nodiscard]] Status kquant_matvec_head_norm_f32(
+    std::uint32_t ggml_type, const HipBuffer& weight, std::size_t rows, std::size_t cols,
+    const HipBuffer& input, const HipBuffer& gate_factor, std::size_t head_dim, float eps,
+    const HipBuffer& residual, HipBuffer& output) const {
+    return Status::from_code(kraken_hip_kquant_matvec_head_norm_f32(
+      ctx_, ggml_type, weight.raw(), rows, cols, input.raw(), gate_factor.raw(), head_dim, eps,
+      residual.raw(), output.raw()));
   }
   [[nodiscard]] Status kquant_top1_fused_f32(std::uint32_t ggml_type, const HipBuffer& weight,
                                              std::size_t rows, std::size_t cols,

@@ -206,6 +206,85 @@ namespace detail {
                                      none, residuals, out);
 }
 
+// KRAKEN_QWEN35_GDN_DECODE=one_kernel keeps the one-kernel linear-attention
+// core in the fused decode step instead of the three-launch layer below.
+[[nodiscard]] inline bool gdn_decode_split_enabled() {
+  const char* value = std::getenv("KRAKEN_QWEN35_GDN_DECODE");
+  return value == nullptr || std::string_view{value} != "one_kernel";
+}
+
+// A linear-attention layer of one decode token in three launches, for head_dim
+// 128, conv kernel 4 and key_heads == value_heads (qwen35_runtime.cpp:
+// 2720-3034): the joint input projection (RMSNorm folded in) whose qkv rows go
+// through the conv and SiLU as they are written (each row owns its conv
+// channel, so the conv-state update has one writer); the gated delta rule over
+// up to 256 workgroups, which also forms the epilogue's norm_weight * silu(z);
+// ssm_out with the rest of the norm-gated epilogue (the per-head RMS scale) on
+// its input and the residual add on its output.  The one-kernel core keeps a head in one
+// workgroup because of those two steps.  linear_layer_decode_split_applies
+// says whether the shape, weights and cache allow it.
+[[nodiscard]] inline bool linear_layer_decode_split_applies(const ExecutionPlan& plan,
+                                                            const DeviceCache& cache,
+                                                            const DecoderLayerWeights& l,
+                                                            std::size_t linear_layer) {
+  const LinearAttentionWeights& w = l.linear;
+  return gdn_decode_split_enabled() && cache.recurrent_offsets.valid() &&
+         plan.linear_key_head_dim == 128 && plan.linear_key_heads == plan.linear_value_heads &&
+         plan.linear_conv_kernel == 4 && l.qkv.cols <= 4096 && l.ssm_out.cols <= 4096 &&
+         w.conv1d != nullptr && w.dt_bias != nullptr && w.ssm_a != nullptr &&
+         w.ssm_norm != nullptr && l.ssm_out.buffer != nullptr && l.attn_norm != nullptr &&
+         linear_layer < plan.cache.linear_attention_layers;
+}
+
+[[nodiscard]] inline Status linear_layer_decode_split(const HipContext& ctx,
+                                                      const ExecutionPlan& plan,
+                                                      DeviceCache& cache,
+                                                      const DecoderLayerWeights& l,
+                                                      std::size_t linear_layer, float eps,
+                                                      DecodeScratch& s) {
+  const LinearAttentionWeights& w = l.linear;
+  const std::size_t hk = plan.linear_key_heads;
+  const std::size_t hv = plan.linear_value_heads;
+  const std::size_t dk = plan.linear_key_head_dim;
+  const Tensor* t[4] = {&l.qkv, &l.gate, &l.beta, &l.alpha};
+  std::uint32_t types[4];
+  std::size_t rows[4];
+  const HipBuffer* weights[4];
+  for (std::size_t i = 0; i < 4; ++i) {
+    if (t[i]->buffer == nullptr || t[i]->cols != l.qkv.cols) {
+      return Status::invalid_argument("Qwen3.5 linear attention projection weights are missing");
+    }
+    types[i] = static_cast<std::uint32_t>(t[i]->type);
+    rows[i] = t[i]->rows;
+    weights[i] = t[i]->buffer;
+  }
+  HipBuffer* out[4] = {&s.a, &s.b, &s.c, &s.d};
+  // Recurrent row 0 of this layer: the offset table holds (conv, state)
+  // element offsets per slot.
+  const std::size_t slot = linear_layer * plan.cache.recurrent_rows;
+  auto* table = static_cast<unsigned char*>(cache.recurrent_offsets.data());
+  const HipBuffer conv_offset =
+    HipBuffer::borrow(table + 2 * slot * sizeof(std::uint64_t), sizeof(std::uint64_t));
+  const HipBuffer state_offset =
+    HipBuffer::borrow(table + (2 * slot + 1) * sizeof(std::uint64_t), sizeof(std::uint64_t));
+  Status st = ctx.kquant_matvec_multi_conv_f32(4, types, weights, rows, l.qkv.cols, s.hidden,
+                                               *l.attn_norm, eps, out, cache.recurrent_r_cache,
+                                               conv_offset, *w.conv1d, 4);
+  // s.normed (free in the fused order) takes the epilogue's gate factor.
+  if (st.is_ok()) {
+    st = ctx.qwen35_gdn_state_ragged_decode_f32(s.a, s.d, s.c, *w.dt_bias, *w.ssm_a, s.b,
+                                                *w.ssm_norm, cache.recurrent_s_cache,
+                                                state_offset, 1, hk, hv, dk, eps, s.attn,
+                                                s.normed);
+  }
+  if (st.is_ok()) {
+    st = ctx.kquant_matvec_head_norm_f32(static_cast<std::uint32_t>(l.ssm_out.type),
+                                         *l.ssm_out.buffer, l.ssm_out.rows, l.ssm_out.cols,
+                                         s.attn, s.normed, dk, eps, s.hidden, s.hidden);
+  }
+  return st;
+}
+
 // The FFN half of a layer (qwen35_runtime.cpp:3024-3144): hidden += down(silu(gate(n)) *
 // up(n)) with n = RMSNorm(hidden) * post_attention_norm.  OpOrder::reference issues
 // the reference's six ops; OpOrder::fused three fused GEMVs.
@@ -284,6 +363,13 @@ using LayerHook = std::function<Status(std::size_t layer, const HipBuffer& hidde
     }
     Status r = fused ? Status::ok()
                      : ctx.rms_norm_f32_f32_batched(s.hidden, *l.attn_norm, 1, h, eps, s.normed);
+    if (kind == LayerKind::linear_attention && fused &&
+        detail::linear_layer_decode_split_applies(plan, cache, l, kind_index)) {
+      if (r.is_ok()) r = detail::linear_layer_decode_split(ctx, plan, cache, l, kind_index, eps, s);
+      if (r.is_ok()) r = detail::ffn_block(ctx, plan, l, eps, order, s);
+      if (r.is_ok() && after_layer != nullptr) r = (*after_layer)(index, s.hidden);
+      return r;
+    }
     if (kind == LayerKind::linear_attention) {
       // qwen35_runtime.cpp:2720-3034: qkv, z, beta, alpha projections; the
       // attention core; ssm_out; residual.

@@ -474,6 +474,28 @@ KRAKEN_API int kraken_hip_qwen35_gdn_layer_ragged_decode_f32(
   kraken_buffer seq_state_offsets, size_t sequences, size_t key_heads, size_t value_heads,
   size_t head_dim, float eps, kraken_buffer output);
 
+/* No counterpart in the reference: the gated delta rule of
+ * kraken_hip_qwen35_gdn_layer_ragged_decode_f32 alone, for the device decode
+ * loop's three-launch linear-attention layer (input projection with the conv
+ * folded in, this, output projection with the norm-gated epilogue finished on
+ * its input).  qkv [sequences][3 * value_heads * head_dim] holds q, k and v
+ * after the conv and SiLU (kraken_hip_kquant_matvec_multi_conv_f32's matrix 0
+ * output); q and k are L2-normalised here.  gate, beta, dt_bias, ssm_a, z,
+ * norm_weight, state_pool and seq_state_offsets as for the layer entry.
+ * output [sequences][value_heads][head_dim] receives y * rsqrt(head_dim) and
+ * gate_output (same shape) norm_weight[c % head_dim] * silu(z[c]): the
+ * norm-gated epilogue is then y * rsqrt(mean(y^2) + eps) * gate_output per
+ * head (kraken_hip_kquant_matvec_head_norm_f32).  State and y equal the layer
+ * entry's bit for bit given the same qkv.  head_dim 128 and key_heads ==
+ * value_heads only.  A sequence whose state offset is outside the pool is
+ * skipped. */
+KRAKEN_API int kraken_hip_qwen35_gdn_state_ragged_decode_f32(
+  kraken_hip_context* context, kraken_buffer qkv, kraken_buffer gate, kraken_buffer beta,
+  kraken_buffer dt_bias, kraken_buffer ssm_a, kraken_buffer z, kraken_buffer norm_weight,
+  kraken_buffer state_pool, kraken_buffer seq_state_offsets, size_t sequences,
+  size_t key_heads, size_t value_heads, size_t head_dim, float eps, kraken_buffer output,
+  kraken_buffer gate_output);
+
 /* ---- K-quant projections (GGUF Q4_K / Q5_K / Q6_K weights) and argmax ----
  *
  * Weights are rows of GGUF super-blocks of 256 values (Q4_K 144 bytes, Q5_K
@@ -589,6 +611,33 @@ KRAKEN_API int kraken_hip_kquant_matvec_multi_f32(
   const kraken_buffer* weights, const size_t* rows, size_t cols, kraken_buffer input,
   kraken_buffer norm_weight, float eps, kraken_buffer up, const kraken_buffer* residuals,
   const kraken_buffer* outputs);
+/* No counterpart in the reference: kraken_hip_kquant_matvec_multi_f32 (no up
+ * input, no residuals) whose matrix 0 rows are the conv channels of one
+ * sequence's linear-attention prologue: each row's value x becomes
+ * silu(sum_j state[r][j] * w[r][j] + x * w[r][3]) and the conv state row
+ * [r][0..2] shifts in x (ssm_conv1_f32_stateful_at then silu_f32_in_place,
+ * qwen35_runtime.cpp:2171-2178, for one token).
+ * conv_pool holds f32 conv states; conv_offset is one uint64 in device memory,
+ * the element offset of this sequence's [rows[0]][3] state (a state outside the
+ * pool leaves matrix 0's output and state untouched); conv_kernel_weights
+ * [rows[0]][4]; conv_kernel must be 4. */
+KRAKEN_API int kraken_hip_kquant_matvec_multi_conv_f32(
+  kraken_hip_context* context, size_t count, const uint32_t* ggml_types,
+  const kraken_buffer* weights, const size_t* rows, size_t cols, kraken_buffer input,
+  kraken_buffer norm_weight, float eps, const kraken_buffer* outputs, kraken_buffer conv_pool,
+  kraken_buffer conv_offset, kraken_buffer conv_kernel_weights, size_t conv_kernel);
+/* No counterpart in the reference: the one-token GEMV of the linear-attention
+ * output projection with the norm-gated epilogue finished on its input: x[c]
+ * = input[c] * rsqrt(mean over c's head of input^2 + eps) * gate_factor[c]
+ * (gate_factor = norm_weight * silu(z) from
+ * kraken_hip_qwen35_gdn_state_ragged_decode_f32; qwen35_norm_gated_f32_in_place
+ * over heads of head_dim values), output = residual + W x as for
+ * kraken_hip_kquant_matvec_fused_f32.  head_dim must be 128, cols <= 4096;
+ * gate_factor 16-byte aligned. */
+KRAKEN_API int kraken_hip_kquant_matvec_head_norm_f32(
+  kraken_hip_context* context, uint32_t ggml_type, kraken_buffer weight, size_t rows,
+  size_t cols, kraken_buffer input, kraken_buffer gate_factor, size_t head_dim, float eps,
+  kraken_buffer residual, kraken_buffer output);
 /* No counterpart in the reference: matvec_q*_k_f32_top1 (probability_output
  * given) or matvec_q*_k_f32_argmax (probability_output empty) with the output
  * RMSNorm folded into the logits GEMV when norm_weight is given. */

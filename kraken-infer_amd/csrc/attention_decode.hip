@@ -1011,6 +1011,7 @@ struct SplitPlan {
 // Ragged decode: a fixed split size, so sequences of any length divide into
 // equal pieces of work (the grid covers the longest; empty splits exit).
 constexpr uint64_t kRaggedKeysPerSplit = 1024;
+constexpr uint64_t kSingleSplitKeys = 256;
 
 SplitPlan plan_splits(const AttentionArgs& a, int cu_count) {
   const bool ragged = a.seq_positions != nullptr;
@@ -1024,6 +1025,11 @@ SplitPlan plan_splits(const AttentionArgs& a, int cu_count) {
     splits_target = 1;
   }
   uint64_t kps = ragged ? kRaggedKeysPerSplit : (max_keys + splits_target - 1) / splits_target;
+  // A short context is one split: its keys are a few loads per wave, and the
+  // merge launch a split would need costs more than they do.
+  if (!ragged && max_keys <= kSingleSplitKeys) {
+    kps = max_keys;
+  }
   if (const char* env = std::getenv("KRAKEN_DECODE_KEYS_PER_SPLIT")) {
     const long v = std::strtol(env, nullptr, 10);
     if (v > 0) {

@@ -521,4 +521,105 @@ KRAKEN_API int kraken_hip_kquant_matvec_multi_f32(
   return finish_launch(ctx, "HIP K-quant multi matvec command failed: ");
 }
 
+// No counterpart in the reference: the multi GEMV above (no up input, no
+// residuals) whose matrix 0 rows are the conv channels of one sequence: each
+// row's value goes through the depthwise conv (kernel 4) and SiLU of the
+// linear-attention prologue, and its conv state shifts, as the row is written.
+KRAKEN_API int kraken_hip_kquant_matvec_multi_conv_f32(
+  kraken_hip_context* ctx, size_t count, const uint32_t* ggml_types, const kraken_buffer* weights,
+  const size_t* rows, size_t cols, kraken_buffer input, kraken_buffer norm_weight, float eps,
+  const kraken_buffer* outputs, kraken_buffer conv_pool, kraken_buffer conv_offset,
+  kraken_buffer conv_kernel_weights, size_t conv_kernel) {
+  const char* what = "K-quant multi conv matvec";
+  KRAKEN_TRY(check_context(ctx));
+  if (count == 0 || count > kKquantMultiMaxMatrices) {
+    return invalid("HIP K-quant multi conv matvec takes 1 to 4 matrices");
+  }
+  if (ggml_types == nullptr || weights == nullptr || rows == nullptr || outputs == nullptr) {
+    return invalid("HIP K-quant multi conv matvec array argument is null");
+  }
+  if (cols > kKquantMultiMaxCols) {
+    return invalid("HIP K-quant multi conv matvec cols exceeds 4096");
+  }
+  if (conv_kernel != 4) {
+    return invalid("HIP K-quant multi conv matvec conv_kernel must be 4");
+  }
+  int formats[kKquantMultiMaxMatrices];
+  const void* w[kKquantMultiMaxMatrices];
+  const float* res[kKquantMultiMaxMatrices] = {nullptr, nullptr, nullptr, nullptr};
+  float* out[kKquantMultiMaxMatrices];
+  for (size_t i = 0; i < count; ++i) {
+    KRAKEN_TRY(fused_common(ctx, what, ggml_types[i], weights[i], rows[i], cols, input,
+                            norm_weight, formats[i]));
+    KRAKEN_TRY(validate_f32(outputs[i], rows[i], "K-quant multi conv matvec output"));
+    w[i] = weights[i].data;
+    out[i] = static_cast<float*>(outputs[i].data);
+  }
+  size_t state_values = 0, kernel_values = 0;
+  if (!checked_mul(rows[0], conv_kernel - 1u, state_values) ||
+      !checked_mul(rows[0], conv_kernel, kernel_values)) {
+    return invalid("HIP K-quant multi conv matvec value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(conv_pool, state_values, "K-quant multi conv matvec conv pool"));
+  if (conv_pool.byte_size % sizeof(float) != 0) {
+    return invalid("HIP K-quant multi conv matvec conv pool size is not a whole number of "
+                   "elements");
+  }
+  KRAKEN_TRY(validate_buffer(conv_offset, 1, sizeof(uint64_t),
+                             "K-quant multi conv matvec conv offset"));
+  KRAKEN_TRY(validate_f32(conv_kernel_weights, kernel_values,
+                          "K-quant multi conv matvec conv kernel"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const GemvConvEpilogue conv{static_cast<float*>(conv_pool.data),
+                              static_cast<const uint64_t*>(conv_offset.data),
+                              (uint64_t)(conv_pool.byte_size / sizeof(float)),
+                              static_cast<const float*>(conv_kernel_weights.data)};
+  const hipError_t e = launch_kquant_matvec_multi(
+    (uint32_t)count, formats, w, rows, cols, static_cast<const float*>(input.data),
+    static_cast<const float*>(norm_weight.data), eps, nullptr, res, out, ctx->stream, &conv);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP K-quant multi conv matvec launch failed: ") +
+                    hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP K-quant multi conv matvec command failed: ");
+}
+
+// No counterpart in the reference: the one-token GEMV of the linear-attention
+// output projection with the rest of the norm-gated epilogue
+// (qwen35_norm_gated_f32_in_place) on its input, given the epilogue's
+// per-value factor, and the residual add on its output.
+KRAKEN_API int kraken_hip_kquant_matvec_head_norm_f32(
+  kraken_hip_context* ctx, uint32_t ggml_type, kraken_buffer weight, size_t rows, size_t cols,
+  kraken_buffer input, kraken_buffer gate_factor, size_t head_dim, float eps,
+  kraken_buffer residual, kraken_buffer output) {
+  const char* what = "K-quant head-norm matvec";
+  int format = -1;
+  const kraken_buffer none{};
+  KRAKEN_TRY(fused_common(ctx, what, ggml_type, weight, rows, cols, input, none, format));
+  if (head_dim != 128) {
+    return invalid("HIP K-quant head-norm matvec head_dim must be 128");
+  }
+  if (cols > kKquantMultiMaxCols) {
+    return invalid("HIP K-quant head-norm matvec cols exceeds 4096");
+  }
+  KRAKEN_TRY(validate_f32(gate_factor, cols, "K-quant head-norm matvec gate factor"));
+  if (((uintptr_t)gate_factor.data & 15u) != 0) {
+    return invalid("HIP K-quant head-norm matvec gate factor must be 16-byte aligned");
+  }
+  if (residual.data != nullptr) {
+    KRAKEN_TRY(validate_f32(residual, rows, "K-quant head-norm matvec residual"));
+  }
+  KRAKEN_TRY(validate_f32(output, rows, "K-quant head-norm matvec output"));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_kquant_matvec_head_norm(
+    format, weight.data, rows, cols, static_cast<const float*>(input.data),
+    static_cast<const float*>(gate_factor.data), eps, static_cast<const float*>(residual.data),
+    static_cast<float*>(output.data), ctx->stream);
+  if (e != hipSuccess) {
+    return internal(std::string("HIP K-quant head-norm matvec launch failed: ") +
+                    hipGetErrorString(e));
+  }
+  return finish_launch(ctx, "HIP K-quant head-norm matvec command failed: ");
+}
+
 }  // extern "C"

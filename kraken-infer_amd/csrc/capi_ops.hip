@@ -1264,6 +1264,79 @@ KRAKEN_API int kraken_hip_qwen35_conv_split_l2_ragged_decode_f32(
   return finish_launch(ctx, (w + " command failed: ").c_str());
 }
 
+// No counterpart in the reference: the gated delta rule of
+// kraken_hip_qwen35_gdn_layer_ragged_decode_f32 for a qkv whose conv and SiLU
+// are already applied (by kraken_hip_kquant_matvec_multi_conv_f32), output
+// y * scale and gate_output the norm-gated epilogue's norm_weight * silu(z),
+// each head over 8 or 16 workgroups.
+KRAKEN_API int kraken_hip_qwen35_gdn_state_ragged_decode_f32(
+  kraken_hip_context* ctx, kraken_buffer qkv, kraken_buffer gate, kraken_buffer beta,
+  kraken_buffer dt_bias, kraken_buffer ssm_a, kraken_buffer z, kraken_buffer norm_weight,
+  kraken_buffer state_pool, kraken_buffer seq_state_offsets, size_t sequences,
+  size_t key_heads, size_t value_heads, size_t head_dim, float eps, kraken_buffer output,
+  kraken_buffer gate_output) {
+  KRAKEN_TRY(check_context(ctx));
+  const std::string w = "HIP ragged Qwen3.5 GDN state";
+  if (sequences == 0 || key_heads == 0 || value_heads == 0 || head_dim == 0) {
+    return invalid(w + " dimensions must be positive");
+  }
+  if (head_dim != 128 || key_heads != value_heads) {
+    return invalid(w + " needs head_dim 128 and key_heads == value_heads");
+  }
+  if ((dt_bias.data == nullptr) != (ssm_a.data == nullptr)) {
+    return invalid(w + " dt_bias and ssm_a must be given together");
+  }
+  size_t dim = 0, channels = 0, qkv_values = 0, value_values = 0, gate_values = 0,
+         state_values = 0;
+  if (!checked_mul(value_heads, head_dim, dim) || !checked_mul(3u, dim, channels) ||
+      !checked_mul(sequences, channels, qkv_values) ||
+      !checked_mul(sequences, dim, value_values) ||
+      !checked_mul(sequences, value_heads, gate_values) ||
+      !checked_mul(dim, head_dim, state_values)) {
+    return invalid(w + " value count overflow");
+  }
+  KRAKEN_TRY(validate_f32(qkv, qkv_values, "ragged Qwen3.5 GDN state qkv"));
+  KRAKEN_TRY(validate_f32(gate, gate_values, "ragged Qwen3.5 GDN state gate"));
+  KRAKEN_TRY(validate_f32(beta, gate_values, "ragged Qwen3.5 GDN state beta"));
+  if (dt_bias.data != nullptr) {
+    KRAKEN_TRY(validate_f32(dt_bias, value_heads, "ragged Qwen3.5 GDN state dt_bias"));
+    KRAKEN_TRY(validate_f32(ssm_a, value_heads, "ragged Qwen3.5 GDN state ssm_a"));
+  }
+  KRAKEN_TRY(validate_f32(z, value_values, "ragged Qwen3.5 GDN state z"));
+  KRAKEN_TRY(validate_f32(norm_weight, head_dim, "ragged Qwen3.5 GDN state norm weight"));
+  uint64_t state_elems = 0;
+  KRAKEN_TRY(pool_elems_of(state_pool, sizeof(float), state_values, w,
+                           "ragged Qwen3.5 GDN state pool", state_elems));
+  KRAKEN_TRY(validate_buffer(seq_state_offsets, sequences, sizeof(uint64_t),
+                             "ragged Qwen3.5 GDN state offsets"));
+  KRAKEN_TRY(validate_f32(output, value_values, "ragged Qwen3.5 GDN state output"));
+  KRAKEN_TRY(validate_f32(gate_output, value_values, "ragged Qwen3.5 GDN state gate output"));
+  KRAKEN_TRY(check_u32(sequences, "ragged Qwen3.5 GDN state sequences"));
+  KRAKEN_TRY(check_u32(value_heads, "ragged Qwen3.5 GDN state value_heads"));
+  KRAKEN_TRY(begin_launch(ctx));
+  GdnLayerArgs a{};
+  a.qkv = static_cast<const float*>(qkv.data);
+  a.gate = static_cast<const float*>(gate.data);
+  a.beta = static_cast<const float*>(beta.data);
+  a.dt_bias = static_cast<const float*>(dt_bias.data);
+  a.ssm_a = static_cast<const float*>(ssm_a.data);
+  a.z = static_cast<const float*>(z.data);
+  a.norm_weight = static_cast<const float*>(norm_weight.data);
+  a.state_pool = static_cast<float*>(state_pool.data);
+  a.seq_state_offsets = static_cast<const uint64_t*>(seq_state_offsets.data);
+  a.state_pool_elems = state_elems;
+  a.output = static_cast<float*>(output.data);
+  a.gate_factor = static_cast<float*>(gate_output.data);
+  a.sequences = (uint32_t)sequences;
+  a.heads = (uint32_t)value_heads;
+  a.eps = eps;
+  const hipError_t e = launch_gdn_state_ragged(a, ctx->stream);
+  if (e != hipSuccess) {
+    return internal(w + " launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (w + " command failed: ").c_str());
+}
+
 // One decode step of the Qwen3.5 linear-attention core for many sequences: the
 // ragged conv prologue, gated delta rule and norm-gated epilogue
 // (qwen35_runtime.cpp:2740-3008 between the projections) in one kernel where

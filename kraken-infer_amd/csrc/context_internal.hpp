@@ -228,6 +228,8 @@ struct GdnLayerArgs {
   const uint64_t* seq_state_offsets;
   uint64_t state_pool_elems;
   float* output;              // [sequences][heads][128]
+  // gdn_state_split_kernel: norm_weight[c % 128] * silu(z[c]) per output value.
+  float* gate_factor;
   uint32_t sequences, heads;
   float eps;
 };
@@ -236,6 +238,11 @@ struct GdnLayerArgs {
 bool gdn_layer_fused_supported(uint32_t head_dim, uint32_t conv_kernel, uint32_t key_heads,
                                uint32_t value_heads);
 hipError_t launch_gdn_layer_ragged(const GdnLayerArgs& a, hipStream_t stream);
+// The one-kernel layer's gated delta rule alone (qkv already through the conv
+// and SiLU; conv fields unused): output gets y * scale and gate_factor the
+// epilogue's norm_weight * silu(z); the per-head RMS scale is left to the
+// caller.  Same shape limits.
+hipError_t launch_gdn_state_ragged(const GdnLayerArgs& a, hipStream_t stream);
 
 hipError_t launch_ssm_conv(const float* input, const float* kernel, float* output,
                            uint32_t conv_kernel, uint32_t channels, uint32_t tokens,
@@ -328,12 +335,30 @@ hipError_t launch_kquant_argmax(int format, const void* weight, size_t rows, siz
 // (cols / 256 <= 16), each with its own format, rows, residual and output.
 constexpr uint32_t kKquantMultiMaxMatrices = 4;
 constexpr size_t kKquantMultiMaxCols = 4096;
+// Conv epilogue of a multi GEMV's matrix 0 (its rows are the conv channels of
+// one sequence): state [rows][3] at pool + *offset (device value, checked
+// against pool_elems), weights [rows][4].
+struct GemvConvEpilogue {
+  float* pool;
+  const uint64_t* offset;
+  uint64_t pool_elems;
+  const float* weights;
+};
 hipError_t launch_kquant_matvec_multi(uint32_t count, const int* formats,
                                       const void* const* weights, const size_t* rows,
                                       size_t cols, const float* input, const float* norm_weight,
                                       float eps, const float* up,
                                       const float* const* residuals, float* const* outputs,
-                                      hipStream_t stream);
+                                      hipStream_t stream,
+                                      const GemvConvEpilogue* conv = nullptr);
+// One-token GEMV of the gated delta net's output: x = per 128-value head,
+// input * rsqrt(mean(input^2) + eps) * gate_factor[c]; output = residual + W x
+// (residual may be null or the output).
+hipError_t launch_kquant_matvec_head_norm(int format, const void* weight, size_t rows,
+                                          size_t cols, const float* input,
+                                          const float* gate_factor, float eps,
+                                          const float* residual, float* output,
+                                          hipStream_t stream);
 // One-token GEMV output[r] = residual[r] (if given) + sum_k W[r][k] x_k, with x =
 // RMSNorm(input) * norm_weight (if norm_weight), silu(input) * up (if up), or input.
 hipError_t launch_kquant_matvec_fused(int format, const void* weight, size_t rows, size_t cols,

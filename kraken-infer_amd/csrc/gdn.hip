@@ -927,6 +927,137 @@ __global__ __launch_bounds__(256) void gdn_layer_ragged_kernel(GdnLayerArgs p) {
   }
 }
 
+// The gated delta rule of gdn_layer_ragged_kernel without its conv prologue
+// and norm-gated epilogue, for a qkv whose conv and SiLU are already applied
+// (the input projection's conv epilogue): workgroup (part, head, sequence)
+// owns 8 * RPL state rows of the head.  Waves 0 and 1 L2-normalise the head's
+// q and k with the conv prologue's lane mapping and reduction order, each
+// 32-lane group updates its RPL rows as the one-kernel layer does, and the
+// rows' y * scale go to output, so state and y equal the one-kernel layer's
+// bit for bit.  The rows' norm_weight * silu(z) go to gate_factor: the
+// output projection's input transform finishes the norm-gated epilogue with
+// the head's RMS scale.  With the conv-state update done per channel by the
+// input projection, no part waits for another: a single sequence's 16 heads
+// spread over 128 (RPL 2) or 256 (RPL 1) workgroups instead of 16.
+template <bool kPrepare, int RPL>
+__global__ __launch_bounds__(256) void gdn_state_split_kernel(GdnLayerArgs p) {
+  constexpr uint32_t D = 128;
+  constexpr int CPL = 2;
+  __shared__ float qs[D], ks[D];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int grp = tid >> 5;
+  const uint32_t part = blockIdx.x;
+  const uint32_t h = blockIdx.y;
+  const uint32_t seq = blockIdx.z;
+  const uint32_t H = p.heads;
+  const size_t channels = (size_t)3 * H * D;
+
+  const uint64_t soff = p.seq_state_offsets[seq];
+  if ((soff & 3u) != 0 || soff > p.state_pool_elems ||
+      p.state_pool_elems - soff < (uint64_t)H * D * D) {
+    return;  // whole workgroup, before any barrier
+  }
+  float* shead = p.state_pool + soff + (size_t)h * D * D;
+  const uint32_t row0 = part * (8u * RPL) + (uint32_t)grp * RPL;
+  const uint32_t col0 = (uint32_t)(lane & 31) * 4;
+  float4 s[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    s[j] = *reinterpret_cast<const float4*>(shead + (size_t)(row0 + j) * D + col0);
+  }
+  const float* qkv = p.qkv + (size_t)seq * channels;
+  float vv[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    vv[j] = qkv[(size_t)(2u * H + h) * D + row0 + j];
+  }
+  const size_t gi = (size_t)seq * H + h;
+  float g = p.gate[gi];
+  float b = p.beta[gi];
+  float dtb = 0.0f, sa = 0.0f;
+  if (kPrepare) {
+    dtb = p.dt_bias[h];
+    sa = p.ssm_a[h];
+  }
+  float zv[RPL], nw[RPL];
+  if ((lane & 31) == 0) {
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+      zv[j] = p.z[gi * D + row0 + j];
+      nw[j] = p.norm_weight[row0 + j];
+    }
+  }
+  if (wave < 2) {
+    const float* src = qkv + (size_t)((uint32_t)wave * H + h) * D;
+    float y[CPL];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      y[i] = src[lane + 64 * i];
+      ss = fmaf(y[i], y[i], ss);
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / fmaxf(sqrtf(ss), p.eps);
+    float* dst = wave == 0 ? qs : ks;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      dst[lane + 64 * i] = y[i] * inv;
+    }
+  }
+  if (kPrepare) {
+    g = softplus_ref(g + dtb) * sa;
+    b = 1.0f / (1.0f + expf(-b));
+  }
+  const float decay = expf(g);
+  __syncthreads();
+
+  const float4 k = *reinterpret_cast<const float4*>(&ks[col0]);
+  const float4 q = *reinterpret_cast<const float4*>(&qs[col0]);
+  const float scale = 1.0f / sqrtf((float)D);
+  float sk[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    s[j].x *= decay;
+    s[j].y *= decay;
+    s[j].z *= decay;
+    s[j].w *= decay;
+    sk[j] = fmaf(s[j].x, k.x, fmaf(s[j].y, k.y, fmaf(s[j].z, k.z, s[j].w * k.w)));
+  }
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    sk[j] = reduce32_sum(sk[j]);
+  }
+  float yv[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    const float delta = (vv[j] - sk[j]) * b;
+    s[j].x = fmaf(k.x, delta, s[j].x);
+    s[j].y = fmaf(k.y, delta, s[j].y);
+    s[j].z = fmaf(k.z, delta, s[j].z);
+    s[j].w = fmaf(k.w, delta, s[j].w);
+    yv[j] = fmaf(s[j].x, q.x, fmaf(s[j].y, q.y, fmaf(s[j].z, q.z, s[j].w * q.w)));
+  }
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    yv[j] = reduce32_sum(yv[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    *reinterpret_cast<float4*>(shead + (size_t)(row0 + j) * D + col0) = s[j];
+  }
+  if ((lane & 31) == 0) {
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+      p.output[gi * D + row0 + j] = yv[j] * scale;
+      // The norm-gated epilogue's per-value factor, norm_weight * silu(z).
+      const float zz = zv[j];
+      p.gate_factor[gi * D + row0 + j] = nw[j] * (zz * (1.0f / (1.0f + expf(-zz))));
+    }
+  }
+}
+
 unsigned grid_for(size_t total, unsigned block = 256) {
   size_t blocks = (total + block - 1) / block;
   if (blocks < 1) {
@@ -1071,6 +1202,25 @@ hipError_t launch_conv_split_l2_ragged(const float* qkv, float* conv_pool,
 bool gdn_layer_fused_supported(uint32_t head_dim, uint32_t conv_kernel, uint32_t key_heads,
                                uint32_t value_heads) {
   return head_dim == 128 && conv_kernel == 4 && key_heads == value_heads;
+}
+
+hipError_t launch_gdn_state_ragged(const GdnLayerArgs& a, hipStream_t stream) {
+  // One row per 32-lane group (256 workgroups per sequence) while that is at
+  // most a few thousand workgroups, else two.
+  const bool one_row = (uint64_t)a.sequences * a.heads * 16u <= 4096u;
+  const dim3 grid(one_row ? 16u : 8u, a.heads, a.sequences);
+  if (a.dt_bias != nullptr) {
+    if (one_row) {
+      gdn_state_split_kernel<true, 1><<<grid, 256, 0, stream>>>(a);
+    } else {
+      gdn_state_split_kernel<true, 2><<<grid, 256, 0, stream>>>(a);
+    }
+  } else if (one_row) {
+    gdn_state_split_kernel<false, 1><<<grid, 256, 0, stream>>>(a);
+  } else {
+    gdn_state_split_kernel<false, 2><<<grid, 256, 0, stream>>>(a);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_gdn_layer_ragged(const GdnLayerArgs& a, hipStream_t stream) {

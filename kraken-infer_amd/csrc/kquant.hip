@@ -652,7 +652,49 @@ struct MultiGemvArgs {
   const float* up;           // input = silu(input) * up
   uint32_t cols, blocks_per_row;
   float eps;
+  // Head-normed input (XF = 3): per head of 128 values, input *
+  // rsqrt(mean(input^2) + eps) * gate_factor[c].
+  const float* gate_factor;
+  // Conv epilogue of matrix 0 (conv_pool set): row r is conv channel r of one
+  // sequence, whose state [rows][3] sits at conv_pool + *conv_offset; the row's
+  // value x becomes silu(sum_j state[r][j] w[r][j] + x w[r][3]) and the state
+  // shifts in x (conv_weights [rows][4]).
+  float* conv_pool;
+  const uint64_t* conv_offset;
+  uint64_t conv_pool_elems;
+  const float* conv_weights;
 };
+
+// The depthwise conv of one channel (kernel 4) over its state window and the
+// new value x, with SiLU, and the state shifted (the conv prologue's
+// arithmetic in the gated delta net kernels).
+struct ConvRow {
+  float win[3], w[4];
+};
+__device__ __forceinline__ ConvRow conv_row_load(const float* state_row, const float* weights) {
+  ConvRow c;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    c.win[j] = state_row[j];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    c.w[j] = weights[j];
+  }
+  return c;
+}
+__device__ __forceinline__ float conv_row_apply(const ConvRow& c, float x, float* state_row) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    acc = fmaf(c.win[j], c.w[j], acc);
+  }
+  acc = fmaf(x, c.w[3], acc);
+  state_row[0] = c.win[1];
+  state_row[1] = c.win[2];
+  state_row[2] = x;
+  return acc / (1.0f + expf(-acc));
+}
 
 // The raw weight bytes one lane holds for its rows of one trip slot.  Q4_K and
 // Q5_K (16-byte aligned blocks): the lane's own chunk loads.  Q6_K with
@@ -810,6 +852,26 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
         yv[k] = reinterpret_cast<const float4*>(a.norm_weight)[vi];
       } else if constexpr (XF == 2) {
         yv[k] = reinterpret_cast<const float4*>(a.up)[vi];
+      } else if constexpr (XF == 3) {
+        yv[k] = reinterpret_cast<const float4*>(a.gate_factor)[vi];
+      }
+    }
+  }
+  // Matrix 0 with the conv epilogue: this lane's first-trip rows' conv state
+  // and weights load with the input (trip slots beyond U load when reached).
+  const bool conv = a.conv_pool != nullptr && m == 0;
+  float* conv_state = nullptr;
+  ConvRow crow[U];
+  if (conv) {
+    const uint64_t coff = *a.conv_offset;
+    if (coff <= a.conv_pool_elems && a.conv_pool_elems - coff >= (uint64_t)rows * 3u) {
+      conv_state = a.conv_pool + coff;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t row = r0 + (uint32_t)u * stride + slot;
+        if (li == 0 && row < rows) {
+          crow[u] = conv_row_load(conv_state + (size_t)row * 3u, a.conv_weights + (size_t)row * 4u);
+        }
       }
     }
   }
@@ -831,6 +893,15 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
         ss = fmaf(v.y, v.y, ss);
         ss = fmaf(v.z, v.z, ss);
         ss = fmaf(v.w, v.w, ss);
+      }
+      if constexpr (XF == 3) {
+        // The head's 32 float4s are held by 32 consecutive lanes.
+        float hs = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, v.w * v.w)));
+        hs = group_sum<32>(hs);
+        const float hscale = 1.0f / sqrtf(hs / 128.0f + a.eps);
+        const float4 g = yv[k];
+        v = make_float4(v.x * hscale * g.x, v.y * hscale * g.y, v.z * hscale * g.z,
+                        v.w * hscale * g.w);
       }
       xv[k] = v;
     }
@@ -916,7 +987,18 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
       }
       const float total = group_sum<LR>(acc);
       if (li == 0 && row < rows) {
-        output[row] = residual != nullptr ? residual[row] + total : total;
+        float value = residual != nullptr ? residual[row] + total : total;
+        if (conv) {
+          if (conv_state == nullptr) {
+            continue;  // offset outside the pool: the sequence is skipped
+          }
+          if (r0 != (wl * kXsWaves + (uint32_t)wave) * RW) {
+            crow[u] = conv_row_load(conv_state + (size_t)row * 3u,
+                                    a.conv_weights + (size_t)row * 4u);
+          }
+          value = conv_row_apply(crow[u], value, conv_state + (size_t)row * 3u);
+        }
+        output[row] = value;
       }
     }
     if (U > 1) {
@@ -1827,6 +1909,9 @@ hipError_t launch_multi(MultiGemvArgs a, hipStream_t stream) {
       a.format[m] = 3;
     }
   }
+  if (a.gate_factor != nullptr) {
+    return launch_xs_x<3>(a, stream);
+  }
   if (a.norm_weight != nullptr) {
     return launch_xs_x<1>(a, stream);
   }
@@ -2108,7 +2193,7 @@ hipError_t launch_kquant_matvec_multi(uint32_t count, const int* formats,
                                       size_t cols, const float* input, const float* norm_weight,
                                       float eps, const float* up,
                                       const float* const* residuals, float* const* outputs,
-                                      hipStream_t stream) {
+                                      hipStream_t stream, const GemvConvEpilogue* conv) {
   if (count == 0 || count > (uint32_t)kXsMaxMatrices || cols / 256u > kXsMaxBlocksPerRow) {
     return hipErrorInvalidValue;
   }
@@ -2124,6 +2209,33 @@ hipError_t launch_kquant_matvec_multi(uint32_t count, const int* formats,
   m.input = input;
   m.norm_weight = norm_weight;
   m.up = up;
+  m.cols = (uint32_t)cols;
+  m.blocks_per_row = (uint32_t)(cols / 256u);
+  m.eps = eps;
+  m.conv_pool = conv != nullptr ? conv->pool : nullptr;
+  m.conv_offset = conv != nullptr ? conv->offset : nullptr;
+  m.conv_pool_elems = conv != nullptr ? conv->pool_elems : 0u;
+  m.conv_weights = conv != nullptr ? conv->weights : nullptr;
+  return launch_multi(m, stream);
+}
+
+hipError_t launch_kquant_matvec_head_norm(int format, const void* weight, size_t rows,
+                                          size_t cols, const float* input,
+                                          const float* gate_factor, float eps,
+                                          const float* residual, float* output,
+                                          hipStream_t stream) {
+  if (cols / 256u > kXsMaxBlocksPerRow || cols % 128u != 0) {
+    return hipErrorInvalidValue;
+  }
+  MultiGemvArgs m{};
+  m.weight[0] = static_cast<const uint8_t*>(weight);
+  m.output[0] = output;
+  m.residual[0] = residual;
+  m.rows[0] = (uint32_t)rows;
+  m.format[0] = format;
+  m.count = 1;
+  m.input = input;
+  m.gate_factor = gate_factor;
   m.cols = (uint32_t)cols;
   m.blocks_per_row = (uint32_t)(cols / 256u);
   m.eps = eps;

@@ -65,6 +65,7 @@ SIGNATURES = {
     "kraken_hip_qwen35_conv_split_l2_ragged_decode_f32": [_B] * 4 + [_sz] * 5 + [_f, _B, _B, _B],
     "kraken_hip_qwen35_gdn_layer_ragged_decode_f32": [_B] * 4 + [_sz] + [_B] * 8 + [_sz] * 4
                                                      + [_f, _B],
+    "kraken_hip_qwen35_gdn_state_ragged_decode_f32": [_B] * 9 + [_sz] * 4 + [_f, _B, _B],
     "kraken_hip_qwen35_gdn_gated_f32": [_B] * 10 + [_sz] * 5 + [_f, _B],
     "kraken_hip_split_qkv_l2_norm_f32_qwen35": [_B] * 4 + [_sz] * 4 + [_f],
     "kraken_hip_l2_norm_f32_in_place": [_B, _sz, _sz, _f],
@@ -109,6 +110,11 @@ SIGNATURES = {
     "kraken_hip_kquant_matvec_multi_f32": [_sz, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                            _sz, _B, _B, _f, _B, ctypes.c_void_p,
                                            ctypes.c_void_p],
+    "kraken_hip_kquant_matvec_multi_conv_f32": [_sz, ctypes.c_void_p, ctypes.c_void_p,
+                                                ctypes.c_void_p, _sz, _B, _B, _f,
+                                                ctypes.c_void_p, _B, _B, _B, _sz],
+    "kraken_hip_kquant_matvec_head_norm_f32": [ctypes.c_uint32, _B, _sz, _sz, _B, _B, _sz, _f,
+                                               _B, _B],
     "kraken_hip_argmax_f32_i32": [_B, _sz, _B],
     "kraken_hip_argmax_prob_f32_i32": [_B, _sz, _B, _B],
     "kraken_hip_begin_graph": [],
@@ -302,6 +308,18 @@ class Context:
         outs = (KrakenBuffer * n)(*[as_buffer(o) for o in outputs])
         self.call("kquant_matvec_multi_f32", n, types, ws, rs, cols, input, norm_weight, eps, up,
                   res, outs)
+
+    def kquant_matvec_multi_conv(self, ggml_types, weights, rows, cols, input, norm_weight, eps,
+                                 outputs, conv_pool, conv_offset, conv_weights, conv_kernel=4):
+        """kraken_hip_kquant_matvec_multi_conv_f32 with Python sequences for the
+        per-matrix arrays."""
+        n = len(weights)
+        types = (ctypes.c_uint32 * n)(*ggml_types)
+        ws = (KrakenBuffer * n)(*[as_buffer(w) for w in weights])
+        rs = (ctypes.c_size_t * n)(*rows)
+        outs = (KrakenBuffer * n)(*[as_buffer(o) for o in outputs])
+        self.call("kquant_matvec_multi_conv_f32", n, types, ws, rs, cols, input, norm_weight, eps,
+                  outs, conv_pool, conv_offset, conv_weights, conv_kernel)
 
     def buffer(self, array=None, *, byte_size: int | None = None, dtype=np.float32):
         """Device buffer holding `array` (or `byte_size` uninitialised bytes)."""

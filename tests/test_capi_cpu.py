@@ -452,3 +452,71 @@ def test_no_alloc_attention_limits_its_scratch(vctx):
             assert code == kh.INVALID_ARGUMENT
             assert msg == ("HIP gated F16 KV batched attention needs 17039360 bytes of split "
                            "partials; the allocation-free entry point has 8388608")
+
+
+# ------------------------------------------- three-launch GDN decode layer ----
+
+def _multi_conv_args(rows0=6144, conv_kernel=4, pool_bytes=None, kernel_bytes=None,
+                     offset_bytes=8):
+    types = (ctypes.c_uint32 * 1)(13)
+    rows = (ctypes.c_size_t * 1)(rows0)
+    ws = (kh.KrakenBuffer * 1)(fake(rows0 * 4 * 176))
+    outs = (kh.KrakenBuffer * 1)(fake(4 * rows0))
+    return (1, types, ws, rows, 1024, fake(4096), fake(4096), 1e-6, outs,
+            fake(pool_bytes if pool_bytes is not None else 4 * 3 * rows0), fake(offset_bytes),
+            fake(kernel_bytes if kernel_bytes is not None else 16 * rows0), conv_kernel)
+
+
+@pytest.mark.parametrize("kw,fragment", [
+    (dict(), None),
+    (dict(conv_kernel=3), "conv_kernel must be 4"),
+    (dict(pool_bytes=4 * 3 * 6144 - 4), "conv pool buffer is too small"),
+    (dict(kernel_bytes=16 * 6144 - 4), "conv kernel buffer is too small"),
+    (dict(offset_bytes=4), "conv offset buffer is too small"),
+])
+def test_multi_conv_matvec_checks(vctx, kw, fragment):
+    code, msg = status(vctx, "kquant_matvec_multi_conv_f32", *_multi_conv_args(**kw))
+    if fragment is None:
+        assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED)
+    else:
+        assert code == kh.INVALID_ARGUMENT and fragment in msg, msg
+
+
+@pytest.mark.parametrize("kw,fragment", [
+    (dict(), None),
+    (dict(head_dim=64), "head_dim must be 128"),
+    (dict(gf=fake(4 * 2048 - 4)), "gate factor buffer is too small"),
+])
+def test_head_norm_matvec_checks(vctx, kw, fragment):
+    a = dict(gf=fake(4 * 2048), head_dim=128)
+    a.update(kw)
+    code, msg = status(vctx, "kquant_matvec_head_norm_f32", 12, fake(1024 * 8 * 144), 1024, 2048,
+                       fake(4 * 2048), a["gf"], a["head_dim"], 1e-6, kh.KrakenBuffer(None, 0),
+                       fake(4 * 1024))
+    if fragment is None:
+        assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED)
+    else:
+        assert code == kh.INVALID_ARGUMENT and fragment in msg, msg
+
+
+@pytest.mark.parametrize("kw,fragment", [
+    (dict(), None),
+    (dict(head_dim=64), "needs head_dim 128"),
+    (dict(key_heads=8), "needs head_dim 128 and key_heads == value_heads"),
+    (dict(ssa=kh.KrakenBuffer(None, 0)), "dt_bias and ssm_a must be given together"),
+    (dict(state=fake(4 * 16 * 128 * 128 - 4)), "state pool buffer is too small"),
+    (dict(qkv=fake(4 * 6144 - 4)), "qkv buffer is too small"),
+    (dict(z=fake(4 * 2048 - 4)), "z buffer is too small"),
+    (dict(gout=fake(4 * 2048 - 4)), "gate output buffer is too small"),
+])
+def test_gdn_state_decode_checks(vctx, kw, fragment):
+    a = dict(qkv=fake(4 * 6144), ssa=fake(64), state=fake(4 * 16 * 128 * 128), head_dim=128,
+             key_heads=16, z=fake(4 * 2048), gout=fake(4 * 2048))
+    a.update(kw)
+    code, msg = status(vctx, "qwen35_gdn_state_ragged_decode_f32", a["qkv"], fake(64), fake(64),
+                       fake(64), a["ssa"], a["z"], fake(512), a["state"], fake(8), 1,
+                       a["key_heads"], 16, a["head_dim"], 1e-6, fake(4 * 2048), a["gout"])
+    if fragment is None:
+        assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED)
+    else:
+        assert code == kh.INVALID_ARGUMENT and fragment in msg, msg
