@@ -1113,29 +1113,43 @@ __global__ __launch_bounds__(256) void kq_dequant_f16_kernel(const uint8_t* weig
     }
     return;
   }
-  const uint64_t id = (uint64_t)(blockIdx.x - convert_blocks) * 256u + threadIdx.x;
-  const uint64_t chunks = (uint64_t)rows * blocks_per_row * 8u;
-  if (id >= chunks) {
-    return;
-  }
-  const uint64_t blk = id / 8u;
-  const uint32_t c = (uint32_t)(id % 8u);
-  ChunkDecoder<F, true> dec;
-  dec.decode(weight + blk * KqFormat<F>::kBytes, c);
-  half_t* o = out + blk * 256u;
-  half8_t h0, h1;
+  // The workgroup's 32 blocks are decoded into LDS and written out as one
+  // contiguous 16 KB run: a lane's own values land in 32-byte pieces spread
+  // over its block, so storing them directly touched four times the cache
+  // lines per store instruction.
+  __shared__ __attribute__((aligned(16))) half_t s_out[32 * 256];
+  const uint64_t first_blk = (uint64_t)(blockIdx.x - convert_blocks) * 32u;
+  const uint64_t id = first_blk * 8u + threadIdx.x;
+  const uint64_t total_blocks = (uint64_t)rows * blocks_per_row;
+  const uint32_t lb = threadIdx.x / 8u;  // block within the workgroup
+  const uint32_t c = threadIdx.x % 8u;
+  if (id < total_blocks * 8u) {
+    ChunkDecoder<F, true> dec;
+    dec.decode(weight + (first_blk + lb) * KqFormat<F>::kBytes, c);
+    half_t* o = s_out + lb * 256u;
 #pragma unroll
-  for (int half_i = 0; half_i < 2; ++half_i) {
+    for (int half_i = 0; half_i < 2; ++half_i) {
+      half8_t h0, h1;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      h0[j] = static_cast<half_t>(dec.v0[8 * half_i + j]);
-      h1[j] = static_cast<half_t>(dec.v1[8 * half_i + j]);
+      for (int j = 0; j < 8; ++j) {
+        h0[j] = static_cast<half_t>(dec.v0[8 * half_i + j]);
+        h1[j] = static_cast<half_t>(dec.v1[8 * half_i + j]);
+      }
+      *reinterpret_cast<half8_t*>(o + dec.p0 + 8 * half_i) = h0;
+      *reinterpret_cast<half8_t*>(o + dec.p1 + 8 * half_i) = h1;
     }
-    *reinterpret_cast<half8_t*>(o + dec.p0 + 8 * half_i) = h0;
-    *reinterpret_cast<half8_t*>(o + dec.p1 + 8 * half_i) = h1;
+  }
+  __syncthreads();
+  const uint64_t valid = total_blocks - first_blk < 32u ? total_blocks - first_blk : 32u;
+  half8_t* dst = reinterpret_cast<half8_t*>(out + first_blk * 256u);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t piece = (uint32_t)j * 256u + threadIdx.x;  // 16-byte piece, 32 per block
+    if (piece / 32u < valid) {
+      dst[piece] = reinterpret_cast<const half8_t*>(s_out)[piece];
+    }
   }
 }
-
 
 // ------------------------------------------------------------------ GEMM ----
 // C[t][r] = sum_k X[t][k] W[r][k] with X [M = tokens][K], W [N = rows][K] fp16
@@ -2052,10 +2066,10 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
   const uint8_t* wq = static_cast<const uint8_t*>(weight);
   hipError_t e = hipSuccess;
   if (unfused) {
-    const uint64_t chunks = (uint64_t)rows * bpr * 8u;
+    const uint64_t blocks = (uint64_t)rows * bpr;
     const uint64_t n8 = (uint64_t)tokens * cols / 8u;
     const uint32_t convert_blocks = (uint32_t)((n8 + 255) / 256);
-    const dim3 dq(convert_blocks + (uint32_t)((chunks + 255) / 256));
+    const dim3 dq(convert_blocks + (uint32_t)((blocks + 31) / 32));
     if (format == 0) {
       kq_dequant_f16_kernel<0><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16, input, x16,
                                                        n8, convert_blocks);
