@@ -620,7 +620,8 @@ KRAKEN_API int kraken_hip_kquant_matvec_multi_f32(
  * conv_pool holds f32 conv states; conv_offset is one uint64 in device memory,
  * the element offset of this sequence's [rows[0]][3] state (a state outside the
  * pool leaves matrix 0's output and state untouched); conv_kernel_weights
- * [rows[0]][4]; conv_kernel must be 4. */
+ * [rows[0]][4]; conv_kernel must be 4, and norm_weight must be given (the
+ * joint projection of a normed hidden state). */
 KRAKEN_API int kraken_hip_kquant_matvec_multi_conv_f32(
   kraken_hip_context* context, size_t count, const uint32_t* ggml_types,
   const kraken_buffer* weights, const size_t* rows, size_t cols, kraken_buffer input,

@@ -544,6 +544,9 @@ KRAKEN_API int kraken_hip_kquant_matvec_multi_conv_f32(
   if (conv_kernel != 4) {
     return invalid("HIP K-quant multi conv matvec conv_kernel must be 4");
   }
+  if (norm_weight.data == nullptr) {
+    return invalid("HIP K-quant multi conv matvec needs a norm weight");
+  }
   int formats[kKquantMultiMaxMatrices];
   const void* w[kKquantMultiMaxMatrices];
   const float* res[kKquantMultiMaxMatrices] = {nullptr, nullptr, nullptr, nullptr};

@@ -740,8 +740,10 @@ __device__ __forceinline__ float silu_mul_fast(float x, float u) {
   return x * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
-// The rows of one matrix for one workgroup (local index wl of nwg).
-template <int F, int LR, int PPL, int XF, int U>
+// The rows of one matrix for one workgroup (local index wl of nwg).  kConv:
+// the launch carries the conv epilogue of matrix 0 (a template option, so the
+// other launches keep its registers).
+template <int F, int LR, int PPL, int XF, int U, bool kConv>
 __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_t wl,
                                           uint32_t nwg, float* s_x, float* s_red,
                                           u32x4_t* s_span) {
@@ -859,9 +861,9 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
   }
   // Matrix 0 with the conv epilogue: this lane's first-trip rows' conv state
   // and weights load with the input (trip slots beyond U load when reached).
-  const bool conv = a.conv_pool != nullptr && m == 0;
+  const bool conv = kConv && m == 0;
   float* conv_state = nullptr;
-  ConvRow crow[U];
+  ConvRow crow[kConv ? U : 1];
   if (conv) {
     const uint64_t coff = *a.conv_offset;
     if (coff <= a.conv_pool_elems && a.conv_pool_elems - coff >= (uint64_t)rows * 3u) {
@@ -1014,7 +1016,7 @@ __device__ __forceinline__ void xs_matrix(const MultiGemvArgs& a, int m, uint32_
 
 // Four workgroups per CU must be resident for the kXsMaxWorkgroups launches
 // (one chunk per lane: at most 128 VGPRs, four waves per SIMD).
-template <int LR, int PPL, int XF, int U>
+template <int LR, int PPL, int XF, int U, bool kConv = false>
 __global__ __launch_bounds__(64 * kXsWaves)
 __attribute__((amdgpu_waves_per_eu(PPL == 1 ? 4 : 1)))
 void kq_gemv_xs_kernel(MultiGemvArgs a) {
@@ -1030,16 +1032,16 @@ void kq_gemv_xs_kernel(MultiGemvArgs a) {
   const uint32_t nwg = a.wg_begin[m + 1] - a.wg_begin[m];
   switch (a.format[m]) {
     case 0:
-      xs_matrix<0, LR, PPL, XF, U>(a, m, wl, nwg, s_x, s_red, s_span);
+      xs_matrix<0, LR, PPL, XF, U, kConv>(a, m, wl, nwg, s_x, s_red, s_span);
       break;
     case 1:
-      xs_matrix<1, LR, PPL, XF, U>(a, m, wl, nwg, s_x, s_red, s_span);
+      xs_matrix<1, LR, PPL, XF, U, kConv>(a, m, wl, nwg, s_x, s_red, s_span);
       break;
     case 2:
-      xs_matrix<2, LR, PPL, XF, U>(a, m, wl, nwg, s_x, s_red, s_span);
+      xs_matrix<2, LR, PPL, XF, U, kConv>(a, m, wl, nwg, s_x, s_red, s_span);
       break;
     default:
-      xs_matrix<3, LR, PPL, XF, U>(a, m, wl, nwg, s_x, s_red, s_span);
+      xs_matrix<3, LR, PPL, XF, U, kConv>(a, m, wl, nwg, s_x, s_red, s_span);
       break;
   }
 }
@@ -1895,6 +1897,19 @@ hipError_t launch_xs(MultiGemvArgs a, hipStream_t stream) {
     a.wg_begin[m + 1] = a.wg_begin[m] + n;
   }
   const dim3 grid(a.wg_begin[a.count]);
+  if (a.conv_pool != nullptr) {
+    // The conv epilogue comes with the RMSNorm input (the joint projection).
+    if constexpr (XF == 1) {
+      if (one_trip) {
+        kq_gemv_xs_kernel<LR, PPL, XF, 1, true><<<grid, 64 * kXsWaves, 0, stream>>>(a);
+      } else {
+        kq_gemv_xs_kernel<LR, PPL, XF, 2, true><<<grid, 64 * kXsWaves, 0, stream>>>(a);
+      }
+      return hipGetLastError();
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   if (one_trip) {
     kq_gemv_xs_kernel<LR, PPL, XF, 1><<<grid, 64 * kXsWaves, 0, stream>>>(a);
   } else {

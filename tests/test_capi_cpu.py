@@ -457,12 +457,13 @@ def test_no_alloc_attention_limits_its_scratch(vctx):
 # ------------------------------------------- three-launch GDN decode layer ----
 
 def _multi_conv_args(rows0=6144, conv_kernel=4, pool_bytes=None, kernel_bytes=None,
-                     offset_bytes=8):
+                     offset_bytes=8, norm=True):
     types = (ctypes.c_uint32 * 1)(13)
     rows = (ctypes.c_size_t * 1)(rows0)
     ws = (kh.KrakenBuffer * 1)(fake(rows0 * 4 * 176))
     outs = (kh.KrakenBuffer * 1)(fake(4 * rows0))
-    return (1, types, ws, rows, 1024, fake(4096), fake(4096), 1e-6, outs,
+    return (1, types, ws, rows, 1024, fake(4096),
+            fake(4096) if norm else kh.KrakenBuffer(None, 0), 1e-6, outs,
             fake(pool_bytes if pool_bytes is not None else 4 * 3 * rows0), fake(offset_bytes),
             fake(kernel_bytes if kernel_bytes is not None else 16 * rows0), conv_kernel)
 
@@ -473,6 +474,7 @@ def _multi_conv_args(rows0=6144, conv_kernel=4, pool_bytes=None, kernel_bytes=No
     (dict(pool_bytes=4 * 3 * 6144 - 4), "conv pool buffer is too small"),
     (dict(kernel_bytes=16 * 6144 - 4), "conv kernel buffer is too small"),
     (dict(offset_bytes=4), "conv offset buffer is too small"),
+    (dict(norm=False), "needs a norm weight"),
 ])
 def test_multi_conv_matvec_checks(vctx, kw, fragment):
     code, msg = status(vctx, "kquant_matvec_multi_conv_f32", *_multi_conv_args(**kw))
