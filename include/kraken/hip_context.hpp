@@ -310,6 +310,24 @@ class HipContext {
       section_3, theta, eps, query_out.raw(), gate_out.raw()));
   }
 
+  // The prologue and the gated attention over the cache (see kraken_hip.h):
+  // one launch for a short decode token, else the two calls.
+  [[nodiscard]] Status qwen35_attention_prologue_gated_f16_kv(
+    const HipBuffer& q_gate, const HipBuffer& key, const HipBuffer& value,
+    const HipBuffer& q_norm, const HipBuffer& k_norm, const HipBuffer& positions,
+    std::size_t mrope_start_position, HipBuffer& key_cache, HipBuffer& value_cache,
+    std::size_t layer, std::size_t start_position, std::size_t tokens,
+    std::size_t capacity_tokens, std::size_t heads, std::size_t kv_heads, std::size_t head_dim,
+    std::size_t n_dims, std::size_t section_0, std::size_t section_1, std::size_t section_2,
+    std::size_t section_3, float theta, float eps, HipBuffer& query_out, HipBuffer& gate_out,
+    HipBuffer& output) const {
+    return Status::from_code(kraken_hip_qwen35_attention_prologue_gated_f16_kv(
+      ctx_, q_gate.raw(), key.raw(), value.raw(), q_norm.raw(), k_norm.raw(), positions.raw(),
+      mrope_start_position, key_cache.raw(), value_cache.raw(), layer, start_position, tokens,
+      capacity_tokens, heads, kv_heads, head_dim, n_dims, section_0, section_1, section_2,
+      section_3, theta, eps, query_out.raw(), gate_out.raw(), output.raw()));
+  }
+
   [[nodiscard]] Status gated_delta_net_f32_batched_in_place_at(
     const HipBuffer& query, const HipBuffer& key, const HipBuffer& value,
     const HipBuffer& gate, const HipBuffer& beta, HipBuffer& state, std::size_t state_offset,

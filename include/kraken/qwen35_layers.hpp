@@ -329,17 +329,12 @@ namespace detail {
 
   if (order == OpOrder::fused && cache.kv_cache_f16) {
     const HipBuffer none;
-    Status s = ctx.qwen35_attention_prologue_f16_kv(
+    return ctx.qwen35_attention_prologue_gated_f16_kv(
       q_gate, key, value, *w.q_norm, *w.k_norm, positions != nullptr ? *positions : none,
       mrope_start_position, cache.key_cache, cache.value_cache, attention_layer, start_position,
       tokens, capacity, heads, kv_heads, head_dim, mrope_dims, mrope_sections[0],
-      mrope_sections[1], mrope_sections[2], mrope_sections[3], rope_theta, rms_eps, qb, gb);
-    if (!s.is_ok()) {
-      return s;
-    }
-    return ctx.attention_f32_batched_f16_kv_gated(qb, cache.key_cache, cache.value_cache, gb,
-                                                  attention_layer, start_position, tokens,
-                                                  capacity, heads, kv_heads, head_dim, output);
+      mrope_sections[1], mrope_sections[2], mrope_sections[3], rope_theta, rms_eps, qb, gb,
+      output);
   }
 
   // :3229-3268 split of the joint projection, q and k RMSNorm.

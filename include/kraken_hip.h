@@ -227,6 +227,28 @@ KRAKEN_API int kraken_hip_qwen35_attention_prologue_f16_kv(
   size_t head_dim, size_t n_dims, size_t section_0, size_t section_1, size_t section_2,
   size_t section_3, float theta, float eps, kraken_buffer query_out, kraken_buffer gate_out);
 
+/* kraken_hip_qwen35_attention_prologue_f16_kv followed by
+ * kraken_hip_attention_f32_batched_f16_kv_gated(query_out, key_cache,
+ * value_cache, gate_out, layer, start_position, tokens, capacity_tokens,
+ * heads, kv_heads, head_dim, output): the fused-order full-attention core of
+ * run_qwen35_full_attention_layer_chunk (qwen35_runtime.cpp:3229-3355).  No
+ * counterpart in the reference as one call; it is for the decode loop, where
+ * the two launches cost more than the work.  One token (tokens == 1) with
+ * head_dim 256, heads / kv_heads in {1, 2, 4} and start_position < 256 runs as
+ * a single launch that writes the same output and cache rows and leaves
+ * query_out and gate_out unwritten; every other shape, and
+ * KRAKEN_QWEN35_ATTENTION_PROLOGUE=two_launch, runs the two entries above
+ * (query_out and gate_out are their scratch).  Arguments as the two entries;
+ * output f32 [tokens][heads][head_dim]. */
+KRAKEN_API int kraken_hip_qwen35_attention_prologue_gated_f16_kv(
+  kraken_hip_context* context, kraken_buffer q_gate, kraken_buffer key, kraken_buffer value,
+  kraken_buffer q_norm, kraken_buffer k_norm, kraken_buffer positions,
+  size_t mrope_start_position, kraken_buffer key_cache, kraken_buffer value_cache, size_t layer,
+  size_t start_position, size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads,
+  size_t head_dim, size_t n_dims, size_t section_0, size_t section_1, size_t section_2,
+  size_t section_3, float theta, float eps, kraken_buffer query_out, kraken_buffer gate_out,
+  kraken_buffer output);
+
 /* ------------------------------------------------------ gated delta net -- */
 
 /* MpsContext::gated_delta_net_f32_batched_in_place_at (mps_backend.hpp:296-300;

@@ -1433,6 +1433,47 @@ hipError_t launch_attention_decode(const AttentionArgs& a, int cu_count, void* w
                   : dispatch_kv<float>(p, a.head_dim, g, tuned, stream);
 }
 
+hipError_t launch_attention_prologue_decode(const PrologueArgs& a, uint32_t layer,
+                                            uint32_t start_position, uint32_t capacity_tokens,
+                                            float* output, hipStream_t stream) {
+  // The contract of the folded kernel: what the two-launch form would run on
+  // the short-split kernel with one split (no kernel or split-size override).
+  const char* kernel_env = std::getenv("KRAKEN_DECODE_KERNEL");
+  if (a.tokens != 1 || a.head_dim != kMD || a.kv_heads == 0 || a.heads % a.kv_heads != 0 ||
+      (uint64_t)start_position + 1u > kSingleSplitKeys || start_position >= capacity_tokens ||
+      std::getenv("KRAKEN_DECODE_KEYS_PER_SPLIT") != nullptr ||
+      (kernel_env != nullptr && std::strcmp(kernel_env, "short") != 0) ||
+      !aligned16(a.key_cache) || !aligned16(a.value_cache) || !aligned16(output)) {
+    return hipErrorNotSupported;
+  }
+  const uint32_t g = a.heads / a.kv_heads;
+  if (g != 1 && g != 2 && g != 4) {
+    return hipErrorNotSupported;
+  }
+  DecodeParams p{};
+  p.key_cache = a.key_cache;
+  p.value_cache = a.value_cache;
+  p.output = output;
+  p.layer = layer;
+  p.start_position = start_position;
+  p.tokens = 1;
+  p.capacity_tokens = capacity_tokens;
+  p.heads = a.heads;
+  p.kv_heads = a.kv_heads;
+  p.keys_per_split = start_position + 1u;
+  p.splits = 1;
+  p.scale_log2 = (1.0f / sqrtf((float)a.head_dim)) * kLog2e;
+  PrologueFold f{};
+  f.q_gate = a.q_gate;
+  f.key = a.key;
+  f.value = a.value;
+  f.q_norm = a.q_norm;
+  f.k_norm = a.k_norm;
+  f.rope = RopeArgs{a.positions, a.mrope_start, 1u, a.n_dims, a.s0, a.s1, a.s2, a.s3, a.theta};
+  f.eps = a.eps;
+  return launch_decode_short_prologue(p, f, g, stream);
+}
+
 hipError_t launch_f16_to_f32(const void* in, float* out, size_t count, hipStream_t stream) {
   if (count == 0) {
     return hipSuccess;

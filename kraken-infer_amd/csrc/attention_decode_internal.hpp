@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdint>
 
+#include "attention_prologue_common.hpp"
 #include "device_common.hpp"
 
 namespace kraken {
@@ -82,11 +83,32 @@ constexpr int kMTileHalfs = kMTile * kMD;         // 8 KB per K or V tile
 
 typedef float float4v_t __attribute__((ext_vector_type(4)));
 
+// The full-attention prologue folded into the short-split kernel for one
+// decode token (one split per KV head): the raw joint projection row and K/V
+// rows of the token, the q/k norm weights and the MRoPE arguments.  The kernel
+// normalises and rotates its query heads and its K head, appends the K/V row
+// (f16) at start_position of the cache and uses it in place of what it loaded
+// for that row; the output gate is the second half of each q_gate head.
+struct PrologueFold {
+  const float* q_gate;  // [heads][2 D]
+  const float* key;     // [kv_heads][D]
+  const float* value;   // [kv_heads][D]
+  const float* q_norm;  // [D]
+  const float* k_norm;  // [D]
+  RopeArgs rope;
+  float eps;
+};
+
 // Launches the short-split MFMA kernel (attention_decode_short.hip) for
 // head_dim 256, an f16 cache and G = heads / kv_heads in {1, 2, 4}, one
 // workgroup per (split, kv_head, token) of `grid`.
 hipError_t launch_decode_short(const DecodeParams& p, uint32_t group, dim3 grid,
                                hipStream_t stream);
+// The same kernel with the prologue folded in: p.tokens == 1, p.splits == 1,
+// p.keys_per_split == p.start_position + 1, p.query and p.gate unused; grid
+// (1, kv_heads, 1).
+hipError_t launch_decode_short_prologue(const DecodeParams& p, const PrologueFold& f,
+                                        uint32_t group, hipStream_t stream);
 
 }  // namespace decode
 }  // namespace kraken

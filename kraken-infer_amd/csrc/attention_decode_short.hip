@@ -29,18 +29,34 @@ namespace {
 // fragments stay in LDS and are read per tile, which leaves the registers for
 // the second (lo) output accumulator.
 // ---------------------------------------------------------------------------
+//
+// kFold (one decode token, one split): the attention prologue runs inside the
+// workgroup.  Its raw inputs are loaded first, then the K/V tile; waves 0..G-1
+// normalise and rotate the workgroup's query heads into LDS (read by the
+// query conversion in place of p.query), one wave does the K head and one the
+// V head: f16 into the cache row at start_position and into LDS, from where
+// the wave holding that row's tile puts it in place of the loaded row (the
+// cache row is written by this same workgroup, so what the load returned for
+// it is not used).  The output gate comes from the second half of each q_gate
+// head, loaded at the start.
+// ---------------------------------------------------------------------------
 constexpr int kSWaves = 4;
 
-template <int G>
-__global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(DecodeParams p) {
+template <int G, bool kFold>
+__global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(DecodeParams p,
+                                                                              PrologueFold f) {
   static_assert(G == 1 || G == 2 || G == 4, "query heads per KV head (rows 0..3 of a tile)");
   __shared__ __attribute__((aligned(16))) half_t s_v[kSWaves][kMTileHalfs];
   // Query fragments (hi, lo) per MFMA step, converted cooperatively.
   __shared__ __attribute__((aligned(16))) half8_t s_q[8][2][64];
   __shared__ float s_m[kSWaves][G];
   __shared__ float s_l[kSWaves][G];
+  // kFold: the new K and V rows (f16), read inside the tile loop.
+  __shared__ __attribute__((aligned(16))) half_t s_new[kFold ? 2 : 1][kFold ? kMD : 8];
   static_assert(sizeof(float) * kSWaves * G * kMD <= sizeof(s_v), "merge area");
   float(*s_o)[G * kMD] = reinterpret_cast<float(*)[G * kMD]>(&s_v[0][0]);
+  // kFold: the prepared query heads, in the V area before the tile loop uses it.
+  float(*s_qf)[kMD] = reinterpret_cast<float(*)[kMD]>(&s_v[0][0]);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -74,7 +90,32 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
   float4 qraw[2][2];
   const int qg = r16 < G ? r16 : 0;
   const float qscale = r16 < G ? p.scale_log2 : 0.0f;
-  {
+  // kFold: the prologue's inputs in the same position (wave k_wave takes the
+  // K head, v_wave the V head, waves below G a query head each).
+  constexpr int k_wave = G < 4 ? G : 0;
+  constexpr int v_wave = G < 3 ? G + 1 : 1;
+  float hv[4], hw[4], kv[4], kw[4], gate_v[G];
+  int32_t rpos[4];
+  if constexpr (kFold) {
+    if (wave < G) {
+      load_head(f.q_gate + (size_t)(kvh * G + wave) * 2u * kMD, f.q_norm, kMD, lane, hv, hw);
+    }
+    if (wave == k_wave) {
+      load_head(f.key + (size_t)kvh * kMD, f.k_norm, kMD, lane, kv, kw);
+    }
+    if (wave == v_wave) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kv[i] = f.value[(size_t)kvh * kMD + lane + 64 * i];
+      }
+    }
+    // Output element tid of head k (the merge's index) and its gate.
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      gate_v[k] = f.q_gate[(size_t)(kvh * G + k) * 2u * kMD + kMD + tid];
+    }
+    rope_positions(f.rope, 0, rpos);
+  } else {
     const float* qh = p.query + ((size_t)token * p.heads + kvh * G + qg) * kMD + 8 * kq;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -109,6 +150,50 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
   }
   __builtin_amdgcn_sched_barrier(0);
 
+  const uint32_t new_key = p.start_position;  // kFold: the appended row
+  if constexpr (kFold) {
+    const size_t cache_row =
+      ((size_t)p.layer * p.capacity_tokens + new_key) * row_stride + (size_t)kvh * kMD;
+    if (wave < G || wave == k_wave) {
+      double sn[4], cs[4];
+      rope_angles(f.rope, rpos, lane, sn, cs);
+      float r[4];
+      if (wave < G) {
+        norm_rope(hv, hw, kMD, f.eps, f.rope.n_dims, sn, cs, lane, r);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s_qf[wave][lane + 64 * i] = r[i];
+        }
+      }
+      if (wave == k_wave) {
+        norm_rope(kv, kw, kMD, f.eps, f.rope.n_dims, sn, cs, lane, r);
+        half_t* dst = static_cast<half_t*>(const_cast<void*>(p.key_cache)) + cache_row;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const half_t h = static_cast<half_t>(r[i]);
+          s_new[0][lane + 64 * i] = h;
+          dst[lane + 64 * i] = h;
+        }
+      }
+    }
+    if (wave == v_wave) {
+      half_t* dst = static_cast<half_t*>(const_cast<void*>(p.value_cache)) + cache_row;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const half_t h = static_cast<half_t>(kv[i]);
+        s_new[1][lane + 64 * i] = h;
+        dst[lane + 64 * i] = h;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float* qh = &s_qf[qg][32 * (2 * wave + i) + 8 * kq];
+      qraw[i][0] = *reinterpret_cast<const float4*>(qh);
+      qraw[i][1] = *reinterpret_cast<const float4*>(qh + 4);
+    }
+  }
+
   // Query fragments (B operand of S^T) in the split fp16 form (split_f16:
   // hi, and lo scaled by 2^11), so that K (exact in f16) times hi plus 2^-11
   // times K lo reproduces the f32 product to about 2^-21 relative.
@@ -127,7 +212,7 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
     s_q[2 * wave + i][0][lane] = hi8;
     s_q[2 * wave + i][1][lane] = lo8;
   }
-  __syncthreads();
+  __syncthreads();  // (kFold: also every wave is done reading s_qf)
 
   float m[G];  // wave-uniform reference max per head (log2 domain)
 #pragma unroll
@@ -149,6 +234,21 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
   }
   half_t* vs = &s_v[wave][0];
   for (; t < ntiles; t += kSWaves) {
+    if constexpr (kFold) {
+      if (t == new_key / kMTile) {  // wave-uniform: put the new row in place
+        const uint32_t row = new_key % kMTile;
+        const half8_t* nk = reinterpret_cast<const half8_t*>(&s_new[0][0]);
+        const u32x4_t* nv = reinterpret_cast<const u32x4_t*>(&s_new[1][0]);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          kf[s] = (uint32_t)r16 == row ? nk[4 * s + kq] : kf[s];
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          vr[c] = 2u * c + (uint32_t)(lane >> 5) == row ? nv[lane & 31] : vr[c];
+        }
+      }
+    }
     // V rows of tile t into the wave's LDS region, 16-byte chunks XOR-swizzled
     // by 2 (row & 3) so that the transposing reads are free of bank conflicts.
     // The region's previous reads were consumed by last tile's MFMAs.
@@ -291,7 +391,12 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
       acc = fmaf(wt, s_o[w][idx], acc);
       den = fmaf(wt, s_l[w][g], den);
     }
-    if (p.splits == 1) {
+    if constexpr (kFold) {
+      const size_t out_index = ((size_t)kvh * G + k) * kMD + tid;
+      float r = den == 0.0f ? 0.0f : acc / den;
+      r *= sigmoidf_acc(gate_v[k]);
+      p.output[out_index] = r;
+    } else if (p.splits == 1) {
       write_final<kMD, G>(p, token, kvh, idx, den, acc);
     } else {
       po[idx] = acc;
@@ -307,15 +412,39 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
 
 hipError_t launch_decode_short(const DecodeParams& p, uint32_t group, dim3 grid,
                                hipStream_t stream) {
+  const PrologueFold none{};
   switch (group) {
     case 1:
-      attention_decode_short_kernel<1><<<grid, 64 * kSWaves, 0, stream>>>(p);
+      attention_decode_short_kernel<1, false><<<grid, 64 * kSWaves, 0, stream>>>(p, none);
       break;
     case 2:
-      attention_decode_short_kernel<2><<<grid, 64 * kSWaves, 0, stream>>>(p);
+      attention_decode_short_kernel<2, false><<<grid, 64 * kSWaves, 0, stream>>>(p, none);
       break;
     case 4:
-      attention_decode_short_kernel<4><<<grid, 64 * kSWaves, 0, stream>>>(p);
+      attention_decode_short_kernel<4, false><<<grid, 64 * kSWaves, 0, stream>>>(p, none);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_short_prologue(const DecodeParams& p, const PrologueFold& f,
+                                        uint32_t group, hipStream_t stream) {
+  if (p.tokens != 1 || p.splits != 1 || p.keys_per_split != p.start_position + 1u ||
+      p.start_position >= p.capacity_tokens || p.heads != group * p.kv_heads) {
+    return hipErrorInvalidValue;
+  }
+  const dim3 grid(1, p.kv_heads, 1);
+  switch (group) {
+    case 1:
+      attention_decode_short_kernel<1, true><<<grid, 64 * kSWaves, 0, stream>>>(p, f);
+      break;
+    case 2:
+      attention_decode_short_kernel<2, true><<<grid, 64 * kSWaves, 0, stream>>>(p, f);
+      break;
+    case 4:
+      attention_decode_short_kernel<4, true><<<grid, 64 * kSWaves, 0, stream>>>(p, f);
       break;
     default:
       return hipErrorInvalidValue;

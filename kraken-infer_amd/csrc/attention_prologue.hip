@@ -11,6 +11,7 @@
 // chain's bit for bit.
 #include <hip/hip_runtime.h>
 
+#include "attention_prologue_common.hpp"
 #include "context_internal.hpp"
 #include "device_common.hpp"
 
@@ -46,65 +47,16 @@ __global__ __launch_bounds__(256) void attention_prologue_kernel(PrologueArgs a)
   const float* src = is_q ? a.q_gate + ((size_t)t * a.heads + head) * 2u * d_head
                           : a.key + (size_t)t * kv_dim + (size_t)head * d_head;
   const float* weight = is_q ? a.q_norm : a.k_norm;
-
-  // RMSNorm: lane holds elements lane + 64 i (the layout of rms_norm_heads_kernel).
-  float v[4];
-  float sum = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t d = lane + 64u * i;
-    v[i] = d < d_head ? src[d] : 0.0f;
-    sum = fmaf(v[i], v[i], sum);
-  }
-  sum = wave_sum(sum);
-  const float scale = 1.0f / sqrtf(sum / (float)d_head + a.eps);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t d = lane + 64u * i;
-    v[i] = d < d_head ? v[i] * scale * weight[d] : 0.0f;
-  }
-
-  // MRoPE on pairs (p, p + n_dims / 2), p < n_dims / 2.  Each lane fetches the
-  // partner of each of its elements from the lane and register that hold it.
-  const uint32_t half_dims = a.n_dims / 2u;
-  const uint32_t sections = a.s0 + a.s1 + a.s2 + a.s3;
+  const RopeArgs rope{a.positions, a.mrope_start, a.tokens, a.n_dims, a.s0, a.s1, a.s2, a.s3,
+                      a.theta};
+  float v[4], w[4];
+  load_head(src, weight, d_head, lane, v, w);
+  int32_t pos[4];
+  rope_positions(rope, t, pos);
+  double sn[4], cs[4];
+  rope_angles(rope, pos, lane, sn, cs);
   float r[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t e = lane + 64u * i;
-    const uint32_t p = e < half_dims ? e + half_dims : (e < a.n_dims ? e - half_dims : e);
-    const int src_lane = (int)(p & 63u);
-    const uint32_t src_reg = p >> 6;
-    float partner = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float x = __shfl(v[j], src_lane, 64);
-      partner = src_reg == (uint32_t)j ? x : partner;
-    }
-    r[i] = v[i];
-    if (e < a.n_dims) {
-      const uint32_t pair = e < half_dims ? e : e - half_dims;
-      const uint32_t sector = pair % sections;
-      uint32_t row = 3;
-      if (sector < a.s0) {
-        row = 0;
-      } else if (sector < a.s0 + a.s1) {
-        row = 1;
-      } else if (sector < a.s0 + a.s1 + a.s2) {
-        row = 2;
-      }
-      const int32_t pos = a.positions != nullptr
-                            ? a.positions[t + (size_t)a.tokens * row]
-                            : (int32_t)(a.mrope_start + t);
-      const double freq = pow((double)a.theta, -(double)(2u * pair) / (double)a.n_dims);
-      const double angle = (double)pos * freq;
-      double sn, cs;
-      sincos(angle, &sn, &cs);
-      const double x0 = e < half_dims ? v[i] : partner;
-      const double x1 = e < half_dims ? partner : v[i];
-      r[i] = e < half_dims ? (float)(x0 * cs - x1 * sn) : (float)(x1 * cs + x0 * sn);
-    }
-  }
+  norm_rope(v, w, d_head, a.eps, a.n_dims, sn, cs, lane, r);
 
   if (is_q) {
     float* q_out = a.query_out + ((size_t)t * a.heads + head) * d_head;

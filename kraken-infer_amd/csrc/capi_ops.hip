@@ -794,13 +794,19 @@ KRAKEN_API int kraken_hip_mrope_f32_in_place(kraken_hip_context* ctx, kraken_buf
   return finish_launch(ctx, "HIP MRoPE command failed: ");
 }
 
-KRAKEN_API int kraken_hip_qwen35_attention_prologue_f16_kv(
-  kraken_hip_context* ctx, kraken_buffer q_gate, kraken_buffer key, kraken_buffer value,
-  kraken_buffer q_norm, kraken_buffer k_norm, kraken_buffer positions,
-  size_t mrope_start_position, kraken_buffer key_cache, kraken_buffer value_cache, size_t layer,
-  size_t start_position, size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads,
-  size_t head_dim, size_t n_dims, size_t section_0, size_t section_1, size_t section_2,
-  size_t section_3, float theta, float eps, kraken_buffer query_out, kraken_buffer gate_out) {
+namespace {
+
+// Validation and argument block of the attention prologue entries.
+int prologue_args(kraken_hip_context* ctx, const kraken_buffer& q_gate, const kraken_buffer& key,
+                  const kraken_buffer& value, const kraken_buffer& q_norm,
+                  const kraken_buffer& k_norm, const kraken_buffer& positions,
+                  size_t mrope_start_position, const kraken_buffer& key_cache,
+                  const kraken_buffer& value_cache, size_t layer, size_t start_position,
+                  size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads,
+                  size_t head_dim, size_t n_dims, size_t section_0, size_t section_1,
+                  size_t section_2, size_t section_3, float theta, float eps,
+                  const kraken_buffer& query_out, const kraken_buffer& gate_out,
+                  PrologueArgs& a) {
   KRAKEN_TRY(check_context(ctx));
   if (tokens == 0 || heads == 0 || kv_heads == 0 || head_dim == 0 || capacity_tokens == 0) {
     return invalid("HIP attention prologue dimensions must be positive");
@@ -861,7 +867,7 @@ KRAKEN_API int kraken_hip_qwen35_attention_prologue_f16_kv(
     }
   }
 
-  PrologueArgs a{};
+  a = PrologueArgs{};
   a.q_gate = static_cast<const float*>(q_gate.data);
   a.key = static_cast<const float*>(key.data);
   a.value = static_cast<const float*>(value.data);
@@ -885,12 +891,73 @@ KRAKEN_API int kraken_hip_qwen35_attention_prologue_f16_kv(
   a.s3 = (uint32_t)section_3;
   a.theta = theta;
   a.eps = eps;
+  return KRAKEN_OK;
+}
+
+}  // namespace
+
+KRAKEN_API int kraken_hip_qwen35_attention_prologue_f16_kv(
+  kraken_hip_context* ctx, kraken_buffer q_gate, kraken_buffer key, kraken_buffer value,
+  kraken_buffer q_norm, kraken_buffer k_norm, kraken_buffer positions,
+  size_t mrope_start_position, kraken_buffer key_cache, kraken_buffer value_cache, size_t layer,
+  size_t start_position, size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads,
+  size_t head_dim, size_t n_dims, size_t section_0, size_t section_1, size_t section_2,
+  size_t section_3, float theta, float eps, kraken_buffer query_out, kraken_buffer gate_out) {
+  PrologueArgs a{};
+  KRAKEN_TRY(prologue_args(ctx, q_gate, key, value, q_norm, k_norm, positions,
+                           mrope_start_position, key_cache, value_cache, layer, start_position,
+                           tokens, capacity_tokens, heads, kv_heads, head_dim, n_dims, section_0,
+                           section_1, section_2, section_3, theta, eps, query_out, gate_out, a));
   KRAKEN_TRY(begin_launch(ctx));
   const hipError_t e = launch_attention_prologue(a, ctx->stream);
   if (e != hipSuccess) {
     return internal(std::string("HIP attention prologue launch failed: ") + hipGetErrorString(e));
   }
   return finish_launch(ctx, "HIP attention prologue command failed: ");
+}
+
+// The prologue followed by the gated attention over the cache it appends to
+// (the fused op order of run_full_attention_chunk, qwen35_runtime.cpp:
+// 3229-3355).  One decode token within the single-split range runs as one
+// launch; anything else as the prologue entry then the gated F16 KV attention
+// entry, through query_out and gate_out.
+KRAKEN_API int kraken_hip_qwen35_attention_prologue_gated_f16_kv(
+  kraken_hip_context* ctx, kraken_buffer q_gate, kraken_buffer key, kraken_buffer value,
+  kraken_buffer q_norm, kraken_buffer k_norm, kraken_buffer positions,
+  size_t mrope_start_position, kraken_buffer key_cache, kraken_buffer value_cache, size_t layer,
+  size_t start_position, size_t tokens, size_t capacity_tokens, size_t heads, size_t kv_heads,
+  size_t head_dim, size_t n_dims, size_t section_0, size_t section_1, size_t section_2,
+  size_t section_3, float theta, float eps, kraken_buffer query_out, kraken_buffer gate_out,
+  kraken_buffer output) {
+  PrologueArgs a{};
+  KRAKEN_TRY(prologue_args(ctx, q_gate, key, value, q_norm, k_norm, positions,
+                           mrope_start_position, key_cache, value_cache, layer, start_position,
+                           tokens, capacity_tokens, heads, kv_heads, head_dim, n_dims, section_0,
+                           section_1, section_2, section_3, theta, eps, query_out, gate_out, a));
+  KRAKEN_TRY(validate_f32(output, tokens * heads * head_dim, "attention prologue output"));
+  KRAKEN_TRY(check_u32(layer, "attention prologue layer"));
+  KRAKEN_TRY(check_u32(capacity_tokens, "attention prologue capacity"));
+  const char* order = std::getenv("KRAKEN_QWEN35_ATTENTION_PROLOGUE");
+  if (order == nullptr || std::strcmp(order, "two_launch") != 0) {
+    KRAKEN_TRY(begin_launch(ctx));
+    const hipError_t e = launch_attention_prologue_decode(
+      a, (uint32_t)layer, (uint32_t)start_position, (uint32_t)capacity_tokens,
+      static_cast<float*>(output.data), ctx->stream);
+    if (e == hipSuccess) {
+      return finish_launch(ctx, "HIP attention prologue decode command failed: ");
+    }
+    if (e != hipErrorNotSupported) {
+      return internal(std::string("HIP attention prologue decode launch failed: ") +
+                      hipGetErrorString(e));
+    }
+  }
+  KRAKEN_TRY(kraken_hip_qwen35_attention_prologue_f16_kv(
+    ctx, q_gate, key, value, q_norm, k_norm, positions, mrope_start_position, key_cache,
+    value_cache, layer, start_position, tokens, capacity_tokens, heads, kv_heads, head_dim,
+    n_dims, section_0, section_1, section_2, section_3, theta, eps, query_out, gate_out));
+  return attention_entry(ctx, "gated F16 KV batched attention", true, query_out, key_cache,
+                         value_cache, &gate_out, layer, start_position, tokens, capacity_tokens,
+                         heads, kv_heads, head_dim, output);
 }
 
 KRAKEN_API int kraken_hip_copy_f32_rows_to_f16(kraken_hip_context* ctx, kraken_buffer source,

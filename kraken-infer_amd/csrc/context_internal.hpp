@@ -297,6 +297,17 @@ struct PrologueArgs {
   float theta, eps;
 };
 hipError_t launch_attention_prologue(const PrologueArgs& a, hipStream_t stream);
+// The prologue and the gated decode attention of one token in one launch
+// (attention_decode.hip, attention_decode_short.hip): a.query_out and
+// a.gate_out are not written; output [heads][head_dim] receives what
+// launch_attention_decode with the prologue's query and gate would write.
+// Returns hipErrorNotSupported, launching nothing, outside the folded kernel's
+// contract: one token, head_dim 256, heads / kv_heads in {1, 2, 4}, at most
+// 256 keys (start_position < 256), 16-byte aligned caches and output, and no
+// KRAKEN_DECODE_KERNEL (other than "short") or KRAKEN_DECODE_KEYS_PER_SPLIT.
+hipError_t launch_attention_prologue_decode(const PrologueArgs& a, uint32_t layer,
+                                            uint32_t start_position, uint32_t capacity_tokens,
+                                            float* output, hipStream_t stream);
 
 // K-quant projections (kquant.hip).  format: 0 = Q4_K, 1 = Q5_K, 2 = Q6_K;
 // weights are row-major blocks (cols / 256 per row).  Up to

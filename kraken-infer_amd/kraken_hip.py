@@ -75,6 +75,8 @@ SIGNATURES = {
     "kraken_hip_mrope_f32_in_place": [_B, _B] + [_sz] * 8 + [_f],
     "kraken_hip_qwen35_attention_prologue_f16_kv": [_B] * 6 + [_sz, _B, _B] + [_sz] * 12
                                                    + [_f, _f, _B, _B],
+    "kraken_hip_qwen35_attention_prologue_gated_f16_kv": [_B] * 6 + [_sz, _B, _B] + [_sz] * 12
+                                                         + [_f, _f, _B, _B, _B],
     "kraken_hip_copy_f32_rows_to_f16": [_B, _B] + [_sz] * 6,
     "kraken_hip_copy_f32_rows": [_B, _B] + [_sz] * 6,
     "kraken_hip_copy_f16_rows": [_B, _B] + [_sz] * 6,

@@ -348,6 +348,26 @@ def test_prologue_generated_positions_must_fit_int32(vctx):
     assert code == kh.INVALID_ARGUMENT and "exceeds int32 range" in msg
 
 
+def test_prologue_gated_accepts_valid(vctx):
+    """The one-launch prologue + gated attention entry takes the prologue's
+    arguments and an output [tokens][heads][head_dim]."""
+    for kw in ({}, dict(tokens=1, start=15), dict(tokens=1, start=255, cap=300),
+               dict(d=128, n_dims=128, heads=4, kv_heads=4)):
+        tokens, heads, d = kw.get("tokens", 4), kw.get("heads", 8), kw.get("d", 256)
+        args = prologue_args(**kw) + (fake(4 * tokens * heads * d),)
+        code, msg = status(vctx, "qwen35_attention_prologue_gated_f16_kv", *args)
+        assert (code, msg) == (kh.UNAVAILABLE, ACCEPTED), kw
+
+
+def test_prologue_gated_rejects(vctx):
+    args = prologue_args(tokens=1, start=3) + (fake(4 * 8 * 256 - 4),)
+    code, msg = status(vctx, "qwen35_attention_prologue_gated_f16_kv", *args)
+    assert code == kh.INVALID_ARGUMENT and "attention prologue output buffer is too small" in msg
+    args = prologue_args(tokens=1, start=3, n_dims=63) + (fake(4 * 8 * 256),)
+    code, msg = status(vctx, "qwen35_attention_prologue_gated_f16_kv", *args)
+    assert code == kh.INVALID_ARGUMENT and "MRoPE dimensions are invalid" in msg
+
+
 # ------------------------------------------------ fused ragged GDN layer --
 
 def gdn_layer_args(b=4, hk=16, hv=16, d=128, k=4, prepare=True, **sizes):

@@ -104,3 +104,85 @@ def test_prologue_matches_unfused_chain_and_oracle(hip_ctx, case):
     np.testing.assert_array_equal(fg, og)
     assert np.abs(fkc.astype(np.int32) - okc.astype(np.int32)).max() <= 1
     np.testing.assert_array_equal(fvc, ovc)
+
+
+# ------------------------------------- prologue folded into decode attention --
+# kraken_hip_qwen35_attention_prologue_gated_f16_kv: one decode token with
+# head_dim 256, G in {1, 2, 4} and at most 256 keys runs as one launch (the
+# short-split decode kernel normalises and rotates its heads, appends the K/V
+# row and uses it in place of the loaded row); other shapes run the prologue
+# entry then the gated attention entry.  Either way the output and both caches
+# equal, bit for bit, those of the two entries called one after the other, and
+# the output is within the attention tests' tolerance of the oracle chain.
+GATED_CASES = [
+    # heads, kv_heads, tokens, start, cap, layers, layer, explicit positions
+    (8, 2, 1, 0, 8, 1, 0, False),
+    (8, 2, 1, 15, 40, 2, 1, False),
+    (8, 2, 1, 16, 40, 2, 1, True),
+    (8, 2, 1, 37, 64, 2, 1, False),
+    (8, 2, 1, 255, 300, 1, 0, False),   # 256 keys: the last one-launch length
+    (8, 2, 1, 256, 300, 1, 0, False),   # 257 keys: two launches (split decode)
+    (4, 4, 1, 20, 32, 1, 0, False),     # G = 1
+    (8, 4, 1, 70, 80, 1, 0, True),      # G = 2
+    (16, 2, 1, 5, 8, 1, 0, False),      # G = 8: two launches
+    (8, 2, 3, 9, 16, 1, 0, False),      # three tokens: two launches
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", GATED_CASES)
+def test_prologue_gated_equals_two_entries_and_oracle(hip_ctx, case):
+    heads, kv_heads, tokens, start, cap, layers, layer, explicit = case
+    print(f"prologue gated {case}", flush=True)
+    d, n_dims, sections, theta = 256, 64, (11, 11, 10, 0), 1e7
+    x = chain_inputs(100 + start, tokens, heads, kv_heads, d, cap, layers)
+    if explicit:
+        pos = np.random.default_rng(start).integers(0, 5000, size=4 * tokens).astype(np.int32)
+    else:
+        pos = oracle.make_mrope_positions(start, tokens)
+    ctx = hip_ctx
+    n = tokens * heads * d
+
+    def run(one_call):
+        b = {k: ctx.buffer(v) for k, v in x.items()}
+        pos_b = ctx.buffer(pos) if explicit else None
+        qo = ctx.buffer(np.full(n, 3.0, np.float32))
+        go = ctx.buffer(np.full(n, 3.0, np.float32))
+        out = ctx.buffer(byte_size=4 * n)
+        args = (b["qg"], b["key"], b["value"], b["q_norm"], b["k_norm"], pos_b, start, b["kc"],
+                b["vc"], layer, start, tokens, cap, heads, kv_heads, d, n_dims, *sections, theta,
+                EPS, qo, go)
+        if one_call:
+            ctx.qwen35_attention_prologue_gated_f16_kv(*args, out)
+        else:
+            ctx.qwen35_attention_prologue_f16_kv(*args)
+            ctx.attention_f32_batched_f16_kv_gated(qo, b["kc"], b["vc"], go, layer, start, tokens,
+                                                   cap, heads, kv_heads, d, out)
+        return (out.download(n), b["kc"].download(dtype=np.uint16),
+                b["vc"].download(dtype=np.uint16), qo.download(n))
+
+    got, gkc, gvc, gq = run(True)
+    want, wkc, wvc, _ = run(False)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    np.testing.assert_array_equal(gkc, wkc)
+    np.testing.assert_array_equal(gvc, wvc)
+    one_launch = tokens == 1 and heads // kv_heads in (1, 2, 4) and start < 256
+    # The one-launch form leaves the two-launch scratch as it was.
+    assert np.all(gq == 3.0) == one_launch
+
+    # The oracle chain: prologue, attention over the updated caches, gate.
+    kv_dim = kv_heads * d
+    qg = x["qg"]
+    oq = np.ascontiguousarray(qg[:, :, 0, :]).ravel()
+    og = np.ascontiguousarray(qg[:, :, 1, :]).ravel()
+    oq = oracle.qk_norm_f32_batched(oq, x["q_norm"], tokens, heads, d, EPS)
+    ok = oracle.qk_norm_f32_batched(x["key"].ravel(), x["k_norm"], tokens, kv_heads, d, EPS)
+    oq = oracle.mrope(oq, pos, tokens, heads, d, n_dims, sections, theta)
+    ok = oracle.mrope(ok, pos, tokens, kv_heads, d, n_dims, sections, theta)
+    off = (layer * cap + start) * kv_dim
+    okc = oracle.copy_f32_rows_to_f16(ok, x["kc"], tokens, kv_dim, kv_dim, 0, kv_dim, off)
+    ovc = oracle.copy_f32_rows_to_f16(x["value"].ravel(), x["vc"], tokens, kv_dim, kv_dim, 0,
+                                      kv_dim, off)
+    ref = oracle.attention_batched(oq, okc, ovc, layer, start, tokens, cap, heads, kv_heads, d)
+    ref = oracle.sigmoid_gate_mul(ref, og)
+    np.testing.assert_allclose(got, ref, rtol=2e-3, atol=1e-3)
