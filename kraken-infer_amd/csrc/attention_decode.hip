@@ -437,10 +437,10 @@ __global__ __launch_bounds__((64 * RowShape<D, KV>::W)) void attention_decode_ke
     if (p.splits == 1) {
       write_final<D, G>(p, token, kvh, idx, den, acc);
     } else {
-      store_partial(&po[idx], acc);
+      store_through(&po[idx], acc);
       if (idx % D == 0) {
-        store_partial(&pml[g * 2 + 0], mx);
-        store_partial(&pml[g * 2 + 1], den);
+        store_through(&pml[g * 2 + 0], mx);
+        store_through(&pml[g * 2 + 1], den);
       }
     }
   }
@@ -743,10 +743,10 @@ __global__ __launch_bounds__(64 * kMWaves) void attention_decode_mfma_kernel(Dec
     if (p.splits == 1) {
       write_final<kMD, G>(p, token, kvh, idx, den, acc);
     } else {
-      store_partial(&po[idx], acc);
+      store_through(&po[idx], acc);
       if (idx % kMD == 0) {
-        store_partial(&pml[g * 2 + 0], mx);
-        store_partial(&pml[g * 2 + 1], den);
+        store_through(&pml[g * 2 + 0], mx);
+        store_through(&pml[g * 2 + 1], den);
       }
     }
   }

@@ -399,10 +399,10 @@ __global__ __launch_bounds__(64 * kSWaves) void attention_decode_short_kernel(De
     } else if (p.splits == 1) {
       write_final<kMD, G>(p, token, kvh, idx, den, acc);
     } else {
-      store_partial(&po[idx], acc);
+      store_through(&po[idx], acc);
       if (idx % kMD == 0) {
-        store_partial(&pml[g * 2 + 0], mx);
-        store_partial(&pml[g * 2 + 1], den);
+        store_through(&pml[g * 2 + 0], mx);
+        store_through(&pml[g * 2 + 1], den);
       }
     }
   }

@@ -243,14 +243,16 @@ __device__ __forceinline__ u32x4_t buffer_load_nt_b128(__amdgpu_buffer_rsrc_t rs
                             __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)offset, 0, 2));
 }
 
-// Stores of the decode kernels' split partials, which a later launch merges:
-// device scope (a vector store with SC1), so they are written through the L2
-// instead of staying there dirty for the kernel's end-of-launch release to
-// write back (C1 at L=4096: 10.37 -> 10.03 us per step).  The merge launch
-// reads them from memory in either case: its workgroups run on other XCDs,
-// whose L2s do not hold them.  (The flash kernel's 16 MB of f16 partials are
-// slower written this way, P=7168 81.5 -> 86.9 us, and keep plain stores.)
-__device__ __forceinline__ void store_partial(float* at, float v) {
+// A store written through the L2 to memory (device scope: a vector store with
+// SC1), for results a later launch reads: they do not stay dirty in the L2 for
+// the kernel's end-of-launch release to write back after the last wave, and
+// the next launch, whose workgroups run on other XCDs, reads them from memory
+// in either case.  Measured: the decode split partials (C1 at L=4096
+// 10.37 -> 10.03 us per step) and the fp16 GEMM's f32 output (Q5_K
+// 6144 x 1024 at 1024 tokens 34.7 -> 32.9 us).  Not a win everywhere: the
+// flash kernel's 16 MB of f16 partials (P=7168 81.5 -> 86.9 us) and the GDN
+// decode state (2.54 -> 2.82 us) keep plain stores.
+__device__ __forceinline__ void store_through(float* at, float v) {
   __hip_atomic_store(at, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

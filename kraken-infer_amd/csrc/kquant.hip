@@ -1096,7 +1096,7 @@ __device__ __forceinline__ void f32_to_f16_8(const float* in, half_t* out, uint6
   const half8_t h = {static_cast<half_t>(a.x), static_cast<half_t>(a.y), static_cast<half_t>(a.z),
                      static_cast<half_t>(a.w), static_cast<half_t>(b.x), static_cast<half_t>(b.y),
                      static_cast<half_t>(b.z), static_cast<half_t>(b.w)};
-  reinterpret_cast<half8_t*>(out)[i] = h;
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, h), reinterpret_cast<u32x4_t*>(out) + i);
 }
 
 // The two-pass GEMM's first pass, one launch: workgroups [0, convert_blocks)
@@ -1148,7 +1148,9 @@ __global__ __launch_bounds__(256) void kq_dequant_f16_kernel(const uint8_t* weig
   for (int j = 0; j < 4; ++j) {
     const uint32_t piece = (uint32_t)j * 256u + threadIdx.x;  // 16-byte piece, 32 per block
     if (piece / 32u < valid) {
-      dst[piece] = reinterpret_cast<const half8_t*>(s_out)[piece];
+      // Nontemporal: the GEMM launch reads the fp16 weights once, from memory.
+      __builtin_nontemporal_store(reinterpret_cast<const u32x4_t*>(s_out)[piece],
+                                  reinterpret_cast<u32x4_t*>(dst) + piece);
     }
   }
 }
@@ -1294,7 +1296,7 @@ __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const
       for (int e = 0; e < 16; ++e) {
         const uint32_t row = m0 + (TM / 2) * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
         if (row < m && col < n) {
-          c[(uint64_t)row * n + col] = acc[i][j][e];
+          store_through(&c[(uint64_t)row * n + col], acc[i][j][e]);
         }
       }
     }
@@ -1460,7 +1462,7 @@ __global__ __launch_bounds__(256) void gemm_f16_pipe_kernel(const half_t* x, con
       for (int e = 0; e < 16; ++e) {
         const uint32_t row = m0 + (TM / 2) * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
         if (row < m && col < n) {
-          c[(uint64_t)row * n + col] = acc[i][j][e];
+          store_through(&c[(uint64_t)row * n + col], acc[i][j][e]);
         }
       }
     }
@@ -1627,7 +1629,7 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(const float* x, const uint
       for (int e = 0; e < 16; ++e) {
         const uint32_t row = m0 + (TM / 2) * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
         if (row < m && col < n) {
-          c[(uint64_t)row * n + col] = acc[i][j][e];
+          store_through(&c[(uint64_t)row * n + col], acc[i][j][e]);
         }
       }
     }
