@@ -739,6 +739,21 @@ class HipContext {
       ctx_, ggml_type, weight.raw(), rows, cols, input.raw(), norm_weight.raw(), eps, up.raw(),
       residual.raw(), output.raw()));
   }
+  // Up to four K-quant matmuls over one input [tokens][cols] (one launch when
+  // their type allows it; see kraken_hip.h).
+  [[nodiscard]] Status kquant_matmul_multi_f32(std::size_t count, const std::uint32_t* ggml_types,
+                                               const HipBuffer* const* weights,
+                                               const std::size_t* rows, std::size_t cols,
+                                               std::size_t tokens, const HipBuffer& input,
+                                               HipBuffer* const* outputs) const {
+    kraken_buffer w[4], out[4];
+    for (std::size_t i = 0; i < count && i < 4; ++i) {
+      w[i] = weights[i]->raw();
+      out[i] = outputs[i]->raw();
+    }
+    return Status::from_code(kraken_hip_kquant_matmul_multi_f32(ctx_, count, ggml_types, w, rows,
+                                                                cols, tokens, input.raw(), out));
+  }
   // Up to four fused GEMVs over one input in one launch; entries of `weights`,
   // `outputs` and `residuals` (nullptr for none) per matrix.
   [[nodiscard]] Status kquant_matvec_multi_f32(std::size_t count, const std::uint32_t* ggml_types,

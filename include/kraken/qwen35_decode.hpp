@@ -85,6 +85,39 @@ struct ModelWeights {
   }
 }
 
+// Up to four projections of the same input [tokens][cols] (one launch where
+// kraken_hip_kquant_matmul_multi_f32 allows; the same checks as project).
+[[nodiscard]] inline Status project_group(const HipContext& ctx, std::size_t count,
+                                          const Tensor* const* w, const HipBuffer& input,
+                                          std::size_t tokens, HipBuffer* const* outputs) {
+  if (tokens == 0) {
+    return Status::invalid_argument("Qwen3.5 matmul requires tokens");
+  }
+  if (count == 0 || count > 4) {
+    return Status::invalid_argument("Qwen3.5 grouped matmul takes 1 to 4 weights");
+  }
+  std::uint32_t types[4];
+  const HipBuffer* bufs[4];
+  std::size_t rows[4];
+  for (std::size_t i = 0; i < count; ++i) {
+    if (w[i]->buffer == nullptr || w[i]->rows == 0 || w[i]->cols == 0) {
+      return Status::invalid_argument("Qwen3.5 matmul weight is missing");
+    }
+    if (w[i]->type != TensorType::q4_k && w[i]->type != TensorType::q5_k &&
+        w[i]->type != TensorType::q6_k) {
+      return Status::invalid_argument("Qwen3.5 matmul weight type is not a K-quant type");
+    }
+    if (w[i]->cols != w[0]->cols) {
+      return Status::invalid_argument("Qwen3.5 grouped matmul weights differ in cols");
+    }
+    types[i] = static_cast<std::uint32_t>(w[i]->type);
+    bufs[i] = w[i]->buffer;
+    rows[i] = w[i]->rows;
+  }
+  return ctx.kquant_matmul_multi_f32(count, types, bufs, rows, w[0]->cols, tokens, input,
+                                     outputs);
+}
+
 // Device buffers one decode step reuses; sized for the plan on first use.
 class DecodeScratch {
  public:

@@ -112,9 +112,9 @@ namespace detail {
 // tokens - 1; on return s.hidden holds the chunk's output of the last layer.
 // Recurrent row 0 and the F16 KV cache of `cache` are read and advanced.  The
 // layer cores follow `order` (OpOrder::reference: the reference's separate ops;
-// OpOrder::fused: the fused conv/recurrence/epilogue and attention entries);
-// the norms, projections, residual adds and SwiGLU are the reference's ops in
-// both.
+// OpOrder::fused: the fused conv/recurrence/epilogue and attention entries, and
+// the z / beta / alpha and FFN up / gate projections as grouped matmuls); the
+// norms, residual adds and SwiGLU are the reference's ops in both.
 [[nodiscard]] inline Status enqueue_prefill_chunk(const HipContext& ctx,
                                                   const ExecutionPlan& plan, DeviceCache& cache,
                                                   const ModelWeights& w, PrefillScratch& s,
@@ -147,9 +147,16 @@ namespace detail {
       // qwen35_runtime.cpp:2720-2745 projections, the core, :3010-3034 ssm_out
       // and the residual.
       if (r.is_ok()) r = proj(l.qkv, s.normed, s.a);
-      if (r.is_ok()) r = proj(l.gate, s.normed, s.b);
-      if (r.is_ok()) r = proj(l.beta, s.normed, s.c);
-      if (r.is_ok()) r = proj(l.alpha, s.normed, s.d);
+      if (r.is_ok() && order == OpOrder::fused) {
+        // z, beta and alpha share the normed input: one launch where their types allow.
+        const Tensor* zba[3] = {&l.gate, &l.beta, &l.alpha};
+        HipBuffer* outs[3] = {&s.b, &s.c, &s.d};
+        r = project_group(ctx, 3, zba, s.normed, tokens, outs);
+      } else {
+        if (r.is_ok()) r = proj(l.gate, s.normed, s.b);
+        if (r.is_ok()) r = proj(l.beta, s.normed, s.c);
+        if (r.is_ok()) r = proj(l.alpha, s.normed, s.d);
+      }
       if (r.is_ok()) {
         r = run_linear_attention_chunk(ctx, plan, cache, l.linear, kind_index, 0, s.a, s.b, s.c,
                                        s.d, tokens, eps, order, s.layer_ws, s.attn);
@@ -173,8 +180,14 @@ namespace detail {
     if (r.is_ok()) {
       r = ctx.rms_norm_f32_f32_batched(s.hidden, *l.post_attention_norm, tokens, h, eps, s.normed);
     }
-    if (r.is_ok()) r = proj(l.ffn_up, s.normed, s.ffn_up);
-    if (r.is_ok()) r = proj(l.ffn_gate, s.normed, s.ffn_gate);
+    if (r.is_ok() && order == OpOrder::fused) {
+      const Tensor* ug[2] = {&l.ffn_up, &l.ffn_gate};
+      HipBuffer* outs[2] = {&s.ffn_up, &s.ffn_gate};
+      r = project_group(ctx, 2, ug, s.normed, tokens, outs);
+    } else {
+      if (r.is_ok()) r = proj(l.ffn_up, s.normed, s.ffn_up);
+      if (r.is_ok()) r = proj(l.ffn_gate, s.normed, s.ffn_gate);
+    }
     if (r.is_ok()) r = ctx.silu_mul_f32_in_place(s.ffn_gate, s.ffn_up, tokens * l.ffn_gate.rows);
     if (r.is_ok()) r = proj(l.ffn_down, s.ffn_gate, s.a);
     if (r.is_ok()) r = ctx.add_f32_in_place(s.hidden, s.a, th);

@@ -633,6 +633,25 @@ KRAKEN_API int kraken_hip_kquant_matvec_multi_f32(
   const kraken_buffer* weights, const size_t* rows, size_t cols, kraken_buffer input,
   kraken_buffer norm_weight, float eps, kraken_buffer up, const kraken_buffer* residuals,
   const kraken_buffer* outputs);
+/* No counterpart in the reference: up to four matmul_q*_k_f32_device calls
+ * (mps_backend.mm:6336-6450) that share input, cols and tokens, for the chunked
+ * prefill's projections of one normed hidden state (the linear-attention z, beta
+ * and alpha; the FFN up and gate).  Arrays of `count` (1..4) entries give each
+ * matrix's GGUF type (12 Q4_K, 13 Q5_K, 14 Q6_K), weight, rows and output
+ * [tokens][rows]; each is checked as its matmul entry checks it.  When every
+ * matrix has the same type, more than 8 tokens and the type takes the GEMM
+ * form that decodes the weights in its B tile (Q4_K by default), the matrices
+ * run as one launch with no K split; otherwise, or with
+ * KRAKEN_KQUANT_GROUP=off, each runs as its matmul entry.  A matrix whose own
+ * entry would split K then sums in another order: within fp32 rounding of its
+ * separate result, bit-identical to it when it would not split.  Outputs must
+ * not overlap each other or the input. */
+KRAKEN_API int kraken_hip_kquant_matmul_multi_f32(kraken_hip_context* context, size_t count,
+                                                  const uint32_t* ggml_types,
+                                                  const kraken_buffer* weights,
+                                                  const size_t* rows, size_t cols, size_t tokens,
+                                                  kraken_buffer input,
+                                                  const kraken_buffer* outputs);
 /* No counterpart in the reference: kraken_hip_kquant_matvec_multi_f32 (no up
  * input, no residuals) whose matrix 0 rows are the conv channels of one
  * sequence's linear-attention prologue: each row's value x becomes

@@ -14,6 +14,8 @@
 // allocation of this library or of torch is.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+#include <cstring>
 #include <string>
 
 #include "context_internal.hpp"
@@ -140,7 +142,7 @@ int top1_entry(kraken_hip_context* ctx, int format, bool with_probability,
 
 // matmul_q*_k_f32_device with make_k_quant_matmul_layout (mps_backend.mm:
 // 4143-4189, 6336-6450).
-int matmul_entry(kraken_hip_context* ctx, int format, const kraken_buffer& weight, size_t rows,
+int matmul_check(kraken_hip_context* ctx, int format, const kraken_buffer& weight, size_t rows,
                  size_t cols, size_t tokens, const kraken_buffer& input,
                  const kraken_buffer& output) {
   KRAKEN_TRY(check_context(ctx));
@@ -181,6 +183,14 @@ int matmul_entry(kraken_hip_context* ctx, int format, const kraken_buffer& weigh
   KRAKEN_TRY(validate_f32(input, input_values, (f + " matmul input").c_str()));
   KRAKEN_TRY(validate_f32(output, output_values, (f + " matmul output").c_str()));
   KRAKEN_TRY(check_alignment(format, weight, input, "matmul"));
+  return KRAKEN_OK;
+}
+
+int matmul_entry(kraken_hip_context* ctx, int format, const kraken_buffer& weight, size_t rows,
+                 size_t cols, size_t tokens, const kraken_buffer& input,
+                 const kraken_buffer& output) {
+  KRAKEN_TRY(matmul_check(ctx, format, weight, rows, cols, tokens, input, output));
+  const std::string p = std::string("HIP ") + fmt_name(format) + " matmul ";
   KRAKEN_TRY(ensure_workspace(ctx, kquant_matmul_workspace_bytes(format, rows, cols, tokens)));
   KRAKEN_TRY(begin_launch(ctx));
   const hipError_t e = launch_kquant_matmul(
@@ -525,6 +535,54 @@ KRAKEN_API int kraken_hip_kquant_matvec_multi_f32(
 // residuals) whose matrix 0 rows are the conv channels of one sequence: each
 // row's value goes through the depthwise conv (kernel 4) and SiLU of the
 // linear-attention prologue, and its conv state shifts, as the row is written.
+KRAKEN_API int kraken_hip_kquant_matmul_multi_f32(kraken_hip_context* ctx, size_t count,
+                                                  const uint32_t* ggml_types,
+                                                  const kraken_buffer* weights, const size_t* rows,
+                                                  size_t cols, size_t tokens, kraken_buffer input,
+                                                  const kraken_buffer* outputs) {
+  KRAKEN_TRY(check_context(ctx));
+  if (count == 0 || count > kKquantGroupMax) {
+    return invalid("HIP K-quant multi matmul takes 1 to 4 matrices");
+  }
+  if (ggml_types == nullptr || weights == nullptr || rows == nullptr || outputs == nullptr) {
+    return invalid("HIP K-quant multi matmul array argument is null");
+  }
+  int formats[kKquantGroupMax];
+  const void* w[kKquantGroupMax];
+  float* out[kKquantGroupMax];
+  bool same_format = true;
+  for (size_t i = 0; i < count; ++i) {
+    formats[i] = format_of_ggml_type(ggml_types[i]);
+    if (formats[i] < 0) {
+      return invalid("HIP K-quant multi matmul type must be Q4_K, Q5_K or Q6_K");
+    }
+    KRAKEN_TRY(matmul_check(ctx, formats[i], weights[i], rows[i], cols, tokens, input,
+                            outputs[i]));
+    w[i] = weights[i].data;
+    out[i] = static_cast<float*>(outputs[i].data);
+    same_format = same_format && formats[i] == formats[0];
+  }
+  const char* group = std::getenv("KRAKEN_KQUANT_GROUP");
+  if (same_format && (group == nullptr || std::strcmp(group, "off") != 0)) {
+    KRAKEN_TRY(begin_launch(ctx));
+    const hipError_t e =
+      launch_kquant_matmul_group(formats[0], count, w, rows, cols, tokens,
+                                 static_cast<const float*>(input.data), out, ctx->stream);
+    if (e == hipSuccess) {
+      return finish_launch(ctx, "HIP K-quant multi matmul command failed: ");
+    }
+    if (e != hipErrorNotSupported) {
+      return internal(std::string("HIP K-quant multi matmul launch failed: ") +
+                      hipGetErrorString(e));
+    }
+  }
+  for (size_t i = 0; i < count; ++i) {
+    KRAKEN_TRY(matmul_entry(ctx, formats[i], weights[i], rows[i], cols, tokens, input,
+                            outputs[i]));
+  }
+  return KRAKEN_OK;
+}
+
 KRAKEN_API int kraken_hip_kquant_matvec_multi_conv_f32(
   kraken_hip_context* ctx, size_t count, const uint32_t* ggml_types, const kraken_buffer* weights,
   const size_t* rows, size_t cols, kraken_buffer input, kraken_buffer norm_weight, float eps,

@@ -314,11 +314,24 @@ hipError_t launch_attention_prologue_decode(const PrologueArgs& a, uint32_t laye
 // kKquantGemvMaxTokens tokens take the fp32 GEMV; more take the fp16 MFMA
 // GEMM, which stages fp16 weights and inputs in the workspace.
 constexpr size_t kKquantGemvMaxTokens = 8;
+// Matrices per grouped GEMM launch (launch_kquant_matmul_group).
+constexpr size_t kKquantGroupMax = 4;
 uint32_t kquant_block_bytes(int format);
 size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens);
 hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, size_t cols,
                                 size_t tokens, const float* input, float* output,
                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
+// Up to kKquantGroupMax matmuls of one format that share input, cols and
+// tokens (kquant.hip).  More than kKquantGemvMaxTokens tokens with the fused
+// GEMM form (weights decoded in the B tile) run as one launch whose grid holds
+// every matrix's tiles, without K splits; anything else runs
+// launch_kquant_matmul per matrix.  Returns hipErrorNotSupported, launching
+// nothing, when it would not be one launch, so the caller can use the
+// per-matrix entry points (and their workspace) instead.
+hipError_t launch_kquant_matmul_group(int format, size_t count, const void* const* weights,
+                                      const size_t* rows, size_t cols, size_t tokens,
+                                      const float* input, float* const* outputs,
+                                      hipStream_t stream);
 // Rows row_ids[t] (or fixed_row when row_ids is null, tokens = 1) dequantized
 // into output [tokens][cols]; ids outside [0, rows) give zero rows.
 hipError_t launch_kquant_dequantize_rows(int format, const void* weight, size_t rows,

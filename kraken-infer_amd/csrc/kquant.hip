@@ -1484,10 +1484,22 @@ __global__ __launch_bounds__(256) void gemm_f16_pipe_kernel(const half_t* x, con
 // chunk j of an LDS row lives at j ^ (row & 15).
 constexpr int kQK = 128;
 
-template <int F>
+// Several matrices of one format that multiply the same input, in one grid:
+// their 128-row tiles are numbered one after the other along blockIdx.x
+// (matrix i owns tiles tile_end[i - 1] .. tile_end[i] - 1).
+struct KqGroup {
+  const uint8_t* w[kKquantGroupMax];
+  float* c[kKquantGroupMax];
+  uint32_t rows[kKquantGroupMax];
+  uint32_t tile_end[kKquantGroupMax];
+  uint32_t count;
+};
+
+template <int F, bool kGroup = false>
 __global__ __launch_bounds__(256) void gemm_kq_kernel(const float* x, const uint8_t* wq,
                                                       float* c, uint32_t m, uint32_t n,
-                                                      uint32_t k, uint32_t split_steps) {
+                                                      uint32_t k, uint32_t split_steps,
+                                                      KqGroup group = KqGroup{}) {
   constexpr int TM = 128;
   constexpr int TN = 128;
   constexpr int IA = TM / 64;
@@ -1499,7 +1511,18 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(const float* x, const uint
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const uint32_t m0 = blockIdx.y * TM;
-  const uint32_t n0 = blockIdx.x * TN;
+  uint32_t tile = blockIdx.x;
+  if constexpr (kGroup) {
+    uint32_t i = 0;
+    while (i + 1 < group.count && tile >= group.tile_end[i]) {
+      ++i;
+    }
+    tile -= i == 0 ? 0u : group.tile_end[i - 1];
+    wq = group.w[i];
+    c = group.c[i];
+    n = group.rows[i];
+  }
+  const uint32_t n0 = tile * TN;
   const uint32_t bpr = k / 256u;
   // The f32 inputs, rounded to fp16 (RNE) on their way into LDS.
   const __amdgpu_buffer_rsrc_t xr =
@@ -2043,6 +2066,45 @@ GemmKernel gemm_f16_kernel_choice(size_t rows, size_t tokens, uint32_t splits) {
   }
   const uint64_t tiles256 = (uint64_t)((rows + 255) / 256) * ((tokens + 127) / 128);
   return splits == 1 && tiles256 >= 160 ? GemmKernel::pipe256 : GemmKernel::pipe128;
+}
+
+hipError_t launch_kquant_matmul_group(int format, size_t count, const void* const* weights,
+                                      const size_t* rows, size_t cols, size_t tokens,
+                                      const float* input, float* const* outputs,
+                                      hipStream_t stream) {
+  if (count == 0 || count > kKquantGroupMax || tokens <= kKquantGemvMaxTokens ||
+      kquant_gemm_unfused(format)) {
+    return hipErrorNotSupported;
+  }
+  KqGroup g{};
+  uint32_t tiles = 0;
+  for (size_t i = 0; i < count; ++i) {
+    g.w[i] = static_cast<const uint8_t*>(weights[i]);
+    g.c[i] = outputs[i];
+    g.rows[i] = (uint32_t)rows[i];
+    tiles += (uint32_t)((rows[i] + 127) / 128);
+    g.tile_end[i] = tiles;
+  }
+  g.count = (uint32_t)count;
+  const dim3 grid(tiles, (uint32_t)((tokens + 127) / 128), 1);
+  const uint32_t steps = (uint32_t)(cols / kQK);
+  switch (format) {
+    case 0:
+      gemm_kq_kernel<0, true><<<grid, 256, 0, stream>>>(input, nullptr, nullptr, (uint32_t)tokens,
+                                                        0u, (uint32_t)cols, steps, g);
+      break;
+    case 1:
+      gemm_kq_kernel<1, true><<<grid, 256, 0, stream>>>(input, nullptr, nullptr, (uint32_t)tokens,
+                                                        0u, (uint32_t)cols, steps, g);
+      break;
+    case 2:
+      gemm_kq_kernel<2, true><<<grid, 256, 0, stream>>>(input, nullptr, nullptr, (uint32_t)tokens,
+                                                        0u, (uint32_t)cols, steps, g);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens) {

@@ -109,6 +109,8 @@ SIGNATURES = {
     "kraken_hip_dequantize_rows_q6_k_f32": [_B, _sz, _B, _sz, _sz, _B],
     "kraken_hip_kquant_matvec_fused_f32": [ctypes.c_uint32, _B, _sz, _sz, _B, _B, _f, _B, _B, _B],
     "kraken_hip_kquant_top1_fused_f32": [ctypes.c_uint32, _B, _sz, _sz, _B, _B, _f, _B, _B],
+    "kraken_hip_kquant_matmul_multi_f32": [_sz, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                           _sz, _sz, _B, ctypes.c_void_p],
     "kraken_hip_kquant_matvec_multi_f32": [_sz, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                            _sz, _B, _B, _f, _B, ctypes.c_void_p,
                                            ctypes.c_void_p],
@@ -310,6 +312,16 @@ class Context:
         outs = (KrakenBuffer * n)(*[as_buffer(o) for o in outputs])
         self.call("kquant_matvec_multi_f32", n, types, ws, rs, cols, input, norm_weight, eps, up,
                   res, outs)
+
+    def kquant_matmul_multi(self, ggml_types, weights, rows, cols, tokens, input, outputs):
+        """kraken_hip_kquant_matmul_multi_f32 with Python sequences for the
+        per-matrix arrays."""
+        n = len(weights)
+        types = (ctypes.c_uint32 * n)(*ggml_types)
+        ws = (KrakenBuffer * n)(*[as_buffer(w) for w in weights])
+        rs = (ctypes.c_size_t * n)(*rows)
+        outs = (KrakenBuffer * n)(*[as_buffer(o) for o in outputs])
+        self.call("kquant_matmul_multi_f32", n, types, ws, rs, cols, tokens, input, outs)
 
     def kquant_matvec_multi_conv(self, ggml_types, weights, rows, cols, input, norm_weight, eps,
                                  outputs, conv_pool, conv_offset, conv_weights, conv_kernel=4):

@@ -218,6 +218,42 @@ def test_pipelined_gemm_equals_plain_gemm(ops, monkeypatch, fmt, rows, cols, tok
     assert np.isfinite(piped).all()
 
 
+# --------------------------------------------------------- grouped matmul ----
+GGML = {"q4_k": 12, "q5_k": 13, "q6_k": 14}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("group,tokens", [
+    ((("q4_k", 2048), ("q4_k", 16), ("q4_k", 16)), 1024),   # prefill z, beta, alpha
+    ((("q4_k", 2048), ("q4_k", 16), ("q4_k", 16)), 9),
+    ((("q4_k", 3584), ("q4_k", 3584)), 1024),                # FFN up, gate
+    ((("q4_k", 130), ("q4_k", 300), ("q4_k", 16), ("q4_k", 1)), 200),  # ragged tiles
+    ((("q5_k", 6144), ("q4_k", 2048)), 1024),                # mixed types: one call each
+])
+def test_multi_matmul_equals_single_matmuls(hip_ctx, ops, group, tokens):
+    """kraken_hip_kquant_matmul_multi_f32 against each matrix's own matmul
+    entry on the same input: bit-identical where the single call runs without a
+    K split (the grouped launch never splits), else within TOL of the oracle
+    like the single call (K split into planes sums in another order)."""
+    print(f"multi matmul {group} tokens={tokens}", flush=True)
+    cols = 1024
+    x = np.random.default_rng(tokens).standard_normal(tokens * cols).astype(np.float32)
+    ws = [kc.random_weight_fast(f, r, cols, seed=31 * i + r) for i, (f, r) in enumerate(group)]
+    xb = hip_ctx.buffer(x)
+    outs = [hip_ctx.buffer(byte_size=4 * tokens * r) for _, r in group]
+    hip_ctx.kquant_matmul_multi([GGML[f] for f, _ in group], [hip_ctx.buffer(w) for w in ws],
+                                [r for _, r in group], cols, tokens, xb, outs)
+    for (f, r), w, ob in zip(group, ws, outs):
+        got = ob.download(tokens * r)
+        single = ops.kquant_matmul(f, w, r, cols, x, tokens)
+        tiles = -(-r // 128) * -(-tokens // 128)
+        if f == "q4_k" and tiles < 128 and tokens > 8:
+            want, scale = oracle_projection(f, w, r, cols, x, tokens)
+            check_projection(got, want, scale, f"{f} {r} rows")
+        else:
+            np.testing.assert_array_equal(got, single, err_msg=f"{f} {r} rows")
+
+
 # ------------------------------------------------------------------ top1 ----
 
 def planted_logit_weight(fmt, rows, cols, winner, seed):

@@ -219,3 +219,49 @@ def test_argmax_check_order(vctx):
     assert status(vctx, op, v, 100, tok, prob) == (kh.UNAVAILABLE, ACCEPTED)
     # Vocabulary-sized inputs take the two-pass path (context workspace).
     assert status(vctx, op, fake(4 * 248320), 248320, tok, prob) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+# ------------------------------------------------------------ grouped matmul --
+# kraken_hip_kquant_matmul_multi_f32: 1..4 matmuls sharing input, cols and
+# tokens, each checked as its own matmul entry.
+def _multi_matmul(vctx, types, rows, cols, tokens, outputs=None, weights=None):
+    import ctypes
+    n = len(types)
+    fmts = {12: "q4_k", 13: "q5_k", 14: "q6_k"}
+    t = (ctypes.c_uint32 * n)(*types)
+    ws = (kh.KrakenBuffer * n)(*(weights or [fake(wbytes(fmts.get(ty, "q4_k"), r, cols))
+                                             for ty, r in zip(types, rows)]))
+    rs = (ctypes.c_size_t * n)(*rows)
+    outs = (kh.KrakenBuffer * n)(*(outputs or [fake(4 * tokens * r) for r in rows]))
+    return status(vctx, "kquant_matmul_multi_f32", n, t, ws, rs, cols, tokens,
+                  fake(4 * tokens * cols), outs)
+
+
+def test_multi_matmul_accepts_group_and_mixed_types(vctx):
+    # The prefill's z / beta / alpha and FFN up / gate groups, and a mixed group.
+    for types, rows in (([12, 12, 12], [2048, 16, 16]), ([12, 12], [3584, 3584]),
+                        ([13, 12, 14], [6144, 2048, 16])):
+        for tokens in (1, 8, 9, 1024):
+            assert _multi_matmul(vctx, types, rows, 1024, tokens) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+def test_multi_matmul_checks(vctx):
+    import ctypes
+    assert _multi_matmul(vctx, [], [], 1024, 64) == invalid(
+        "HIP K-quant multi matmul takes 1 to 4 matrices")
+    assert _multi_matmul(vctx, [12] * 5, [16] * 5, 1024, 64) == invalid(
+        "HIP K-quant multi matmul takes 1 to 4 matrices")
+    assert status(vctx, "kquant_matmul_multi_f32", 1, None, None, None, 1024, 64,
+                  fake(4 * 64 * 1024), None) == invalid(
+        "HIP K-quant multi matmul array argument is null")
+    assert _multi_matmul(vctx, [12, 2], [16, 16], 1024, 64) == invalid(
+        "HIP K-quant multi matmul type must be Q4_K, Q5_K or Q6_K")
+    # Each matrix's own matmul checks, in its own wording.
+    code, msg = _multi_matmul(vctx, [12, 12], [16, 32], 1024, 64,
+                              outputs=[fake(4 * 64 * 16), fake(4 * 64 * 16)])
+    assert code == kh.INVALID_ARGUMENT and "Q4_K matmul output" in msg
+    assert _multi_matmul(vctx, [12, 14], [16, 16], 1024, 64,
+                         weights=[fake(wbytes("q4_k", 16, 1024)), fake(100)]) == invalid(
+        "HIP Q6_K matmul weight buffer is too small")
+    assert _multi_matmul(vctx, [12], [16], 1000, 64) == invalid(
+        "HIP Q4_K matmul cols must be divisible by 256")
