@@ -739,6 +739,18 @@ class HipContext {
       ctx_, ggml_type, weight.raw(), rows, cols, input.raw(), norm_weight.raw(), eps, up.raw(),
       residual.raw(), output.raw()));
   }
+  // A K-quant matmul of more than 8 tokens with SwiGLU on its input (up given)
+  // and a residual add (which may be `output`) folded in; see kraken_hip.h.
+  [[nodiscard]] Status kquant_matmul_fused_f32(std::uint32_t ggml_type, const HipBuffer& weight,
+                                               std::size_t rows, std::size_t cols,
+                                               std::size_t tokens, const HipBuffer& input,
+                                               const HipBuffer& up, const HipBuffer& residual,
+                                               HipBuffer& output) const {
+    return Status::from_code(kraken_hip_kquant_matmul_fused_f32(ctx_, ggml_type, weight.raw(),
+                                                                rows, cols, tokens, input.raw(),
+                                                                up.raw(), residual.raw(),
+                                                                output.raw()));
+  }
   // Up to four K-quant matmuls over one input [tokens][cols] (one launch when
   // their type allows it; see kraken_hip.h).
   [[nodiscard]] Status kquant_matmul_multi_f32(std::size_t count, const std::uint32_t* ggml_types,

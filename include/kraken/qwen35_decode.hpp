@@ -118,6 +118,21 @@ struct ModelWeights {
                                      outputs);
 }
 
+// A projection of more than 8 tokens with the input's SwiGLU (up, or null) and
+// the residual add (residual, or null; it may be `out`) folded into the GEMM.
+[[nodiscard]] inline Status project_gemm_fused(const HipContext& ctx, const Tensor& w,
+                                               const HipBuffer& input, std::size_t tokens,
+                                               const HipBuffer* up, const HipBuffer* residual,
+                                               HipBuffer& out) {
+  if (w.buffer == nullptr || w.rows == 0 || w.cols == 0) {
+    return Status::invalid_argument("Qwen3.5 matmul weight is missing");
+  }
+  const HipBuffer none;
+  return ctx.kquant_matmul_fused_f32(static_cast<std::uint32_t>(w.type), *w.buffer, w.rows,
+                                     w.cols, tokens, input, up != nullptr ? *up : none,
+                                     residual != nullptr ? *residual : none, out);
+}
+
 // Device buffers one decode step reuses; sized for the plan on first use.
 class DecodeScratch {
  public:

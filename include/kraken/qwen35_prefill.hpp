@@ -137,6 +137,18 @@ namespace detail {
   auto proj = [&](const Tensor& t, const HipBuffer& in, HipBuffer& out) {
     return project(ctx, t, in, tokens, out);
   };
+  // The fused order folds the residual adds (and the FFN's SwiGLU) into the
+  // GEMMs of the output projections, which take more than 8 tokens.
+  const bool fold = order == OpOrder::fused && tokens > 8;
+  auto proj_residual = [&](const Tensor& t, HipBuffer& in, const HipBuffer* up) {
+    if (fold) {
+      return project_gemm_fused(ctx, t, in, tokens, up, &s.hidden, s.hidden);
+    }
+    Status st = up != nullptr ? ctx.silu_mul_f32_in_place(in, *up, tokens * t.cols) : Status::ok();
+    if (st.is_ok()) st = proj(t, in, s.a);
+    if (st.is_ok()) st = ctx.add_f32_in_place(s.hidden, s.a, th);
+    return st;
+  };
   return for_each_main_layer(plan, [&](std::size_t index, LayerKind kind, std::size_t kind_index) {
     const DecoderLayerWeights& l = w.layers[index];
     if (l.attn_norm == nullptr || l.post_attention_norm == nullptr) {
@@ -161,7 +173,7 @@ namespace detail {
         r = run_linear_attention_chunk(ctx, plan, cache, l.linear, kind_index, 0, s.a, s.b, s.c,
                                        s.d, tokens, eps, order, s.layer_ws, s.attn);
       }
-      if (r.is_ok()) r = proj(l.ssm_out, s.attn, s.a);
+      if (r.is_ok()) r = proj_residual(l.ssm_out, s.attn, nullptr);
     } else {
       // qwen35_runtime.cpp:3200-3228 projections, the core over the cached
       // prefix and the chunk, :3357-3400 attn_output and the residual.
@@ -173,9 +185,8 @@ namespace detail {
                                      chunk_start, chunk_start, w.mrope_sections, w.rope_theta, eps,
                                      nullptr, order, s.layer_ws, s.attn);
       }
-      if (r.is_ok()) r = proj(l.output, s.attn, s.a);
+      if (r.is_ok()) r = proj_residual(l.output, s.attn, nullptr);
     }
-    if (r.is_ok()) r = ctx.add_f32_in_place(s.hidden, s.a, th);
     // qwen35_runtime.cpp:3036-3144: the FFN half.
     if (r.is_ok()) {
       r = ctx.rms_norm_f32_f32_batched(s.hidden, *l.post_attention_norm, tokens, h, eps, s.normed);
@@ -188,9 +199,7 @@ namespace detail {
       if (r.is_ok()) r = proj(l.ffn_up, s.normed, s.ffn_up);
       if (r.is_ok()) r = proj(l.ffn_gate, s.normed, s.ffn_gate);
     }
-    if (r.is_ok()) r = ctx.silu_mul_f32_in_place(s.ffn_gate, s.ffn_up, tokens * l.ffn_gate.rows);
-    if (r.is_ok()) r = proj(l.ffn_down, s.ffn_gate, s.a);
-    if (r.is_ok()) r = ctx.add_f32_in_place(s.hidden, s.a, th);
+    if (r.is_ok()) r = proj_residual(l.ffn_down, s.ffn_gate, &s.ffn_up);
     if (r.is_ok() && after_layer != nullptr) {
       r = (*after_layer)(index, s.hidden, chunk_start, tokens);
     }

@@ -633,6 +633,19 @@ KRAKEN_API int kraken_hip_kquant_matvec_multi_f32(
   const kraken_buffer* weights, const size_t* rows, size_t cols, kraken_buffer input,
   kraken_buffer norm_weight, float eps, kraken_buffer up, const kraken_buffer* residuals,
   const kraken_buffer* outputs);
+/* No counterpart in the reference: matmul_q*_k_f32_device (mps_backend.mm:
+ * 6336-6450) with a decoder layer's neighbouring ops folded in, for the chunked
+ * prefill: output = residual + W x, where x = silu(input) * up when up is given
+ * (silu_mul_f32_in_place, then the matmul's fp16 rounding of its input) and
+ * input otherwise; residual may be empty (then 0) or the output buffer itself
+ * (add_f32_in_place), but no other view that overlaps the output.  The same
+ * bits as the separate ops.  More than 8 tokens (the GEMM path); up and
+ * residual 16-byte aligned; a given up takes the two-pass GEMM form. */
+KRAKEN_API int kraken_hip_kquant_matmul_fused_f32(kraken_hip_context* context, uint32_t ggml_type,
+                                                  kraken_buffer weight, size_t rows, size_t cols,
+                                                  size_t tokens, kraken_buffer input,
+                                                  kraken_buffer up, kraken_buffer residual,
+                                                  kraken_buffer output);
 /* No counterpart in the reference: up to four matmul_q*_k_f32_device calls
  * (mps_backend.mm:6336-6450) that share input, cols and tokens, for the chunked
  * prefill's projections of one normed hidden state (the linear-attention z, beta

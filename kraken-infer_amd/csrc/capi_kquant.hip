@@ -535,6 +535,53 @@ KRAKEN_API int kraken_hip_kquant_matvec_multi_f32(
 // residuals) whose matrix 0 rows are the conv channels of one sequence: each
 // row's value goes through the depthwise conv (kernel 4) and SiLU of the
 // linear-attention prologue, and its conv state shifts, as the row is written.
+KRAKEN_API int kraken_hip_kquant_matmul_fused_f32(kraken_hip_context* ctx, uint32_t ggml_type,
+                                                  kraken_buffer weight, size_t rows, size_t cols,
+                                                  size_t tokens, kraken_buffer input,
+                                                  kraken_buffer up, kraken_buffer residual,
+                                                  kraken_buffer output) {
+  KRAKEN_TRY(check_context(ctx));
+  const int format = format_of_ggml_type(ggml_type);
+  if (format < 0) {
+    return invalid("HIP K-quant fused matmul type must be Q4_K, Q5_K or Q6_K");
+  }
+  KRAKEN_TRY(matmul_check(ctx, format, weight, rows, cols, tokens, input, output));
+  if (tokens <= kKquantGemvMaxTokens) {
+    return invalid("HIP K-quant fused matmul needs more than 8 tokens");
+  }
+  if (up.data != nullptr) {
+    KRAKEN_TRY(validate_f32(up, tokens * cols, "K-quant fused matmul up"));
+    if (((uintptr_t)up.data & 15u) != 0) {
+      return invalid("HIP K-quant fused matmul up buffer must be 16-byte aligned");
+    }
+  }
+  if (residual.data != nullptr) {
+    KRAKEN_TRY(validate_f32(residual, tokens * rows, "K-quant fused matmul residual"));
+    if (((uintptr_t)residual.data & 15u) != 0) {
+      return invalid("HIP K-quant fused matmul residual buffer must be 16-byte aligned");
+    }
+    // Each output element is read from the residual and written by one thread:
+    // the residual may be the output itself, but not a shifted view of it.
+    const uintptr_t r0 = (uintptr_t)residual.data, o0 = (uintptr_t)output.data;
+    const size_t bytes = tokens * rows * sizeof(float);
+    if (r0 != o0 && r0 < o0 + bytes && o0 < r0 + bytes) {
+      return invalid("HIP K-quant fused matmul residual overlaps the output");
+    }
+  }
+  const std::string p = std::string("HIP ") + fmt_name(format) + " fused matmul ";
+  KRAKEN_TRY(ensure_workspace(
+    ctx, kquant_matmul_workspace_bytes(format, rows, cols, tokens, up.data != nullptr)));
+  KRAKEN_TRY(begin_launch(ctx));
+  const hipError_t e = launch_kquant_matmul(
+    format, weight.data, rows, cols, tokens, static_cast<const float*>(input.data),
+    static_cast<float*>(output.data), ctx->workspace, ctx->workspace_bytes, ctx->stream,
+    static_cast<const float*>(up.data), static_cast<const float*>(residual.data));
+  if (e != hipSuccess) {
+    return internal(p + "launch failed: " + hipGetErrorString(e));
+  }
+  return finish_launch(ctx, (p + "command failed: ").c_str());
+}
+
 KRAKEN_API int kraken_hip_kquant_matmul_multi_f32(kraken_hip_context* ctx, size_t count,
                                                   const uint32_t* ggml_types,
                                                   const kraken_buffer* weights, const size_t* rows,

@@ -317,10 +317,16 @@ constexpr size_t kKquantGemvMaxTokens = 8;
 // Matrices per grouped GEMM launch (launch_kquant_matmul_group).
 constexpr size_t kKquantGroupMax = 4;
 uint32_t kquant_block_bytes(int format);
-size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens);
+// With `up` (GEMM path only), the input is silu(input) * up (the two-pass
+// form's first pass forms it, as silu_mul_f32_in_place rounds it); with
+// `residual` (GEMM path only; it may be `output`), output = residual + W x, the
+// sum add_f32_in_place would form.  swiglu: whether `up` will be given.
+size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens,
+                                     bool swiglu = false);
 hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, size_t cols,
                                 size_t tokens, const float* input, float* output,
-                                void* workspace, size_t workspace_bytes, hipStream_t stream);
+                                void* workspace, size_t workspace_bytes, hipStream_t stream,
+                                const float* up = nullptr, const float* residual = nullptr);
 // Up to kKquantGroupMax matmuls of one format that share input, cols and
 // tokens (kquant.hip).  More than kKquantGemvMaxTokens tokens with the fused
 // GEMM form (weights decoded in the B tile) run as one launch whose grid holds

@@ -1099,6 +1099,24 @@ __device__ __forceinline__ void f32_to_f16_8(const float* in, half_t* out, uint6
   __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, h), reinterpret_cast<u32x4_t*>(out) + i);
 }
 
+// The same for silu(in) * up, with silu_mul_f32_in_place's arithmetic (the
+// f32 product, then one rounding to fp16).
+__device__ __forceinline__ void f32_swiglu_to_f16_8(const float* in, const float* up,
+                                                    half_t* out, uint64_t i) {
+  const float4 a = reinterpret_cast<const float4*>(in)[2 * i];
+  const float4 b = reinterpret_cast<const float4*>(in)[2 * i + 1];
+  const float4 ua = reinterpret_cast<const float4*>(up)[2 * i];
+  const float4 ub = reinterpret_cast<const float4*>(up)[2 * i + 1];
+  const float g[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  const float u[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+  half8_t h;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    h[j] = static_cast<half_t>((g[j] / (1.0f + expf(-g[j]))) * u[j]);
+  }
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, h), reinterpret_cast<u32x4_t*>(out) + i);
+}
+
 // The two-pass GEMM's first pass, one launch: workgroups [0, convert_blocks)
 // round the f32 inputs to fp16 (n8 groups of eight), the rest dequantize the
 // weights and round them to fp16 (RNE), [rows][cols].
@@ -1107,11 +1125,16 @@ __global__ __launch_bounds__(256) void kq_dequant_f16_kernel(const uint8_t* weig
                                                              uint32_t blocks_per_row,
                                                              half_t* out, const float* xin,
                                                              half_t* x16, uint64_t n8,
-                                                             uint32_t convert_blocks) {
+                                                             uint32_t convert_blocks,
+                                                             const float* up) {
   if (blockIdx.x < convert_blocks) {
     const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     if (i < n8) {
-      f32_to_f16_8(xin, x16, i);
+      if (up != nullptr) {
+        f32_swiglu_to_f16_8(xin, up, x16, i);
+      } else {
+        f32_to_f16_8(xin, x16, i);
+      }
     }
     return;
   }
@@ -1175,7 +1198,8 @@ typedef float float16v_t __attribute__((ext_vector_type(16)));
 template <int TM, int TN>
 __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const half_t* w,
                                                           float* c, uint32_t m, uint32_t n,
-                                                          uint32_t k, uint32_t split_steps) {
+                                                          uint32_t k, uint32_t split_steps,
+                                                          const float* residual) {
   static_assert(TM % 64 == 0 && TN % 64 == 0, "whole 32 x 32 MFMA tiles per wave");
   constexpr int IA = TM / 64;   // MFMA tiles per wave along tokens
   constexpr int JB = TN / 64;   // along rows
@@ -1296,7 +1320,8 @@ __global__ __launch_bounds__(256) void gemm_f16_nt_kernel(const half_t* x, const
       for (int e = 0; e < 16; ++e) {
         const uint32_t row = m0 + (TM / 2) * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
         if (row < m && col < n) {
-          store_through(&c[(uint64_t)row * n + col], acc[i][j][e]);
+          const uint64_t at = (uint64_t)row * n + col;
+          store_through(&c[at], residual != nullptr ? residual[at] + acc[i][j][e] : acc[i][j][e]);
         }
       }
     }
@@ -1327,7 +1352,8 @@ struct GemmPipe {
 template <int TN>
 __global__ __launch_bounds__(256) void gemm_f16_pipe_kernel(const half_t* x, const half_t* w,
                                                             float* c, uint32_t m, uint32_t n,
-                                                            uint32_t k, uint32_t split_steps) {
+                                                            uint32_t k, uint32_t split_steps,
+                                                            const float* residual) {
   using G = GemmPipe<TN>;
   constexpr int TM = G::kTM;
   constexpr int NS = G::kStages;
@@ -1462,7 +1488,8 @@ __global__ __launch_bounds__(256) void gemm_f16_pipe_kernel(const half_t* x, con
       for (int e = 0; e < 16; ++e) {
         const uint32_t row = m0 + (TM / 2) * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
         if (row < m && col < n) {
-          store_through(&c[(uint64_t)row * n + col], acc[i][j][e]);
+          const uint64_t at = (uint64_t)row * n + col;
+          store_through(&c[at], residual != nullptr ? residual[at] + acc[i][j][e] : acc[i][j][e]);
         }
       }
     }
@@ -1499,6 +1526,7 @@ template <int F, bool kGroup = false>
 __global__ __launch_bounds__(256) void gemm_kq_kernel(const float* x, const uint8_t* wq,
                                                       float* c, uint32_t m, uint32_t n,
                                                       uint32_t k, uint32_t split_steps,
+                                                      const float* residual,
                                                       KqGroup group = KqGroup{}) {
   constexpr int TM = 128;
   constexpr int TN = 128;
@@ -1652,7 +1680,8 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(const float* x, const uint
       for (int e = 0; e < 16; ++e) {
         const uint32_t row = m0 + (TM / 2) * wm + 32u * i + 8u * (e / 4) + 4u * fk + (e % 4);
         if (row < m && col < n) {
-          store_through(&c[(uint64_t)row * n + col], acc[i][j][e]);
+          const uint64_t at = (uint64_t)row * n + col;
+          store_through(&c[at], residual != nullptr ? residual[at] + acc[i][j][e] : acc[i][j][e]);
         }
       }
     }
@@ -1680,7 +1709,8 @@ uint32_t gemm_k_splits(size_t rows, size_t cols, size_t tokens) {
 }
 
 __global__ __launch_bounds__(256) void sum_planes_kernel(const float* planes, float* out,
-                                                         uint64_t n4, uint32_t count) {
+                                                         uint64_t n4, uint32_t count,
+                                                         const float* residual) {
   const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
   if (i >= n4) {
     return;
@@ -1693,6 +1723,10 @@ __global__ __launch_bounds__(256) void sum_planes_kernel(const float* planes, fl
     acc.y += v.y;
     acc.z += v.z;
     acc.w += v.w;
+  }
+  if (residual != nullptr) {  // add_f32_in_place(residual, W x) on the sum
+    const float4 r = reinterpret_cast<const float4*>(residual)[i];
+    acc = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
   }
   reinterpret_cast<float4*>(out)[i] = acc;
 }
@@ -2091,15 +2125,15 @@ hipError_t launch_kquant_matmul_group(int format, size_t count, const void* cons
   switch (format) {
     case 0:
       gemm_kq_kernel<0, true><<<grid, 256, 0, stream>>>(input, nullptr, nullptr, (uint32_t)tokens,
-                                                        0u, (uint32_t)cols, steps, g);
+                                                        0u, (uint32_t)cols, steps, nullptr, g);
       break;
     case 1:
       gemm_kq_kernel<1, true><<<grid, 256, 0, stream>>>(input, nullptr, nullptr, (uint32_t)tokens,
-                                                        0u, (uint32_t)cols, steps, g);
+                                                        0u, (uint32_t)cols, steps, nullptr, g);
       break;
     case 2:
       gemm_kq_kernel<2, true><<<grid, 256, 0, stream>>>(input, nullptr, nullptr, (uint32_t)tokens,
-                                                        0u, (uint32_t)cols, steps, g);
+                                                        0u, (uint32_t)cols, steps, nullptr, g);
       break;
     default:
       return hipErrorInvalidValue;
@@ -2107,24 +2141,30 @@ hipError_t launch_kquant_matmul_group(int format, size_t count, const void* cons
   return hipGetLastError();
 }
 
-size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens) {
+size_t kquant_matmul_workspace_bytes(int format, size_t rows, size_t cols, size_t tokens,
+                                     bool swiglu) {
   if (tokens <= kKquantGemvMaxTokens) {
     return 0;
   }
   const uint32_t splits = gemm_k_splits(rows, cols, tokens);
-  return (kquant_gemm_unfused(format) ? align256(rows * cols * 2u) + align256(tokens * cols * 2u)
-                                      : 0u) +
+  return (swiglu || kquant_gemm_unfused(format)
+            ? align256(rows * cols * 2u) + align256(tokens * cols * 2u)
+            : 0u) +
          (splits > 1 ? align256(splits * tokens * rows * 4u) : 0u);
 }
 
 hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, size_t cols,
                                 size_t tokens, const float* input, float* output,
-                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                                void* workspace, size_t workspace_bytes, hipStream_t stream,
+                                const float* up, const float* residual) {
   const uint32_t bpr = (uint32_t)(cols / 256u);
   if (tokens == 1 && bpr <= kXsMaxBlocksPerRow) {
     FusedGemvArgs f{static_cast<const uint8_t*>(weight), input, nullptr, nullptr, nullptr, output,
                     (uint32_t)rows, (uint32_t)cols, bpr, 0.0f};
     return launch_gemv_fused(format, f, stream);
+  }
+  if ((up != nullptr || residual != nullptr) && tokens <= kKquantGemvMaxTokens) {
+    return hipErrorInvalidValue;  // the GEMM path only
   }
   if (tokens <= kKquantGemvMaxTokens) {
     // The reference's batched matvec (4 to 8 tokens) multiplies fp16-rounded
@@ -2133,12 +2173,13 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
                (uint32_t)cols, bpr, (uint32_t)tokens, 0u, tokens >= 4u ? 1u : 0u};
     return launch_gemv(format, a, stream);
   }
-  const size_t need = kquant_matmul_workspace_bytes(format, rows, cols, tokens);
+  const size_t need = kquant_matmul_workspace_bytes(format, rows, cols, tokens, up != nullptr);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     return hipErrorInvalidValue;
   }
   // Workspace: [fp16 weights] [fp16 inputs] (two-pass form only) [K-split planes].
-  const bool unfused = kquant_gemm_unfused(format);
+  // A SwiGLU input takes the two-pass form, whose first pass forms it.
+  const bool unfused = up != nullptr || kquant_gemm_unfused(format);
   half_t* w16 = static_cast<half_t*>(workspace);
   half_t* x16 = reinterpret_cast<half_t*>(static_cast<char*>(workspace) +
                                           (unfused ? align256(rows * cols * 2u) : 0u));
@@ -2151,13 +2192,13 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
     const dim3 dq(convert_blocks + (uint32_t)((blocks + 31) / 32));
     if (format == 0) {
       kq_dequant_f16_kernel<0><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16, input, x16,
-                                                       n8, convert_blocks);
+                                                       n8, convert_blocks, up);
     } else if (format == 1) {
       kq_dequant_f16_kernel<1><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16, input, x16,
-                                                       n8, convert_blocks);
+                                                       n8, convert_blocks, up);
     } else {
       kq_dequant_f16_kernel<2><<<dq, 256, 0, stream>>>(wq, (uint32_t)rows, bpr, w16, input, x16,
-                                                       n8, convert_blocks);
+                                                       n8, convert_blocks, up);
     }
     if ((e = hipGetLastError()) != hipSuccess) {
       return e;
@@ -2170,6 +2211,8 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
                                           : 0u))
                              : output;
   const dim3 grid((uint32_t)((rows + 127) / 128), (uint32_t)((tokens + 127) / 128), splits);
+  // Without K splits the GEMM adds the residual itself; with them the plane sum does.
+  const float* res = splits == 1 ? residual : nullptr;
   if (unfused) {
     const uint32_t steps = (uint32_t)(cols / kGK);
     const uint32_t split_steps = (steps + splits - 1) / splits;
@@ -2178,28 +2221,31 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
       const dim3 g256((uint32_t)((rows + 255) / 256), (uint32_t)((tokens + 127) / 128), splits);
       gemm_f16_pipe_kernel<256><<<g256, 256, 0, stream>>>(x16, w16, planes, (uint32_t)tokens,
                                                           (uint32_t)rows, (uint32_t)cols,
-                                                          split_steps);
+                                                          split_steps, res);
     } else if (kernel == GemmKernel::pipe128) {
       gemm_f16_pipe_kernel<128><<<grid, 256, 0, stream>>>(x16, w16, planes, (uint32_t)tokens,
                                                           (uint32_t)rows, (uint32_t)cols,
-                                                          split_steps);
+                                                          split_steps, res);
     } else {
       gemm_f16_nt_kernel<128, 128><<<grid, 256, 0, stream>>>(x16, w16, planes, (uint32_t)tokens,
                                                              (uint32_t)rows, (uint32_t)cols,
-                                                             split_steps);
+                                                             split_steps, res);
     }
   } else {
     const uint32_t steps = (uint32_t)(cols / kQK);
     const uint32_t split_steps = (steps + splits - 1) / splits;
     if (format == 0) {
       gemm_kq_kernel<0><<<grid, 256, 0, stream>>>(input, wq, planes, (uint32_t)tokens,
-                                                  (uint32_t)rows, (uint32_t)cols, split_steps);
+                                                  (uint32_t)rows, (uint32_t)cols, split_steps,
+                                                  res);
     } else if (format == 1) {
       gemm_kq_kernel<1><<<grid, 256, 0, stream>>>(input, wq, planes, (uint32_t)tokens,
-                                                  (uint32_t)rows, (uint32_t)cols, split_steps);
+                                                  (uint32_t)rows, (uint32_t)cols, split_steps,
+                                                  res);
     } else {
       gemm_kq_kernel<2><<<grid, 256, 0, stream>>>(input, wq, planes, (uint32_t)tokens,
-                                                  (uint32_t)rows, (uint32_t)cols, split_steps);
+                                                  (uint32_t)rows, (uint32_t)cols, split_steps,
+                                                  res);
     }
   }
   if ((e = hipGetLastError()) != hipSuccess || splits == 1) {
@@ -2207,7 +2253,7 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
   }
   const uint64_t n4 = (uint64_t)tokens * rows / 4u;
   sum_planes_kernel<<<dim3((uint32_t)((n4 + 255) / 256)), 256, 0, stream>>>(planes, output, n4,
-                                                                         splits);
+                                                                         splits, residual);
   return hipGetLastError();
 }
 

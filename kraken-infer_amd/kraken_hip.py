@@ -109,6 +109,7 @@ SIGNATURES = {
     "kraken_hip_dequantize_rows_q6_k_f32": [_B, _sz, _B, _sz, _sz, _B],
     "kraken_hip_kquant_matvec_fused_f32": [ctypes.c_uint32, _B, _sz, _sz, _B, _B, _f, _B, _B, _B],
     "kraken_hip_kquant_top1_fused_f32": [ctypes.c_uint32, _B, _sz, _sz, _B, _B, _f, _B, _B],
+    "kraken_hip_kquant_matmul_fused_f32": [ctypes.c_uint32, _B, _sz, _sz, _sz, _B, _B, _B, _B],
     "kraken_hip_kquant_matmul_multi_f32": [_sz, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                            _sz, _sz, _B, ctypes.c_void_p],
     "kraken_hip_kquant_matvec_multi_f32": [_sz, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,

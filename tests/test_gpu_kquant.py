@@ -254,6 +254,55 @@ def test_multi_matmul_equals_single_matmuls(hip_ctx, ops, group, tokens):
             np.testing.assert_array_equal(got, single, err_msg=f"{f} {r} rows")
 
 
+# ----------------------------------------------------------- fused matmul ----
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt,rows,cols", [("q6_k", 1024, 3584), ("q4_k", 1024, 2048),
+                                           ("q4_k", 3584, 1024), ("q5_k", 6144, 1024)])
+@pytest.mark.parametrize("tokens", [9, 1024])
+def test_fused_matmul_equals_separate_ops(hip_ctx, fmt, rows, cols, tokens):
+    """kraken_hip_kquant_matmul_fused_f32 against the ops it folds:
+    silu_mul_f32_in_place(gate, up), the matmul entry, add_f32_in_place(residual,
+    out).  Bit-identical with SwiGLU, with the residual (given as the output
+    buffer itself, and as a separate buffer), with both and with neither, with
+    and without K splits, in both GEMM forms."""
+    print(f"fused matmul {fmt} {rows}x{cols} tokens={tokens}", flush=True)
+    rng = np.random.default_rng(rows + tokens)
+    w = hip_ctx.buffer(kc.random_weight_fast(fmt, rows, cols, seed=rows + cols))
+    gate = rng.standard_normal(tokens * cols).astype(np.float32)
+    up = rng.standard_normal(tokens * cols).astype(np.float32)
+    res = rng.standard_normal(tokens * rows).astype(np.float32)
+    ty = GGML[fmt]
+    none = None
+    for swiglu in (False, True):
+        # The separate ops.
+        g = hip_ctx.buffer(gate)
+        if swiglu:
+            hip_ctx.silu_mul_f32_in_place(g, hip_ctx.buffer(up), tokens * cols)
+        plain = hip_ctx.buffer(byte_size=4 * tokens * rows)
+        getattr(hip_ctx, f"matmul_{fmt}_f32_device")(w, rows, cols, tokens, g, plain)
+        want_plain = plain.download(tokens * rows)
+        summed = hip_ctx.buffer(res)
+        hip_ctx.add_f32_in_place(summed, plain, tokens * rows)
+        want_res = summed.download(tokens * rows)
+        ub = hip_ctx.buffer(up) if swiglu else none
+        # Folded: no residual; the residual as the output; a separate residual.
+        out = hip_ctx.buffer(byte_size=4 * tokens * rows)
+        hip_ctx.kquant_matmul_fused_f32(ty, w, rows, cols, tokens, hip_ctx.buffer(gate), ub, none,
+                                        out)
+        np.testing.assert_array_equal(out.download(tokens * rows).view(np.uint32),
+                                      want_plain.view(np.uint32), err_msg=f"swiglu={swiglu}")
+        inplace = hip_ctx.buffer(res)
+        hip_ctx.kquant_matmul_fused_f32(ty, w, rows, cols, tokens, hip_ctx.buffer(gate), ub,
+                                        inplace, inplace)
+        np.testing.assert_array_equal(inplace.download(tokens * rows).view(np.uint32),
+                                      want_res.view(np.uint32), err_msg=f"in place {swiglu}")
+        out2 = hip_ctx.buffer(byte_size=4 * tokens * rows)
+        hip_ctx.kquant_matmul_fused_f32(ty, w, rows, cols, tokens, hip_ctx.buffer(gate), ub,
+                                        hip_ctx.buffer(res), out2)
+        np.testing.assert_array_equal(out2.download(tokens * rows).view(np.uint32),
+                                      want_res.view(np.uint32), err_msg=f"separate {swiglu}")
+
+
 # ------------------------------------------------------------------ top1 ----
 
 def planted_logit_weight(fmt, rows, cols, winner, seed):
@@ -401,7 +450,7 @@ def test_fused_matvec_against_oracle_chain(hip_ctx, fmt, rows, cols, mode, resid
     want, scale = oracle_projection(fmt, w, rows, cols, xt, 1)
     if residual:
         want = want + res
-    none = kh.KrakenBuffer(None, 0)
+    none = None
     out = hip_ctx.buffer(res) if residual else hip_ctx.buffer(byte_size=4 * rows)
     hip_ctx.kquant_matvec_fused_f32(
         GGML[fmt], hip_ctx.buffer(w), rows, cols, hip_ctx.buffer(x),
@@ -454,7 +503,7 @@ def test_multi_matvec_against_oracle_chain(hip_ctx, shapes, mode):
     res = rng.standard_normal(shapes[0][1]).astype(np.float32)
     outs = [hip_ctx.buffer(res)] + [hip_ctx.buffer(byte_size=4 * r) for _, r in shapes[1:]]
     residuals = [outs[0]] + [None] * (len(shapes) - 1)
-    none = kh.KrakenBuffer(None, 0)
+    none = None
     print(f"multi matvec {shapes} {mode}", flush=True)
     hip_ctx.kquant_matvec_multi(
         [GGML[f] for f, _ in shapes], [hip_ctx.buffer(w) for w in ws], [r for _, r in shapes],
@@ -472,7 +521,7 @@ def test_multi_matvec_rejections(hip_ctx):
     w = hip_ctx.buffer(kc.random_weight_fast("q4_k", 16, 8192, seed=1))
     x = hip_ctx.buffer(np.ones(8192, np.float32))
     out = hip_ctx.buffer(byte_size=64)
-    none = kh.KrakenBuffer(None, 0)
+    none = None
     with pytest.raises(kh.KrakenError, match="cols exceeds 4096"):
         hip_ctx.kquant_matvec_multi([12], [w], [16], 8192, x, none, 1e-6, none, [None], [out])
     with pytest.raises(kh.KrakenError, match="1 to 4 matrices"):

@@ -265,3 +265,43 @@ def test_multi_matmul_checks(vctx):
         "HIP Q6_K matmul weight buffer is too small")
     assert _multi_matmul(vctx, [12], [16], 1000, 64) == invalid(
         "HIP Q4_K matmul cols must be divisible by 256")
+
+
+# -------------------------------------------------------------- fused matmul --
+# kraken_hip_kquant_matmul_fused_f32: the matmul entry's checks, then its own.
+def _fused(vctx, fmt="q6_k", rows=1024, cols=3584, tokens=64, up=True, residual=True, **over):
+    w = over.get("w", fake(wbytes(fmt, rows, cols)))
+    x = over.get("x", fake(4 * tokens * cols))
+    u = over.get("upbuf", fake(4 * tokens * cols, 0x100000) if up else null())
+    out = over.get("out", fake(4 * tokens * rows, 0x200000))
+    r = over.get("resbuf", fake(4 * tokens * rows, 0x10000000) if residual else null())
+    return status(vctx, "kquant_matmul_fused_f32", {"q4_k": 12, "q5_k": 13, "q6_k": 14}[fmt], w,
+                  rows, cols, tokens, x, u, r, out)
+
+
+def test_fused_matmul_accepts(vctx):
+    for kw in ({}, dict(up=False), dict(residual=False), dict(up=False, residual=False),
+               dict(fmt="q4_k", rows=1024, cols=2048), dict(fmt="q5_k", rows=6144, cols=1024),
+               dict(tokens=9), dict(tokens=1024)):
+        assert _fused(vctx, **kw) == (kh.UNAVAILABLE, ACCEPTED), kw
+    # The residual may be the output itself.
+    out = fake(4 * 64 * 1024, 0x200000)
+    assert _fused(vctx, out=out, resbuf=out) == (kh.UNAVAILABLE, ACCEPTED)
+
+
+def test_fused_matmul_checks(vctx):
+    assert status(vctx, "kquant_matmul_fused_f32", 2, fake(100), 16, 256, 64, fake(4 * 64 * 256),
+                  null(), null(), fake(4 * 64 * 16)) == invalid(
+        "HIP K-quant fused matmul type must be Q4_K, Q5_K or Q6_K")
+    assert _fused(vctx, w=fake(100)) == invalid("HIP Q6_K matmul weight buffer is too small")
+    assert _fused(vctx, tokens=8) == invalid("HIP K-quant fused matmul needs more than 8 tokens")
+    code, msg = _fused(vctx, upbuf=fake(4 * 64 * 3584 - 4, 0x100000))
+    assert code == kh.INVALID_ARGUMENT and "K-quant fused matmul up" in msg
+    assert _fused(vctx, upbuf=fake(4 * 64 * 3584, 0x100004)) == invalid(
+        "HIP K-quant fused matmul up buffer must be 16-byte aligned")
+    code, msg = _fused(vctx, resbuf=fake(4 * 64 * 1024 - 4, 0x10000000))
+    assert code == kh.INVALID_ARGUMENT and "K-quant fused matmul residual" in msg
+    assert _fused(vctx, resbuf=fake(4 * 64 * 1024, 0x10000004)) == invalid(
+        "HIP K-quant fused matmul residual buffer must be 16-byte aligned")
+    assert _fused(vctx, resbuf=fake(4 * 64 * 1024, 0x200000 + 4096)) == invalid(
+        "HIP K-quant fused matmul residual overlaps the output")
