@@ -684,11 +684,11 @@ void flash256_kernel(FlashParams p) {
   step(Last{}, ntiles - 1, ca, cb, na, nb);
 
   l = xor32_sum(l);  // both lane halves hold keys of query n
-  if (!token_ok) {
-    return;
-  }
   // ---- epilogue: lane owns query n; dims 32*dt + c_row(r, h) ----
   if (p.splits == 1) {
+    if (!token_ok) {
+      return;
+    }
     const float inv = l == 0.0f ? 0.0f : 1.0f / l;
     float* orow = p.output + ((size_t)token * p.heads + head) * kD;
     const float* grow = p.gate != nullptr ? p.gate + ((size_t)token * p.heads + head) * kD : nullptr;
@@ -711,25 +711,39 @@ void flash256_kernel(FlashParams p) {
     }
   } else {
     // The split's o / l in f16 (its values are a weighted average of V rows,
-    // so within V's range); the merge scales it back by l.
-    const size_t base = (((size_t)token * p.kv_heads + kvh) * p.splits + split) * G + g_in_group;
-    half_t* po = p.partial_o + base * kD;
+    // so within V's range); the merge scales it back by l.  The wave's 32 rows
+    // go through its 16 KB of K's LDS (free after the loop: the last step reads
+    // only V) so that each store writes whole 512-byte rows.
     const float inv = l == 0.0f ? 0.0f : 1.0f / l;
+    half_t* stage = s_k + wave * (kQTile * kD);
 #pragma unroll
     for (int dt = 0; dt < kD / 32; ++dt) {
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        const int d = dt * 32 + r4 * 8 + h * 4;
+        const int c = 4 * dt + r4;  // 16-byte chunk of the row; h picks its half
         const half4_t v = {static_cast<half_t>(o[dt][r4 * 4 + 0] * inv),
                            static_cast<half_t>(o[dt][r4 * 4 + 1] * inv),
                            static_cast<half_t>(o[dt][r4 * 4 + 2] * inv),
                            static_cast<half_t>(o[dt][r4 * 4 + 3] * inv)};
-        *reinterpret_cast<half4_t*>(po + d) = v;
+        *reinterpret_cast<half4_t*>(stage + n * kD + 8 * (c ^ n) + 4 * h) = v;
       }
     }
-    if (h == 0) {
+    if (h == 0 && token_ok) {
+      const size_t base = (((size_t)token * p.kv_heads + kvh) * p.splits + split) * G + g_in_group;
       p.partial_ml[base * 2 + 0] = m;
       p.partial_ml[base * 2 + 1] = l;
+    }
+    const size_t row_units = (size_t)p.kv_heads * p.splits * G;  // units between tokens
+    const size_t base0 = (((size_t)t0 * p.kv_heads + kvh) * p.splits + split) * G + g_in_group;
+    const int chunk = lane & 31;
+#pragma unroll
+    for (int i = 0; i < kQTile / 2; ++i) {
+      const int row = 2 * i + (lane >> 5);
+      if (t0 + (uint32_t)row < p.tokens) {
+        const u32x4_t val = *reinterpret_cast<const u32x4_t*>(stage + row * kD + 8 * (chunk ^ row));
+        u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.partial_o + (base0 + row * row_units) * kD) + chunk;
+        *dst = val;
+      }
     }
   }
 }
