@@ -1103,6 +1103,9 @@ __device__ __forceinline__ void f32_to_f16_8(const float* in, half_t* out, uint6
 // f32 product, then one rounding to fp16).
 __device__ __forceinline__ void f32_swiglu_to_f16_8(const float* in, const float* up,
                                                     half_t* out, uint64_t i) {
+  // No contraction into the inlined expf: the same bits as binary_kernel's
+  // silu_mul wherever either is inlined.
+#pragma clang fp contract(off)
   const float4 a = reinterpret_cast<const float4*>(in)[2 * i];
   const float4 b = reinterpret_cast<const float4*>(in)[2 * i + 1];
   const float4 ua = reinterpret_cast<const float4*>(up)[2 * i];

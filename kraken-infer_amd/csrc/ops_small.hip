@@ -266,6 +266,9 @@ __global__ void binary_kernel(float* target, const float* rhs, size_t size, size
       target[i] += rhs[i];
     } else {
       // silu(gate) * up, as silu_mul_f32_in_place writes it (mps_backend.mm:2620-2629).
+      // No contraction into the inlined expf (the K-quant GEMM's first pass
+      // forms the same product and must get the same bits).
+#pragma clang fp contract(off)
       const float g = target[i];
       target[i] = (g / (1.0f + expf(-g))) * rhs[i];
     }
