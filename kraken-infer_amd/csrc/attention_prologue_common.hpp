@@ -112,6 +112,11 @@ __device__ __forceinline__ void norm_rope(const float v_in[4], const float w[4],
       const double x1 = e < half_dims ? partner : v[i];
       r[i] = e < half_dims ? (float)(x0 * cs[i] - x1 * sn[i]) : (float)(x1 * cs[i] + x0 * sn[i]);
     }
+    // The f32 result kept as such: a caller that rounds it to fp16 (the K
+    // append) must not get the norm's last multiply and that rounding fused
+    // into one v_fma_mix, which the separate qk_norm / mrope / copy ops (each
+    // storing f32) cannot do.
+    asm("" : "+v"(r[i]));
   }
 }
 
