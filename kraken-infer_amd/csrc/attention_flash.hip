@@ -330,7 +330,7 @@ void flash256_kernel(FlashParams p) {
                         (uint32_t)(uintptr_t)(lds_void_t*)s_v + slot_bytes};
 
   // K(0)'s copies go out before the query is loaded; K(1)'s and V(0)'s after
-  // the query is staged, so that the first S^T waits only for K(0) and the
+  // the query's loads, so that the first S^T waits only for K(0) and the
   // query (K(1) past key_end reads as zeros).
   issue_tile_copy<W, false>(ksrc, coff, key_begin, ksrc.lds);
 
@@ -342,28 +342,45 @@ void flash256_kernel(FlashParams p) {
   // chunks XOR-swizzled by row % 16 like the K tiles so that the fragment
   // reads are free of bank conflicts.
   half8_t qf[kD / 16];
-  {
-    half_t* stage = wave < 2 ? s_q + wave * (kQTile * kRowHalfs)
-                             : s_v + kTileHalfs + (wave - 2) * (kQTile * kRowHalfs);
+  half_t* const q_stage = wave < 2 ? s_q + wave * (kQTile * kRowHalfs)
+                                   : s_v + kTileHalfs + (wave - 2) * (kQTile * kRowHalfs);
+  auto read_query_fragments = [&]() {
+#pragma unroll
+    for (int step = 0; step < kD / 16; ++step) {
+      const int chunk = (2 * step + h) ^ (n & 15);
+      qf[step] = *reinterpret_cast<const half8_t*>(q_stage + n * kRowHalfs + chunk * 8);
+    }
+    // Q stays in AGPRs (an MFMA reads its B operand from either file), which
+    // leaves the architectural VGPRs to the scores, P and the fragment rings.
+#pragma unroll
+    for (int step = 0; step < kD / 16; ++step) {
+      asm volatile("" : "+a"(qf[step]));
+    }
+  };
+  if constexpr (kQF16) {
+    // An f16 query row is copied straight into LDS like a key row: copy i
+    // brings rows 2 i and 2 i + 1 (lanes 0-31 and 32-63), lane l fetching
+    // logical chunk (l % 32) ^ (row % 16) into physical chunk l % 32.  The
+    // resource starts at the tile's first row of this head and ends after the
+    // last token's row, so rows past the end read as zeros.
+    const uint32_t q_row_bytes = p.heads * kD * 2u;
+    const uint32_t rows_left = p.tokens - t0;
+    const i32x4_t qsrc = rsrc_words(p.query_f16 + ((size_t)t0 * p.heads + head) * kD,
+                                    (rows_left - 1u) * q_row_bytes + kD * 2u);
+    const uint32_t q_lds = (uint32_t)(uintptr_t)(lds_void_t*)q_stage;
+    const uint32_t q_lane = (uint32_t)(lane >> 5) * q_row_bytes;
+#pragma unroll
+    for (int i = 0; i < kQTile / 2; ++i) {
+      const int r = 2 * i + (lane >> 5);
+      const uint32_t voff = q_lane + 2u * (uint32_t)i * q_row_bytes +
+                            16u * (uint32_t)((lane & 31) ^ (r & 15));
+      copy16_to_lds_m0(qsrc, voff, q_lds + (uint32_t)i * 2u * kRowHalfs * 2u);
+    }
+  } else {
+    half_t* stage = q_stage;
     // Unconditional loads from a valid row (token 0 stands in for tokens past the
-    // end), zeroed afterwards, so all 32 loads are in flight together.  An f16
-    // query is read as it is (8 bytes per lane of a 512-byte row).
-    if constexpr (kQF16) {
-      half4_t rows[kQTile];
-#pragma unroll
-      for (int r = 0; r < kQTile; ++r) {
-        const uint32_t tok = t0 + (uint32_t)r < p.tokens ? t0 + (uint32_t)r : 0u;
-        const half_t* qrow = p.query_f16 + ((size_t)tok * p.heads + head) * kD;
-        rows[r] = *reinterpret_cast<const half4_t*>(qrow + 4 * lane);
-      }
-#pragma unroll
-      for (int r = 0; r < kQTile; ++r) {
-        const half4_t zero = {0, 0, 0, 0};
-        const half4_t hv = t0 + (uint32_t)r < p.tokens ? rows[r] : zero;
-        const int chunk = (lane >> 1) ^ (r & 15);
-        *reinterpret_cast<half4_t*>(stage + r * kRowHalfs + chunk * 8 + (lane & 1) * 4) = hv;
-      }
-    } else {
+    // end), zeroed afterwards, so all 32 loads are in flight together.
+    {
       float4 rows[kQTile];
 #pragma unroll
       for (int r = 0; r < kQTile; ++r) {
@@ -380,17 +397,7 @@ void flash256_kernel(FlashParams p) {
         *reinterpret_cast<half4_t*>(stage + r * kRowHalfs + chunk * 8 + (lane & 1) * 4) = hv;
       }
     }
-#pragma unroll
-    for (int step = 0; step < kD / 16; ++step) {
-      const int chunk = (2 * step + h) ^ (n & 15);
-      qf[step] = *reinterpret_cast<const half8_t*>(stage + n * kRowHalfs + chunk * 8);
-    }
-    // Q stays in AGPRs (an MFMA reads its B operand from either file), which
-    // leaves the architectural VGPRs to the scores, P and the fragment rings.
-#pragma unroll
-    for (int step = 0; step < kD / 16; ++step) {
-      asm volatile("" : "+a"(qf[step]));
-    }
+    read_query_fragments();
   }
   issue_tile_copy<W, false>(ksrc, coff, key_begin + kKTile, ksrc.lds + kStageBytes);
   issue_tile_copy<W, true>(vsrc, coff, key_begin, vsrc.lds);
@@ -668,11 +675,15 @@ void flash256_kernel(FlashParams p) {
 
   // Prologue: publish K(0) (its copies and the query loads were issued before
   // K(1)'s and V(0)'s, and loads complete in issue order) and compute S^T of
-  // tile 0; step 0 waits for K(1) and V(0).
+  // tile 0; step 0 waits for K(1) and V(0).  An f16 query's rows are in LDS
+  // once its copies are done (this wave's own), and go to the registers here.
   float16_t ca, cb, na, nb;
   constexpr int kAfterK0 = 2 * kCopiesPerTile<W> <= 63 ? 2 * kCopiesPerTile<W> : kCopiesPerTile<W>;
   wait_copies_but<kAfterK0>();
   __syncthreads();
+  if constexpr (kQF16) {
+    read_query_fragments();
+  }
   first_scores(ca, cb);
   using Next = std::integral_constant<bool, true>;
   using Last = std::integral_constant<bool, false>;
