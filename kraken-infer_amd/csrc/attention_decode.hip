@@ -1254,6 +1254,75 @@ __global__ __launch_bounds__(256) void attention_merge_narrow(CombineArgs p) {
   store_gated4(p, out_index, r, inv, gv);
 }
 
+// The f16 partials of the flash path: as attention_merge_narrow<S, true>, with
+// eight dims per thread (one 16-byte load per split, two output stores), the
+// same arithmetic per element.
+template <int S>
+__global__ __launch_bounds__(256) void attention_merge_narrow_f16x8(CombineArgs p) {
+  const uint32_t chunks = p.head_dim / 8;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)p.tokens * p.heads * chunks) {
+    return;
+  }
+  const uint32_t chunk = (uint32_t)(idx % chunks);
+  const size_t th = idx / chunks;  // token * heads + head
+  const uint32_t head = (uint32_t)(th % p.heads);
+  const uint32_t token = (uint32_t)(th / p.heads);
+  const uint32_t group = p.heads / p.kv_heads;
+  const uint32_t kvh = head / group;
+  const uint32_t g = head % group;
+  const size_t base = (size_t)token * p.kv_heads + kvh;
+  const uint32_t nsp = token_splits(p, token);
+  const size_t out_index = th * p.head_dim + chunk * 8;
+  const float4 gv0 = load_gate4(p.gate, out_index, true);
+  const float4 gv1 = load_gate4(p.gate, out_index + 4, true);
+  float mv[S], lv[S];
+  float4 ov0[S], ov1[S];
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const uint32_t s = min((uint32_t)j, nsp - 1u);
+    const size_t unit = (base * p.splits + s) * group + g;
+    mv[j] = p.partial_ml[unit * 2];
+    lv[j] = p.partial_ml[unit * 2 + 1];
+    const half8_t h = *reinterpret_cast<const half8_t*>(
+      reinterpret_cast<const half_t*>(p.partial_o) + unit * p.head_dim + chunk * 8);
+    ov0[j] = make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+    ov1[j] = make_float4((float)h[4], (float)h[5], (float)h[6], (float)h[7]);
+  }
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    ov0[j] = make_float4(ov0[j].x * lv[j], ov0[j].y * lv[j], ov0[j].z * lv[j], ov0[j].w * lv[j]);
+    ov1[j] = make_float4(ov1[j].x * lv[j], ov1[j].y * lv[j], ov1[j].z * lv[j], ov1[j].w * lv[j]);
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    if ((uint32_t)j >= nsp) {
+      mv[j] = -INFINITY;
+    }
+    mx = fmaxf(mx, mv[j]);
+  }
+  float den = 0.0f;
+  float4 r0 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 r1 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const float w = mv[j] == -INFINITY ? 0.0f : fast_exp2(mv[j] - mx);
+    den = fmaf(w, lv[j], den);
+    r0.x = fmaf(w, ov0[j].x, r0.x);
+    r0.y = fmaf(w, ov0[j].y, r0.y);
+    r0.z = fmaf(w, ov0[j].z, r0.z);
+    r0.w = fmaf(w, ov0[j].w, r0.w);
+    r1.x = fmaf(w, ov1[j].x, r1.x);
+    r1.y = fmaf(w, ov1[j].y, r1.y);
+    r1.z = fmaf(w, ov1[j].z, r1.z);
+    r1.w = fmaf(w, ov1[j].w, r1.w);
+  }
+  const float inv = den == 0.0f ? 0.0f : 1.0f / den;
+  store_gated4(p, out_index, r0, inv, gv0);
+  store_gated4(p, out_index + 4, r1, inv, gv1);
+}
+
 // Many tokens with more than 16 splits (ragged batched decode): the same
 // per-thread layout as attention_merge_narrow, walking a token's splits in
 // batches of 8 (all loads of a batch in flight) with an online log-sum-exp, so
@@ -1330,7 +1399,17 @@ hipError_t launch_attention_combine(const CombineArgs& c, hipStream_t stream) {
   if (c.splits <= 16) {
     const size_t threads = (size_t)c.tokens * c.heads * (c.head_dim / 4);
     const dim3 grid((uint32_t)((threads + 255) / 256));
-    if (c.partial_f16 != 0) {
+    if (c.partial_f16 != 0 && c.head_dim % 8 == 0) {
+      const size_t threads8 = (size_t)c.tokens * c.heads * (c.head_dim / 8);
+      const dim3 grid8((uint32_t)((threads8 + 255) / 256));
+      if (c.splits <= 4) {
+        attention_merge_narrow_f16x8<4><<<grid8, 256, 0, stream>>>(c);
+      } else if (c.splits <= 8) {
+        attention_merge_narrow_f16x8<8><<<grid8, 256, 0, stream>>>(c);
+      } else {
+        attention_merge_narrow_f16x8<16><<<grid8, 256, 0, stream>>>(c);
+      }
+    } else if (c.partial_f16 != 0) {
       if (c.splits <= 4) {
         attention_merge_narrow<4, true><<<grid, 256, 0, stream>>>(c);
       } else if (c.splits <= 8) {
