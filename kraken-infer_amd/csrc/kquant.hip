@@ -2208,10 +2208,12 @@ hipError_t launch_kquant_matmul(int format, const void* weight, size_t rows, siz
   if (unfused) {
     const uint64_t blocks = (uint64_t)rows * bpr;
     const uint64_t n8 = (uint64_t)tokens * cols / 8u;
-    // A large input (the 3584-wide FFN activations) converts four groups of
-    // eight per thread: Q6_K 1024 x 3584 at 1024 tokens 31.0 -> 28.7 us; a
-    // 1024-wide one keeps one group (Q5_K 30.2 against 31.5 us with four).
-    const bool wide = n8 >= kWideConvertGroups;
+    // A large plain input (the 3584-wide FFN activations) converts four groups
+    // of eight per thread: Q6_K 1024 x 3584 at 1024 tokens 31.0 -> 28.7 us; a
+    // 1024-wide one keeps one group (Q5_K 30.2 against 31.5 us with four), and
+    // so does the SwiGLU input, whose exponentials make four groups a long
+    // chain (first pass 9.9 -> 11.1 us in the whole-model prefill).
+    const bool wide = n8 >= kWideConvertGroups && up == nullptr;
     const uint32_t per_wg = wide ? 1024u : 256u;
     const uint32_t convert_blocks = (uint32_t)((n8 + per_wg - 1) / per_wg);
     const dim3 dq(convert_blocks + (uint32_t)((blocks + 31) / 32));
