@@ -96,7 +96,6 @@ struct FlashParams {
   float* partial_ml;  // [tokens][kv_heads][splits][G][2]
   uint32_t layer, start_position, tokens, capacity_tokens, heads, kv_heads;
   uint32_t key_count, keys_per_split, splits, q_tiles, head_groups;
-  uint32_t splits_fastest;  // work items numbered with the key split fastest
   float scale_log2;
 };
 
@@ -267,11 +266,10 @@ void flash256_kernel(FlashParams p) {
   const uint32_t G = p.heads / p.kv_heads;
 
   // XCD-aware renumbering of the linear workgroup id (see header), then the
-  // work item (kv head, head group, split, query tile), the heaviest (latest)
-  // query tiles first.  Query tiles fastest: an XCD's run shares one key range.
-  // Splits fastest (long key ranges): an XCD's run holds all splits of its
-  // query tiles, so each query row is read into one L2 instead of four, and
-  // each K/V tile is read by fewer workgroups at a time.
+  // work item (kv head, head group, query tile, split), the heaviest (latest)
+  // query tiles first and the splits of a query tile fastest: an XCD's run
+  // holds all splits of its query tiles, so each query row is read into one L2
+  // instead of four, and each K/V tile is read by fewer workgroups at a time.
   const uint32_t total = p.q_tiles * p.kv_heads * p.head_groups * p.splits;
   const uint32_t lin = blockIdx.x;
   const uint32_t per_xcd = total / 8u;
@@ -279,14 +277,14 @@ void flash256_kernel(FlashParams p) {
   const uint32_t xcd = lin % 8u;
   const uint32_t item = xcd * per_xcd + min(xcd, rem) + lin / 8u;
   const uint32_t qs = item % (p.q_tiles * p.splits);
-  uint32_t q_rank = p.splits_fastest != 0u ? qs / p.splits : qs % p.q_tiles;
-  if (p.splits_fastest != 0u && (p.q_tiles & 3u) == 0u) {
+  uint32_t q_rank = qs / p.splits;
+  if ((p.q_tiles & 3u) == 0u) {
     // Consecutive ranks (one XCD's run) take query tiles a quarter apart, so
     // every XCD gets early and late (light and heavy causal) tiles.
     q_rank = (q_rank & 3u) * (p.q_tiles >> 2) + (q_rank >> 2);
   }
   const uint32_t q_tile = p.q_tiles - 1u - q_rank;
-  const uint32_t split = p.splits_fastest != 0u ? qs % p.splits : qs / p.q_tiles;
+  const uint32_t split = qs % p.splits;
   const uint32_t hg = (item / (p.q_tiles * p.splits)) % p.head_groups;
   const uint32_t kvh = item / (p.q_tiles * p.splits * p.head_groups);
   const uint32_t g_in_group = hg * GW + wave;
@@ -862,10 +860,11 @@ hipError_t launch_attention_flash(const AttentionArgs& a, int cu_count, void* wo
   p.splits = plan.splits;
   p.q_tiles = plan.q_tiles;
   p.head_groups = plan.head_groups;
-  // Measured on C2 (T = 1024, 4 splits): splits fastest with interleaved query
-  // tiles took P = 3072 from 45.7 to 42.7 us and P = 7168 from 77 to 72.5 us,
-  // and P = 0 (1024 keys) from 20.9 to 22.2 us.
-  p.splits_fastest = p.key_count > 2048u ? 1u : 0u;
+  // Work items are numbered with the splits of a query tile fastest, query
+  // tiles a quarter apart interleaved.  Measured on C2 (T = 1024, 4 splits)
+  // against query tiles fastest: P = 3072 45.7 -> 42.7 us, P = 7168 77 ->
+  // 72.5 us, and, with the query copied into LDS and the eight-dim merge,
+  // P = 1024 31.7-31.85 -> 30.3-31.5 us, P = 0 level (22.2-22.9 us).
   p.scale_log2 = (1.0f / sqrtf(256.0f)) * kLog2e;
   if (plan.splits > 1) {
     const size_t units = (size_t)a.tokens * a.heads * plan.splits;
