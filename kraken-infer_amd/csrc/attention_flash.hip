@@ -49,7 +49,8 @@
 //    in the decode path's layout; the decode combine pass merges them.  The
 //    workgroup order is XCD-aware: the dispatcher deals workgroup i to XCD i % 8,
 //    so work items are renumbered to give each XCD a contiguous run of
-//    (split, query tile) items that share K/V in its L2.
+//    (query tile, split) items, all splits of a query tile together, which
+//    then share the tile's query rows in that XCD's L2.
 //
 // MFMA 32x32x16 lane layout (gfx950): A[i][k]: lane l holds row i = l%32, k =
 // 8*(l/32) + j (j < 8).  B[k][n]: lane l holds column n = l%32, same k.  C: lane l
