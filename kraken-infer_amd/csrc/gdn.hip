@@ -603,15 +603,33 @@ __global__ __launch_bounds__(256) void conv_split_l2_kernel(
     }
   }
 
+  // The wave's rows, all loads in flight before the first output (rows past
+  // the end read as zeros and are not used): whole-model prefill 5.77 -> 5.74
+  // ms per 1024-token chunk.
+  float xs[kConvTokensPerWave][CPL];
+#pragma unroll
+  for (int k = 0; k < kConvTokensPerWave; ++k) {
+    const uint32_t t = t_begin + (uint32_t)k;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const uint32_t d = lane + 64u * i;
+      xs[k][i] = d < head_dim && t < t_end ? qkv[(size_t)t * channels + cbase + d] : 0.0f;
+    }
+  }
   const bool is_v = unit >= 2u * key_heads;
-  for (uint32_t t = t_begin; t < t_end; ++t) {
+#pragma unroll
+  for (int k = 0; k < kConvTokensPerWave; ++k) {
+    const uint32_t t = t_begin + (uint32_t)k;
+    if (t >= t_end) {
+      break;
+    }
     float y[CPL];
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const uint32_t d = lane + 64u * i;
       const bool ok = d < head_dim;
-      const float xt = ok ? qkv[(size_t)t * channels + cbase + d] : 0.0f;
+      const float xt = xs[k][i];
       float acc = 0.0f;
 #pragma unroll
       for (int j = 0; j < W; ++j) {

@@ -235,10 +235,33 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* input,
   __shared__ float s_part[4];
   const float* x = input + (size_t)blockIdx.x * size;
   float* y = output + (size_t)blockIdx.x * size;
+  // Rows of up to 256 * kHeld values stay in registers between the sum of
+  // squares and the scaling (with the weights loaded beside them), instead of
+  // being read a second time; the sum runs over the same elements in the same
+  // order either way (whole-model prefill 5.77 -> 5.72 ms per 1024-token
+  // chunk, 48 calls per chunk).
+  constexpr uint32_t kHeld = 8;
+  const bool held = size <= 256u * kHeld;
+  float xv[kHeld], wv[kHeld];
   float sum = 0.0f;
-  for (uint32_t i = threadIdx.x; i < size; i += 256u) {
-    const float v = x[i];
-    sum = fmaf(v, v, sum);
+  if (held) {
+#pragma unroll
+    for (uint32_t k = 0; k < kHeld; ++k) {
+      const uint32_t i = threadIdx.x + 256u * k;
+      xv[k] = i < size ? x[i] : 0.0f;
+      wv[k] = i < size ? weight[i] : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kHeld; ++k) {
+      if (threadIdx.x + 256u * k < size) {
+        sum = fmaf(xv[k], xv[k], sum);
+      }
+    }
+  } else {
+    for (uint32_t i = threadIdx.x; i < size; i += 256u) {
+      const float v = x[i];
+      sum = fmaf(v, v, sum);
+    }
   }
   sum = wave_sum(sum);
   if ((threadIdx.x & 63) == 0) {
@@ -247,8 +270,18 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* input,
   __syncthreads();
   const float total = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
   const float scale = 1.0f / sqrtf(total / (float)size + eps);
-  for (uint32_t i = threadIdx.x; i < size; i += 256u) {
-    y[i] = x[i] * scale * weight[i];
+  if (held) {
+#pragma unroll
+    for (uint32_t k = 0; k < kHeld; ++k) {
+      const uint32_t i = threadIdx.x + 256u * k;
+      if (i < size) {
+        y[i] = xv[k] * scale * wv[k];
+      }
+    }
+  } else {
+    for (uint32_t i = threadIdx.x; i < size; i += 256u) {
+      y[i] = x[i] * scale * weight[i];
+    }
   }
 }
 
