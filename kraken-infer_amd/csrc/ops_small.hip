@@ -34,12 +34,19 @@ __global__ __launch_bounds__(256) void rms_norm_heads_kernel(float* values, cons
     return;  // whole wave exits together
   }
   float* x = values + (size_t)row * head_dim;
-  float v[4];
-  float sum = 0.0f;
+  // The weights and the gate are loaded with the row, before the reduction,
+  // so the scaling does not wait for a second round trip.
+  float v[4], w[4], z[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t d = lane + 64u * i;
     v[i] = d < head_dim ? x[d] : 0.0f;
+    w[i] = d < head_dim ? weight[d] : 0.0f;
+    z[i] = d < head_dim && gate != nullptr ? gate[(size_t)row * head_dim + d] : 0.0f;
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
     sum = fmaf(v[i], v[i], sum);
   }
   sum = wave_sum(sum);
@@ -48,10 +55,9 @@ __global__ __launch_bounds__(256) void rms_norm_heads_kernel(float* values, cons
   for (int i = 0; i < 4; ++i) {
     const uint32_t d = lane + 64u * i;
     if (d < head_dim) {
-      float r = v[i] * scale * weight[d];
+      float r = v[i] * scale * w[i];
       if (gate != nullptr) {
-        const float z = gate[(size_t)row * head_dim + d];
-        r *= z * sigmoid_acc(z);
+        r *= z[i] * sigmoid_acc(z[i]);
       }
       x[d] = r;
     }
