@@ -49,8 +49,14 @@ __global__ __launch_bounds__(256) void attention_prologue_kernel(PrologueArgs a)
   const float* weight = is_q ? a.q_norm : a.k_norm;
   const RopeArgs rope{a.positions, a.mrope_start, a.tokens, a.n_dims, a.s0, a.s1, a.s2, a.s3,
                       a.theta};
-  float v[4], w[4];
+  float v[4], w[4], g[4];
   load_head(src, weight, d_head, lane, v, w);
+  // The gate half of a q_gate head is copied out; its loads go out with the rest.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t d = lane + 64u * i;
+    g[i] = is_q && d < d_head ? src[d_head + d] : 0.0f;
+  }
   int32_t pos[4];
   rope_positions(rope, t, pos);
   double sn[4], cs[4];
@@ -66,7 +72,7 @@ __global__ __launch_bounds__(256) void attention_prologue_kernel(PrologueArgs a)
       const uint32_t d = lane + 64u * i;
       if (d < d_head) {
         q_out[d] = r[i];
-        g_out[d] = src[d_head + d];
+        g_out[d] = g[i];
       }
     }
   } else {

@@ -686,6 +686,22 @@ __global__ void conv_state_update_kernel(float* conv_state, const float* qkv,
   // New entry j is row tokens - width + j of [old state | chunk]: a chunk row,
   // or old entry j + tokens.  Ascending j reads each old entry before it is
   // overwritten (j + tokens > j), so the shift needs no private copy.
+  constexpr uint32_t kHeld = 8;
+  if (tokens >= width && width <= kHeld) {
+    // Chunk rows only: every load goes out before the first store.
+    float v[kHeld];
+#pragma unroll
+    for (uint32_t j = 0; j < kHeld; ++j) {
+      v[j] = j < width ? qkv[(size_t)(tokens - width + j) * channels + c] : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kHeld; ++j) {
+      if (j < width) {
+        state[j] = v[j];
+      }
+    }
+    return;
+  }
   for (uint32_t j = 0; j < width; ++j) {
     const int64_t r = (int64_t)tokens - (int64_t)width + j;
     state[j] = r >= 0 ? qkv[(size_t)r * channels + c] : state[j + tokens];
