@@ -816,24 +816,12 @@ __global__ __launch_bounds__(256) void gdn_layer_ragged_kernel(GdnLayerArgs p) {
   const uint32_t seq = blockIdx.y;
   const uint32_t H = p.heads;
   const size_t channels = (size_t)3 * H * D;
-
-  const uint64_t soff = p.seq_state_offsets[seq];
-  const uint64_t coff = p.seq_conv_offsets[seq];
-  if ((soff & 3u) != 0 || soff > p.state_pool_elems ||
-      p.state_pool_elems - soff < (uint64_t)H * D * D || coff > p.conv_pool_elems ||
-      p.conv_pool_elems - coff < channels * W) {
-    return;  // whole workgroup, before any barrier
-  }
-  float* shead = p.state_pool + soff + (size_t)h * D * D;
   const uint32_t row0 = (uint32_t)grp * RPL;
   const uint32_t col0 = (uint32_t)(lane & 31) * 4;
-  float4 s[RPL];
-#pragma unroll
-  for (int j = 0; j < RPL; ++j) {
-    s[j] = *reinterpret_cast<const float4*>(shead + (size_t)(row0 + j) * D + col0);
-  }
-  // The epilogue's and the gate's inputs are loaded now too, so that no stage
-  // after the conv waits on a global round trip.
+
+  // Everything that does not depend on the sequence's pool offsets (which are
+  // themselves loads) goes out first: the epilogue's and the gate's inputs,
+  // and the conv's input row and weights.
   const size_t gi = (size_t)seq * H + h;
   float g = p.gate[gi];
   float b = p.beta[gi];
@@ -850,33 +838,63 @@ __global__ __launch_bounds__(256) void gdn_layer_ragged_kernel(GdnLayerArgs p) {
       nw[i] = p.norm_weight[lane + 64 * i];
     }
   }
+  const uint32_t cbase = ((uint32_t)(wave < 3 ? wave : 0) * H + h) * D;
+  float xt[CPL], cw[CPL][K];
+  if (wave < 3) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const size_t c = cbase + lane + 64u * i;
+      xt[i] = p.qkv[(size_t)seq * channels + c];
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        cw[i][j] = p.conv_weights[c * K + j];
+      }
+    }
+  }
+
+  const uint64_t soff = p.seq_state_offsets[seq];
+  const uint64_t coff = p.seq_conv_offsets[seq];
+  if ((soff & 3u) != 0 || soff > p.state_pool_elems ||
+      p.state_pool_elems - soff < (uint64_t)H * D * D || coff > p.conv_pool_elems ||
+      p.conv_pool_elems - coff < channels * W) {
+    return;  // whole workgroup, before any barrier
+  }
+  float* shead = p.state_pool + soff + (size_t)h * D * D;
+  float4 s[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    s[j] = *reinterpret_cast<const float4*>(shead + (size_t)(row0 + j) * D + col0);
+  }
 
   if (wave < 3) {
-    // Unit wave * H + h: the q, k or v channels of this head.
+    // Unit wave * H + h: the q, k or v channels of this head.  Both channels'
+    // windows are loaded before either is written back.
     float* state = p.conv_pool + coff;
-    const uint32_t cbase = ((uint32_t)wave * H + h) * D;
+    float win[CPL][W];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const size_t c = cbase + lane + 64u * i;
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        win[i][j] = state[c * W + j];
+      }
+    }
     float y[CPL];
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const size_t c = cbase + lane + 64u * i;
-      float win[W];
-#pragma unroll
-      for (int j = 0; j < W; ++j) {
-        win[j] = state[c * W + j];
-      }
-      const float xt = p.qkv[(size_t)seq * channels + c];
       float acc = 0.0f;
 #pragma unroll
       for (int j = 0; j < W; ++j) {
-        acc = fmaf(win[j], p.conv_weights[c * K + j], acc);
+        acc = fmaf(win[i][j], cw[i][j], acc);
       }
-      acc = fmaf(xt, p.conv_weights[c * K + W], acc);
+      acc = fmaf(xt[i], cw[i][W], acc);
 #pragma unroll
       for (int j = 0; j + 1 < W; ++j) {
-        state[c * W + j] = win[j + 1];
+        state[c * W + j] = win[i][j + 1];
       }
-      state[c * W + (W - 1)] = xt;
+      state[c * W + (W - 1)] = xt[i];
       y[i] = acc / (1.0f + expf(-acc));  // SiLU
       ss = fmaf(y[i], y[i], ss);
     }
